@@ -1,0 +1,175 @@
+/*
+ * ud_encoder.h -- C ABI of the MI355X (gfx950) cache-aware streaming FastConformer encoder step.
+ *
+ * This is the drop-in boundary for DictatorEngine's encoder step.  Each entry point names the
+ * reference interface it replaces (paths relative to the reference repository root).
+ *
+ * Conventions (all entry points):
+ *  - Return UD_OK (0) or a negative ud_status.  Nothing throws or aborts across the ABI; the
+ *    message of the last failure on the calling thread is available from ud_last_error().
+ *    (Reference: Swift `throws EngineError.io`, Sources/DictatorCore/Errors.swift:3-11; GPU faults
+ *    `fatalError`, Sources/DictatorEngine/Core/Kernels.swift:40; shape misuse `precondition`,
+ *    Sources/DictatorEngine/Models/FastConformer.swift:450.)
+ *  - Pointers named *_dev are device (HBM) pointers; *_host are host pointers.  Caller buffers are
+ *    borrowed for the duration of the call only.
+ *  - `hip_stream` is a hipStream_t (NULL = the null stream).  Device work is enqueued on it and
+ *    the call returns without waiting, except where a function says it synchronizes.
+ *  - One encoder may be stepped by one thread at a time; distinct encoders are independent.
+ */
+#ifndef UD_ENCODER_H
+#define UD_ENCODER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UD_API __attribute__((visibility("default")))
+
+typedef enum {
+    UD_OK = 0,
+    UD_ERR_INVALID = -1,      /* null handle / bad argument */
+    UD_ERR_SHAPE = -2,        /* size outside what the encoder or kernel supports */
+    UD_ERR_NOMEM = -3,        /* device or host allocation failed */
+    UD_ERR_HIP = -4,          /* a HIP runtime call failed */
+    UD_ERR_STATE = -5,        /* call order violated (e.g. step before finalize) */
+    UD_ERR_WEIGHT = -6,       /* unknown weight name or wrong element count */
+    UD_ERR_CAPACITY = -7      /* stream pool exhausted */
+} ud_status;
+
+typedef enum {
+    UD_F32 = 0,               /* fp32 weights, activations, caches */
+    UD_BF16 = 1               /* bf16 weights, GEMM inputs, K/V caches and position tables;
+                                 fp32 accumulation, residual stream, norms, pos_bias, depthwise
+                                 conv and conv cache (the keep-fp32 policy of
+                                 Sources/DictatorEngine/Core/Convert.swift:76-83) */
+} ud_dtype;
+
+/* FastConformerConfig (Sources/DictatorEngine/Models/FastConformer.swift:5-38) plus the streaming
+ * geometry of StreamState (FastConformer.swift:406-435) and a stream pool capacity. */
+typedef struct {
+    int32_t layers;           /* 24 */
+    int32_t d_model;          /* 1024 */
+    int32_t heads;            /* 8 (head_dim = d_model / heads must be 128) */
+    int32_t ff_dim;           /* 4096 */
+    int32_t conv_kernel;      /* 9 (causal depthwise conv) */
+    int32_t left_context;     /* L = 70 cached frames */
+    int32_t max_chunk;        /* largest T per step (position tables cover -(T-1)..L+T-1) */
+    int32_t max_streams;      /* stream pool capacity of this encoder */
+    int32_t dtype;            /* ud_dtype */
+} ud_encoder_config;
+
+typedef struct ud_encoder ud_encoder;
+typedef struct ud_stream ud_stream;
+
+/* Human-readable message of the last failure on this thread ("" if none). */
+UD_API const char* ud_last_error(void);
+
+/* ---------------------------------------------------------------- encoder lifetime */
+
+/* Replaces FastConformerEncoder.init (FastConformer.swift:72-144) and makeWorkspace (:211-213):
+ * allocates device weights, the per-step workspace and the stream pool on the current device. */
+UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder** out);
+UD_API void ud_encoder_destroy(ud_encoder* enc);
+
+/* Replaces the per-tensor loads of FastConformer.swift:96-143.  `name` is a NeMo state_dict
+ * name ("encoder.layers.{i}.feed_forward1.linear1.weight", ..., the 26 per-layer tensors of the
+ * checkpoint's name map); `host` holds `count` fp32 values in the checkpoint layout ([out, in]
+ * for linears, k=1 axis squeezed, depthwise [D, 1, K]).  The values are converted to the
+ * encoder's dtype on upload (bf16: round-to-nearest-even, Tensor.swift:116-122).  Synchronous. */
+UD_API int ud_encoder_set_weight(ud_encoder* enc, const char* name, const float* host, int64_t count);
+
+/* Replaces preparePositionTables (FastConformer.swift:161-178) as called by makeStreamState
+ * (:431-435): builds P_l = PE . W_pos,l^T over rel = -(max_chunk-1) .. L+max_chunk-1 for every
+ * layer.  Every weight must have been set.  Synchronous. */
+UD_API int ud_encoder_finalize(ud_encoder* enc);
+
+/* ---------------------------------------------------------------- streams */
+
+/* Replaces makeStreamState / StreamState (FastConformer.swift:406-435): takes one slot of the
+ * encoder's stream pool (K/V ring caches [layers][heads][L][head_dim] and the conv ring
+ * [layers][K-1][d_model]), zero-initialised, cache_len 0. */
+UD_API int ud_stream_create(ud_encoder* enc, ud_stream** out);
+UD_API int ud_stream_reset(ud_stream* s);              /* zero caches, cache_len 0, steps 0 */
+UD_API void ud_stream_destroy(ud_stream* s);
+/* StreamState.cacheLen / .step (FastConformer.swift:413-414). */
+UD_API int ud_stream_info(const ud_stream* s, int32_t* cache_len, int32_t* steps);
+
+/* ---------------------------------------------------------------- the step */
+
+/* Replaces encodeStreamStep (FastConformer.swift:441-480) from the kept subsampled rows on, for a
+ * batch of independent streams (the reference runs one stream per NemotronEncoder.step,
+ * Sources/DictatorCore/Nemotron/NemotronStreamer.swift:6-12).
+ *   streams[n]     distinct streams of this encoder
+ *   T              frames per stream this step (1 <= T <= max_chunk, T <= L)
+ *   x_dev          fp32 [n, T, d_model] chunk input, stream-major
+ *   valid_T_host   [n] valid frames per stream (clamped to [0, T]); frames >= valid are masked
+ *                  as keys and their GLU rows are zeroed, but all T frames enter the caches and
+ *                  cache_len advances by T (FastConformer.swift:449, 459-462, 302, 477)
+ *   out_dev        fp32 [n, T, d_model] encoder output; may not alias x_dev
+ * Each stream's caches advance in place (ring buffers).  Asynchronous on hip_stream. */
+UD_API int ud_encoder_step(ud_encoder* enc, ud_stream* const* streams, int32_t n, int32_t T,
+                           const float* x_dev, const int32_t* valid_T_host, float* out_dev,
+                           void* hip_stream);
+
+/* Cache window of one stream and layer in logical (time) order, oldest row first, as fp32:
+ * k/v [L, d_model], conv [K-1, d_model]; rows older than cache_len are whatever the pool holds
+ * (zeros for a fresh stream).  This is the StreamState content after a step
+ * (FastConformer.swift:469-472, the rows the next step reads).  Synchronous. */
+UD_API int ud_stream_export_cache(const ud_stream* s, int32_t layer, float* k_host, float* v_host,
+                                  float* conv_host, int32_t* cache_len);
+/* Inverse of export: loads a logical window (converted to the cache dtype) and sets cache_len
+ * (shared by all layers; the last import wins).  Synchronous. */
+UD_API int ud_stream_import_cache(ud_stream* s, int32_t layer, const float* k_host, const float* v_host,
+                                  const float* conv_host, int32_t cache_len);
+
+/* ---------------------------------------------------------------- single ops (KATs, config 1) */
+
+/* Replaces Step.relPosAttention (Sources/DictatorEngine/Core/Ops.swift:80-90) and its kernel
+ * (Sources/DictatorEngine/Metal/20_conformer.metal:140-220):
+ *   score[i,j] = ((q_i+u_h).k_j + (q_i+v_h).P[(Tk-Tq+i)-j+rel_offset]) / sqrt(dk)
+ * for j in [max(r_i.x,0), min(r_i.y,Tk)), softmax, . V; an empty range gives 0.
+ *   q [Tq, H*dk], k/v [Tk, H*dk], P [n_rel, H*dk], u/v [H, dk] (fp32), ranges int32 [Tq, 2],
+ *   out [Tq, H*dk]; all device pointers, dtype UD_F32 or UD_BF16 for q/k/v/P/out.
+ * Supported: dk in {16, 32, 64, 128}, Tq <= 16; rows 16-byte aligned.
+ * Rows referenced by a valid (i, j) pair must lie inside P (caller contract, as in the
+ * reference).  Asynchronous on hip_stream. */
+UD_API int ud_relpos_attention(int32_t dtype, const void* q_dev, const void* k_dev, const void* v_dev,
+                               const void* p_dev, const float* u_dev, const float* vb_dev,
+                               const int32_t* ranges_dev, void* out_dev, int32_t Tq, int32_t Tk,
+                               int32_t H, int32_t dk, int32_t rel_offset, int32_t n_rel,
+                               void* hip_stream);
+
+/* The streaming attention of one layer on its own, over the stream's ring caches: the fused
+ * kernel the step runs between the QKV projection and linear_out (FastConformer.swift:285-291 with
+ * the cache rule of :458-472).
+ *   qkv_dev  [n, T, 3*d_model] in the encoder dtype: q | k_new | v_new per row
+ *   att_dev  [n, T, d_model] in the encoder dtype
+ * Keys are [L cached ; T new], range [L - cache_len, L + valid); afterwards the T new K/V rows
+ * are in the ring and the logical window is the last L rows.  Does not advance cache_len or the
+ * ring position: call ud_stream_advance to commit the step (ud_encoder_step does both).
+ * Asynchronous on hip_stream. */
+UD_API int ud_layer_attention(ud_encoder* enc, ud_stream* const* streams, int32_t n, int32_t T,
+                              int32_t layer, const void* qkv_dev, const int32_t* valid_T_host,
+                              void* att_dev, void* hip_stream);
+
+/* Advances cache_len = min(cache_len + T, L), the ring positions and the step counter of each
+ * stream (FastConformer.swift:476-478).  Host-side bookkeeping only. */
+UD_API int ud_stream_advance(ud_stream* const* streams, int32_t n, int32_t T);
+
+/* Profiling hook (no reference counterpart; the reference times whole command buffers,
+ * Sources/DictatorEngine/Core/Kernels.swift:33-42): uploads the batch descriptor once, then
+ * launches the fused attention kernel of `layer` `iters` times back to back between two HIP events
+ * on hip_stream and returns the average kernel duration in milliseconds.  Every launch reads the
+ * same caches and writes the same T new rows to the same ring slots, so repeating it leaves the
+ * state as one ud_layer_attention call would.  Synchronizes hip_stream. */
+UD_API int ud_time_layer_attention(ud_encoder* enc, ud_stream* const* streams, int32_t n, int32_t T,
+                                   int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
+                                   void* hip_stream, float* avg_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UD_ENCODER_H */

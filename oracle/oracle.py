@@ -1,0 +1,224 @@
+"""ctypes binding of the CPU oracle (oracle/ud_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke entry point and by the benchmark's
+cpu_baseline leg, as the checker and the timed CPU baseline.  The product path never imports it.
+
+Each wrapper takes and returns float32/int32 numpy arrays (C-contiguous).  The reference file:line
+each function restates is in the C source.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "libud_oracle.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_lib = None
+
+# Per-layer weight order of the oracle (ConformerLayerWeights, FastConformer.swift:41-54), with the
+# NeMo state_dict suffix of each slot.
+WEIGHT_SUFFIXES = [
+    "norm_feed_forward1.weight", "norm_feed_forward1.bias", "feed_forward1.linear1.weight",
+    "feed_forward1.linear2.weight", "norm_self_att.weight", "norm_self_att.bias", "self_attn.linear_q.weight",
+    "self_attn.linear_k.weight", "self_attn.linear_v.weight", "self_attn.linear_out.weight",
+    "self_attn.linear_pos.weight", "self_attn.pos_bias_u", "self_attn.pos_bias_v", "norm_conv.weight",
+    "norm_conv.bias", "conv.pointwise_conv1.weight", "conv.depthwise_conv.weight", "conv.batch_norm.weight",
+    "conv.batch_norm.bias", "conv.pointwise_conv2.weight", "norm_feed_forward2.weight", "norm_feed_forward2.bias",
+    "feed_forward2.linear1.weight", "feed_forward2.linear2.weight", "norm_out.weight", "norm_out.bias",
+]
+
+ACT_NONE, ACT_RELU, ACT_SILU, ACT_GELU_ERF = 0, 1, 2, 4
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            import importlib.util
+            spec = importlib.util.spec_from_file_location("_ud_oracle_build", os.path.join(_HERE, "build.py"))
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            mod.build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        _lib.orc_bf16_bits.restype = ctypes.c_uint16
+        _lib.orc_bf16_bits.argtypes = [ctypes.c_float]
+        _lib.orc_bf16_to_float.restype = ctypes.c_float
+        _lib.orc_bf16_to_float.argtypes = [ctypes.c_uint16]
+        _lib.orc_weight_count.restype = ctypes.c_int
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(_f32p) if a is not None else None
+
+
+def _ip(a):
+    return a.ctypes.data_as(_i32p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def set_threads(n):
+    """Sets the OpenMP thread count of the oracle (the CPU baseline's core count)."""
+    os.environ["OMP_NUM_THREADS"] = str(n)
+    try:
+        ctypes.CDLL("libgomp.so.1").omp_set_num_threads(int(n))
+    except OSError:
+        pass
+
+
+def lcg_floats(n, seed):
+    out = np.empty(n, np.float32)
+    lib().orc_lcg_floats(_p(out), ctypes.c_int64(n), ctypes.c_uint64(seed))
+    return out
+
+
+def bf16_bits(x):
+    x = _f32(x).ravel()
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_to_bf16(_p(x), out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), ctypes.c_int64(x.size))
+    return out
+
+
+def round_bf16(x):
+    x = _f32(x).copy()
+    lib().orc_round_bf16(_p(x), ctypes.c_int64(x.size))
+    return x
+
+
+def layer_norm(x, g, b, eps=1e-5, act=ACT_NONE):
+    x = _f32(x)
+    D = x.shape[-1]
+    out = np.empty_like(x)
+    lib().orc_layer_norm(_p(x), _p(_f32(g)), _p(_f32(b)) if b is not None else None, _p(out),
+                         ctypes.c_int64(x.size // D), D, ctypes.c_float(eps), act)
+    return out
+
+
+def gemm_nt(A, W, bias=None, R=None, alpha=1.0, act=ACT_NONE, out_scale=1.0, res_scale=1.0):
+    A, W = _f32(A), _f32(W)
+    M, K = A.shape
+    N = W.shape[0]
+    C = np.empty((M, N), np.float32)
+    lib().orc_gemm_nt(_p(A), _p(W), _p(_f32(bias)) if bias is not None else None,
+                      _p(_f32(R)) if R is not None else None, _p(C), M, N, K, ctypes.c_float(alpha), act,
+                      ctypes.c_float(out_scale), ctypes.c_float(res_scale))
+    return C
+
+
+def glu(x):
+    x = _f32(x)
+    T, D2 = x.shape
+    out = np.empty((T, D2 // 2), np.float32)
+    lib().orc_glu(_p(x), _p(out), ctypes.c_int64(T), D2 // 2)
+    return out
+
+
+def dwconv1d(x, w, bias=None, act=ACT_NONE):
+    x, w = _f32(x), _f32(w)
+    D, K = w.shape
+    Tout = x.shape[0] - K + 1
+    out = np.empty((Tout, D), np.float32)
+    lib().orc_dwconv1d(_p(x), _p(w), _p(_f32(bias)) if bias is not None else None, _p(out), Tout, D, K, act)
+    return out
+
+
+def sinusoid(pos, D):
+    out = np.empty(D, np.float32)
+    lib().orc_sinusoid(int(pos), D, _p(out))
+    return out
+
+
+def pe_rows(lo, hi, D):
+    out = np.empty((hi - lo + 1, D), np.float32)
+    lib().orc_pe_rows(lo, hi, D, _p(out))
+    return out
+
+
+def pos_table(wpos, lo, hi):
+    wpos = _f32(wpos)
+    D = wpos.shape[0]
+    P = np.empty((hi - lo + 1, D), np.float32)
+    lib().orc_pos_table(_p(wpos), lo, hi, D, _p(P))
+    return P
+
+
+def relpos_attention(q, k, v, P, u, vb, ranges, rel_offset, H):
+    """q [Tq, H*dk], k/v [Tk, H*dk], P [n_rel, H*dk], u/vb [H, dk], ranges int32 [Tq, 2]."""
+    q, k, v, P = _f32(q), _f32(k), _f32(v), _f32(P)
+    Tq, HD = q.shape
+    Tk = k.shape[0]
+    dk = HD // H
+    out = np.empty_like(q)
+    rr = np.ascontiguousarray(ranges, dtype=np.int32)
+    lib().orc_relpos_attention(_p(q), _p(k), _p(v), _p(P), _p(_f32(u)), _p(_f32(vb)), _ip(rr), _p(out),
+                               Tq, Tk, H, dk, HD, HD, HD, HD, rel_offset, P.shape[0],
+                               ctypes.c_float(1.0 / np.sqrt(np.float32(dk))))
+    return out
+
+
+def chunked_limited_ranges(T, left, right):
+    r = np.empty((T, 2), np.int32)
+    lib().orc_chunked_limited_ranges(T, left, right, _ip(r))
+    return r
+
+
+class Model:
+    """Oracle-side model: per-layer fp32 weight arrays (keyed by NeMo suffix) and the position
+    tables P_l over rel = lo..hi (FastConformer.swift:161-178)."""
+
+    def __init__(self, layer_weights, D, H, ff, Kc):
+        self.layers = [[_f32(lw[s]) for s in WEIGHT_SUFFIXES] for lw in layer_weights]
+        self.D, self.H, self.ff, self.Kc = D, H, ff, Kc
+        self._ptrs = None
+        self.P = None
+
+    def prepare(self, lo, hi):
+        D = self.D
+        self.lo, self.hi = lo, hi
+        self.rel_offset = -lo
+        self.P = [pos_table(lw[WEIGHT_SUFFIXES.index("self_attn.linear_pos.weight")], lo, hi) for lw in self.layers]
+        flat = [w for lw in self.layers for w in lw]
+        self._keep = flat
+        self._wptrs = (_f32p * len(flat))(*[_p(w) for w in flat])
+        self._pptrs = (_f32p * len(self.P))(*[_p(p) for p in self.P])
+        return self
+
+    @property
+    def n_rel(self):
+        return self.P[0].shape[0]
+
+
+def stream_step(model, x, valid, kcache, vcache, ccache, cache_len):
+    """encodeStreamStep for S streams (FastConformer.swift:441-480).
+
+    x [S, T, D]; valid int32 [S]; kcache/vcache [S, layers, L, D]; ccache [S, layers, K-1, D];
+    cache_len int32 [S].  The caches and cache_len are updated in place; returns out [S, T, D]."""
+    x = _f32(x)
+    S, T, D = x.shape
+    layers = len(model.layers)
+    L = kcache.shape[2]
+    for a in (kcache, vcache, ccache):
+        assert a.dtype == np.float32 and a.flags.c_contiguous
+    assert cache_len.dtype == np.int32
+    out = np.empty_like(x)
+    lib().orc_stream_step(model._wptrs, model._pptrs, model.rel_offset, model.n_rel, layers, S, T, L, D,
+                          model.H, model.ff, model.Kc, _p(x), _ip(np.ascontiguousarray(valid, np.int32)),
+                          _p(kcache), _p(vcache), _p(ccache), _ip(cache_len), _p(out))
+    return out
+
+
+def encoder_offline(model, x, ranges, valid):
+    """forwardOffline after the subsampling (FastConformer.swift:361-398); x [T, D], ranges [T, 2]."""
+    x = _f32(x)
+    T, D = x.shape
+    out = np.empty_like(x)
+    lib().orc_encoder_offline(model._wptrs, model._pptrs, model.rel_offset, model.n_rel, len(model.layers), T, D,
+                              model.H, model.ff, model.Kc, _p(x), _ip(np.ascontiguousarray(ranges, np.int32)),
+                              int(valid), _p(out))
+    return out

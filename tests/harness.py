@@ -1,0 +1,72 @@
+"""Shared set-up for GPU parity tests: the same seeded weights go to the HIP encoder and to the
+oracle (fp32 activations; in bf16 mode the oracle gets the bf16-rounded linear weights that the
+encoder stores, which is the reference's own bf16-weight setting, Core/Kernels.swift:79-112)."""
+import numpy as np
+
+# Linear weights that a bf16 encoder stores in bf16 (the rest stay fp32: norms, pos_bias, depthwise
+# conv -- Sources/DictatorEngine/Core/Convert.swift:76-83).
+BF16_WEIGHTS = {
+    "feed_forward1.linear1.weight", "feed_forward1.linear2.weight", "self_attn.linear_q.weight",
+    "self_attn.linear_k.weight", "self_attn.linear_v.weight", "self_attn.linear_out.weight",
+    "self_attn.linear_pos.weight", "conv.pointwise_conv1.weight", "conv.pointwise_conv2.weight",
+    "feed_forward2.linear1.weight", "feed_forward2.linear2.weight",
+}
+
+
+def make_encoder(ud, orc, cfg, seed=1234, ln_jitter=0.1):
+    lw = [ud.synthetic_layer_weights(cfg, seed, l, ln_jitter=ln_jitter) for l in range(cfg.layers)]
+    enc = ud.Encoder(cfg)
+    for l, w in enumerate(lw):
+        enc.set_layer_weights(l, w)
+    enc.finalize()
+    if cfg.dtype == "bf16":
+        lw = [{k: (ud.round_bf16(v) if k in BF16_WEIGHTS else v) for k, v in w.items()} for w in lw]
+    model = orc.Model(lw, cfg.d_model, cfg.heads, cfg.ff_dim, cfg.conv_kernel)
+    model.prepare(-(cfg.max_chunk - 1), cfg.left_context + cfg.max_chunk - 1)
+    return enc, model, lw
+
+
+def rel_err(got, ref):
+    """Max abs error relative to max |ref| (the fp32 path's <= 1e-4 bar)."""
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def cosine(a, b):
+    a = a.ravel().astype(np.float64)
+    b = b.ravel().astype(np.float64)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b) + 1e-300))
+
+
+def assert_bf16_close(got, ref, what=""):
+    """The bf16 bar: max abs error <= 2e-2 and cosine >= 0.9995."""
+    err = float(np.abs(got - ref).max())
+    cos = cosine(got, ref)
+    assert err <= 2e-2 and cos >= 0.9995, "%s: max abs err %.3g, cosine %.6f" % (what, err, cos)
+    return err, cos
+
+
+class OracleState:
+    """Oracle-side caches of S streams in logical order."""
+
+    def __init__(self, S, cfg):
+        L, D, KC = cfg.left_context, cfg.d_model, cfg.conv_kernel - 1
+        self.k = np.zeros((S, cfg.layers, L, D), np.float32)
+        self.v = np.zeros((S, cfg.layers, L, D), np.float32)
+        self.c = np.zeros((S, cfg.layers, KC, D), np.float32)
+        self.len = np.zeros(S, np.int32)
+
+    def seed_random(self, rng, cache_len):
+        self.k[:] = rng.standard_normal(self.k.shape, dtype=np.float32)
+        self.v[:] = rng.standard_normal(self.v.shape, dtype=np.float32)
+        self.c[:] = rng.standard_normal(self.c.shape, dtype=np.float32)
+        self.len[:] = cache_len
+
+    def import_into(self, streams, ud, bf16):
+        """Loads these caches into the encoder's streams (bf16 caches are rounded on import, so the
+        oracle copy is rounded the same way)."""
+        if bf16:
+            self.k[:] = ud.round_bf16(self.k)
+            self.v[:] = ud.round_bf16(self.v)
+        for s, st in enumerate(streams):
+            for l in range(self.k.shape[1]):
+                st.import_cache(l, self.k[s, l], self.v[s, l], self.c[s, l], int(self.len[s]))

@@ -1,0 +1,84 @@
+"""Independent checkers used to pin the oracle (tests only).
+
+These restate NeMo's modules with torch/numpy library routines in float64, in the structure NeMo
+uses rather than the oracle's: rel_shift is the literal pad/view trick
+(Tests/DictatorEngineTests/ConformerOpTests.swift:111-122; reference/nemo/check_spec.py:143-146),
+the depthwise conv is torch conv1d with causal left padding, masks are boolean matrices filled
+with -10000 before softmax and zeroed after (docs/specs/nemotron.md §3).
+"""
+import numpy as np
+
+
+def nemo_rel_shift(x):
+    """NeMo RelPositionMultiHeadAttention.rel_shift on x [..., Tq, nPos] (numpy or torch): pad one
+    zero column on the left, view as [..., nPos+1, Tq], drop the first row, view back as
+    [..., Tq, nPos]."""
+    *lead, tq, npos = x.shape
+    if isinstance(x, np.ndarray):
+        pad = np.concatenate([np.zeros((*lead, tq, 1), x.dtype), x], axis=-1)
+    else:
+        import torch.nn.functional as F
+        pad = F.pad(x, (1, 0))
+    pad = pad.reshape(*lead, npos + 1, tq)
+    return pad[..., 1:, :].reshape(*lead, tq, npos)
+
+
+def nemo_pe(T, D):
+    """NeMo RelPositionalEncoding rows for positions T-1 ... -(T-1) (row r = position T-1-r), in
+    float64 closed form."""
+    pos = np.arange(T - 1, -T, -1, dtype=np.float64)[:, None]
+    div = np.exp(np.arange(0, D, 2, dtype=np.float64) * -(np.log(10000.0) / D))
+    pe = np.zeros((2 * T - 1, D))
+    pe[:, 0::2] = np.sin(pos * div)
+    pe[:, 1::2] = np.cos(pos * div)
+    return pe
+
+
+def layer_nemo(x, w, pe, mask, valid, H, Kc=9):
+    """One NeMo ConformerLayer (conformer_modules.py:160-233 per docs/specs/nemotron.md §3) on a
+    full utterance x [T, D] (float64 torch).  pe: projected-input table rows for positions
+    T-1..-(T-1) [2T-1, D]; mask [T, T] bool, True = hidden; rows >= valid are padding."""
+    import torch
+    import torch.nn.functional as F
+    T, D = x.shape
+    dk = D // H
+    t = lambda k: torch.as_tensor(w[k], dtype=torch.float64)
+    ln = lambda y, n: F.layer_norm(y, (D,), t(n + ".weight"), t(n + ".bias"), eps=1e-5)
+    r = x + 0.5 * F.linear(F.silu(F.linear(ln(x, "norm_feed_forward1"), t("feed_forward1.linear1.weight"))),
+                           t("feed_forward1.linear2.weight"))
+    z = ln(r, "norm_self_att")
+    q = F.linear(z, t("self_attn.linear_q.weight")).view(T, H, dk).transpose(0, 1)
+    k = F.linear(z, t("self_attn.linear_k.weight")).view(T, H, dk).transpose(0, 1)
+    v = F.linear(z, t("self_attn.linear_v.weight")).view(T, H, dk).transpose(0, 1)
+    p = F.linear(torch.as_tensor(pe), t("self_attn.linear_pos.weight")).view(2 * T - 1, H, dk).transpose(0, 1)
+    qu = q + t("self_attn.pos_bias_u").view(H, 1, dk)
+    qv = q + t("self_attn.pos_bias_v").view(H, 1, dk)
+    ac = qu @ k.transpose(1, 2)
+    bd = nemo_rel_shift(qv @ p.transpose(1, 2))[:, :, :T]
+    s = (ac + bd) / np.sqrt(dk)
+    m = torch.as_tensor(mask)
+    s = s.masked_fill(m, -10000.0)
+    a = torch.softmax(s, dim=-1).masked_fill(m, 0.0)
+    o = (a @ v).transpose(0, 1).reshape(T, D)
+    r = r + F.linear(o, t("self_attn.linear_out.weight"))
+    z = ln(r, "norm_conv")
+    g = F.glu(F.linear(z, t("conv.pointwise_conv1.weight")), dim=-1)
+    g[valid:] = 0.0
+    dw = t("conv.depthwise_conv.weight").view(D, 1, Kc)
+    c = F.conv1d(F.pad(g.T.unsqueeze(0), (Kc - 1, 0)), dw, groups=D)[0].T
+    c = F.silu(F.layer_norm(c, (D,), t("conv.batch_norm.weight"), t("conv.batch_norm.bias"), eps=1e-5))
+    r = r + F.linear(c, t("conv.pointwise_conv2.weight"))
+    r = r + 0.5 * F.linear(F.silu(F.linear(ln(r, "norm_feed_forward2"), t("feed_forward2.linear1.weight"))),
+                           t("feed_forward2.linear2.weight"))
+    return ln(r, "norm_out")
+
+
+def chunked_limited_mask(T, left, right, valid):
+    """NeMo chunked_limited visibility (conformer_encoder.py:803-822 per docs/specs/nemotron.md §4):
+    visible(i,j) = 0 <= i//chunk - j//chunk <= left//chunk; keys >= valid hidden.  True = hidden."""
+    cs = right + 1
+    i = np.arange(T)[:, None] // cs
+    j = np.arange(T)[None, :] // cs
+    vis = (i - j >= 0) & (i - j <= left // cs)
+    vis &= np.arange(T)[None, :] < valid
+    return ~vis

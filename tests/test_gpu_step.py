@@ -1,0 +1,150 @@
+"""GPU parity of the whole cache-aware encoder step (ud_encoder_step) against the oracle's
+encodeStreamStep, over several consecutive steps: fresh and full caches, valid < T, fp32 and bf16,
+the 64-stream chunk-2 shape and the chunk-14 shape, graph replay vs eager launches, error paths."""
+import os
+
+import numpy as np
+import pytest
+
+import harness
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_steps(ud, orc, cfg, S, T, n_steps, seed, seed_caches, valid_plan=None, enc_model=None):
+    enc, model, _ = enc_model or harness.make_encoder(ud, orc, cfg, seed=seed)
+    rng = np.random.default_rng(seed + 1)
+    streams = [enc.new_stream() for _ in range(S)]
+    st = harness.OracleState(S, cfg)
+    if seed_caches:
+        st.seed_random(rng, cfg.left_context)
+        st.import_into(streams, ud, cfg.dtype == "bf16")
+    D = cfg.d_model
+    xbuf = ud.DeviceBuffer(S * T * D * 4)
+    obuf = ud.DeviceBuffer(S * T * D * 4)
+    results = []
+    for step in range(n_steps):
+        x = rng.standard_normal((S, T, D)).astype(np.float32)
+        valid = np.full(S, T, np.int32) if valid_plan is None else np.asarray(valid_plan(step, S, T), np.int32)
+        xbuf.upload(x)
+        enc.encode_stream_step(streams, xbuf, obuf, valid=valid, T=T)
+        got = obuf.download((S, T, D))
+        ref = orc.stream_step(model, x, valid, st.k, st.v, st.c, st.len)
+        results.append((got, ref))
+        for s, stream in enumerate(streams):
+            assert stream.cache_len == st.len[s]
+    return enc, streams, st, results
+
+
+def test_step_fp32_two_layers_fresh_streams(gpu, orc):
+    cfg = gpu.EncoderConfig(layers=2, max_chunk=2, max_streams=4, dtype="f32")
+    plan = lambda step, S, T: [T, 1 if step == 2 else T, 0 if step == 3 else T]
+    enc, streams, st, res = _run_steps(gpu, orc, cfg, S=3, T=2, n_steps=5, seed=21, seed_caches=False,
+                                       valid_plan=plan)
+    for i, (got, ref) in enumerate(res):
+        assert harness.rel_err(got, ref) <= 1e-4, i
+    # the caches after the steps match the oracle's (computed values, fp32 tolerance)
+    for s, stream in enumerate(streams):
+        for l in range(cfg.layers):
+            k, v, c, n = stream.export_cache(l)
+            assert n == st.len[s]
+            assert harness.rel_err(k, st.k[s, l]) <= 1e-4
+            assert harness.rel_err(v, st.v[s, l]) <= 1e-4
+            assert harness.rel_err(c, st.c[s, l]) <= 1e-4
+    enc.close()
+
+
+def test_step_fp32_full_cache_chunk5(gpu, orc):
+    cfg = gpu.EncoderConfig(layers=2, max_chunk=5, max_streams=2, dtype="f32")
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=2, T=5, n_steps=3, seed=31, seed_caches=True)
+    for i, (got, ref) in enumerate(res):
+        assert harness.rel_err(got, ref) <= 1e-4, i
+    enc.close()
+
+
+def test_step_bf16_64_streams_chunk2(gpu, orc):
+    """Config 2's shape (64 streams x 2 frames, L=70, seeded full caches) over 4 layers."""
+    cfg = gpu.EncoderConfig(layers=4, max_chunk=2, max_streams=64, dtype="bf16")
+    plan = lambda step, S, T: [T - (s % 3 == 1 and step == 1) for s in range(S)]
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=64, T=2, n_steps=3, seed=41, seed_caches=True, valid_plan=plan)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
+def test_step_bf16_24_layers(gpu, orc):
+    """Full depth: bf16 error accumulated over 24 layers stays within 2e-2 abs / cosine 0.9995."""
+    cfg = gpu.EncoderConfig(layers=24, max_chunk=2, max_streams=4, dtype="bf16")
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=4, T=2, n_steps=2, seed=51, seed_caches=True)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
+def test_step_bf16_chunk14(gpu, orc):
+    """Config 3's chunk shape (14 frames, 84 keys) on a few streams."""
+    cfg = gpu.EncoderConfig(layers=2, max_chunk=14, max_streams=8, dtype="bf16")
+    plan = lambda step, S, T: [T, 9, T, 0, T, T, 3, T][:S]
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=8, T=14, n_steps=3, seed=61, seed_caches=True, valid_plan=plan)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
+def test_graph_replay_matches_eager(gpu, orc):
+    """The captured hipGraph replay gives bit-identical results to eager launches."""
+    outs = []
+    for graphs in ("1", "0"):
+        os.environ["UD_GRAPHS"] = graphs
+        try:
+            cfg = gpu.EncoderConfig(layers=2, max_chunk=2, max_streams=8, dtype="bf16")
+            enc, _, _, res = _run_steps(gpu, orc, cfg, S=8, T=2, n_steps=3, seed=71, seed_caches=True)
+            outs.append([g for g, _ in res])
+            enc.close()
+        finally:
+            os.environ.pop("UD_GRAPHS", None)
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_error_paths(gpu, orc):
+    ud = gpu
+    cfg = ud.EncoderConfig(layers=1, max_chunk=2, max_streams=2, dtype="bf16")
+    enc = ud.Encoder(cfg)
+    s0 = enc.new_stream()
+    x = ud.DeviceBuffer(2 * 1024 * 4)
+    o = ud.DeviceBuffer(2 * 1024 * 4)
+    with pytest.raises(ud.EngineError) as e:
+        enc.encode_stream_step([s0], x, o, T=2)
+    assert e.value.status == -5                      # not finalized
+    with pytest.raises(ud.EngineError) as e:
+        enc.set_weight("encoder.layers.0.no_such.weight", np.zeros(4, np.float32))
+    assert e.value.status == -6
+    with pytest.raises(ud.EngineError) as e:
+        enc.set_weight("encoder.layers.0.norm_out.weight", np.zeros(5, np.float32))
+    assert e.value.status == -6
+    with pytest.raises(ud.EngineError) as e:
+        enc.finalize()                               # weights missing
+    assert e.value.status == -5
+    for l, w in enumerate([ud.synthetic_layer_weights(cfg, 1, 0)]):
+        enc.set_layer_weights(l, w)
+    enc.finalize()
+    s1 = enc.new_stream()
+    with pytest.raises(ud.EngineError) as e:
+        enc.new_stream()
+    assert e.value.status == -7                      # pool exhausted
+    with pytest.raises(ud.EngineError) as e:
+        enc.encode_stream_step([s0, s0], x, o, T=1)
+    assert e.value.status == -1                      # duplicate stream
+    with pytest.raises(ud.EngineError) as e:
+        enc.encode_stream_step([s0], x, o, T=3)
+    assert e.value.status == -2                      # T > max_chunk
+    with pytest.raises(ud.EngineError) as e:
+        enc.encode_stream_step([s0], x, x, T=1)
+    assert e.value.status == -1                      # aliasing
+    enc.encode_stream_step([s0, s1], x, o, T=1)
+    ud.synchronize()
+    assert s0.cache_len == 1 and s0.step == 1
+    s0.reset()
+    assert s0.cache_len == 0 and s0.step == 0
+    enc.close()

@@ -1,0 +1,433 @@
+"""Host-side binding of the MI355X (gfx950) streaming FastConformer encoder step.
+
+Mirrors the reference's encoder-step interface over the C ABI in include/ud_encoder.h:
+
+  Encoder            FastConformerEncoder (Sources/DictatorEngine/Models/FastConformer.swift:62-144)
+  Encoder.new_stream FastConformerEncoder.makeStreamState (FastConformer.swift:431-435)
+  Encoder.encode_stream_step
+                     encodeStreamStep (FastConformer.swift:441-480), batched over streams
+  rel_pos_attention  Step.relPosAttention (Sources/DictatorEngine/Core/Ops.swift:80-90)
+  EngineError        EngineError.io (Sources/DictatorCore/Errors.swift:3-11)
+
+All compute runs in libud_encoder.so (hand-written HIP for gfx950).  There is no CPU fallback:
+loading raises EngineError when the library is missing or no HIP device is present.
+Device buffers are DeviceBuffer objects (HBM allocations owned by the library's allocator).
+"""
+import ctypes
+import dataclasses
+import os
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libud_encoder.so")
+INCLUDE_DIR = os.path.join(os.path.dirname(PKG_DIR), "include")
+
+UD_F32, UD_BF16 = 0, 1
+_DTYPES = {"f32": UD_F32, "fp32": UD_F32, "float32": UD_F32, "bf16": UD_BF16, "bfloat16": UD_BF16}
+
+STATUS = {0: "ok", -1: "invalid argument", -2: "shape", -3: "out of memory", -4: "HIP error", -5: "state",
+          -6: "weight", -7: "capacity"}
+
+
+class EngineError(RuntimeError):
+    """A failed library call: status code and the library's message (EngineError.io)."""
+
+    def __init__(self, status, message):
+        super().__init__("%s (%d): %s" % (STATUS.get(status, "error"), status, message))
+        self.status = status
+
+
+class _Config(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("layers", "d_model", "heads", "ff_dim", "conv_kernel",
+                                               "left_context", "max_chunk", "max_streams", "dtype")]
+
+
+_lib = None
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+
+
+def _sig(lib):
+    i, v, p, f = ctypes.c_int, None, _vp, ctypes.POINTER(ctypes.c_float)
+    ip = ctypes.POINTER(_i32)
+    sigs = {
+        "ud_last_error": (ctypes.c_char_p, []),
+        "ud_encoder_create": (i, [ctypes.POINTER(_Config), ctypes.POINTER(_vp)]),
+        "ud_encoder_destroy": (v, [p]),
+        "ud_encoder_set_weight": (i, [p, ctypes.c_char_p, f, ctypes.c_int64]),
+        "ud_encoder_finalize": (i, [p]),
+        "ud_stream_create": (i, [p, ctypes.POINTER(_vp)]),
+        "ud_stream_reset": (i, [p]),
+        "ud_stream_destroy": (v, [p]),
+        "ud_stream_info": (i, [p, ip, ip]),
+        "ud_encoder_step": (i, [p, ctypes.POINTER(_vp), _i32, _i32, p, ip, p, p]),
+        "ud_stream_export_cache": (i, [p, _i32, f, f, f, ip]),
+        "ud_stream_import_cache": (i, [p, _i32, f, f, f, _i32]),
+        "ud_relpos_attention": (i, [_i32, p, p, p, p, p, p, p, p, _i32, _i32, _i32, _i32, _i32, _i32, p]),
+        "ud_layer_attention": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, ip, p, p]),
+        "ud_stream_advance": (i, [ctypes.POINTER(_vp), _i32, _i32]),
+        "ud_time_layer_attention": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, p, _i32, p, f]),
+        "ud_device_count": (i, [ip]),
+        "ud_device_arch": (i, [ctypes.c_char_p, _i32]),
+        "ud_malloc": (i, [ctypes.POINTER(_vp), ctypes.c_size_t]),
+        "ud_free": (i, [p]),
+        "ud_memcpy_htod": (i, [p, p, ctypes.c_size_t]),
+        "ud_memcpy_dtoh": (i, [p, p, ctypes.c_size_t]),
+        "ud_memcpy_dtod": (i, [p, p, ctypes.c_size_t]),
+        "ud_memset": (i, [p, _i32, ctypes.c_size_t]),
+        "ud_device_synchronize": (i, []),
+        "ud_hip_stream_create": (i, [ctypes.POINTER(_vp)]),
+        "ud_hip_stream_destroy": (i, [p]),
+        "ud_hip_stream_synchronize": (i, [p]),
+        "ud_event_create": (i, [ctypes.POINTER(_vp)]),
+        "ud_event_destroy": (i, [p]),
+        "ud_event_record": (i, [p, p]),
+        "ud_event_synchronize": (i, [p]),
+        "ud_event_elapsed_ms": (i, [f, p, p]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def load_library(path=LIB_PATH):
+    """Loads libud_encoder.so (no device check).  Raises EngineError if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise EngineError(-5, "libud_encoder.so is not built (run universal-dictator_amd/build.py): " + path)
+        _lib = _sig(ctypes.CDLL(path))
+    return _lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise EngineError(rc, (_lib.ud_last_error() or b"").decode())
+
+
+def lib():
+    """The library, after checking that a HIP device is present."""
+    l = load_library()
+    n = _i32(0)
+    rc = l.ud_device_count(ctypes.byref(n))
+    if rc != 0 or n.value < 1:
+        raise EngineError(-4, "no HIP device visible: the encoder step runs only on the GPU")
+    return l
+
+
+def device_arch():
+    buf = ctypes.create_string_buffer(64)
+    _check(lib().ud_device_arch(buf, 64))
+    return buf.value.decode()
+
+
+def synchronize():
+    _check(lib().ud_device_synchronize())
+
+
+# ---------------------------------------------------------------- device memory, streams, events
+
+class DeviceBuffer:
+    """An HBM allocation."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        p = _vp()
+        _check(lib().ud_malloc(ctypes.byref(p), self.nbytes))
+        self.ptr = p.value
+
+    @classmethod
+    def from_numpy(cls, a):
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    @classmethod
+    def zeros(cls, nbytes):
+        b = cls(nbytes)
+        _check(lib().ud_memset(b.ptr, 0, b.nbytes))
+        return b
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise EngineError(-2, "upload of %d bytes into a %d-byte buffer" % (a.nbytes, self.nbytes))
+        _check(_lib.ud_memcpy_htod(self.ptr, a.ctypes.data, a.nbytes))
+
+    def download(self, shape, dtype=np.float32):
+        out = np.empty(shape, dtype)
+        if out.nbytes > self.nbytes:
+            raise EngineError(-2, "download of %d bytes from a %d-byte buffer" % (out.nbytes, self.nbytes))
+        _check(_lib.ud_memcpy_dtoh(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            _lib.ud_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HipStream:
+    def __init__(self):
+        p = _vp()
+        _check(lib().ud_hip_stream_create(ctypes.byref(p)))
+        self.ptr = p.value
+
+    def synchronize(self):
+        _check(_lib.ud_hip_stream_synchronize(self.ptr))
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                _lib.ud_hip_stream_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        p = _vp()
+        _check(lib().ud_event_create(ctypes.byref(p)))
+        self.ptr = p.value
+
+    def record(self, stream=None):
+        _check(_lib.ud_event_record(self.ptr, stream.ptr if stream else None))
+
+    def synchronize(self):
+        _check(_lib.ud_event_synchronize(self.ptr))
+
+    def elapsed_ms(self, end):
+        ms = ctypes.c_float(0)
+        _check(_lib.ud_event_elapsed_ms(ctypes.byref(ms), self.ptr, end.ptr))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                _lib.ud_event_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------- encoder
+
+@dataclasses.dataclass
+class EncoderConfig:
+    """FastConformerConfig.nemotron (FastConformer.swift:5-38) plus streaming geometry."""
+    layers: int = 24
+    d_model: int = 1024
+    heads: int = 8
+    ff_dim: int = 4096
+    conv_kernel: int = 9
+    left_context: int = 70
+    max_chunk: int = 2
+    max_streams: int = 64
+    dtype: str = "bf16"
+
+    def _c(self):
+        return _Config(self.layers, self.d_model, self.heads, self.ff_dim, self.conv_kernel, self.left_context,
+                       self.max_chunk, self.max_streams, _DTYPES[self.dtype])
+
+
+LAYER_WEIGHT_SUFFIXES = (
+    "norm_feed_forward1.weight", "norm_feed_forward1.bias", "feed_forward1.linear1.weight",
+    "feed_forward1.linear2.weight", "norm_self_att.weight", "norm_self_att.bias", "self_attn.linear_q.weight",
+    "self_attn.linear_k.weight", "self_attn.linear_v.weight", "self_attn.linear_out.weight",
+    "self_attn.linear_pos.weight", "self_attn.pos_bias_u", "self_attn.pos_bias_v", "norm_conv.weight",
+    "norm_conv.bias", "conv.pointwise_conv1.weight", "conv.depthwise_conv.weight", "conv.batch_norm.weight",
+    "conv.batch_norm.bias", "conv.pointwise_conv2.weight", "norm_feed_forward2.weight", "norm_feed_forward2.bias",
+    "feed_forward2.linear1.weight", "feed_forward2.linear2.weight", "norm_out.weight", "norm_out.bias",
+)
+
+
+class Stream:
+    """One audio stream's encoder state (StreamState, FastConformer.swift:406-429)."""
+
+    def __init__(self, encoder):
+        self.encoder = encoder
+        p = _vp()
+        _check(lib().ud_stream_create(encoder.handle, ctypes.byref(p)))
+        self.handle = p.value
+
+    @property
+    def cache_len(self):
+        c, s = _i32(0), _i32(0)
+        _check(_lib.ud_stream_info(self.handle, ctypes.byref(c), ctypes.byref(s)))
+        return c.value
+
+    @property
+    def step(self):
+        c, s = _i32(0), _i32(0)
+        _check(_lib.ud_stream_info(self.handle, ctypes.byref(c), ctypes.byref(s)))
+        return s.value
+
+    def reset(self):
+        _check(_lib.ud_stream_reset(self.handle))
+
+    def export_cache(self, layer):
+        """(k [L, D], v [L, D], conv [K-1, D], cache_len) in logical order, fp32."""
+        cfg = self.encoder.config
+        L, D, KC = cfg.left_context, cfg.d_model, cfg.conv_kernel - 1
+        k = np.empty((L, D), np.float32)
+        v = np.empty((L, D), np.float32)
+        c = np.empty((KC, D), np.float32)
+        n = _i32(0)
+        fp = ctypes.POINTER(ctypes.c_float)
+        _check(_lib.ud_stream_export_cache(self.handle, layer, k.ctypes.data_as(fp), v.ctypes.data_as(fp),
+                                           c.ctypes.data_as(fp), ctypes.byref(n)))
+        return k, v, c, n.value
+
+    def import_cache(self, layer, k, v, conv, cache_len):
+        fp = ctypes.POINTER(ctypes.c_float)
+        k, v, conv = (np.ascontiguousarray(a, np.float32) for a in (k, v, conv))
+        _check(_lib.ud_stream_import_cache(self.handle, layer, k.ctypes.data_as(fp), v.ctypes.data_as(fp),
+                                           conv.ctypes.data_as(fp), int(cache_len)))
+
+    def close(self):
+        if self.handle:
+            _lib.ud_stream_destroy(self.handle)
+            self.handle = None
+
+
+def _handles(streams):
+    arr = (_vp * len(streams))(*[s.handle for s in streams])
+    return arr
+
+
+def _valid_arr(valid, n, T):
+    if valid is None:
+        valid = [T] * n
+    return np.ascontiguousarray(valid, np.int32)
+
+
+class Encoder:
+    """Device weights, position tables, workspace and stream pool of one encoder."""
+
+    def __init__(self, config=None):
+        self.config = config or EncoderConfig()
+        p = _vp()
+        c = self.config._c()
+        _check(lib().ud_encoder_create(ctypes.byref(c), ctypes.byref(p)))
+        self.handle = p.value
+
+    def set_weight(self, name, array):
+        a = np.ascontiguousarray(array, np.float32)
+        _check(_lib.ud_encoder_set_weight(self.handle, name.encode(), a.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                          a.size))
+
+    def set_layer_weights(self, layer, weights):
+        """weights: dict NeMo-suffix -> array (as synthetic_layer_weights returns)."""
+        for suffix, a in weights.items():
+            self.set_weight("encoder.layers.%d.%s" % (layer, suffix), a)
+
+    def finalize(self):
+        _check(_lib.ud_encoder_finalize(self.handle))
+
+    def new_stream(self):
+        return Stream(self)
+
+    def encode_stream_step(self, streams, x, out, valid=None, T=None, hip_stream=None):
+        """One chunk step for `streams`: x/out are DeviceBuffers of fp32 [n, T, d_model]."""
+        n = len(streams)
+        T = T or x.nbytes // (4 * n * self.config.d_model)
+        va = _valid_arr(valid, n, T)
+        _check(_lib.ud_encoder_step(self.handle, _handles(streams), n, T, x.ptr,
+                                    va.ctypes.data_as(ctypes.POINTER(_i32)), out.ptr,
+                                    hip_stream.ptr if hip_stream else None))
+
+    def layer_attention(self, streams, T, layer, qkv, att, valid=None, hip_stream=None):
+        n = len(streams)
+        va = _valid_arr(valid, n, T)
+        _check(_lib.ud_layer_attention(self.handle, _handles(streams), n, T, layer, qkv.ptr,
+                                       va.ctypes.data_as(ctypes.POINTER(_i32)), att.ptr,
+                                       hip_stream.ptr if hip_stream else None))
+
+    def time_layer_attention(self, streams, T, layer, qkv, att, iters, hip_stream=None):
+        """Average duration (ms) of the fused attention kernel over `iters` back-to-back launches,
+        from HIP events on hip_stream."""
+        ms = ctypes.c_float(0)
+        _check(_lib.ud_time_layer_attention(self.handle, _handles(streams), len(streams), T, layer, qkv.ptr, att.ptr,
+                                            iters, hip_stream.ptr if hip_stream else None, ctypes.byref(ms)))
+        return ms.value
+
+    @staticmethod
+    def advance(streams, T):
+        _check(_lib.ud_stream_advance(_handles(streams), len(streams), T))
+
+    def close(self):
+        if self.handle:
+            _lib.ud_encoder_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def rel_pos_attention(q, k, v, pos_table, rel_offset, bias_u, bias_v, ranges, out, heads, Tq, Tk, head_dim,
+                      n_rel, dtype="f32", hip_stream=None):
+    """Step.relPosAttention (Ops.swift:80-90) on DeviceBuffers: q [Tq, H*dk], k/v [Tk, H*dk],
+    pos_table [n_rel, H*dk] (dtype f32 or bf16), bias_u/bias_v fp32 [H, dk], ranges int32 [Tq, 2]."""
+    _check(lib().ud_relpos_attention(_DTYPES[dtype], q.ptr, k.ptr, v.ptr, pos_table.ptr, bias_u.ptr, bias_v.ptr,
+                                     ranges.ptr, out.ptr, Tq, Tk, heads, head_dim, rel_offset, n_rel,
+                                     hip_stream.ptr if hip_stream else None))
+
+
+# ---------------------------------------------------------------- synthetic weights
+
+def synthetic_layer_weights(cfg, seed, layer, ln_jitter=0.1):
+    """Random-init weights of one Nemotron FastConformer layer in the checkpoint layout.
+
+    Linear and conv weights are Xavier-uniform; pos_bias_u/v ~ N(0, 0.02^2); LayerNorm gamma =
+    1 + ln_jitter*U(-1,1), beta = ln_jitter*U(-1,1) (ln_jitter=0 gives gamma=1, beta=0)."""
+    rng = np.random.default_rng([int(seed), int(layer)])
+    D, ff, K, H = cfg.d_model, cfg.ff_dim, cfg.conv_kernel, cfg.heads
+
+    def xavier(shape, fan_in, fan_out):
+        b = np.float32(np.sqrt(6.0 / (fan_in + fan_out)))
+        return ((rng.random(shape, dtype=np.float32) * 2 - 1) * b).astype(np.float32)
+
+    def ln():
+        g = (1 + ln_jitter * (rng.random(D, dtype=np.float32) * 2 - 1)).astype(np.float32)
+        b = (ln_jitter * (rng.random(D, dtype=np.float32) * 2 - 1)).astype(np.float32)
+        return g, b
+
+    w = {}
+    for name in ("norm_feed_forward1", "norm_self_att", "norm_conv", "conv.batch_norm", "norm_feed_forward2",
+                 "norm_out"):
+        g, b = ln()
+        w[name + ".weight"], w[name + ".bias"] = g, b
+    w["feed_forward1.linear1.weight"] = xavier((ff, D), D, ff)
+    w["feed_forward1.linear2.weight"] = xavier((D, ff), ff, D)
+    for n in ("q", "k", "v", "out", "pos"):
+        w["self_attn.linear_%s.weight" % n] = xavier((D, D), D, D)
+    w["self_attn.pos_bias_u"] = (rng.standard_normal((H, D // H), dtype=np.float32) * 0.02).astype(np.float32)
+    w["self_attn.pos_bias_v"] = (rng.standard_normal((H, D // H), dtype=np.float32) * 0.02).astype(np.float32)
+    w["conv.pointwise_conv1.weight"] = xavier((2 * D, D), D, 2 * D)
+    w["conv.depthwise_conv.weight"] = xavier((D, K), K, K)
+    w["conv.pointwise_conv2.weight"] = xavier((D, D), D, D)
+    w["feed_forward2.linear1.weight"] = xavier((ff, D), D, ff)
+    w["feed_forward2.linear2.weight"] = xavier((D, ff), ff, D)
+    return w
+
+
+def round_bf16(a):
+    """Round-to-nearest-even to bfloat16 and back to fp32 (the upload rule of bf16 encoders,
+    Sources/DictatorEngine/Core/Tensor.swift:116-122)."""
+    a = np.ascontiguousarray(a, np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32) << 16
+    r = np.where(np.isnan(a), np.uint32(0x7FC00000), r.astype(np.uint32))
+    return r.astype(np.uint32).view(np.float32).reshape(a.shape)

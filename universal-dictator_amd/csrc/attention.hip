@@ -1,0 +1,336 @@
+// Fused relative-position multi-head attention for gfx950.
+//
+// Semantics: Sources/DictatorEngine/Metal/20_conformer.metal:140-220 (relpos_attention) as
+// dispatched by Sources/DictatorEngine/Core/Ops.swift:80-90.  For query i, head h, key j in the
+// query's range:
+//     s_ij = ((q_i + u_h) . k_j + (q_i + v_h) . P[(Tk - Tq + i) - j + rel_offset]) * scale
+//     out_i = sum_j softmax_j(s_ij) v_j          (0 when the range is empty)
+// which is NeMo's  ac + rel_shift(bd)  with the pad/view shift folded into the P row index.
+//
+// Design (one workgroup of 4 wave64s per (sequence, head)):
+//  - keys are processed in blocks of KB rows with an online softmax, so any Tk works;
+//  - every K row, V row and P-band row of a block is fetched with one 16-byte load per lane
+//    (LPR = head_dim*sizeof/16 lanes per row), all issued before any arithmetic, so a workgroup
+//    has the whole block in flight;
+//  - bd is computed once per P row of the block's band (band = keys + queries - 1 rows, shared by
+//    all queries) rather than once per (query, key): rel_shift becomes the index i - jj + nk - 1;
+//  - dot products are reduced inside the LPR-lane row group with DPP; softmax max/sum are wave64
+//    DPP/shuffle reductions; V is staged in LDS and the P.V product is done by threads that own
+//    (query, channel) outputs.
+//  - ring mode: keys are [L cached ; T new]; cached row j lives in ring slot (wpos + j) % L of
+//    the stream's [H][L][dk] cache; after the block loop (every read done) the workgroup writes
+//    its head's T new K/V rows over the T oldest slots.  Each (stream, head) owns its ring slice,
+//    so no other workgroup touches those bytes.
+#include "ud_common.hpp"
+#include "kernels.hpp"
+
+namespace ud {
+
+template <typename T, int DK, int TQ, int KB>
+struct AttnCfg {
+    static constexpr int NT = 256;
+    static constexpr int VEC = Vec16<T>::N;
+    static constexpr int LPR = DK / VEC;               // lanes per row
+    static constexpr int G = NT / LPR;                 // rows per pass
+    static constexpr int NB = KB + TQ - 1;             // band rows per block
+    static constexpr int KR = (KB + G - 1) / G;        // K (and V) rows per thread
+    static constexpr int PR = (NB + G - 1) / G;        // P rows per thread
+    static constexpr int OUTS = (TQ * DK + NT - 1) / NT;
+    static_assert(LPR >= 1 && LPR <= 64 && (LPR & (LPR - 1)) == 0, "lanes per row");
+};
+
+// Source adaptor: reference layout (Q [Tq, H*dk], K/V [Tk, H*dk], P [n_rel, H*dk]).
+template <typename T>
+struct OpSrc {
+    const T* Q; const T* K; const T* V; const T* P; T* O;
+    const float* u; const float* vb; const int32_t* ranges;
+    int Tq, Tk, ld, hoff, rel_offset, n_rel;
+    __device__ const T* qrow(int i) const { return Q + (int64_t)i * ld + hoff; }
+    __device__ const T* krow(int j) const { return K + (int64_t)j * ld + hoff; }
+    __device__ const T* vrow(int j) const { return V + (int64_t)j * ld + hoff; }
+    __device__ const T* prow(int r) const { return P + (int64_t)r * ld + hoff; }
+    __device__ T* orow(int i) const { return O + (int64_t)i * ld + hoff; }
+    __device__ void range(int i, int& ks, int& ke) const {
+        ks = max(ranges[2 * i], 0);
+        ke = min(ranges[2 * i + 1], Tk);
+    }
+};
+
+// Source adaptor: streaming step over one stream's ring caches.
+template <typename T>
+struct RingSrc {
+    const T* kr; const T* vr;      // this (stream, head) ring slice: [L][dk]
+    const T* qkv;                  // first row of this stream in [n*T, 3*D]
+    const T* P; T* O;              // P [n_rel, D]; O first row of this stream in [n*T, D]
+    const float* u; const float* vb;
+    int Tq, Tk, L, D, hoff, wpos, rel_offset, n_rel, ks, ke;
+    __device__ const T* qrow(int i) const { return qkv + (int64_t)i * 3 * D + hoff; }
+    __device__ const T* krow(int j) const {
+        if (j < L) { int s = wpos + j; s -= (s >= L) ? L : 0; return kr + (int64_t)s * 128; }
+        return qkv + (int64_t)(j - L) * 3 * D + D + hoff;
+    }
+    __device__ const T* vrow(int j) const {
+        if (j < L) { int s = wpos + j; s -= (s >= L) ? L : 0; return vr + (int64_t)s * 128; }
+        return qkv + (int64_t)(j - L) * 3 * D + 2 * D + hoff;
+    }
+    __device__ const T* prow(int r) const { return P + (int64_t)r * D + hoff; }
+    __device__ T* orow(int i) const { return O + (int64_t)i * D + hoff; }
+    __device__ void range(int, int& s, int& e) const { s = ks; e = ke; }
+};
+
+template <typename T, int DK, int TQ, int KB, typename Src>
+__device__ __forceinline__ void relpos_core(const Src& src, float scale) {
+    using C = AttnCfg<T, DK, TQ, KB>;
+    constexpr int NT = C::NT, VEC = C::VEC, LPR = C::LPR, G = C::G;
+    __shared__ float qu[TQ][DK];
+    __shared__ float qv[TQ][DK];
+    __shared__ float sc[TQ][KB];
+    __shared__ float bd[TQ][C::NB];
+    __shared__ __attribute__((aligned(16))) T vs[KB][DK];
+    __shared__ float mrow[TQ], lrow[TQ], crow[TQ];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = tid / LPR, sub = tid % LPR;
+    const int Tq = src.Tq, Tk = src.Tk;
+
+    for (int idx = tid; idx < Tq * DK; idx += NT) {
+        int i = idx / DK, d = idx % DK;
+        float q = to_f<T>(src.qrow(i)[d]);
+        qu[i][d] = q + src.u[d];
+        qv[i][d] = q + src.vb[d];
+    }
+    if (tid < TQ) { mrow[tid] = -INFINITY; lrow[tid] = 0.0f; crow[tid] = 0.0f; }
+    int kl = Tk, kh = 0;
+    for (int i = 0; i < Tq; i++) {
+        int s, e;
+        src.range(i, s, e);
+        if (s < e) { kl = min(kl, s); kh = max(kh, e); }
+    }
+    float acc[C::OUTS];
+#pragma unroll
+    for (int o = 0; o < C::OUTS; o++) acc[o] = 0.0f;
+    __syncthreads();
+
+    const int shift0 = Tk - Tq;
+    for (int kb = kl; kb < kh; kb += KB) {
+        const int nk = min(KB, kh - kb);
+        const int nb = nk + Tq - 1;
+        const int rbase = shift0 - (kb + nk - 1) + src.rel_offset;   // table row of band index 0
+
+        uint4 kreg[C::KR], vreg[C::KR], preg[C::PR];
+#pragma unroll
+        for (int k = 0; k < C::KR; k++) {
+            int row = grp + k * G;
+            kreg[k] = make_uint4(0, 0, 0, 0);
+            vreg[k] = make_uint4(0, 0, 0, 0);
+            if (row < nk) {
+                kreg[k] = ld16(src.krow(kb + row) + sub * VEC);
+                vreg[k] = ld16(src.vrow(kb + row) + sub * VEC);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < C::PR; k++) {
+            int b = grp + k * G;
+            int r = rbase + b;
+            preg[k] = make_uint4(0, 0, 0, 0);
+            if (b < nb && r >= 0 && r < src.n_rel) preg[k] = ld16(src.prow(r) + sub * VEC);
+        }
+        __syncthreads();   // the previous block's P.V no longer reads vs / sc
+#pragma unroll
+        for (int k = 0; k < C::KR; k++) {
+            int row = grp + k * G;
+            if (row < nk) st16(&vs[row][sub * VEC], vreg[k]);
+        }
+        for (int i = 0; i < Tq; i++) {
+            float a[VEC], bq[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; e++) { a[e] = qu[i][sub * VEC + e]; bq[e] = qv[i][sub * VEC + e]; }
+#pragma unroll
+            for (int k = 0; k < C::KR; k++) {
+                float f[VEC];
+                unpack16<T>(kreg[k], f);
+                float s = 0.0f;
+#pragma unroll
+                for (int e = 0; e < VEC; e++) s += a[e] * f[e];
+                s = group_sum<LPR>(s);
+                int row = grp + k * G;
+                if (sub == 0 && row < nk) sc[i][row] = s;
+            }
+#pragma unroll
+            for (int k = 0; k < C::PR; k++) {
+                float f[VEC];
+                unpack16<T>(preg[k], f);
+                float s = 0.0f;
+#pragma unroll
+                for (int e = 0; e < VEC; e++) s += bq[e] * f[e];
+                s = group_sum<LPR>(s);
+                int b = grp + k * G;
+                if (sub == 0 && b < nb) bd[i][b] = s;
+            }
+        }
+        __syncthreads();
+
+        // Online softmax, one wave per query.
+        for (int i = wave; i < Tq; i += NT / 64) {
+            int qs, qe;
+            src.range(i, qs, qe);
+            const int lo = max(qs, kb) - kb, hi = min(qe, kb + nk) - kb;
+            constexpr int PER = (KB + 63) / 64;
+            float sv[PER];
+            float bm = -INFINITY;
+#pragma unroll
+            for (int p = 0; p < PER; p++) {
+                int jj = lane + p * 64;
+                bool ok = jj < nk && jj >= lo && jj < hi;
+                sv[p] = ok ? (sc[i][jj] + bd[i][i - jj + nk - 1]) * scale : -INFINITY;
+                bm = fmaxf(bm, sv[p]);
+            }
+            bm = wave_max(bm);
+            const float mold = mrow[i];
+            const float mnew = fmaxf(mold, bm);
+            float ls = 0.0f;
+#pragma unroll
+            for (int p = 0; p < PER; p++) {
+                int jj = lane + p * 64;
+                float e = (sv[p] == -INFINITY) ? 0.0f : __expf(sv[p] - mnew);
+                if (jj < nk) sc[i][jj] = e;
+                ls += e;
+            }
+            ls = wave_sum(ls);
+            if (lane == 0) {
+                float c = (mold == -INFINITY) ? 0.0f : __expf(mold - mnew);
+                crow[i] = c;
+                lrow[i] = lrow[i] * c + ls;
+                mrow[i] = mnew;
+            }
+        }
+        __syncthreads();
+
+#pragma unroll
+        for (int o = 0; o < C::OUTS; o++) {
+            int idx = tid + o * NT;
+            if (idx < Tq * DK) {
+                int i = idx / DK, d = idx % DK;
+                float a = acc[o] * crow[i];
+                for (int jj = 0; jj < nk; jj++) a += sc[i][jj] * to_f<T>(vs[jj][d]);
+                acc[o] = a;
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 0; o < C::OUTS; o++) {
+        int idx = tid + o * NT;
+        if (idx < Tq * DK) {
+            int i = idx / DK, d = idx % DK;
+            float l = (kl < kh) ? lrow[i] : 0.0f;
+            src.orow(i)[d] = from_f<T>(l > 0.0f ? acc[o] / l : 0.0f);
+        }
+    }
+}
+
+template <typename T, int DK, int TQ, int KB>
+__global__ __launch_bounds__(256) void relpos_op_kernel(const T* Q, const T* K, const T* V, const T* P,
+                                                        const float* u, const float* vb, const int32_t* ranges,
+                                                        T* O, int Tq, int Tk, int H, int rel_offset, int n_rel,
+                                                        float scale) {
+    const int h = blockIdx.x;
+    OpSrc<T> src;
+    src.Q = Q; src.K = K; src.V = V; src.P = P; src.O = O;
+    src.u = u + h * DK; src.vb = vb + h * DK; src.ranges = ranges;
+    src.Tq = Tq; src.Tk = Tk; src.ld = H * DK; src.hoff = h * DK;
+    src.rel_offset = rel_offset; src.n_rel = n_rel;
+    relpos_core<T, DK, TQ, KB>(src, scale);
+}
+
+// One workgroup per (stream, head): blockIdx.x = stream * H + head, so consecutive heads of a
+// layer land on consecutive XCDs and each XCD's L2 serves one head's P rows to every stream.
+template <typename T, int TQ, int KB>
+__global__ __launch_bounds__(256) void relpos_ring_kernel(RingArgs a) {
+    constexpr int DK = 128;
+    const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
+    const int32_t* d = a.desc + s * 4;
+    const int slot = d[0], frames = d[1], valid = d[2], cache_len = d[3];
+    const int wpos = frames % a.L;
+    const int D = a.H * DK;
+    const T* kr = static_cast<const T*>(a.kring) + ((int64_t)slot * a.H + h) * a.L * DK;
+    const T* vr = static_cast<const T*>(a.vring) + ((int64_t)slot * a.H + h) * a.L * DK;
+    const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)s * a.T * 3 * D;
+
+    RingSrc<T> src;
+    src.kr = kr; src.vr = vr; src.qkv = qkv;
+    src.P = static_cast<const T*>(a.P);
+    src.O = static_cast<T*>(a.att) + (int64_t)s * a.T * D;
+    src.u = a.u + h * DK; src.vb = a.vb + h * DK;
+    src.Tq = a.T; src.Tk = a.L + a.T; src.L = a.L; src.D = D; src.hoff = h * DK;
+    src.wpos = wpos; src.rel_offset = a.rel_offset; src.n_rel = a.n_rel;
+    src.ks = a.L - cache_len;
+    src.ke = a.L + min(max(valid, 0), a.T);
+    relpos_core<T, DK, TQ, KB>(src, a.scale);
+
+    // Commit: the T new rows replace the T oldest ring slots (logical keys 0..T-1, all read above).
+    __syncthreads();
+    constexpr int VEC = Vec16<T>::N, LPR = DK / VEC;
+    T* kw = static_cast<T*>(a.kring) + ((int64_t)slot * a.H + h) * a.L * DK;
+    T* vw = static_cast<T*>(a.vring) + ((int64_t)slot * a.H + h) * a.L * DK;
+    for (int idx = threadIdx.x; idx < a.T * LPR; idx += 256) {
+        int t = idx / LPR, c = (idx % LPR) * VEC;
+        int slot_row = wpos + t;
+        slot_row -= (slot_row >= a.L) ? a.L : 0;
+        const T* q = qkv + (int64_t)t * 3 * D + h * DK + c;
+        st16(kw + (int64_t)slot_row * DK + c, ld16(q + D));
+        st16(vw + (int64_t)slot_row * DK + c, ld16(q + 2 * D));
+    }
+}
+
+// ------------------------------------------------------------------ launchers
+
+// Keys per block: as many as keep the workgroup's LDS under 64 KB.
+template <typename T, int TQ> struct KeyBlock { static constexpr int KB = sizeof(T) == 2 ? (TQ <= 8 ? 128 : 96) : 64; };
+
+template <typename T, int DK>
+static int launch_op_dk(const OpArgs& a, hipStream_t st) {
+    dim3 grid(a.H), block(256);
+    const T* Q = static_cast<const T*>(a.q); const T* K = static_cast<const T*>(a.k);
+    const T* V = static_cast<const T*>(a.v); const T* P = static_cast<const T*>(a.p);
+    T* O = static_cast<T*>(a.out);
+    if (a.Tq <= 2)
+        hipLaunchKernelGGL((relpos_op_kernel<T, DK, 2, KeyBlock<T, 2>::KB>), grid, block, 0, st, Q, K, V, P, a.u,
+                           a.vb, a.ranges, O, a.Tq, a.Tk, a.H, a.rel_offset, a.n_rel, a.scale);
+    else
+        hipLaunchKernelGGL((relpos_op_kernel<T, DK, 16, KeyBlock<T, 16>::KB>), grid, block, 0, st, Q, K, V, P, a.u,
+                           a.vb, a.ranges, O, a.Tq, a.Tk, a.H, a.rel_offset, a.n_rel, a.scale);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <typename T>
+static int launch_op_t(const OpArgs& a, hipStream_t st) {
+    switch (a.dk) {
+        case 16: return launch_op_dk<T, 16>(a, st);
+        case 32: return launch_op_dk<T, 32>(a, st);
+        case 64: return launch_op_dk<T, 64>(a, st);
+        case 128: return launch_op_dk<T, 128>(a, st);
+        default: return -2;
+    }
+}
+
+int launch_relpos_op(const OpArgs& a, bool bf16_data, hipStream_t st) {
+    if (a.Tq < 1 || a.Tq > 16 || a.H < 1) return -2;
+    return bf16_data ? launch_op_t<bf16>(a, st) : launch_op_t<float>(a, st);
+}
+
+template <typename T>
+static int launch_ring_t(const RingArgs& a, hipStream_t st) {
+    dim3 grid(a.n * a.H), block(256);
+    if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_kernel<T, 2, KeyBlock<T, 2>::KB>), grid, block, 0, st, a);
+    else if (a.T <= 4) hipLaunchKernelGGL((relpos_ring_kernel<T, 4, KeyBlock<T, 4>::KB>), grid, block, 0, st, a);
+    else if (a.T <= 8) hipLaunchKernelGGL((relpos_ring_kernel<T, 8, KeyBlock<T, 8>::KB>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((relpos_ring_kernel<T, 16, KeyBlock<T, 16>::KB>), grid, block, 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_relpos_ring(const RingArgs& a, bool bf16_data, hipStream_t st) {
+    if (a.T < 1 || a.T > 16 || a.T > a.L || a.n < 1) return -2;
+    return bf16_data ? launch_ring_t<bf16>(a, st) : launch_ring_t<float>(a, st);
+}
+
+}  // namespace ud

@@ -1,0 +1,778 @@
+// Host layer and C ABI of the gfx950 streaming encoder step (include/ud_encoder.h).
+//
+// Mirrors FastConformerEncoder + StreamState + encodeStreamStep
+// (Sources/DictatorEngine/Models/FastConformer.swift:62-480) for a batch of streams:
+//  - one encoder owns device weights (bf16 or fp32), per-layer position tables, a step workspace
+//    sized for max_streams x max_chunk rows and a pool of per-stream caches;
+//  - caches are rings updated in place by the attention and conv kernels (no ping-pong copies);
+//    a stream's ring origin is derived from its frame counter, so the host carries one integer
+//    per stream and uploads a small descriptor {slot, frames, valid} per step;
+//  - the 24-layer kernel sequence of a step is captured once per (batch size, T, input, output)
+//    into a hipGraph and replayed.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/ud_encoder.h"
+#include "kernels.hpp"
+
+using namespace ud;
+
+// ---------------------------------------------------------------- errors
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIPC(call)                                                                               \
+    do {                                                                                         \
+        hipError_t e_ = (call);                                                                  \
+        if (e_ != hipSuccess) return fail(UD_ERR_HIP, "%s: %s (%s:%d)", #call, hipGetErrorString(e_), \
+                                          __FILE__, __LINE__);                                   \
+    } while (0)
+
+static int launch_status(int rc, const char* what) {
+    if (rc == 0) return UD_OK;
+    if (rc == -2) return fail(UD_ERR_SHAPE, "%s: shape not supported by the kernel", what);
+    return fail(UD_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(hipGetLastError()));
+}
+#define LAUNCH(expr, what)                                  \
+    do {                                                    \
+        int r_ = launch_status((expr), what);               \
+        if (r_ != UD_OK) return r_;                         \
+    } while (0)
+
+extern "C" UD_API const char* ud_last_error(void) { return g_err.c_str(); }
+
+int ud_set_error(int code, const char* msg) {
+    g_err = msg;
+    return code;
+}
+
+// ---------------------------------------------------------------- bf16 host conversion
+
+// Round-to-nearest-even, NaN -> 0x7FC0 (Sources/DictatorEngine/Core/Tensor.swift:116-122).
+static inline uint16_t host_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7FC0;
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+static inline float host_bf16_to_f(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+// ---------------------------------------------------------------- weights
+
+// The 26 tensors of one layer (docs/specs/nemotron.md tensor-name map; loading at
+// FastConformer.swift:96-143).
+enum WSlot {
+    NORM_FF1_W, NORM_FF1_B, FF1_W1, FF1_W2, NORM_ATT_W, NORM_ATT_B, LIN_Q, LIN_K, LIN_V, LIN_OUT, LIN_POS,
+    BIAS_U, BIAS_V, NORM_CONV_W, NORM_CONV_B, PW1, DW, CONV_LN_W, CONV_LN_B, PW2, NORM_FF2_W, NORM_FF2_B,
+    FF2_W1, FF2_W2, NORM_OUT_W, NORM_OUT_B, NSLOTS
+};
+static const char* kSuffix[NSLOTS] = {
+    "norm_feed_forward1.weight", "norm_feed_forward1.bias", "feed_forward1.linear1.weight",
+    "feed_forward1.linear2.weight", "norm_self_att.weight", "norm_self_att.bias", "self_attn.linear_q.weight",
+    "self_attn.linear_k.weight", "self_attn.linear_v.weight", "self_attn.linear_out.weight",
+    "self_attn.linear_pos.weight", "self_attn.pos_bias_u", "self_attn.pos_bias_v", "norm_conv.weight",
+    "norm_conv.bias", "conv.pointwise_conv1.weight", "conv.depthwise_conv.weight", "conv.batch_norm.weight",
+    "conv.batch_norm.bias", "conv.pointwise_conv2.weight", "norm_feed_forward2.weight", "norm_feed_forward2.bias",
+    "feed_forward2.linear1.weight", "feed_forward2.linear2.weight", "norm_out.weight", "norm_out.bias"};
+
+struct LayerDev {
+    void* ff1_w1 = nullptr; void* ff1_w2 = nullptr; void* wqkv = nullptr; void* wo = nullptr;
+    void* pw1 = nullptr; void* pw2 = nullptr; void* ff2_w1 = nullptr; void* ff2_w2 = nullptr;
+    float* ln[12] = {};          // ff1 g,b; att g,b; conv g,b; conv-ln g,b; ff2 g,b; out g,b
+    float* bias_u = nullptr; float* bias_v = nullptr;
+    float* dw_t = nullptr;       // [K][D]
+    void* P = nullptr;           // [n_rel][D]
+    std::vector<float> wpos;     // host copy until finalize (dtype-rounded)
+    uint32_t set_mask = 0;
+};
+
+struct GraphEntry {
+    int n, T;
+    const void* x;
+    void* out;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+struct ud_stream {
+    ud_encoder* enc;
+    int slot;
+    int64_t frames;   // frames appended so far (ring origin and cache_len derive from it)
+    int steps;
+};
+
+struct ud_encoder {
+    ud_encoder_config cfg;
+    bool bf;
+    size_t esz;
+    int D, H, dk, ff, Kc, L, layers, n_rel, rel_offset, max_rows;
+    std::vector<LayerDev> lw;
+    // stream pool
+    void* kring = nullptr; void* vring = nullptr; float* cring = nullptr;
+    size_t ring_layer_elems = 0;   // slots * H * L * dk
+    size_t cring_layer_elems = 0;  // slots * (K-1) * D
+    std::vector<int> free_slots;
+    std::vector<ud_stream*> live;
+    // workspace
+    float* res = nullptr; void* z = nullptr; void* h = nullptr; void* qkv = nullptr; void* att = nullptr;
+    float* g = nullptr; float* pw = nullptr;
+    int32_t* desc_dev = nullptr;
+    int32_t* desc_host[4] = {};
+    hipEvent_t desc_ev[4] = {};
+    bool desc_used[4] = {};
+    int desc_next = 0;
+    bool finalized = false;
+    bool use_graphs = true;
+    hipStream_t capture_stream = nullptr;
+    std::vector<GraphEntry> graphs;
+};
+
+static void* dev_alloc(size_t bytes) {
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 16) != hipSuccess) return nullptr;
+    return p;
+}
+
+static void free_encoder(ud_encoder* e) {
+    if (!e) return;
+    (void)hipDeviceSynchronize();
+    for (auto& g : e->graphs) { (void)hipGraphExecDestroy(g.exec); (void)hipGraphDestroy(g.graph); }
+    for (auto& l : e->lw) {
+        void* ps[] = {l.ff1_w1, l.ff1_w2, l.wqkv, l.wo, l.pw1, l.pw2, l.ff2_w1, l.ff2_w2, l.bias_u, l.bias_v, l.dw_t, l.P};
+        for (void* p : ps) if (p) (void)hipFree(p);
+        for (float* p : l.ln) if (p) (void)hipFree(p);
+    }
+    void* ws[] = {e->kring, e->vring, e->cring, e->res, e->z, e->h, e->qkv, e->att, e->g, e->pw, e->desc_dev};
+    for (void* p : ws) if (p) (void)hipFree(p);
+    for (int i = 0; i < 4; i++) {
+        if (e->desc_host[i]) (void)hipHostFree(e->desc_host[i]);
+        if (e->desc_ev[i]) (void)hipEventDestroy(e->desc_ev[i]);
+    }
+    if (e->capture_stream) (void)hipStreamDestroy(e->capture_stream);
+    for (ud_stream* s : e->live) delete s;
+    delete e;
+}
+
+extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder** out) {
+    if (!cfg || !out) return fail(UD_ERR_INVALID, "ud_encoder_create: null argument");
+    *out = nullptr;
+    const ud_encoder_config& c = *cfg;
+    if (c.layers < 1 || c.d_model < 1 || c.heads < 1 || c.d_model % c.heads != 0 || c.ff_dim < 1)
+        return fail(UD_ERR_SHAPE, "ud_encoder_create: bad model dimensions");
+    if (c.d_model / c.heads != 128) return fail(UD_ERR_SHAPE, "ud_encoder_create: head_dim must be 128");
+    if (c.d_model != 1024) return fail(UD_ERR_SHAPE, "ud_encoder_create: d_model must be 1024");
+    if (c.ff_dim % 64 != 0) return fail(UD_ERR_SHAPE, "ud_encoder_create: ff_dim must be a multiple of 64");
+    if (c.conv_kernel != 9) return fail(UD_ERR_SHAPE, "ud_encoder_create: conv_kernel must be 9");
+    if (c.left_context < 1 || c.max_chunk < 1 || c.max_chunk > 16 || c.max_chunk > c.left_context)
+        return fail(UD_ERR_SHAPE, "ud_encoder_create: need 1 <= max_chunk <= min(16, left_context)");
+    if (c.max_streams < 1) return fail(UD_ERR_SHAPE, "ud_encoder_create: max_streams must be >= 1");
+    if (c.dtype != UD_F32 && c.dtype != UD_BF16) return fail(UD_ERR_INVALID, "ud_encoder_create: bad dtype");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1)
+        return fail(UD_ERR_HIP, "ud_encoder_create: no HIP device");
+
+    ud_encoder* e = new ud_encoder();
+    e->cfg = c;
+    e->bf = c.dtype == UD_BF16;
+    e->esz = e->bf ? 2 : 4;
+    e->D = c.d_model; e->H = c.heads; e->dk = c.d_model / c.heads; e->ff = c.ff_dim; e->Kc = c.conv_kernel;
+    e->L = c.left_context; e->layers = c.layers;
+    // makeStreamState: tables over rel = -(maxChunk-1) ... L+maxChunk-1 (FastConformer.swift:433)
+    e->rel_offset = c.max_chunk - 1;
+    e->n_rel = c.left_context + 2 * c.max_chunk - 1;
+    e->max_rows = c.max_streams * c.max_chunk;
+    const char* ev = getenv("UD_GRAPHS");
+    e->use_graphs = !(ev && ev[0] == '0');
+    e->lw.resize(c.layers);
+
+    const size_t D = e->D, ff = e->ff, esz = e->esz;
+    bool ok = true;
+    for (auto& l : e->lw) {
+        ok &= (l.ff1_w1 = dev_alloc(ff * D * esz)) != nullptr;
+        ok &= (l.ff1_w2 = dev_alloc(D * ff * esz)) != nullptr;
+        ok &= (l.wqkv = dev_alloc(3 * D * D * esz)) != nullptr;
+        ok &= (l.wo = dev_alloc(D * D * esz)) != nullptr;
+        ok &= (l.pw1 = dev_alloc(2 * D * D * esz)) != nullptr;
+        ok &= (l.pw2 = dev_alloc(D * D * esz)) != nullptr;
+        ok &= (l.ff2_w1 = dev_alloc(ff * D * esz)) != nullptr;
+        ok &= (l.ff2_w2 = dev_alloc(D * ff * esz)) != nullptr;
+        for (auto& p : l.ln) ok &= (p = (float*)dev_alloc(D * 4)) != nullptr;
+        ok &= (l.bias_u = (float*)dev_alloc(D * 4)) != nullptr;
+        ok &= (l.bias_v = (float*)dev_alloc(D * 4)) != nullptr;
+        ok &= (l.dw_t = (float*)dev_alloc((size_t)e->Kc * D * 4)) != nullptr;
+        ok &= (l.P = dev_alloc((size_t)e->n_rel * D * esz)) != nullptr;
+        if (!ok) break;
+    }
+    const size_t slots = c.max_streams;
+    e->ring_layer_elems = slots * e->H * e->L * e->dk;
+    e->cring_layer_elems = slots * (e->Kc - 1) * D;
+    if (ok) {
+        ok &= (e->kring = dev_alloc(e->ring_layer_elems * e->layers * esz)) != nullptr;
+        ok &= (e->vring = dev_alloc(e->ring_layer_elems * e->layers * esz)) != nullptr;
+        ok &= (e->cring = (float*)dev_alloc(e->cring_layer_elems * e->layers * 4)) != nullptr;
+    }
+    const size_t R = e->max_rows;
+    if (ok) {
+        ok &= (e->res = (float*)dev_alloc(R * D * 4)) != nullptr;
+        ok &= (e->z = dev_alloc(R * D * esz)) != nullptr;
+        ok &= (e->h = dev_alloc(R * ff * esz)) != nullptr;
+        ok &= (e->qkv = dev_alloc(R * 3 * D * esz)) != nullptr;
+        ok &= (e->att = dev_alloc(R * D * esz)) != nullptr;
+        ok &= (e->g = (float*)dev_alloc(R * D * 4)) != nullptr;
+        if (!e->bf) ok &= (e->pw = (float*)dev_alloc(R * 2 * D * 4)) != nullptr;
+        ok &= (e->desc_dev = (int32_t*)dev_alloc(slots * DESC_INTS * 4)) != nullptr;
+    }
+    for (int i = 0; ok && i < 4; i++) {
+        ok &= hipHostMalloc((void**)&e->desc_host[i], slots * DESC_INTS * 4, hipHostMallocDefault) == hipSuccess;
+        ok &= hipEventCreateWithFlags(&e->desc_ev[i], hipEventDisableTiming) == hipSuccess;
+    }
+    if (!ok) {
+        free_encoder(e);
+        return fail(UD_ERR_NOMEM, "ud_encoder_create: device allocation failed");
+    }
+    if (hipMemset(e->kring, 0, e->ring_layer_elems * e->layers * esz) != hipSuccess ||
+        hipMemset(e->vring, 0, e->ring_layer_elems * e->layers * esz) != hipSuccess ||
+        hipMemset(e->cring, 0, e->cring_layer_elems * e->layers * 4) != hipSuccess ||
+        hipStreamCreateWithFlags(&e->capture_stream, hipStreamNonBlocking) != hipSuccess) {
+        free_encoder(e);
+        return fail(UD_ERR_HIP, "ud_encoder_create: initialisation failed");
+    }
+    for (int s = (int)slots - 1; s >= 0; s--) e->free_slots.push_back(s);
+    *out = e;
+    return UD_OK;
+}
+
+extern "C" UD_API void ud_encoder_destroy(ud_encoder* enc) { free_encoder(enc); }
+
+static int upload(void* dst, const void* src, size_t bytes) {
+    HIPC(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return UD_OK;
+}
+
+// Converts `rows` x `cols` fp32 values to the encoder dtype and writes them at dst row offset.
+static int upload_matrix(ud_encoder* e, void* dst, size_t dst_row0, const float* src, size_t rows, size_t cols) {
+    const size_t n = rows * cols;
+    if (e->bf) {
+        std::vector<uint16_t> tmp(n);
+        for (size_t i = 0; i < n; i++) tmp[i] = host_bf16(src[i]);
+        return upload(static_cast<uint16_t*>(dst) + dst_row0 * cols, tmp.data(), n * 2);
+    }
+    return upload(static_cast<float*>(dst) + dst_row0 * cols, src, n * 4);
+}
+
+static bool parse_name(const char* name, int layers, int* layer, int* slot) {
+    const char* p = name;
+    if (strncmp(p, "encoder.", 8) == 0) p += 8;
+    if (strncmp(p, "layers.", 7) != 0) return false;
+    p += 7;
+    char* end = nullptr;
+    long li = strtol(p, &end, 10);
+    if (end == p || *end != '.' || li < 0 || li >= layers) return false;
+    p = end + 1;
+    for (int s = 0; s < NSLOTS; s++)
+        if (strcmp(p, kSuffix[s]) == 0) { *layer = (int)li; *slot = s; return true; }
+    return false;
+}
+
+extern "C" UD_API int ud_encoder_set_weight(ud_encoder* e, const char* name, const float* host, int64_t count) {
+    if (!e || !name || !host) return fail(UD_ERR_INVALID, "ud_encoder_set_weight: null argument");
+    int li = -1, slot = -1;
+    if (!parse_name(name, e->layers, &li, &slot)) return fail(UD_ERR_WEIGHT, "unknown weight name '%s'", name);
+    const int64_t D = e->D, ff = e->ff;
+    int64_t want = 0;
+    switch (slot) {
+        case FF1_W1: case FF2_W1: case FF1_W2: case FF2_W2: want = ff * D; break;
+        case LIN_Q: case LIN_K: case LIN_V: case LIN_OUT: case LIN_POS: case PW2: want = D * D; break;
+        case PW1: want = 2 * D * D; break;
+        case DW: want = D * e->Kc; break;
+        default: want = D; break;   // norms, pos_bias_u/v ([H, dk] = D values)
+    }
+    if (count != want)
+        return fail(UD_ERR_WEIGHT, "weight '%s': %lld values, expected %lld", name, (long long)count, (long long)want);
+    LayerDev& l = e->lw[li];
+    int rc = UD_OK;
+    switch (slot) {
+        case FF1_W1: rc = upload_matrix(e, l.ff1_w1, 0, host, ff, D); break;
+        case FF1_W2: rc = upload_matrix(e, l.ff1_w2, 0, host, D, ff); break;
+        case FF2_W1: rc = upload_matrix(e, l.ff2_w1, 0, host, ff, D); break;
+        case FF2_W2: rc = upload_matrix(e, l.ff2_w2, 0, host, D, ff); break;
+        case LIN_Q: rc = upload_matrix(e, l.wqkv, 0, host, D, D); break;
+        case LIN_K: rc = upload_matrix(e, l.wqkv, D, host, D, D); break;
+        case LIN_V: rc = upload_matrix(e, l.wqkv, 2 * D, host, D, D); break;
+        case LIN_OUT: rc = upload_matrix(e, l.wo, 0, host, D, D); break;
+        case PW2: rc = upload_matrix(e, l.pw2, 0, host, D, D); break;
+        case PW1: {
+            if (!e->bf) { rc = upload_matrix(e, l.pw1, 0, host, 2 * D, D); break; }
+            // bf16: interleave 16-row blocks, [value c..c+15 | gate c..c+15], for the GLU epilogue.
+            std::vector<float> perm((size_t)2 * D * D);
+            for (int64_t c = 0; c < D; c++) {
+                int64_t dv = 32 * (c / 16) + (c % 16), dg = dv + 16;
+                memcpy(&perm[dv * D], host + c * D, D * 4);
+                memcpy(&perm[dg * D], host + (D + c) * D, D * 4);
+            }
+            rc = upload_matrix(e, l.pw1, 0, perm.data(), 2 * D, D);
+            break;
+        }
+        case LIN_POS: {
+            l.wpos.assign(host, host + D * D);
+            if (e->bf) for (auto& v : l.wpos) v = host_bf16_to_f(host_bf16(v));
+            e->finalized = false;
+            break;
+        }
+        case DW: {
+            std::vector<float> t((size_t)e->Kc * D);
+            for (int64_t d = 0; d < D; d++)
+                for (int k = 0; k < e->Kc; k++) t[(size_t)k * D + d] = host[d * e->Kc + k];
+            rc = upload(l.dw_t, t.data(), t.size() * 4);
+            break;
+        }
+        case BIAS_U: rc = upload(l.bias_u, host, D * 4); break;
+        case BIAS_V: rc = upload(l.bias_v, host, D * 4); break;
+        default: {
+            static const int ln_index[NSLOTS] = {0, 1, -1, -1, 2, 3, -1, -1, -1, -1, -1, -1, -1, 4, 5,
+                                                 -1, -1, 6, 7, -1, 8, 9, -1, -1, 10, 11};
+            rc = upload(l.ln[ln_index[slot]], host, D * 4);
+        }
+    }
+    if (rc != UD_OK) return rc;
+    l.set_mask |= 1u << slot;
+    return UD_OK;
+}
+
+// NeMo RelPositionalEncoding row for relative position `pos` (FastConformer.swift:147-158):
+// k and the angle in fp32, exp/sin/cos in double then rounded to fp32.
+static void sinusoid_row(int pos, int D, float* pe) {
+    const float k = -((float)std::log(10000.0) / (float)D);
+    for (int i = 0; i < D; i += 2) {
+        float div = (float)std::exp((double)((float)i * k));
+        float angle = (float)pos * div;
+        pe[i] = (float)std::sin((double)angle);
+        pe[i + 1] = (float)std::cos((double)angle);
+    }
+}
+
+extern "C" UD_API int ud_encoder_finalize(ud_encoder* e) {
+    if (!e) return fail(UD_ERR_INVALID, "ud_encoder_finalize: null encoder");
+    const uint32_t all = (1u << NSLOTS) - 1;
+    for (int li = 0; li < e->layers; li++)
+        if (e->lw[li].set_mask != all) {
+            for (int s = 0; s < NSLOTS; s++)
+                if (!(e->lw[li].set_mask & (1u << s)))
+                    return fail(UD_ERR_STATE, "ud_encoder_finalize: weight encoder.layers.%d.%s not set", li, kSuffix[s]);
+        }
+    const int D = e->D, n = e->n_rel;
+    std::vector<float> pe((size_t)n * D);
+    for (int r = 0; r < n; r++) sinusoid_row(r - e->rel_offset, D, &pe[(size_t)r * D]);
+    float *pe_d = nullptr, *w_d = nullptr, *p_d = nullptr;
+    pe_d = (float*)dev_alloc(pe.size() * 4);
+    w_d = (float*)dev_alloc((size_t)D * D * 4);
+    p_d = (float*)dev_alloc(pe.size() * 4);
+    int rc = UD_OK;
+    if (!pe_d || !w_d || !p_d) rc = fail(UD_ERR_NOMEM, "ud_encoder_finalize: allocation failed");
+    if (rc == UD_OK) rc = upload(pe_d, pe.data(), pe.size() * 4);
+    std::vector<float> P(pe.size());
+    std::vector<uint16_t> Pb(e->bf ? pe.size() : 0);
+    for (int li = 0; rc == UD_OK && li < e->layers; li++) {
+        LayerDev& l = e->lw[li];
+        rc = upload(w_d, l.wpos.data(), (size_t)D * D * 4);
+        if (rc != UD_OK) break;
+        // P_l = PE . W_pos^T in fp32 (FastConformer.swift:168-174)
+        GemmArgs g{};
+        g.A = pe_d; g.W = w_d; g.C = p_d; g.M = n; g.N = D; g.K = D; g.lda = D; g.ldw = D; g.ldc = D;
+        g.epi = EPI_STORE_F32; g.act = 0; g.out_scale = 1.0f;
+        rc = launch_status(launch_gemm(g, false, nullptr), "position table");
+        if (rc != UD_OK) break;
+        if (e->bf) {
+            if (hipMemcpy(P.data(), p_d, P.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+                rc = fail(UD_ERR_HIP, "ud_encoder_finalize: copy back failed");
+                break;
+            }
+            for (size_t i = 0; i < P.size(); i++) Pb[i] = host_bf16(P[i]);
+            rc = upload(l.P, Pb.data(), Pb.size() * 2);
+        } else if (hipMemcpy(l.P, p_d, P.size() * 4, hipMemcpyDeviceToDevice) != hipSuccess) {
+            rc = fail(UD_ERR_HIP, "ud_encoder_finalize: copy failed");
+        }
+    }
+    if (pe_d) (void)hipFree(pe_d);
+    if (w_d) (void)hipFree(w_d);
+    if (p_d) (void)hipFree(p_d);
+    if (rc != UD_OK) return rc;
+    HIPC(hipDeviceSynchronize());
+    e->finalized = true;
+    return UD_OK;
+}
+
+// ---------------------------------------------------------------- streams
+
+static int zero_slot(ud_encoder* e, int slot) {
+    const size_t per = (size_t)e->H * e->L * e->dk, cper = (size_t)(e->Kc - 1) * e->D;
+    for (int li = 0; li < e->layers; li++) {
+        char* kb = static_cast<char*>(e->kring) + ((size_t)li * e->ring_layer_elems + slot * per) * e->esz;
+        char* vb = static_cast<char*>(e->vring) + ((size_t)li * e->ring_layer_elems + slot * per) * e->esz;
+        float* cb = e->cring + (size_t)li * e->cring_layer_elems + slot * cper;
+        HIPC(hipMemset(kb, 0, per * e->esz));
+        HIPC(hipMemset(vb, 0, per * e->esz));
+        HIPC(hipMemset(cb, 0, cper * 4));
+    }
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_stream_create(ud_encoder* e, ud_stream** out) {
+    if (!e || !out) return fail(UD_ERR_INVALID, "ud_stream_create: null argument");
+    *out = nullptr;
+    if (e->free_slots.empty()) return fail(UD_ERR_CAPACITY, "ud_stream_create: all %d stream slots in use", e->cfg.max_streams);
+    int slot = e->free_slots.back();
+    int rc = zero_slot(e, slot);
+    if (rc != UD_OK) return rc;
+    e->free_slots.pop_back();
+    ud_stream* s = new ud_stream{e, slot, 0, 0};
+    e->live.push_back(s);
+    *out = s;
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_stream_reset(ud_stream* s) {
+    if (!s) return fail(UD_ERR_INVALID, "ud_stream_reset: null stream");
+    HIPC(hipDeviceSynchronize());
+    int rc = zero_slot(s->enc, s->slot);
+    if (rc != UD_OK) return rc;
+    s->frames = 0;
+    s->steps = 0;
+    return UD_OK;
+}
+
+extern "C" UD_API void ud_stream_destroy(ud_stream* s) {
+    if (!s) return;
+    ud_encoder* e = s->enc;
+    for (size_t i = 0; i < e->live.size(); i++)
+        if (e->live[i] == s) { e->live.erase(e->live.begin() + i); break; }
+    e->free_slots.push_back(s->slot);
+    delete s;
+}
+
+extern "C" UD_API int ud_stream_info(const ud_stream* s, int32_t* cache_len, int32_t* steps) {
+    if (!s) return fail(UD_ERR_INVALID, "ud_stream_info: null stream");
+    if (cache_len) *cache_len = (int32_t)(s->frames < s->enc->L ? s->frames : s->enc->L);
+    if (steps) *steps = s->steps;
+    return UD_OK;
+}
+
+static int check_batch(ud_encoder* e, ud_stream* const* streams, int n, int T, const char* who) {
+    if (!e || !streams) return fail(UD_ERR_INVALID, "%s: null argument", who);
+    if (n < 1 || n > e->cfg.max_streams) return fail(UD_ERR_SHAPE, "%s: n=%d outside [1, %d]", who, n, e->cfg.max_streams);
+    if (T < 1 || T > e->cfg.max_chunk) return fail(UD_ERR_SHAPE, "%s: T=%d outside [1, %d]", who, T, e->cfg.max_chunk);
+    std::vector<char> seen(e->cfg.max_streams, 0);
+    for (int i = 0; i < n; i++) {
+        ud_stream* s = streams[i];
+        if (!s || s->enc != e) return fail(UD_ERR_INVALID, "%s: stream %d is null or of another encoder", who, i);
+        if (seen[s->slot]) return fail(UD_ERR_INVALID, "%s: stream %d appears twice in the batch", who, i);
+        seen[s->slot] = 1;
+    }
+    return UD_OK;
+}
+
+// Writes the batch descriptor into the next pinned staging buffer and copies it to the device.
+static int upload_desc(ud_encoder* e, ud_stream* const* streams, int n, int T, const int32_t* valid, hipStream_t st) {
+    const int k = e->desc_next;
+    e->desc_next = (k + 1) % 4;
+    if (e->desc_used[k]) HIPC(hipEventSynchronize(e->desc_ev[k]));
+    int32_t* d = e->desc_host[k];
+    for (int i = 0; i < n; i++) {
+        int v = valid ? valid[i] : T;
+        d[i * DESC_INTS + 0] = streams[i]->slot;
+        d[i * DESC_INTS + 1] = (int32_t)(streams[i]->frames % (int64_t)(e->L * (e->Kc - 1)));
+        d[i * DESC_INTS + 2] = v < 0 ? 0 : (v > T ? T : v);
+        d[i * DESC_INTS + 3] = (int32_t)(streams[i]->frames < e->L ? streams[i]->frames : e->L);
+    }
+    HIPC(hipMemcpyAsync(e->desc_dev, d, (size_t)n * DESC_INTS * 4, hipMemcpyHostToDevice, st));
+    HIPC(hipEventRecord(e->desc_ev[k], st));
+    e->desc_used[k] = true;
+    return UD_OK;
+}
+
+// ---------------------------------------------------------------- the step
+
+// encodeLayer (FastConformer.swift:262-321) for every layer, over n streams x T rows, on `st`.
+// The fp32 residual stream `res` is updated in place by the residual GEMMs.
+static int enqueue_step(ud_encoder* e, int n, int T, const float* x, float* out, hipStream_t st) {
+    const int D = e->D, ff = e->ff, M = n * T;
+    const bool bf = e->bf;
+    auto gemm = [&](const void* A, const void* W, void* C, int N, int K, int ldc, int epi, int act, float scale,
+                    const char* what) -> int {
+        GemmArgs g{};
+        g.A = A; g.W = W; g.C = C; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldw = K; g.ldc = ldc;
+        g.epi = epi; g.act = act; g.out_scale = scale; g.desc = e->desc_dev; g.T = T;
+        return launch_status(launch_gemm(g, bf, st), what);
+    };
+    for (int li = 0; li < e->layers; li++) {
+        LayerDev& l = e->lw[li];
+        const size_t roff = (size_t)li * e->ring_layer_elems * e->esz;
+        // res <- x (layer 0) or norm_out of the previous layer; z <- norm_feed_forward1(res)
+        if (li == 0)
+            LAUNCH(launch_layernorm2(x, e->res, nullptr, nullptr, l.ln[0], l.ln[1], e->z, bf, M, D, st), "layernorm");
+        else
+            LAUNCH(launch_layernorm2(e->res, e->res, e->lw[li - 1].ln[10], e->lw[li - 1].ln[11], l.ln[0], l.ln[1],
+                                     e->z, bf, M, D, st), "layernorm");
+        int rc;
+        // FF1: res += 0.5 * linear2(silu(linear1(z)))
+        if ((rc = gemm(e->z, l.ff1_w1, e->h, ff, D, ff, EPI_STORE, ACT_SILU, 1.0f, "ff1.linear1"))) return rc;
+        if ((rc = gemm(e->h, l.ff1_w2, e->res, D, ff, D, EPI_RESID, ACT_NONE, 0.5f, "ff1.linear2"))) return rc;
+        // MHSA: res += linear_out(relpos_attention(q, [cache; k], [cache; v]))
+        LAUNCH(launch_layernorm(e->res, l.ln[2], l.ln[3], e->z, bf, M, D, ACT_NONE, st), "layernorm");
+        if ((rc = gemm(e->z, l.wqkv, e->qkv, 3 * D, D, 3 * D, EPI_STORE, ACT_NONE, 1.0f, "qkv"))) return rc;
+        RingArgs ra{};
+        ra.kring = static_cast<char*>(e->kring) + roff;
+        ra.vring = static_cast<char*>(e->vring) + roff;
+        ra.qkv = e->qkv; ra.P = l.P; ra.u = l.bias_u; ra.vb = l.bias_v; ra.att = e->att; ra.desc = e->desc_dev;
+        ra.n = n; ra.T = T; ra.L = e->L; ra.H = e->H; ra.rel_offset = e->rel_offset; ra.n_rel = e->n_rel;
+        ra.scale = 1.0f / std::sqrt((float)e->dk);
+        LAUNCH(launch_relpos_ring(ra, bf, st), "relpos attention");
+        if ((rc = gemm(e->att, l.wo, e->res, D, D, D, EPI_RESID, ACT_NONE, 1.0f, "linear_out"))) return rc;
+        // Conv module: res += pw2(silu(LN(dwconv([ring; glu(pw1(z))]))))
+        LAUNCH(launch_layernorm(e->res, l.ln[4], l.ln[5], e->z, bf, M, D, ACT_NONE, st), "layernorm");
+        if (bf) {
+            if ((rc = gemm(e->z, l.pw1, e->g, 2 * D, D, D, EPI_GLU, ACT_NONE, 1.0f, "pointwise_conv1"))) return rc;
+        } else {
+            if ((rc = gemm(e->z, l.pw1, e->pw, 2 * D, D, 2 * D, EPI_STORE_F32, ACT_NONE, 1.0f, "pointwise_conv1")))
+                return rc;
+            LAUNCH(launch_glu_mask(e->pw, e->g, M, D, e->desc_dev, T, st), "glu");
+        }
+        ConvArgs ca{};
+        ca.g = e->g; ca.ring = e->cring + (size_t)li * e->cring_layer_elems; ca.w_t = l.dw_t;
+        ca.ln_g = l.ln[6]; ca.ln_b = l.ln[7]; ca.z = e->z; ca.desc = e->desc_dev;
+        ca.n = n; ca.T = T; ca.D = D; ca.K = e->Kc; ca.z_bf16 = bf;
+        LAUNCH(launch_dwconv_ln(ca, st), "depthwise conv");
+        if ((rc = gemm(e->z, l.pw2, e->res, D, D, D, EPI_RESID, ACT_NONE, 1.0f, "pointwise_conv2"))) return rc;
+        // FF2: res += 0.5 * linear2(silu(linear1(LN(res))))
+        LAUNCH(launch_layernorm(e->res, l.ln[8], l.ln[9], e->z, bf, M, D, ACT_NONE, st), "layernorm");
+        if ((rc = gemm(e->z, l.ff2_w1, e->h, ff, D, ff, EPI_STORE, ACT_SILU, 1.0f, "ff2.linear1"))) return rc;
+        if ((rc = gemm(e->h, l.ff2_w2, e->res, D, ff, D, EPI_RESID, ACT_NONE, 0.5f, "ff2.linear2"))) return rc;
+    }
+    const LayerDev& last = e->lw[e->layers - 1];
+    LAUNCH(launch_layernorm(e->res, last.ln[10], last.ln[11], out, false, M, D, ACT_NONE, st), "layernorm");
+    return UD_OK;
+}
+
+static int run_step(ud_encoder* e, int n, int T, const float* x, float* out, hipStream_t st) {
+    if (!e->use_graphs) return enqueue_step(e, n, T, x, out, st);
+    GraphEntry* ge = nullptr;
+    for (auto& g : e->graphs)
+        if (g.n == n && g.T == T && g.x == x && g.out == out) { ge = &g; break; }
+    if (!ge) {
+        if (e->graphs.size() >= 8) {
+            HIPC(hipStreamSynchronize(st));
+            (void)hipGraphExecDestroy(e->graphs.front().exec);
+            (void)hipGraphDestroy(e->graphs.front().graph);
+            e->graphs.erase(e->graphs.begin());
+        }
+        GraphEntry g{n, T, x, out, nullptr, nullptr};
+        HIPC(hipStreamBeginCapture(e->capture_stream, hipStreamCaptureModeThreadLocal));
+        int rc = enqueue_step(e, n, T, x, out, e->capture_stream);
+        hipGraph_t graph = nullptr;
+        hipError_t ce = hipStreamEndCapture(e->capture_stream, &graph);
+        if (rc != UD_OK) { if (graph) (void)hipGraphDestroy(graph); return rc; }
+        if (ce != hipSuccess) return fail(UD_ERR_HIP, "graph capture failed: %s", hipGetErrorString(ce));
+        g.graph = graph;
+        HIPC(hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0));
+        e->graphs.push_back(g);
+        ge = &e->graphs.back();
+    }
+    HIPC(hipGraphLaunch(ge->exec, st));
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_encoder_step(ud_encoder* e, ud_stream* const* streams, int32_t n, int32_t T,
+                                      const float* x_dev, const int32_t* valid_T_host, float* out_dev,
+                                      void* hip_stream) {
+    int rc = check_batch(e, streams, n, T, "ud_encoder_step");
+    if (rc != UD_OK) return rc;
+    if (!e->finalized) return fail(UD_ERR_STATE, "ud_encoder_step: encoder not finalized");
+    if (!x_dev || !out_dev) return fail(UD_ERR_INVALID, "ud_encoder_step: null input/output");
+    if (x_dev == out_dev) return fail(UD_ERR_INVALID, "ud_encoder_step: out_dev aliases x_dev");
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    if ((rc = upload_desc(e, streams, n, T, valid_T_host, st)) != UD_OK) return rc;
+    if ((rc = run_step(e, n, T, x_dev, out_dev, st)) != UD_OK) return rc;
+    for (int i = 0; i < n; i++) { streams[i]->frames += T; streams[i]->steps++; }
+    return UD_OK;
+}
+
+static RingArgs ring_args(ud_encoder* e, int n, int T, int layer, const void* qkv, void* att) {
+    const size_t roff = (size_t)layer * e->ring_layer_elems * e->esz;
+    const LayerDev& l = e->lw[layer];
+    RingArgs ra{};
+    ra.kring = static_cast<char*>(e->kring) + roff;
+    ra.vring = static_cast<char*>(e->vring) + roff;
+    ra.qkv = qkv; ra.P = l.P; ra.u = l.bias_u; ra.vb = l.bias_v; ra.att = att; ra.desc = e->desc_dev;
+    ra.n = n; ra.T = T; ra.L = e->L; ra.H = e->H; ra.rel_offset = e->rel_offset; ra.n_rel = e->n_rel;
+    ra.scale = 1.0f / std::sqrt((float)e->dk);
+    return ra;
+}
+
+static int check_layer_call(ud_encoder* e, ud_stream* const* streams, int n, int T, int layer, const void* qkv,
+                            const void* att, const char* who) {
+    int rc = check_batch(e, streams, n, T, who);
+    if (rc != UD_OK) return rc;
+    if (!e->finalized) return fail(UD_ERR_STATE, "%s: encoder not finalized", who);
+    if (layer < 0 || layer >= e->layers) return fail(UD_ERR_SHAPE, "%s: bad layer %d", who, layer);
+    if (!qkv || !att) return fail(UD_ERR_INVALID, "%s: null buffer", who);
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_layer_attention(ud_encoder* e, ud_stream* const* streams, int32_t n, int32_t T, int32_t layer,
+                                         const void* qkv_dev, const int32_t* valid_T_host, void* att_dev,
+                                         void* hip_stream) {
+    int rc = check_layer_call(e, streams, n, T, layer, qkv_dev, att_dev, "ud_layer_attention");
+    if (rc != UD_OK) return rc;
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    if ((rc = upload_desc(e, streams, n, T, valid_T_host, st)) != UD_OK) return rc;
+    return launch_status(launch_relpos_ring(ring_args(e, n, T, layer, qkv_dev, att_dev), e->bf, st),
+                         "relpos attention");
+}
+
+extern "C" UD_API int ud_time_layer_attention(ud_encoder* e, ud_stream* const* streams, int32_t n, int32_t T,
+                                              int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
+                                              void* hip_stream, float* avg_ms) {
+    int rc = check_layer_call(e, streams, n, T, layer, qkv_dev, att_dev, "ud_time_layer_attention");
+    if (rc != UD_OK) return rc;
+    if (iters < 1 || !avg_ms) return fail(UD_ERR_INVALID, "ud_time_layer_attention: bad iters / output");
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    if ((rc = upload_desc(e, streams, n, T, nullptr, st)) != UD_OK) return rc;
+    const RingArgs ra = ring_args(e, n, T, layer, qkv_dev, att_dev);
+    hipEvent_t ev[2];
+    HIPC(hipEventCreate(&ev[0]));
+    HIPC(hipEventCreate(&ev[1]));
+    rc = launch_status(launch_relpos_ring(ra, e->bf, st), "relpos attention");   // warm-up
+    if (rc == UD_OK && hipEventRecord(ev[0], st) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventRecord failed");
+    for (int i = 0; rc == UD_OK && i < iters; i++) rc = launch_status(launch_relpos_ring(ra, e->bf, st), "relpos attention");
+    if (rc == UD_OK && hipEventRecord(ev[1], st) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventRecord failed");
+    float ms = 0.0f;
+    if (rc == UD_OK && hipEventSynchronize(ev[1]) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventSynchronize failed");
+    if (rc == UD_OK && hipEventElapsedTime(&ms, ev[0], ev[1]) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventElapsedTime failed");
+    (void)hipEventDestroy(ev[0]);
+    (void)hipEventDestroy(ev[1]);
+    if (rc == UD_OK) *avg_ms = ms / (float)iters;
+    return rc;
+}
+
+extern "C" UD_API int ud_stream_advance(ud_stream* const* streams, int32_t n, int32_t T) {
+    if (!streams || n < 0 || T < 0) return fail(UD_ERR_INVALID, "ud_stream_advance: bad argument");
+    for (int i = 0; i < n; i++) {
+        if (!streams[i]) return fail(UD_ERR_INVALID, "ud_stream_advance: null stream");
+        streams[i]->frames += T;
+        streams[i]->steps++;
+    }
+    return UD_OK;
+}
+
+// ---------------------------------------------------------------- cache export / import
+
+static int cache_io(ud_stream* s, int layer, float* k, float* v, float* conv, const float* ik, const float* iv,
+                    const float* iconv, bool do_import) {
+    ud_encoder* e = s->enc;
+    if (layer < 0 || layer >= e->layers) return fail(UD_ERR_SHAPE, "cache: bad layer %d", layer);
+    HIPC(hipDeviceSynchronize());
+    const int L = e->L, H = e->H, dk = e->dk, D = e->D, KC = e->Kc - 1;
+    const size_t per = (size_t)H * L * dk, cper = (size_t)KC * D;
+    char* kb = static_cast<char*>(e->kring) + ((size_t)layer * e->ring_layer_elems + s->slot * per) * e->esz;
+    char* vb = static_cast<char*>(e->vring) + ((size_t)layer * e->ring_layer_elems + s->slot * per) * e->esz;
+    float* cb = e->cring + (size_t)layer * e->cring_layer_elems + s->slot * cper;
+    const int wpos = (int)(s->frames % L), cpos = (int)(s->frames % KC);
+    std::vector<uint8_t> kr(per * e->esz), vr(per * e->esz);
+    std::vector<float> cr(cper);
+    auto get = [&](const std::vector<uint8_t>& buf, size_t i) -> float {
+        return e->bf ? host_bf16_to_f(reinterpret_cast<const uint16_t*>(buf.data())[i])
+                     : reinterpret_cast<const float*>(buf.data())[i];
+    };
+    auto put = [&](std::vector<uint8_t>& buf, size_t i, float x) {
+        if (e->bf) reinterpret_cast<uint16_t*>(buf.data())[i] = host_bf16(x);
+        else reinterpret_cast<float*>(buf.data())[i] = x;
+    };
+    if (!do_import) {
+        HIPC(hipMemcpy(kr.data(), kb, kr.size(), hipMemcpyDeviceToHost));
+        HIPC(hipMemcpy(vr.data(), vb, vr.size(), hipMemcpyDeviceToHost));
+        HIPC(hipMemcpy(cr.data(), cb, cr.size() * 4, hipMemcpyDeviceToHost));
+    }
+    for (int r = 0; r < L; r++) {
+        const int sl = (wpos + r) % L;
+        for (int h = 0; h < H; h++)
+            for (int d = 0; d < dk; d++) {
+                const size_t ri = ((size_t)h * L + sl) * dk + d, li = (size_t)r * D + h * dk + d;
+                if (do_import) { put(kr, ri, ik[li]); put(vr, ri, iv[li]); }
+                else { if (k) k[li] = get(kr, ri); if (v) v[li] = get(vr, ri); }
+            }
+    }
+    for (int r = 0; r < KC; r++) {
+        const int sl = (cpos + r) % KC;
+        for (int d = 0; d < D; d++) {
+            if (do_import) cr[(size_t)sl * D + d] = iconv[(size_t)r * D + d];
+            else if (conv) conv[(size_t)r * D + d] = cr[(size_t)sl * D + d];
+        }
+    }
+    if (do_import) {
+        HIPC(hipMemcpy(kb, kr.data(), kr.size(), hipMemcpyHostToDevice));
+        HIPC(hipMemcpy(vb, vr.data(), vr.size(), hipMemcpyHostToDevice));
+        HIPC(hipMemcpy(cb, cr.data(), cr.size() * 4, hipMemcpyHostToDevice));
+    }
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_stream_export_cache(const ud_stream* s, int32_t layer, float* k_host, float* v_host,
+                                             float* conv_host, int32_t* cache_len) {
+    if (!s) return fail(UD_ERR_INVALID, "ud_stream_export_cache: null stream");
+    int rc = cache_io(const_cast<ud_stream*>(s), layer, k_host, v_host, conv_host, nullptr, nullptr, nullptr, false);
+    if (rc == UD_OK && cache_len) *cache_len = (int32_t)(s->frames < s->enc->L ? s->frames : s->enc->L);
+    return rc;
+}
+
+extern "C" UD_API int ud_stream_import_cache(ud_stream* s, int32_t layer, const float* k_host, const float* v_host,
+                                             const float* conv_host, int32_t cache_len) {
+    if (!s || !k_host || !v_host || !conv_host) return fail(UD_ERR_INVALID, "ud_stream_import_cache: null argument");
+    ud_encoder* e = s->enc;
+    if (cache_len < 0 || cache_len > e->L) return fail(UD_ERR_SHAPE, "ud_stream_import_cache: cache_len %d", cache_len);
+    // Keep the ring origin when the window length is unchanged, so layers imported one by one stay
+    // consistent; otherwise re-base (then every layer should be imported).
+    const int64_t cur = s->frames < e->L ? s->frames : e->L;
+    if (cur != cache_len) s->frames = cache_len;
+    return cache_io(s, layer, nullptr, nullptr, nullptr, k_host, v_host, conv_host, true);
+}
+
+// ---------------------------------------------------------------- single-op entry
+
+extern "C" UD_API int ud_relpos_attention(int32_t dtype, const void* q, const void* k, const void* v, const void* p,
+                                          const float* u, const float* vb, const int32_t* ranges, void* out,
+                                          int32_t Tq, int32_t Tk, int32_t H, int32_t dk, int32_t rel_offset,
+                                          int32_t n_rel, void* hip_stream) {
+    if (!q || !k || !v || !p || !u || !vb || !ranges || !out) return fail(UD_ERR_INVALID, "ud_relpos_attention: null pointer");
+    if (dtype != UD_F32 && dtype != UD_BF16) return fail(UD_ERR_INVALID, "ud_relpos_attention: bad dtype");
+    if (dk != 16 && dk != 32 && dk != 64 && dk != 128) return fail(UD_ERR_SHAPE, "ud_relpos_attention: dk=%d", dk);
+    if (Tq < 1 || Tq > 16 || Tk < 1 || H < 1 || n_rel < 1) return fail(UD_ERR_SHAPE, "ud_relpos_attention: bad sizes");
+    const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)p | (uintptr_t)out;
+    if (al % 16 != 0) return fail(UD_ERR_INVALID, "ud_relpos_attention: pointers must be 16-byte aligned");
+    OpArgs a{};
+    a.q = q; a.k = k; a.v = v; a.p = p; a.u = u; a.vb = vb; a.ranges = ranges; a.out = out;
+    a.Tq = Tq; a.Tk = Tk; a.H = H; a.dk = dk; a.rel_offset = rel_offset; a.n_rel = n_rel;
+    a.scale = 1.0f / std::sqrt((float)dk);
+    return launch_status(launch_relpos_op(a, dtype == UD_BF16, static_cast<hipStream_t>(hip_stream)), "relpos attention");
+}

@@ -1,0 +1,268 @@
+// Row-wise kernels of the encoder step: LayerNorm (single and fused pair), the fp32-mode GLU, and
+// the causal depthwise conv fused with the conv module's LayerNorm + SiLU and the conv-cache ring.
+//
+// LayerNorm semantics: Sources/DictatorEngine/Metal/20_conformer.metal:25-49 (two passes,
+// population variance, y = act((x-mean)*rsqrt(var+eps)*g + b)), eps 1e-5 (Core/Ops.swift:27).
+// One wave64 per row: the row lives in registers (D/64 values per lane, 16-byte loads), so the
+// two passes cost one HBM read and one write.
+#include "ud_common.hpp"
+#include "kernels.hpp"
+
+namespace ud {
+
+constexpr float LN_EPS = 1e-5f;
+
+template <int NPER>
+__device__ __forceinline__ void ln_row_stats(const float4 (&x)[NPER], int D, float& mean, float& rstd) {
+    float s = 0.0f;
+#pragma unroll
+    for (int p = 0; p < NPER; p++) s += (x[p].x + x[p].y) + (x[p].z + x[p].w);
+    mean = wave_sum(s) / (float)D;
+    float v = 0.0f;
+#pragma unroll
+    for (int p = 0; p < NPER; p++) {
+        float a = x[p].x - mean, b = x[p].y - mean, c = x[p].z - mean, d = x[p].w - mean;
+        v += (a * a + b * b) + (c * c + d * d);
+    }
+    rstd = 1.0f / sqrtf(wave_sum(v) / (float)D + LN_EPS);
+}
+
+template <int NPER>
+__device__ __forceinline__ void ln_apply(float4 (&x)[NPER], const float* g, const float* b, float mean, float rstd,
+                                         int lane, int act) {
+#pragma unroll
+    for (int p = 0; p < NPER; p++) {
+        const int c = (p * 64 + lane) * 4;
+        float4 gg = *reinterpret_cast<const float4*>(g + c);
+        float4 bb = *reinterpret_cast<const float4*>(b + c);
+        x[p].x = apply_act((x[p].x - mean) * rstd * gg.x + bb.x, act);
+        x[p].y = apply_act((x[p].y - mean) * rstd * gg.y + bb.y, act);
+        x[p].z = apply_act((x[p].z - mean) * rstd * gg.z + bb.z, act);
+        x[p].w = apply_act((x[p].w - mean) * rstd * gg.w + bb.w, act);
+    }
+}
+
+template <int NPER>
+__device__ __forceinline__ void store_row(void* out, bool bf, int64_t row, int D, const float4 (&x)[NPER], int lane) {
+#pragma unroll
+    for (int p = 0; p < NPER; p++) {
+        const int c = (p * 64 + lane) * 4;
+        if (bf) {
+            uint2 u;
+            u.x = (uint32_t)f2bf(x[p].x) | ((uint32_t)f2bf(x[p].y) << 16);
+            u.y = (uint32_t)f2bf(x[p].z) | ((uint32_t)f2bf(x[p].w) << 16);
+            *reinterpret_cast<uint2*>(static_cast<bf16*>(out) + row * D + c) = u;
+        } else {
+            *reinterpret_cast<float4*>(static_cast<float*>(out) + row * D + c) = x[p];
+        }
+    }
+}
+
+template <int NPER>
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* x, const float* g, const float* b, void* out,
+                                                        int out_bf16, int rows, int D, int act) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float4 v[NPER];
+#pragma unroll
+    for (int p = 0; p < NPER; p++) v[p] = *reinterpret_cast<const float4*>(x + row * D + (p * 64 + lane) * 4);
+    float mean, rstd;
+    ln_row_stats(v, D, mean, rstd);
+    ln_apply(v, g, b, mean, rstd, lane, act);
+    store_row(out, out_bf16 != 0, row, D, v, lane);
+}
+
+// res <- LN_a(src) (copy when ga is null), z <- LN_b(res).  Joins one layer's norm_out with the
+// next layer's norm_feed_forward1 (FastConformer.swift:320 then :277).
+template <int NPER>
+__global__ __launch_bounds__(256) void layernorm2_kernel(const float* src, float* res, const float* ga, const float* ba,
+                                                         const float* gb, const float* bb, void* z, int z_bf16,
+                                                         int rows, int D) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float4 v[NPER];
+#pragma unroll
+    for (int p = 0; p < NPER; p++) v[p] = *reinterpret_cast<const float4*>(src + row * D + (p * 64 + lane) * 4);
+    float mean, rstd;
+    if (ga != nullptr) {
+        ln_row_stats(v, D, mean, rstd);
+        ln_apply(v, ga, ba, mean, rstd, lane, ACT_NONE);
+    }
+    store_row(res, false, row, D, v, lane);
+    ln_row_stats(v, D, mean, rstd);
+    ln_apply(v, gb, bb, mean, rstd, lane, ACT_NONE);
+    store_row(z, z_bf16 != 0, row, D, v, lane);
+}
+
+// GLU over channels with the frame mask, fp32 mode (Metal/20_conformer.metal:76-85 and
+// FastConformer.swift:299-302): g[m, d] = pw[m, d] * sigmoid(pw[m, D + d]); rows t >= valid -> 0.
+__global__ void glu_mask_kernel(const float* pw, float* g, int M, int D, const int32_t* desc, int T) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)M * D) return;
+    const int m = (int)(idx / D), d = (int)(idx % D);
+    const int s = m / T, t = m - s * T;
+    const float y = pw[(int64_t)m * 2 * D + d] * sigmoidf(pw[(int64_t)m * 2 * D + D + d]);
+    g[idx] = t < desc[s * DESC_INTS + 2] ? y : 0.0f;
+}
+
+// Causal depthwise conv k=KC+1 over [conv cache (KC rows, oldest first) ; T new rows]
+// (Metal/20_conformer.metal:87-102, tap KC = the current frame), then the conv module's LayerNorm
+// + SiLU (FastConformer.swift:303-306).  One workgroup per stream, 4 channels per thread, the
+// whole [KC + T] x 4 window in registers.  The cache is a ring of KC rows per stream: logical row r
+// is slot (frames + r) % KC; new row t (only the last KC matter) goes to slot (frames + t) % KC,
+// written by the thread that read the slot, so the update is in place with no hazard.
+template <int KC, int TMAX>
+__global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
+    const int s = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nw = blockDim.x / 64;
+    const int D = a.D, T = a.T;
+    const int c0 = tid * 4;
+    const int32_t* d = a.desc + s * DESC_INTS;
+    const int slot = d[0], frames = d[1];
+    const int cpos = frames % KC;
+    float* ring = a.ring + (int64_t)slot * KC * D;
+
+    float4 in[KC + TMAX];
+#pragma unroll
+    for (int r = 0; r < KC; r++) {
+        int sr = cpos + r;
+        sr -= (sr >= KC) ? KC : 0;
+        in[r] = *reinterpret_cast<const float4*>(ring + (int64_t)sr * D + c0);
+    }
+#pragma unroll
+    for (int t = 0; t < TMAX; t++)
+        in[KC + t] = t < T ? *reinterpret_cast<const float4*>(a.g + ((int64_t)s * T + t) * D + c0)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 w[KC + 1];
+#pragma unroll
+    for (int k = 0; k <= KC; k++) w[k] = *reinterpret_cast<const float4*>(a.w_t + (int64_t)k * D + c0);
+
+    float4 o[TMAX];
+#pragma unroll
+    for (int t = 0; t < TMAX; t++) {
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k <= KC; k++) {
+            acc.x += w[k].x * in[t + k].x; acc.y += w[k].y * in[t + k].y;
+            acc.z += w[k].z * in[t + k].z; acc.w += w[k].w * in[t + k].w;
+        }
+        o[t] = acc;
+    }
+    // Ring update (all reads of this thread's slots are done).
+#pragma unroll
+    for (int t = 0; t < TMAX; t++) {
+        if (t < T && t >= T - KC) {
+            int sr = (cpos + t) % KC;
+            *reinterpret_cast<float4*>(ring + (int64_t)sr * D + c0) = in[KC + t];
+        }
+    }
+
+    // LayerNorm over the D channels of each frame: block reductions through LDS.
+    __shared__ float red[4][TMAX];
+    __shared__ float stat[TMAX];
+    float part[TMAX];
+#pragma unroll
+    for (int t = 0; t < TMAX; t++) part[t] = wave_sum((o[t].x + o[t].y) + (o[t].z + o[t].w));
+    if (lane == 0)
+#pragma unroll
+        for (int t = 0; t < TMAX; t++) red[wave][t] = part[t];
+    __syncthreads();
+    if (tid < TMAX) {
+        float sum = 0.f;
+        for (int w2 = 0; w2 < nw; w2++) sum += red[w2][tid];
+        stat[tid] = sum / (float)D;
+    }
+    __syncthreads();
+    float mean[TMAX];
+#pragma unroll
+    for (int t = 0; t < TMAX; t++) {
+        mean[t] = stat[t];
+        float a0 = o[t].x - mean[t], a1 = o[t].y - mean[t], a2 = o[t].z - mean[t], a3 = o[t].w - mean[t];
+        part[t] = wave_sum((a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3));
+    }
+    __syncthreads();
+    if (lane == 0)
+#pragma unroll
+        for (int t = 0; t < TMAX; t++) red[wave][t] = part[t];
+    __syncthreads();
+    if (tid < TMAX) {
+        float sum = 0.f;
+        for (int w2 = 0; w2 < nw; w2++) sum += red[w2][tid];
+        stat[tid] = 1.0f / sqrtf(sum / (float)D + LN_EPS);
+    }
+    __syncthreads();
+    const float4 gg = *reinterpret_cast<const float4*>(a.ln_g + c0);
+    const float4 bb = *reinterpret_cast<const float4*>(a.ln_b + c0);
+#pragma unroll
+    for (int t = 0; t < TMAX; t++) {
+        if (t >= T) break;
+        const float rstd = stat[t];
+        float4 y;
+        y.x = silu((o[t].x - mean[t]) * rstd * gg.x + bb.x);
+        y.y = silu((o[t].y - mean[t]) * rstd * gg.y + bb.y);
+        y.z = silu((o[t].z - mean[t]) * rstd * gg.z + bb.z);
+        y.w = silu((o[t].w - mean[t]) * rstd * gg.w + bb.w);
+        const int64_t row = (int64_t)s * T + t;
+        if (a.z_bf16) {
+            uint2 u;
+            u.x = (uint32_t)f2bf(y.x) | ((uint32_t)f2bf(y.y) << 16);
+            u.y = (uint32_t)f2bf(y.z) | ((uint32_t)f2bf(y.w) << 16);
+            *reinterpret_cast<uint2*>(static_cast<bf16*>(a.z) + row * D + c0) = u;
+        } else {
+            *reinterpret_cast<float4*>(static_cast<float*>(a.z) + row * D + c0) = y;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- launchers
+
+int launch_layernorm(const float* x, const float* g, const float* b, void* out, bool out_bf16, int rows, int D,
+                     int act, hipStream_t st) {
+    if (rows <= 0) return 0;
+    dim3 grid((rows + 3) / 4), block(256);
+    switch (D) {
+        case 256: hipLaunchKernelGGL(layernorm_kernel<1>, grid, block, 0, st, x, g, b, out, (int)out_bf16, rows, D, act); break;
+        case 512: hipLaunchKernelGGL(layernorm_kernel<2>, grid, block, 0, st, x, g, b, out, (int)out_bf16, rows, D, act); break;
+        case 1024: hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, st, x, g, b, out, (int)out_bf16, rows, D, act); break;
+        case 2048: hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, st, x, g, b, out, (int)out_bf16, rows, D, act); break;
+        default: return -2;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_layernorm2(const float* src, float* res, const float* ga, const float* ba, const float* gb,
+                      const float* bb, void* z, bool z_bf16, int rows, int D, hipStream_t st) {
+    if (rows <= 0) return 0;
+    dim3 grid((rows + 3) / 4), block(256);
+    switch (D) {
+        case 256: hipLaunchKernelGGL(layernorm2_kernel<1>, grid, block, 0, st, src, res, ga, ba, gb, bb, z, (int)z_bf16, rows, D); break;
+        case 512: hipLaunchKernelGGL(layernorm2_kernel<2>, grid, block, 0, st, src, res, ga, ba, gb, bb, z, (int)z_bf16, rows, D); break;
+        case 1024: hipLaunchKernelGGL(layernorm2_kernel<4>, grid, block, 0, st, src, res, ga, ba, gb, bb, z, (int)z_bf16, rows, D); break;
+        case 2048: hipLaunchKernelGGL(layernorm2_kernel<8>, grid, block, 0, st, src, res, ga, ba, gb, bb, z, (int)z_bf16, rows, D); break;
+        default: return -2;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_glu_mask(const float* pw, float* g, int M, int D, const int32_t* desc, int T, hipStream_t st) {
+    const int64_t n = (int64_t)M * D;
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(glu_mask_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, pw, g, M, D, desc, T);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_dwconv_ln(const ConvArgs& a, hipStream_t st) {
+    if (a.K != 9 || a.D % 256 != 0 || a.D / 4 > 1024 || a.T < 1 || a.T > 16 || a.n < 1) return -2;
+    dim3 grid(a.n), block(a.D / 4);
+    if (a.D / 4 != 256) return -2;   // the block reduction is sized for 4 waves
+    if (a.T <= 2) hipLaunchKernelGGL((dwconv_ln_kernel<8, 2>), grid, block, 0, st, a);
+    else if (a.T <= 4) hipLaunchKernelGGL((dwconv_ln_kernel<8, 4>), grid, block, 0, st, a);
+    else if (a.T <= 8) hipLaunchKernelGGL((dwconv_ln_kernel<8, 8>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((dwconv_ln_kernel<8, 16>), grid, block, 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace ud

@@ -1,0 +1,96 @@
+// Shared device helpers for the gfx950 encoder-step kernels: bf16 storage, wave64 reductions,
+// vector loads, activations.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.hpp"
+
+namespace ud {
+
+typedef uint16_t bf16;  // bfloat16 storage (upper half of an fp32)
+
+// Widening is a shift (Sources/DictatorEngine/Metal/00_common.metal:32).
+__device__ __forceinline__ float bf2f(bf16 b) { return __uint_as_float((uint32_t)b << 16); }
+
+// Round-to-nearest-even, NaN -> 0x7FC0 (Sources/DictatorEngine/Core/Tensor.swift:116-122).
+__device__ __forceinline__ bf16 f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7FC0;
+    return (bf16)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+template <typename T> __device__ __forceinline__ float to_f(T v);
+template <> __device__ __forceinline__ float to_f<float>(float v) { return v; }
+template <> __device__ __forceinline__ float to_f<bf16>(bf16 v) { return bf2f(v); }
+
+template <typename T> __device__ __forceinline__ T from_f(float v);
+template <> __device__ __forceinline__ float from_f<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16 from_f<bf16>(float v) { return f2bf(v); }
+
+// SiLU x * sigmoid(x) (00_common.metal:25).
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+__device__ __forceinline__ float apply_act(float x, int act) {
+    if (act == ACT_SILU) return silu(x);
+    if (act == ACT_RELU) return x > 0.0f ? x : 0.0f;
+    return x;
+}
+
+// 16-byte vector of storage elements: 8 bf16 or 4 fp32.
+template <typename T> struct Vec16;
+template <> struct Vec16<float> { static constexpr int N = 4; };
+template <> struct Vec16<bf16> { static constexpr int N = 8; };
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+// Unpack a 16-byte vector of T into floats (N = Vec16<T>::N values).
+template <typename T> __device__ __forceinline__ void unpack16(uint4 v, float* f);
+template <> __device__ __forceinline__ void unpack16<float>(uint4 v, float* f) {
+    f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+    f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+}
+template <> __device__ __forceinline__ void unpack16<bf16>(uint4 v, float* f) {
+    f[0] = __uint_as_float(v.x << 16); f[1] = __uint_as_float(v.x & 0xffff0000u);
+    f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xffff0000u);
+    f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xffff0000u);
+    f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xffff0000u);
+}
+
+// DPP lane moves within 16-lane rows.
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_QUAD_1032 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_2301 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+
+// Sum over aligned groups of W lanes (W a power of two <= 64); every lane of a group receives the
+// group total.  DPP inside a 16-lane row, cross-row steps through ds_swizzle/bpermute shuffles.
+template <int W> __device__ __forceinline__ float group_sum(float v) {
+    if constexpr (W >= 2) v += dpp_mov<DPP_QUAD_1032>(v);
+    if constexpr (W >= 4) v += dpp_mov<DPP_QUAD_2301>(v);
+    if constexpr (W >= 8) v += dpp_mov<DPP_ROW_HALF_MIRROR>(v);
+    if constexpr (W >= 16) v += dpp_mov<DPP_ROW_MIRROR>(v);
+    if constexpr (W >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (W >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+template <int W> __device__ __forceinline__ float group_max(float v) {
+    if constexpr (W >= 2) v = fmaxf(v, dpp_mov<DPP_QUAD_1032>(v));
+    if constexpr (W >= 4) v = fmaxf(v, dpp_mov<DPP_QUAD_2301>(v));
+    if constexpr (W >= 8) v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
+    if constexpr (W >= 16) v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
+    if constexpr (W >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    if constexpr (W >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
+
+}  // namespace ud
