@@ -145,7 +145,7 @@ UD_API int ud_relpos_attention(int32_t dtype, const void* q_dev, const void* k_d
  * kernel the step runs between the QKV projection and linear_out (FastConformer.swift:285-291 with
  * the cache rule of :458-472).
  *   qkv_dev  [n, T, 3*d_model] in the encoder dtype: q | k_new | v_new per row
- *   att_dev  [n, T, d_model] in the encoder dtype
+ *   att_dev  [n, T, d_model] in the encoder dtype, row-major
  * Keys are [L cached ; T new], range [L - cache_len, L + valid); afterwards the T new K/V rows
  * are in the ring and the logical window is the last L rows.  Does not advance cache_len or the
  * ring position: call ud_stream_advance to commit the step (ud_encoder_step does both).

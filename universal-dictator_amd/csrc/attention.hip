@@ -49,7 +49,7 @@ struct OpSrc {
     __device__ const T* krow(int j) const { return K + (int64_t)j * ld + hoff; }
     __device__ const T* vrow(int j) const { return V + (int64_t)j * ld + hoff; }
     __device__ const T* prow(int r) const { return P + (int64_t)r * ld + hoff; }
-    __device__ T* orow(int i) const { return O + (int64_t)i * ld + hoff; }
+    __device__ void store(int i, int d, float v) const { O[(int64_t)i * ld + hoff + d] = from_f<T>(v); }
     __device__ void range(int i, int& ks, int& ke) const {
         ks = max(ranges[2 * i], 0);
         ke = min(ranges[2 * i + 1], Tk);
@@ -61,9 +61,11 @@ template <typename T>
 struct RingSrc {
     const T* kr; const T* vr;      // this (stream, head) ring slice: [L][dk]
     const T* qkv;                  // first row of this stream in [n*T, 3*D]
-    const T* P; T* O;              // P [n_rel, D]; O first row of this stream in [n*T, D]
+    const T* P; T* O;              // P [n_rel, D]; O = att [n*T, D] (bf16: fragment-major)
     const float* u; const float* vb;
     int Tq, Tk, L, D, hoff, wpos, rel_offset, n_rel, ks, ke;
+    int64_t row0;                  // global row of this stream's first query
+    bool frag;                     // bf16 output in the fragment-major layout
     __device__ const T* qrow(int i) const { return qkv + (int64_t)i * 3 * D + hoff; }
     __device__ const T* krow(int j) const {
         if (j < L) { int s = wpos + j; s -= (s >= L) ? L : 0; return kr + (int64_t)s * 128; }
@@ -74,7 +76,11 @@ struct RingSrc {
         return qkv + (int64_t)(j - L) * 3 * D + 2 * D + hoff;
     }
     __device__ const T* prow(int r) const { return P + (int64_t)r * D + hoff; }
-    __device__ T* orow(int i) const { return O + (int64_t)i * D + hoff; }
+    // The output feeds linear_out: bf16 goes fragment-major (the GEMM's operand order).
+    __device__ void store(int i, int d, float v) const {
+        if (sizeof(T) == 2 && frag) O[frag_index(row0 + i, hoff + d, D / 64)] = from_f<T>(v);
+        else O[(row0 + i) * D + hoff + d] = from_f<T>(v);
+    }
     __device__ void range(int, int& s, int& e) const { s = ks; e = ke; }
 };
 
@@ -223,7 +229,7 @@ __device__ __forceinline__ void relpos_core(const Src& src, float scale) {
         if (idx < Tq * DK) {
             int i = idx / DK, d = idx % DK;
             float l = (kl < kh) ? lrow[i] : 0.0f;
-            src.orow(i)[d] = from_f<T>(l > 0.0f ? acc[o] / l : 0.0f);
+            src.store(i, d, l > 0.0f ? acc[o] / l : 0.0f);
         }
     }
 }
@@ -259,7 +265,9 @@ __global__ __launch_bounds__(256) void relpos_ring_kernel(RingArgs a) {
     RingSrc<T> src;
     src.kr = kr; src.vr = vr; src.qkv = qkv;
     src.P = static_cast<const T*>(a.P);
-    src.O = static_cast<T*>(a.att) + (int64_t)s * a.T * D;
+    src.O = static_cast<T*>(a.att);
+    src.row0 = (int64_t)s * a.T;
+    src.frag = a.att_frag != 0;
     src.u = a.u + h * DK; src.vb = a.vb + h * DK;
     src.Tq = a.T; src.Tk = a.L + a.T; src.L = a.L; src.D = D; src.hoff = h * DK;
     src.wpos = wpos; src.rel_offset = a.rel_offset; src.n_rel = a.n_rel;

@@ -108,6 +108,9 @@ struct LayerDev {
     uint32_t set_mask = 0;
 };
 
+// K splits of the bf16 residual projections (when K allows; see launch_gemm).
+constexpr int KSPLIT = 4;
+
 struct GraphEntry {
     int n, T;
     const void* x;
@@ -137,7 +140,8 @@ struct ud_encoder {
     std::vector<ud_stream*> live;
     // workspace
     float* res = nullptr; void* z = nullptr; void* h = nullptr; void* qkv = nullptr; void* att = nullptr;
-    float* g = nullptr; float* pw = nullptr;
+    float* pw = nullptr;
+    float* part = nullptr;          // split-K residual partial slabs [KSPLIT][max_rows][D]
     int32_t* desc_dev = nullptr;
     int32_t* desc_host[4] = {};
     hipEvent_t desc_ev[4] = {};
@@ -164,7 +168,7 @@ static void free_encoder(ud_encoder* e) {
         for (void* p : ps) if (p) (void)hipFree(p);
         for (float* p : l.ln) if (p) (void)hipFree(p);
     }
-    void* ws[] = {e->kring, e->vring, e->cring, e->res, e->z, e->h, e->qkv, e->att, e->g, e->pw, e->desc_dev};
+    void* ws[] = {e->kring, e->vring, e->cring, e->res, e->z, e->h, e->qkv, e->att, e->pw, e->part, e->desc_dev};
     for (void* p : ws) if (p) (void)hipFree(p);
     for (int i = 0; i < 4; i++) {
         if (e->desc_host[i]) (void)hipHostFree(e->desc_host[i]);
@@ -233,15 +237,16 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
         ok &= (e->vring = dev_alloc(e->ring_layer_elems * e->layers * esz)) != nullptr;
         ok &= (e->cring = (float*)dev_alloc(e->cring_layer_elems * e->layers * 4)) != nullptr;
     }
-    const size_t R = e->max_rows;
+    // GEMM operands (z, h, att) hold whole 16-row tiles in the fragment-major bf16 layout.
+    const size_t R = e->max_rows, Rp = (R + 15) / 16 * 16;
     if (ok) {
         ok &= (e->res = (float*)dev_alloc(R * D * 4)) != nullptr;
-        ok &= (e->z = dev_alloc(R * D * esz)) != nullptr;
-        ok &= (e->h = dev_alloc(R * ff * esz)) != nullptr;
+        ok &= (e->z = dev_alloc(Rp * D * esz)) != nullptr;
+        ok &= (e->h = dev_alloc(Rp * ff * esz)) != nullptr;
         ok &= (e->qkv = dev_alloc(R * 3 * D * esz)) != nullptr;
-        ok &= (e->att = dev_alloc(R * D * esz)) != nullptr;
-        ok &= (e->g = (float*)dev_alloc(R * D * 4)) != nullptr;
-        if (!e->bf) ok &= (e->pw = (float*)dev_alloc(R * 2 * D * 4)) != nullptr;
+        ok &= (e->att = dev_alloc(Rp * D * esz)) != nullptr;
+        ok &= (e->pw = (float*)dev_alloc(R * 2 * D * 4)) != nullptr;
+        if (e->bf) ok &= (e->part = (float*)dev_alloc(KSPLIT * R * D * 4)) != nullptr;
         ok &= (e->desc_dev = (int32_t*)dev_alloc(slots * DESC_INTS * 4)) != nullptr;
     }
     for (int i = 0; ok && i < 4; i++) {
@@ -271,12 +276,16 @@ static int upload(void* dst, const void* src, size_t bytes) {
     return UD_OK;
 }
 
-// Converts `rows` x `cols` fp32 values to the encoder dtype and writes them at dst row offset.
+// Converts a `rows` x `cols` fp32 weight matrix to the encoder dtype and writes it at row offset
+// dst_row0 (a multiple of 16) of the destination: bf16 in the fragment-major GEMM layout, fp32
+// row-major.
 static int upload_matrix(ud_encoder* e, void* dst, size_t dst_row0, const float* src, size_t rows, size_t cols) {
     const size_t n = rows * cols;
     if (e->bf) {
         std::vector<uint16_t> tmp(n);
-        for (size_t i = 0; i < n; i++) tmp[i] = host_bf16(src[i]);
+        const int nk = (int)(cols / 64);
+        for (size_t r = 0; r < rows; r++)
+            for (size_t c = 0; c < cols; c++) tmp[frag_index((int64_t)r, (int)c, nk)] = host_bf16(src[r * cols + c]);
         return upload(static_cast<uint16_t*>(dst) + dst_row0 * cols, tmp.data(), n * 2);
     }
     return upload(static_cast<float*>(dst) + dst_row0 * cols, src, n * 4);
@@ -323,18 +332,7 @@ extern "C" UD_API int ud_encoder_set_weight(ud_encoder* e, const char* name, con
         case LIN_V: rc = upload_matrix(e, l.wqkv, 2 * D, host, D, D); break;
         case LIN_OUT: rc = upload_matrix(e, l.wo, 0, host, D, D); break;
         case PW2: rc = upload_matrix(e, l.pw2, 0, host, D, D); break;
-        case PW1: {
-            if (!e->bf) { rc = upload_matrix(e, l.pw1, 0, host, 2 * D, D); break; }
-            // bf16: interleave 16-row blocks, [value c..c+15 | gate c..c+15], for the GLU epilogue.
-            std::vector<float> perm((size_t)2 * D * D);
-            for (int64_t c = 0; c < D; c++) {
-                int64_t dv = 32 * (c / 16) + (c % 16), dg = dv + 16;
-                memcpy(&perm[dv * D], host + c * D, D * 4);
-                memcpy(&perm[dg * D], host + (D + c) * D, D * 4);
-            }
-            rc = upload_matrix(e, l.pw1, 0, perm.data(), 2 * D, D);
-            break;
-        }
+        case PW1: rc = upload_matrix(e, l.pw1, 0, host, 2 * D, D); break;
         case LIN_POS: {
             l.wpos.assign(host, host + D * D);
             if (e->bf) for (auto& v : l.wpos) v = host_bf16_to_f(host_bf16(v));
@@ -515,32 +513,48 @@ static int upload_desc(ud_encoder* e, ud_stream* const* streams, int n, int T, c
 // ---------------------------------------------------------------- the step
 
 // encodeLayer (FastConformer.swift:262-321) for every layer, over n streams x T rows, on `st`.
-// The fp32 residual stream `res` is updated in place by the residual GEMMs.
+// The fp32 residual stream `res` advances in place.  In bf16 mode the residual projections write
+// K-split partial slabs that the next LayerNorm folds into `res` (in slab order); in fp32 mode they
+// accumulate into `res` directly.
 static int enqueue_step(ud_encoder* e, int n, int T, const float* x, float* out, hipStream_t st) {
     const int D = e->D, ff = e->ff, M = n * T;
     const bool bf = e->bf;
+    Partials pend{e->part, 0};
     auto gemm = [&](const void* A, const void* W, void* C, int N, int K, int ldc, int epi, int act, float scale,
                     const char* what) -> int {
         GemmArgs g{};
         g.A = A; g.W = W; g.C = C; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldw = K; g.ldc = ldc;
-        g.epi = epi; g.act = act; g.out_scale = scale; g.desc = e->desc_dev; g.T = T;
+        g.epi = epi; g.act = act; g.out_scale = scale; g.ksplit = 1;
         return launch_status(launch_gemm(g, bf, st), what);
     };
+    // res += scale * A . W^T (N = D)
+    auto resid = [&](const void* A, const void* W, int K, float scale, const char* what) -> int {
+        if (!bf) return gemm(A, W, e->res, D, K, D, EPI_RESID, ACT_NONE, scale, what);
+        GemmArgs g{};
+        g.A = A; g.W = W; g.C = e->part; g.M = M; g.N = D; g.K = K; g.lda = K; g.ldw = K; g.ldc = D;
+        g.epi = EPI_PARTIAL; g.act = ACT_NONE; g.out_scale = scale;
+        g.ksplit = K % (128 * KSPLIT) == 0 ? KSPLIT : 1;
+        pend.n = g.ksplit;
+        return launch_status(launch_gemm(g, bf, st), what);
+    };
+    auto take = [&]() { Partials p = pend; pend.n = 0; return p; };
+    const int EPI_H = bf ? EPI_STORE_FRAG : EPI_STORE;   // FF hidden: operand of the next GEMM
     for (int li = 0; li < e->layers; li++) {
         LayerDev& l = e->lw[li];
         const size_t roff = (size_t)li * e->ring_layer_elems * e->esz;
         // res <- x (layer 0) or norm_out of the previous layer; z <- norm_feed_forward1(res)
         if (li == 0)
-            LAUNCH(launch_layernorm2(x, e->res, nullptr, nullptr, l.ln[0], l.ln[1], e->z, bf, M, D, st), "layernorm");
+            LAUNCH(launch_layernorm2(x, take(), e->res, nullptr, nullptr, l.ln[0], l.ln[1], e->z, bf, M, D, st),
+                   "layernorm");
         else
-            LAUNCH(launch_layernorm2(e->res, e->res, e->lw[li - 1].ln[10], e->lw[li - 1].ln[11], l.ln[0], l.ln[1],
-                                     e->z, bf, M, D, st), "layernorm");
+            LAUNCH(launch_layernorm2(e->res, take(), e->res, e->lw[li - 1].ln[10], e->lw[li - 1].ln[11], l.ln[0],
+                                     l.ln[1], e->z, bf, M, D, st), "layernorm");
         int rc;
         // FF1: res += 0.5 * linear2(silu(linear1(z)))
-        if ((rc = gemm(e->z, l.ff1_w1, e->h, ff, D, ff, EPI_STORE, ACT_SILU, 1.0f, "ff1.linear1"))) return rc;
-        if ((rc = gemm(e->h, l.ff1_w2, e->res, D, ff, D, EPI_RESID, ACT_NONE, 0.5f, "ff1.linear2"))) return rc;
+        if ((rc = gemm(e->z, l.ff1_w1, e->h, ff, D, ff, EPI_H, ACT_SILU, 1.0f, "ff1.linear1"))) return rc;
+        if ((rc = resid(e->h, l.ff1_w2, ff, 0.5f, "ff1.linear2"))) return rc;
         // MHSA: res += linear_out(relpos_attention(q, [cache; k], [cache; v]))
-        LAUNCH(launch_layernorm(e->res, l.ln[2], l.ln[3], e->z, bf, M, D, ACT_NONE, st), "layernorm");
+        LAUNCH(launch_layernorm(e->res, take(), l.ln[2], l.ln[3], e->z, bf, M, D, ACT_NONE, st), "layernorm");
         if ((rc = gemm(e->z, l.wqkv, e->qkv, 3 * D, D, 3 * D, EPI_STORE, ACT_NONE, 1.0f, "qkv"))) return rc;
         RingArgs ra{};
         ra.kring = static_cast<char*>(e->kring) + roff;
@@ -548,30 +562,26 @@ static int enqueue_step(ud_encoder* e, int n, int T, const float* x, float* out,
         ra.qkv = e->qkv; ra.P = l.P; ra.u = l.bias_u; ra.vb = l.bias_v; ra.att = e->att; ra.desc = e->desc_dev;
         ra.n = n; ra.T = T; ra.L = e->L; ra.H = e->H; ra.rel_offset = e->rel_offset; ra.n_rel = e->n_rel;
         ra.scale = 1.0f / std::sqrt((float)e->dk);
+        ra.att_frag = bf ? 1 : 0;
         LAUNCH(launch_relpos_ring(ra, bf, st), "relpos attention");
-        if ((rc = gemm(e->att, l.wo, e->res, D, D, D, EPI_RESID, ACT_NONE, 1.0f, "linear_out"))) return rc;
-        // Conv module: res += pw2(silu(LN(dwconv([ring; glu(pw1(z))]))))
-        LAUNCH(launch_layernorm(e->res, l.ln[4], l.ln[5], e->z, bf, M, D, ACT_NONE, st), "layernorm");
-        if (bf) {
-            if ((rc = gemm(e->z, l.pw1, e->g, 2 * D, D, D, EPI_GLU, ACT_NONE, 1.0f, "pointwise_conv1"))) return rc;
-        } else {
-            if ((rc = gemm(e->z, l.pw1, e->pw, 2 * D, D, 2 * D, EPI_STORE_F32, ACT_NONE, 1.0f, "pointwise_conv1")))
-                return rc;
-            LAUNCH(launch_glu_mask(e->pw, e->g, M, D, e->desc_dev, T, st), "glu");
-        }
+        if ((rc = resid(e->att, l.wo, D, 1.0f, "linear_out"))) return rc;
+        // Conv module: res += pw2(silu(LN(dwconv([ring; mask(glu(pw1(z)))]))))
+        LAUNCH(launch_layernorm(e->res, take(), l.ln[4], l.ln[5], e->z, bf, M, D, ACT_NONE, st), "layernorm");
+        if ((rc = gemm(e->z, l.pw1, e->pw, 2 * D, D, 2 * D, EPI_STORE_F32, ACT_NONE, 1.0f, "pointwise_conv1")))
+            return rc;
         ConvArgs ca{};
-        ca.g = e->g; ca.ring = e->cring + (size_t)li * e->cring_layer_elems; ca.w_t = l.dw_t;
+        ca.pw = e->pw; ca.ring = e->cring + (size_t)li * e->cring_layer_elems; ca.w_t = l.dw_t;
         ca.ln_g = l.ln[6]; ca.ln_b = l.ln[7]; ca.z = e->z; ca.desc = e->desc_dev;
         ca.n = n; ca.T = T; ca.D = D; ca.K = e->Kc; ca.z_bf16 = bf;
         LAUNCH(launch_dwconv_ln(ca, st), "depthwise conv");
-        if ((rc = gemm(e->z, l.pw2, e->res, D, D, D, EPI_RESID, ACT_NONE, 1.0f, "pointwise_conv2"))) return rc;
+        if ((rc = resid(e->z, l.pw2, D, 1.0f, "pointwise_conv2"))) return rc;
         // FF2: res += 0.5 * linear2(silu(linear1(LN(res))))
-        LAUNCH(launch_layernorm(e->res, l.ln[8], l.ln[9], e->z, bf, M, D, ACT_NONE, st), "layernorm");
-        if ((rc = gemm(e->z, l.ff2_w1, e->h, ff, D, ff, EPI_STORE, ACT_SILU, 1.0f, "ff2.linear1"))) return rc;
-        if ((rc = gemm(e->h, l.ff2_w2, e->res, D, ff, D, EPI_RESID, ACT_NONE, 0.5f, "ff2.linear2"))) return rc;
+        LAUNCH(launch_layernorm(e->res, take(), l.ln[8], l.ln[9], e->z, bf, M, D, ACT_NONE, st), "layernorm");
+        if ((rc = gemm(e->z, l.ff2_w1, e->h, ff, D, ff, EPI_H, ACT_SILU, 1.0f, "ff2.linear1"))) return rc;
+        if ((rc = resid(e->h, l.ff2_w2, ff, 0.5f, "ff2.linear2"))) return rc;
     }
-    const LayerDev& last = e->lw[e->layers - 1];
-    LAUNCH(launch_layernorm(e->res, last.ln[10], last.ln[11], out, false, M, D, ACT_NONE, st), "layernorm");
+    LayerDev& last = e->lw[e->layers - 1];
+    LAUNCH(launch_layernorm(e->res, take(), last.ln[10], last.ln[11], out, false, M, D, ACT_NONE, st), "layernorm");
     return UD_OK;
 }
 

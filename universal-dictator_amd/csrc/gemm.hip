@@ -1,20 +1,21 @@
 // GEMMs of the encoder step, C = epilogue(A[M,K] . W[N,K]^T), W in the checkpoint's [out, in]
-// layout (Sources/DictatorEngine/Core/Kernels.swift:79-112; epilogue order of
+// orientation (Sources/DictatorEngine/Core/Kernels.swift:79-112; epilogue order of
 // Sources/DictatorEngine/Metal/12_gemm2.metal:111-122: act, then out_scale, then + residual).
 //
 // bf16 path: v_mfma_f32_16x16x32_bf16 (gfx950).  The streaming step multiplies M = streams x T
-// rows (128 at 64 streams x 2 frames) against 2-8 MB weight matrices, so it is bound by streaming
-// W from HBM.  Each wave owns a [16*MT x 16*NTL] output tile and a strided subset of the 64-wide
-// K chunks; A and W fragments are loaded straight from global memory into MFMA operand registers
-// (16 bytes per lane per operand half), double-buffered so the next chunk's loads are in flight
-// while the current chunk's MFMAs run.  The WK waves of a workgroup split K and are summed through
-// LDS.  Both operands use the same k permutation inside a 64-chunk (lane group g holds k in
-// [16g, 16g+16) as two 8-element halves), which leaves the dot products unchanged.
-//
-// Epilogues are fused: SiLU + bf16 store (FF linear1), plain store (QKV), in-place fp32 residual
-// accumulate (FF linear2 x0.5, linear_out, pointwise_conv2), and GLU with the frame mask
-// (pointwise_conv1, whose weight rows are interleaved in 16-row value/gate blocks on upload so
-// that a value column and its gate column sit in the same lane of two adjacent MFMA tiles).
+// rows (128 at 64 streams x 2 frames) against 2-8 MB weight matrices.  Measured on MI355X, the
+// limit at this shape is not HBM but the L2 -> CU traffic of the activation fragments, which every
+// column tile re-reads; so both operands are stored fragment-major (see frag_index): each operand
+// fragment is one contiguous 1 KB load, with no partially used cache lines.
+//  - each wave owns a [16*MT x 16] output tile (MT = 8: all 128 rows of a 64-stream chunk-2 step)
+//    and every WK-th 64-wide K chunk of its workgroup's K range; the WK waves are summed in LDS;
+//  - two register buffers, separated by scheduling barriers, keep the next chunk's loads in flight
+//    behind the current chunk's MFMAs;
+//  - ksplit > 1 splits K over workgroups (parallelism for the N = 1024 projections); each split
+//    writes its own fp32 partial slab and the following LayerNorm adds the slabs, in order, to the
+//    residual row it reads anyway -- deterministic, no atomics, no extra kernel.
+// Epilogues: act + bf16 store (row-major for the QKV buffer the attention reads, fragment-major for
+// a following GEMM), fp32 store, in-place fp32 residual accumulate, split-K partial slabs.
 #include "ud_common.hpp"
 #include "kernels.hpp"
 
@@ -30,154 +31,131 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
 }
 
 // Maps the linear workgroup id so that tiles t, t+1, ... of one XCD's share are contiguous
-// (workgroups are dealt round-robin to the 8 XCDs): the M tiles of one N tile then run on the
-// same XCD and reuse the W tile from its L2.
+// (workgroups are dealt round-robin to the 8 XCDs): the M tiles and K splits of one N tile then
+// run on the same XCD and share its L2.
 __device__ __forceinline__ int xcd_tile(int bid, int total) {
     if (total % 8 != 0) return bid;
     return (bid % 8) * (total / 8) + bid / 8;
 }
 
-template <int MT, int NTL>
+template <int MT>
 struct Frag {
     uint4 a[MT][2];
-    uint4 b[NTL][2];
+    uint4 b[2];
 };
 
-template <int MT, int NTL>
-__device__ __forceinline__ void load_frag(Frag<MT, NTL>& f, const bf16* const* ap, const bool* aok,
-                                          const bf16* const* wp, int k) {
+template <int MT>
+__device__ __forceinline__ void load_frag(Frag<MT>& f, const bf16* const* ap, const bf16* wp, int64_t off) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-        if (aok[mt]) {
-            f.a[mt][0] = ld16(ap[mt] + k);
-            f.a[mt][1] = ld16(ap[mt] + k + 8);
-        } else {
-            f.a[mt][0] = make_uint4(0, 0, 0, 0);
-            f.a[mt][1] = make_uint4(0, 0, 0, 0);
-        }
+        f.a[mt][0] = ld16(ap[mt] + off);
+        f.a[mt][1] = ld16(ap[mt] + off + 512);
     }
-#pragma unroll
-    for (int nt = 0; nt < NTL; nt++) {
-        f.b[nt][0] = ld16(wp[nt] + k);
-        f.b[nt][1] = ld16(wp[nt] + k + 8);
-    }
+    f.b[0] = ld16(wp + off);
+    f.b[1] = ld16(wp + off + 512);
 }
 
-template <int MT, int NTL>
-__device__ __forceinline__ void mma_frag(const Frag<MT, NTL>& f, f32x4_t (&acc)[MT][NTL]) {
+template <int MT>
+__device__ __forceinline__ void mma_frag(const Frag<MT>& f, f32x4_t (&acc)[MT]) {
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int nt = 0; nt < NTL; nt++)
-                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(f.a[mt][h]), as_bf16x8(f.b[nt][h]),
-                                                                     acc[mt][nt], 0, 0, 0);
+            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(f.a[mt][h]), as_bf16x8(f.b[h]), acc[mt], 0, 0, 0);
 }
 
-template <int MT, int NTL, int WK>
-__global__ __launch_bounds__(64 * WK) void gemm_bf16_kernel(GemmArgs a) {
-    constexpr int BM = 16 * MT, BN = 16 * NTL;
+// Grid: (N/16) x ceil(M/(16*MT)) x ksplit workgroups of WK waves.  The host guarantees
+// K % (64 * WK * ksplit) == 0.
+template <int MT, int WK>
+__global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
-    const int nN = a.N / BN, nM = (a.M + BM - 1) / BM;
-    const int t = xcd_tile(blockIdx.x, nN * nM);
-    const int n0 = (t / nM) * BN, m0 = (t % nM) * BM;
+    const int nN = a.N / 16, nM = (a.M + 16 * MT - 1) / (16 * MT);
+    const int ks = a.ksplit;
+    const int t = xcd_tile(blockIdx.x, nN * nM * ks);
+    const int kz = t % ks, tile = t / ks;
+    const int nt = tile / nM, mb = tile % nM;
+    const int nk = a.K / 64;
+    const int kper = nk / ks;
+    const int kc0 = kz * kper + wave;
+    const int rtiles = (a.M + 15) / 16;
 
     const bf16* A = static_cast<const bf16*>(a.A);
     const bf16* W = static_cast<const bf16*>(a.W);
     const bf16* ap[MT];
-    bool aok[MT];
-    const bf16* wp[NTL];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-        int m = m0 + mt * 16 + r16;
-        aok[mt] = m < a.M;
-        ap[mt] = A + (int64_t)(aok[mt] ? m : 0) * a.lda + g * 16;
+        const int rt = min(mb * MT + mt, rtiles - 1);      // clamped tiles are computed, not stored
+        ap[mt] = A + (((int64_t)rt * nk + kc0) << 10) + lane * 8;
     }
-#pragma unroll
-    for (int nt = 0; nt < NTL; nt++) wp[nt] = W + (int64_t)(n0 + nt * 16 + r16) * a.ldw + g * 16;
+    const bf16* wp = W + (((int64_t)nt * nk + kc0) << 10) + lane * 8;
 
-    f32x4_t acc[MT][NTL];
+    f32x4_t acc[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int nt = 0; nt < NTL; nt++) acc[mt][nt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int nchunks = a.K / 64;
-    Frag<MT, NTL> f0, f1;
-    int c = wave;
-    if (c < nchunks) load_frag(f0, ap, aok, wp, c * 64);
-    while (c < nchunks) {
-        int cn = c + WK;
-        if (cn < nchunks) load_frag(f1, ap, aok, wp, cn * 64);
+    const int cnt = kper / WK;            // chunks per wave (>= 1)
+    constexpr int STEP = WK * 1024;       // element stride between a wave's consecutive chunks
+    Frag<MT> f0, f1;
+    load_frag(f0, ap, wp, 0);
+    int i = 0;
+    for (; i + 2 < cnt; i += 2) {
+        load_frag(f1, ap, wp, (int64_t)(i + 1) * STEP);
+        __builtin_amdgcn_sched_barrier(0);
         mma_frag(f0, acc);
-        c = cn;
-        if (c >= nchunks) break;
-        cn = c + WK;
-        if (cn < nchunks) load_frag(f0, ap, aok, wp, cn * 64);
+        __builtin_amdgcn_sched_barrier(0);
+        load_frag(f0, ap, wp, (int64_t)(i + 2) * STEP);
+        __builtin_amdgcn_sched_barrier(0);
         mma_frag(f1, acc);
-        c = cn;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i + 1 < cnt) {
+        load_frag(f1, ap, wp, (int64_t)(i + 1) * STEP);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_frag(f0, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_frag(f1, acc);
+    } else {
+        mma_frag(f0, acc);
     }
 
     if constexpr (WK > 1) {
-        __shared__ f32x4_t red[WK - 1][MT][NTL][64];
+        __shared__ f32x4_t red[WK - 1][MT][64];
         if (wave > 0) {
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int nt = 0; nt < NTL; nt++) red[wave - 1][mt][nt][lane] = acc[mt][nt];
+            for (int mt = 0; mt < MT; mt++) red[wave - 1][mt][lane] = acc[mt];
         }
         __syncthreads();
         if (wave != 0) return;
 #pragma unroll
         for (int w = 0; w < WK - 1; w++)
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int nt = 0; nt < NTL; nt++) acc[mt][nt] += red[w][mt][nt][lane];
+            for (int mt = 0; mt < MT; mt++) acc[mt] += red[w][mt][lane];
     }
 
-    // Lane holds rows m0 + 16*mt + 4*g + i (i < 4) of column n0 + 16*nt + r16.
-    if (a.epi == EPI_GLU) {
-        float* C = static_cast<float*>(a.C);
+    // Lane holds rows 16*(mb*MT + mt) + 4*g + i (i < 4) of column 16*nt + r16.
+    const int n = nt * 16 + r16;
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
+    for (int mt = 0; mt < MT; mt++) {
 #pragma unroll
-            for (int p = 0; p < NTL / 2; p++) {
-                const int ch = n0 / 2 + 16 * p + r16;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int m = m0 + mt * 16 + g * 4 + i;
-                    if (m >= a.M) continue;
-                    const int s = m / a.T, tt = m - s * a.T;
-                    const int valid = a.desc[s * DESC_INTS + 2];
-                    float y = acc[mt][2 * p][i] * sigmoidf(acc[mt][2 * p + 1][i]);
-                    C[(int64_t)m * a.ldc + ch] = tt < valid ? y : 0.0f;
-                }
-            }
-        return;
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int nt = 0; nt < NTL; nt++) {
-            const int n = n0 + nt * 16 + r16;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = m0 + mt * 16 + g * 4 + i;
-                if (m >= a.M) continue;
-                const float v = acc[mt][nt][i];
-                if (a.epi == EPI_RESID) {
-                    float* C = static_cast<float*>(a.C) + (int64_t)m * a.ldc + n;
-                    *C = *C + a.out_scale * v;
-                } else if (a.epi == EPI_STORE_F32) {
-                    static_cast<float*>(a.C)[(int64_t)m * a.ldc + n] = apply_act(v, a.act) * a.out_scale;
-                } else {
-                    static_cast<bf16*>(a.C)[(int64_t)m * a.ldc + n] = f2bf(apply_act(v, a.act) * a.out_scale);
-                }
+        for (int i2 = 0; i2 < 4; i2++) {
+            const int64_t m = (int64_t)(mb * MT + mt) * 16 + g * 4 + i2;
+            if (m >= a.M) continue;
+            const float v = acc[mt][i2];
+            if (a.epi == EPI_PARTIAL) {
+                static_cast<float*>(a.C)[((int64_t)kz * a.M + m) * a.ldc + n] = a.out_scale * v;
+            } else if (a.epi == EPI_RESID) {
+                float* C = static_cast<float*>(a.C) + m * a.ldc + n;
+                *C = *C + a.out_scale * v;
+            } else if (a.epi == EPI_STORE_F32) {
+                static_cast<float*>(a.C)[m * a.ldc + n] = apply_act(v, a.act) * a.out_scale;
+            } else if (a.epi == EPI_STORE_FRAG) {
+                static_cast<bf16*>(a.C)[frag_index(m, n, a.N / 64)] = f2bf(apply_act(v, a.act) * a.out_scale);
+            } else {
+                static_cast<bf16*>(a.C)[m * a.ldc + n] = f2bf(apply_act(v, a.act) * a.out_scale);
             }
         }
+    }
 }
 
 // ---------------------------------------------------------------- fp32 (VALU) GEMM
@@ -228,30 +206,30 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
 
 // ---------------------------------------------------------------- launch
 
-template <int MT, int NTL, int WK>
-static int launch_bf16_cfg(const GemmArgs& a, hipStream_t st) {
-    constexpr int BM = 16 * MT, BN = 16 * NTL;
-    if (a.N % BN != 0) return -2;
-    const int tiles = (a.N / BN) * ((a.M + BM - 1) / BM);
-    hipLaunchKernelGGL((gemm_bf16_kernel<MT, NTL, WK>), dim3(tiles), dim3(64 * WK), 0, st, a);
+template <int MT, int WK>
+static int launch_bf16_cfg(GemmArgs a, int ksplit, hipStream_t st) {
+    if (a.N % 16 != 0 || ksplit < 1 || a.K % (64 * WK * ksplit) != 0) return -2;
+    if (ksplit > 1 && a.epi != EPI_PARTIAL) return -2;
+    if (a.epi == EPI_STORE_FRAG && a.N % 64 != 0) return -2;
+    a.ksplit = ksplit;
+    const int tiles = (a.N / 16) * ((a.M + 16 * MT - 1) / (16 * MT)) * ksplit;
+    hipLaunchKernelGGL((gemm_bf16_kernel<MT, WK>), dim3(tiles), dim3(64 * WK), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st) {
     if (a.M <= 0 || a.N <= 0 || a.K <= 0) return -2;
     if (!bf16_data) {
-        if (a.epi == EPI_GLU) return -2;
+        if (a.epi == EPI_STORE_FRAG) return -2;
         dim3 grid((a.N + F_BN - 1) / F_BN, (a.M + F_BM - 1) / F_BM);
         hipLaunchKernelGGL(gemm_f32_kernel, grid, dim3(256), 0, st, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    // bf16 MFMA: K in 64-chunks, 16-byte aligned rows.
-    if (a.K % 64 != 0 || a.lda % 8 != 0 || a.ldw % 8 != 0) return -2;
-    if (a.epi == EPI_GLU && a.N % 32 != 0) return -2;
-    // Skinny (streaming) shapes: full M in one tile when M <= 128; 32 output columns per
-    // workgroup, K split over 4 waves.
-    if (a.M <= 64) return launch_bf16_cfg<4, 2, 4>(a, st);
-    return launch_bf16_cfg<8, 2, 4>(a, st);
+    if (a.K % 128 != 0) return -2;
+    // One workgroup per 16-column tile (and K split for EPI_PARTIAL), two waves splitting K.
+    const int ks = a.epi == EPI_PARTIAL ? a.ksplit : 1;
+    if (a.M <= 64) return launch_bf16_cfg<4, 2>(a, ks, st);
+    return launch_bf16_cfg<8, 2>(a, ks, st);
 }
 
 }  // namespace ud

@@ -28,43 +28,65 @@ struct RingArgs {
     const void* qkv;                // [n*T, 3*D]
     const void* P;                  // [n_rel, D]
     const float* u; const float* vb;   // [H*128]
-    void* att;                      // [n*T, D]
+    void* att;                      // [n*T, D]: row-major, or fragment-major when att_frag (bf16)
     const int32_t* desc;            // [n][DESC_INTS]
     int n, T, L, H, rel_offset, n_rel;
     float scale;
+    int att_frag;
 };
 int launch_relpos_ring(const RingArgs& a, bool bf16_data, hipStream_t st);
 
+// ---------------------------------------------------------------- fragment-major layout
+// bf16 GEMM operands live in HBM in the order the v_mfma_f32_16x16x32_bf16 lanes consume them:
+// a [R, K] matrix (R padded to 16, K % 64 == 0) is a sequence of 2 KB blocks, block (rt, kc) =
+// rows [16rt, 16rt+16) x cols [64kc, 64kc+64) at element offset (rt * K/64 + kc) * 1024; inside a
+// block, element h*512 + lane*8 + e (lane = 16*g + r) holds X[16rt + r][64kc + 32h + 8g + e].
+// Every fragment load of a wave is then one contiguous, fully used 1 KB access.
+__host__ __device__ inline int64_t frag_index(int64_t m, int c, int nk) {
+    const int rt = (int)(m >> 4), r = (int)(m & 15), kc = c >> 6, w = c & 63;
+    const int h = w >> 5, g = (w >> 3) & 3, e = w & 7;
+    return (((int64_t)rt * nk + kc) << 10) + (h << 9) + ((g * 16 + r) << 3) + e;
+}
+
 // ---------------------------------------------------------------- GEMM  C = epi(A . W^T)
 enum Epi : int {
-    EPI_STORE = 0,     // C[m,n] = act(acc)                        (C in the activation dtype)
-    EPI_RESID = 1,     // C[m,n] += out_scale * acc                (C fp32 residual, in place)
-    EPI_GLU = 2,       // C[m,c] = value * sigmoid(gate), rows >= valid zeroed   (C fp32 [M, N/2])
-    EPI_STORE_F32 = 3  // C[m,n] = act(acc) as fp32
+    EPI_STORE = 0,      // C[m,n] = act(acc) * out_scale, activation dtype, row-major
+    EPI_RESID = 1,      // C[m,n] += out_scale * acc   (C fp32 residual, in place)
+    EPI_STORE_F32 = 3,  // C[m,n] = act(acc) * out_scale as fp32, row-major
+    EPI_STORE_FRAG = 4, // as EPI_STORE but bf16 in fragment-major layout (the next GEMM's A)
+    EPI_PARTIAL = 5     // C[kz][m][n] = out_scale * (K-split kz partial), fp32; slabs M*ldc apart
 };
+// bf16: A [M, K] and W [N, K] in fragment-major layout (lda/ldw unused); M may be any size, the
+// A buffer holding ceil(M/16)*16 rows.  fp32: row-major with leading dimensions lda/ldw/ldc.
 struct GemmArgs {
     const void* A; const void* W; void* C;
     int M, N, K, lda, ldw, ldc;
     int epi, act;
     float out_scale;
-    const int32_t* desc;            // EPI_GLU: per-stream valid frames (desc[s*4+2]), rows = s*T+t
-    int T;
+    int ksplit;                     // EPI_PARTIAL: K splits (1 or 4) chosen by the caller
 };
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st);
 
 // ---------------------------------------------------------------- LayerNorm / conv / misc
-// z = act(LN(x; g, b)) for rows of D (fp32 in), out in fp32 or bf16.
-int launch_layernorm(const float* x, const float* g, const float* b, void* out, bool out_bf16, int rows, int D,
-                     int act, hipStream_t st);
-// res <- LN_a(src) (or a plain copy of src when ga == nullptr); z <- LN_b(res) in fp32/bf16.
-int launch_layernorm2(const float* src, float* res, const float* ga, const float* ba, const float* gb,
+// Pending residual update: nparts fp32 slabs [rows, D] (stride rows*D) that a split-K residual
+// GEMM left; the LayerNorm kernels add them to the residual row in slab order before normalising.
+struct Partials {
+    const float* p;
+    int n;
+};
+// x <- x + sum(parts) (written back when parts.n > 0); out = act(LN(x; g, b)), fp32 row-major
+// or bf16 fragment-major.
+int launch_layernorm(float* x, Partials parts, const float* g, const float* b, void* out, bool out_bf16, int rows,
+                     int D, int act, hipStream_t st);
+// v = src + sum(parts); res <- LN_a(v) (v itself when ga == nullptr); z <- LN_b(res) (fp32
+// row-major or bf16 fragment-major).
+int launch_layernorm2(const float* src, Partials parts, float* res, const float* ga, const float* ba, const float* gb,
                       const float* bb, void* z, bool z_bf16, int rows, int D, hipStream_t st);
-// GLU of an unpermuted [M, 2D] fp32 buffer with rows >= valid zeroed (fp32 encoder mode).
-int launch_glu_mask(const float* pw, float* g, int M, int D, const int32_t* desc, int T, hipStream_t st);
-// Causal depthwise conv over [conv ring (K-1 rows) ; T new rows of g] + conv LayerNorm + SiLU;
-// writes z and the updated conv ring.
+// GLU of pointwise_conv1's fp32 [n*T, 2D] output (value | gate) with the frame mask, causal
+// depthwise conv over [conv ring (K-1 rows) ; T new GLU rows], conv LayerNorm + SiLU; writes z
+// and the updated conv ring (which holds GLU rows).
 struct ConvArgs {
-    const float* g;                 // [n*T, D] GLU output
+    const float* pw;                // [n*T, 2D] pointwise_conv1 output
     float* ring;                    // layer base of the conv pool: [slots][K-1][D]
     const float* w_t;               // [K][D] depthwise weights, tap-major
     const float* ln_g; const float* ln_b;

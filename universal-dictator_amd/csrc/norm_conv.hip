@@ -1,5 +1,6 @@
-// Row-wise kernels of the encoder step: LayerNorm (single and fused pair), the fp32-mode GLU, and
-// the causal depthwise conv fused with the conv module's LayerNorm + SiLU and the conv-cache ring.
+// Row-wise kernels of the encoder step: LayerNorm (single and fused pair) and the conv module's
+// GLU + frame mask + causal depthwise conv + LayerNorm + SiLU, fused with the conv-cache ring.
+// bf16 outputs feed a GEMM and are written fragment-major (frag_index), fp32 outputs row-major.
 //
 // LayerNorm semantics: Sources/DictatorEngine/Metal/20_conformer.metal:25-49 (two passes,
 // population variance, y = act((x-mean)*rsqrt(var+eps)*g + b)), eps 1e-5 (Core/Ops.swift:27).
@@ -42,31 +43,52 @@ __device__ __forceinline__ void ln_apply(float4 (&x)[NPER], const float* g, cons
     }
 }
 
+// Four consecutive columns c..c+3 (c % 4 == 0) of row `row`: bf16 fragment-major, 8 bytes.
+__device__ __forceinline__ void store4_frag(void* out, int64_t row, int c, int D, float4 v) {
+    uint2 u;
+    u.x = (uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16);
+    u.y = (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16);
+    *reinterpret_cast<uint2*>(static_cast<bf16*>(out) + frag_index(row, c, D / 64)) = u;
+}
+
 template <int NPER>
 __device__ __forceinline__ void store_row(void* out, bool bf, int64_t row, int D, const float4 (&x)[NPER], int lane) {
 #pragma unroll
     for (int p = 0; p < NPER; p++) {
         const int c = (p * 64 + lane) * 4;
         if (bf) {
-            uint2 u;
-            u.x = (uint32_t)f2bf(x[p].x) | ((uint32_t)f2bf(x[p].y) << 16);
-            u.y = (uint32_t)f2bf(x[p].z) | ((uint32_t)f2bf(x[p].w) << 16);
-            *reinterpret_cast<uint2*>(static_cast<bf16*>(out) + row * D + c) = u;
+            store4_frag(out, row, c, D, x[p]);
         } else {
             *reinterpret_cast<float4*>(static_cast<float*>(out) + row * D + c) = x[p];
         }
     }
 }
 
+// v = row of x plus the pending split-K residual slabs, added in slab order.
 template <int NPER>
-__global__ __launch_bounds__(256) void layernorm_kernel(const float* x, const float* g, const float* b, void* out,
-                                                        int out_bf16, int rows, int D, int act) {
+__device__ __forceinline__ void load_row(float4 (&v)[NPER], const float* x, Partials parts, int64_t row, int rows,
+                                         int D, int lane) {
+#pragma unroll
+    for (int p = 0; p < NPER; p++) v[p] = *reinterpret_cast<const float4*>(x + row * D + (p * 64 + lane) * 4);
+    for (int j = 0; j < parts.n; j++) {
+        const float* pj = parts.p + ((int64_t)j * rows + row) * D;
+#pragma unroll
+        for (int p = 0; p < NPER; p++) {
+            const float4 q = *reinterpret_cast<const float4*>(pj + (p * 64 + lane) * 4);
+            v[p].x += q.x; v[p].y += q.y; v[p].z += q.z; v[p].w += q.w;
+        }
+    }
+}
+
+template <int NPER>
+__global__ __launch_bounds__(256) void layernorm_kernel(float* x, Partials parts, const float* g, const float* b,
+                                                        void* out, int out_bf16, int rows, int D, int act) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     float4 v[NPER];
-#pragma unroll
-    for (int p = 0; p < NPER; p++) v[p] = *reinterpret_cast<const float4*>(x + row * D + (p * 64 + lane) * 4);
+    load_row(v, x, parts, row, rows, D, lane);
+    if (parts.n > 0) store_row(x, false, row, D, v, lane);
     float mean, rstd;
     ln_row_stats(v, D, mean, rstd);
     ln_apply(v, g, b, mean, rstd, lane, act);
@@ -76,15 +98,14 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float* x, const fl
 // res <- LN_a(src) (copy when ga is null), z <- LN_b(res).  Joins one layer's norm_out with the
 // next layer's norm_feed_forward1 (FastConformer.swift:320 then :277).
 template <int NPER>
-__global__ __launch_bounds__(256) void layernorm2_kernel(const float* src, float* res, const float* ga, const float* ba,
-                                                         const float* gb, const float* bb, void* z, int z_bf16,
-                                                         int rows, int D) {
+__global__ __launch_bounds__(256) void layernorm2_kernel(const float* src, Partials parts, float* res, const float* ga,
+                                                         const float* ba, const float* gb, const float* bb, void* z,
+                                                         int z_bf16, int rows, int D) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     float4 v[NPER];
-#pragma unroll
-    for (int p = 0; p < NPER; p++) v[p] = *reinterpret_cast<const float4*>(src + row * D + (p * 64 + lane) * 4);
+    load_row(v, src, parts, row, rows, D, lane);
     float mean, rstd;
     if (ga != nullptr) {
         ln_row_stats(v, D, mean, rstd);
@@ -96,22 +117,13 @@ __global__ __launch_bounds__(256) void layernorm2_kernel(const float* src, float
     store_row(z, z_bf16 != 0, row, D, v, lane);
 }
 
-// GLU over channels with the frame mask, fp32 mode (Metal/20_conformer.metal:76-85 and
-// FastConformer.swift:299-302): g[m, d] = pw[m, d] * sigmoid(pw[m, D + d]); rows t >= valid -> 0.
-__global__ void glu_mask_kernel(const float* pw, float* g, int M, int D, const int32_t* desc, int T) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)M * D) return;
-    const int m = (int)(idx / D), d = (int)(idx % D);
-    const int s = m / T, t = m - s * T;
-    const float y = pw[(int64_t)m * 2 * D + d] * sigmoidf(pw[(int64_t)m * 2 * D + D + d]);
-    g[idx] = t < desc[s * DESC_INTS + 2] ? y : 0.0f;
-}
-
-// Causal depthwise conv k=KC+1 over [conv cache (KC rows, oldest first) ; T new rows]
-// (Metal/20_conformer.metal:87-102, tap KC = the current frame), then the conv module's LayerNorm
-// + SiLU (FastConformer.swift:303-306).  One workgroup per stream, 4 channels per thread, the
-// whole [KC + T] x 4 window in registers.  The cache is a ring of KC rows per stream: logical row r
-// is slot (frames + r) % KC; new row t (only the last KC matter) goes to slot (frames + t) % KC,
+// The conv module after pointwise_conv1 (FastConformer.swift:298-306): GLU over channels,
+// out[t,d] = pw[t,d] * sigmoid(pw[t,D+d]) (Metal/20_conformer.metal:76-85), rows t >= valid zeroed
+// (maskRows, FastConformer.swift:302); causal depthwise conv k=KC+1 over [conv cache (KC rows,
+// oldest first) ; T GLU rows] (Metal/20_conformer.metal:87-102, tap KC = the current frame); then
+// the conv LayerNorm + SiLU.  One workgroup per stream, 4 channels per thread, the whole
+// [KC + T] x 4 window in registers.  The cache is a ring of KC rows per stream: logical row r is
+// slot (frames + r) % KC; new row t (only the last KC matter) goes to slot (frames + t) % KC,
 // written by the thread that read the slot, so the update is in place with no hazard.
 template <int KC, int TMAX>
 __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
@@ -121,7 +133,7 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
     const int D = a.D, T = a.T;
     const int c0 = tid * 4;
     const int32_t* d = a.desc + s * DESC_INTS;
-    const int slot = d[0], frames = d[1];
+    const int slot = d[0], frames = d[1], valid = d[2];
     const int cpos = frames % KC;
     float* ring = a.ring + (int64_t)slot * KC * D;
 
@@ -133,9 +145,16 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
         in[r] = *reinterpret_cast<const float4*>(ring + (int64_t)sr * D + c0);
     }
 #pragma unroll
-    for (int t = 0; t < TMAX; t++)
-        in[KC + t] = t < T ? *reinterpret_cast<const float4*>(a.g + ((int64_t)s * T + t) * D + c0)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t = 0; t < TMAX; t++) {
+        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t < T && t < valid) {
+            const float* row = a.pw + ((int64_t)s * T + t) * 2 * D;
+            const float4 v = *reinterpret_cast<const float4*>(row + c0);
+            const float4 gt = *reinterpret_cast<const float4*>(row + D + c0);
+            y = make_float4(v.x * sigmoidf(gt.x), v.y * sigmoidf(gt.y), v.z * sigmoidf(gt.z), v.w * sigmoidf(gt.w));
+        }
+        in[KC + t] = y;
+    }
     float4 w[KC + 1];
 #pragma unroll
     for (int k = 0; k <= KC; k++) w[k] = *reinterpret_cast<const float4*>(a.w_t + (int64_t)k * D + c0);
@@ -207,10 +226,7 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
         y.w = silu((o[t].w - mean[t]) * rstd * gg.w + bb.w);
         const int64_t row = (int64_t)s * T + t;
         if (a.z_bf16) {
-            uint2 u;
-            u.x = (uint32_t)f2bf(y.x) | ((uint32_t)f2bf(y.y) << 16);
-            u.y = (uint32_t)f2bf(y.z) | ((uint32_t)f2bf(y.w) << 16);
-            *reinterpret_cast<uint2*>(static_cast<bf16*>(a.z) + row * D + c0) = u;
+            store4_frag(a.z, row, c0, D, y);
         } else {
             *reinterpret_cast<float4*>(static_cast<float*>(a.z) + row * D + c0) = y;
         }
@@ -219,38 +235,33 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
 
 // ---------------------------------------------------------------- launchers
 
-int launch_layernorm(const float* x, const float* g, const float* b, void* out, bool out_bf16, int rows, int D,
-                     int act, hipStream_t st) {
+int launch_layernorm(float* x, Partials parts, const float* g, const float* b, void* out, bool out_bf16, int rows,
+                     int D, int act, hipStream_t st) {
     if (rows <= 0) return 0;
     dim3 grid((rows + 3) / 4), block(256);
+    const int ob = out_bf16 ? 1 : 0;
     switch (D) {
-        case 256: hipLaunchKernelGGL(layernorm_kernel<1>, grid, block, 0, st, x, g, b, out, (int)out_bf16, rows, D, act); break;
-        case 512: hipLaunchKernelGGL(layernorm_kernel<2>, grid, block, 0, st, x, g, b, out, (int)out_bf16, rows, D, act); break;
-        case 1024: hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, st, x, g, b, out, (int)out_bf16, rows, D, act); break;
-        case 2048: hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, st, x, g, b, out, (int)out_bf16, rows, D, act); break;
+        case 256: hipLaunchKernelGGL(layernorm_kernel<1>, grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act); break;
+        case 512: hipLaunchKernelGGL(layernorm_kernel<2>, grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act); break;
+        case 1024: hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act); break;
+        case 2048: hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act); break;
         default: return -2;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_layernorm2(const float* src, float* res, const float* ga, const float* ba, const float* gb,
+int launch_layernorm2(const float* src, Partials parts, float* res, const float* ga, const float* ba, const float* gb,
                       const float* bb, void* z, bool z_bf16, int rows, int D, hipStream_t st) {
     if (rows <= 0) return 0;
     dim3 grid((rows + 3) / 4), block(256);
+    const int zb = z_bf16 ? 1 : 0;
     switch (D) {
-        case 256: hipLaunchKernelGGL(layernorm2_kernel<1>, grid, block, 0, st, src, res, ga, ba, gb, bb, z, (int)z_bf16, rows, D); break;
-        case 512: hipLaunchKernelGGL(layernorm2_kernel<2>, grid, block, 0, st, src, res, ga, ba, gb, bb, z, (int)z_bf16, rows, D); break;
-        case 1024: hipLaunchKernelGGL(layernorm2_kernel<4>, grid, block, 0, st, src, res, ga, ba, gb, bb, z, (int)z_bf16, rows, D); break;
-        case 2048: hipLaunchKernelGGL(layernorm2_kernel<8>, grid, block, 0, st, src, res, ga, ba, gb, bb, z, (int)z_bf16, rows, D); break;
+        case 256: hipLaunchKernelGGL(layernorm2_kernel<1>, grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
+        case 512: hipLaunchKernelGGL(layernorm2_kernel<2>, grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
+        case 1024: hipLaunchKernelGGL(layernorm2_kernel<4>, grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
+        case 2048: hipLaunchKernelGGL(layernorm2_kernel<8>, grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
         default: return -2;
     }
-    return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
-int launch_glu_mask(const float* pw, float* g, int M, int D, const int32_t* desc, int T, hipStream_t st) {
-    const int64_t n = (int64_t)M * D;
-    if (n <= 0) return 0;
-    hipLaunchKernelGGL(glu_mask_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, pw, g, M, D, desc, T);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
