@@ -94,6 +94,9 @@ def main():
     ap.add_argument("--attn-iters", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="also run one device-to-device copy of this many MiB (a known-size kernel for "
+                         "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -102,6 +105,13 @@ def main():
         sys.exit(2)
 
     ud = load_pkg()
+    if args.calibrate_copy_mib > 0:
+        nbytes = args.calibrate_copy_mib << 20
+        src, dst = ud.DeviceBuffer.zeros(nbytes), ud.DeviceBuffer(nbytes)
+        ud.lib().ud_memcpy_dtod(dst.ptr, src.ptr, nbytes)
+        ud.synchronize()
+        log("calibration copy: %d MiB device-to-device" % args.calibrate_copy_mib)
+        src.free(); dst.free()
     wl = WORKLOADS[args.workload]
     S, T = wl["streams"], wl["T"]
     cfg = ud.EncoderConfig(layers=24, max_chunk=T, max_streams=S, dtype="bf16")

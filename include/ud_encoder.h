@@ -160,10 +160,11 @@ UD_API int ud_stream_advance(ud_stream* const* streams, int32_t n, int32_t T);
 
 /* Profiling hook (no reference counterpart; the reference times whole command buffers,
  * Sources/DictatorEngine/Core/Kernels.swift:33-42): uploads the batch descriptor once, then
- * launches the fused attention kernel of `layer` `iters` times back to back between two HIP events
- * on hip_stream and returns the average kernel duration in milliseconds.  Every launch reads the
- * same caches and writes the same T new rows to the same ring slots, so repeating it leaves the
- * state as one ud_layer_attention call would.  Synchronizes hip_stream. */
+ * launches the fused attention kernel `iters` times back to back between two HIP events on
+ * hip_stream -- launch i on layer (layer + 1 + i) % layers, so that, as in a real step, the ring
+ * caches stream from HBM -- and returns the average kernel duration in milliseconds.  Each launch
+ * writes the T new rows of qkv_dev into that layer's rings at the stream's current write position
+ * (overwriting the T oldest cached rows).  Synchronizes hip_stream. */
 UD_API int ud_time_layer_attention(ud_encoder* enc, ud_stream* const* streams, int32_t n, int32_t T,
                                    int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
                                    void* hip_stream, float* avg_ms);

@@ -290,6 +290,258 @@ __global__ __launch_bounds__(256) void relpos_ring_kernel(RingArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ streaming ring kernel (T <= 4)
+// The chunk shapes of streaming (2..4 queries over L + T <= 96 keys) get a kernel built for one
+// memory round trip: every load of the workgroup (q, the P band, K rows, V rows, the T new rows to
+// commit) is issued up front in that order, so each phase waits only for its own operands -- bd is
+// computed from the L2-resident P band while K and V are still arriving from HBM.  q+u and q+v live
+// in registers; the TQ partial dot products of a 16-lane row group are reduced together with a
+// transposed DPP butterfly (TQ values in TQ + log2(16/TQ) - 1 DPP steps instead of 4 per value);
+// P.V runs from the V registers, reduced across row groups with shuffles and once through LDS.
+
+// DPP row rotation (within 16 lanes) by R.
+template <int R> __device__ __forceinline__ float dpp_ror(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + R, 0xF, 0xF, false));
+}
+
+// Transposed reduction over a 16-lane row for Q in {1, 2, 4} values per lane.  Returns, in every
+// lane, the row total of value index qidx(lane) where qidx = bit-reverse of the low log2(Q) lane
+// bits.
+template <int Q>
+__device__ __forceinline__ float tsum16(float (&v)[Q], int lane) {
+    if constexpr (Q == 4) {
+        const bool b0 = lane & 1;
+        float k0 = b0 ? v[2] : v[0], s0 = b0 ? v[0] : v[2];
+        float k1 = b0 ? v[3] : v[1], s1 = b0 ? v[1] : v[3];
+        k0 += dpp_mov<DPP_QUAD_1032>(s0);
+        k1 += dpp_mov<DPP_QUAD_1032>(s1);
+        const bool b1 = lane & 2;
+        float k = b1 ? k1 : k0, sd = b1 ? k0 : k1;
+        k += dpp_mov<DPP_QUAD_2301>(sd);
+        k += dpp_ror<4>(k);
+        k += dpp_ror<8>(k);
+        return k;
+    } else if constexpr (Q == 2) {
+        const bool b0 = lane & 1;
+        float k = b0 ? v[1] : v[0], sd = b0 ? v[0] : v[1];
+        k += dpp_mov<DPP_QUAD_1032>(sd);
+        k += dpp_ror<2>(k);
+        k += dpp_ror<4>(k);
+        k += dpp_ror<8>(k);
+        return k;
+    } else {
+        return group_sum<16>(v[0]);
+    }
+}
+template <int Q> __device__ __forceinline__ int tsum16_index(int lane) {
+    if constexpr (Q == 4) return ((lane & 1) << 1) | ((lane >> 1) & 1);
+    else if constexpr (Q == 2) return lane & 1;
+    else return 0;
+}
+
+// One workgroup (4 waves) per (stream, head); bf16 K/V/P/q (LPR = 16 lanes per 128-wide row,
+// 16 row groups).  TQ in {2, 4}: the queries of the chunk; KR passes of 16 rows cover L + T keys.
+template <int TQ, int KR>
+__global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
+    using T = bf16;
+    constexpr int DK = 128, VEC = 8, LPR = 16, G = 16, NT = 256;
+    constexpr int KMAX = KR * G, PRR = (KMAX + TQ - 1 + G - 1) / G;
+    __shared__ float sc[TQ][KMAX];
+    __shared__ float bd[TQ][KMAX + TQ];
+    __shared__ float red[4][TQ][DK];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = tid / LPR, sub = tid % LPR;
+    const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
+    const int32_t* d = a.desc + s * DESC_INTS;
+    const int slot = d[0], frames = d[1], valid = min(max(d[2], 0), a.T), cache_len = d[3];
+    const int L = a.L, Tq = a.T, D = a.H * DK;
+    const int wpos = frames % L;
+    const int ks = L - cache_len, ke = L + valid;     // keys [ks, ke) of [L cached ; T new]
+    const int nk = ke - ks, nb = nk + Tq - 1;
+    const int rbase = (L - (ke - 1)) + a.rel_offset;  // table row of band index 0 (shift0 = L)
+    const T* kr = static_cast<const T*>(a.kring) + ((int64_t)slot * a.H + h) * L * DK;
+    const T* vr = static_cast<const T*>(a.vring) + ((int64_t)slot * a.H + h) * L * DK;
+    const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)s * a.T * 3 * D + h * DK;
+    const T* P = static_cast<const T*>(a.P) + h * DK;
+    auto key_ptr = [&](const T* ring, int j, int part) -> const T* {   // part 1: K, 2: V
+        if (j < L) { int r = wpos + j; r -= (r >= L) ? L : 0; return ring + (int64_t)r * DK; }
+        return qkv + (int64_t)(j - L) * 3 * D + part * D;
+    };
+
+    // ---- issue every load: q, u/v, P band, K, V, commit rows
+    uint4 qreg[TQ];
+#pragma unroll
+    for (int i = 0; i < TQ; i++) qreg[i] = i < Tq ? ld16(qkv + (int64_t)i * 3 * D + sub * VEC) : make_uint4(0, 0, 0, 0);
+    const float4 u0 = *reinterpret_cast<const float4*>(a.u + h * DK + sub * VEC);
+    const float4 u1 = *reinterpret_cast<const float4*>(a.u + h * DK + sub * VEC + 4);
+    const float4 v0 = *reinterpret_cast<const float4*>(a.vb + h * DK + sub * VEC);
+    const float4 v1 = *reinterpret_cast<const float4*>(a.vb + h * DK + sub * VEC + 4);
+    uint4 preg[PRR], kreg[KR], vreg[KR];
+#pragma unroll
+    for (int k = 0; k < PRR; k++) {
+        const int b = grp + k * G, r = rbase + b;
+        preg[k] = make_uint4(0, 0, 0, 0);
+        if (k * G < nb && b < nb && r >= 0 && r < a.n_rel) preg[k] = ld16(P + (int64_t)r * D + sub * VEC);
+    }
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int row = grp + k * G;
+        kreg[k] = make_uint4(0, 0, 0, 0);
+        if (k * G < nk && row < nk) kreg[k] = ld16(key_ptr(kr, ks + row, 1) + sub * VEC);
+    }
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int row = grp + k * G;
+        vreg[k] = make_uint4(0, 0, 0, 0);
+        if (k * G < nk && row < nk) vreg[k] = ld16(key_ptr(vr, ks + row, 2) + sub * VEC);
+    }
+    const bool has_commit = tid < Tq * LPR;
+    uint4 ck = make_uint4(0, 0, 0, 0), cv = make_uint4(0, 0, 0, 0);
+    if (has_commit) {
+        const T* q = qkv + (int64_t)(tid / LPR) * 3 * D + sub * VEC;
+        ck = ld16(q + D);
+        cv = ld16(q + 2 * D);
+    }
+
+    // ---- q + u, q + v in registers
+    const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float qu[TQ][VEC], qv[TQ][VEC];
+#pragma unroll
+    for (int i = 0; i < TQ; i++) {
+        float f[VEC];
+        unpack16<T>(qreg[i], f);
+#pragma unroll
+        for (int e = 0; e < VEC; e++) { qu[i][e] = f[e] + uu[e]; qv[i][e] = f[e] + vv[e]; }
+    }
+    const int qi = tsum16_index<TQ>(sub);
+
+    // ---- bd = (q + v) . P band   (P arrives first: it is read from L2)
+#pragma unroll
+    for (int k = 0; k < PRR; k++) {
+        if (k * G < nb) {
+            float f[VEC];
+            unpack16<T>(preg[k], f);
+            float part[TQ];
+#pragma unroll
+            for (int i = 0; i < TQ; i++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < VEC; e++) acc += qv[i][e] * f[e];
+                part[i] = acc;
+            }
+            const float tot = tsum16<TQ>(part, sub);
+            const int b = grp + k * G;
+            if (sub < TQ && qi < Tq && b < nb) bd[qi][b] = tot;
+        }
+    }
+    // ---- ac = (q + u) . K
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        if (k * G < nk) {
+            float f[VEC];
+            unpack16<T>(kreg[k], f);
+            float part[TQ];
+#pragma unroll
+            for (int i = 0; i < TQ; i++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < VEC; e++) acc += qu[i][e] * f[e];
+                part[i] = acc;
+            }
+            const float tot = tsum16<TQ>(part, sub);
+            const int row = grp + k * G;
+            if (sub < TQ && qi < Tq && row < nk) sc[qi][row] = tot;
+        }
+    }
+    __syncthreads();
+
+    // ---- softmax over the nk keys, one wave per query; probabilities overwrite sc
+    for (int i = wave; i < Tq; i += NT / 64) {
+        constexpr int PER = (KMAX + 63) / 64;
+        float sv[PER];
+        float m = -INFINITY;
+#pragma unroll
+        for (int p = 0; p < PER; p++) {
+            const int jj = lane + p * 64;
+            sv[p] = jj < nk ? (sc[i][jj] + bd[i][i - jj + nk - 1]) * a.scale : -INFINITY;
+            m = fmaxf(m, sv[p]);
+        }
+        m = wave_max(m);
+        float l = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PER; p++) {
+            sv[p] = sv[p] == -INFINITY ? 0.0f : __expf(sv[p] - m);
+            l += sv[p];
+        }
+        l = wave_sum(l);
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int p = 0; p < PER; p++) {
+            const int jj = lane + p * 64;
+            if (jj < nk) sc[i][jj] = sv[p] * inv;
+        }
+    }
+    __syncthreads();
+
+    // ---- out = P . V from the V registers
+    float acc[TQ][VEC];
+#pragma unroll
+    for (int i = 0; i < TQ; i++)
+#pragma unroll
+        for (int e = 0; e < VEC; e++) acc[i][e] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int row = grp + k * G;
+        if (k * G < nk && row < nk) {
+            float f[VEC];
+            unpack16<T>(vreg[k], f);
+#pragma unroll
+            for (int i = 0; i < TQ; i++) {
+                const float p = i < Tq ? sc[i][row] : 0.0f;
+#pragma unroll
+                for (int e = 0; e < VEC; e++) acc[i][e] += p * f[e];
+            }
+        }
+    }
+    // sum the 4 row groups of the wave (lanes sub, sub+16, sub+32, sub+48), then the 4 waves
+#pragma unroll
+    for (int i = 0; i < TQ; i++)
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+            float x = acc[i][e];
+            x += __shfl_xor(x, 16, 64);
+            x += __shfl_xor(x, 32, 64);
+            acc[i][e] = x;
+        }
+    if (lane < LPR) {
+#pragma unroll
+        for (int i = 0; i < TQ; i++)
+#pragma unroll
+            for (int e = 0; e < VEC; e++) red[wave][i][sub * VEC + e] = acc[i][e];
+    }
+    __syncthreads();
+
+    // ---- commit the new rows over the T oldest ring slots (every ring read finished above)
+    if (has_commit) {
+        int slot_row = wpos + tid / LPR;
+        slot_row -= (slot_row >= L) ? L : 0;
+        T* kw = static_cast<T*>(a.kring) + ((int64_t)slot * a.H + h) * L * DK;
+        T* vw = static_cast<T*>(a.vring) + ((int64_t)slot * a.H + h) * L * DK;
+        st16(kw + (int64_t)slot_row * DK + sub * VEC, ck);
+        st16(vw + (int64_t)slot_row * DK + sub * VEC, cv);
+    }
+    // ---- output (0 for an empty key range)
+    for (int idx = tid; idx < Tq * DK; idx += NT) {
+        const int i = idx / DK, dd = idx % DK;
+        const float o = nk > 0 ? red[0][i][dd] + red[1][i][dd] + red[2][i][dd] + red[3][i][dd] : 0.0f;
+        const int64_t row = (int64_t)s * a.T + i;
+        if (a.att_frag) static_cast<T*>(a.att)[frag_index(row, h * DK + dd, D / 64)] = f2bf(o);
+        else static_cast<T*>(a.att)[row * D + h * DK + dd] = f2bf(o);
+    }
+}
+
 // ------------------------------------------------------------------ launchers
 
 // Keys per block: as many as keep the workgroup's LDS under 64 KB.
@@ -329,6 +581,12 @@ int launch_relpos_op(const OpArgs& a, bool bf16_data, hipStream_t st) {
 template <typename T>
 static int launch_ring_t(const RingArgs& a, hipStream_t st) {
     dim3 grid(a.n * a.H), block(256);
+    // bf16 streaming chunks (T <= 4, L + T <= 96 keys, head_dim 128): the one-round-trip kernel.
+    if (sizeof(T) == 2 && a.T <= 4 && a.L + a.T <= 96 && a.n_rel >= 1) {
+        if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_small_kernel<2, 6>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((relpos_ring_small_kernel<4, 6>), grid, block, 0, st, a);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_kernel<T, 2, KeyBlock<T, 2>::KB>), grid, block, 0, st, a);
     else if (a.T <= 4) hipLaunchKernelGGL((relpos_ring_kernel<T, 4, KeyBlock<T, 4>::KB>), grid, block, 0, st, a);
     else if (a.T <= 8) hipLaunchKernelGGL((relpos_ring_kernel<T, 8, KeyBlock<T, 8>::KB>), grid, block, 0, st, a);

@@ -669,13 +669,16 @@ extern "C" UD_API int ud_time_layer_attention(ud_encoder* e, ud_stream* const* s
     if (iters < 1 || !avg_ms) return fail(UD_ERR_INVALID, "ud_time_layer_attention: bad iters / output");
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     if ((rc = upload_desc(e, streams, n, T, nullptr, st)) != UD_OK) return rc;
-    const RingArgs ra = ring_args(e, n, T, layer, qkv_dev, att_dev);
     hipEvent_t ev[2];
     HIPC(hipEventCreate(&ev[0]));
     HIPC(hipEventCreate(&ev[1]));
-    rc = launch_status(launch_relpos_ring(ra, e->bf, st), "relpos attention");   // warm-up
+    // Launch i uses layer (layer + i) % layers, so the caches come from HBM as in a real step
+    // (one layer's rings would otherwise stay in the 256 MB last-level cache across launches).
+    rc = launch_status(launch_relpos_ring(ring_args(e, n, T, layer, qkv_dev, att_dev), e->bf, st), "relpos attention");
     if (rc == UD_OK && hipEventRecord(ev[0], st) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventRecord failed");
-    for (int i = 0; rc == UD_OK && i < iters; i++) rc = launch_status(launch_relpos_ring(ra, e->bf, st), "relpos attention");
+    for (int i = 0; rc == UD_OK && i < iters; i++)
+        rc = launch_status(launch_relpos_ring(ring_args(e, n, T, (layer + 1 + i) % e->layers, qkv_dev, att_dev), e->bf, st),
+                           "relpos attention");
     if (rc == UD_OK && hipEventRecord(ev[1], st) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventRecord failed");
     float ms = 0.0f;
     if (rc == UD_OK && hipEventSynchronize(ev[1]) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventSynchronize failed");
