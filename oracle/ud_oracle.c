@@ -13,7 +13,7 @@
  * statistics and attention in double); GEMMs accumulate in fp32 with a SIMD
  * reduction, which is what the reference's fp32 kernels do.
  *
- * Pinning (what checks each function; see tests/test_oracle_*.py):
+ * Pinning (what checks each function; see tests/test_oracle.py):
  *   orc_lcg_floats        reference KAT generator, closed form + fixture
  *   orc_bf16_*            exhaustive/edge cases against the bit rule
  *   orc_layer_norm        numpy float64 LayerNorm + SiLU (library routine)
