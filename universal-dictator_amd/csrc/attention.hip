@@ -254,9 +254,8 @@ template <typename T, int TQ, int KB>
 __global__ __launch_bounds__(256) void relpos_ring_kernel(RingArgs a) {
     constexpr int DK = 128;
     const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
-    const int32_t* d = a.desc + s * 4;
-    const int slot = d[0], frames = d[1], valid = d[2], cache_len = d[3];
-    const int wpos = frames % a.L;
+    const int32_t* d = a.desc + s * DESC_INTS;
+    const int slot = d[0], wpos = d[1], valid = d[2], cache_len = d[3];
     const int D = a.H * DK;
     const T* kr = static_cast<const T*>(a.kring) + ((int64_t)slot * a.H + h) * a.L * DK;
     const T* vr = static_cast<const T*>(a.vring) + ((int64_t)slot * a.H + h) * a.L * DK;
@@ -291,13 +290,20 @@ __global__ __launch_bounds__(256) void relpos_ring_kernel(RingArgs a) {
 }
 
 // ------------------------------------------------------------------ streaming ring kernel (T <= 4)
-// The chunk shapes of streaming (2..4 queries over L + T <= 96 keys) get a kernel built for one
-// memory round trip: every load of the workgroup (q, the P band, K rows, V rows, the T new rows to
-// commit) is issued up front in that order, so each phase waits only for its own operands -- bd is
-// computed from the L2-resident P band while K and V are still arriving from HBM.  q+u and q+v live
-// in registers; the TQ partial dot products of a 16-lane row group are reduced together with a
-// transposed DPP butterfly (TQ values in TQ + log2(16/TQ) - 1 DPP steps instead of 4 per value);
-// P.V runs from the V registers, reduced across row groups with shuffles and once through LDS.
+// The chunk shapes of streaming (2..4 queries over L + T <= 96 keys, bf16, head_dim 128) get a
+// kernel built for one memory round trip.  It works on the whole window [L cached ; T new] and on
+// the whole positional band of the chunk (rel = 1-T .. L+T-1, the same rows for every stream), so
+// the addresses of q, u/v and the band depend only on the launch, and those of K/V only on the
+// stream's ring slot and position (read first, from a 32-byte descriptor).  Every load is
+// unconditional -- lanes past the window read a clamped row and are masked later -- so all of a
+// workgroup's loads issue back to back with no wait in between, and bd is computed from the
+// L2-resident band while K and V still arrive.  The key range [L - cache_len, L + valid) is a mask
+// in the softmax; V rows outside it are zeroed in registers, so probability-0 keys contribute exact
+// zeros whatever the pool holds there.
+// Reductions: the TQ partial dot products of a 16-lane row group are reduced together with a
+// transposed DPP butterfly; P.V is reduced over the 4 row groups of a wave with
+// v_permlane32_swap / v_permlane16_swap (each lane keeps a quarter of the sums) and over the 4
+// waves once through LDS.  The T new K/V rows are committed from the registers that loaded them.
 
 // DPP row rotation (within 16 lanes) by R.
 template <int R> __device__ __forceinline__ float dpp_ror(float v) {
@@ -339,72 +345,78 @@ template <int Q> __device__ __forceinline__ int tsum16_index(int lane) {
     else return 0;
 }
 
-// One workgroup (4 waves) per (stream, head); bf16 K/V/P/q (LPR = 16 lanes per 128-wide row,
-// 16 row groups).  TQ in {2, 4}: the queries of the chunk; KR passes of 16 rows cover L + T keys.
-template <int TQ, int KR>
+// a + (a from lane l^32) into lanes 0-31 and b + (b from lane l^32) into lanes 32-63.
+__device__ __forceinline__ float xsum32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// a + (a from lane l^16) into rows 0 and 2 (lanes 0-15, 32-47), b + ... into rows 1 and 3.
+__device__ __forceinline__ float xsum16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// One workgroup (4 waves) per (stream, head).  16 lanes own one 128-wide bf16 row (8 values per
+// lane), 16 row groups per pass: KR passes cover the window's L + T keys, PR passes the band's
+// L + 2T - 1 rows.  TQ in {2, 4} queries (T < TQ runs with clamped duplicate queries).
+template <int TQ, int KR, int PR>
 __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
     using T = bf16;
-    constexpr int DK = 128, VEC = 8, LPR = 16, G = 16, NT = 256;
-    constexpr int KMAX = KR * G, PRR = (KMAX + TQ - 1 + G - 1) / G;
+    constexpr int DK = 128, VEC = 8, LPR = 16, G = 16;
+    constexpr int KMAX = KR * G, BMAX = PR * G, NV = TQ * VEC, NQ = NV / 4;
+    static_assert(NQ % 4 == 0, "float4 partial sums");
     __shared__ float sc[TQ][KMAX];
-    __shared__ float bd[TQ][KMAX + TQ];
-    __shared__ float red[4][TQ][DK];
+    __shared__ float bd[TQ][BMAX];
+    __shared__ __align__(16) float red[4][TQ * DK];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int grp = tid / LPR, sub = tid % LPR;
+    const int grp = tid / LPR, sub = tid % LPR, row4 = lane >> 4;
     const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
+    const int L = a.L, Tq = a.T, D = a.H * DK, W = L + Tq, NB = L + 2 * Tq - 1;
+    const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)s * Tq * 3 * D + h * DK + sub * VEC;
+    const T* P = static_cast<const T*>(a.P) + (int64_t)(a.rel_offset + 1 - Tq) * D + h * DK + sub * VEC;
+    // the stream's descriptor (one scalar load, in flight while the launch-only loads issue)
     const int32_t* d = a.desc + s * DESC_INTS;
-    const int slot = d[0], frames = d[1], valid = min(max(d[2], 0), a.T), cache_len = d[3];
-    const int L = a.L, Tq = a.T, D = a.H * DK;
-    const int wpos = frames % L;
-    const int ks = L - cache_len, ke = L + valid;     // keys [ks, ke) of [L cached ; T new]
-    const int nk = ke - ks, nb = nk + Tq - 1;
-    const int rbase = (L - (ke - 1)) + a.rel_offset;  // table row of band index 0 (shift0 = L)
-    const T* kr = static_cast<const T*>(a.kring) + ((int64_t)slot * a.H + h) * L * DK;
-    const T* vr = static_cast<const T*>(a.vring) + ((int64_t)slot * a.H + h) * L * DK;
-    const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)s * a.T * 3 * D + h * DK;
-    const T* P = static_cast<const T*>(a.P) + h * DK;
-    auto key_ptr = [&](const T* ring, int j, int part) -> const T* {   // part 1: K, 2: V
-        if (j < L) { int r = wpos + j; r -= (r >= L) ? L : 0; return ring + (int64_t)r * DK; }
-        return qkv + (int64_t)(j - L) * 3 * D + part * D;
-    };
+    const int slot = d[0], wpos = d[1], valid = min(max(d[2], 0), Tq), cache_len = d[3];
 
-    // ---- issue every load: q, u/v, P band, K, V, commit rows
+    // ---- launch-only addresses: q, u/v, the band
     uint4 qreg[TQ];
 #pragma unroll
-    for (int i = 0; i < TQ; i++) qreg[i] = i < Tq ? ld16(qkv + (int64_t)i * 3 * D + sub * VEC) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < TQ; i++) qreg[i] = ld16(qkv + (int64_t)min(i, Tq - 1) * 3 * D);
     const float4 u0 = *reinterpret_cast<const float4*>(a.u + h * DK + sub * VEC);
     const float4 u1 = *reinterpret_cast<const float4*>(a.u + h * DK + sub * VEC + 4);
     const float4 v0 = *reinterpret_cast<const float4*>(a.vb + h * DK + sub * VEC);
     const float4 v1 = *reinterpret_cast<const float4*>(a.vb + h * DK + sub * VEC + 4);
-    uint4 preg[PRR], kreg[KR], vreg[KR];
+    uint4 preg[PR];
 #pragma unroll
-    for (int k = 0; k < PRR; k++) {
-        const int b = grp + k * G, r = rbase + b;
-        preg[k] = make_uint4(0, 0, 0, 0);
-        if (k * G < nb && b < nb && r >= 0 && r < a.n_rel) preg[k] = ld16(P + (int64_t)r * D + sub * VEC);
-    }
-#pragma unroll
-    for (int k = 0; k < KR; k++) {
-        const int row = grp + k * G;
-        kreg[k] = make_uint4(0, 0, 0, 0);
-        if (k * G < nk && row < nk) kreg[k] = ld16(key_ptr(kr, ks + row, 1) + sub * VEC);
-    }
-#pragma unroll
-    for (int k = 0; k < KR; k++) {
-        const int row = grp + k * G;
-        vreg[k] = make_uint4(0, 0, 0, 0);
-        if (k * G < nk && row < nk) vreg[k] = ld16(key_ptr(vr, ks + row, 2) + sub * VEC);
-    }
-    const bool has_commit = tid < Tq * LPR;
-    uint4 ck = make_uint4(0, 0, 0, 0), cv = make_uint4(0, 0, 0, 0);
-    if (has_commit) {
-        const T* q = qkv + (int64_t)(tid / LPR) * 3 * D + sub * VEC;
-        ck = ld16(q + D);
-        cv = ld16(q + 2 * D);
-    }
+    for (int k = 0; k < PR; k++) preg[k] = ld16(P + (int64_t)min(grp + k * G, NB - 1) * D);
 
-    // ---- q + u, q + v in registers
+    // ---- K and V of the window: key j = grp + 16k is ring row (wpos + j) mod L while j < L,
+    //      else new row j - L of qkv
+    const int ks = L - cache_len, ke = L + valid;
+    T* kring = static_cast<T*>(a.kring) + ((int64_t)slot * a.H + h) * L * DK + sub * VEC;
+    T* vring = static_cast<T*>(a.vring) + ((int64_t)slot * a.H + h) * L * DK + sub * VEC;
+    const T* knew = qkv + D;
+    const T* vnew = qkv + 2 * D;
+    uint32_t koff[KR];
+    bool cached[KR];
+    int r = wpos + grp;
+    r -= (r >= L) ? L : 0;
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int j = min(grp + k * G, W - 1);
+        cached[k] = j < L;
+        koff[k] = cached[k] ? (uint32_t)r * DK : (uint32_t)(j - L) * 3 * D;
+        r += G;
+        r -= (r >= L) ? L : 0;
+    }
+    uint4 kreg[KR], vreg[KR];
+#pragma unroll
+    for (int k = 0; k < KR; k++) kreg[k] = ld16((cached[k] ? kring : knew) + koff[k]);
+#pragma unroll
+    for (int k = 0; k < KR; k++) vreg[k] = ld16((cached[k] ? vring : vnew) + koff[k]);
+
+    // ---- q + u, q + v
     const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
     const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
     float qu[TQ][VEC], qv[TQ][VEC];
@@ -417,55 +429,51 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
     }
     const int qi = tsum16_index<TQ>(sub);
 
-    // ---- bd = (q + v) . P band   (P arrives first: it is read from L2)
+    // ---- bd[i][b] = (q_i + v) . band row b
 #pragma unroll
-    for (int k = 0; k < PRR; k++) {
-        if (k * G < nb) {
-            float f[VEC];
-            unpack16<T>(preg[k], f);
-            float part[TQ];
+    for (int k = 0; k < PR; k++) {
+        float f[VEC];
+        unpack16<T>(preg[k], f);
+        float part[TQ];
 #pragma unroll
-            for (int i = 0; i < TQ; i++) {
-                float acc = 0.0f;
+        for (int i = 0; i < TQ; i++) {
+            float acc = 0.0f;
 #pragma unroll
-                for (int e = 0; e < VEC; e++) acc += qv[i][e] * f[e];
-                part[i] = acc;
-            }
-            const float tot = tsum16<TQ>(part, sub);
-            const int b = grp + k * G;
-            if (sub < TQ && qi < Tq && b < nb) bd[qi][b] = tot;
+            for (int e = 0; e < VEC; e++) acc += qv[i][e] * f[e];
+            part[i] = acc;
         }
+        const float tot = tsum16<TQ>(part, sub);
+        if (sub < TQ) bd[qi][grp + k * G] = tot;
     }
-    // ---- ac = (q + u) . K
+    // ---- ac[i][j] = (q_i + u) . K_j
 #pragma unroll
     for (int k = 0; k < KR; k++) {
-        if (k * G < nk) {
-            float f[VEC];
-            unpack16<T>(kreg[k], f);
-            float part[TQ];
+        float f[VEC];
+        unpack16<T>(kreg[k], f);
+        float part[TQ];
 #pragma unroll
-            for (int i = 0; i < TQ; i++) {
-                float acc = 0.0f;
+        for (int i = 0; i < TQ; i++) {
+            float acc = 0.0f;
 #pragma unroll
-                for (int e = 0; e < VEC; e++) acc += qu[i][e] * f[e];
-                part[i] = acc;
-            }
-            const float tot = tsum16<TQ>(part, sub);
-            const int row = grp + k * G;
-            if (sub < TQ && qi < Tq && row < nk) sc[qi][row] = tot;
+            for (int e = 0; e < VEC; e++) acc += qu[i][e] * f[e];
+            part[i] = acc;
         }
+        const float tot = tsum16<TQ>(part, sub);
+        if (sub < TQ) sc[qi][grp + k * G] = tot;
     }
     __syncthreads();
 
-    // ---- softmax over the nk keys, one wave per query; probabilities overwrite sc
-    for (int i = wave; i < Tq; i += NT / 64) {
+    // ---- softmax over keys [ks, ke), one wave per query; rel_shift is the band index
+    //      W - 1 + i - j (table row (L + i - j) + rel_offset).  Probabilities overwrite sc.
+    for (int i = wave; i < Tq; i += 4) {
         constexpr int PER = (KMAX + 63) / 64;
         float sv[PER];
         float m = -INFINITY;
 #pragma unroll
         for (int p = 0; p < PER; p++) {
-            const int jj = lane + p * 64;
-            sv[p] = jj < nk ? (sc[i][jj] + bd[i][i - jj + nk - 1]) * a.scale : -INFINITY;
+            const int j = lane + p * 64, jc = min(j, W - 1);
+            const float x = (sc[i][jc] + bd[i][W - 1 + i - jc]) * a.scale;
+            sv[p] = (j >= ks && j < ke) ? x : -INFINITY;
             m = fmaxf(m, sv[p]);
         }
         m = wave_max(m);
@@ -479,66 +487,77 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
         for (int p = 0; p < PER; p++) {
-            const int jj = lane + p * 64;
-            if (jj < nk) sc[i][jj] = sv[p] * inv;
+            const int j = lane + p * 64;
+            if (j < KMAX) sc[i][j] = sv[p] * inv;
         }
     }
     __syncthreads();
 
-    // ---- out = P . V from the V registers
-    float acc[TQ][VEC];
+    // ---- out = P . V from the V registers (rows outside the range zeroed)
+    float acc[NV];
 #pragma unroll
-    for (int i = 0; i < TQ; i++)
-#pragma unroll
-        for (int e = 0; e < VEC; e++) acc[i][e] = 0.0f;
+    for (int f = 0; f < NV; f++) acc[f] = 0.0f;
 #pragma unroll
     for (int k = 0; k < KR; k++) {
-        const int row = grp + k * G;
-        if (k * G < nk && row < nk) {
-            float f[VEC];
-            unpack16<T>(vreg[k], f);
+        const int j = grp + k * G;
+        const bool in = j >= ks && j < ke;
+        const uint4 z = make_uint4(0, 0, 0, 0);
+        float f[VEC];
+        unpack16<T>(in ? vreg[k] : z, f);
 #pragma unroll
-            for (int i = 0; i < TQ; i++) {
-                const float p = i < Tq ? sc[i][row] : 0.0f;
+        for (int i = 0; i < TQ; i++) {
+            const float p = sc[i][j];
 #pragma unroll
-                for (int e = 0; e < VEC; e++) acc[i][e] += p * f[e];
-            }
+            for (int e = 0; e < VEC; e++) acc[i * VEC + e] += p * f[e];
         }
     }
-    // sum the 4 row groups of the wave (lanes sub, sub+16, sub+32, sub+48), then the 4 waves
+    // over the 4 row groups of the wave: lane (row4, sub) ends with flat sums row4*NQ .. +NQ-1
+    float h1[NV / 2], h2[NQ];
 #pragma unroll
-    for (int i = 0; i < TQ; i++)
+    for (int m = 0; m < NV / 2; m++) h1[m] = xsum32(acc[m], acc[m + NV / 2]);
 #pragma unroll
-        for (int e = 0; e < VEC; e++) {
-            float x = acc[i][e];
-            x += __shfl_xor(x, 16, 64);
-            x += __shfl_xor(x, 32, 64);
-            acc[i][e] = x;
-        }
-    if (lane < LPR) {
+    for (int m = 0; m < NQ; m++) h2[m] = xsum16(h1[m], h1[m + NQ]);
 #pragma unroll
-        for (int i = 0; i < TQ; i++)
-#pragma unroll
-            for (int e = 0; e < VEC; e++) red[wave][i][sub * VEC + e] = acc[i][e];
+    for (int m = 0; m < NQ; m += 4) {
+        const int f = row4 * NQ + m, i = f >> 3, e = f & 7;
+        *reinterpret_cast<float4*>(&red[wave][i * DK + sub * VEC + e]) = make_float4(h2[m], h2[m + 1], h2[m + 2], h2[m + 3]);
     }
     __syncthreads();
 
-    // ---- commit the new rows over the T oldest ring slots (every ring read finished above)
-    if (has_commit) {
-        int slot_row = wpos + tid / LPR;
-        slot_row -= (slot_row >= L) ? L : 0;
-        T* kw = static_cast<T*>(a.kring) + ((int64_t)slot * a.H + h) * L * DK;
-        T* vw = static_cast<T*>(a.vring) + ((int64_t)slot * a.H + h) * L * DK;
-        st16(kw + (int64_t)slot_row * DK + sub * VEC, ck);
-        st16(vw + (int64_t)slot_row * DK + sub * VEC, cv);
+    // ---- commit the T new K/V rows over the T oldest ring slots (every ring read is done)
+#pragma unroll
+    for (int k = 0; k < KR; k++) {
+        const int j = grp + k * G;
+        if (j >= L && j < W) {
+            int rr = wpos + (j - L);
+            rr -= (rr >= L) ? L : 0;
+            st16(kring + (int64_t)rr * DK, kreg[k]);
+            st16(vring + (int64_t)rr * DK, vreg[k]);
+        }
     }
-    // ---- output (0 for an empty key range)
-    for (int idx = tid; idx < Tq * DK; idx += NT) {
-        const int i = idx / DK, dd = idx % DK;
-        const float o = nk > 0 ? red[0][i][dd] + red[1][i][dd] + red[2][i][dd] + red[3][i][dd] : 0.0f;
-        const int64_t row = (int64_t)s * a.T + i;
-        if (a.att_frag) static_cast<T*>(a.att)[frag_index(row, h * DK + dd, D / 64)] = f2bf(o);
-        else static_cast<T*>(a.att)[row * D + h * DK + dd] = f2bf(o);
+    // ---- output rows (0 for an empty key range), 8 channels per thread
+    if (tid < Tq * LPR) {
+        const int i = tid / LPR;
+        float o[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; e += 4) {
+            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float4 x = *reinterpret_cast<const float4*>(&red[w][i * DK + sub * VEC + e]);
+                t.x += x.x; t.y += x.y; t.z += x.z; t.w += x.w;
+            }
+            o[e] = t.x; o[e + 1] = t.y; o[e + 2] = t.z; o[e + 3] = t.w;
+        }
+        const bool empty = ke <= ks;
+        uint32_t pk[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            pk[e] = empty ? 0u : ((uint32_t)f2bf(o[2 * e]) | ((uint32_t)f2bf(o[2 * e + 1]) << 16));
+        const int64_t row = (int64_t)s * Tq + i;
+        T* att = static_cast<T*>(a.att);
+        T* dst = a.att_frag ? att + frag_index(row, h * DK + sub * VEC, D / 64) : att + row * D + h * DK + sub * VEC;
+        st16(dst, make_uint4(pk[0], pk[1], pk[2], pk[3]));
     }
 }
 
@@ -581,10 +600,15 @@ int launch_relpos_op(const OpArgs& a, bool bf16_data, hipStream_t st) {
 template <typename T>
 static int launch_ring_t(const RingArgs& a, hipStream_t st) {
     dim3 grid(a.n * a.H), block(256);
-    // bf16 streaming chunks (T <= 4, L + T <= 96 keys, head_dim 128): the one-round-trip kernel.
-    if (sizeof(T) == 2 && a.T <= 4 && a.L + a.T <= 96 && a.n_rel >= 1) {
-        if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_small_kernel<2, 6>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((relpos_ring_small_kernel<4, 6>), grid, block, 0, st, a);
+    // bf16 streaming chunks (T <= 4, 16 <= L, L + T <= 96 keys, head_dim 128): the one-round-trip kernel.
+    // It reads the band rel = 1-T .. L+T-1 (table rows rel_offset+1-T .. rel_offset+L+T-1).
+    const bool band_ok = a.rel_offset + 1 - a.T >= 0 && a.rel_offset + a.L + a.T - 1 < a.n_rel;
+    if (sizeof(T) == 2 && a.T <= 4 && a.L >= 16 && a.L + a.T <= 96 && a.L + 2 * a.T - 1 <= 112 && band_ok) {
+        const int kr = (a.L + a.T + 15) / 16, pr = (a.L + 2 * a.T - 1 + 15) / 16;
+        if (a.T <= 2 && kr <= 5 && pr <= 5) hipLaunchKernelGGL((relpos_ring_small_kernel<2, 5, 5>), grid, block, 0, st, a);
+        else if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_small_kernel<2, 6, 7>), grid, block, 0, st, a);
+        else if (kr <= 5 && pr <= 5) hipLaunchKernelGGL((relpos_ring_small_kernel<4, 5, 5>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((relpos_ring_small_kernel<4, 6, 7>), grid, block, 0, st, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_kernel<T, 2, KeyBlock<T, 2>::KB>), grid, block, 0, st, a);

@@ -6,7 +6,7 @@
 //    sized for max_streams x max_chunk rows and a pool of per-stream caches;
 //  - caches are rings updated in place by the attention and conv kernels (no ping-pong copies);
 //    a stream's ring origin is derived from its frame counter, so the host carries one integer
-//    per stream and uploads a small descriptor {slot, frames, valid} per step;
+//    per stream and uploads a small descriptor {slot, ring origins, valid, cache_len} per step;
 //  - the 24-layer kernel sequence of a step is captured once per (batch size, T, input, output)
 //    into a hipGraph and replayed.
 #include <hip/hip_runtime.h>
@@ -499,10 +499,13 @@ static int upload_desc(ud_encoder* e, ud_stream* const* streams, int n, int T, c
     int32_t* d = e->desc_host[k];
     for (int i = 0; i < n; i++) {
         int v = valid ? valid[i] : T;
-        d[i * DESC_INTS + 0] = streams[i]->slot;
-        d[i * DESC_INTS + 1] = (int32_t)(streams[i]->frames % (int64_t)(e->L * (e->Kc - 1)));
-        d[i * DESC_INTS + 2] = v < 0 ? 0 : (v > T ? T : v);
-        d[i * DESC_INTS + 3] = (int32_t)(streams[i]->frames < e->L ? streams[i]->frames : e->L);
+        int32_t* di = d + i * DESC_INTS;
+        di[0] = streams[i]->slot;
+        di[1] = (int32_t)(streams[i]->frames % e->L);
+        di[2] = v < 0 ? 0 : (v > T ? T : v);
+        di[3] = (int32_t)(streams[i]->frames < e->L ? streams[i]->frames : e->L);
+        di[4] = (int32_t)(streams[i]->frames % (e->Kc - 1));
+        di[5] = di[6] = di[7] = 0;
     }
     HIPC(hipMemcpyAsync(e->desc_dev, d, (size_t)n * DESC_INTS * 4, hipMemcpyHostToDevice, st));
     HIPC(hipEventRecord(e->desc_ev[k], st));

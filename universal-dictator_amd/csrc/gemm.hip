@@ -21,15 +21,6 @@
 
 namespace ud {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
-    bf16x8_t r;
-    __builtin_memcpy(&r, &v, 16);
-    return r;
-}
-
 // Maps the linear workgroup id so that tiles t, t+1, ... of one XCD's share are contiguous
 // (workgroups are dealt round-robin to the 8 XCDs): the M tiles and K splits of one N tile then
 // run on the same XCD and share its L2.

@@ -10,9 +10,10 @@ namespace ud {
 // Activation codes (Sources/DictatorEngine/Core/Kernels.swift:4-6).
 enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_SILU = 2 };
 
-// Per-stream step descriptor, int32 x4: {pool slot, frames appended so far modulo L*(K-1) (the
-// ring origins are frames % L and frames % (K-1)), valid frames this step, cached frames}.
-constexpr int DESC_INTS = 4;
+// Per-stream step descriptor, int32 x8: {pool slot, K/V ring origin (frames appended so far mod L),
+// valid frames this step, cached frames (min(frames, L)), conv ring origin (frames mod (K-1)),
+// 0, 0, 0}.  32 bytes: one scalar load per workgroup.
+constexpr int DESC_INTS = 8;
 
 // ---------------------------------------------------------------- attention
 struct OpArgs {

@@ -133,8 +133,7 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
     const int D = a.D, T = a.T;
     const int c0 = tid * 4;
     const int32_t* d = a.desc + s * DESC_INTS;
-    const int slot = d[0], frames = d[1], valid = d[2];
-    const int cpos = frames % KC;
+    const int slot = d[0], cpos = d[4], valid = d[2];
     float* ring = a.ring + (int64_t)slot * KC * D;
 
     float4 in[KC + TMAX];

@@ -20,6 +20,15 @@ __device__ __forceinline__ bf16 f2bf(float f) {
     return (bf16)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
+// MFMA operand types (v_mfma_f32_16x16x32_bf16: 8 bf16 of A and of B per lane, 4 fp32 of C).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
+    bf16x8_t r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+
 template <typename T> __device__ __forceinline__ float to_f(T v);
 template <> __device__ __forceinline__ float to_f<float>(float v) { return v; }
 template <> __device__ __forceinline__ float to_f<bf16>(bf16 v) { return bf2f(v); }
