@@ -561,6 +561,240 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ streaming ring kernel on MFMA (T <= 16)
+// Longer chunks (config of 14 frames) make the per-(stream, head) work a real matrix product:
+// 16 query rows (T of them real) against L + T keys and L + 2T - 1 band rows.  One wave64 per
+// (stream, head), everything on v_mfma_f32_16x16x32_bf16:
+//   bd^T-free form: C[query][band row] = (q+v) . P_band^T   (A = q+v, B = P rows straight from HBM/L2)
+//   C[query][key] = (q+u) . K^T                              (B = K rows straight from the ring)
+//   out[query][chan] = softmax . V                           (A = probabilities, B = V^T)
+// A lane's B operand is 8 consecutive k values for one n: for the score products that is one
+// 16-byte chunk of a K / P row (n = row, k = channels), loaded directly; for P.V it is 8 keys of one
+// channel, which ds_read_b64_tr_b16 produces from V rows staged row-major in LDS.  q+u, q+v and the
+// probabilities are fp32 and enter as bf16 hi/lo pairs (two MFMAs), so products keep ~2^-17
+// relative accuracy.  Scores stay in registers (lane: queries 4g..4g+3 of key 16t + lane%16);
+// rel_shift is a gather of the band tile from LDS; softmax reduces within 16-lane DPP rows.
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+
+// fp32 x 8 -> bf16 hi (round to nearest even) and lo = bf16(x - hi), packed for an MFMA operand.
+__device__ __forceinline__ void split_bf16x8(const float (&x)[8], uint4& hi, uint4& lo) {
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const bf16 h0 = f2bf(x[e]), h1 = f2bf(x[e + 1]);
+        hw[e / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        lw[e / 2] = (uint32_t)f2bf(x[e] - bf2f(h0)) | ((uint32_t)f2bf(x[e + 1] - bf2f(h1)) << 16);
+    }
+    hi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    lo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+}
+
+template <int KT, int BT>
+__global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
+    using T = bf16;
+    constexpr int DK = 128, KMAX = KT * 16, BMAX = BT * 16, VST = DK + 8;
+    static_assert(KMAX % 32 == 0, "P.V k-steps of 32 keys");
+    __shared__ __align__(16) bf16 vl[KMAX][VST];          // V rows of the window (masked rows 0)
+    __shared__ __align__(16) float sl[16][BMAX + 4];       // band tile for the gather, then probabilities
+
+    const int lane = threadIdx.x, col = lane & 15, g = lane >> 4;
+    const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
+    const int L = a.L, Tq = a.T, D = a.H * DK, W = L + Tq, NB = L + 2 * Tq - 1;
+    const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)s * Tq * 3 * D + h * DK;
+    const T* P = static_cast<const T*>(a.P) + (int64_t)(a.rel_offset + 1 - Tq) * D + h * DK;
+    const int32_t* d = a.desc + s * DESC_INTS;
+    const int slot = d[0], wpos = d[1], valid = min(max(d[2], 0), Tq), cache_len = d[3];
+    const int ks = L - cache_len, ke = L + valid;
+    T* kring = static_cast<T*>(a.kring) + ((int64_t)slot * a.H + h) * L * DK;
+    T* vring = static_cast<T*>(a.vring) + ((int64_t)slot * a.H + h) * L * DK;
+    auto key_row = [&](T* ring, int j, int part) -> const T* {   // part 1: K, 2: V
+        int r = wpos + j;
+        r -= (r >= L) ? L : 0;
+        return j < L ? ring + (int64_t)r * DK : qkv + (int64_t)(j - L) * 3 * D + part * D;
+    };
+
+    // ---- loads: q (A rows = queries), u/v, the band tiles, the K tiles (B rows), k-chunk 4st + g
+    uint4 qraw[4];
+    float4 ua[4][2], va[4][2];
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+        const int c = (4 * st + g) * 8;
+        qraw[st] = ld16(qkv + (int64_t)min(col, Tq - 1) * 3 * D + c);
+        ua[st][0] = *reinterpret_cast<const float4*>(a.u + h * DK + c);
+        ua[st][1] = *reinterpret_cast<const float4*>(a.u + h * DK + c + 4);
+        va[st][0] = *reinterpret_cast<const float4*>(a.vb + h * DK + c);
+        va[st][1] = *reinterpret_cast<const float4*>(a.vb + h * DK + c + 4);
+    }
+    uint4 pb[BT][4];
+#pragma unroll
+    for (int t = 0; t < BT; t++) {
+        const T* row = P + (int64_t)min(16 * t + col, NB - 1) * D;
+#pragma unroll
+        for (int st = 0; st < 4; st++) pb[t][st] = ld16(row + (4 * st + g) * 8);
+    }
+    uint4 kb[KT][4];
+#pragma unroll
+    for (int t = 0; t < KT; t++) {
+        const T* row = key_row(kring, min(16 * t + col, W - 1), 1);
+#pragma unroll
+        for (int st = 0; st < 4; st++) kb[t][st] = ld16(row + (4 * st + g) * 8);
+    }
+
+    // ---- A operands: q + u and q + v as bf16 hi/lo
+    uint4 auh[4], aul[4], avh[4], avl[4];
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+        float q[8], x[8], y[8];
+        unpack16<T>(qraw[st], q);
+        const float uu[8] = {ua[st][0].x, ua[st][0].y, ua[st][0].z, ua[st][0].w, ua[st][1].x, ua[st][1].y, ua[st][1].z, ua[st][1].w};
+        const float vv[8] = {va[st][0].x, va[st][0].y, va[st][0].z, va[st][0].w, va[st][1].x, va[st][1].y, va[st][1].z, va[st][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) { x[e] = q[e] + uu[e]; y[e] = q[e] + vv[e]; }
+        split_bf16x8(x, auh[st], aul[st]);
+        split_bf16x8(y, avh[st], avl[st]);
+    }
+
+    // ---- bd tiles -> LDS: sl[query][band row]
+#pragma unroll
+    for (int t = 0; t < BT; t++) {
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avh[st]), as_bf16x8(pb[t][st]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avl[st]), as_bf16x8(pb[t][st]), acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) sl[4 * g + r][16 * t + col] = acc[r];
+    }
+
+    // ---- V rows of the window -> LDS (4 rows per pass, 16 lanes x 16 bytes per row)
+    uint4 vr[KMAX / 4];
+#pragma unroll
+    for (int it = 0; it < KMAX / 4; it++) vr[it] = ld16(key_row(vring, min(4 * it + g, W - 1), 2) + col * 8);
+
+    // ---- ac tiles in registers: lane holds queries 4g..4g+3 of key 16t + col
+    f32x4_t sacc[KT];
+#pragma unroll
+    for (int t = 0; t < KT; t++) {
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(auh[st]), as_bf16x8(kb[t][st]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aul[st]), as_bf16x8(kb[t][st]), acc, 0, 0, 0);
+        }
+        sacc[t] = acc;
+    }
+    // commit the new K rows (this wave read every ring row it overwrites, above)
+#pragma unroll
+    for (int t = 0; t < KT; t++) {
+        const int j = 16 * t + col;
+        if (j >= L && j < W) {
+            int r = wpos + (j - L);
+            r -= (r >= L) ? L : 0;
+#pragma unroll
+            for (int st = 0; st < 4; st++) st16(kring + (int64_t)r * DK + (4 * st + g) * 8, kb[t][st]);
+        }
+    }
+    __syncthreads();
+
+    // ---- scores, rel_shift gather, softmax over keys [ks, ke) (16-lane rows hold one query set)
+    float pr[KT][4];
+    float mx[4], sm[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) mx[r] = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < KT; t++) {
+        const int j = 16 * t + col;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int i = 4 * g + r;
+            const int b = min(max(W - 1 + i - j, 0), BMAX - 1);
+            const float x = (sacc[t][r] + sl[i][b]) * a.scale;
+            pr[t][r] = (i < Tq && j >= ks && j < ke) ? x : -INFINITY;
+            mx[r] = fmaxf(mx[r], pr[t][r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) { mx[r] = group_max<16>(mx[r]); sm[r] = 0.0f; }
+#pragma unroll
+    for (int t = 0; t < KT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            pr[t][r] = pr[t][r] == -INFINITY ? 0.0f : __expf(pr[t][r] - mx[r]);
+            sm[r] += pr[t][r];
+        }
+#pragma unroll
+    for (int r = 0; r < 4; r++) { sm[r] = group_sum<16>(sm[r]); sm[r] = sm[r] > 0.0f ? 1.0f / sm[r] : 0.0f; }
+    // V rows to LDS (zero outside [ks, ke)); the band tile is no longer needed: probabilities
+    // overwrite it as sl[query][key]
+#pragma unroll
+    for (int it = 0; it < KMAX / 4; it++) {
+        const int j = 4 * it + g;
+        const bool in = j >= ks && j < ke;
+        *reinterpret_cast<uint4*>(&vl[j][col * 8]) = in ? vr[it] : make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < KT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sl[4 * g + r][16 * t + col] = pr[t][r] * sm[r];
+    // commit the new V rows
+#pragma unroll
+    for (int it = 0; it < KMAX / 4; it++) {
+        const int j = 4 * it + g;
+        if (j >= L && j < W) {
+            int r = wpos + (j - L);
+            r -= (r >= L) ? L : 0;
+            st16(vring + (int64_t)r * DK + col * 8, vr[it]);
+        }
+    }
+    __syncthreads();
+
+    // ---- out = P . V: A = probabilities (query col, keys 32kk + 8g ..), B = V^T via transposed reads
+    f32x4_t oacc[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) oacc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kk = 0; kk < KMAX / 32; kk++) {
+        float pf[8];
+        const float4 p0 = *reinterpret_cast<const float4*>(&sl[col][32 * kk + 8 * g]);
+        const float4 p1 = *reinterpret_cast<const float4*>(&sl[col][32 * kk + 8 * g + 4]);
+        pf[0] = p0.x; pf[1] = p0.y; pf[2] = p0.z; pf[3] = p0.w; pf[4] = p1.x; pf[5] = p1.y; pf[6] = p1.z; pf[7] = p1.w;
+        uint4 ph, pl;
+        split_bf16x8(pf, ph, pl);
+        const int k0 = 32 * kk + 8 * g + (col >> 2);
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            const int c0 = 16 * dt + 4 * (col & 3);
+            const v4i16_t b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vl[k0][c0]);
+            const v4i16_t b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vl[k0 + 4][c0]);
+            uint4 bv;
+            __builtin_memcpy(&bv.x, &b0, 8);
+            __builtin_memcpy(&bv.z, &b1, 8);
+            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ph), as_bf16x8(bv), oacc[dt], 0, 0, 0);
+            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pl), as_bf16x8(bv), oacc[dt], 0, 0, 0);
+        }
+    }
+
+    // ---- output: lane holds out[4g + r][16dt + col]  (0 for an empty key range)
+    const bool empty = ke <= ks;
+    T* att = static_cast<T*>(a.att);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int i = 4 * g + r;
+        if (i < Tq) {
+            const int64_t orow = (int64_t)s * Tq + i;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const int c = h * DK + 16 * dt + col;
+                const int64_t idx = a.att_frag ? frag_index(orow, c, D / 64) : orow * D + c;
+                att[idx] = empty ? (T)0 : f2bf(oacc[dt][r]);
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ launchers
 
 // Keys per block: as many as keep the workgroup's LDS under 64 KB.
@@ -609,6 +843,11 @@ static int launch_ring_t(const RingArgs& a, hipStream_t st) {
         else if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_small_kernel<2, 6, 7>), grid, block, 0, st, a);
         else if (kr <= 5 && pr <= 5) hipLaunchKernelGGL((relpos_ring_small_kernel<4, 5, 5>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((relpos_ring_small_kernel<4, 6, 7>), grid, block, 0, st, a);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    // bf16 chunks of 5..16 frames (L + T <= 96 keys): the MFMA kernel, one wave per (stream, head).
+    if (sizeof(T) == 2 && a.T <= 16 && a.L + a.T <= 96 && a.L + 2 * a.T - 1 <= 112 && band_ok) {
+        hipLaunchKernelGGL((relpos_ring_mfma_kernel<6, 7>), dim3(a.n * a.H), dim3(64), 0, st, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_kernel<T, 2, KeyBlock<T, 2>::KB>), grid, block, 0, st, a);
