@@ -40,10 +40,12 @@ typedef enum {
 
 typedef enum {
     UD_F32 = 0,               /* fp32 weights, activations, caches */
-    UD_BF16 = 1               /* bf16 weights, GEMM inputs, K/V caches and position tables;
+    UD_BF16 = 1,              /* bf16 weights, GEMM inputs, K/V caches and position tables;
                                  fp32 accumulation, residual stream, norms, pos_bias, depthwise
                                  conv and conv cache (the keep-fp32 policy of
                                  Sources/DictatorEngine/Core/Convert.swift:76-83) */
+    UD_F16 = 2                /* IEEE half: the decoder K/V cache format of the reference
+                                 (Sources/DictatorEngine/Core/Ops.swift:147); decode entry points only */
 } ud_dtype;
 
 /* FastConformerConfig (Sources/DictatorEngine/Models/FastConformer.swift:5-38) plus the streaming

@@ -162,6 +162,30 @@ def relpos_attention(q, k, v, P, u, vb, ranges, rel_offset, H):
     return out
 
 
+def gqa_attention(q, k, v, ranges, Hq, Hkv, scale=None):
+    """attention_gqa (30_voxtral.metal:45-101): q [Tq, Hq*d], k/v [Tk, Hkv*d], ranges int32 [Tq, 2]."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    Tq, QW = q.shape
+    d = QW // Hq
+    Tk = k.shape[0]
+    out = np.empty_like(q)
+    rr = np.ascontiguousarray(ranges, dtype=np.int32)
+    if scale is None:
+        scale = 1.0 / np.sqrt(np.float32(d))
+    lib().orc_gqa_attention(_p(q), _p(k), _p(v), _ip(rr), _p(out), Tq, Tk, Hq, Hkv, d, QW, Hkv * d, QW,
+                            ctypes.c_float(scale))
+    return out
+
+
+def rope_rotate_half(x, H, d, inv_freq, positions=None, pos0=0):
+    """rope_rotate_half (30_voxtral.metal:20-36) on a copy of x [T, ld]."""
+    y = _f32(x).copy()
+    T, ld = y.shape
+    pos = None if positions is None else np.ascontiguousarray(positions, dtype=np.int32)
+    lib().orc_rope_rotate_half(_p(y), T, H, d, ld, _ip(pos) if pos is not None else None, pos0, _p(_f32(inv_freq)))
+    return y
+
+
 def chunked_limited_ranges(T, left, right):
     r = np.empty((T, 2), np.int32)
     lib().orc_chunked_limited_ranges(T, left, right, _ip(r))

@@ -28,6 +28,10 @@
  *                         rel_shift, chunked_limited mask)
  *   orc_stream_step       streaming == offline equivalence through the
  *                         torch restatement, and the cache rule
+ *   orc_gqa_attention     reference KAT (VoxtralOpTests.swift:6-38) against a
+ *                         numpy float64 softmax attention; GQA head map
+ *   orc_rope_rotate_half  reference KAT (VoxtralOpTests.swift:60-75) against
+ *                         rotation by a complex exponential (numpy)
  */
 #include <math.h>
 #include <stdint.h>
@@ -228,6 +232,70 @@ ORC_API void orc_relpos_attention(const float* Q, const float* K, const float* V
                 out[(int64_t)i * ldo + hoff + d] = (float)(acc * inv);
             }
             free(s);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ decoder attention */
+
+/* Sources/DictatorEngine/Metal/30_voxtral.metal:45-101 (attention_gqa), dispatched by
+ * Sources/DictatorEngine/Core/Ops.swift:136-169: query i, head h uses kv head h / (Hq/Hkv); scores
+ * (q . k) * scale over keys [max(r.x, 0), min(r.y, Tk)); softmax; . V; 0 for an empty range.
+ * Q [Tq, ldq], K/V [Tk, ldk] (row strides), out [Tq, ldo].  Accumulates in double. */
+ORC_API void orc_gqa_attention(const float* Q, const float* K, const float* V, const int32_t* ranges, float* out,
+                               int Tq, int Tk, int Hq, int Hkv, int d, int ldq, int ldk, int ldo, float scale) {
+    const int group = Hq / Hkv;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int i = 0; i < Tq; i++) {
+        for (int h = 0; h < Hq; h++) {
+            const int kvh = h / group;
+            const int ks = ranges[2 * i] > 0 ? ranges[2 * i] : 0;
+            const int ke = ranges[2 * i + 1] < Tk ? ranges[2 * i + 1] : Tk;
+            const float* q = Q + (int64_t)i * ldq + h * d;
+            float* o = out + (int64_t)i * ldo + h * d;
+            if (ke <= ks) {
+                for (int e = 0; e < d; e++) o[e] = 0.0f;
+                continue;
+            }
+            double* s = (double*)malloc(sizeof(double) * (size_t)(ke - ks));
+            double m = -INFINITY;
+            for (int j = ks; j < ke; j++) {
+                const float* kr = K + (int64_t)j * ldk + kvh * d;
+                double a = 0;
+                for (int e = 0; e < d; e++) a += (double)q[e] * kr[e];
+                s[j - ks] = a * scale;
+                if (s[j - ks] > m) m = s[j - ks];
+            }
+            double den = 0;
+            for (int j = ks; j < ke; j++) { s[j - ks] = exp(s[j - ks] - m); den += s[j - ks]; }
+            for (int e = 0; e < d; e++) {
+                double acc = 0;
+                for (int j = ks; j < ke; j++) acc += s[j - ks] * V[(int64_t)j * ldk + kvh * d + e];
+                o[e] = (float)(acc / den);
+            }
+            free(s);
+        }
+    }
+}
+
+/* Sources/DictatorEngine/Metal/30_voxtral.metal:20-36 (rope_rotate_half) in place on x [T, ld]:
+ * for head h and pair (i, i + d/2), angle = float(pos(t)) * inv_freq[i] (a float product, as the
+ * reference computes it), x_i' = x_i cos - x_{i+d/2} sin, x_{i+d/2}' = x_{i+d/2} cos + x_i sin, with
+ * cos/sin of that angle in double.  pos(t) = positions[t] if positions, else pos0 + t. */
+ORC_API void orc_rope_rotate_half(float* x, int T, int H, int d, int ld, const int32_t* positions, int pos0,
+                                  const float* inv_freq) {
+    const int half = d / 2;
+    for (int t = 0; t < T; t++) {
+        const int p = positions ? positions[t] : pos0 + t;
+        for (int h = 0; h < H; h++) {
+            float* row = x + (int64_t)t * ld + h * d;
+            for (int i = 0; i < half; i++) {
+                const float angle = (float)p * inv_freq[i];
+                const double c = cos((double)angle), sn = sin((double)angle);
+                const double a = row[i], b = row[i + half];
+                row[i] = (float)(a * c - b * sn);
+                row[i + half] = (float)(b * c + a * sn);
+            }
         }
     }
 }

@@ -23,8 +23,9 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libud_encoder.so")
 INCLUDE_DIR = os.path.join(os.path.dirname(PKG_DIR), "include")
 
-UD_F32, UD_BF16 = 0, 1
-_DTYPES = {"f32": UD_F32, "fp32": UD_F32, "float32": UD_F32, "bf16": UD_BF16, "bfloat16": UD_BF16}
+UD_F32, UD_BF16, UD_F16 = 0, 1, 2
+_DTYPES = {"f32": UD_F32, "fp32": UD_F32, "float32": UD_F32, "bf16": UD_BF16, "bfloat16": UD_BF16,
+           "f16": UD_F16, "float16": UD_F16}
 
 STATUS = {0: "ok", -1: "invalid argument", -2: "shape", -3: "out of memory", -4: "HIP error", -5: "state",
           -6: "weight", -7: "capacity"}
@@ -85,6 +86,11 @@ def _sig(lib):
         "ud_event_record": (i, [p, p]),
         "ud_event_synchronize": (i, [p]),
         "ud_event_elapsed_ms": (i, [f, p, p]),
+        "ud_gqa_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32]),
+        "ud_gqa_attention_paged": (i, [_i32, p, p, p, p, _i32, p, p, _i32, _i32, _i32, _i32, _i32, _i32, p,
+                                       ctypes.c_size_t, p]),
+        "ud_rope_rotate_half": (i, [_i32, p, _i32, _i32, _i32, _i32, p, _i32, p, p]),
+        "ud_paged_kv_append": (i, [_i32, p, p, p, p, p, _i32, p, _i32, _i32, _i32, _i32, p]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -383,6 +389,47 @@ def rel_pos_attention(q, k, v, pos_table, rel_offset, bias_u, bias_v, ranges, ou
     _check(lib().ud_relpos_attention(_DTYPES[dtype], q.ptr, k.ptr, v.ptr, pos_table.ptr, bias_u.ptr, bias_v.ptr,
                                      ranges.ptr, out.ptr, Tq, Tk, heads, head_dim, rel_offset, n_rel,
                                      hip_stream.ptr if hip_stream else None))
+
+
+# ---------------------------------------------------------------- decoder attention (ud_decode.h)
+
+def rope_inv_freq(head_dim, theta=1e6):
+    """inv_freq_i = 1 / theta^(2i/d), evaluated in float64 and rounded to float32 as the reference
+    builds it (Sources/DictatorEngine/Models/Voxtral.swift:176-179)."""
+    i = np.arange(head_dim // 2, dtype=np.float64)
+    return (1.0 / np.power(float(theta), 2.0 * i / head_dim)).astype(np.float32)
+
+
+def gqa_workspace_bytes(n, q_heads, head_dim, max_keys):
+    return int(lib().ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys))
+
+
+def gqa_attention_paged(q, k_pages, v_pages, block_table, max_blocks, ranges, out, n, q_heads, kv_heads, head_dim,
+                        max_keys, workspace, kv_dtype="bf16", block_size=16, hip_stream=None):
+    """Step.attention (Ops.swift:136-169) for one query token per sequence over a paged K/V cache:
+    q/out fp32 [n, q_heads*head_dim]; k_pages/v_pages [num_blocks, kv_heads, block_size, head_dim]
+    (kv_dtype bf16 or f16); block_table int32 [n, max_blocks]; ranges int32 [n, 2]."""
+    _check(lib().ud_gqa_attention_paged(_DTYPES[kv_dtype], q.ptr, k_pages.ptr, v_pages.ptr, block_table.ptr,
+                                        max_blocks, ranges.ptr, out.ptr, n, q_heads, kv_heads, head_dim, block_size,
+                                        max_keys, workspace.ptr, workspace.nbytes,
+                                        hip_stream.ptr if hip_stream else None))
+
+
+def rope_rotate_half(x, rows, heads, head_dim, ld, inv_freq, positions=None, pos0=0, dtype="f32", hip_stream=None):
+    """Step.rope / rope_rotate_half (30_voxtral.metal:20-36) in place on x [rows, ld]; positions is
+    an int32 DeviceBuffer [rows] or None for pos0 + row."""
+    _check(lib().ud_rope_rotate_half(_DTYPES[dtype], x.ptr, rows, heads, head_dim, ld,
+                                     positions.ptr if positions is not None else None, pos0, inv_freq.ptr,
+                                     hip_stream.ptr if hip_stream else None))
+
+
+def paged_kv_append(k_new, v_new, k_pages, v_pages, block_table, max_blocks, positions, n, kv_heads, head_dim,
+                    kv_dtype="bf16", block_size=16, hip_stream=None):
+    """Writes row i of k_new / v_new [n, kv_heads*head_dim] at logical position positions[i] of
+    sequence i in the paged cache."""
+    _check(lib().ud_paged_kv_append(_DTYPES[kv_dtype], k_new.ptr, v_new.ptr, k_pages.ptr, v_pages.ptr, block_table.ptr,
+                                    max_blocks, positions.ptr, n, kv_heads, head_dim, block_size,
+                                    hip_stream.ptr if hip_stream else None))
 
 
 # ---------------------------------------------------------------- synthetic weights

@@ -345,16 +345,6 @@ template <int Q> __device__ __forceinline__ int tsum16_index(int lane) {
     else return 0;
 }
 
-// a + (a from lane l^32) into lanes 0-31 and b + (b from lane l^32) into lanes 32-63.
-__device__ __forceinline__ float xsum32(float a, float b) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-// a + (a from lane l^16) into rows 0 and 2 (lanes 0-15, 32-47), b + ... into rows 1 and 3.
-__device__ __forceinline__ float xsum16(float a, float b) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
 // One workgroup (4 waves) per (stream, head).  16 lanes own one 128-wide bf16 row (8 values per
 // lane), 16 row groups per pass: KR passes cover the window's L + T keys, PR passes the band's

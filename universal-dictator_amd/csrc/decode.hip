@@ -1,0 +1,430 @@
+// Decoder attention for gfx950: grouped-query attention of one new token per sequence over a paged
+// K/V cache, the rotate-half RoPE and the paged cache append (include/ud_decode.h).
+//
+// Semantics: Sources/DictatorEngine/Metal/30_voxtral.metal:45-101 (attention_gqa: query head h
+// reads kv head h / (Hq/Hkv); scores q.k * 1/sqrt(d); softmax over the query's key range; 0 for an
+// empty range) and :20-36 (rope_rotate_half), dispatched by Sources/DictatorEngine/Core/Ops.swift
+// (Step.attention :136-169, Step.rope).  The reference keeps one sliding K/V window per session
+// (Sources/DictatorEngine/Models/Voxtral.swift:206-250); here the caches of many sequences share
+// one pool of fixed-size pages addressed through a block table.
+//
+// Design (HBM-bound: every K/V byte of every sequence is read once per step):
+//  - split-K ("flash decoding"): workgroup = (256-key split, kv head, sequence), 4 wave64s.  The
+//    Hq/Hkv query heads of a kv head share each K/V row read, so GQA costs no extra traffic;
+//  - 16 B per lane loads: a head_dim row is D/8 lanes wide; K and V of the split are all issued
+//    before the first score, V zeroed in registers outside the key range;
+//  - scores: per-row dot products of the G query heads reduced together with a transposed DPP
+//    butterfly inside the row's lanes; softmax of a split in LDS; P.V reduced across row groups with
+//    v_permlane32_swap / v_permlane16_swap / DPP and across waves once through LDS;
+//  - a second kernel merges the splits of each (sequence, head) with the usual max/sum rescaling.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/ud_decode.h"
+#include "ud_common.hpp"
+
+int ud_set_error(int code, const char* msg);   // encoder.hip
+
+namespace ud {
+
+constexpr int SPLIT = 256;      // keys per split workgroup
+constexpr int PAGE = 16;        // block_size
+
+// Element formats of 16-bit K/V and RoPE rows (both stored as uint16_t).
+struct BF16 {};
+struct F16 {};
+
+template <typename T> struct KvTraits;
+template <> struct KvTraits<BF16> {
+    static __device__ __forceinline__ void unpack(uint4 v, float* f) { unpack16<bf16>(v, f); }
+    static __device__ __forceinline__ float to_f(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
+    static __device__ __forceinline__ uint16_t from_f(float x) { return f2bf(x); }
+};
+template <> struct KvTraits<F16> {
+    static __device__ __forceinline__ float h2f(uint32_t u) { return (float)__builtin_bit_cast(_Float16, (uint16_t)u); }
+    static __device__ __forceinline__ void unpack(uint4 v, float* f) {
+        f[0] = h2f(v.x & 0xffffu); f[1] = h2f(v.x >> 16);
+        f[2] = h2f(v.y & 0xffffu); f[3] = h2f(v.y >> 16);
+        f[4] = h2f(v.z & 0xffffu); f[5] = h2f(v.z >> 16);
+        f[6] = h2f(v.w & 0xffffu); f[7] = h2f(v.w >> 16);
+    }
+    static __device__ __forceinline__ float to_f(uint16_t u) { return h2f(u); }
+    static __device__ __forceinline__ uint16_t from_f(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+};
+
+// Transposed sum over the W lanes of a row (W in {8, 16}, aligned groups) of Q values per lane
+// (Q <= W).  Steps pair lanes with row_mirror (W = 16), row_half_mirror, quad_perm [1,0,3,2] and
+// [2,3,0,1]; the first log2(Q) of them keep half of the values (selected by lane bit 3, 2, 0, 1),
+// the rest are plain sums.  Returns, in every lane, the row total of value index qidx(lane).
+template <int CTRL, int N>
+__device__ __forceinline__ void tkeep(float* v, bool bit) {
+#pragma unroll
+    for (int m = 0; m < N / 2; m++) {
+        const float keep = bit ? v[m + N / 2] : v[m], send = bit ? v[m] : v[m + N / 2];
+        v[m] = keep + dpp_mov<CTRL>(send);
+    }
+}
+template <int CTRL, int K, int Q>
+__device__ __forceinline__ void tstage(float* v, bool bit) {
+    if constexpr ((1 << K) < Q) tkeep<CTRL, (Q >> K)>(v, bit);
+    else v[0] += dpp_mov<CTRL>(v[0]);
+}
+template <int W, int Q>
+__device__ __forceinline__ float tsum_row(float (&v)[Q], int lane) {
+    static_assert((W == 8 || W == 16) && Q >= 1 && Q <= W, "row sum");
+    if constexpr (W == 16) {
+        tstage<DPP_ROW_MIRROR, 0, Q>(v, lane & 8);
+        tstage<DPP_ROW_HALF_MIRROR, 1, Q>(v, lane & 4);
+        tstage<DPP_QUAD_1032, 2, Q>(v, lane & 1);
+        tstage<DPP_QUAD_2301, 3, Q>(v, lane & 2);
+    } else {
+        tstage<DPP_ROW_HALF_MIRROR, 0, Q>(v, lane & 4);
+        tstage<DPP_QUAD_1032, 1, Q>(v, lane & 1);
+        tstage<DPP_QUAD_2301, 2, Q>(v, lane & 2);
+    }
+    return v[0];
+}
+// Value index a lane holds after tsum_row, and whether it is the lane that reports it.
+template <int W, int Q>
+__device__ __forceinline__ int tsum_row_index(int lane, bool& writer) {
+    constexpr int b[4] = {W == 16 ? 3 : 2, W == 16 ? 2 : 0, W == 16 ? 0 : 1, 1};
+    int m = 0, rest = 0;
+#pragma unroll
+    for (int k = 0; k < (W == 16 ? 4 : 3); k++) {
+        const int bit = (lane >> b[k]) & 1;
+        if ((1 << k) < Q) m += bit * (Q >> (k + 1));
+        else rest |= bit;
+    }
+    writer = rest == 0;
+    return m;
+}
+
+// a + (a from lane l^8) into lanes with bit 3 clear, b + ... into lanes with bit 3 set.
+__device__ __forceinline__ float xsum8(float a, float b, bool bit3) {
+    const float keep = bit3 ? b : a, send = bit3 ? a : b;
+    return keep + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(send), 0x128, 0xF, 0xF, false));
+}
+
+struct GqaArgs {
+    const float* q; const void* kp; const void* vp;
+    const int32_t* bt; const int32_t* ranges;
+    float* part;                   // [n][Hq][NS][D + 2]: unnormalised sum, max, sum of exp
+    int max_blocks, Hq, Hkv, NS;
+    int kmax;                      // keys the pages and the split grid can hold
+    float scale;
+};
+
+template <typename KT, int D, int G>
+__global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
+    constexpr int LPR = D / 8, RG = 256 / LPR, NP = SPLIT / RG, NV = G * 8;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = tid / LPR, sub = tid % LPR;
+    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const int lo = max(a.ranges[2 * seq], 0), hi = min(a.ranges[2 * seq + 1], a.kmax);
+    const int s0 = split * SPLIT;
+    const int klo = max(lo, s0), khi = min(hi, s0 + SPLIT);
+    if (klo >= khi) return;                       // this split holds no key of the range
+    __shared__ float sc[G][SPLIT];
+    __shared__ float stat[G][2];
+    __shared__ __align__(16) float red[4][G][D];
+
+    // ---- the G query heads of this kv head (8 channels per lane)
+    float q[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float* qr = a.q + (int64_t)seq * a.Hq * D + (kvh * G + g) * D + sub * 8;
+        const float4 x0 = *reinterpret_cast<const float4*>(qr), x1 = *reinterpret_cast<const float4*>(qr + 4);
+        q[g][0] = x0.x; q[g][1] = x0.y; q[g][2] = x0.z; q[g][3] = x0.w;
+        q[g][4] = x1.x; q[g][5] = x1.y; q[g][6] = x1.z; q[g][7] = x1.w;
+    }
+    // ---- K and V rows: key s0 + grp + RG p; pages outside [klo, khi) are never looked up
+    const int blo = klo / PAGE, bhi = (khi - 1) / PAGE;
+    const int32_t* bt = a.bt + (int64_t)seq * a.max_blocks;
+    uint32_t off[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int j = s0 + grp + RG * p;
+        const int b = min(max(j / PAGE, blo), bhi);
+        const int phys = bt[b];
+        off[p] = ((uint32_t)(phys * a.Hkv + kvh) * PAGE + (uint32_t)(j % PAGE)) * D + sub * 8;
+    }
+    const uint16_t* kp = static_cast<const uint16_t*>(a.kp);
+    const uint16_t* vp = static_cast<const uint16_t*>(a.vp);
+    uint4 kr[NP], vr[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++) kr[p] = ld16(kp + off[p]);
+#pragma unroll
+    for (int p = 0; p < NP; p++) vr[p] = ld16(vp + off[p]);
+
+    // ---- scores of the G heads -> sc (masked keys -inf)
+    bool writer;
+    const int qi = tsum_row_index<LPR, G>(sub, writer);
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        float f[8];
+        KvTraits<KT>::unpack(kr[p], f);
+        float part[G];
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc += q[g][e] * f[e];
+            part[g] = acc;
+        }
+        const float tot = tsum_row<LPR, G>(part, sub);
+        const int jj = grp + RG * p, j = s0 + jj;
+        if (writer) sc[qi][jj] = (j >= klo && j < khi) ? tot * a.scale : -INFINITY;
+    }
+    __syncthreads();
+
+    // ---- softmax of the split, one wave per head: probabilities in sc, (max, sum) in stat
+    for (int g = wave; g < G; g += 4) {
+        float v[SPLIT / 64];
+        float m = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < SPLIT / 64; k++) { v[k] = sc[g][lane + 64 * k]; m = fmaxf(m, v[k]); }
+        m = wave_max(m);
+        float l = 0.0f;
+#pragma unroll
+        for (int k = 0; k < SPLIT / 64; k++) {
+            v[k] = v[k] == -INFINITY ? 0.0f : __expf(v[k] - m);
+            l += v[k];
+            sc[g][lane + 64 * k] = v[k];
+        }
+        l = wave_sum(l);
+        if (lane == 0) { stat[g][0] = m; stat[g][1] = l; }
+    }
+    __syncthreads();
+
+    // ---- P.V over this lane's rows (rows outside the range zeroed)
+    float acc[NV];
+#pragma unroll
+    for (int f = 0; f < NV; f++) acc[f] = 0.0f;
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int jj = grp + RG * p, j = s0 + jj;
+        const bool in = j >= klo && j < khi;
+        float f[8];
+        KvTraits<KT>::unpack(in ? vr[p] : make_uint4(0, 0, 0, 0), f);
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            const float pg = sc[g][jj];
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[g * 8 + e] += pg * f[e];
+        }
+    }
+    // over the row groups of the wave (lanes with equal sub): xor 32, 16 (and 8 when LPR = 8)
+    constexpr int S1 = NV / 2, S2 = NV / 4;
+    float h1[S1], h2[S2];
+#pragma unroll
+    for (int m = 0; m < S1; m++) h1[m] = xsum32(acc[m], acc[m + S1]);
+#pragma unroll
+    for (int m = 0; m < S2; m++) h2[m] = xsum16(h1[m], h1[m + S2]);
+    int fbase = ((lane >> 5) & 1) * S1 + ((lane >> 4) & 1) * S2;
+    if constexpr (LPR == 16) {
+#pragma unroll
+        for (int m = 0; m < S2; m++) { const int f = fbase + m; red[wave][f / 8][sub * 8 + f % 8] = h2[m]; }
+    } else {
+        constexpr int S3 = NV / 8;
+        float h3[S3];
+#pragma unroll
+        for (int m = 0; m < S3; m++) h3[m] = xsum8(h2[m], h2[m + S3], lane & 8);
+        fbase += ((lane >> 3) & 1) * S3;
+#pragma unroll
+        for (int m = 0; m < S3; m++) { const int f = fbase + m; red[wave][f / 8][sub * 8 + f % 8] = h3[m]; }
+    }
+    __syncthreads();
+
+    // ---- partial of each head: sum over the 4 waves, then (max, sum of exp)
+    for (int idx = tid; idx < G * D; idx += 256) {
+        const int g = idx / D, dd = idx % D;
+        const float s = red[0][g][dd] + red[1][g][dd] + red[2][g][dd] + red[3][g][dd];
+        float* pr = a.part + (((int64_t)seq * a.Hq + kvh * G + g) * a.NS + split) * (D + 2);
+        pr[dd] = s;
+        if (dd == 0) { pr[D] = stat[g][0]; pr[D + 1] = stat[g][1]; }
+    }
+}
+
+// Merge the splits of one (sequence, head): out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
+template <int D>
+__global__ __launch_bounds__(D) void gqa_combine_kernel(const float* part, const int32_t* ranges, float* out,
+                                                        int Hq, int NS, int kmax) {
+    const int h = blockIdx.x, seq = blockIdx.y, dd = threadIdx.x;
+    const int lo = max(ranges[2 * seq], 0), hi = min(ranges[2 * seq + 1], kmax);
+    float* o = out + ((int64_t)seq * Hq + h) * D + dd;
+    if (lo >= hi) { *o = 0.0f; return; }
+    const int sa = lo / SPLIT, sb = (hi - 1) / SPLIT;
+    const float* pr = part + ((int64_t)seq * Hq + h) * NS * (D + 2);
+    float M = -INFINITY;
+    for (int s = sa; s <= sb; s++) M = fmaxf(M, pr[s * (D + 2) + D]);
+    float L = 0.0f, acc = 0.0f;
+    for (int s = sa; s <= sb; s++) {
+        const float* ps = pr + s * (D + 2);
+        const float w = ps[D] == -INFINITY ? 0.0f : __expf(ps[D] - M);
+        L += w * ps[D + 1];
+        acc += w * ps[dd];
+    }
+    *o = L > 0.0f ? acc / L : 0.0f;
+}
+
+// ---------------------------------------------------------------- RoPE
+template <typename T> struct RopeIO;    // fp32 rows, or 16-bit rows of format T
+template <> struct RopeIO<float> {
+    typedef float S;
+    static __device__ float ld(const float* p) { return *p; }
+    static __device__ void st(float* p, float v) { *p = v; }
+};
+template <typename F> struct RopeIO {
+    typedef uint16_t S;
+    static __device__ float ld(const uint16_t* p) { return KvTraits<F>::to_f(*p); }
+    static __device__ void st(uint16_t* p, float v) { *p = KvTraits<F>::from_f(v); }
+};
+
+template <typename T>
+__global__ void rope_kernel(typename RopeIO<T>::S* x, int rows, int H, int d, int ld, const int32_t* pos, int pos0,
+                            const float* inv_freq) {
+    const int half = d / 2;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)rows * H * half) return;
+    const int i = (int)(idx % half), h = (int)((idx / half) % H), t = (int)(idx / ((int64_t)half * H));
+    const int p = pos ? pos[t] : pos0 + t;
+    const float angle = (float)p * inv_freq[i];
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    typename RopeIO<T>::S* row = x + (int64_t)t * ld + h * d;
+    const float u = RopeIO<T>::ld(row + i), v = RopeIO<T>::ld(row + i + half);
+    RopeIO<T>::st(row + i, u * cs - v * sn);
+    RopeIO<T>::st(row + i + half, v * cs + u * sn);
+}
+
+// ---------------------------------------------------------------- paged append
+template <int D>
+__global__ void kv_append_kernel(const uint16_t* kn, const uint16_t* vn, uint16_t* kp, uint16_t* vp, const int32_t* bt,
+                                 int max_blocks, const int32_t* pos, int Hkv) {
+    const int seq = blockIdx.x, kvh = blockIdx.y, c = threadIdx.x;   // c: 16-byte chunk of the row
+    const int p = min(max(pos[seq], 0), max_blocks * PAGE - 1);
+    const int phys = bt[(int64_t)seq * max_blocks + p / PAGE];
+    const int64_t dst = (((int64_t)phys * Hkv + kvh) * PAGE + p % PAGE) * D + c * 8;
+    const int64_t src = ((int64_t)seq * Hkv + kvh) * D + c * 8;
+    st16(kp + dst, ld16(kn + src));
+    st16(vp + dst, ld16(vn + src));
+}
+
+}  // namespace ud
+
+using namespace ud;
+
+static int dfail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    return ud_set_error(code, buf);
+}
+
+static int nsplits(int32_t max_keys) { return max_keys <= 0 ? 1 : (max_keys + SPLIT - 1) / SPLIT; }
+
+extern "C" UD_API size_t ud_gqa_workspace_bytes(int32_t n, int32_t q_heads, int32_t head_dim, int32_t max_keys) {
+    if (n <= 0 || q_heads <= 0 || head_dim <= 0) return 0;
+    return (size_t)n * q_heads * nsplits(max_keys) * (head_dim + 2) * sizeof(float);
+}
+
+template <typename KT, int D>
+static int launch_gqa(const GqaArgs& a, int n, int G, int nsplit, float* out, hipStream_t st) {
+    dim3 grid(nsplit, a.Hkv, n), block(256);
+    switch (G) {
+        case 1: hipLaunchKernelGGL((gqa_split_kernel<KT, D, 1>), grid, block, 0, st, a); break;
+        case 2: hipLaunchKernelGGL((gqa_split_kernel<KT, D, 2>), grid, block, 0, st, a); break;
+        case 4: hipLaunchKernelGGL((gqa_split_kernel<KT, D, 4>), grid, block, 0, st, a); break;
+        case 8: hipLaunchKernelGGL((gqa_split_kernel<KT, D, 8>), grid, block, 0, st, a); break;
+        default: return UD_ERR_SHAPE;
+    }
+    hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n), dim3(D), 0, st, a.part, a.ranges, out, a.Hq, a.NS, a.kmax);
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_gqa_attention_paged(int32_t kv_dtype, const float* q_dev, const void* k_pages,
+                                             const void* v_pages, const int32_t* block_table, int32_t max_blocks,
+                                             const int32_t* ranges_dev, float* out_dev, int32_t n, int32_t q_heads,
+                                             int32_t kv_heads, int32_t head_dim, int32_t block_size, int32_t max_keys,
+                                             void* workspace, size_t workspace_bytes, void* hip_stream) {
+    if (!q_dev || !k_pages || !v_pages || !block_table || !ranges_dev || !out_dev || !workspace)
+        return dfail(UD_ERR_INVALID, "ud_gqa_attention_paged: null pointer");
+    if (kv_dtype != UD_BF16 && kv_dtype != UD_F16) return dfail(UD_ERR_INVALID, "ud_gqa_attention_paged: kv dtype %d", kv_dtype);
+    if (n < 1 || q_heads < 1 || kv_heads < 1 || q_heads % kv_heads) return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: heads %d/%d, n %d", q_heads, kv_heads, n);
+    const int G = q_heads / kv_heads;
+    if (G != 1 && G != 2 && G != 4 && G != 8) return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: group %d not in {1,2,4,8}", G);
+    if (head_dim != 64 && head_dim != 128) return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: head_dim %d", head_dim);
+    if (block_size != PAGE) return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: block_size %d (16 supported)", block_size);
+    if (max_blocks < 1 || max_keys < 0 || max_keys > max_blocks * PAGE)
+        return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: max_keys %d beyond %d blocks", max_keys, max_blocks);
+    if (workspace_bytes < ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys))
+        return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: workspace %zu < %zu bytes", workspace_bytes,
+                     ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys));
+    if (((uintptr_t)q_dev | (uintptr_t)k_pages | (uintptr_t)v_pages | (uintptr_t)workspace) & 15)
+        return dfail(UD_ERR_INVALID, "ud_gqa_attention_paged: buffers must be 16-byte aligned");
+    GqaArgs a{};
+    a.q = q_dev; a.kp = k_pages; a.vp = v_pages; a.bt = block_table; a.ranges = ranges_dev;
+    a.part = static_cast<float*>(workspace);
+    a.max_blocks = max_blocks; a.Hq = q_heads; a.Hkv = kv_heads; a.NS = nsplits(max_keys);
+    a.kmax = min(max_blocks * PAGE, a.NS * SPLIT);
+    a.scale = 1.0f / sqrtf((float)head_dim);
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    int rc;
+    if (kv_dtype == UD_BF16)
+        rc = head_dim == 128 ? launch_gqa<BF16, 128>(a, n, G, a.NS, out_dev, st) : launch_gqa<BF16, 64>(a, n, G, a.NS, out_dev, st);
+    else
+        rc = head_dim == 128 ? launch_gqa<F16, 128>(a, n, G, a.NS, out_dev, st) : launch_gqa<F16, 64>(a, n, G, a.NS, out_dev, st);
+    if (rc != UD_OK) return dfail(rc, "ud_gqa_attention_paged: unsupported shape");
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return dfail(UD_ERR_HIP, "ud_gqa_attention_paged: %s", hipGetErrorString(e));
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_rope_rotate_half(int32_t dtype, void* x_dev, int32_t rows, int32_t heads, int32_t head_dim,
+                                          int32_t ld, const int32_t* positions_dev, int32_t pos0,
+                                          const float* inv_freq_dev, void* hip_stream) {
+    if (!x_dev || !inv_freq_dev) return dfail(UD_ERR_INVALID, "ud_rope_rotate_half: null pointer");
+    if (rows < 0 || heads < 1 || head_dim < 2 || head_dim % 2 || ld < heads * head_dim)
+        return dfail(UD_ERR_SHAPE, "ud_rope_rotate_half: rows %d heads %d head_dim %d ld %d", rows, heads, head_dim, ld);
+    if (rows == 0) return UD_OK;
+    const int64_t total = (int64_t)rows * heads * (head_dim / 2);
+    dim3 grid((unsigned)((total + 255) / 256)), block(256);
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    switch (dtype) {
+        case UD_F32: hipLaunchKernelGGL(rope_kernel<float>, grid, block, 0, st, static_cast<float*>(x_dev), rows, heads, head_dim, ld, positions_dev, pos0, inv_freq_dev); break;
+        case UD_BF16: hipLaunchKernelGGL(rope_kernel<BF16>, grid, block, 0, st, static_cast<uint16_t*>(x_dev), rows, heads, head_dim, ld, positions_dev, pos0, inv_freq_dev); break;
+        case UD_F16: hipLaunchKernelGGL(rope_kernel<F16>, grid, block, 0, st, static_cast<uint16_t*>(x_dev), rows, heads, head_dim, ld, positions_dev, pos0, inv_freq_dev); break;
+        default: return dfail(UD_ERR_INVALID, "ud_rope_rotate_half: dtype %d", dtype);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return dfail(UD_ERR_HIP, "ud_rope_rotate_half: %s", hipGetErrorString(e));
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_paged_kv_append(int32_t kv_dtype, const void* k_new, const void* v_new, void* k_pages,
+                                         void* v_pages, const int32_t* block_table, int32_t max_blocks,
+                                         const int32_t* positions_dev, int32_t n, int32_t kv_heads, int32_t head_dim,
+                                         int32_t block_size, void* hip_stream) {
+    if (!k_new || !v_new || !k_pages || !v_pages || !block_table || !positions_dev)
+        return dfail(UD_ERR_INVALID, "ud_paged_kv_append: null pointer");
+    if (kv_dtype != UD_BF16 && kv_dtype != UD_F16) return dfail(UD_ERR_INVALID, "ud_paged_kv_append: kv dtype %d", kv_dtype);
+    if (n < 0 || kv_heads < 1 || (head_dim != 64 && head_dim != 128) || block_size != PAGE || max_blocks < 1)
+        return dfail(UD_ERR_SHAPE, "ud_paged_kv_append: n %d kv_heads %d head_dim %d block %d", n, kv_heads, head_dim, block_size);
+    if (((uintptr_t)k_new | (uintptr_t)v_new | (uintptr_t)k_pages | (uintptr_t)v_pages) & 15)
+        return dfail(UD_ERR_INVALID, "ud_paged_kv_append: buffers must be 16-byte aligned");
+    if (n == 0) return UD_OK;
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    const uint16_t* kn = static_cast<const uint16_t*>(k_new);
+    const uint16_t* vn = static_cast<const uint16_t*>(v_new);
+    uint16_t* kp = static_cast<uint16_t*>(k_pages);
+    uint16_t* vp = static_cast<uint16_t*>(v_pages);
+    if (head_dim == 128) hipLaunchKernelGGL(kv_append_kernel<128>, dim3(n, kv_heads), dim3(16), 0, st, kn, vn, kp, vp, block_table, max_blocks, positions_dev, kv_heads);
+    else hipLaunchKernelGGL(kv_append_kernel<64>, dim3(n, kv_heads), dim3(8), 0, st, kn, vn, kp, vp, block_table, max_blocks, positions_dev, kv_heads);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return dfail(UD_ERR_HIP, "ud_paged_kv_append: %s", hipGetErrorString(e));
+    return UD_OK;
+}

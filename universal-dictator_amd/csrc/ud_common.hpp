@@ -102,4 +102,16 @@ template <int W> __device__ __forceinline__ float group_max(float v) {
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 
+// Cross-row sums with the gfx950 lane-swap instructions: a + (a from lane l^32) into lanes 0-31 and
+// b + (b from lane l^32) into lanes 32-63; likewise for l^16 (rows 0, 2 get a, rows 1, 3 get b).
+__device__ __forceinline__ float xsum32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xsum16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+
 }  // namespace ud
