@@ -1,6 +1,6 @@
 """Benchmark of the cache-aware streaming FastConformer encoder step on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode] [--no-cpu-baseline]
 
 A step is one 24-layer encoder chunk step (bf16 weights/activations, fp32 accumulation) for every
 stream of the batch, with inputs already in HBM and full 70-frame caches seeded from N(0,1).
@@ -8,6 +8,11 @@ Default workload: 64 streams x 2 frames (160 ms of audio per stream per step).  
 line: aggregate streamed audio-seconds per second, the fused attention kernel's achieved HBM
 bandwidth against 8 TB/s (HIP events on the kernel's own stream), and the CPU oracle's throughput
 on a bounded sample timed on this host.
+
+--workload chunk14 runs the same step at 256 streams x 14 frames.  --workload decode measures the
+decoder's paged grouped-query attention instead: 64 sequences x 1 new token, 32 query / 8 kv heads
+x 128, contexts uniform in 512..4096 keys in bf16 pages of 16 (one line in the same format, value in
+tokens/s).
 """
 import argparse
 import importlib.util
@@ -25,6 +30,7 @@ HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, vendor nominal
 WORKLOADS = {
     "chunk2": dict(streams=64, T=2),     # 64 concurrent streams, 160 ms chunks
     "chunk14": dict(streams=256, T=14),  # 256 concurrent streams, 1120 ms chunks
+    "decode": dict(seqs=64, q_heads=32, kv_heads=8, head_dim=128, page=16, ctx=(512, 4096)),
 }
 
 
@@ -85,6 +91,93 @@ def cpu_baseline(lw, cfg, S, T, budget_s, threads):
                        % (n, S, T, cfg.layers, el, step_s))
 
 
+def decode_bench(ud, args):
+    """Paged GQA decode attention: one new token for each of 64 sequences."""
+    wl = WORKLOADS["decode"]
+    n, Hq, Hkv, d, page = wl["seqs"], wl["q_heads"], wl["kv_heads"], wl["head_dim"], wl["page"]
+    rng = np.random.default_rng(17)
+    lens = rng.integers(wl["ctx"][0], wl["ctx"][1] + 1, n)
+    nb = (lens + page - 1) // page
+    max_blocks = (wl["ctx"][1] + page - 1) // page
+    nblk = int(nb.sum())
+    perm = rng.permutation(nblk).astype(np.int32)
+    table = np.zeros((n, max_blocks), np.int32)
+    o = 0
+    for i in range(n):
+        table[i, :nb[i]] = perm[o:o + nb[i]]
+        o += nb[i]
+    log("device %s; workload decode: %d sequences, %d/%d heads x %d, context %d..%d (total %d keys), bf16 pages of %d"
+        % (ud.device_arch(), n, Hq, Hkv, d, lens.min(), lens.max(), lens.sum(), page))
+
+    def pages():
+        x = rng.standard_normal((nblk, Hkv, page, d), dtype=np.float32)
+        return (ud.round_bf16(x).view(np.uint32) >> 16).astype(np.uint16)
+    kp_h, vp_h = pages(), pages()
+    kp, vp = ud.DeviceBuffer.from_numpy(kp_h), ud.DeviceBuffer.from_numpy(vp_h)
+    q_h = rng.standard_normal((n, Hq * d), dtype=np.float32)
+    q = ud.DeviceBuffer.from_numpy(q_h)
+    ranges_h = np.stack([np.zeros(n, np.int32), lens.astype(np.int32)], 1)
+    ranges = ud.DeviceBuffer.from_numpy(ranges_h)
+    tbl = ud.DeviceBuffer.from_numpy(table)
+    max_keys = int(lens.max())
+    ws = ud.DeviceBuffer.zeros(ud.gqa_workspace_bytes(n, Hq, d, max_keys))
+    out = ud.DeviceBuffer(n * Hq * d * 4)
+    hs = ud.HipStream()
+    call = lambda: ud.gqa_attention_paged(q, kp, vp, tbl, max_blocks, ranges, out, n, Hq, Hkv, d, max_keys, ws,
+                                          hip_stream=hs)
+    for _ in range(args.warmup):
+        call()
+    hs.synchronize()
+    e0, e1 = ud.Event(), ud.Event()
+    e0.record(hs)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        call()
+    e1.record(hs)
+    e1.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1000.0
+    ms = max(wall_ms, e0.elapsed_ms(e1)) / args.steps
+    kv_bytes = int(lens.sum()) * Hkv * d * 2 * 2
+    algo = kv_bytes + n * Hq * d * 4 * 2 + int(nb.sum()) * 4
+    achieved = algo / (ms / 1000.0) / 1e9
+    log("timed %d calls: %.2f us per decode attention step (split + combine), %.0f GB/s" % (args.steps, ms * 1000, achieved))
+    result = {
+        "metric": "paged GQA decode attention: tokens/s and HBM roofline fraction",
+        "value": round(n / (ms / 1000.0), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) queries and bf16 K/V pages, random page table)",
+        "config": {"workload": "decode-step grouped-query attention over a paged K/V cache, %d sequences x 1 token, "
+                               "%d query / %d kv heads x %d, context %d..%d, pages of %d"
+                               % (n, Hq, Hkv, d, wl["ctx"][0], wl["ctx"][1], page),
+                   "sequences": n, "q_heads": Hq, "kv_heads": Hkv, "head_dim": d, "total_keys": int(lens.sum())},
+        "roofline": {"kernel": "gqa_split_kernel + gqa_combine_kernel (timed together)", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("gqa_decode"),
+                     "algorithmic_bytes_per_launch": algo},
+    }
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        sys.path.insert(0, ROOT)
+        from oracle import oracle as orc
+        orc.set_threads(threads)
+        log("cpu baseline: oracle attention on %d threads, ~%.0f s" % (threads, args.cpu_seconds))
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds and done < n:
+            i = done
+            rows = lambda pg: pg[table[i, :nb[i]]].transpose(0, 2, 1, 3).reshape(-1, Hkv * d)[:lens[i]]
+            k = (rows(kp_h).astype(np.uint32) << 16).view(np.float32)
+            v = (rows(vp_h).astype(np.uint32) << 16).view(np.float32)
+            orc.gqa_attention(q_h[i:i + 1], k, v, ranges_h[i:i + 1], Hq, Hkv)
+            done += 1
+        el = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": round(done / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+                                  "sample": "%d of the %d sequences (one token each, all heads) in %.1f s, "
+                                            "including the page gather" % (done, n, el)}
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -112,6 +205,9 @@ def main():
         ud.synchronize()
         log("calibration copy: %d MiB device-to-device" % args.calibrate_copy_mib)
         src.free(); dst.free()
+    if args.workload == "decode":
+        decode_bench(ud, args)
+        return
     wl = WORKLOADS[args.workload]
     S, T = wl["streams"], wl["T"]
     cfg = ud.EncoderConfig(layers=24, max_chunk=T, max_streams=S, dtype="bf16")

@@ -55,7 +55,7 @@ def run_paged(ud, q, kseqs, vseqs, ranges, Hq, Hkv, d, kv_dtype, rng):
             vp[table[i, b], :, :len(rows), :] = rows.transpose(1, 0, 2)
     max_keys = int(max(1, ranges[:, 1].max()))
     dev = ud.DeviceBuffer.from_numpy
-    ws = ud.DeviceBuffer(max(16, ud.gqa_workspace_bytes(n, Hq, d, max_keys)))
+    ws = ud.DeviceBuffer.zeros(max(16, ud.gqa_workspace_bytes(n, Hq, d, max_keys)))
     out = ud.DeviceBuffer(n * Hq * d * 4)
     ud.gqa_attention_paged(dev(np.ascontiguousarray(q, np.float32)), dev(kp), dev(vp), dev(table), max_blocks,
                            dev(np.ascontiguousarray(ranges, np.int32)), out, n, Hq, Hkv, d, max_keys, ws,

@@ -9,7 +9,7 @@
 // one pool of fixed-size pages addressed through a block table.
 //
 // Design (HBM-bound: every K/V byte of every sequence is read once per step):
-//  - split-K ("flash decoding"): workgroup = (256-key split, kv head, sequence), 4 wave64s.  The
+//  - split-K ("flash decoding"): workgroup = (128-key split, kv head, sequence), 4 wave64s.  The
 //    Hq/Hkv query heads of a kv head share each K/V row read, so GQA costs no extra traffic;
 //  - 16 B per lane loads: a head_dim row is D/8 lanes wide; K and V of the split are all issued
 //    before the first score, V zeroed in registers outside the key range;
@@ -29,7 +29,7 @@ int ud_set_error(int code, const char* msg);   // encoder.hip
 
 namespace ud {
 
-constexpr int SPLIT = 256;      // keys per split workgroup
+constexpr int SPLIT = 128;      // keys per split workgroup
 constexpr int PAGE = 16;        // block_size
 
 // Element formats of 16-bit K/V and RoPE rows (both stored as uint16_t).
@@ -247,26 +247,56 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
     }
 }
 
-// Merge the splits of one (sequence, head): out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
+// Merge the splits of one (sequence, head), one wave: out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
+// Lane s holds split s's (max, sum) of a chunk of up to 64 splits; the weights reach every lane
+// with readlane, and the dims (D/64 per lane) accumulate with independent loads.
 template <int D>
-__global__ __launch_bounds__(D) void gqa_combine_kernel(const float* part, const int32_t* ranges, float* out,
-                                                        int Hq, int NS, int kmax) {
-    const int h = blockIdx.x, seq = blockIdx.y, dd = threadIdx.x;
+__global__ __launch_bounds__(64) void gqa_combine_kernel(const float* part, const int32_t* ranges, float* out,
+                                                         int Hq, int NS, int kmax) {
+    constexpr int DL = D / 64;
+    const int h = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
     const int lo = max(ranges[2 * seq], 0), hi = min(ranges[2 * seq + 1], kmax);
-    float* o = out + ((int64_t)seq * Hq + h) * D + dd;
-    if (lo >= hi) { *o = 0.0f; return; }
+    float* o = out + ((int64_t)seq * Hq + h) * D;
+    if (lo >= hi) {
+#pragma unroll
+        for (int k = 0; k < DL; k++) o[lane + 64 * k] = 0.0f;
+        return;
+    }
     const int sa = lo / SPLIT, sb = (hi - 1) / SPLIT;
     const float* pr = part + ((int64_t)seq * Hq + h) * NS * (D + 2);
-    float M = -INFINITY;
-    for (int s = sa; s <= sb; s++) M = fmaxf(M, pr[s * (D + 2) + D]);
-    float L = 0.0f, acc = 0.0f;
-    for (int s = sa; s <= sb; s++) {
-        const float* ps = pr + s * (D + 2);
-        const float w = ps[D] == -INFINITY ? 0.0f : __expf(ps[D] - M);
-        L += w * ps[D + 1];
-        acc += w * ps[dd];
+    float M = -INFINITY, L = 0.0f, acc[DL];
+#pragma unroll
+    for (int k = 0; k < DL; k++) acc[k] = 0.0f;
+    for (int c0 = sa; c0 <= sb; c0 += 64) {
+        const int cnt = min(64, sb - c0 + 1);
+        const float m = lane < cnt ? pr[(c0 + lane) * (D + 2) + D] : -INFINITY;
+        const float l = lane < cnt ? pr[(c0 + lane) * (D + 2) + D + 1] : 0.0f;
+        const float nm = fmaxf(M, wave_max(m));
+        const float keep = M == -INFINITY ? 0.0f : __expf(M - nm);
+        const float w = lane < cnt ? __expf(m - nm) : 0.0f;
+        L = L * keep + wave_sum(w * l);
+#pragma unroll
+        for (int k = 0; k < DL; k++) acc[k] *= keep;
+        for (int s0 = 0; s0 < cnt; s0 += 8) {         // 8 splits' loads in flight at a time
+            float ws[8], x[8][DL];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int si = min(s0 + u, cnt - 1);
+                ws[u] = s0 + u < cnt ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), si)) : 0.0f;
+                const float* ps = pr + (c0 + si) * (D + 2);
+#pragma unroll
+                for (int k = 0; k < DL; k++) x[u][k] = ps[lane + 64 * k];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int k = 0; k < DL; k++) acc[k] += ws[u] * x[u][k];
+        }
+        M = nm;
     }
-    *o = L > 0.0f ? acc / L : 0.0f;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+#pragma unroll
+    for (int k = 0; k < DL; k++) o[lane + 64 * k] = acc[k] * inv;
 }
 
 // ---------------------------------------------------------------- RoPE
@@ -342,7 +372,7 @@ static int launch_gqa(const GqaArgs& a, int n, int G, int nsplit, float* out, hi
         case 8: hipLaunchKernelGGL((gqa_split_kernel<KT, D, 8>), grid, block, 0, st, a); break;
         default: return UD_ERR_SHAPE;
     }
-    hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n), dim3(D), 0, st, a.part, a.ranges, out, a.Hq, a.NS, a.kmax);
+    hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n), dim3(64), 0, st, a.part, a.ranges, out, a.Hq, a.NS, a.kmax);
     return UD_OK;
 }
 
