@@ -1,6 +1,7 @@
 """Benchmark of the cache-aware streaming FastConformer encoder step on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|offline]
+                    [--no-cpu-baseline]
 
 A step is one 24-layer encoder chunk step (bf16 weights/activations, fp32 accumulation) for every
 stream of the batch, with inputs already in HBM and full 70-frame caches seeded from N(0,1).
@@ -12,7 +13,9 @@ on a bounded sample timed on this host.
 --workload chunk14 runs the same step at 256 streams x 14 frames.  --workload decode measures the
 decoder's paged grouped-query attention instead: 64 sequences x 1 new token, 32 query / 8 kv heads
 x 128, contexts uniform in 512..4096 keys in bf16 pages of 16 (one line in the same format, value in
-tokens/s).
+tokens/s).  --workload offline measures the whole-utterance rel-pos attention: 8 utterances x 1500
+frames, 8 heads x 128, valid lengths uniform in 900..1500 as key padding (value in frames/s, roofline
+against the bf16 MFMA peak).
 """
 import argparse
 import importlib.util
@@ -31,7 +34,9 @@ WORKLOADS = {
     "chunk2": dict(streams=64, T=2),     # 64 concurrent streams, 160 ms chunks
     "chunk14": dict(streams=256, T=14),  # 256 concurrent streams, 1120 ms chunks
     "decode": dict(seqs=64, q_heads=32, kv_heads=8, head_dim=128, page=16, ctx=(512, 4096)),
+    "offline": dict(batch=8, frames=1500, heads=8, head_dim=128, valid=(900, 1500)),
 }
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
 
 
 def log(msg):
@@ -178,6 +183,83 @@ def decode_bench(ud, args):
     print(json.dumps(result), flush=True)
 
 
+def offline_bench(ud, args):
+    """Offline rel-pos attention over a padded batch of whole utterances (one launch = one layer)."""
+    wl = WORKLOADS["offline"]
+    B, T, H, dk = wl["batch"], wl["frames"], wl["heads"], wl["head_dim"]
+    D = H * dk
+    rng = np.random.default_rng(23)
+    lens = rng.integers(wl["valid"][0], wl["valid"][1] + 1, B)
+    log("device %s; workload offline: %d utterances x %d frames, valid %s, %d heads x %d, bf16"
+        % (ud.device_arch(), B, T, [int(x) for x in lens], H, dk))
+    bits = lambda a: (ud.round_bf16(a).view(np.uint32) >> 16).astype(np.uint16)
+    q, k, v = (ud.DeviceBuffer.from_numpy(bits(rng.standard_normal((B, T, D), dtype=np.float32))) for _ in range(3))
+    n_rel = 2 * T - 1
+    P = ud.DeviceBuffer.from_numpy(bits((rng.standard_normal((n_rel, D)) * 0.5).astype(np.float32)))
+    u = ud.DeviceBuffer.from_numpy((rng.standard_normal((H, dk)) * 0.02).astype(np.float32))
+    vb = ud.DeviceBuffer.from_numpy((rng.standard_normal((H, dk)) * 0.02).astype(np.float32))
+    ranges_h = np.zeros((B, T, 2), np.int32)
+    ranges_h[:, :, 1] = lens[:, None]
+    ranges = ud.DeviceBuffer.from_numpy(ranges_h)
+    out = ud.DeviceBuffer(B * T * D * 2)
+    hs = ud.HipStream()
+    call = lambda: ud.rel_pos_attention_batched(q, k, v, P, T - 1, u, vb, ranges, out, B, T, H, n_rel, hip_stream=hs)
+    for _ in range(args.warmup):
+        call()
+    hs.synchronize()
+    e0, e1 = ud.Event(), ud.Event()
+    e0.record(hs)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        call()
+    e1.record(hs)
+    e1.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1000.0
+    ms = max(wall_ms, e0.elapsed_ms(e1)) / args.steps
+    flops_dense = 6.0 * B * H * T * T * dk               # ac + bd + P.V over the padded T x T
+    flops_valid = 6.0 * H * T * float(lens.sum()) * dk   # keys limited to each utterance's valid frames
+    tflops = flops_dense / (ms / 1000.0) / 1e12
+    log("timed %d launches: %.2f us each, %.1f TFLOP/s dense-equivalent (%.1f on valid keys)"
+        % (args.steps, ms * 1000, tflops, flops_valid / (ms / 1000.0) / 1e12))
+    result = {
+        "metric": "offline rel-pos attention: frames/s and bf16 MFMA roofline fraction",
+        "value": round(B * T / (ms / 1000.0), 1),
+        "unit": "frames/s (one layer, all heads)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, random position table, random valid lengths)",
+        "config": {"workload": "offline full-context rel-pos MHSA, %d utterances x %d frames (%d s), %d heads x %d, "
+                               "key padding %d..%d" % (B, T, int(T * FRAME_SEC), H, dk, wl["valid"][0], wl["valid"][1]),
+                   "batch": B, "frames": T, "heads": H, "head_dim": dk, "valid_lengths": [int(x) for x in lens]},
+        "roofline": {"kernel": "relpos_dense_kernel", "bound": "mfma", "achieved": round(tflops, 2),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": read_traffic("relpos_dense_offline"),
+                     "algorithmic_flops_per_launch": flops_dense, "valid_key_flops_per_launch": flops_valid},
+    }
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        sys.path.insert(0, ROOT)
+        from oracle import oracle as orc
+        orc.set_threads(threads)
+        log("cpu baseline: oracle attention on %d threads, ~%.0f s" % (threads, args.cpu_seconds))
+        qh = ud.round_bf16(rng.standard_normal((T, D)).astype(np.float32))
+        kh = ud.round_bf16(rng.standard_normal((T, D)).astype(np.float32))
+        Ph = ud.round_bf16(rng.standard_normal((n_rel, D)).astype(np.float32))
+        uh = np.zeros((H, dk), np.float32)
+        rows, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds and rows < T:
+            sel = np.zeros((T, 2), np.int32)
+            sel[rows:rows + 64] = [0, int(lens[0])]
+            orc.relpos_attention(qh, kh, kh, Ph, uh, uh, sel, T - 1, H)
+            rows += 64
+        el = time.perf_counter() - t0
+        result["cpu_baseline"] = {"value": round(rows / el, 2), "unit": "frames/s (one layer, all heads)",
+                                  "cores": threads, "kind": "port",
+                                  "sample": "%d query frames of one %d-frame utterance (%d valid keys) in %.1f s"
+                                            % (rows, T, lens[0], el)}
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -207,6 +289,9 @@ def main():
         src.free(); dst.free()
     if args.workload == "decode":
         decode_bench(ud, args)
+        return
+    if args.workload == "offline":
+        offline_bench(ud, args)
         return
     wl = WORKLOADS[args.workload]
     S, T = wl["streams"], wl["T"]

@@ -143,6 +143,19 @@ UD_API int ud_relpos_attention(int32_t dtype, const void* q_dev, const void* k_d
                                int32_t H, int32_t dk, int32_t rel_offset, int32_t n_rel,
                                void* hip_stream);
 
+/* Replaces Step.relPosAttention (Ops.swift:80-90) on the offline path, forwardOffline
+ * (Sources/DictatorEngine/Models/FastConformer.swift:361-398): whole utterances, every frame a
+ * query over the same frames as keys (Tq = Tk = T), key ranges per query (chunked masks clipped to
+ * the valid length, or plain key padding), for a batch of B utterances:
+ *   q/k/v/out  bf16 [B, T, H*128]   P bf16 [n_rel, H*128] (rel -(T-1)..T-1 at rel_offset = T-1)
+ *   u/v        fp32 [H, 128]        ranges int32 [B, T, 2]
+ * Same formula and empty-range rule as ud_relpos_attention.  bf16 and head_dim 128 only.
+ * Asynchronous on hip_stream. */
+UD_API int ud_relpos_attention_batched(int32_t dtype, const void* q, const void* k, const void* v, const void* p,
+                                       const float* u, const float* vb, const int32_t* ranges, void* out,
+                                       int32_t B, int32_t T, int32_t H, int32_t dk, int32_t rel_offset,
+                                       int32_t n_rel, void* hip_stream);
+
 /* The streaming attention of one layer on its own, over the stream's ring caches: the fused
  * kernel the step runs between the QKV projection and linear_out (FastConformer.swift:285-291 with
  * the cache rule of :458-472).

@@ -66,6 +66,7 @@ def _sig(lib):
         "ud_stream_export_cache": (i, [p, _i32, f, f, f, ip]),
         "ud_stream_import_cache": (i, [p, _i32, f, f, f, _i32]),
         "ud_relpos_attention": (i, [_i32, p, p, p, p, p, p, p, p, _i32, _i32, _i32, _i32, _i32, _i32, p]),
+        "ud_relpos_attention_batched": (i, [_i32, p, p, p, p, p, p, p, p, _i32, _i32, _i32, _i32, _i32, _i32, p]),
         "ud_layer_attention": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, ip, p, p]),
         "ud_stream_advance": (i, [ctypes.POINTER(_vp), _i32, _i32]),
         "ud_time_layer_attention": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, p, _i32, p, f]),
@@ -389,6 +390,15 @@ def rel_pos_attention(q, k, v, pos_table, rel_offset, bias_u, bias_v, ranges, ou
     _check(lib().ud_relpos_attention(_DTYPES[dtype], q.ptr, k.ptr, v.ptr, pos_table.ptr, bias_u.ptr, bias_v.ptr,
                                      ranges.ptr, out.ptr, Tq, Tk, heads, head_dim, rel_offset, n_rel,
                                      hip_stream.ptr if hip_stream else None))
+
+
+def rel_pos_attention_batched(q, k, v, pos_table, rel_offset, bias_u, bias_v, ranges, out, B, T, heads,
+                              n_rel, head_dim=128, hip_stream=None):
+    """Offline relPosAttention over B whole utterances (bf16): q/k/v/out [B, T, H*128], pos_table
+    [n_rel, H*128], bias_u/bias_v fp32 [H, 128], ranges int32 [B, T, 2]."""
+    _check(lib().ud_relpos_attention_batched(UD_BF16, q.ptr, k.ptr, v.ptr, pos_table.ptr, bias_u.ptr, bias_v.ptr,
+                                             ranges.ptr, out.ptr, B, T, heads, head_dim, rel_offset, n_rel,
+                                             hip_stream.ptr if hip_stream else None))
 
 
 # ---------------------------------------------------------------- decoder attention (ud_decode.h)

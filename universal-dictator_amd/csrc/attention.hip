@@ -785,6 +785,243 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ offline (dense) MFMA kernel
+// Whole-utterance attention (the offline path's relpos_attention over T x T with per-query key
+// ranges; key padding and chunked masks are both ranges).  Flash-style: a workgroup of 8 wave64s
+// owns 128 queries of one (sequence, head) and sweeps 64-key tiles with an online softmax; each
+// wave owns 16 queries, all products on v_mfma_f32_16x16x32_bf16 with plain bf16 operands
+// (q+u, q+v and probabilities rounded to bf16: the errors average over the long key range).
+//   K and V tiles are staged in LDS (V^T for P.V through ds_read_b64_tr_b16);
+//   the positional band: tile t needs table rows rel = i - j over [i0 - 63 - 64t, i0 + 128 - 64t),
+//   three 64-row chunks; consecutive tiles share two of them, so LDS keeps a 3-chunk ring and each
+//   tile fetches one new chunk;
+//   bd tiles are computed per wave over its 80-row sub-band and gathered through LDS for the
+//   rel_shift (score (i, j) reads band row i - j + 63 of the wave's window);
+//   the next tile's K, V and band chunk are prefetched into registers during the current tile.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): this wave's LDS ops are done
+    __asm__ volatile("" ::: "memory");
+}
+
+__global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
+    using T = bf16;
+    constexpr int DK = 128, KT = 64, VST = DK + 8, NW = 8;
+    __shared__ __align__(16) bf16 kl[KT][VST];
+    __shared__ __align__(16) bf16 vl[KT][VST];
+    __shared__ __align__(16) bf16 pl[3 * KT][VST];
+    __shared__ __align__(16) float sw[NW][16][80];
+    __shared__ int kbound[2];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 15, g = lane >> 4;
+    const int Tn = a.T, D = a.H * DK, h = blockIdx.y, b = blockIdx.z;
+    const int i0 = blockIdx.x * 128, iw = i0 + 16 * wave;
+    const T* Q = static_cast<const T*>(a.q) + (int64_t)b * Tn * D + h * DK;
+    const T* K = static_cast<const T*>(a.k) + (int64_t)b * Tn * D + h * DK;
+    const T* V = static_cast<const T*>(a.v) + (int64_t)b * Tn * D + h * DK;
+    const T* P = static_cast<const T*>(a.P) + h * DK;
+    const int32_t* R = a.ranges + (int64_t)b * Tn * 2;
+
+    // ---- key range of the block: union of its queries' ranges
+    if (tid == 0) { kbound[0] = Tn; kbound[1] = 0; }
+    __syncthreads();
+    if (tid < 128 && i0 + tid < Tn) {
+        const int ks = max(R[2 * (i0 + tid)], 0), ke = min(R[2 * (i0 + tid) + 1], Tn);
+        if (ks < ke) { atomicMin(&kbound[0], ks); atomicMax(&kbound[1], ke); }
+    }
+    __syncthreads();
+    const int t_lo = kbound[0] / KT, t_hi = kbound[0] < kbound[1] ? (kbound[1] + KT - 1) / KT : t_lo;
+
+    // ---- the lane's 4 queries (rows 4g + r of the wave's 16) and their key ranges
+    int qks[4], qke[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int i = iw + 4 * g + r;
+        qks[r] = i < Tn ? max(R[2 * i], 0) : 0;
+        qke[r] = i < Tn ? min(R[2 * i + 1], Tn) : 0;
+    }
+    // ---- A operands: q + u, q + v in bf16 (query iw + col, k-chunk 4st + g)
+    uint4 aqu[4], aqv[4];
+    {
+        const T* qr = Q + (int64_t)min(iw + col, Tn - 1) * D;
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const int c = (4 * st + g) * 8;
+            float qf[8];
+            unpack16<T>(ld16(qr + c), qf);
+            const float4 u0 = *reinterpret_cast<const float4*>(a.u + h * DK + c);
+            const float4 u1 = *reinterpret_cast<const float4*>(a.u + h * DK + c + 4);
+            const float4 v0 = *reinterpret_cast<const float4*>(a.vb + h * DK + c);
+            const float4 v1 = *reinterpret_cast<const float4*>(a.vb + h * DK + c + 4);
+            const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+            const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            uint32_t pu[4], pv[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                pu[e / 2] = (uint32_t)f2bf(qf[e] + uu[e]) | ((uint32_t)f2bf(qf[e + 1] + uu[e + 1]) << 16);
+                pv[e / 2] = (uint32_t)f2bf(qf[e] + vv[e]) | ((uint32_t)f2bf(qf[e + 1] + vv[e + 1]) << 16);
+            }
+            aqu[st] = make_uint4(pu[0], pu[1], pu[2], pu[3]);
+            aqv[st] = make_uint4(pv[0], pv[1], pv[2], pv[3]);
+        }
+    }
+
+    // ---- tile loaders: 1024 16-byte pieces per 64-row tile, 2 per thread
+    auto load_rows = [&](const T* base, int r0, uint4 (&x)[2]) {
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int idx = tid + 512 * e, row = idx >> 4, cc = idx & 15;
+            x[e] = ld16(base + (int64_t)min(r0 + row, Tn - 1) * D + cc * 8);
+        }
+    };
+    auto load_chunk = [&](int k, uint4 (&x)[2]) {       // band chunk k: rel in [i0 - 63 - 64k, i0 + 1 - 64k)
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int idx = tid + 512 * e, row = idx >> 4, cc = idx & 15;
+            const int tr = min(max(i0 - 63 - 64 * k + row + a.rel_offset, 0), a.n_rel - 1);
+            x[e] = ld16(P + (int64_t)tr * D + cc * 8);
+        }
+    };
+    auto store_rows = [&](bf16 (*dst)[VST], const uint4 (&x)[2]) {
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int idx = tid + 512 * e, row = idx >> 4, cc = idx & 15;
+            *reinterpret_cast<uint4*>(&dst[row][cc * 8]) = x[e];
+        }
+    };
+    auto ring = [](int k) { return ((k % 3) + 3) % 3; };
+
+    float m[4], l[4];
+    f32x4_t oacc[8];
+#pragma unroll
+    for (int r = 0; r < 4; r++) { m[r] = -INFINITY; l[r] = 0.0f; }
+#pragma unroll
+    for (int dt = 0; dt < 8; dt++) oacc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    if (t_lo < t_hi) {                        // prologue: tile t_lo and its three band chunks
+        uint4 x[2];
+        load_rows(K, t_lo * KT, x); store_rows(kl, x);
+        load_rows(V, t_lo * KT, x); store_rows(vl, x);
+#pragma unroll
+        for (int c = 0; c < 3; c++) { load_chunk(t_lo - c, x); store_rows(&pl[ring(t_lo - c) * KT], x); }
+    }
+    for (int t = t_lo; t < t_hi; t++) {
+        const int j0 = t * KT;
+        uint4 nk[2], nv[2], np[2];
+        const bool more = t + 1 < t_hi;
+        if (more) { load_rows(K, j0 + KT, nk); load_rows(V, j0 + KT, nv); load_chunk(t + 1, np); }
+        __syncthreads();
+
+        // ---- ac: 4 key subtiles (lane: queries 4g.., key 16ts + col)
+        f32x4_t sacc[4];
+#pragma unroll
+        for (int ts = 0; ts < 4; ts++) {
+            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const uint4 bk = *reinterpret_cast<const uint4*>(&kl[16 * ts + col][(4 * st + g) * 8]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aqu[st]), as_bf16x8(bk), acc, 0, 0, 0);
+            }
+            sacc[ts] = acc;
+        }
+        // ---- bd over the wave's 80 band rows rel = iw - j0 - 63 + n (n < 80), gathered through LDS
+#pragma unroll
+        for (int tb = 0; tb < 5; tb++) {
+            const int rel = iw - j0 - 63 + 16 * tb + col;
+            const int x = i0 - rel;
+            const int k = x >= 0 ? x / 64 : -((-x + 63) / 64);
+            const int prow = ring(k) * KT + (rel - (i0 - 63 - 64 * k));
+            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                const uint4 bp = *reinterpret_cast<const uint4*>(&pl[prow][(4 * st + g) * 8]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aqv[st]), as_bf16x8(bp), acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) sw[wave][4 * g + r][16 * tb + col] = acc[r];
+        }
+        wave_lds_sync();
+
+        // ---- scores and the online softmax of the lane's 4 queries
+        float s[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++) {
+                const int j = j0 + 16 * ts + col;
+                const float x = (sacc[ts][r] + sw[wave][4 * g + r][4 * g + r - 16 * ts - col + 63]) * a.scale;
+                s[ts][r] = (j >= qks[r] && j < qke[r]) ? x : -INFINITY;
+                mx = fmaxf(mx, s[ts][r]);
+            }
+            mx = group_max<16>(mx);
+            const float nm = fmaxf(m[r], mx);
+            const float corr = nm == -INFINITY ? 1.0f : __expf(m[r] - nm);
+            float ps = 0.0f;
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++) {
+                s[ts][r] = s[ts][r] == -INFINITY ? 0.0f : __expf(s[ts][r] - nm);
+                ps += s[ts][r];
+            }
+            l[r] = l[r] * corr + group_sum<16>(ps);
+            m[r] = nm;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) oacc[dt][r] *= corr;
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++) sw[wave][4 * g + r][16 * ts + col] = s[ts][r];
+        wave_lds_sync();
+
+        // ---- P.V: A = probabilities (query col, keys 32kk + 8g ..), B = V^T by transposed LDS reads
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            const float4 p0 = *reinterpret_cast<const float4*>(&sw[wave][col][32 * kk + 8 * g]);
+            const float4 p1 = *reinterpret_cast<const float4*>(&sw[wave][col][32 * kk + 8 * g + 4]);
+            const uint4 pa = make_uint4((uint32_t)f2bf(p0.x) | ((uint32_t)f2bf(p0.y) << 16),
+                                        (uint32_t)f2bf(p0.z) | ((uint32_t)f2bf(p0.w) << 16),
+                                        (uint32_t)f2bf(p1.x) | ((uint32_t)f2bf(p1.y) << 16),
+                                        (uint32_t)f2bf(p1.z) | ((uint32_t)f2bf(p1.w) << 16));
+            const int k0 = 32 * kk + 8 * g + (col >> 2);
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const int c0 = 16 * dt + 4 * (col & 3);
+                const v4i16_t b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vl[k0][c0]);
+                const v4i16_t b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vl[k0 + 4][c0]);
+                uint4 bv;
+                __builtin_memcpy(&bv.x, &b0, 8);
+                __builtin_memcpy(&bv.z, &b1, 8);
+                oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pa), as_bf16x8(bv), oacc[dt], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+        if (more) {
+            store_rows(kl, nk);
+            store_rows(vl, nv);
+            store_rows(&pl[ring(t + 1) * KT], np);
+        }
+    }
+
+    // ---- output: out[iw + 4g + r][16dt + col] (0 for an empty key range)
+    T* O = static_cast<T*>(a.out) + (int64_t)b * Tn * D + h * DK;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int i = iw + 4 * g + r;
+        if (i < Tn) {
+            const float inv = l[r] > 0.0f ? 1.0f / l[r] : 0.0f;
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) O[(int64_t)i * D + 16 * dt + col] = f2bf(oacc[dt][r] * inv);
+        }
+    }
+}
+
+int launch_relpos_dense(const DenseArgs& a, hipStream_t st) {
+    if (a.B < 1 || a.T < 1 || a.H < 1) return -2;
+    hipLaunchKernelGGL(relpos_dense_kernel, dim3((a.T + 127) / 128, a.H, a.B), dim3(512), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // ------------------------------------------------------------------ launchers
 
 // Keys per block: as many as keep the workgroup's LDS under 64 KB.

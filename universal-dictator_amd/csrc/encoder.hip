@@ -776,6 +776,23 @@ extern "C" UD_API int ud_stream_import_cache(ud_stream* s, int32_t layer, const 
 
 // ---------------------------------------------------------------- single-op entry
 
+extern "C" UD_API int ud_relpos_attention_batched(int32_t dtype, const void* q, const void* k, const void* v,
+                                                  const void* p, const float* u, const float* vb,
+                                                  const int32_t* ranges, void* out, int32_t B, int32_t T, int32_t H,
+                                                  int32_t dk, int32_t rel_offset, int32_t n_rel, void* hip_stream) {
+    if (!q || !k || !v || !p || !u || !vb || !ranges || !out) return fail(UD_ERR_INVALID, "ud_relpos_attention_batched: null pointer");
+    if (dtype != UD_BF16) return fail(UD_ERR_INVALID, "ud_relpos_attention_batched: bf16 only");
+    if (dk != 128) return fail(UD_ERR_SHAPE, "ud_relpos_attention_batched: head_dim %d (128 supported)", dk);
+    if (B < 1 || T < 1 || H < 1 || n_rel < 1) return fail(UD_ERR_SHAPE, "ud_relpos_attention_batched: bad sizes");
+    const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)p | (uintptr_t)u | (uintptr_t)vb;
+    if (al % 16 != 0) return fail(UD_ERR_INVALID, "ud_relpos_attention_batched: pointers must be 16-byte aligned");
+    DenseArgs a{};
+    a.q = q; a.k = k; a.v = v; a.P = p; a.u = u; a.vb = vb; a.ranges = ranges; a.out = out;
+    a.B = B; a.T = T; a.H = H; a.rel_offset = rel_offset; a.n_rel = n_rel;
+    a.scale = 1.0f / sqrtf((float)dk);
+    return launch_status(launch_relpos_dense(a, static_cast<hipStream_t>(hip_stream)), "offline relpos attention");
+}
+
 extern "C" UD_API int ud_relpos_attention(int32_t dtype, const void* q, const void* k, const void* v, const void* p,
                                           const float* u, const float* vb, const int32_t* ranges, void* out,
                                           int32_t Tq, int32_t Tk, int32_t H, int32_t dk, int32_t rel_offset,

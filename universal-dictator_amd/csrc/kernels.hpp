@@ -24,6 +24,17 @@ struct OpArgs {
 };
 int launch_relpos_op(const OpArgs& a, bool bf16_data, hipStream_t st);
 
+// Offline (whole-utterance) rel-pos attention over a batch of B sequences of T frames, bf16,
+// head_dim 128: q/k/v/out [B][T][H*128], P [n_rel][H*128], ranges int32 [B][T][2].
+struct DenseArgs {
+    const void* q; const void* k; const void* v; const void* P;
+    const float* u; const float* vb; const int32_t* ranges;
+    void* out;
+    int B, T, H, rel_offset, n_rel;
+    float scale;
+};
+int launch_relpos_dense(const DenseArgs& a, hipStream_t st);
+
 struct RingArgs {
     void* kring; void* vring;       // layer base of the pool: [slots][H][L][128]
     const void* qkv;                // [n*T, 3*D]
