@@ -351,6 +351,12 @@ def main():
     attn_bytes = S * Tk * H * dk * 2 * 2 + S * 2 * T * H * dk * 2 + n_rel * H * dk * 2 + 2 * H * dk * 4
     achieved = attn_bytes / (attn_ms / 1000.0) / 1e9
     log("attention kernel: %.2f us/launch, %.0f GB/s" % (attn_ms * 1000.0, achieved))
+    floor_ms = None
+    if T <= 2:
+        # the same loads with no arithmetic: what memory alone costs for this launch shape
+        floor_ms = enc.time_ring_read_floor(streams, T, 0, qkv, att, args.attn_iters, hip_stream=hs)
+        log("read floor of the same access pattern: %.2f us/launch, %.0f GB/s"
+            % (floor_ms * 1000.0, attn_bytes / (floor_ms / 1000.0) / 1e9))
 
     result = {
         "metric": "aggregate audio-sec/sec at 64 streams; attention-kernel % of HBM roofline",
@@ -384,6 +390,8 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": read_traffic("relpos_ring_%s" % args.workload),
             "algorithmic_bytes_per_launch": attn_bytes,
+            "read_floor_us": round(floor_ms * 1000.0, 3) if floor_ms else None,
+            "read_floor_frac": round(attn_bytes / (floor_ms / 1000.0) / 1e9 / HBM_PEAK_GBS, 4) if floor_ms else None,
         },
     }
     enc.close()

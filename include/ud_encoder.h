@@ -184,6 +184,15 @@ UD_API int ud_time_layer_attention(ud_encoder* enc, ud_stream* const* streams, i
                                    int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
                                    void* hip_stream, float* avg_ms);
 
+/* Profiling hook (no reference counterpart): like ud_time_layer_attention, but each launch is a
+ * kernel that performs only the loads of the bf16 streaming attention kernel (same grid, same
+ * addresses, no arithmetic and no stores to the rings) -- the memory floor that kernel is measured
+ * against.  bf16 encoders, T <= 2, L + T <= 80.  att_dev may be written with garbage.  Synchronizes
+ * hip_stream. */
+UD_API int ud_time_ring_read_floor(ud_encoder* enc, ud_stream* const* streams, int32_t n, int32_t T,
+                                   int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
+                                   void* hip_stream, float* avg_ms);
+
 #ifdef __cplusplus
 }
 #endif

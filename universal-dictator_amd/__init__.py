@@ -70,6 +70,7 @@ def _sig(lib):
         "ud_layer_attention": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, ip, p, p]),
         "ud_stream_advance": (i, [ctypes.POINTER(_vp), _i32, _i32]),
         "ud_time_layer_attention": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, p, _i32, p, f]),
+        "ud_time_ring_read_floor": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, p, _i32, p, f]),
         "ud_device_count": (i, [ip]),
         "ud_device_arch": (i, [ctypes.c_char_p, _i32]),
         "ud_malloc": (i, [ctypes.POINTER(_vp), ctypes.c_size_t]),
@@ -364,6 +365,14 @@ class Encoder:
         from HIP events on hip_stream."""
         ms = ctypes.c_float(0)
         _check(_lib.ud_time_layer_attention(self.handle, _handles(streams), len(streams), T, layer, qkv.ptr, att.ptr,
+                                            iters, hip_stream.ptr if hip_stream else None, ctypes.byref(ms)))
+        return ms.value
+
+    def time_ring_read_floor(self, streams, T, layer, qkv, att, iters, hip_stream=None):
+        """Average duration (ms) of a kernel that performs only the attention kernel's loads (bf16,
+        T <= 2): the memory floor of that access pattern."""
+        ms = ctypes.c_float(0)
+        _check(_lib.ud_time_ring_read_floor(self.handle, _handles(streams), len(streams), T, layer, qkv.ptr, att.ptr,
                                             iters, hip_stream.ptr if hip_stream else None, ctypes.byref(ms)))
         return ms.value
 

@@ -664,24 +664,26 @@ extern "C" UD_API int ud_layer_attention(ud_encoder* e, ud_stream* const* stream
                          "relpos attention");
 }
 
-extern "C" UD_API int ud_time_layer_attention(ud_encoder* e, ud_stream* const* streams, int32_t n, int32_t T,
-                                              int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
-                                              void* hip_stream, float* avg_ms) {
-    int rc = check_layer_call(e, streams, n, T, layer, qkv_dev, att_dev, "ud_time_layer_attention");
+// Launches `iters` kernels back to back between two HIP events, launch i on layer
+// (layer + 1 + i) % layers, and returns the average time per launch.
+template <typename Launch>
+static int time_layers(ud_encoder* e, ud_stream* const* streams, int32_t n, int32_t T, int32_t layer,
+                       const void* qkv_dev, void* att_dev, int32_t iters, void* hip_stream, float* avg_ms,
+                       const char* what, Launch launch) {
+    int rc = check_layer_call(e, streams, n, T, layer, qkv_dev, att_dev, what);
     if (rc != UD_OK) return rc;
-    if (iters < 1 || !avg_ms) return fail(UD_ERR_INVALID, "ud_time_layer_attention: bad iters / output");
+    if (iters < 1 || !avg_ms) return fail(UD_ERR_INVALID, "%s: bad iters / output", what);
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     if ((rc = upload_desc(e, streams, n, T, nullptr, st)) != UD_OK) return rc;
     hipEvent_t ev[2];
     HIPC(hipEventCreate(&ev[0]));
     HIPC(hipEventCreate(&ev[1]));
-    // Launch i uses layer (layer + i) % layers, so the caches come from HBM as in a real step
+    // Launch i uses layer (layer + 1 + i) % layers, so the caches come from HBM as in a real step
     // (one layer's rings would otherwise stay in the 256 MB last-level cache across launches).
-    rc = launch_status(launch_relpos_ring(ring_args(e, n, T, layer, qkv_dev, att_dev), e->bf, st), "relpos attention");
+    rc = launch_status(launch(ring_args(e, n, T, layer, qkv_dev, att_dev), st), what);
     if (rc == UD_OK && hipEventRecord(ev[0], st) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventRecord failed");
     for (int i = 0; rc == UD_OK && i < iters; i++)
-        rc = launch_status(launch_relpos_ring(ring_args(e, n, T, (layer + 1 + i) % e->layers, qkv_dev, att_dev), e->bf, st),
-                           "relpos attention");
+        rc = launch_status(launch(ring_args(e, n, T, (layer + 1 + i) % e->layers, qkv_dev, att_dev), st), what);
     if (rc == UD_OK && hipEventRecord(ev[1], st) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventRecord failed");
     float ms = 0.0f;
     if (rc == UD_OK && hipEventSynchronize(ev[1]) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventSynchronize failed");
@@ -690,6 +692,21 @@ extern "C" UD_API int ud_time_layer_attention(ud_encoder* e, ud_stream* const* s
     (void)hipEventDestroy(ev[1]);
     if (rc == UD_OK) *avg_ms = ms / (float)iters;
     return rc;
+}
+
+extern "C" UD_API int ud_time_layer_attention(ud_encoder* e, ud_stream* const* streams, int32_t n, int32_t T,
+                                              int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
+                                              void* hip_stream, float* avg_ms) {
+    return time_layers(e, streams, n, T, layer, qkv_dev, att_dev, iters, hip_stream, avg_ms, "ud_time_layer_attention",
+                       [e](const RingArgs& a, hipStream_t st) { return launch_relpos_ring(a, e->bf, st); });
+}
+
+extern "C" UD_API int ud_time_ring_read_floor(ud_encoder* e, ud_stream* const* streams, int32_t n, int32_t T,
+                                              int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
+                                              void* hip_stream, float* avg_ms) {
+    if (e && !e->bf) return fail(UD_ERR_INVALID, "ud_time_ring_read_floor: bf16 encoders only");
+    return time_layers(e, streams, n, T, layer, qkv_dev, att_dev, iters, hip_stream, avg_ms, "ud_time_ring_read_floor",
+                       [](const RingArgs& a, hipStream_t st) { return launch_ring_read_floor(a, st); });
 }
 
 extern "C" UD_API int ud_stream_advance(ud_stream* const* streams, int32_t n, int32_t T) {

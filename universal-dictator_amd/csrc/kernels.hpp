@@ -47,6 +47,8 @@ struct RingArgs {
     int att_frag;
 };
 int launch_relpos_ring(const RingArgs& a, bool bf16_data, hipStream_t st);
+// Read floor of the bf16 streaming kernel (chunks of <= 2 frames, L + T <= 80): its loads only.
+int launch_ring_read_floor(const RingArgs& a, hipStream_t st);
 
 // ---------------------------------------------------------------- fragment-major layout
 // bf16 GEMM operands live in HBM in the order the v_mfma_f32_16x16x32_bf16 lanes consume them:
