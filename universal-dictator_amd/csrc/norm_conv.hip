@@ -28,18 +28,27 @@ __device__ __forceinline__ void ln_row_stats(const float4 (&x)[NPER], int D, flo
     rstd = 1.0f / sqrtf(wave_sum(v) / (float)D + LN_EPS);
 }
 
+// gamma / beta of this lane's columns, loaded up front (independent of the row data)
 template <int NPER>
-__device__ __forceinline__ void ln_apply(float4 (&x)[NPER], const float* g, const float* b, float mean, float rstd,
-                                         int lane, int act) {
+__device__ __forceinline__ void ln_params(float4 (&gg)[NPER], float4 (&bb)[NPER], const float* __restrict__ g,
+                                          const float* __restrict__ b, int lane) {
 #pragma unroll
     for (int p = 0; p < NPER; p++) {
         const int c = (p * 64 + lane) * 4;
-        float4 gg = *reinterpret_cast<const float4*>(g + c);
-        float4 bb = *reinterpret_cast<const float4*>(b + c);
-        x[p].x = apply_act((x[p].x - mean) * rstd * gg.x + bb.x, act);
-        x[p].y = apply_act((x[p].y - mean) * rstd * gg.y + bb.y, act);
-        x[p].z = apply_act((x[p].z - mean) * rstd * gg.z + bb.z, act);
-        x[p].w = apply_act((x[p].w - mean) * rstd * gg.w + bb.w, act);
+        gg[p] = *reinterpret_cast<const float4*>(g + c);
+        bb[p] = *reinterpret_cast<const float4*>(b + c);
+    }
+}
+
+template <int NPER>
+__device__ __forceinline__ void ln_apply(float4 (&x)[NPER], const float4 (&gg)[NPER], const float4 (&bb)[NPER],
+                                         float mean, float rstd, int act) {
+#pragma unroll
+    for (int p = 0; p < NPER; p++) {
+        x[p].x = apply_act((x[p].x - mean) * rstd * gg[p].x + bb[p].x, act);
+        x[p].y = apply_act((x[p].y - mean) * rstd * gg[p].y + bb[p].y, act);
+        x[p].z = apply_act((x[p].z - mean) * rstd * gg[p].z + bb[p].z, act);
+        x[p].w = apply_act((x[p].w - mean) * rstd * gg[p].w + bb[p].w, act);
     }
 }
 
@@ -64,56 +73,76 @@ __device__ __forceinline__ void store_row(void* out, bool bf, int64_t row, int D
     }
 }
 
-// v = row of x plus the pending split-K residual slabs, added in slab order.
-template <int NPER>
-__device__ __forceinline__ void load_row(float4 (&v)[NPER], const float* x, Partials parts, int64_t row, int rows,
-                                         int D, int lane) {
+// v = row of x plus the pending split-K residual slabs, added in slab order.  NP = number of slabs
+// known at compile time (all loads issued before the first add), or -1 for a count known only at
+// run time.
+template <int NPER, int NP>
+__device__ __forceinline__ void load_row(float4 (&v)[NPER], const float* __restrict__ x, Partials parts, int64_t row,
+                                         int rows, int D, int lane) {
 #pragma unroll
     for (int p = 0; p < NPER; p++) v[p] = *reinterpret_cast<const float4*>(x + row * D + (p * 64 + lane) * 4);
-    for (int j = 0; j < parts.n; j++) {
-        const float* pj = parts.p + ((int64_t)j * rows + row) * D;
+    if constexpr (NP > 0) {
+        float4 q[NP][NPER];
 #pragma unroll
-        for (int p = 0; p < NPER; p++) {
-            const float4 q = *reinterpret_cast<const float4*>(pj + (p * 64 + lane) * 4);
-            v[p].x += q.x; v[p].y += q.y; v[p].z += q.z; v[p].w += q.w;
+        for (int j = 0; j < NP; j++)
+#pragma unroll
+            for (int p = 0; p < NPER; p++)
+                q[j][p] = *reinterpret_cast<const float4*>(parts.p + ((int64_t)j * rows + row) * D + (p * 64 + lane) * 4);
+#pragma unroll
+        for (int j = 0; j < NP; j++)
+#pragma unroll
+            for (int p = 0; p < NPER; p++) { v[p].x += q[j][p].x; v[p].y += q[j][p].y; v[p].z += q[j][p].z; v[p].w += q[j][p].w; }
+    } else if constexpr (NP < 0) {
+        for (int j = 0; j < parts.n; j++) {
+            const float* pj = parts.p + ((int64_t)j * rows + row) * D;
+#pragma unroll
+            for (int p = 0; p < NPER; p++) {
+                const float4 q = *reinterpret_cast<const float4*>(pj + (p * 64 + lane) * 4);
+                v[p].x += q.x; v[p].y += q.y; v[p].z += q.z; v[p].w += q.w;
+            }
         }
     }
 }
 
-template <int NPER>
-__global__ __launch_bounds__(256) void layernorm_kernel(float* x, Partials parts, const float* g, const float* b,
-                                                        void* out, int out_bf16, int rows, int D, int act) {
+template <int NPER, int NP>
+__global__ __launch_bounds__(256) void layernorm_kernel(float* x, Partials parts, const float* __restrict__ g,
+                                                        const float* __restrict__ b, void* out, int out_bf16, int rows,
+                                                        int D, int act) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
-    float4 v[NPER];
-    load_row(v, x, parts, row, rows, D, lane);
-    if (parts.n > 0) store_row(x, false, row, D, v, lane);
+    float4 v[NPER], gg[NPER], bb[NPER];
+    ln_params(gg, bb, g, b, lane);
+    load_row<NPER, NP>(v, x, parts, row, rows, D, lane);
+    if (NP != 0 && parts.n > 0) store_row(x, false, row, D, v, lane);
     float mean, rstd;
     ln_row_stats(v, D, mean, rstd);
-    ln_apply(v, g, b, mean, rstd, lane, act);
+    ln_apply(v, gg, bb, mean, rstd, act);
     store_row(out, out_bf16 != 0, row, D, v, lane);
 }
 
 // res <- LN_a(src) (copy when ga is null), z <- LN_b(res).  Joins one layer's norm_out with the
 // next layer's norm_feed_forward1 (FastConformer.swift:320 then :277).
-template <int NPER>
-__global__ __launch_bounds__(256) void layernorm2_kernel(const float* src, Partials parts, float* res, const float* ga,
-                                                         const float* ba, const float* gb, const float* bb, void* z,
-                                                         int z_bf16, int rows, int D) {
+template <int NPER, int NP>
+__global__ __launch_bounds__(256) void layernorm2_kernel(const float* src, Partials parts, float* res,
+                                                         const float* __restrict__ ga, const float* __restrict__ ba,
+                                                         const float* __restrict__ gb, const float* __restrict__ bb,
+                                                         void* z, int z_bf16, int rows, int D) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
-    float4 v[NPER];
-    load_row(v, src, parts, row, rows, D, lane);
+    float4 v[NPER], g1[NPER], b1[NPER], g2[NPER], b2[NPER];
+    if (ga != nullptr) ln_params(g1, b1, ga, ba, lane);
+    ln_params(g2, b2, gb, bb, lane);
+    load_row<NPER, NP>(v, src, parts, row, rows, D, lane);
     float mean, rstd;
     if (ga != nullptr) {
         ln_row_stats(v, D, mean, rstd);
-        ln_apply(v, ga, ba, mean, rstd, lane, ACT_NONE);
+        ln_apply(v, g1, b1, mean, rstd, ACT_NONE);
     }
     store_row(res, false, row, D, v, lane);
     ln_row_stats(v, D, mean, rstd);
-    ln_apply(v, gb, bb, mean, rstd, lane, ACT_NONE);
+    ln_apply(v, g2, b2, mean, rstd, ACT_NONE);
     store_row(z, z_bf16 != 0, row, D, v, lane);
 }
 
@@ -234,19 +263,36 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
 
 // ---------------------------------------------------------------- launchers
 
+template <int NPER>
+static void ln_dispatch(dim3 grid, dim3 block, hipStream_t st, float* x, Partials parts, const float* g, const float* b,
+                        void* out, int ob, int rows, int D, int act) {
+    if (parts.n == 0) hipLaunchKernelGGL((layernorm_kernel<NPER, 0>), grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act);
+    else if (parts.n == 4) hipLaunchKernelGGL((layernorm_kernel<NPER, 4>), grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act);
+    else hipLaunchKernelGGL((layernorm_kernel<NPER, -1>), grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act);
+}
+
 int launch_layernorm(float* x, Partials parts, const float* g, const float* b, void* out, bool out_bf16, int rows,
                      int D, int act, hipStream_t st) {
     if (rows <= 0) return 0;
     dim3 grid((rows + 3) / 4), block(256);
     const int ob = out_bf16 ? 1 : 0;
     switch (D) {
-        case 256: hipLaunchKernelGGL(layernorm_kernel<1>, grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act); break;
-        case 512: hipLaunchKernelGGL(layernorm_kernel<2>, grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act); break;
-        case 1024: hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act); break;
-        case 2048: hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act); break;
+        case 256: ln_dispatch<1>(grid, block, st, x, parts, g, b, out, ob, rows, D, act); break;
+        case 512: ln_dispatch<2>(grid, block, st, x, parts, g, b, out, ob, rows, D, act); break;
+        case 1024: ln_dispatch<4>(grid, block, st, x, parts, g, b, out, ob, rows, D, act); break;
+        case 2048: ln_dispatch<8>(grid, block, st, x, parts, g, b, out, ob, rows, D, act); break;
         default: return -2;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <int NPER>
+static void ln2_dispatch(dim3 grid, dim3 block, hipStream_t st, const float* src, Partials parts, float* res,
+                         const float* ga, const float* ba, const float* gb, const float* bb, void* z, int zb, int rows,
+                         int D) {
+    if (parts.n == 0) hipLaunchKernelGGL((layernorm2_kernel<NPER, 0>), grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D);
+    else if (parts.n == 4) hipLaunchKernelGGL((layernorm2_kernel<NPER, 4>), grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D);
+    else hipLaunchKernelGGL((layernorm2_kernel<NPER, -1>), grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D);
 }
 
 int launch_layernorm2(const float* src, Partials parts, float* res, const float* ga, const float* ba, const float* gb,
@@ -255,10 +301,10 @@ int launch_layernorm2(const float* src, Partials parts, float* res, const float*
     dim3 grid((rows + 3) / 4), block(256);
     const int zb = z_bf16 ? 1 : 0;
     switch (D) {
-        case 256: hipLaunchKernelGGL(layernorm2_kernel<1>, grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
-        case 512: hipLaunchKernelGGL(layernorm2_kernel<2>, grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
-        case 1024: hipLaunchKernelGGL(layernorm2_kernel<4>, grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
-        case 2048: hipLaunchKernelGGL(layernorm2_kernel<8>, grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
+        case 256: ln2_dispatch<1>(grid, block, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
+        case 512: ln2_dispatch<2>(grid, block, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
+        case 1024: ln2_dispatch<4>(grid, block, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
+        case 2048: ln2_dispatch<8>(grid, block, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
         default: return -2;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
