@@ -108,9 +108,6 @@ struct LayerDev {
     uint32_t set_mask = 0;
 };
 
-// K splits of the bf16 residual projections (when K allows; see launch_gemm).
-constexpr int KSPLIT = 4;
-
 struct GraphEntry {
     int n, T;
     const void* x;
@@ -536,7 +533,7 @@ static int enqueue_step(ud_encoder* e, int n, int T, const float* x, float* out,
         GemmArgs g{};
         g.A = A; g.W = W; g.C = e->part; g.M = M; g.N = D; g.K = K; g.lda = K; g.ldw = K; g.ldc = D;
         g.epi = EPI_PARTIAL; g.act = ACT_NONE; g.out_scale = scale;
-        g.ksplit = K % (128 * KSPLIT) == 0 ? KSPLIT : 1;
+        g.ksplit = gemm_partial_splits(M, D, K, bf);
         pend.n = g.ksplit;
         return launch_status(launch_gemm(g, bf, st), what);
     };

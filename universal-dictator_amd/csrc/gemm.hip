@@ -165,6 +165,181 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- bf16, many rows (LDS-staged)
+// For M in the thousands (256 streams x 14 frames = 3584 rows) the projections are MFMA-bound, and
+// the register-direct kernel above would re-read each activation fragment once per 16-column tile.
+// Here a workgroup of 8 waves (2 per SIMD, so one wave's MFMAs run while the other waits on LDS)
+// owns a 256 x 64*NT output tile.  Per 64-wide K chunk it copies the 16 row fragments and 4*NT
+// column fragments (each a contiguous 2 KB block in the fragment-major layout, so the copy is
+// linear) into one of two LDS buffers with direct global -> LDS loads (global_load_lds_dwordx4,
+// no staging registers), while the waves multiply out of the other buffer.  Phases per chunk c:
+//   P1  8 MFMAs on half 0 of c (read in the previous iteration); LDS reads of half 1 of c; direct
+//       loads of chunk c+1 into the other buffer
+//   P2  the remaining MFMAs on half 0
+//   P3  MFMAs on half 1, first half of the columns
+//   P4  wait for this wave's direct loads; barrier: chunk c+1 is in LDS, all waves are done with c
+//   P5  LDS reads of half 0 of chunk c+1
+//   P6  MFMAs on half 1, second half of the columns (hides P5)
+// The buffer written in P1 was last read in the previous iteration, before its barrier.  The LDS
+// reads of half 1 are issued before the direct loads because the compiler cannot tell the two
+// buffers apart and would otherwise wait for the direct loads first.
+//
+// The MFMAs are inline asm with the accumulators pinned in place in the accumulator registers:
+// compiled from the builtin, the register allocator copied part of the accumulator between
+// register files every chunk, each copy waiting for an MFMA result (measured: a single wave then
+// issues an MFMA every ~32 cycles instead of ~20).  The compiler's hazard checks do not see inside
+// the asm, so the required wait states are explicit at the two points where compiled code touches
+// the accumulators; empty asm statements pin the zeroing before, and the epilogue's reads after,
+// those waits.
+
+// 16 bytes per lane from global memory straight into LDS at dst + 16 * lane (dst wave-uniform).
+// (A plain function: inside a lambda of a kernel template the host pass drops the kernel's stub.)
+__device__ __forceinline__ void lds_direct16(const bf16* src, bf16* dst) {
+    __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+
+template <int NT, int MT>
+__device__ __forceinline__ void pin_acc(f32x4_t (&acc)[NT][MT]) {
+#pragma unroll
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+        for (int i = 0; i < MT; i++) asm volatile("" : "+a"(acc[j][i]));
+}
+
+// SiLU for epilogues that round to bf16: v_exp_f32 and v_rcp_f32 (about 1 ulp of fp32 each) in
+// place of expf and an IEEE divide; exact 0 / x limits for large |x|.
+__device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+template <int ACT>
+__device__ __forceinline__ float act_fast(float x) {
+    if constexpr (ACT == ACT_SILU) return silu_fast(x);
+    else return apply_act(x, ACT);
+}
+
+// Waves form a 2 x 4 grid; each owns 128 x 16*NT (NT = 4: 128 pinned accumulator registers;
+// with about 120 vector registers two waves fit per SIMD).  Narrower tiles (NT 3, 2) give more
+// workgroups where 256 x 256 tiles would leave CUs idle.  The MFMA operands are swapped (weights as
+// the row operand), so each 16 x 16 accumulator holds C^T: a lane has 4 consecutive output columns
+// of one row, and the epilogue writes 16 bytes (fp32) or 8 bytes (bf16, row-major or
+// fragment-major) per lane.
+template <int NT, int EPI, int ACT>
+__global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
+    constexpr int MT = 8, BB = 4 * NT;                       // W blocks (16 columns each) per tile
+    constexpr int STAGE = (16 + BB) * 1024, CPW = 4 + NT;    // CPW: 1 KB copies per wave per chunk
+    __shared__ __attribute__((aligned(16))) bf16 lds[2 * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int nN = a.N / (64 * NT), nM = (a.M + 255) / 256;
+    const int ks = a.ksplit;
+    const int t = xcd_tile(blockIdx.x, nN * nM * ks);
+    const int kz = t % ks, tile = t / ks;
+    const int mb = tile / nN, nb = tile % nN;
+    const int nk = a.K / 64, kper = nk / ks, kc0 = kz * kper;
+    const int rtiles = (a.M + 15) / 16;
+    const bf16* A = static_cast<const bf16*>(a.A);
+    const bf16* W = static_cast<const bf16*>(a.W);
+
+    // Wave w copies the 1 KB half-blocks u = w + 8j (j < CPW): A's row tiles for u < 32 (j < 4).
+    int soff[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; j++) {
+        const int u = wave + 8 * j, b = u >> 1, hb = u & 1;
+        int o;
+        if (b < 16) o = ((min(mb * 16 + b, rtiles - 1) * nk + kc0) << 10) + hb * 512;   // clamped rows: not stored
+        else o = (((nb * BB + b - 16) * nk + kc0) << 10) + hb * 512;
+        soff[j] = o;
+    }
+    const int lo = lane * 8;
+    auto copy_chunk = [&](int c, bf16* dst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < CPW; j++)
+            lds_direct16((j < 4 ? A : W) + soff[j] + (c << 10) + lo, dst + wave * 512 + j * 4096);
+    };
+
+    f32x4_t acc[NT][MT];
+#pragma unroll
+    for (int j = 0; j < NT; j++)
+#pragma unroll
+        for (int i = 0; i < MT; i++) acc[j][i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int aoff = (wm * MT) * 1024 + lo, boff = (16 + wn * NT) * 1024 + lo;
+    uint4 fa0[MT], fb0[NT], fa1[MT], fb1[NT];
+    auto read_half = [&](const bf16* buf, int h, uint4 (&fa)[MT], uint4 (&fb)[NT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MT; i++) fa[i] = *reinterpret_cast<const uint4*>(buf + aoff + i * 1024 + h * 512);
+#pragma unroll
+        for (int j = 0; j < NT; j++) fb[j] = *reinterpret_cast<const uint4*>(buf + boff + j * 1024 + h * 512);
+    };
+    auto mma = [&](const uint4 (&fa)[MT], const uint4 (&fb)[NT], int j0, int j1) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = j0; j < j1; j++)
+#pragma unroll
+            for (int i = 0; i < MT; i++)
+                asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                             : "+a"(acc[j][i]) : "v"(as_bf16x8(fb[j])), "v"(as_bf16x8(fa[i])));
+    };
+    copy_chunk(0, lds);
+    __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0): this wave's direct loads landed
+    __syncthreads();
+    read_half(lds, 0, fa0, fb0);
+    pin_acc(acc);
+    asm volatile("s_nop 7");                                 // accumulator zeroing -> first MFMA
+    for (int c = 0; c < kper; c++) {
+        const bf16* buf = lds + (c & 1) * STAGE;
+        bf16* nbuf = lds + ((c + 1) & 1) * STAGE;
+        const bool more = c + 1 < kper;
+        mma(fa0, fb0, 0, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        read_half(buf, 1, fa1, fb1);
+        if (more) copy_chunk(c + 1, nbuf);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fa0, fb0, 1, NT);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fa1, fb1, 0, NT / 2);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+            read_half(nbuf, 0, fa0, fb0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fa1, fb1, NT / 2, NT);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7");   // last MFMA results -> epilogue reads
+    pin_acc(acc);
+
+    // acc[j][i] is tile (column tile j, row tile i) transposed: lane holds row 16*rt + r16 and the
+    // 4 columns 16*ct + 4*g + e (e < 4).
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+        const int64_t m = (int64_t)(mb * 16 + wm * MT + i) * 16 + r16;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            const int n = (nb * BB + wn * NT + j) * 16 + g * 4;
+            const f32x4_t v = acc[j][i];
+            if constexpr (EPI == EPI_PARTIAL) {
+                *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.C) + ((int64_t)kz * a.M + m) * a.ldc + n) =
+                    v * a.out_scale;
+            } else if constexpr (EPI == EPI_STORE_F32) {
+                f32x4_t o;
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] = apply_act(v[e], ACT) * a.out_scale;
+                *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.C) + m * a.ldc + n) = o;
+            } else {
+                uint2 o;
+                o.x = (uint32_t)f2bf(act_fast<ACT>(v[0]) * a.out_scale) | ((uint32_t)f2bf(act_fast<ACT>(v[1]) * a.out_scale) << 16);
+                o.y = (uint32_t)f2bf(act_fast<ACT>(v[2]) * a.out_scale) | ((uint32_t)f2bf(act_fast<ACT>(v[3]) * a.out_scale) << 16);
+                bf16* dst = static_cast<bf16*>(a.C) + (EPI == EPI_STORE_FRAG ? frag_index(m, n, a.N / 64) : m * a.ldc + n);
+                *reinterpret_cast<uint2*>(dst) = o;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- fp32 (VALU) GEMM
 // 64x64 tiles, 256 threads with 4x4 outputs each, K staged through LDS in slices of 16.
 constexpr int F_BM = 64, F_BN = 64, F_BK = 16;
@@ -224,6 +399,79 @@ static int launch_bf16_cfg(GemmArgs a, int ksplit, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+template <int NT, int EPI, int ACT>
+static int launch_lds_cfg(GemmArgs a, int ksplit, hipStream_t st) {
+    if (a.N % (64 * NT) != 0 || ksplit < 1 || a.K % (64 * ksplit) != 0 || a.ldc % 4 != 0) return -2;
+    if (ksplit > 1 && EPI != EPI_PARTIAL) return -2;
+    if ((int64_t)((a.M + 15) / 16) * a.K * 16 >= (1ll << 31) || (int64_t)a.N * a.K >= (1ll << 31)) return -2;
+    a.ksplit = ksplit;
+    const int tiles = (a.N / (64 * NT)) * ((a.M + 255) / 256) * ksplit;
+    hipLaunchKernelGGL((gemm_bf16_lds_kernel<NT, EPI, ACT>), dim3(tiles), dim3(512), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <int NT>
+static int launch_lds_act(const GemmArgs& a, int ks, hipStream_t st) {
+    const bool silu = a.act == ACT_SILU;
+    if (a.act != ACT_SILU && a.act != ACT_NONE) return -2;
+    switch (a.epi) {
+        case EPI_PARTIAL: return silu ? -2 : launch_lds_cfg<NT, EPI_PARTIAL, ACT_NONE>(a, ks, st);
+        case EPI_STORE_F32:
+            return silu ? launch_lds_cfg<NT, EPI_STORE_F32, ACT_SILU>(a, ks, st) : launch_lds_cfg<NT, EPI_STORE_F32, ACT_NONE>(a, ks, st);
+        case EPI_STORE_FRAG:
+            return silu ? launch_lds_cfg<NT, EPI_STORE_FRAG, ACT_SILU>(a, ks, st) : launch_lds_cfg<NT, EPI_STORE_FRAG, ACT_NONE>(a, ks, st);
+        case EPI_STORE:
+            return silu ? launch_lds_cfg<NT, EPI_STORE, ACT_SILU>(a, ks, st) : launch_lds_cfg<NT, EPI_STORE, ACT_NONE>(a, ks, st);
+        default: return -2;
+    }
+}
+
+static int device_cus() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
+    return cus;
+}
+
+// Tile width (NT: 64*NT columns) and K splits of the LDS-staged kernel for one projection.  Cost
+// model: rounds of workgroups over the CUs x the per-workgroup MFMA work, scaled by the per-flop cost
+// measured on MI355X for each width (NT 4: 1.00, 3: 1.28, 2: 1.36 at 3584 rows), plus for K splits
+// the fp32 partial slabs they write (400 units per slab per 3584 x 1024 outputs).  Measured choices
+// at 3584 rows: N 4096 -> NT 4; N 3072 -> NT 3; N 2048 -> NT 2; N 1024, K 4096 -> NT 4 with 4 splits;
+// N 1024, K 1024 -> NT 2 with 2 splits.
+BigTile big_tile(int M, int N, int K, bool partial) {
+    static const double cost_nt[5] = {0.0, 0.0, 1.36, 1.28, 1.0};
+    const int cus = device_cus();
+    BigTile best{0, 1};
+    double best_cost = 1e300;
+    for (int nt = 4; nt >= 2; nt--) {
+        if (N % (64 * nt) != 0) continue;
+        for (int ks = 1; ks <= (partial ? 4 : 1); ks *= 2) {
+            if (K % (64 * ks) != 0 || (ks > 1 && K / ks < 256)) continue;
+            const long tiles = (long)(N / (64 * nt)) * ((M + 255) / 256) * ks;
+            const long rounds = (tiles + cus - 1) / cus;
+            double cost = (double)rounds * nt * (K / ks) * cost_nt[nt];
+            if (ks > 1) cost += 400.0 * ks * ((double)M * N / (3584.0 * 1024.0));
+            if (cost < best_cost) { best_cost = cost; best = BigTile{nt, ks}; }
+        }
+    }
+    return best;
+}
+
+int gemm_partial_splits(int M, int N, int K, bool bf16_data) {
+    if (!bf16_data) return 1;
+    if (M >= LDS_MIN_ROWS) {
+        const BigTile bt = big_tile(M, N, K, true);
+        if (bt.nt != 0) return bt.ks;
+    }
+    return K % (128 * KSPLIT) == 0 ? KSPLIT : 1;
+}
+
 template <int MT, int WK, int NT, int EPI>
 static int launch_act(const GemmArgs& a, int ks, hipStream_t st) {
     if (a.act == ACT_SILU) return launch_bf16_cfg<MT, WK, NT, EPI, ACT_SILU>(a, ks, st);
@@ -258,6 +506,16 @@ static int launch_bf16(const GemmArgs& a, int ks, hipStream_t st) {
                 if (a.K % (128 * ks) == 0) return launch_bf16_cfg<4, 2, 1, EPI_PARTIAL, ACT_NONE>(a, ks, st);
                 break;
             default: return -2;   // the residual accumulate is an fp32-path epilogue
+        }
+    }
+    if (a.M >= LDS_MIN_ROWS) {
+        const BigTile bt = big_tile(a.M, a.N, a.K, a.epi == EPI_PARTIAL);
+        if (bt.nt != 0 && (a.epi != EPI_PARTIAL || bt.ks == ks)) {
+            switch (bt.nt) {
+                case 4: return launch_lds_act<4>(a, ks, st);
+                case 3: return launch_lds_act<3>(a, ks, st);
+                default: return launch_lds_act<2>(a, ks, st);
+            }
         }
     }
     switch (a.epi) {

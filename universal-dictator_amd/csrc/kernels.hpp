@@ -80,6 +80,15 @@ struct GemmArgs {
     int ksplit;                     // EPI_PARTIAL: K splits (1 or 4) chosen by the caller
 };
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st);
+// Most K splits of a bf16 residual projection (partial slabs the workspace holds).
+constexpr int KSPLIT = 4;
+// Rows from which the bf16 projections use the LDS-staged 256-row-tile kernel.
+constexpr int LDS_MIN_ROWS = 2048;
+struct BigTile { int nt, ks; };   // 64*nt-column tiles, ks K splits (nt 0: shape not supported)
+BigTile big_tile(int M, int N, int K, bool partial);
+// K splits (partial slabs) a residual projection of this shape writes; launch_gemm expects it in
+// GemmArgs::ksplit for EPI_PARTIAL.
+int gemm_partial_splits(int M, int N, int K, bool bf16_data);
 
 // ---------------------------------------------------------------- LayerNorm / conv / misc
 // Pending residual update: nparts fp32 slabs [rows, D] (stride rows*D) that a split-K residual
