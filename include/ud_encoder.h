@@ -75,10 +75,11 @@ UD_API const char* ud_last_error(void);
 UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder** out);
 UD_API void ud_encoder_destroy(ud_encoder* enc);
 
-/* Replaces the per-tensor loads of FastConformer.swift:96-143.  `name` is a NeMo state_dict
+/* Replaces the per-tensor loads of FastConformer.swift:72-143.  `name` is a NeMo state_dict
  * name ("encoder.layers.{i}.feed_forward1.linear1.weight", ..., the 26 per-layer tensors of the
- * checkpoint's name map); `host` holds `count` fp32 values in the checkpoint layout ([out, in]
- * for linears, k=1 axis squeezed, depthwise [D, 1, K]).  The values are converted to the
+ * checkpoint's name map, and the 12 optional encoder.pre_encode.* subsampling tensors); `host`
+ * holds `count` fp32 values in the checkpoint layout ([out, in] for linears, k=1 axes squeezed,
+ * depthwise [D, 1, K], conv2d [256, 1, 3, 3]).  The values are converted to the
  * encoder's dtype on upload (bf16: round-to-nearest-even, Tensor.swift:116-122).  Synchronous. */
 UD_API int ud_encoder_set_weight(ud_encoder* enc, const char* name, const float* host, int64_t count);
 
@@ -114,6 +115,25 @@ UD_API int ud_stream_info(const ud_stream* s, int32_t* cache_len, int32_t* steps
 UD_API int ud_encoder_step(ud_encoder* enc, ud_stream* const* streams, int32_t n, int32_t T,
                            const float* x_dev, const int32_t* valid_T_host, float* out_dev,
                            void* hip_stream);
+
+/* Replaces encodeSubsampling (FastConformer.swift:219-243) and the drop/validT rule of
+ * encodeStreamStep (:444-453): NeMo's causal dw_striding 8x subsampling of a batch of mel chunks.
+ *   n              streams (1 <= n <= max_streams); all chunks have mel_rows rows
+ *   mel_dev        fp32 [n, mel_rows, 128] mel rows, pre-encode cache rows included
+ *   valid_mel_host [n] real rows per chunk (NULL = all); rows beyond are masked as NeMo's
+ *                  MaskedConvSequential does, and the valid length follows L -> L/2 + 1 per stage
+ *   drop           leading subsampled frames to discard (2 after a stream's first step,
+ *                  NemotronSchedule.swift dropExtra; 0 on the first)
+ *   out_dev        fp32 [n, T, d_model] encoder input rows, T = mel_rows -> 3 x (L/2 + 1) - drop,
+ *                  1 <= T <= max_chunk; feed it to ud_encoder_step
+ *   T_out          (may be NULL) receives T;  valid_T_host (may be NULL) receives [n] valid frames,
+ *                  clamp(valid_sub - drop, 0, T), the valid_T_host of ud_encoder_step
+ * Weights: the 12 encoder.pre_encode.* tensors via ud_encoder_set_weight (checkpoint layout;
+ * out.weight [d_model, 256*17] with NeMo's (channel, freq) column order).  The first call
+ * allocates the front-end workspace.  Asynchronous on hip_stream. */
+UD_API int ud_encoder_subsample(ud_encoder* enc, int32_t n, int32_t mel_rows, const float* mel_dev,
+                                const int32_t* valid_mel_host, int32_t drop, float* out_dev, int32_t* T_out,
+                                int32_t* valid_T_host, void* hip_stream);
 
 /* Cache window of one stream and layer in logical (time) order, oldest row first, as fp32:
  * k/v [L, d_model], conv [K-1, d_model]; rows older than cache_len are whatever the pool holds

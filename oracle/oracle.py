@@ -32,6 +32,16 @@ WEIGHT_SUFFIXES = [
 
 ACT_NONE, ACT_RELU, ACT_SILU, ACT_GELU_ERF = 0, 1, 2, 4
 
+# Subsampling tensors (FastConformer.swift:56-95), in the order orc_subsample takes them.
+SUB_WEIGHT_NAMES = [
+    "encoder.pre_encode.conv.0.weight", "encoder.pre_encode.conv.0.bias",
+    "encoder.pre_encode.conv.2.weight", "encoder.pre_encode.conv.2.bias",
+    "encoder.pre_encode.conv.3.weight", "encoder.pre_encode.conv.3.bias",
+    "encoder.pre_encode.conv.5.weight", "encoder.pre_encode.conv.5.bias",
+    "encoder.pre_encode.conv.6.weight", "encoder.pre_encode.conv.6.bias",
+    "encoder.pre_encode.out.weight", "encoder.pre_encode.out.bias",
+]
+
 
 def lib():
     global _lib
@@ -245,4 +255,43 @@ def encoder_offline(model, x, ranges, valid):
     lib().orc_encoder_offline(model._wptrs, model._pptrs, model.rel_offset, model.n_rel, len(model.layers), T, D,
                               model.H, model.ff, model.Kc, _p(x), _ip(np.ascontiguousarray(ranges, np.int32)),
                               int(valid), _p(out))
+    return out
+
+
+def conv2d_cl(x, w, bias, stride, pad_top, pad_left, groups, act=ACT_NONE, valid_h=None, out_hw=None):
+    """conv2d_cl (20_conformer.metal:104-138): x [Hin, Win, Cin] channel-last, w [Cout, Cin/groups,
+    KH, KW]; out [Hout, Wout, Cout] with Hout/Wout from out_hw or the causal rule (L + 2 pads - K)/s + 1
+    with one bottom/right pad row (Ops.swift callers)."""
+    x = _f32(x)
+    w = _f32(w)
+    Hin, Win, Cin = x.shape
+    Cout, _, KH, KW = w.shape
+    if out_hw is None:
+        Hout = (Hin + pad_top + 1 - KH) // stride + 1
+        Wout = (Win + pad_left + 1 - KW) // stride + 1
+    else:
+        Hout, Wout = out_hw
+    out = np.empty((Hout, Wout, Cout), np.float32)
+    lib().orc_conv2d_cl(_p(x), Hin, Win, Cin, _p(w), _p(_f32(bias)), _p(out), Hout, Wout, Cout, KH, KW, stride,
+                        pad_top, pad_left, groups, act, Hout if valid_h is None else valid_h)
+    return out
+
+
+def sub_next_len(t):
+    """Causal stride-2 stage length (FastConformer.swift:219): t // 2 + 1."""
+    return t // 2 + 1
+
+
+def subsample(mel, valid_mel, sw, C=256, D=1024):
+    """encodeSubsampling (FastConformer.swift:219-243): mel [T0, 128] -> [T3, D].  sw maps the
+    names in SUB_WEIGHT_NAMES to arrays in the checkpoint layout (out.weight columns in
+    (channel, freq) order)."""
+    mel = _f32(mel)
+    T0, F0 = mel.shape
+    T3 = sub_next_len(sub_next_len(sub_next_len(T0)))
+    ws = [_f32(sw[n]).reshape(-1) for n in SUB_WEIGHT_NAMES]
+    ptrs = (_f32p * len(ws))(*[_p(w) for w in ws])
+    out = np.empty((T3, D), np.float32)
+    got = lib().orc_subsample(_p(mel), T0, F0, int(valid_mel), ptrs, C, D, _p(out))
+    assert got == T3
     return out

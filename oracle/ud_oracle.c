@@ -32,6 +32,13 @@
  *                         numpy float64 softmax attention; GQA head map
  *   orc_rope_rotate_half  reference KAT (VoxtralOpTests.swift:60-75) against
  *                         rotation by a complex exponential (numpy)
+ *   orc_conv2d_cl         reference KAT shapes (ConformerOpTests.swift:49-78)
+ *                         against torch.nn.functional.conv2d with explicit
+ *                         F.pad (library routine)
+ *   orc_subsample         torch restatement of NeMo's causal dw_striding
+ *                         ConvSubsampling with MaskedConvSequential length
+ *                         masks and the (channel, freq) flatten on the
+ *                         checkpoint's out.weight (tests/refimpl.py)
  */
 #include <math.h>
 #include <stdint.h>
@@ -485,4 +492,81 @@ ORC_API void orc_encoder_offline(const float* const* w, const float* const* P, i
     }
     memcpy(out, xa, sizeof(float) * (size_t)T * D);
     free(keys); free(vals); free(conv); free(xa); free(xb);
+}
+
+/* ------------------------------------------------------------------ subsampling */
+
+/* Sources/DictatorEngine/Metal/20_conformer.metal:104-138 (conv2d_cl), dispatched by
+ * Sources/DictatorEngine/Core/Ops.swift:63-75: channel-last x [Hin, Win, Cin], torch-layout
+ * w [Cout, Cin/groups, KH, KW], out [Hout, Wout, Cout].  Input coordinates outside the image read
+ * as zero (the padding); output rows h >= valid_h are written as zero. */
+ORC_API void orc_conv2d_cl(const float* x, int Hin, int Win, int Cin, const float* w, const float* bias, float* out,
+                           int Hout, int Wout, int Cout, int KH, int KW, int stride, int pad_top, int pad_left,
+                           int groups, int act, int valid_h) {
+    const int cpg = Cin / groups, opg = Cout / groups;
+#pragma omp parallel for schedule(static)
+    for (int ho = 0; ho < Hout; ho++)
+        for (int wo = 0; wo < Wout; wo++)
+            for (int co = 0; co < Cout; co++) {
+                float* o = out + ((int64_t)ho * Wout + wo) * Cout + co;
+                if (ho >= valid_h) { *o = 0.0f; continue; }
+                const int g0 = (co / opg) * cpg;
+                float acc = bias[co];
+                for (int kh = 0; kh < KH; kh++) {
+                    const int hi = ho * stride + kh - pad_top;
+                    if (hi < 0 || hi >= Hin) continue;
+                    for (int kw = 0; kw < KW; kw++) {
+                        const int wi = wo * stride + kw - pad_left;
+                        if (wi < 0 || wi >= Win) continue;
+                        const float* xp = x + ((int64_t)hi * Win + wi) * Cin + g0;
+                        const float* wp = w + ((int64_t)co * cpg * KH + kh) * KW + kw;
+                        for (int ci = 0; ci < cpg; ci++) acc += wp[(int64_t)ci * KH * KW] * xp[ci];
+                    }
+                }
+                *o = orc_act(acc, act);
+            }
+}
+
+/* FastConformer.swift:219 (nextLen): causal stride-2 stage, L -> L/2 + 1. */
+ORC_API int orc_sub_next_len(int t) { return t / 2 + 1; }
+
+static void orc_mask_rows(float* x, int T, int64_t row_elems, int valid) {
+    if (valid < 0) valid = 0;
+    if (valid < T) memset(x + (int64_t)valid * row_elems, 0, (size_t)(T - valid) * row_elems * sizeof(float));
+}
+
+/* FastConformer.swift:219-243 (encodeSubsampling) with the weight set of :72-95.  mel [T0, F0]
+ * (F0 = 128 mel bins), the first valid_mel rows real; C = 256 channels.  sw: conv.0 w/b, conv.2
+ * w/b, conv.3 w/b, conv.5 w/b, conv.6 w/b, out.weight [D, C*F3] in the checkpoint's (channel, freq)
+ * column order, out.bias -- 12 arrays.  The out weight's columns are permuted to (freq, channel)
+ * for the channel-last activations, as the reference does at load (:78-89).  out [T3, D].
+ * Returns T3. */
+ORC_API int orc_subsample(const float* mel, int T0, int F0, int valid_mel, const float* const* sw, int C, int D,
+                          float* out) {
+    const int T1 = orc_sub_next_len(T0), F1 = orc_sub_next_len(F0), T2 = orc_sub_next_len(T1),
+              F2 = orc_sub_next_len(F1), T3 = orc_sub_next_len(T2), F3 = orc_sub_next_len(F2);
+    const int v1 = orc_sub_next_len(valid_mel), v2 = orc_sub_next_len(v1), v3 = orc_sub_next_len(v2);
+    float* x0 = (float*)malloc((size_t)T0 * F0 * sizeof(float));
+    float* a1 = (float*)malloc((size_t)T1 * F1 * C * sizeof(float));
+    float* a2 = (float*)malloc((size_t)T2 * F2 * C * sizeof(float));
+    float* a3 = (float*)malloc((size_t)T2 * F2 * C * sizeof(float));
+    float* a4 = (float*)malloc((size_t)T3 * F3 * C * sizeof(float));
+    float* a5 = (float*)malloc((size_t)T3 * F3 * C * sizeof(float));
+    float* wp = (float*)malloc((size_t)D * C * F3 * sizeof(float));
+    memcpy(x0, mel, (size_t)T0 * F0 * sizeof(float));
+    orc_mask_rows(x0, T0, F0, valid_mel);
+    orc_conv2d_cl(x0, T0, F0, 1, sw[0], sw[1], a1, T1, F1, C, 3, 3, 2, 2, 2, 1, ORC_ACT_RELU, v1);
+    orc_conv2d_cl(a1, T1, F1, C, sw[2], sw[3], a2, T2, F2, C, 3, 3, 2, 2, 2, C, ORC_ACT_NONE, T2);
+    orc_gemm_nt(a2, sw[4], sw[5], NULL, a3, T2 * F2, C, C, 1.0f, ORC_ACT_RELU, 1.0f, 0.0f);
+    orc_mask_rows(a3, T2, (int64_t)F2 * C, v2);
+    orc_conv2d_cl(a3, T2, F2, C, sw[6], sw[7], a4, T3, F3, C, 3, 3, 2, 2, 2, C, ORC_ACT_NONE, T3);
+    orc_gemm_nt(a4, sw[8], sw[9], NULL, a5, T3 * F3, C, C, 1.0f, ORC_ACT_RELU, 1.0f, 0.0f);
+    orc_mask_rows(a5, T3, (int64_t)F3 * C, v3);
+    for (int o = 0; o < D; o++)
+        for (int c = 0; c < C; c++)
+            for (int f = 0; f < F3; f++)
+                wp[((int64_t)o * F3 + f) * C + c] = sw[10][((int64_t)o * C + c) * F3 + f];
+    orc_gemm_nt(a5, wp, sw[11], NULL, out, T3, D, F3 * C, 1.0f, ORC_ACT_NONE, 1.0f, 0.0f);
+    free(x0); free(a1); free(a2); free(a3); free(a4); free(a5); free(wp);
+    return T3;
 }

@@ -82,3 +82,41 @@ def chunked_limited_mask(T, left, right, valid):
     vis = (i - j >= 0) & (i - j <= left // cs)
     vis &= np.arange(T)[None, :] < valid
     return ~vis
+
+
+def subsampling_nemo(mel, valid, w):
+    """NeMo ConvSubsampling, dw_striding causal 8x (subsampling.py:142-215, 425-431 per
+    docs/specs/nemotron.md §2) on one utterance, float64 torch: the image is [1, 1, T, F] (time =
+    height), CausalConv2D pads (left 2, right 1, top 2, bottom 1) and convolves with stride 2,
+    MaskedConvSequential zeroes time rows >= the running length before every layer and after the
+    last, the length after a stride-2 conv is (L + 2 + 1 - 3) // 2 + 1, and the flatten is
+    [B, C, T, F] -> [B, T, C*F] (channel-major) into pre_encode.out.  w maps NeMo names to arrays."""
+    import torch
+    import torch.nn.functional as F
+    t = lambda n: torch.as_tensor(np.asarray(w["encoder.pre_encode." + n]), dtype=torch.float64)
+    x = torch.as_tensor(np.asarray(mel), dtype=torch.float64)[None, None]
+    C = t("conv.0.weight").shape[0]
+    length = int(valid)
+
+    def mask(y):
+        keep = (torch.arange(y.shape[2]) < length).to(y.dtype).view(1, 1, -1, 1)
+        return y * keep
+
+    def causal(y, i, groups):
+        return F.conv2d(F.pad(y, (2, 1, 2, 1)), t("conv.%d.weight" % i), t("conv.%d.bias" % i), stride=2,
+                        groups=groups)
+
+    layers = [("c", 0, 1), ("relu",), ("c", 2, C), ("p", 3), ("relu",), ("c", 5, C), ("p", 6), ("relu",)]
+    for layer in layers:
+        x = mask(x)
+        if layer[0] == "c":
+            x = causal(x, layer[1], layer[2])
+            length = (length + 2 + 1 - 3) // 2 + 1
+        elif layer[0] == "p":
+            x = F.conv2d(x, t("conv.%d.weight" % layer[1]), t("conv.%d.bias" % layer[1]))
+        else:
+            x = F.relu(x)
+    x = mask(x)
+    _, Cc, T, Fq = x.shape
+    x = x.transpose(1, 2).reshape(1, T, Cc * Fq)
+    return F.linear(x, t("out.weight"), t("out.bias"))[0]

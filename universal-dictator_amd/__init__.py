@@ -63,6 +63,7 @@ def _sig(lib):
         "ud_stream_destroy": (v, [p]),
         "ud_stream_info": (i, [p, ip, ip]),
         "ud_encoder_step": (i, [p, ctypes.POINTER(_vp), _i32, _i32, p, ip, p, p]),
+        "ud_encoder_subsample": (i, [p, _i32, _i32, p, ip, _i32, p, ip, ip, p]),
         "ud_stream_export_cache": (i, [p, _i32, f, f, f, ip]),
         "ud_stream_import_cache": (i, [p, _i32, f, f, f, _i32]),
         "ud_relpos_attention": (i, [_i32, p, p, p, p, p, p, p, p, _i32, _i32, _i32, _i32, _i32, _i32, p]),
@@ -338,8 +339,27 @@ class Encoder:
         for suffix, a in weights.items():
             self.set_weight("encoder.layers.%d.%s" % (layer, suffix), a)
 
+    def set_subsampling_weights(self, weights):
+        """weights: dict of the 12 encoder.pre_encode.* tensors (as synthetic_subsampling_weights
+        returns), checkpoint layout."""
+        for name, a in weights.items():
+            self.set_weight(name, a)
+
     def finalize(self):
         _check(_lib.ud_encoder_finalize(self.handle))
+
+    def subsample(self, n, mel, out, valid_mel=None, drop=0, mel_rows=None, hip_stream=None):
+        """encodeSubsampling + drop (ud_encoder_subsample): mel a DeviceBuffer of fp32
+        [n, mel_rows, 128]; out a DeviceBuffer of fp32 [n, T, d_model].  Returns (T, valid_T)."""
+        mel_rows = mel_rows or mel.nbytes // (4 * n * MEL_BINS)
+        vm = None if valid_mel is None else np.ascontiguousarray(valid_mel, np.int32)
+        T = _i32(0)
+        vt = np.zeros(n, np.int32)
+        _check(_lib.ud_encoder_subsample(self.handle, n, mel_rows, mel.ptr,
+                                         vm.ctypes.data_as(ctypes.POINTER(_i32)) if vm is not None else None,
+                                         int(drop), out.ptr, ctypes.byref(T), vt.ctypes.data_as(ctypes.POINTER(_i32)),
+                                         hip_stream.ptr if hip_stream else None))
+        return T.value, vt
 
     def new_stream(self):
         return Stream(self)
@@ -486,6 +506,37 @@ def synthetic_layer_weights(cfg, seed, layer, ln_jitter=0.1):
     w["conv.pointwise_conv2.weight"] = xavier((D, D), D, D)
     w["feed_forward2.linear1.weight"] = xavier((ff, D), D, ff)
     w["feed_forward2.linear2.weight"] = xavier((D, ff), ff, D)
+    return w
+
+
+SUB_CHANNELS, MEL_BINS = 256, 128
+
+
+def synthetic_subsampling_weights(seed, D=1024, C=SUB_CHANNELS, mel_bins=MEL_BINS):
+    """Random-init weights of the causal dw_striding subsampling (encoder.pre_encode.*) in the
+    checkpoint layout: conv weights Xavier-uniform over torch's fan_in/fan_out
+    (in_channels/groups * k * k, out_channels/groups * k * k), biases U(-1/sqrt(fan_in), +), the
+    output Linear [D, C*F3] with columns in NeMo's (channel, freq) order."""
+    rng = np.random.default_rng([int(seed), 1 << 20])
+    F3 = mel_bins
+    for _ in range(3):
+        F3 = F3 // 2 + 1
+
+    def xavier(shape, fan_in, fan_out):
+        b = np.float32(np.sqrt(6.0 / (fan_in + fan_out)))
+        return ((rng.random(shape, dtype=np.float32) * 2 - 1) * b).astype(np.float32)
+
+    def bias(n, fan_in):
+        return ((rng.random(n, dtype=np.float32) * 2 - 1) / np.float32(np.sqrt(fan_in))).astype(np.float32)
+
+    p = "encoder.pre_encode."
+    w = {}
+    w[p + "conv.0.weight"], w[p + "conv.0.bias"] = xavier((C, 1, 3, 3), 9, 9 * C), bias(C, 9)
+    for i in (2, 5):
+        w[p + "conv.%d.weight" % i], w[p + "conv.%d.bias" % i] = xavier((C, 1, 3, 3), 9, 9), bias(C, 9)
+    for i in (3, 6):
+        w[p + "conv.%d.weight" % i], w[p + "conv.%d.bias" % i] = xavier((C, C, 1, 1), C, C), bias(C, C)
+    w[p + "out.weight"], w[p + "out.bias"] = xavier((D, C * F3), C * F3, D), bias(D, C * F3)
     return w
 
 

@@ -123,6 +123,24 @@ struct ud_stream {
     int steps;
 };
 
+// Subsampling front-end (encoder.pre_encode.*, FastConformer.swift:56-95): weights and a workspace
+// sized on first use for max_streams x the longest mel chunk (8 max_chunk + 9 rows).
+enum SubSlot { SUB_C0W, SUB_C0B, SUB_C2W, SUB_C2B, SUB_C3W, SUB_C3B, SUB_C5W, SUB_C5B, SUB_C6W, SUB_C6B, SUB_OUTW,
+               SUB_OUTB, SUB_NSLOTS };
+static const char* kSubName[SUB_NSLOTS] = {
+    "pre_encode.conv.0.weight", "pre_encode.conv.0.bias", "pre_encode.conv.2.weight", "pre_encode.conv.2.bias",
+    "pre_encode.conv.3.weight", "pre_encode.conv.3.bias", "pre_encode.conv.5.weight", "pre_encode.conv.5.bias",
+    "pre_encode.conv.6.weight", "pre_encode.conv.6.bias", "pre_encode.out.weight", "pre_encode.out.bias"};
+constexpr int SUB_CH = 256, SUB_MEL = 128, SUB_F1 = SUB_MEL / 2 + 1, SUB_F2 = SUB_F1 / 2 + 1, SUB_F3 = SUB_F2 / 2 + 1;
+
+struct SubDev {
+    void* w[SUB_NSLOTS] = {};      // conv.3 / conv.6 / out weights in the GEMM layout, the rest fp32
+    uint32_t set_mask = 0;
+    void* a2 = nullptr; float* a3 = nullptr; void* a4 = nullptr; float* a5 = nullptr; void* af = nullptr;
+    int32_t* vlen = nullptr;
+    bool ws = false;
+};
+
 struct ud_encoder {
     ud_encoder_config cfg;
     bool bf;
@@ -148,6 +166,7 @@ struct ud_encoder {
     bool use_graphs = true;
     hipStream_t capture_stream = nullptr;
     std::vector<GraphEntry> graphs;
+    SubDev sub;
 };
 
 static void* dev_alloc(size_t bytes) {
@@ -167,6 +186,9 @@ static void free_encoder(ud_encoder* e) {
     }
     void* ws[] = {e->kring, e->vring, e->cring, e->res, e->z, e->h, e->qkv, e->att, e->pw, e->part, e->desc_dev};
     for (void* p : ws) if (p) (void)hipFree(p);
+    for (void* p : e->sub.w) if (p) (void)hipFree(p);
+    void* sws[] = {e->sub.a2, e->sub.a3, e->sub.a4, e->sub.a5, e->sub.af, e->sub.vlen};
+    for (void* p : sws) if (p) (void)hipFree(p);
     for (int i = 0; i < 4; i++) {
         if (e->desc_host[i]) (void)hipHostFree(e->desc_host[i]);
         if (e->desc_ev[i]) (void)hipEventDestroy(e->desc_ev[i]);
@@ -302,8 +324,49 @@ static bool parse_name(const char* name, int layers, int* layer, int* slot) {
     return false;
 }
 
+static int set_sub_weight(ud_encoder* e, int slot, const char* name, const float* host, int64_t count) {
+    const int64_t C = SUB_CH, D = e->D;
+    int64_t want = C;
+    switch (slot) {
+        case SUB_C0W: case SUB_C2W: case SUB_C5W: want = C * 9; break;
+        case SUB_C3W: case SUB_C6W: want = C * C; break;
+        case SUB_OUTW: want = D * C * SUB_F3; break;
+        case SUB_OUTB: want = D; break;
+        default: break;
+    }
+    if (count != want)
+        return fail(UD_ERR_WEIGHT, "weight '%s': %lld values, expected %lld", name, (long long)count, (long long)want);
+    const bool gemm_w = slot == SUB_C3W || slot == SUB_C6W || slot == SUB_OUTW;
+    void*& dst = e->sub.w[slot];
+    if (!dst && !(dst = dev_alloc((size_t)want * (gemm_w ? e->esz : 4))))
+        return fail(UD_ERR_NOMEM, "ud_encoder_set_weight: allocation failed");
+    int rc;
+    if (slot == SUB_OUTW) {
+        // (channel, freq) columns of the checkpoint -> (freq, channel) for channel-last activations
+        // (FastConformer.swift:78-89).
+        std::vector<float> perm((size_t)want);
+        for (int64_t o = 0; o < D; o++)
+            for (int64_t c = 0; c < C; c++)
+                for (int64_t f = 0; f < SUB_F3; f++)
+                    perm[(size_t)((o * SUB_F3 + f) * C + c)] = host[(o * C + c) * SUB_F3 + f];
+        rc = upload_matrix(e, dst, 0, perm.data(), (size_t)D, (size_t)(C * SUB_F3));
+    } else if (gemm_w) {
+        rc = upload_matrix(e, dst, 0, host, (size_t)C, (size_t)C);
+    } else {
+        rc = upload(dst, host, (size_t)want * 4);
+    }
+    if (rc != UD_OK) return rc;
+    e->sub.set_mask |= 1u << slot;
+    return UD_OK;
+}
+
 extern "C" UD_API int ud_encoder_set_weight(ud_encoder* e, const char* name, const float* host, int64_t count) {
     if (!e || !name || !host) return fail(UD_ERR_INVALID, "ud_encoder_set_weight: null argument");
+    {
+        const char* p = strncmp(name, "encoder.", 8) == 0 ? name + 8 : name;
+        for (int s = 0; s < SUB_NSLOTS; s++)
+            if (strcmp(p, kSubName[s]) == 0) return set_sub_weight(e, s, name, host, count);
+    }
     int li = -1, slot = -1;
     if (!parse_name(name, e->layers, &li, &slot)) return fail(UD_ERR_WEIGHT, "unknown weight name '%s'", name);
     const int64_t D = e->D, ff = e->ff;
@@ -626,6 +689,88 @@ extern "C" UD_API int ud_encoder_step(ud_encoder* e, ud_stream* const* streams, 
     if ((rc = run_step(e, n, T, x_dev, out_dev, st)) != UD_OK) return rc;
     for (int i = 0; i < n; i++) { streams[i]->frames += T; streams[i]->steps++; }
     return UD_OK;
+}
+
+// ---------------------------------------------------------------- subsampling front-end
+
+static int sub_len(int t) { return t / 2 + 1; }   // FastConformer.swift:219 (causal stride-2 stage)
+
+static int sub_workspace(ud_encoder* e) {
+    if (e->sub.ws) return UD_OK;
+    const size_t n = (size_t)e->cfg.max_streams;
+    const int T0 = 8 * e->cfg.max_chunk + 9, T2 = sub_len(sub_len(T0)), T3 = sub_len(T2);
+    const size_t r2 = n * T2 * SUB_F2, r3 = n * T3 * SUB_F3, rf = n * e->cfg.max_chunk;
+    auto pad = [](size_t r) { return (r + 15) / 16 * 16; };
+    SubDev& u = e->sub;
+    bool ok = (u.a2 = dev_alloc(pad(r2) * SUB_CH * e->esz)) != nullptr;
+    ok = ok && (u.a3 = (float*)dev_alloc(r2 * SUB_CH * 4)) != nullptr;
+    ok = ok && (u.a4 = dev_alloc(pad(r3) * SUB_CH * e->esz)) != nullptr;
+    ok = ok && (u.a5 = (float*)dev_alloc(r3 * SUB_CH * 4)) != nullptr;
+    ok = ok && (u.af = dev_alloc(pad(rf) * SUB_CH * SUB_F3 * e->esz)) != nullptr;
+    ok = ok && (u.vlen = (int32_t*)dev_alloc(n * 4 * sizeof(int32_t))) != nullptr;
+    if (!ok) return fail(UD_ERR_NOMEM, "ud_encoder_subsample: workspace allocation failed");
+    u.ws = true;
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_encoder_subsample(ud_encoder* e, int32_t n, int32_t mel_rows, const float* mel_dev,
+                                           const int32_t* valid_mel_host, int32_t drop, float* out_dev,
+                                           int32_t* T_out, int32_t* valid_T_host, void* hip_stream) {
+    if (!e || !mel_dev || !out_dev) return fail(UD_ERR_INVALID, "ud_encoder_subsample: null argument");
+    if (e->sub.set_mask != (1u << SUB_NSLOTS) - 1) {
+        for (int s = 0; s < SUB_NSLOTS; s++)
+            if (!(e->sub.set_mask & (1u << s)))
+                return fail(UD_ERR_STATE, "ud_encoder_subsample: weight encoder.%s not set", kSubName[s]);
+    }
+    if (n < 1 || n > e->cfg.max_streams) return fail(UD_ERR_SHAPE, "ud_encoder_subsample: n = %d outside 1..%d", n, e->cfg.max_streams);
+    const int T0 = mel_rows, T1 = sub_len(T0), T2 = sub_len(T1), T3 = sub_len(T2);
+    const int T = T3 - drop;
+    if (mel_rows < 1 || drop < 0 || T < 1 || T > e->cfg.max_chunk)
+        return fail(UD_ERR_SHAPE, "ud_encoder_subsample: %d mel rows with drop %d give %d frames (need 1..%d)", mel_rows,
+                    drop, T, e->cfg.max_chunk);
+    int rc = sub_workspace(e);
+    if (rc != UD_OK) return rc;
+    // Valid rows per stage (FastConformer.swift:446-450): mel rows, then L -> L/2 + 1 per stage.
+    std::vector<int32_t> vl((size_t)n * 4);
+    for (int i = 0; i < n; i++) {
+        int v = valid_mel_host ? valid_mel_host[i] : T0;
+        v = v < 0 ? 0 : (v > T0 ? T0 : v);
+        vl[i * 4 + 0] = v;
+        for (int k = 1; k < 4; k++) vl[i * 4 + k] = sub_len(vl[i * 4 + k - 1]);
+        if (valid_T_host) {
+            const int vt = vl[i * 4 + 3] - drop;
+            valid_T_host[i] = vt < 0 ? 0 : (vt > T ? T : vt);
+        }
+    }
+    if (T_out) *T_out = T;
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    SubDev& u = e->sub;
+    HIPC(hipMemcpyAsync(u.vlen, vl.data(), vl.size() * sizeof(int32_t), hipMemcpyHostToDevice, st));
+    const bool bf = e->bf;
+    SubArgs c01{};
+    c01.mel = mel_dev; c01.vlen = u.vlen;
+    c01.c0w = (const float*)u.w[SUB_C0W]; c01.c0b = (const float*)u.w[SUB_C0B];
+    c01.c2w = (const float*)u.w[SUB_C2W]; c01.c2b = (const float*)u.w[SUB_C2B];
+    c01.out = u.a2; c01.n = n; c01.T0 = T0; c01.F0 = SUB_MEL; c01.T1 = T1; c01.F1 = SUB_F1; c01.T2 = T2; c01.F2 = SUB_F2;
+    LAUNCH(launch_sub_conv01(c01, bf, st), "subsampling conv.0 + conv.2");
+    auto gemm = [&](const void* A, int slot_w, int slot_b, void* C, int M, int N, int K, int act, const char* what) {
+        GemmArgs g{};
+        g.A = A; g.W = u.w[slot_w]; g.C = C; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldw = K; g.ldc = N;
+        g.epi = EPI_STORE_F32; g.act = act; g.out_scale = 1.0f; g.ksplit = 1; g.bias = (const float*)u.w[slot_b];
+        return launch_status(launch_gemm(g, bf, st), what);
+    };
+    if ((rc = gemm(u.a2, SUB_C3W, SUB_C3B, u.a3, n * T2 * SUB_F2, SUB_CH, SUB_CH, ACT_RELU, "subsampling conv.3")))
+        return rc;
+    SubDwArgs dw{};
+    dw.x = u.a3; dw.vlen = u.vlen; dw.w = (const float*)u.w[SUB_C5W]; dw.b = (const float*)u.w[SUB_C5B]; dw.out = u.a4;
+    dw.n = n; dw.Hin = T2; dw.Win = SUB_F2; dw.Hout = T3; dw.Wout = SUB_F3; dw.stage = 2;
+    LAUNCH(launch_sub_dw(dw, bf, st), "subsampling conv.5");
+    if ((rc = gemm(u.a4, SUB_C6W, SUB_C6B, u.a5, n * T3 * SUB_F3, SUB_CH, SUB_CH, ACT_RELU, "subsampling conv.6")))
+        return rc;
+    SubFlatArgs fl{};
+    fl.x = u.a5; fl.vlen = u.vlen; fl.out = u.af; fl.n = n; fl.T3 = T3; fl.F3 = SUB_F3; fl.T = T; fl.drop = drop;
+    LAUNCH(launch_sub_flatten(fl, bf, st), "subsampling flatten");
+    return gemm(u.af, SUB_OUTW, SUB_OUTB, out_dev, n * T, e->D, SUB_CH * SUB_F3, ACT_NONE, "subsampling out");
 }
 
 static RingArgs ring_args(ud_encoder* e, int n, int T, int layer, const void* qkv, void* att) {

@@ -151,7 +151,7 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
         for (int i2 = 0; i2 < 4; i2++) {
             const int64_t m = (int64_t)(mb * MT + mt) * 16 + g * 4 + i2;
             if (m >= a.M) continue;
-            const float v = acc[j][mt][i2];
+            const float v = acc[j][mt][i2] + (a.bias != nullptr && kz == 0 ? a.bias[n] : 0.0f);
             if constexpr (EPI == EPI_PARTIAL) {
                 static_cast<float*>(a.C)[((int64_t)kz * a.M + m) * a.ldc + n] = a.out_scale * v;
             } else if constexpr (EPI == EPI_STORE_F32) {
@@ -320,7 +320,8 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < NT; j++) {
             const int n = (nb * BB + wn * NT + j) * 16 + g * 4;
-            const f32x4_t v = acc[j][i];
+            f32x4_t v = acc[j][i];
+            if (a.bias != nullptr && kz == 0) v += *reinterpret_cast<const f32x4_t*>(a.bias + n);
             if constexpr (EPI == EPI_PARTIAL) {
                 *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.C) + ((int64_t)kz * a.M + m) * a.ldc + n) =
                     v * a.out_scale;
@@ -380,6 +381,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
             int n = n0 + tn + j;
             if (n >= a.N) continue;
             float* C = static_cast<float*>(a.C) + (int64_t)m * a.ldc + n;
+            if (a.bias != nullptr) acc[i][j] += a.bias[n];
             if (a.epi == EPI_RESID) *C = *C + a.out_scale * acc[i][j];
             else *C = apply_act(acc[i][j], a.act) * a.out_scale;
         }
@@ -410,18 +412,23 @@ static int launch_lds_cfg(GemmArgs a, int ksplit, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+template <int NT, int EPI>
+static int launch_lds_epi(const GemmArgs& a, int ks, hipStream_t st) {
+    switch (a.act) {
+        case ACT_NONE: return launch_lds_cfg<NT, EPI, ACT_NONE>(a, ks, st);
+        case ACT_SILU: return launch_lds_cfg<NT, EPI, ACT_SILU>(a, ks, st);
+        case ACT_RELU: return launch_lds_cfg<NT, EPI, ACT_RELU>(a, ks, st);
+        default: return -2;
+    }
+}
+
 template <int NT>
 static int launch_lds_act(const GemmArgs& a, int ks, hipStream_t st) {
-    const bool silu = a.act == ACT_SILU;
-    if (a.act != ACT_SILU && a.act != ACT_NONE) return -2;
     switch (a.epi) {
-        case EPI_PARTIAL: return silu ? -2 : launch_lds_cfg<NT, EPI_PARTIAL, ACT_NONE>(a, ks, st);
-        case EPI_STORE_F32:
-            return silu ? launch_lds_cfg<NT, EPI_STORE_F32, ACT_SILU>(a, ks, st) : launch_lds_cfg<NT, EPI_STORE_F32, ACT_NONE>(a, ks, st);
-        case EPI_STORE_FRAG:
-            return silu ? launch_lds_cfg<NT, EPI_STORE_FRAG, ACT_SILU>(a, ks, st) : launch_lds_cfg<NT, EPI_STORE_FRAG, ACT_NONE>(a, ks, st);
-        case EPI_STORE:
-            return silu ? launch_lds_cfg<NT, EPI_STORE, ACT_SILU>(a, ks, st) : launch_lds_cfg<NT, EPI_STORE, ACT_NONE>(a, ks, st);
+        case EPI_PARTIAL: return a.act == ACT_NONE ? launch_lds_cfg<NT, EPI_PARTIAL, ACT_NONE>(a, ks, st) : -2;
+        case EPI_STORE_F32: return launch_lds_epi<NT, EPI_STORE_F32>(a, ks, st);
+        case EPI_STORE_FRAG: return launch_lds_epi<NT, EPI_STORE_FRAG>(a, ks, st);
+        case EPI_STORE: return launch_lds_epi<NT, EPI_STORE>(a, ks, st);
         default: return -2;
     }
 }
@@ -476,6 +483,7 @@ template <int MT, int WK, int NT, int EPI>
 static int launch_act(const GemmArgs& a, int ks, hipStream_t st) {
     if (a.act == ACT_SILU) return launch_bf16_cfg<MT, WK, NT, EPI, ACT_SILU>(a, ks, st);
     if (a.act == ACT_NONE) return launch_bf16_cfg<MT, WK, NT, EPI, ACT_NONE>(a, ks, st);
+    if (a.act == ACT_RELU) return launch_bf16_cfg<MT, WK, NT, EPI, ACT_RELU>(a, ks, st);
     return -2;
 }
 

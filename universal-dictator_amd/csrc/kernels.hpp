@@ -77,7 +77,8 @@ struct GemmArgs {
     int M, N, K, lda, ldw, ldc;
     int epi, act;
     float out_scale;
-    int ksplit;                     // EPI_PARTIAL: K splits (1 or 4) chosen by the caller
+    int ksplit;                     // EPI_PARTIAL: K splits chosen by the caller (gemm_partial_splits)
+    const float* bias;              // optional [N], added before the activation (EPI_PARTIAL: by split 0)
 };
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st);
 // Most K splits of a bf16 residual projection (partial slabs the workspace holds).
@@ -119,5 +120,31 @@ struct ConvArgs {
     bool z_bf16;
 };
 int launch_dwconv_ln(const ConvArgs& a, hipStream_t st);
+
+// ---------------------------------------------------------------- subsampling front-end
+// vlen: per stream 4 ints, the valid rows before conv.0 (mel) and after each stride-2 stage.
+struct SubArgs {
+    const float* mel;               // [n, T0, F0]
+    const int32_t* vlen;            // [n][4]
+    const float* c0w; const float* c0b; const float* c2w; const float* c2b;   // [C][9], [C]
+    void* out;                      // conv.2 output as the conv.3 GEMM's A: [n*T2*F2, C]
+    int n, T0, F0, T1, F1, T2, F2;
+};
+int launch_sub_conv01(const SubArgs& a, bool bf16_out, hipStream_t st);
+struct SubDwArgs {
+    const float* x;                 // [n, Hin, Win, C] fp32
+    const int32_t* vlen;
+    const float* w; const float* b; // [C][9], [C]
+    void* out;                      // [n*Hout*Wout, C] GEMM A operand
+    int n, Hin, Win, Hout, Wout, stage;   // stage: vlen index of x's valid rows
+};
+int launch_sub_dw(const SubDwArgs& a, bool bf16_out, hipStream_t st);
+struct SubFlatArgs {
+    const float* x;                 // [n, T3, F3, C] fp32
+    const int32_t* vlen;
+    void* out;                      // [n*T, F3*C] GEMM A operand
+    int n, T3, F3, T, drop;
+};
+int launch_sub_flatten(const SubFlatArgs& a, bool bf16_out, hipStream_t st);
 
 }  // namespace ud

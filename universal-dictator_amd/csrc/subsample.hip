@@ -1,0 +1,133 @@
+// Causal dw_striding 8x subsampling of the streaming step (FastConformer.swift:219-243 encodeSubsampling;
+// Metal/20_conformer.metal:104-138 conv2d_cl; NeMo ConvSubsampling as in docs/specs/nemotron.md §2),
+// batched over streams.  Activations are channel-last [stream, time, freq, C = 256]; every stride-2
+// stage is a 3 x 3 causal conv with 2 zero rows/columns of top/left padding, L -> L/2 + 1.
+//
+//   conv.0 (1 -> C) + ReLU, rows >= v1 zero     } sub_conv01_kernel: conv.0 is recomputed for each
+//   conv.2 (depthwise)                          } depthwise tap (a 7 x 7 mel patch per output), so
+//                                                 its T1 x 65 x 256 activation never reaches HBM
+//   conv.3 (pointwise) + ReLU                   GEMM (bias epilogue), fp32 out
+//   rows >= v2 zero; conv.5 (depthwise)         sub_dw_kernel (mask applied on read)
+//   conv.6 (pointwise) + ReLU                   GEMM, fp32 out
+//   rows >= v3 zero; drop; flatten (f, c)       sub_flatten_kernel -> rows of the out Linear's A
+//   out Linear (C*F3 -> D) + bias               GEMM, fp32 out = the encoder's input rows
+//
+// The GEMM operands (conv.3 / conv.6 inputs, the flattened rows) are written in the GEMM's A
+// layout: fragment-major bf16 for a bf16 encoder, row-major fp32 for an fp32 one.
+#include "ud_common.hpp"
+#include "kernels.hpp"
+
+namespace ud {
+
+constexpr int SUB_C = 256;
+
+template <bool BF>
+__device__ __forceinline__ void store_a(void* A, int64_t m, int col, int cols, float v) {
+    if constexpr (BF) static_cast<bf16*>(A)[frag_index(m, col, cols / 64)] = f2bf(v);
+    else static_cast<float*>(A)[m * cols + col] = v;
+}
+
+// One workgroup per conv.2 output position (stream s, time t2, freq f2); thread c = channel.
+// conv.2 tap (kh, kw) reads conv.0's output at (2 t2 + kh - 2, 2 f2 + kw - 2), which reads mel rows
+// 2 h + i - 2 = 4 t2 + 2 kh + i - 6 and columns 4 f2 + 2 kw + j - 6: a 7 x 7 patch.
+template <bool BF>
+__global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
+    const int c = threadIdx.x;
+    const int pos = blockIdx.x;                     // (s * T2 + t2) * F2 + f2
+    const int f2 = pos % a.F2, t2 = (pos / a.F2) % a.T2, s = pos / (a.F2 * a.T2);
+    const int v0 = a.vlen[s * 4 + 0], v1 = a.vlen[s * 4 + 1];
+    __shared__ float patch[7][8];
+    if (c < 49) {
+        const int pr = c / 7, pc = c % 7;
+        const int r = 4 * t2 - 6 + pr, q = 4 * f2 - 6 + pc;
+        float v = 0.0f;
+        if (r >= 0 && r < a.T0 && r < v0 && q >= 0 && q < a.F0) v = a.mel[((int64_t)s * a.T0 + r) * a.F0 + q];
+        patch[pr][pc] = v;
+    }
+    float w0[9], w2[9];
+#pragma unroll
+    for (int k = 0; k < 9; k++) { w0[k] = a.c0w[c * 9 + k]; w2[k] = a.c2w[c * 9 + k]; }
+    const float b0 = a.c0b[c];
+    float acc = a.c2b[c];
+    __syncthreads();
+#pragma unroll
+    for (int kh = 0; kh < 3; kh++) {
+        const int h = 2 * t2 + kh - 2;
+#pragma unroll
+        for (int kw = 0; kw < 3; kw++) {
+            const int w = 2 * f2 + kw - 2;
+            if (h < 0 || h >= a.T1 || h >= v1 || w < 0 || w >= a.F1) continue;   // padding or masked row
+            float y = b0;
+#pragma unroll
+            for (int i = 0; i < 3; i++)
+#pragma unroll
+                for (int j = 0; j < 3; j++) y += w0[i * 3 + j] * patch[2 * kh + i][2 * kw + j];
+            acc += w2[kh * 3 + kw] * (y > 0.0f ? y : 0.0f);
+        }
+    }
+    store_a<BF>(a.out, pos, c, SUB_C, acc);
+}
+
+// Depthwise 3 x 3 stride-2 causal conv over x [n, Hin, Win, C] fp32 whose rows >= vlen[s][stage]
+// read as zero (the mask NeMo applies before this layer); one workgroup per output position.
+template <bool BF>
+__global__ __launch_bounds__(SUB_C) void sub_dw_kernel(SubDwArgs a) {
+    const int c = threadIdx.x;
+    const int pos = blockIdx.x;                     // (s * Hout + ho) * Wout + wo
+    const int wo = pos % a.Wout, ho = (pos / a.Wout) % a.Hout, s = pos / (a.Wout * a.Hout);
+    const int vin = a.vlen[s * 4 + a.stage];
+    float acc = a.b[c];
+#pragma unroll
+    for (int kh = 0; kh < 3; kh++) {
+        const int h = 2 * ho + kh - 2;
+        if (h < 0 || h >= a.Hin || h >= vin) continue;
+#pragma unroll
+        for (int kw = 0; kw < 3; kw++) {
+            const int w = 2 * wo + kw - 2;
+            if (w < 0 || w >= a.Win) continue;
+            acc += a.w[c * 9 + kh * 3 + kw] * a.x[(((int64_t)s * a.Hin + h) * a.Win + w) * SUB_C + c];
+        }
+    }
+    store_a<BF>(a.out, pos, c, SUB_C, acc);
+}
+
+// Rows of the out Linear: row (s, t) for t < T takes conv.6's output frame t3 = t + drop, zero when
+// t3 >= v3 (NeMo's final mask), flattened as (freq, channel) -- the column order the out weight
+// is permuted to at load.  One workgroup per row.
+template <bool BF>
+__global__ __launch_bounds__(SUB_C) void sub_flatten_kernel(SubFlatArgs a) {
+    const int c = threadIdx.x;
+    const int row = blockIdx.x, s = row / a.T, t3 = row % a.T + a.drop;
+    const bool valid = t3 < a.vlen[s * 4 + 3];
+    const float* src = a.x + (((int64_t)s * a.T3 + t3) * a.F3) * SUB_C;
+    for (int f = 0; f < a.F3; f++) {
+        const float v = valid ? src[f * SUB_C + c] : 0.0f;
+        store_a<BF>(a.out, row, f * SUB_C + c, a.F3 * SUB_C, v);
+    }
+}
+
+int launch_sub_conv01(const SubArgs& a, bool bf, hipStream_t st) {
+    const int blocks = a.n * a.T2 * a.F2;
+    if (blocks <= 0) return 0;
+    if (bf) hipLaunchKernelGGL(sub_conv01_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
+    else hipLaunchKernelGGL(sub_conv01_kernel<false>, dim3(blocks), dim3(SUB_C), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_sub_dw(const SubDwArgs& a, bool bf, hipStream_t st) {
+    const int blocks = a.n * a.Hout * a.Wout;
+    if (blocks <= 0) return 0;
+    if (bf) hipLaunchKernelGGL(sub_dw_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
+    else hipLaunchKernelGGL(sub_dw_kernel<false>, dim3(blocks), dim3(SUB_C), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int launch_sub_flatten(const SubFlatArgs& a, bool bf, hipStream_t st) {
+    const int blocks = a.n * a.T;
+    if (blocks <= 0) return 0;
+    if (bf) hipLaunchKernelGGL(sub_flatten_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
+    else hipLaunchKernelGGL(sub_flatten_kernel<false>, dim3(blocks), dim3(SUB_C), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+}  // namespace ud
