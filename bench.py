@@ -3,9 +3,11 @@
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|offline]
                     [--no-cpu-baseline]
 
-A step is one 24-layer encoder chunk step (bf16 weights/activations, fp32 accumulation) for every
-stream of the batch, with inputs already in HBM and full 70-frame caches seeded from N(0,1).
-Default workload: 64 streams x 2 frames (160 ms of audio per stream per step).  Prints one JSON
+A step is one cache-aware encoder chunk step for every stream of the batch: the mel chunk (new rows
+plus the 9-row pre-encode cache) through the causal dw_striding 8x subsampling with 2 frames dropped,
+then 24 conformer layers (bf16 weights/activations, fp32 accumulation), with inputs already in HBM
+and full 70-frame caches seeded from N(0,1).  Default workload: 64 streams x 2 frames (25 mel rows
+in, 160 ms of audio per stream per step).  Prints one JSON
 line: aggregate streamed audio-seconds per second, the fused attention kernel's achieved HBM
 bandwidth against 8 TB/s (HIP events on the kernel's own stream), and the CPU oracle's throughput
 on a bounded sample timed on this host.
@@ -66,9 +68,10 @@ def read_traffic(kernel_tag):
     return None
 
 
-def cpu_baseline(lw, cfg, S, T, budget_s, threads):
+def cpu_baseline(lw, sw, cfg, S, T, budget_s, threads):
     """The oracle's encodeStreamStep (fp32, OpenMP) on this host: whole steps of the same workload
-    (all S streams, all layers) until about budget_s seconds have passed."""
+    (subsampling of every stream's mel chunk, then all layers for all S streams) until about
+    budget_s seconds have passed."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
     orc.set_threads(threads)
@@ -80,20 +83,32 @@ def cpu_baseline(lw, cfg, S, T, budget_s, threads):
     vc = rng.standard_normal((S, cfg.layers, L, D), dtype=np.float32)
     cc = rng.standard_normal((S, cfg.layers, cfg.conv_kernel - 1, D), dtype=np.float32)
     cl = np.full(S, L, np.int32)
-    x = rng.standard_normal((S, T, D), dtype=np.float32)
+    rows = mel_rows(T)
+    mel = rng.standard_normal((S, rows, 128), dtype=np.float32)
     valid = np.full(S, T, np.int32)
-    orc.stream_step(model, x, valid, kc, vc, cc, cl)          # warm-up
+
+    def step():
+        x = np.stack([orc.subsample(mel[s], rows, sw)[2:] for s in range(S)])
+        orc.stream_step(model, x, valid, kc, vc, cc, cl)
+
+    step()                                                    # warm-up
     n, t0 = 0, time.perf_counter()
     while True:
-        orc.stream_step(model, x, valid, kc, vc, cc, cl)
+        step()
         n += 1
         el = time.perf_counter() - t0
         if el >= budget_s or n >= 50:
             break
     step_s = el / n
     return dict(value=round(S * T * FRAME_SEC / step_s, 3), unit="audio-sec/sec", cores=threads, kind="port",
-                sample="%d full steps (%d streams x %d frames, %d layers, fp32) in %.1f s; %.3f s/step"
-                       % (n, S, T, cfg.layers, el, step_s))
+                sample="%d full steps (%d streams x %d mel rows -> %d frames, %d layers, fp32) in %.1f s; "
+                       "%.3f s/step" % (n, S, rows, T, cfg.layers, el, step_s))
+
+
+def mel_rows(T):
+    """Mel rows of a chunk that yields T encoder frames after the 2 dropped ones: 8 (T + 2) - 7
+    (16 new rows + 9 pre-encode cache rows for T = 2, NemotronSchedule.swift)."""
+    return 8 * (T + 2) - 7
 
 
 def decode_bench(ud, args):
@@ -301,9 +316,11 @@ def main():
         % (ud.device_arch(), args.workload, S, T, L, cfg.layers))
 
     lw = [ud.synthetic_layer_weights(cfg, 2024, l, ln_jitter=0.0) for l in range(cfg.layers)]
+    sw = ud.synthetic_subsampling_weights(2025)
     enc = ud.Encoder(cfg)
     for l, w in enumerate(lw):
         enc.set_layer_weights(l, w)
+    enc.set_subsampling_weights(sw)
     enc.finalize()
     log("weights uploaded")
     streams = [enc.new_stream() for _ in range(S)]
@@ -317,30 +334,45 @@ def main():
             s.import_cache(l, k, v, conv, L)
     log("caches seeded (cache_len %d)" % L)
 
-    x = ud.DeviceBuffer.from_numpy(rng.standard_normal((S, T, D), dtype=np.float32))
+    rows = mel_rows(T)
+    mel = ud.DeviceBuffer.from_numpy(rng.standard_normal((S, rows, 128), dtype=np.float32))
+    x = ud.DeviceBuffer(S * T * D * 4)
     out = ud.DeviceBuffer(S * T * D * 4)
     hs = ud.HipStream()
-    valid = np.full(S, T, np.int32)
+
+    def step():
+        Tn, valid = enc.subsample(S, mel, x, drop=2, mel_rows=rows, hip_stream=hs)
+        enc.encode_stream_step(streams, x, out, valid=valid, T=Tn, hip_stream=hs)
+
     for _ in range(args.warmup):
-        enc.encode_stream_step(streams, x, out, valid=valid, T=T, hip_stream=hs)
+        step()
     hs.synchronize()
     log("warm-up done (%d steps)" % args.warmup)
 
-    e0, e1 = ud.Event(), ud.Event()
-    ud.synchronize()
-    e0.record(hs)
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        enc.encode_stream_step(streams, x, out, valid=valid, T=T, hip_stream=hs)
-    e1.record(hs)
-    e1.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1000.0
-    ud.synchronize()
-    gpu_ms = e0.elapsed_ms(e1)
+    def timed(fn, iters):
+        e0, e1 = ud.Event(), ud.Event()
+        ud.synchronize()
+        e0.record(hs)
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        e1.record(hs)
+        e1.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1000.0
+        ud.synchronize()
+        return wall_ms, e0.elapsed_ms(e1)
+
+    wall_ms, gpu_ms = timed(step, args.steps)
     ms_per_step = max(wall_ms, gpu_ms) / args.steps
     audio_per_step = S * T * FRAME_SEC
     value = audio_per_step / (ms_per_step / 1000.0)
     log("timed %d steps: %.4f ms/step (wall %.1f ms, events %.1f ms)" % (args.steps, ms_per_step, wall_ms, gpu_ms))
+    parts = max(20, args.steps // 4)
+    fw, fg = timed(lambda: enc.subsample(S, mel, x, drop=2, mel_rows=rows, hip_stream=hs), parts)
+    valid = np.full(S, T, np.int32)
+    lw_, lg = timed(lambda: enc.encode_stream_step(streams, x, out, valid=valid, T=T, hip_stream=hs), parts)
+    front_ms, layers_ms = max(fw, fg) / parts, max(lw_, lg) / parts
+    log("parts: subsampling %.4f ms, 24 layers %.4f ms" % (front_ms, layers_ms))
 
     # The fused attention kernel alone, on the stream it is launched on.
     qkv = ud.DeviceBuffer.from_numpy((ud.round_bf16(rng.standard_normal((S * T, 3 * D), dtype=np.float32))
@@ -372,11 +404,14 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded random-init weights, N(0,1) inputs and caches)",
         "config": {
-            "workload": "24-layer cache-aware FastConformer encoder step, %d streams x %d frames (%d ms), "
-                        "left context %d, bf16" % (S, T, int(T * FRAME_SEC * 1000), L),
-            "streams": S, "chunk_frames": T, "left_context": L, "layers": cfg.layers, "d_model": D,
-            "heads": H, "ff_dim": cfg.ff_dim, "conv_kernel": cfg.conv_kernel,
+            "workload": "cache-aware FastConformer encoder step (dw_striding 8x subsampling + 24 layers), "
+                        "%d streams x %d mel rows -> %d frames (%d ms), left context %d, bf16"
+                        % (S, rows, T, int(T * FRAME_SEC * 1000), L),
+            "streams": S, "mel_rows": rows, "chunk_frames": T, "left_context": L, "layers": cfg.layers,
+            "d_model": D, "heads": H, "ff_dim": cfg.ff_dim, "conv_kernel": cfg.conv_kernel,
         },
+        "subsampling_ms_per_step": round(front_ms, 5),
+        "layers_ms_per_step": round(layers_ms, 5),
         "realtime_factor": round(value, 2),
         "attention_steps_per_sec": round(1000.0 / attn_ms, 1),
         "attention_us_per_launch": round(attn_ms * 1000.0, 3),
@@ -398,7 +433,7 @@ def main():
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         log("cpu baseline: oracle on %d threads, ~%.0f s" % (threads, args.cpu_seconds))
-        result["cpu_baseline"] = cpu_baseline(lw, cfg, S, T, args.cpu_seconds, threads)
+        result["cpu_baseline"] = cpu_baseline(lw, sw, cfg, S, T, args.cpu_seconds, threads)
     print(json.dumps(result), flush=True)
 
 

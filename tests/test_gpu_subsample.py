@@ -8,12 +8,17 @@ import harness
 
 pytestmark = pytest.mark.gpu
 
-SUB_BF16 = {"encoder.pre_encode.conv.3.weight", "encoder.pre_encode.conv.6.weight", "encoder.pre_encode.out.weight"}
+# Front-end GEMM weights a bf16 encoder stores as IEEE half (its front-end GEMMs run on the f16 MFMA).
+SUB_HALF = {"encoder.pre_encode.conv.3.weight", "encoder.pre_encode.conv.6.weight", "encoder.pre_encode.out.weight"}
 
 
-def _sub_weights(ud, seed, bf16):
+def _round_f16(a):
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def _sub_weights(ud, seed, half):
     w = ud.synthetic_subsampling_weights(seed)
-    oracle_w = {k: (ud.round_bf16(v) if bf16 and k in SUB_BF16 else v) for k, v in w.items()}
+    oracle_w = {k: (_round_f16(v) if half and k in SUB_HALF else v) for k, v in w.items()}
     return w, oracle_w
 
 
@@ -22,6 +27,17 @@ def _check(got, ref, bf16, what):
         harness.assert_bf16_close(got, ref, what)
     else:
         assert harness.rel_err(got, ref) <= 1e-4, what
+
+
+def _check_front(got, ref, half, what):
+    """Front-end output alone.  fp32: <= 1e-4 relative.  Half operands (activations rounded to
+    11-bit mantissas, fp32 accumulation): max abs error <= 2e-3 x max(1, max |ref|), cosine >= 0.99999."""
+    if not half:
+        assert harness.rel_err(got, ref) <= 1e-4, what
+        return
+    err = float(np.abs(got - ref).max())
+    cos = harness.cosine(got, ref)
+    assert err <= 2e-3 * max(1.0, float(np.abs(ref).max())) and cos >= 0.99999, "%s: err %.3g cos %.7f" % (what, err, cos)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -47,7 +63,7 @@ def test_subsample_matches_oracle(gpu, orc, dtype, rows, drop):
     got = obuf.download((n, T, 1024))
     for s in range(n):
         ref = orc.subsample(mel[s], int(valid[s]), ow)[drop:]
-        _check(got[s], ref, bf16, "stream %d (valid %d)" % (s, valid[s]))
+        _check_front(got[s], ref, bf16, "stream %d (valid %d)" % (s, valid[s]))
         v3 = orc.sub_next_len(orc.sub_next_len(orc.sub_next_len(max(int(valid[s]), 0))))
         assert vt[s] == min(max(v3 - drop, 0), T)
     enc.close()
@@ -72,7 +88,7 @@ def test_subsample_64_streams_chunk2_shape(gpu, orc):
     assert T == 2
     got = obuf.download((n, 2, 1024))
     ref = np.stack([orc.subsample(mel[s], int(valid[s]), ow)[2:] for s in range(n)])
-    harness.assert_bf16_close(got, ref, "64 streams")
+    _check_front(got, ref, True, "64 streams")
     enc.close()
 
 

@@ -324,6 +324,21 @@ static bool parse_name(const char* name, int layers, int* layer, int* slot) {
     return false;
 }
 
+// As upload_matrix, for the front-end GEMMs: a bf16 encoder stores these as IEEE half.
+static int upload_matrix_sub(ud_encoder* e, void* dst, const float* src, size_t rows, size_t cols) {
+    if (!e->bf) return upload(dst, src, rows * cols * 4);
+    std::vector<uint16_t> tmp(rows * cols);
+    const int nk = (int)(cols / 64);
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++) {
+            const _Float16 h = (_Float16)src[r * cols + c];
+            uint16_t b;
+            memcpy(&b, &h, 2);
+            tmp[frag_index((int64_t)r, (int)c, nk)] = b;
+        }
+    return upload(dst, tmp.data(), tmp.size() * 2);
+}
+
 static int set_sub_weight(ud_encoder* e, int slot, const char* name, const float* host, int64_t count) {
     const int64_t C = SUB_CH, D = e->D;
     int64_t want = C;
@@ -349,9 +364,9 @@ static int set_sub_weight(ud_encoder* e, int slot, const char* name, const float
             for (int64_t c = 0; c < C; c++)
                 for (int64_t f = 0; f < SUB_F3; f++)
                     perm[(size_t)((o * SUB_F3 + f) * C + c)] = host[(o * C + c) * SUB_F3 + f];
-        rc = upload_matrix(e, dst, 0, perm.data(), (size_t)D, (size_t)(C * SUB_F3));
+        rc = upload_matrix_sub(e, dst, perm.data(), (size_t)D, (size_t)(C * SUB_F3));
     } else if (gemm_w) {
-        rc = upload_matrix(e, dst, 0, host, (size_t)C, (size_t)C);
+        rc = upload_matrix_sub(e, dst, host, (size_t)C, (size_t)C);
     } else {
         rc = upload(dst, host, (size_t)want * 4);
     }
@@ -757,6 +772,7 @@ extern "C" UD_API int ud_encoder_subsample(ud_encoder* e, int32_t n, int32_t mel
         GemmArgs g{};
         g.A = A; g.W = u.w[slot_w]; g.C = C; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldw = K; g.ldc = N;
         g.epi = EPI_STORE_F32; g.act = act; g.out_scale = 1.0f; g.ksplit = 1; g.bias = (const float*)u.w[slot_b];
+        g.f16 = bf ? 1 : 0;
         return launch_status(launch_gemm(g, bf, st), what);
     };
     if ((rc = gemm(u.a2, SUB_C3W, SUB_C3B, u.a3, n * T2 * SUB_F2, SUB_CH, SUB_CH, ACT_RELU, "subsampling conv.3")))

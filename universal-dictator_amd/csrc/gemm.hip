@@ -49,23 +49,28 @@ __device__ __forceinline__ void load_frag(Frag<MT, NT>& f, const bf16* const* ap
     }
 }
 
-template <int MT, int NT>
+template <int MT, int NT, bool H>
 __device__ __forceinline__ void mma_frag(const Frag<MT, NT>& f, f32x4_t (&acc)[NT][MT]) {
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(f.a[mt][h]), as_bf16x8(f.b[nt][h]),
-                                                                      acc[nt][mt], 0, 0, 0);
+            for (int mt = 0; mt < MT; mt++) {
+                if constexpr (H)
+                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(f.a[mt][h]), as_f16x8(f.b[nt][h]),
+                                                                         acc[nt][mt], 0, 0, 0);
+                else
+                    acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(f.a[mt][h]), as_bf16x8(f.b[nt][h]),
+                                                                          acc[nt][mt], 0, 0, 0);
+            }
 }
 
 // Grid: (N/16) x ceil(M/(16*MT)) x ksplit workgroups of WK waves.  The host guarantees
 // K % (64 * WK * ksplit) == 0.  The epilogue kind and activation are template parameters: a
 // runtime-switched, fully unrolled epilogue measured ~3.5 us slower per launch on MI355X (its
 // code does not stay in the instruction cache).
-template <int MT, int WK, int EPI, int ACT, int NT>
+template <int MT, int WK, int EPI, int ACT, int NT, bool H = false, bool BIAS = false>
 __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
@@ -106,21 +111,21 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
     for (; i + 2 < cnt; i += 2) {
         load_frag(f1, ap, wp, off(i + 1));
         __builtin_amdgcn_sched_barrier(0);
-        mma_frag(f0, acc);
+        mma_frag<MT, NT, H>(f0, acc);
         __builtin_amdgcn_sched_barrier(0);
         load_frag(f0, ap, wp, off(i + 2));
         __builtin_amdgcn_sched_barrier(0);
-        mma_frag(f1, acc);
+        mma_frag<MT, NT, H>(f1, acc);
         __builtin_amdgcn_sched_barrier(0);
     }
     if (i + 1 < cnt) {
         load_frag(f1, ap, wp, off(i + 1));
         __builtin_amdgcn_sched_barrier(0);
-        mma_frag(f0, acc);
+        mma_frag<MT, NT, H>(f0, acc);
         __builtin_amdgcn_sched_barrier(0);
-        mma_frag(f1, acc);
+        mma_frag<MT, NT, H>(f1, acc);
     } else {
-        mma_frag(f0, acc);
+        mma_frag<MT, NT, H>(f0, acc);
     }
 
     if constexpr (WK > 1) {
@@ -151,7 +156,8 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
         for (int i2 = 0; i2 < 4; i2++) {
             const int64_t m = (int64_t)(mb * MT + mt) * 16 + g * 4 + i2;
             if (m >= a.M) continue;
-            const float v = acc[j][mt][i2] + (a.bias != nullptr && kz == 0 ? a.bias[n] : 0.0f);
+            float v = acc[j][mt][i2];
+            if constexpr (BIAS) v += kz == 0 ? a.bias[n] : 0.0f;
             if constexpr (EPI == EPI_PARTIAL) {
                 static_cast<float*>(a.C)[((int64_t)kz * a.M + m) * a.ldc + n] = a.out_scale * v;
             } else if constexpr (EPI == EPI_STORE_F32) {
@@ -222,7 +228,7 @@ __device__ __forceinline__ float act_fast(float x) {
 // the row operand), so each 16 x 16 accumulator holds C^T: a lane has 4 consecutive output columns
 // of one row, and the epilogue writes 16 bytes (fp32) or 8 bytes (bf16, row-major or
 // fragment-major) per lane.
-template <int NT, int EPI, int ACT>
+template <int NT, int EPI, int ACT, bool H = false, bool BIAS = false>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
     constexpr int MT = 8, BB = 4 * NT;                       // W blocks (16 columns each) per tile
     constexpr int STAGE = (16 + BB) * 1024, CPW = 4 + NT;    // CPW: 1 KB copies per wave per chunk
@@ -277,8 +283,12 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
         for (int j = j0; j < j1; j++)
 #pragma unroll
             for (int i = 0; i < MT; i++)
-                asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
-                             : "+a"(acc[j][i]) : "v"(as_bf16x8(fb[j])), "v"(as_bf16x8(fa[i])));
+                if constexpr (H)
+                    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"
+                                 : "+a"(acc[j][i]) : "v"(as_f16x8(fb[j])), "v"(as_f16x8(fa[i])));
+                else
+                    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+                                 : "+a"(acc[j][i]) : "v"(as_bf16x8(fb[j])), "v"(as_bf16x8(fa[i])));
     };
     copy_chunk(0, lds);
     __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0): this wave's direct loads landed
@@ -321,7 +331,9 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
         for (int j = 0; j < NT; j++) {
             const int n = (nb * BB + wn * NT + j) * 16 + g * 4;
             f32x4_t v = acc[j][i];
-            if (a.bias != nullptr && kz == 0) v += *reinterpret_cast<const f32x4_t*>(a.bias + n);
+            if constexpr (BIAS) {
+                if (kz == 0) v += *reinterpret_cast<const f32x4_t*>(a.bias + n);
+            }
             if constexpr (EPI == EPI_PARTIAL) {
                 *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.C) + ((int64_t)kz * a.M + m) * a.ldc + n) =
                     v * a.out_scale;
@@ -390,25 +402,25 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
 
 // ---------------------------------------------------------------- launch
 
-template <int MT, int WK, int NT, int EPI, int ACT>
+template <int MT, int WK, int NT, int EPI, int ACT, bool H = false, bool BIAS = false>
 static int launch_bf16_cfg(GemmArgs a, int ksplit, hipStream_t st) {
     if (a.N % (16 * NT) != 0 || ksplit < 1 || a.K % (64 * WK * ksplit) != 0) return -2;
     if (ksplit > 1 && EPI != EPI_PARTIAL) return -2;
     if (EPI == EPI_STORE_FRAG && a.N % 64 != 0) return -2;
     a.ksplit = ksplit;
     const int tiles = (a.N / (16 * NT)) * ((a.M + 16 * MT - 1) / (16 * MT)) * ksplit;
-    hipLaunchKernelGGL((gemm_bf16_kernel<MT, WK, EPI, ACT, NT>), dim3(tiles), dim3(64 * WK), 0, st, a);
+    hipLaunchKernelGGL((gemm_bf16_kernel<MT, WK, EPI, ACT, NT, H, BIAS>), dim3(tiles), dim3(64 * WK), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-template <int NT, int EPI, int ACT>
+template <int NT, int EPI, int ACT, bool H = false, bool BIAS = false>
 static int launch_lds_cfg(GemmArgs a, int ksplit, hipStream_t st) {
     if (a.N % (64 * NT) != 0 || ksplit < 1 || a.K % (64 * ksplit) != 0 || a.ldc % 4 != 0) return -2;
     if (ksplit > 1 && EPI != EPI_PARTIAL) return -2;
     if ((int64_t)((a.M + 15) / 16) * a.K * 16 >= (1ll << 31) || (int64_t)a.N * a.K >= (1ll << 31)) return -2;
     a.ksplit = ksplit;
     const int tiles = (a.N / (64 * NT)) * ((a.M + 255) / 256) * ksplit;
-    hipLaunchKernelGGL((gemm_bf16_lds_kernel<NT, EPI, ACT>), dim3(tiles), dim3(512), 0, st, a);
+    hipLaunchKernelGGL((gemm_bf16_lds_kernel<NT, EPI, ACT, H, BIAS>), dim3(tiles), dim3(512), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -495,7 +507,31 @@ static int launch_act(const GemmArgs& a, int ks, hipStream_t st) {
 //   split-K 4, K >= 4096 (ff linear2):           MT 4 x NT 2, 4 waves    7.8 -> 6.5 us
 //   split-K 4, K 1024 (linear_out, pw2):         MT 4 x NT 1, 2 waves    5.0 -> 3.7 us
 // Larger M keeps 128-row tiles (MT 8, 2 waves).
+// IEEE-half operands with a bias (the subsampling front-end's GEMMs): fp32 outputs, no activation
+// or ReLU.  The bias is a template parameter: a runtime-optional bias in the encoder's own GEMMs
+// made their epilogues larger and cost ~2 us per launch at 128 rows.
+template <int ACT>
+static int launch_f16(const GemmArgs& a, hipStream_t st) {
+    if (a.M <= 128 && a.N % 32 == 0 && a.K % 256 == 0) return launch_bf16_cfg<4, 4, 2, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+    if (a.M >= LDS_MIN_ROWS) {
+        switch (big_tile(a.M, a.N, a.K, false).nt) {
+            case 4: return launch_lds_cfg<4, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+            case 3: return launch_lds_cfg<3, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+            case 2: return launch_lds_cfg<2, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+            default: break;
+        }
+    }
+    return launch_bf16_cfg<8, 2, 1, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+}
+
 static int launch_bf16(const GemmArgs& a, int ks, hipStream_t st) {
+    if (a.f16) {
+        if (a.epi != EPI_STORE_F32 || ks != 1 || a.bias == nullptr) return -2;
+        if (a.act == ACT_NONE) return launch_f16<ACT_NONE>(a, st);
+        if (a.act == ACT_RELU) return launch_f16<ACT_RELU>(a, st);
+        return -2;
+    }
+    if (a.bias != nullptr) return -2;   // bf16 operands: the encoder's projections have no bias
     if (a.M <= 128) {
         switch (a.epi) {
             case EPI_STORE_FRAG:

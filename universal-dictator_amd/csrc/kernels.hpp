@@ -78,7 +78,10 @@ struct GemmArgs {
     int epi, act;
     float out_scale;
     int ksplit;                     // EPI_PARTIAL: K splits chosen by the caller (gemm_partial_splits)
-    const float* bias;              // optional [N], added before the activation (EPI_PARTIAL: by split 0)
+    const float* bias;              // [N] added before the activation: fp32 path (optional) and the
+                                    // IEEE-half path (required); not the bf16 path
+    int f16;                        // 16-bit path: operands are IEEE half instead of bf16
+                                    // (EPI_STORE_F32 with a bias only)
 };
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st);
 // Most K splits of a bf16 residual projection (partial slabs the workspace holds).
@@ -130,7 +133,7 @@ struct SubArgs {
     void* out;                      // conv.2 output as the conv.3 GEMM's A: [n*T2*F2, C]
     int n, T0, F0, T1, F1, T2, F2;
 };
-int launch_sub_conv01(const SubArgs& a, bool bf16_out, hipStream_t st);
+int launch_sub_conv01(const SubArgs& a, bool half_out, hipStream_t st);
 struct SubDwArgs {
     const float* x;                 // [n, Hin, Win, C] fp32
     const int32_t* vlen;
@@ -138,13 +141,13 @@ struct SubDwArgs {
     void* out;                      // [n*Hout*Wout, C] GEMM A operand
     int n, Hin, Win, Hout, Wout, stage;   // stage: vlen index of x's valid rows
 };
-int launch_sub_dw(const SubDwArgs& a, bool bf16_out, hipStream_t st);
+int launch_sub_dw(const SubDwArgs& a, bool half_out, hipStream_t st);
 struct SubFlatArgs {
     const float* x;                 // [n, T3, F3, C] fp32
     const int32_t* vlen;
     void* out;                      // [n*T, F3*C] GEMM A operand
     int n, T3, F3, T, drop;
 };
-int launch_sub_flatten(const SubFlatArgs& a, bool bf16_out, hipStream_t st);
+int launch_sub_flatten(const SubFlatArgs& a, bool half_out, hipStream_t st);
 
 }  // namespace ud

@@ -13,7 +13,9 @@
 //   out Linear (C*F3 -> D) + bias               GEMM, fp32 out = the encoder's input rows
 //
 // The GEMM operands (conv.3 / conv.6 inputs, the flattened rows) are written in the GEMM's A
-// layout: fragment-major bf16 for a bf16 encoder, row-major fp32 for an fp32 one.
+// layout: for a bf16 encoder fragment-major IEEE half (the front-end GEMMs run on the f16 MFMA:
+// 11-bit mantissas, where the reference keeps these convolutions in fp32 and its out Linear in f16,
+// Sources/DictatorEngine/Core/Convert.swift:74-83), row-major fp32 for an fp32 encoder.
 #include "ud_common.hpp"
 #include "kernels.hpp"
 
@@ -21,16 +23,16 @@ namespace ud {
 
 constexpr int SUB_C = 256;
 
-template <bool BF>
+template <bool H>
 __device__ __forceinline__ void store_a(void* A, int64_t m, int col, int cols, float v) {
-    if constexpr (BF) static_cast<bf16*>(A)[frag_index(m, col, cols / 64)] = f2bf(v);
+    if constexpr (H) static_cast<uint16_t*>(A)[frag_index(m, col, cols / 64)] = f2h(v);
     else static_cast<float*>(A)[m * cols + col] = v;
 }
 
 // One workgroup per conv.2 output position (stream s, time t2, freq f2); thread c = channel.
 // conv.2 tap (kh, kw) reads conv.0's output at (2 t2 + kh - 2, 2 f2 + kw - 2), which reads mel rows
 // 2 h + i - 2 = 4 t2 + 2 kh + i - 6 and columns 4 f2 + 2 kw + j - 6: a 7 x 7 patch.
-template <bool BF>
+template <bool H>
 __global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
     const int c = threadIdx.x;
     const int pos = blockIdx.x;                     // (s * T2 + t2) * F2 + f2
@@ -65,12 +67,12 @@ __global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
             acc += w2[kh * 3 + kw] * (y > 0.0f ? y : 0.0f);
         }
     }
-    store_a<BF>(a.out, pos, c, SUB_C, acc);
+    store_a<H>(a.out, pos, c, SUB_C, acc);
 }
 
 // Depthwise 3 x 3 stride-2 causal conv over x [n, Hin, Win, C] fp32 whose rows >= vlen[s][stage]
 // read as zero (the mask NeMo applies before this layer); one workgroup per output position.
-template <bool BF>
+template <bool H>
 __global__ __launch_bounds__(SUB_C) void sub_dw_kernel(SubDwArgs a) {
     const int c = threadIdx.x;
     const int pos = blockIdx.x;                     // (s * Hout + ho) * Wout + wo
@@ -88,13 +90,13 @@ __global__ __launch_bounds__(SUB_C) void sub_dw_kernel(SubDwArgs a) {
             acc += a.w[c * 9 + kh * 3 + kw] * a.x[(((int64_t)s * a.Hin + h) * a.Win + w) * SUB_C + c];
         }
     }
-    store_a<BF>(a.out, pos, c, SUB_C, acc);
+    store_a<H>(a.out, pos, c, SUB_C, acc);
 }
 
 // Rows of the out Linear: row (s, t) for t < T takes conv.6's output frame t3 = t + drop, zero when
 // t3 >= v3 (NeMo's final mask), flattened as (freq, channel) -- the column order the out weight
 // is permuted to at load.  One workgroup per row.
-template <bool BF>
+template <bool H>
 __global__ __launch_bounds__(SUB_C) void sub_flatten_kernel(SubFlatArgs a) {
     const int c = threadIdx.x;
     const int row = blockIdx.x, s = row / a.T, t3 = row % a.T + a.drop;
@@ -102,30 +104,30 @@ __global__ __launch_bounds__(SUB_C) void sub_flatten_kernel(SubFlatArgs a) {
     const float* src = a.x + (((int64_t)s * a.T3 + t3) * a.F3) * SUB_C;
     for (int f = 0; f < a.F3; f++) {
         const float v = valid ? src[f * SUB_C + c] : 0.0f;
-        store_a<BF>(a.out, row, f * SUB_C + c, a.F3 * SUB_C, v);
+        store_a<H>(a.out, row, f * SUB_C + c, a.F3 * SUB_C, v);
     }
 }
 
-int launch_sub_conv01(const SubArgs& a, bool bf, hipStream_t st) {
+int launch_sub_conv01(const SubArgs& a, bool half, hipStream_t st) {
     const int blocks = a.n * a.T2 * a.F2;
     if (blocks <= 0) return 0;
-    if (bf) hipLaunchKernelGGL(sub_conv01_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
+    if (half) hipLaunchKernelGGL(sub_conv01_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
     else hipLaunchKernelGGL(sub_conv01_kernel<false>, dim3(blocks), dim3(SUB_C), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_sub_dw(const SubDwArgs& a, bool bf, hipStream_t st) {
+int launch_sub_dw(const SubDwArgs& a, bool half, hipStream_t st) {
     const int blocks = a.n * a.Hout * a.Wout;
     if (blocks <= 0) return 0;
-    if (bf) hipLaunchKernelGGL(sub_dw_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
+    if (half) hipLaunchKernelGGL(sub_dw_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
     else hipLaunchKernelGGL(sub_dw_kernel<false>, dim3(blocks), dim3(SUB_C), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_sub_flatten(const SubFlatArgs& a, bool bf, hipStream_t st) {
+int launch_sub_flatten(const SubFlatArgs& a, bool half, hipStream_t st) {
     const int blocks = a.n * a.T;
     if (blocks <= 0) return 0;
-    if (bf) hipLaunchKernelGGL(sub_flatten_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
+    if (half) hipLaunchKernelGGL(sub_flatten_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
     else hipLaunchKernelGGL(sub_flatten_kernel<false>, dim3(blocks), dim3(SUB_C), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

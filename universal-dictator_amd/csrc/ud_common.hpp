@@ -28,6 +28,14 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
     __builtin_memcpy(&r, &v, 16);
     return r;
 }
+// IEEE half operands (v_mfma_f32_16x16x32_f16) in the same fragment layout.
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f16x8_t as_f16x8(uint4 v) {
+    f16x8_t r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
 template <typename T> __device__ __forceinline__ float to_f(T v);
 template <> __device__ __forceinline__ float to_f<float>(float v) { return v; }
