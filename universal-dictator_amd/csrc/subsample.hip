@@ -3,9 +3,9 @@
 // batched over streams.  Activations are channel-last [stream, time, freq, C = 256]; every stride-2
 // stage is a 3 x 3 causal conv with 2 zero rows/columns of top/left padding, L -> L/2 + 1.
 //
-//   conv.0 (1 -> C) + ReLU, rows >= v1 zero     } sub_conv01_kernel: conv.0 is recomputed for each
-//   conv.2 (depthwise)                          } depthwise tap (a 7 x 7 mel patch per output), so
-//                                                 its T1 x 65 x 256 activation never reaches HBM
+//   conv.0 (1 -> C) + ReLU, rows >= v1 zero     } sub_conv01_kernel: conv.0's outputs live in a
+//   conv.2 (depthwise)                          } register window per channel, so its
+//                                                 T1 x 65 x 256 activation never reaches HBM
 //   conv.3 (pointwise) + ReLU                   GEMM (bias epilogue), fp32 out
 //   rows >= v2 zero; conv.5 (depthwise)         sub_dw_kernel (mask applied on read)
 //   conv.6 (pointwise) + ReLU                   GEMM, fp32 out
@@ -29,68 +29,105 @@ __device__ __forceinline__ void store_a(void* A, int64_t m, int col, int cols, f
     else static_cast<float*>(A)[m * cols + col] = v;
 }
 
-// One workgroup per conv.2 output position (stream s, time t2, freq f2); thread c = channel.
-// conv.2 tap (kh, kw) reads conv.0's output at (2 t2 + kh - 2, 2 f2 + kw - 2), which reads mel rows
-// 2 h + i - 2 = 4 t2 + 2 kh + i - 6 and columns 4 f2 + 2 kw + j - 6: a 7 x 7 patch.
+// One workgroup per conv.2 output row (stream s, time t2); thread c = channel.  conv.2 output
+// (t2, f2) reads conv.0's output at rows 2 t2 - 2 .. 2 t2 and columns 2 f2 - 2 .. 2 f2; conv.0 at
+// (h, w) reads mel rows 2 h - 2 .. 2 h and columns 2 w - 2 .. 2 w.  The 7 mel rows 4 t2 - 6 ..
+// 4 t2 sit in LDS with 2 zero columns of left padding (rows outside the chunk or >= v0 are zero);
+// along the row each thread keeps a 3 x 3 window of its channel's conv.0 outputs in registers
+// and computes the 2 new columns per output position.
+constexpr int SUB_PW = 132;       // 2 + 128 mel columns, rounded up
+
 template <bool H>
 __global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
     const int c = threadIdx.x;
-    const int pos = blockIdx.x;                     // (s * T2 + t2) * F2 + f2
-    const int f2 = pos % a.F2, t2 = (pos / a.F2) % a.T2, s = pos / (a.F2 * a.T2);
+    const int t2 = blockIdx.x % a.T2, s = blockIdx.x / a.T2;
     const int v0 = a.vlen[s * 4 + 0], v1 = a.vlen[s * 4 + 1];
-    __shared__ float patch[7][8];
-    if (c < 49) {
-        const int pr = c / 7, pc = c % 7;
-        const int r = 4 * t2 - 6 + pr, q = 4 * f2 - 6 + pc;
+    __shared__ float patch[7][SUB_PW];
+    for (int i = c; i < 7 * SUB_PW; i += SUB_C) {
+        const int pr = i / SUB_PW, q = i % SUB_PW - 2;
+        const int r = 4 * t2 - 6 + pr;
         float v = 0.0f;
         if (r >= 0 && r < a.T0 && r < v0 && q >= 0 && q < a.F0) v = a.mel[((int64_t)s * a.T0 + r) * a.F0 + q];
-        patch[pr][pc] = v;
+        patch[pr][i % SUB_PW] = v;
     }
     float w0[9], w2[9];
 #pragma unroll
     for (int k = 0; k < 9; k++) { w0[k] = a.c0w[c * 9 + k]; w2[k] = a.c2w[c * 9 + k]; }
-    const float b0 = a.c0b[c];
-    float acc = a.c2b[c];
-    __syncthreads();
+    const float b0 = a.c0b[c], b2 = a.c2b[c];
+    bool hv[3];
 #pragma unroll
     for (int kh = 0; kh < 3; kh++) {
         const int h = 2 * t2 + kh - 2;
-#pragma unroll
-        for (int kw = 0; kw < 3; kw++) {
-            const int w = 2 * f2 + kw - 2;
-            if (h < 0 || h >= a.T1 || h >= v1 || w < 0 || w >= a.F1) continue;   // padding or masked row
-            float y = b0;
-#pragma unroll
-            for (int i = 0; i < 3; i++)
-#pragma unroll
-                for (int j = 0; j < 3; j++) y += w0[i * 3 + j] * patch[2 * kh + i][2 * kw + j];
-            acc += w2[kh * 3 + kw] * (y > 0.0f ? y : 0.0f);
-        }
+        hv[kh] = h >= 0 && h < a.T1 && h < v1;        // else padding or a masked row: zero
     }
-    store_a<H>(a.out, pos, c, SUB_C, acc);
+    __syncthreads();
+    // conv.0 + ReLU at (row 2 t2 + kh - 2, column w); patch column 2 w + j holds mel column 2 w + j - 2.
+    auto conv0 = [&](int kh, int w) -> float {
+        if (!hv[kh] || w < 0 || w >= a.F1) return 0.0f;
+        float y = b0;
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++) y += w0[i * 3 + j] * patch[2 * kh + i][2 * w + j];
+        return y > 0.0f ? y : 0.0f;
+    };
+    float win[3][3];
+#pragma unroll
+    for (int kh = 0; kh < 3; kh++) win[kh][2] = 0.0f;     // column -2
+    const int64_t row0 = ((int64_t)s * a.T2 + t2) * a.F2;
+    for (int f2 = 0; f2 < a.F2; f2++) {
+        float acc = b2;
+#pragma unroll
+        for (int kh = 0; kh < 3; kh++) {
+            win[kh][0] = win[kh][2];
+            win[kh][1] = conv0(kh, 2 * f2 - 1);
+            win[kh][2] = conv0(kh, 2 * f2);
+#pragma unroll
+            for (int kw = 0; kw < 3; kw++) acc += w2[kh * 3 + kw] * win[kh][kw];
+        }
+        store_a<H>(a.out, row0 + f2, c, SUB_C, acc);
+    }
 }
 
 // Depthwise 3 x 3 stride-2 causal conv over x [n, Hin, Win, C] fp32 whose rows >= vlen[s][stage]
-// read as zero (the mask NeMo applies before this layer); one workgroup per output position.
+// read as zero (the mask NeMo applies before this layer).  One workgroup per output row (s, ho);
+// each thread slides a 3 x 3 window of its channel along the row, so every input is loaded once.
 template <bool H>
 __global__ __launch_bounds__(SUB_C) void sub_dw_kernel(SubDwArgs a) {
     const int c = threadIdx.x;
-    const int pos = blockIdx.x;                     // (s * Hout + ho) * Wout + wo
-    const int wo = pos % a.Wout, ho = (pos / a.Wout) % a.Hout, s = pos / (a.Wout * a.Hout);
+    const int ho = blockIdx.x % a.Hout, s = blockIdx.x / a.Hout;
     const int vin = a.vlen[s * 4 + a.stage];
-    float acc = a.b[c];
+    float w[9];
+#pragma unroll
+    for (int k = 0; k < 9; k++) w[k] = a.w[c * 9 + k];
+    const float b = a.b[c];
+    const float* rows[3];
+    bool hv[3];
 #pragma unroll
     for (int kh = 0; kh < 3; kh++) {
         const int h = 2 * ho + kh - 2;
-        if (h < 0 || h >= a.Hin || h >= vin) continue;
-#pragma unroll
-        for (int kw = 0; kw < 3; kw++) {
-            const int w = 2 * wo + kw - 2;
-            if (w < 0 || w >= a.Win) continue;
-            acc += a.w[c * 9 + kh * 3 + kw] * a.x[(((int64_t)s * a.Hin + h) * a.Win + w) * SUB_C + c];
-        }
+        hv[kh] = h >= 0 && h < a.Hin && h < vin;
+        rows[kh] = a.x + (((int64_t)s * a.Hin + (hv[kh] ? h : 0)) * a.Win) * SUB_C + c;
     }
-    store_a<H>(a.out, pos, c, SUB_C, acc);
+    auto ld = [&](int kh, int col) -> float {
+        return (hv[kh] && col >= 0 && col < a.Win) ? rows[kh][(int64_t)col * SUB_C] : 0.0f;
+    };
+    float win[3][3];
+#pragma unroll
+    for (int kh = 0; kh < 3; kh++) win[kh][2] = 0.0f;     // column -2
+    const int64_t row0 = ((int64_t)s * a.Hout + ho) * a.Wout;
+    for (int wo = 0; wo < a.Wout; wo++) {
+        float acc = b;
+#pragma unroll
+        for (int kh = 0; kh < 3; kh++) {
+            win[kh][0] = win[kh][2];
+            win[kh][1] = ld(kh, 2 * wo - 1);
+            win[kh][2] = ld(kh, 2 * wo);
+#pragma unroll
+            for (int kw = 0; kw < 3; kw++) acc += w[kh * 3 + kw] * win[kh][kw];
+        }
+        store_a<H>(a.out, row0 + wo, c, SUB_C, acc);
+    }
 }
 
 // Rows of the out Linear: row (s, t) for t < T takes conv.6's output frame t3 = t + drop, zero when
@@ -109,7 +146,8 @@ __global__ __launch_bounds__(SUB_C) void sub_flatten_kernel(SubFlatArgs a) {
 }
 
 int launch_sub_conv01(const SubArgs& a, bool half, hipStream_t st) {
-    const int blocks = a.n * a.T2 * a.F2;
+    if (a.F0 + 2 > SUB_PW || 2 * (a.F1 - 1) + 2 >= SUB_PW) return -2;
+    const int blocks = a.n * a.T2;
     if (blocks <= 0) return 0;
     if (half) hipLaunchKernelGGL(sub_conv01_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
     else hipLaunchKernelGGL(sub_conv01_kernel<false>, dim3(blocks), dim3(SUB_C), 0, st, a);
@@ -117,7 +155,7 @@ int launch_sub_conv01(const SubArgs& a, bool half, hipStream_t st) {
 }
 
 int launch_sub_dw(const SubDwArgs& a, bool half, hipStream_t st) {
-    const int blocks = a.n * a.Hout * a.Wout;
+    const int blocks = a.n * a.Hout;
     if (blocks <= 0) return 0;
     if (half) hipLaunchKernelGGL(sub_dw_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
     else hipLaunchKernelGGL(sub_dw_kernel<false>, dim3(blocks), dim3(SUB_C), 0, st, a);
