@@ -295,3 +295,58 @@ def subsample(mel, valid_mel, sw, C=256, D=1024):
     got = lib().orc_subsample(_p(mel), T0, F0, int(valid_mel), ptrs, C, D, _p(out))
     assert got == T3
     return out
+
+
+def rnnt_weight_names(layers=2):
+    """RNN-T prediction + joint tensors (RNNTDecoder.init, RNNT.swift:27-63) in the oracle's order."""
+    names = ["decoder.prediction.embed.weight"]
+    for l in range(layers):
+        names += ["decoder.prediction.dec_rnn.lstm.%s_l%d" % (k, l) for k in ("weight_ih", "weight_hh", "bias_ih", "bias_hh")]
+    return names + ["joint.pred.weight", "joint.pred.bias", "joint.joint_net.2.weight", "joint.joint_net.2.bias"]
+
+
+class RnntState:
+    """RNNTDecoder.State (RNNT.swift:18-26) of one stream: committed h, c [L, H], last token, and
+    the cached prediction for it (committed when a non-blank token is emitted)."""
+
+    def __init__(self, H, V, L):
+        self.h = np.zeros((L, H), np.float32)
+        self.c = np.zeros((L, H), np.float32)
+        self.last = np.array([V - 1], np.int32)
+        self.pending = np.zeros(1, np.int32)
+        self.pproj = np.zeros(H, np.float32)
+        self.ph = np.zeros((L, H), np.float32)
+        self.pc = np.zeros((L, H), np.float32)
+
+
+class Rnnt:
+    """Oracle RNN-T decoder over a dict of checkpoint tensors."""
+
+    def __init__(self, w, max_symbols=10):
+        self.V, self.H = np.asarray(w["decoder.prediction.embed.weight"]).shape
+        self.L = 0
+        while "decoder.prediction.dec_rnn.lstm.weight_ih_l%d" % self.L in w:
+            self.L += 1
+        self._keep = [_f32(w[n]).reshape(-1) for n in rnnt_weight_names(self.L)]
+        self._ptrs = (_f32p * len(self._keep))(*[_p(a) for a in self._keep])
+        self.max_symbols = max_symbols
+
+    def state(self):
+        return RnntState(self.H, self.V, self.L)
+
+    def greedy(self, enc_proj, st, cap=4096):
+        """Greedy decode of projected frames [frames, H] from state st (updated); returns the tokens."""
+        enc_proj = _f32(enc_proj)
+        toks = np.zeros(cap, np.int32)
+        n = lib().orc_rnnt_greedy(self._ptrs, self.H, self.V, self.L, _p(enc_proj), enc_proj.shape[0], self.max_symbols,
+                                  _p(st.h), _p(st.c), _ip(st.last), _ip(st.pending), _p(st.pproj), _p(st.ph),
+                                  _p(st.pc), _ip(toks), cap)
+        return [int(t) for t in toks[:min(n, cap)]]
+
+    def predict(self, token, h, c):
+        proj = np.zeros(self.H, np.float32)
+        ho = np.zeros((self.L, self.H), np.float32)
+        co = np.zeros((self.L, self.H), np.float32)
+        lib().orc_rnnt_predict(self._ptrs, self.H, self.V, self.L, int(token), _p(_f32(h)), _p(_f32(c)), _p(proj),
+                               _p(ho), _p(co))
+        return proj, ho, co

@@ -39,6 +39,10 @@
  *                         ConvSubsampling with MaskedConvSequential length
  *                         masks and the (channel, freq) flatten on the
  *                         checkpoint's out.weight (tests/refimpl.py)
+ *   orc_rnnt_*            torch.nn.LSTMCell prediction network and NeMo's
+ *                         greedy loop without a prediction cache
+ *                         (reference/nemo/check_spec.py:176-207 structure,
+ *                         tests/refimpl.py), across chunk boundaries
  */
 #include <math.h>
 #include <stdint.h>
@@ -569,4 +573,100 @@ ORC_API int orc_subsample(const float* mel, int T0, int F0, int valid_mel, const
     orc_gemm_nt(a5, wp, sw[11], NULL, out, T3, D, F3 * C, 1.0f, ORC_ACT_NONE, 1.0f, 0.0f);
     free(x0); free(a1); free(a2); free(a3); free(a4); free(a5); free(wp);
     return T3;
+}
+
+/* ------------------------------------------------------------------ RNN-T decoder (CPU in the reference) */
+
+/* Weights, Sources/DictatorCore/Decoding/RNNT.swift:27-63: w[0] embed [V, H]; per layer l:
+ * w[1+4l] weight_ih [4H, H], w[2+4l] weight_hh [4H, H], w[3+4l] bias_ih, w[4+4l] bias_hh; then
+ * joint.pred weight [H, H] and bias, joint.joint_net.2 weight [V, H] and bias.  Gate order i, f, g, o. */
+typedef struct {
+    const float* const* w;
+    int H, V, L;
+} OrcRnnt;
+
+static double orc_sigmoid(double x) { return 1.0 / (1.0 + exp(-x)); }
+
+/* RNNT.swift:73-107 (predict): x = embed[token] (zeros for blank), per layer gates = b_ih + b_hh +
+ * W_ih x + W_hh h, c' = f c + i g, h' = o tanh(c'), next layer input h'; proj = joint.pred(h_top). */
+ORC_API void orc_rnnt_predict(const float* const* w, int H, int V, int L, int token, const float* h, const float* c,
+                              float* proj, float* h_out, float* c_out) {
+    const int blank = V - 1;
+    float* x = (float*)calloc((size_t)H, sizeof(float));
+    float* gates = (float*)malloc((size_t)4 * H * sizeof(float));
+    if (token != blank) memcpy(x, w[0] + (int64_t)token * H, (size_t)H * sizeof(float));
+    for (int l = 0; l < L; l++) {
+        const float *wih = w[1 + 4 * l], *whh = w[2 + 4 * l], *bih = w[3 + 4 * l], *bhh = w[4 + 4 * l];
+        const float* hl = h + (int64_t)l * H;
+        for (int r = 0; r < 4 * H; r++) {
+            double a = (double)bih[r] + (double)bhh[r];
+            for (int k = 0; k < H; k++) a += (double)wih[(int64_t)r * H + k] * x[k] + (double)whh[(int64_t)r * H + k] * hl[k];
+            gates[r] = (float)a;
+        }
+        for (int j = 0; j < H; j++) {
+            const double ig = orc_sigmoid(gates[j]), fg = orc_sigmoid(gates[H + j]), gg = tanh((double)gates[2 * H + j]),
+                         og = orc_sigmoid(gates[3 * H + j]);
+            const double cn = fg * c[(int64_t)l * H + j] + ig * gg;
+            c_out[(int64_t)l * H + j] = (float)cn;
+            h_out[(int64_t)l * H + j] = (float)(og * tanh(cn));
+        }
+        memcpy(x, h_out + (int64_t)l * H, (size_t)H * sizeof(float));
+    }
+    const float *pw = w[1 + 4 * L], *pb = w[2 + 4 * L];
+    for (int j = 0; j < H; j++) {
+        double a = pb[j];
+        for (int k = 0; k < H; k++) a += (double)pw[(int64_t)j * H + k] * x[k];
+        proj[j] = (float)a;
+    }
+    free(x);
+    free(gates);
+}
+
+/* RNNT.swift:110-116 (jointLogits) + the argmax of :137-139 (first index of the maximum). */
+ORC_API int orc_rnnt_joint_argmax(const float* const* w, int H, int V, int L, const float* enc, const float* pred,
+                                  float* logits) {
+    const float *ow = w[3 + 4 * L], *ob = w[4 + 4 * L];
+    int best = 0;
+    for (int v = 0; v < V; v++) {
+        double a = ob[v];
+        for (int k = 0; k < H; k++) {
+            const float hs = enc[k] + pred[k];
+            a += (double)ow[(int64_t)v * H + k] * (hs > 0 ? hs : 0.0f);
+        }
+        logits[v] = (float)a;
+        if (logits[v] > logits[best]) best = v;
+    }
+    return best;
+}
+
+/* RNNT.swift:120-151 (greedy) over `frames` projected encoder frames [frames, H].  State
+ * (carried across calls): h, c [L, H]; *last_token; *pending with pend_proj [H], pend_h/pend_c
+ * [L, H] (the prediction for last_token, committed only when a non-blank token is emitted).
+ * Appends up to cap tokens; returns the number appended. */
+ORC_API int orc_rnnt_greedy(const float* const* w, int H, int V, int L, const float* enc, int frames, int max_symbols,
+                            float* h, float* c, int* last_token, int* pending, float* pend_proj, float* pend_h,
+                            float* pend_c, int* tokens, int cap) {
+    const int blank = V - 1;
+    float* logits = (float*)malloc((size_t)V * sizeof(float));
+    int n = 0;
+    for (int t = 0; t < frames; t++) {
+        int emitted = 0;
+        while (emitted < max_symbols) {
+            if (!*pending) {
+                orc_rnnt_predict(w, H, V, L, *last_token, h, c, pend_proj, pend_h, pend_c);
+                *pending = 1;
+            }
+            const int best = orc_rnnt_joint_argmax(w, H, V, L, enc + (int64_t)t * H, pend_proj, logits);
+            if (best == blank) break;
+            if (n < cap) tokens[n] = best;
+            n++;
+            emitted++;
+            memcpy(h, pend_h, (size_t)L * H * sizeof(float));
+            memcpy(c, pend_c, (size_t)L * H * sizeof(float));
+            *last_token = best;
+            *pending = 0;
+        }
+    }
+    free(logits);
+    return n;
 }

@@ -120,3 +120,57 @@ def subsampling_nemo(mel, valid, w):
     _, Cc, T, Fq = x.shape
     x = x.transpose(1, 2).reshape(1, T, Cc * Fq)
     return F.linear(x, t("out.weight"), t("out.bias"))[0]
+
+
+def rnnt_greedy_nemo(f, w, state=None, max_symbols=10):
+    """NeMo greedy RNN-T (reference/nemo/check_spec.py:176-207 structure; docs/specs/nemotron.md §7)
+    on projected encoder frames f [T, H] (joint.enc applied), float64 torch with torch.nn.LSTMCell,
+    with no prediction cache: the prediction is recomputed from the committed state whenever the
+    loop needs it.  state (dict h, c: lists of [H], token) carries across calls; returns tokens."""
+    import torch
+    import torch.nn.functional as F
+    t_ = lambda n: torch.as_tensor(np.asarray(w[n]), dtype=torch.float64)
+    emb = t_("decoder.prediction.embed.weight")
+    V, H = emb.shape
+    blank = V - 1
+    L = 0
+    while "decoder.prediction.dec_rnn.lstm.weight_ih_l%d" % L in w:
+        L += 1
+    cells = []
+    for l in range(L):
+        cell = torch.nn.LSTMCell(H, H).double()
+        with torch.no_grad():
+            cell.weight_ih.copy_(t_("decoder.prediction.dec_rnn.lstm.weight_ih_l%d" % l))
+            cell.weight_hh.copy_(t_("decoder.prediction.dec_rnn.lstm.weight_hh_l%d" % l))
+            cell.bias_ih.copy_(t_("decoder.prediction.dec_rnn.lstm.bias_ih_l%d" % l))
+            cell.bias_hh.copy_(t_("decoder.prediction.dec_rnn.lstm.bias_hh_l%d" % l))
+        cells.append(cell)
+    if state is None:
+        state = dict(h=[torch.zeros(H, dtype=torch.float64) for _ in range(L)],
+                     c=[torch.zeros(H, dtype=torch.float64) for _ in range(L)], token=blank)
+
+    def pred(tok, hs, cs):
+        x = torch.zeros(H, dtype=torch.float64) if tok == blank else emb[tok]
+        nh, nc = [], []
+        with torch.no_grad():
+            for l, cell in enumerate(cells):
+                hh, cc = cell(x[None], (hs[l][None], cs[l][None]))
+                nh.append(hh[0])
+                nc.append(cc[0])
+                x = hh[0]
+        return F.linear(x, t_("joint.pred.weight"), t_("joint.pred.bias")), nh, nc
+
+    f = torch.as_tensor(np.asarray(f), dtype=torch.float64)
+    toks = []
+    for t in range(f.shape[0]):
+        n = 0
+        while n < max_symbols:
+            g, nh, nc = pred(state["token"], state["h"], state["c"])
+            logits = F.linear(F.relu(f[t] + g), t_("joint.joint_net.2.weight"), t_("joint.joint_net.2.bias"))
+            k = int(torch.argmax(logits))
+            if k == blank:
+                break
+            toks.append(k)
+            state["h"], state["c"], state["token"] = nh, nc, k
+            n += 1
+    return toks, state

@@ -94,6 +94,12 @@ def _sig(lib):
                                        ctypes.c_size_t, p]),
         "ud_rope_rotate_half": (i, [_i32, p, _i32, _i32, _i32, _i32, p, _i32, p, p]),
         "ud_paged_kv_append": (i, [_i32, p, p, p, p, p, _i32, p, _i32, _i32, _i32, _i32, p]),
+        "ud_rnnt_create": (i, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_vp)]),
+        "ud_rnnt_destroy": (v, [p]),
+        "ud_rnnt_set_weight": (i, [p, ctypes.c_char_p, f, ctypes.c_int64]),
+        "ud_rnnt_reset": (i, [p, _i32]),
+        "ud_rnnt_project": (i, [p, _i32, p, p, p]),
+        "ud_rnnt_greedy": (i, [p, _i32, ip, p, _i32, ip, ip, _i32, ip, p]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -509,6 +515,57 @@ def synthetic_layer_weights(cfg, seed, layer, ln_jitter=0.1):
     return w
 
 
+class Rnnt:
+    """RNN-T joint + greedy decoder for a pool of stream slots (include/ud_rnnt.h), mirroring
+    RNNTDecoder (Sources/DictatorCore/Decoding/RNNT.swift): set_weights, project (joint.enc),
+    greedy over projected frames with per-slot state carried across calls."""
+
+    def __init__(self, max_streams, hidden=640, vocab=1025, layers=2, enc_dim=1024, max_symbols=10):
+        p = _vp()
+        _check(lib().ud_rnnt_create(hidden, vocab, layers, enc_dim, max_streams, max_symbols, ctypes.byref(p)))
+        self.handle = p.value
+        self.H, self.V, self.L, self.E, self.S = hidden, vocab, layers, enc_dim, max_streams
+
+    def set_weights(self, weights):
+        """weights: dict of checkpoint tensors (as synthetic_rnnt_weights returns)."""
+        for name, a in weights.items():
+            a = np.ascontiguousarray(a, np.float32)
+            _check(_lib.ud_rnnt_set_weight(self.handle, name.encode(),
+                                           a.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), a.size))
+
+    def reset(self, slot):
+        _check(_lib.ud_rnnt_reset(self.handle, int(slot)))
+
+    def project(self, rows, enc, out, hip_stream=None):
+        """out [rows, hidden] = joint.enc(enc [rows, enc_dim]); DeviceBuffers of fp32."""
+        _check(_lib.ud_rnnt_project(self.handle, int(rows), enc.ptr, out.ptr, hip_stream.ptr if hip_stream else None))
+
+    def greedy(self, slots, proj, rows_per_stream, frames, cap=4096, hip_stream=None):
+        """Greedy decode: proj a DeviceBuffer of fp32 [len(slots) * rows_per_stream, hidden];
+        returns a list of token lists (and the full emitted counts)."""
+        n = len(slots)
+        sl = np.ascontiguousarray(slots, np.int32)
+        fr = np.ascontiguousarray(frames, np.int32)
+        toks = np.zeros((n, max(cap, 1)), np.int32)
+        cnt = np.zeros(n, np.int32)
+        P = ctypes.POINTER(_i32)
+        _check(_lib.ud_rnnt_greedy(self.handle, n, sl.ctypes.data_as(P), proj.ptr, int(rows_per_stream),
+                                   fr.ctypes.data_as(P), toks.ctypes.data_as(P), int(cap), cnt.ctypes.data_as(P),
+                                   hip_stream.ptr if hip_stream else None))
+        return [list(map(int, toks[b, :min(cnt[b], cap)])) for b in range(n)], cnt
+
+    def close(self):
+        if self.handle:
+            _lib.ud_rnnt_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 SUB_CHANNELS, MEL_BINS = 256, 128
 
 
@@ -537,6 +594,34 @@ def synthetic_subsampling_weights(seed, D=1024, C=SUB_CHANNELS, mel_bins=MEL_BIN
     for i in (3, 6):
         w[p + "conv.%d.weight" % i], w[p + "conv.%d.bias" % i] = xavier((C, C, 1, 1), C, C), bias(C, C)
     w[p + "out.weight"], w[p + "out.bias"] = xavier((D, C * F3), C * F3, D), bias(D, C * F3)
+    return w
+
+
+def synthetic_rnnt_weights(seed, H=640, V=1025, L=2, enc_dim=1024, blank_bias=0.0):
+    """Random-init RNN-T prediction and joint networks in the checkpoint layout (torch's LSTM and
+    Linear init: U(-1/sqrt(H), 1/sqrt(H)) for the LSTM, U(-1/sqrt(fan_in), +) for the Linears,
+    embedding N(0, 1) with the blank row zero), joint.enc included.  blank_bias is added to the
+    blank logit's bias, which sets how often the greedy loop emits."""
+    rng = np.random.default_rng([int(seed), 1 << 21])
+
+    def u(shape, bound):
+        return ((rng.random(shape, dtype=np.float32) * 2 - 1) * np.float32(bound)).astype(np.float32)
+
+    w = {}
+    emb = rng.standard_normal((V, H), dtype=np.float32)
+    emb[V - 1] = 0.0
+    w["decoder.prediction.embed.weight"] = emb
+    k = 1.0 / np.sqrt(H)
+    for l in range(L):
+        p = "decoder.prediction.dec_rnn.lstm."
+        w[p + "weight_ih_l%d" % l] = u((4 * H, H), k)
+        w[p + "weight_hh_l%d" % l] = u((4 * H, H), k)
+        w[p + "bias_ih_l%d" % l] = u(4 * H, k)
+        w[p + "bias_hh_l%d" % l] = u(4 * H, k)
+    w["joint.pred.weight"], w["joint.pred.bias"] = u((H, H), k), u(H, k)
+    w["joint.enc.weight"], w["joint.enc.bias"] = u((H, enc_dim), 1 / np.sqrt(enc_dim)), u(H, 1 / np.sqrt(enc_dim))
+    w["joint.joint_net.2.weight"], w["joint.joint_net.2.bias"] = u((V, H), k), u(V, k)
+    w["joint.joint_net.2.bias"][V - 1] += np.float32(blank_bias)
     return w
 
 

@@ -365,13 +365,17 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
     const int tid = threadIdx.x;
     const int m0 = blockIdx.y * F_BM, n0 = blockIdx.x * F_BN;
     const int tm = (tid / 16) * 4, tn = (tid % 16) * 4;
+    // EPI_PARTIAL: blockIdx.z = K split kz over K range [kb, ke), its own fp32 slab.
+    const int kz = blockIdx.z;
+    const int kper = (a.K + (int)gridDim.z - 1) / (int)gridDim.z;
+    const int kb = kz * kper, ke = min(a.K, kb + kper);
     float acc[4][4] = {};
-    for (int k0 = 0; k0 < a.K; k0 += F_BK) {
+    for (int k0 = kb; k0 < ke; k0 += F_BK) {
         for (int idx = tid; idx < F_BM * F_BK; idx += 256) {
             int r = idx / F_BK, kk = idx % F_BK;
             int m = m0 + r, n = n0 + r, k = k0 + kk;
-            As[kk][r] = (m < a.M && k < a.K) ? A[(int64_t)m * a.lda + k] : 0.0f;
-            Ws[kk][r] = (n < a.N && k < a.K) ? W[(int64_t)n * a.ldw + k] : 0.0f;
+            As[kk][r] = (m < a.M && k < ke) ? A[(int64_t)m * a.lda + k] : 0.0f;
+            Ws[kk][r] = (n < a.N && k < ke) ? W[(int64_t)n * a.ldw + k] : 0.0f;
         }
         __syncthreads();
 #pragma unroll
@@ -392,9 +396,10 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
         for (int j = 0; j < 4; j++) {
             int n = n0 + tn + j;
             if (n >= a.N) continue;
-            float* C = static_cast<float*>(a.C) + (int64_t)m * a.ldc + n;
-            if (a.bias != nullptr) acc[i][j] += a.bias[n];
+            float* C = static_cast<float*>(a.C) + ((int64_t)kz * a.M + m) * a.ldc + n;
+            if (a.bias != nullptr && kz == 0) acc[i][j] += a.bias[n];
             if (a.epi == EPI_RESID) *C = *C + a.out_scale * acc[i][j];
+            else if (a.epi == EPI_PARTIAL) *C = a.out_scale * acc[i][j];
             else *C = apply_act(acc[i][j], a.act) * a.out_scale;
         }
     }
@@ -575,7 +580,9 @@ int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st) {
     if (a.M <= 0 || a.N <= 0 || a.K <= 0) return -2;
     if (!bf16_data) {
         if (a.epi == EPI_STORE_FRAG) return -2;
-        dim3 grid((a.N + F_BN - 1) / F_BN, (a.M + F_BM - 1) / F_BM);
+        const int ks = a.epi == EPI_PARTIAL ? a.ksplit : 1;
+        if (ks < 1 || ks > 64) return -2;
+        dim3 grid((a.N + F_BN - 1) / F_BN, (a.M + F_BM - 1) / F_BM, ks);
         hipLaunchKernelGGL(gemm_f32_kernel, grid, dim3(256), 0, st, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }

@@ -1,0 +1,437 @@
+// RNN-T joint and greedy decoding, batched over streams (include/ud_rnnt.h).
+//
+// The reference decodes one stream at a time on the CPU (Sources/DictatorCore/Decoding/RNNT.swift):
+// per emitted token one prediction step (embedding, 2 LSTM layers of [4H, 2H] sgemv, joint.pred)
+// and per (frame, symbol) one joint evaluation ([V, H] sgemv).  Here one greedy iteration does
+// that work for every active stream of the call at once, as fp32 GEMMs over M = active streams
+// (the weights are read once per iteration, not once per stream), with split-K partial slabs that
+// the following pointwise kernel sums in a fixed order (deterministic, no atomics):
+//
+//   predict (streams without a cached prediction):
+//     rnnt_embed_kernel        xh = [embed(last token) ; h_0]
+//     per layer: GEMM xh . [W_ih | W_hh]^T -> slabs;  rnnt_cell_kernel: gates = b + sum(slabs),
+//                c' = f c + i g, h' = o tanh(c') -> cached state; xh = [h' ; h_{l+1}]
+//     GEMM h_top . W_pred^T -> slabs;  rnnt_sum_kernel -> cached projection g
+//   joint (all active streams):
+//     rnnt_joint_in_kernel     relu(f_t + g)
+//     GEMM . W_out^T -> slabs; rnnt_argmax_kernel: logits = b + sum(slabs), first index of the max
+//   commit (streams that emitted a token): rnnt_commit_kernel, h, c <- cached state
+//
+// The host keeps the greedy control (RNNT.swift:120-151): blank ends a frame, at most
+// max_symbols tokens per frame, and the prediction for the last token is cached until a token is
+// emitted (so frames that end in blank do not rerun the LSTM).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/ud_rnnt.h"
+#include "kernels.hpp"
+#include "ud_common.hpp"
+
+int ud_set_error(int code, const char* msg);   // encoder.hip
+
+namespace ud {
+
+constexpr int RNNT_KS = 8;          // K splits of the decoder GEMMs
+
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// xh[b] = [x ; h[slot][0]] with x = embed[tok] (zeros for blank, NeMo's padding row).
+__global__ void rnnt_embed_kernel(const float* __restrict__ embed, const int32_t* __restrict__ slot,
+                                  const int32_t* __restrict__ tok, const float* __restrict__ h, float* __restrict__ xh,
+                                  int H, int L, int blank) {
+    const int b = blockIdx.x, s = slot[b], t = tok[b];
+    for (int j = threadIdx.x; j < H; j += blockDim.x) {
+        xh[(int64_t)b * 2 * H + j] = t == blank ? 0.0f : embed[(int64_t)t * H + j];
+        xh[(int64_t)b * 2 * H + H + j] = h[((int64_t)s * L + 0) * H + j];
+    }
+}
+
+// One LSTM layer's cell from the gate slabs [ks][n][4H]; writes the cached state of the slot and
+// the next layer's input row.
+__global__ void rnnt_cell_kernel(const float* __restrict__ slabs, int ks, int n, const float* __restrict__ bias,
+                                 const float* __restrict__ h, const float* __restrict__ c, float* __restrict__ ph,
+                                 float* __restrict__ pc, float* __restrict__ xh, const int32_t* __restrict__ slot,
+                                 int H, int L, int layer) {
+    const int b = blockIdx.x, s = slot[b];
+    const int64_t G = 4 * (int64_t)H;
+    for (int j = threadIdx.x; j < H; j += blockDim.x) {
+        float g[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float v = bias[q * H + j];
+            for (int z = 0; z < ks; z++) v += slabs[((int64_t)z * n + b) * G + q * H + j];
+            g[q] = v;
+        }
+        const float ig = sigmoid_f(g[0]), fg = sigmoid_f(g[1]), gg = tanhf(g[2]), og = sigmoid_f(g[3]);
+        const int64_t si = ((int64_t)s * L + layer) * H + j;
+        const float cn = fg * c[si] + ig * gg;
+        const float hn = og * tanhf(cn);
+        pc[si] = cn;
+        ph[si] = hn;
+        xh[(int64_t)b * 2 * H + j] = hn;
+        if (layer + 1 < L) xh[(int64_t)b * 2 * H + H + j] = h[((int64_t)s * L + layer + 1) * H + j];
+    }
+}
+
+// out[slot(b)] (or out[b] when slot is null) = bias + sum of the slabs [ks][n][N].
+__global__ void rnnt_sum_kernel(const float* __restrict__ slabs, int ks, int n, const float* __restrict__ bias,
+                                float* __restrict__ out, const int32_t* __restrict__ slot, int N) {
+    const int b = blockIdx.x;
+    const int64_t o = (int64_t)(slot ? slot[b] : b) * N;
+    for (int j = threadIdx.x; j < N; j += blockDim.x) {
+        float v = bias[j];
+        for (int z = 0; z < ks; z++) v += slabs[((int64_t)z * n + b) * N + j];
+        out[o + j] = v;
+    }
+}
+
+// hsum[b] = relu(f[erow(b)] + g[slot(b)]).
+__global__ void rnnt_joint_in_kernel(const float* __restrict__ f, const int32_t* __restrict__ erow,
+                                     const float* __restrict__ g, const int32_t* __restrict__ slot,
+                                     float* __restrict__ hsum, int H) {
+    const int b = blockIdx.x;
+    const float* fr = f + (int64_t)erow[b] * H;
+    const float* gr = g + (int64_t)slot[b] * H;
+    for (int j = threadIdx.x; j < H; j += blockDim.x) {
+        const float v = fr[j] + gr[j];
+        hsum[(int64_t)b * H + j] = v > 0.0f ? v : 0.0f;
+    }
+}
+
+// best[b] = the first index of the maximum of bias + sum of the slabs [ks][n][V].
+__global__ __launch_bounds__(256) void rnnt_argmax_kernel(const float* __restrict__ slabs, int ks, int n,
+                                                          const float* __restrict__ bias, int32_t* __restrict__ best,
+                                                          int V) {
+    const int b = blockIdx.x;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int v = threadIdx.x; v < V; v += blockDim.x) {
+        float x = bias[v];
+        for (int z = 0; z < ks; z++) x += slabs[((int64_t)z * n + b) * V + v];
+        if (x > bv) { bv = x; bi = v; }        // ascending v per thread: keeps the first maximum
+    }
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) {
+            const float ov = sv[threadIdx.x + w];
+            const int oi = si[threadIdx.x + w];
+            if (ov > sv[threadIdx.x] || (ov == sv[threadIdx.x] && oi < si[threadIdx.x])) {
+                sv[threadIdx.x] = ov;
+                si[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) best[b] = si[0];
+}
+
+// h, c of slot(b) <- the cached state (RNNT.swift:144-147).
+__global__ void rnnt_commit_kernel(const float* __restrict__ ph, const float* __restrict__ pc, float* __restrict__ h,
+                                   float* __restrict__ c, const int32_t* __restrict__ slot, int LH) {
+    const int64_t o = (int64_t)slot[blockIdx.x] * LH;
+    for (int j = threadIdx.x; j < LH; j += blockDim.x) {
+        h[o + j] = ph[o + j];
+        c[o + j] = pc[o + j];
+    }
+}
+
+}  // namespace ud
+
+using namespace ud;
+
+static int rfail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    return ud_set_error(code, buf);
+}
+
+#define RHIPC(call)                                                                              \
+    do {                                                                                         \
+        hipError_t e_ = (call);                                                                  \
+        if (e_ != hipSuccess) return rfail(UD_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_));  \
+    } while (0)
+#define RLAUNCH(what)                                                                            \
+    do {                                                                                         \
+        hipError_t e_ = hipGetLastError();                                                       \
+        if (e_ != hipSuccess) return rfail(UD_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e_)); \
+    } while (0)
+
+enum RSlot { R_EMBED, R_PRED_W, R_PRED_B, R_OUT_W, R_OUT_B, R_ENC_W, R_ENC_B, R_FIXED };
+
+struct ud_rnnt {
+    int H, V, L, E, S, max_sym;
+    float* w[R_FIXED] = {};
+    std::vector<float*> wcat, bias;             // per layer [4H][2H] = [W_ih | W_hh], b_ih + b_hh
+    std::vector<std::vector<float>> ih, hh, bih, bhh;   // host copies until both halves are set
+    uint32_t set_fixed = 0;
+    std::vector<uint32_t> set_layer;            // bit 0..3: weight_ih, weight_hh, bias_ih, bias_hh
+    // per-slot state: committed h, c [S][L][H]; cached prediction ph, pc [S][L][H], pg [S][H]
+    float *h = nullptr, *c = nullptr, *ph = nullptr, *pc = nullptr, *pg = nullptr;
+    std::vector<int> last, pending;
+    // workspace
+    float *xh = nullptr, *slabs = nullptr, *hsum = nullptr;
+    // slot lists of the three phases in separate buffers: no upload overwrites a list that an
+    // earlier kernel of the same iteration may still read
+    int32_t *dslot_p = nullptr, *dslot_j = nullptr, *dslot_c = nullptr, *dtok = nullptr, *drow = nullptr, *dbest = nullptr;
+    int32_t* hbest = nullptr;                   // pinned
+};
+
+static float* ralloc(size_t floats) {
+    void* p = nullptr;
+    if (hipMalloc(&p, floats ? floats * 4 : 16) != hipSuccess) return nullptr;
+    return static_cast<float*>(p);
+}
+
+static void free_rnnt(ud_rnnt* r) {
+    if (!r) return;
+    (void)hipDeviceSynchronize();
+    for (float* p : r->w) if (p) (void)hipFree(p);
+    for (float* p : r->wcat) if (p) (void)hipFree(p);
+    for (float* p : r->bias) if (p) (void)hipFree(p);
+    void* ps[] = {r->h, r->c, r->ph, r->pc, r->pg, r->xh, r->slabs, r->hsum, r->dslot_p, r->dslot_j, r->dslot_c,
+                  r->dtok, r->drow, r->dbest};
+    for (void* p : ps) if (p) (void)hipFree(p);
+    if (r->hbest) (void)hipHostFree(r->hbest);
+    delete r;
+}
+
+extern "C" UD_API int ud_rnnt_create(int32_t hidden, int32_t vocab, int32_t layers, int32_t enc_dim,
+                                     int32_t max_streams, int32_t max_symbols_per_frame, ud_rnnt** out) {
+    if (!out) return rfail(UD_ERR_INVALID, "ud_rnnt_create: null out pointer");
+    *out = nullptr;
+    if (hidden < 1 || vocab < 2 || layers < 1 || layers > 8 || enc_dim < 1 || max_streams < 1 || max_symbols_per_frame < 1)
+        return rfail(UD_ERR_SHAPE, "ud_rnnt_create: bad dimensions");
+    ud_rnnt* r = new ud_rnnt();
+    r->H = hidden; r->V = vocab; r->L = layers; r->E = enc_dim; r->S = max_streams; r->max_sym = max_symbols_per_frame;
+    const size_t H = hidden, V = vocab, L = layers, S = max_streams;
+    r->wcat.assign(L, nullptr);
+    r->bias.assign(L, nullptr);
+    r->ih.resize(L); r->hh.resize(L); r->bih.resize(L); r->bhh.resize(L);
+    r->set_layer.assign(L, 0);
+    const size_t gmax = 4 * H > V ? 4 * H : V;
+    bool ok = (r->h = ralloc(S * L * H)) && (r->c = ralloc(S * L * H)) && (r->ph = ralloc(S * L * H)) &&
+              (r->pc = ralloc(S * L * H)) && (r->pg = ralloc(S * H)) && (r->xh = ralloc(S * 2 * H)) &&
+              (r->slabs = ralloc((size_t)RNNT_KS * S * gmax)) && (r->hsum = ralloc(S * H)) &&
+              (r->dslot_p = (int32_t*)ralloc(S)) && (r->dslot_j = (int32_t*)ralloc(S)) &&
+              (r->dslot_c = (int32_t*)ralloc(S)) && (r->dtok = (int32_t*)ralloc(S)) && (r->drow = (int32_t*)ralloc(S)) &&
+              (r->dbest = (int32_t*)ralloc(S)) && hipHostMalloc((void**)&r->hbest, S * 4) == hipSuccess;
+    if (!ok || hipMemset(r->h, 0, S * L * H * 4) != hipSuccess || hipMemset(r->c, 0, S * L * H * 4) != hipSuccess) {
+        free_rnnt(r);
+        return rfail(UD_ERR_NOMEM, "ud_rnnt_create: device allocation failed");
+    }
+    r->last.assign(S, vocab - 1);
+    r->pending.assign(S, 0);
+    *out = r;
+    return UD_OK;
+}
+
+extern "C" UD_API void ud_rnnt_destroy(ud_rnnt* r) { free_rnnt(r); }
+
+static int rupload(float*& dst, const float* src, size_t n) {
+    if (!dst && !(dst = ralloc(n))) return rfail(UD_ERR_NOMEM, "ud_rnnt_set_weight: allocation failed");
+    RHIPC(hipMemcpy(dst, src, n * 4, hipMemcpyHostToDevice));
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_rnnt_set_weight(ud_rnnt* r, const char* name, const float* host, int64_t count) {
+    if (!r || !name || !host) return rfail(UD_ERR_INVALID, "ud_rnnt_set_weight: null argument");
+    const int64_t H = r->H, V = r->V, E = r->E;
+    struct Fixed { const char* n; int slot; int64_t count; };
+    const Fixed fixed[] = {{"decoder.prediction.embed.weight", R_EMBED, V * H}, {"joint.pred.weight", R_PRED_W, H * H},
+                           {"joint.pred.bias", R_PRED_B, H}, {"joint.joint_net.2.weight", R_OUT_W, V * H},
+                           {"joint.joint_net.2.bias", R_OUT_B, V}, {"joint.enc.weight", R_ENC_W, H * E},
+                           {"joint.enc.bias", R_ENC_B, H}};
+    for (const Fixed& f : fixed) {
+        if (strcmp(name, f.n) != 0) continue;
+        if (count != f.count)
+            return rfail(UD_ERR_WEIGHT, "weight '%s': %lld values, expected %lld", name, (long long)count, (long long)f.count);
+        int rc = rupload(r->w[f.slot], host, (size_t)count);
+        if (rc == UD_OK) r->set_fixed |= 1u << f.slot;
+        return rc;
+    }
+    const char* pre = "decoder.prediction.dec_rnn.lstm.";
+    if (strncmp(name, pre, strlen(pre)) == 0) {
+        const char* p = name + strlen(pre);
+        const char* kinds[4] = {"weight_ih_l", "weight_hh_l", "bias_ih_l", "bias_hh_l"};
+        for (int k = 0; k < 4; k++) {
+            const size_t kl = strlen(kinds[k]);
+            if (strncmp(p, kinds[k], kl) != 0) continue;
+            char* end = nullptr;
+            const long l = strtol(p + kl, &end, 10);
+            if (end == p + kl || *end != '\0' || l < 0 || l >= r->L) break;
+            const int64_t want = k < 2 ? 4 * H * H : 4 * H;
+            if (count != want)
+                return rfail(UD_ERR_WEIGHT, "weight '%s': %lld values, expected %lld", name, (long long)count, (long long)want);
+            std::vector<float>& dst = k == 0 ? r->ih[l] : k == 1 ? r->hh[l] : k == 2 ? r->bih[l] : r->bhh[l];
+            dst.assign(host, host + count);
+            r->set_layer[l] |= 1u << k;
+            int rc = UD_OK;
+            if ((r->set_layer[l] & 3u) == 3u) {     // both matrices: [4H][2H] = [W_ih | W_hh]
+                std::vector<float> cat((size_t)4 * H * 2 * H);
+                for (int64_t row = 0; row < 4 * H; row++) {
+                    memcpy(&cat[(size_t)row * 2 * H], &r->ih[l][(size_t)row * H], (size_t)H * 4);
+                    memcpy(&cat[(size_t)row * 2 * H + H], &r->hh[l][(size_t)row * H], (size_t)H * 4);
+                }
+                rc = rupload(r->wcat[l], cat.data(), cat.size());
+            }
+            if (rc == UD_OK && (r->set_layer[l] & 12u) == 12u) {
+                std::vector<float> b((size_t)4 * H);
+                for (int64_t i = 0; i < 4 * H; i++) b[i] = r->bih[l][i] + r->bhh[l][i];
+                rc = rupload(r->bias[l], b.data(), b.size());
+            }
+            return rc;
+        }
+    }
+    return rfail(UD_ERR_WEIGHT, "unknown RNN-T weight name '%s'", name);
+}
+
+static int check_weights(const ud_rnnt* r, const char* who) {
+    if (r->set_fixed != (1u << R_FIXED) - 1) return rfail(UD_ERR_STATE, "%s: joint / embedding weights not all set", who);
+    for (int l = 0; l < r->L; l++)
+        if (r->set_layer[l] != 15u) return rfail(UD_ERR_STATE, "%s: LSTM layer %d weights not all set", who, l);
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_rnnt_reset(ud_rnnt* r, int32_t slot) {
+    if (!r) return rfail(UD_ERR_INVALID, "ud_rnnt_reset: null decoder");
+    if (slot < 0 || slot >= r->S) return rfail(UD_ERR_SHAPE, "ud_rnnt_reset: slot %d outside 0..%d", slot, r->S - 1);
+    const size_t LH = (size_t)r->L * r->H;
+    RHIPC(hipMemset(r->h + slot * LH, 0, LH * 4));
+    RHIPC(hipMemset(r->c + slot * LH, 0, LH * 4));
+    r->last[slot] = r->V - 1;
+    r->pending[slot] = 0;
+    return UD_OK;
+}
+
+// C[n, N] slabs = A[n, K] (row stride lda) . W[N, K]^T, RNNT_KS K splits, fp32.
+static int slab_gemm(ud_rnnt* r, const float* A, int lda, const float* W, int n, int N, int K, hipStream_t st) {
+    GemmArgs g{};
+    g.A = A; g.W = W; g.C = r->slabs; g.M = n; g.N = N; g.K = K; g.lda = lda; g.ldw = K; g.ldc = N;
+    g.epi = EPI_PARTIAL; g.act = ACT_NONE; g.out_scale = 1.0f; g.ksplit = RNNT_KS;
+    if (launch_gemm(g, false, st) != 0) return rfail(UD_ERR_HIP, "rnnt GEMM launch failed");
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_rnnt_project(ud_rnnt* r, int32_t rows, const float* enc_dev, float* out_dev, void* hip_stream) {
+    if (!r || !enc_dev || !out_dev) return rfail(UD_ERR_INVALID, "ud_rnnt_project: null argument");
+    if (!(r->set_fixed & (1u << R_ENC_W)) || !(r->set_fixed & (1u << R_ENC_B)))
+        return rfail(UD_ERR_STATE, "ud_rnnt_project: joint.enc weights not set");
+    if (rows < 1) return rfail(UD_ERR_SHAPE, "ud_rnnt_project: rows must be >= 1");
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    GemmArgs g{};
+    g.A = enc_dev; g.W = r->w[R_ENC_W]; g.C = out_dev; g.M = rows; g.N = r->H; g.K = r->E; g.lda = r->E; g.ldw = r->E;
+    g.ldc = r->H; g.epi = EPI_STORE; g.act = ACT_NONE; g.out_scale = 1.0f; g.bias = r->w[R_ENC_B];
+    if (launch_gemm(g, false, st) != 0) return rfail(UD_ERR_HIP, "ud_rnnt_project: GEMM launch failed");
+    return UD_OK;
+}
+
+// The prediction network for rows (slots) without a cached prediction.
+static int predict(ud_rnnt* r, const std::vector<int>& slots, hipStream_t st) {
+    const int n = (int)slots.size(), H = r->H, L = r->L;
+    std::vector<int32_t> tok(n);
+    for (int i = 0; i < n; i++) tok[i] = r->last[slots[i]];
+    RHIPC(hipMemcpyAsync(r->dslot_p, slots.data(), n * 4, hipMemcpyHostToDevice, st));
+    RHIPC(hipMemcpyAsync(r->dtok, tok.data(), n * 4, hipMemcpyHostToDevice, st));
+    hipLaunchKernelGGL(rnnt_embed_kernel, dim3(n), dim3(256), 0, st, r->w[R_EMBED], r->dslot_p, r->dtok, r->h, r->xh, H, L,
+                       r->V - 1);
+    RLAUNCH("rnnt embed");
+    for (int l = 0; l < L; l++) {
+        int rc = slab_gemm(r, r->xh, 2 * H, r->wcat[l], n, 4 * H, 2 * H, st);
+        if (rc != UD_OK) return rc;
+        hipLaunchKernelGGL(rnnt_cell_kernel, dim3(n), dim3(256), 0, st, r->slabs, RNNT_KS, n, r->bias[l], r->h, r->c,
+                           r->ph, r->pc, r->xh, r->dslot_p, H, L, l);
+        RLAUNCH("rnnt cell");
+    }
+    int rc = slab_gemm(r, r->xh, 2 * H, r->w[R_PRED_W], n, H, H, st);
+    if (rc != UD_OK) return rc;
+    hipLaunchKernelGGL(rnnt_sum_kernel, dim3(n), dim3(256), 0, st, r->slabs, RNNT_KS, n, r->w[R_PRED_B], r->pg, r->dslot_p, H);
+    RLAUNCH("rnnt pred");
+    for (int s : slots) r->pending[s] = 1;
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots_host, const float* proj_dev,
+                                     int32_t rows_per_stream, const int32_t* frames_host, int32_t* tokens_host,
+                                     int32_t cap, int32_t* n_tokens_host, void* hip_stream) {
+    if (!r || !slots_host || !proj_dev || !frames_host || !n_tokens_host || (cap > 0 && !tokens_host))
+        return rfail(UD_ERR_INVALID, "ud_rnnt_greedy: null argument");
+    int rc = check_weights(r, "ud_rnnt_greedy");
+    if (rc != UD_OK) return rc;
+    if (n < 1 || n > r->S) return rfail(UD_ERR_SHAPE, "ud_rnnt_greedy: n = %d outside 1..%d", n, r->S);
+    std::vector<char> seen(r->S, 0);
+    int max_frames = 0;
+    for (int b = 0; b < n; b++) {
+        const int s = slots_host[b];
+        if (s < 0 || s >= r->S || seen[s]) return rfail(UD_ERR_INVALID, "ud_rnnt_greedy: bad or repeated slot %d", s);
+        seen[s] = 1;
+        if (frames_host[b] < 0 || frames_host[b] > rows_per_stream)
+            return rfail(UD_ERR_SHAPE, "ud_rnnt_greedy: frames %d outside 0..%d", frames_host[b], rows_per_stream);
+        if (frames_host[b] > max_frames) max_frames = frames_host[b];
+        n_tokens_host[b] = 0;
+    }
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    const int H = r->H, V = r->V, blank = V - 1;
+    std::vector<int> act, emitted(n), pred_slots, commit_slots, next;
+    std::vector<int32_t> aslot, arow;
+    for (int t = 0; t < max_frames; t++) {
+        act.clear();
+        for (int b = 0; b < n; b++)
+            if (t < frames_host[b]) { act.push_back(b); emitted[b] = 0; }
+        while (!act.empty()) {
+            pred_slots.clear();
+            for (int b : act)
+                if (!r->pending[slots_host[b]]) pred_slots.push_back(slots_host[b]);
+            if (!pred_slots.empty() && (rc = predict(r, pred_slots, st)) != UD_OK) return rc;
+            const int m = (int)act.size();
+            aslot.resize(m);
+            arow.resize(m);
+            for (int i = 0; i < m; i++) { aslot[i] = slots_host[act[i]]; arow[i] = act[i] * rows_per_stream + t; }
+            RHIPC(hipMemcpyAsync(r->dslot_j, aslot.data(), m * 4, hipMemcpyHostToDevice, st));
+            RHIPC(hipMemcpyAsync(r->drow, arow.data(), m * 4, hipMemcpyHostToDevice, st));
+            hipLaunchKernelGGL(rnnt_joint_in_kernel, dim3(m), dim3(256), 0, st, proj_dev, r->drow, r->pg, r->dslot_j,
+                               r->hsum, H);
+            RLAUNCH("rnnt joint input");
+            if ((rc = slab_gemm(r, r->hsum, H, r->w[R_OUT_W], m, V, H, st)) != UD_OK) return rc;
+            hipLaunchKernelGGL(rnnt_argmax_kernel, dim3(m), dim3(256), 0, st, r->slabs, RNNT_KS, m, r->w[R_OUT_B],
+                               r->dbest, V);
+            RLAUNCH("rnnt argmax");
+            RHIPC(hipMemcpyAsync(r->hbest, r->dbest, m * 4, hipMemcpyDeviceToHost, st));
+            RHIPC(hipStreamSynchronize(st));
+            commit_slots.clear();
+            next.clear();
+            for (int i = 0; i < m; i++) {
+                const int b = act[i], s = slots_host[b], k = r->hbest[i];
+                if (k == blank || k < 0 || k >= V) continue;   // (out of range only for NaN logits)
+                if (n_tokens_host[b] < cap) tokens_host[(int64_t)b * cap + n_tokens_host[b]] = k;
+                n_tokens_host[b]++;
+                r->last[s] = k;
+                r->pending[s] = 0;
+                commit_slots.push_back(s);
+                if (++emitted[b] < r->max_sym) next.push_back(b);
+            }
+            if (!commit_slots.empty()) {
+                RHIPC(hipMemcpyAsync(r->dslot_c, commit_slots.data(), commit_slots.size() * 4, hipMemcpyHostToDevice, st));
+                hipLaunchKernelGGL(rnnt_commit_kernel, dim3((unsigned)commit_slots.size()), dim3(256), 0, st, r->ph,
+                                   r->pc, r->h, r->c, r->dslot_c, r->L * H);
+                RLAUNCH("rnnt commit");
+            }
+            act.swap(next);
+        }
+    }
+    RHIPC(hipStreamSynchronize(st));
+    return UD_OK;
+}
