@@ -1,6 +1,6 @@
 """Benchmark of the cache-aware streaming FastConformer encoder step on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|offline]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|offline|rnnt]
                     [--no-cpu-baseline]
 
 A step is one cache-aware encoder chunk step for every stream of the batch: the mel chunk (new rows
@@ -17,7 +17,8 @@ decoder's paged grouped-query attention instead: 64 sequences x 1 new token, 32 
 x 128, contexts uniform in 512..4096 keys in bf16 pages of 16 (one line in the same format, value in
 tokens/s).  --workload offline measures the whole-utterance rel-pos attention: 8 utterances x 1500
 frames, 8 heads x 128, valid lengths uniform in 900..1500 as key padding (value in frames/s, roofline
-against the bf16 MFMA peak).
+against the bf16 MFMA peak).  --workload rnnt measures the joint.enc projection and greedy RNN-T
+decoding of 64 streams x 2 frames per chunk.
 """
 import argparse
 import importlib.util
@@ -37,6 +38,7 @@ WORKLOADS = {
     "chunk14": dict(streams=256, T=14),  # 256 concurrent streams, 1120 ms chunks
     "decode": dict(seqs=64, q_heads=32, kv_heads=8, head_dim=128, page=16, ctx=(512, 4096)),
     "offline": dict(batch=8, frames=1500, heads=8, head_dim=128, valid=(900, 1500)),
+    "rnnt": dict(streams=64, T=2, hidden=640, vocab=1025, layers=2),
 }
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
 
@@ -275,6 +277,57 @@ def offline_bench(ud, args):
     print(json.dumps(result), flush=True)
 
 
+def rnnt_bench(ud, args):
+    """joint.enc projection + greedy RNN-T decode of 64 streams x 2 encoder frames per chunk (the
+    step after the encoder, Nemotron.swift:82-90 + RNNT.swift:120-151), timed at the two emission
+    extremes: every frame blank (one joint per frame, the cached prediction reused) and every frame
+    at the 10-symbol cap (a prediction and a joint per symbol).  value: audio-sec/sec of the
+    all-blank regime."""
+    wl = WORKLOADS["rnnt"]
+    S, T = wl["streams"], wl["T"]
+    log("device %s; workload rnnt: %d streams x %d frames, hidden %d, vocab %d, %d LSTM layers, fp32"
+        % (ud.device_arch(), S, T, wl["hidden"], wl["vocab"], wl["layers"]))
+    rng = np.random.default_rng(3)
+    enc = ud.DeviceBuffer.from_numpy(rng.standard_normal((S * T, 1024), dtype=np.float32))
+    proj = ud.DeviceBuffer(S * T * wl["hidden"] * 4)
+    hs = ud.HipStream()
+    res = {}
+    for regime, bias in (("blank", 50.0), ("cap", -50.0)):
+        r = ud.Rnnt(max_streams=S)
+        r.set_weights(ud.synthetic_rnnt_weights(7, blank_bias=bias))
+        slots = list(range(S))
+
+        def chunk():
+            r.project(S * T, enc, proj, hip_stream=hs)
+            return r.greedy(slots, proj, T, [T] * S, cap=32, hip_stream=hs)[1]
+
+        for _ in range(max(2, args.warmup // 4)):
+            chunk()
+        steps = max(5, args.steps // 10)
+        t0 = time.perf_counter()
+        toks = 0
+        for _ in range(steps):
+            toks += int(chunk().sum())
+        ms = (time.perf_counter() - t0) * 1000.0 / steps
+        res[regime] = (ms, toks / steps)
+        log("%s regime: %.3f ms per chunk, %.1f tokens per chunk" % (regime, ms, toks / steps))
+        r.close()
+    ms = res["blank"][0]
+    result = {
+        "metric": "aggregate audio-sec/sec of joint + greedy RNN-T decoding at 64 streams",
+        "value": round(S * T * FRAME_SEC / (ms / 1000.0), 2),
+        "unit": "audio-sec/sec",
+        "n_gpus": 1, "steps": max(5, args.steps // 10), "warmup": max(2, args.warmup // 4),
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded random-init prediction/joint weights, N(0,1) encoder rows)",
+        "config": {"workload": "joint.enc + greedy RNN-T, %d streams x %d frames per chunk, all frames blank" % (S, T),
+                   "streams": S, "frames": T, "hidden": wl["hidden"], "vocab": wl["vocab"], "layers": wl["layers"]},
+        "cap_regime_ms_per_chunk": round(res["cap"][0], 4),
+        "cap_regime_tokens_per_chunk": res["cap"][1],
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -307,6 +360,9 @@ def main():
         return
     if args.workload == "offline":
         offline_bench(ud, args)
+        return
+    if args.workload == "rnnt":
+        rnnt_bench(ud, args)
         return
     wl = WORKLOADS[args.workload]
     S, T = wl["streams"], wl["T"]
