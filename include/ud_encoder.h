@@ -74,6 +74,8 @@ UD_API const char* ud_last_error(void);
  * allocates device weights, the per-step workspace and the stream pool on the current device. */
 UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder** out);
 UD_API void ud_encoder_destroy(ud_encoder* enc);
+/* The configuration an encoder was created with (FastConformerEncoder.config, FastConformer.swift:62). */
+UD_API int ud_encoder_get_config(const ud_encoder* enc, ud_encoder_config* out);
 
 /* Replaces the per-tensor loads of FastConformer.swift:72-143.  `name` is a NeMo state_dict
  * name ("encoder.layers.{i}.feed_forward1.linear1.weight", ..., the 26 per-layer tensors of the

@@ -94,6 +94,16 @@ def _sig(lib):
                                        ctypes.c_size_t, p]),
         "ud_rope_rotate_half": (i, [_i32, p, _i32, _i32, _i32, _i32, p, _i32, p, p]),
         "ud_paged_kv_append": (i, [_i32, p, p, p, p, p, _i32, p, _i32, _i32, _i32, _i32, p]),
+        "ud_encoder_get_config": (i, [p, ctypes.POINTER(_Config)]),
+        "ud_safetensors_open": (i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+        "ud_safetensors_close": (v, [p]),
+        "ud_safetensors_count": (_i32, [p]),
+        "ud_safetensors_name": (ctypes.c_char_p, [p, _i32]),
+        "ud_safetensors_info": (i, [p, ctypes.c_char_p, ip, ctypes.POINTER(ctypes.c_int64), ip]),
+        "ud_safetensors_read_f32": (i, [p, ctypes.c_char_p, f, ctypes.c_int64]),
+        "ud_nemo_name": (i, [ctypes.c_char_p, ctypes.c_char_p, _i32]),
+        "ud_encoder_load_safetensors": (i, [p, p, ip]),
+        "ud_rnnt_load_safetensors": (i, [p, p, ip]),
         "ud_rnnt_create": (i, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_vp)]),
         "ud_rnnt_destroy": (v, [p]),
         "ud_rnnt_set_weight": (i, [p, ctypes.c_char_p, f, ctypes.c_int64]),
@@ -345,6 +355,13 @@ class Encoder:
         for suffix, a in weights.items():
             self.set_weight("encoder.layers.%d.%s" % (layer, suffix), a)
 
+    def load_safetensors(self, st):
+        """Sets every encoder tensor of a SafeTensors file (NeMo or HF names; layers beyond this
+        encoder's depth skipped); returns the count.  Call finalize() afterwards."""
+        n = _i32(0)
+        _check(_lib.ud_encoder_load_safetensors(self.handle, st.handle, ctypes.byref(n)))
+        return n.value
+
     def set_subsampling_weights(self, weights):
         """weights: dict of the 12 encoder.pre_encode.* tensors (as synthetic_subsampling_weights
         returns), checkpoint layout."""
@@ -515,6 +532,54 @@ def synthetic_layer_weights(cfg, seed, layer, ln_jitter=0.1):
     return w
 
 
+ST_DTYPES = {0: "F32", 1: "BF16", 2: "F16", 3: "other"}
+
+
+class SafeTensors:
+    """A memory-mapped safetensors file (include/ud_safetensors.h), mirroring SafeTensorsReader
+    (Sources/DictatorCore/Weights/WeightSource.swift): names, info, tensors widened to fp32."""
+
+    def __init__(self, path):
+        p = _vp()
+        _check(load_library().ud_safetensors_open(os.fsencode(path), ctypes.byref(p)))
+        self.handle = p.value
+
+    def names(self):
+        return [_lib.ud_safetensors_name(self.handle, i).decode() for i in range(_lib.ud_safetensors_count(self.handle))]
+
+    def info(self, name):
+        dt = _i32(0)
+        nd = _i32(0)
+        shape = (ctypes.c_int64 * 8)()
+        _check(_lib.ud_safetensors_info(self.handle, name.encode(), ctypes.byref(dt), shape, ctypes.byref(nd)))
+        return ST_DTYPES[dt.value], tuple(shape[i] for i in range(nd.value))
+
+    def floats(self, name):
+        _, shape = self.info(name)
+        out = np.empty(shape, np.float32)
+        _check(_lib.ud_safetensors_read_f32(self.handle, name.encode(),
+                                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), out.size))
+        return out
+
+    def close(self):
+        if self.handle:
+            _lib.ud_safetensors_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def nemo_name(name):
+    """The NeMo state_dict name of a tensor name (HF model.safetensors aliases mapped)."""
+    buf = ctypes.create_string_buffer(512)
+    _check(load_library().ud_nemo_name(name.encode(), buf, 512))
+    return buf.value.decode()
+
+
 class Rnnt:
     """RNN-T joint + greedy decoder for a pool of stream slots (include/ud_rnnt.h), mirroring
     RNNTDecoder (Sources/DictatorCore/Decoding/RNNT.swift): set_weights, project (joint.enc),
@@ -535,6 +600,12 @@ class Rnnt:
 
     def reset(self, slot):
         _check(_lib.ud_rnnt_reset(self.handle, int(slot)))
+
+    def load_safetensors(self, st):
+        """Sets every decoder.prediction.* / joint.* tensor of a SafeTensors file; returns the count."""
+        n = _i32(0)
+        _check(_lib.ud_rnnt_load_safetensors(self.handle, st.handle, ctypes.byref(n)))
+        return n.value
 
     def project(self, rows, enc, out, hip_stream=None):
         """out [rows, hidden] = joint.enc(enc [rows, enc_dim]); DeviceBuffers of fp32."""

@@ -290,6 +290,12 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
 
 extern "C" UD_API void ud_encoder_destroy(ud_encoder* enc) { free_encoder(enc); }
 
+extern "C" UD_API int ud_encoder_get_config(const ud_encoder* enc, ud_encoder_config* out) {
+    if (!enc || !out) return fail(UD_ERR_INVALID, "ud_encoder_get_config: null argument");
+    *out = enc->cfg;
+    return UD_OK;
+}
+
 static int upload(void* dst, const void* src, size_t bytes) {
     HIPC(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
     return UD_OK;
