@@ -33,6 +33,10 @@ UD_API int ud_rnnt_create(int32_t hidden, int32_t vocab, int32_t layers, int32_t
                           int32_t max_symbols_per_frame, ud_rnnt** out);
 UD_API void ud_rnnt_destroy(ud_rnnt* r);
 
+/* Dimensions the decoder was created with (any pointer may be NULL). */
+UD_API int ud_rnnt_get_info(const ud_rnnt* r, int32_t* hidden, int32_t* vocab, int32_t* layers, int32_t* enc_dim,
+                            int32_t* max_streams, int32_t* max_symbols_per_frame);
+
 /* Checkpoint tensors by NeMo name, fp32 host values in the checkpoint layout:
  * decoder.prediction.embed.weight [V, H]; decoder.prediction.dec_rnn.lstm.{weight_ih,weight_hh}_l{l}
  * [4H, H] and {bias_ih,bias_hh}_l{l} [4H] (gate order i, f, g, o); joint.pred.{weight,bias};

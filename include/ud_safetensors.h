@@ -17,6 +17,7 @@
 #include <stdint.h>
 
 #include "ud_encoder.h"
+#include "ud_mel.h"
 #include "ud_rnnt.h"
 
 #ifdef __cplusplus
@@ -49,6 +50,10 @@ UD_API int ud_nemo_name(const char* name, char* out, int32_t cap);
 UD_API int ud_encoder_load_safetensors(ud_encoder* enc, const ud_safetensors* st, int32_t* n_loaded);
 /* Sets every RNN-T tensor of the file (decoder.prediction.*, joint.*) through ud_rnnt_set_weight. */
 UD_API int ud_rnnt_load_safetensors(ud_rnnt* r, const ud_safetensors* st, int32_t* n_loaded);
+/* ud_mel_create from the file's preprocessor.featurizer.fb [1, n_mels, 257] and
+ * preprocessor.featurizer.window [400] (NemotronModel.init, Sources/DictatorEngine/Models/
+ * Nemotron.swift:45-46); UD_ERR_WEIGHT if either is missing (the HF model.safetensors has neither). */
+UD_API int ud_mel_load_safetensors(const ud_safetensors* st, ud_mel** out);
 
 #ifdef __cplusplus
 }

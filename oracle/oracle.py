@@ -350,3 +350,198 @@ class Rnnt:
         lib().orc_rnnt_predict(self._ptrs, self.H, self.V, self.L, int(token), _p(_f32(h)), _p(_f32(c)), _p(proj),
                                _p(ho), _p(co))
         return proj, ho, co
+
+
+# ---------------------------------------------------------------- mel frontend and streaming
+
+MEL_FFT, MEL_HOP, MEL_WIN, MEL_FFT_BINS = 512, 160, 400, 257
+
+
+class MelFrontend:
+    """NemoMelFrontend (Sources/DictatorCore/Audio/NemoMel.swift:11-108) over the C restatement:
+    fb [n_mels, 257], window [400] (the checkpoint's preprocessor.featurizer buffers)."""
+
+    def __init__(self, fb, window):
+        self.fb = _f32(fb).reshape(-1, MEL_FFT_BINS)
+        self.n_mels = self.fb.shape[0]
+        self.window = _f32(window).reshape(MEL_WIN)
+        self.cos_t = np.empty((MEL_FFT_BINS, MEL_WIN), np.float32)
+        self.sin_t = np.empty((MEL_FFT_BINS, MEL_WIN), np.float32)
+        lib().orc_mel_tables(_p(self.window), _p(self.cos_t), _p(self.sin_t))
+
+    @staticmethod
+    def valid_frames(samples):
+        return samples // MEL_HOP
+
+    def frames(self, audio, f0, nf, valid_end):
+        audio = _f32(audio)
+        out = np.empty((nf, self.n_mels), np.float32)
+        lib().orc_mel_frames(_p(audio), ctypes.c_int64(audio.size), ctypes.c_int64(f0), int(nf),
+                             ctypes.c_int64(valid_end), _p(self.cos_t), _p(self.sin_t), _p(self.fb), self.n_mels,
+                             _p(out))
+        return out
+
+    def features(self, audio):
+        """Full-utterance features [n // 160 + 1, n_mels], the last frame zero (NemoMel.swift:46-67)."""
+        n = int(np.asarray(audio).size)
+        return self.frames(audio, 0, n // MEL_HOP + 1, n // MEL_HOP)
+
+
+class MelStream:
+    """NemoMelStream (NemoMel.swift:113-161): push audio in any sizes, frames come out once their
+    window is complete; finish() emits the tail exactly as features() would."""
+
+    def __init__(self, fe):
+        self.fe = fe
+        self.audio = np.zeros(0, np.float32)
+        self.emitted = 0
+
+    def _emit(self, end, valid):
+        if end <= self.emitted:
+            return np.zeros((0, self.fe.n_mels), np.float32)
+        out = self.fe.frames(self.audio, self.emitted, end - self.emitted, valid)
+        self.emitted = end
+        return out
+
+    def push(self, samples):
+        self.audio = np.concatenate([self.audio, _f32(samples).ravel()])
+        n = self.audio.size
+        ready = (n - 200) // MEL_HOP + 1 if n >= 200 else 0
+        return self._emit(ready, 1 << 62)
+
+    def finish(self):
+        n = self.audio.size
+        return self._emit(n // MEL_HOP + 1, n // MEL_HOP)
+
+
+class Schedule:
+    """NemotronSchedule (Sources/DictatorCore/Nemotron/NemotronSchedule.swift:7-17)."""
+
+    def __init__(self, lookahead):
+        self.lookahead = lookahead
+        self.left_context = 70
+        self.pre_encode_cache = 9
+        self.drop_extra = 2
+        self.first_chunk = 1 + 8 * lookahead
+        self.chunk = 8 + 8 * lookahead
+        self.out_frames_per_chunk = lookahead + 1
+
+
+class Streamer:
+    """NemotronStreamer (Sources/DictatorCore/Nemotron/NemotronStreamer.swift:16-153) driving the
+    oracle encoder step of MetalNemotronEncoder.step (Sources/DictatorEngine/Models/Nemotron.swift:
+    75-100): subsampling + drop, the stream step, joint.enc on the kept frames, greedy RNN-T.
+    One stream; every chunk runs at its own (unpadded) size, as the reference does.
+
+    model: an oracle Model prepared for the rel range of the schedule; sw: subsampling weights;
+    rw: RNN-T weights (joint.enc included); fe: a MelFrontend (live input only)."""
+
+    def __init__(self, model, sw, rw, lookahead, fe=None, layers=None):
+        self.model, self.sw, self.fe = model, sw, fe
+        self.schedule = Schedule(lookahead)
+        self.dec = Rnnt(rw)
+        self.dec_state = self.dec.state()
+        self.w_enc = _f32(rw["joint.enc.weight"])
+        self.b_enc = _f32(rw["joint.enc.bias"])
+        nl = len(model.layers)
+        L, D, Kc = self.schedule.left_context, model.D, model.Kc
+        self.k = np.zeros((1, nl, L, D), np.float32)
+        self.v = np.zeros((1, nl, L, D), np.float32)
+        self.c = np.zeros((1, nl, Kc, D), np.float32)
+        self.len = np.zeros(1, np.int32)
+        self.steps = 0
+        self.tokens = []
+        self.enc_rows = []          # kept encoder output rows per chunk
+        self.proj_rows = []         # kept joint.enc rows per chunk
+        self.end_padding = True
+        self.live_mel = MelStream(fe) if fe is not None else None
+        self.live_buffer = np.zeros((0, fe.n_mels if fe is not None else 128), np.float32)
+        self.live_start = 0
+        self.live_next = 0
+
+    def encoder_step(self, mel_rows, n_rows, valid_rows, keep_all):
+        s = self.schedule
+        drop = 0 if self.steps == 0 else s.drop_extra
+        x = subsample(mel_rows[:n_rows], valid_rows, self.sw)[drop:]
+        T = x.shape[0]
+        vs = sub_next_len(sub_next_len(sub_next_len(valid_rows)))
+        valid_t = max(0, min(vs - drop, T))
+        y = stream_step(self.model, x[None], np.array([valid_t], np.int32), self.k, self.v, self.c, self.len)[0]
+        self.steps += 1
+        keep = valid_t if keep_all else min(valid_t, s.out_frames_per_chunk)
+        if keep == 0:
+            return np.zeros((0, self.w_enc.shape[0]), np.float32), y[:0]
+        proj = gemm_nt(y[:keep], self.w_enc, bias=self.b_enc)
+        return proj, y[:keep]
+
+    def step(self, mel_rows, n_rows, valid_rows, keep_all):
+        proj, y = self.encoder_step(mel_rows, n_rows, valid_rows, keep_all)
+        new = self.dec.greedy(proj, self.dec_state) if proj.shape[0] > 0 else []
+        self.tokens += new
+        self.enc_rows.append(y)
+        self.proj_rows.append(proj)
+        return new
+
+    def run_buffered(self, mel, frames, valid_frames):
+        """runBuffered (NemotronStreamer.swift:70-91)."""
+        s = self.schedule
+        idx = 0
+        while idx < frames:
+            first = idx == 0
+            size = s.first_chunk if first else s.chunk
+            end = min(idx + size, frames)
+            chunk_len = end - idx
+            if chunk_len < (1 if first else 8):
+                return
+            cache_start = idx if first else max(0, idx - s.pre_encode_cache)
+            added = idx - cache_start
+            rows = added + chunk_len
+            valid = max(0, min(valid_frames - idx + added, rows))
+            idx += size
+            self.step(mel[cache_start:cache_start + rows], rows, valid, idx >= frames)
+
+    def push(self, samples):
+        self.live_buffer = np.concatenate([self.live_buffer, self.live_mel.push(samples)])
+        return self._drain(False)
+
+    def flush(self):
+        self.live_buffer = np.concatenate([self.live_buffer, self.live_mel.finish()])
+        return self._drain(True)
+
+    def _drain(self, final):
+        """drainChunks (NemotronStreamer.swift:109-153)."""
+        s = self.schedule
+        have = self.live_buffer.shape[0] + self.live_start
+        out = []
+        while True:
+            idx = self.live_next
+            first = idx == 0
+            size = s.first_chunk if first else s.chunk
+            end = idx + size
+            if end > have and not final:
+                break
+            chunk_end = min(end, have)
+            chunk_len = chunk_end - idx
+            min_len = 1 if first else 8
+            if chunk_len <= 0 or (chunk_len < min_len and not (final and self.end_padding)):
+                break
+            cache_start = idx if first else max(0, idx - s.pre_encode_cache)
+            rows = chunk_end - cache_start
+            pad_rows = max(0, min_len - chunk_len)
+            is_last = final and end >= have
+            a = cache_start - self.live_start
+            m = self.live_buffer[a:a + rows]
+            if pad_rows > 0:
+                m = np.concatenate([m, np.zeros((pad_rows, m.shape[1]), np.float32)])
+                out += self.step(m, rows + pad_rows, rows, True)
+            else:
+                out += self.step(m, rows, rows, is_last)
+            self.live_next = end
+            keep_from = self.live_next - s.pre_encode_cache
+            if keep_from > self.live_start:
+                drop = min(self.live_buffer.shape[0], keep_from - self.live_start)
+                self.live_buffer = self.live_buffer[drop:]
+                self.live_start = keep_from
+            if is_last:
+                break
+        return out

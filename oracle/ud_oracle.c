@@ -43,6 +43,12 @@
  *                         greedy loop without a prediction cache
  *                         (reference/nemo/check_spec.py:176-207 structure,
  *                         tests/refimpl.py), across chunk boundaries
+ *   orc_mel_tables/frames torch.stft restatement of NeMo FilterbankFeatures
+ *                         (preemphasis, centred constant-padded STFT with the
+ *                         400-sample Hann window in 512, |X|^2, filterbank,
+ *                         log guard 2^-24) and numpy.fft.rfft; the reference
+ *                         KAT NemoMelStream == features (StreamingEquivalence
+ *                         Tests.swift:9-20)
  */
 #include <math.h>
 #include <stdint.h>
@@ -669,4 +675,71 @@ ORC_API int orc_rnnt_greedy(const float* const* w, int H, int V, int L, const fl
     }
     free(logits);
     return n;
+}
+
+/* ------------------------------------------------------------ mel frontend */
+
+enum { ORC_MEL_FFT = 512, ORC_MEL_HOP = 160, ORC_MEL_WIN = 400, ORC_MEL_BINS = 257 };
+
+/* NemoMelFrontend.init (Sources/DictatorCore/Audio/NemoMel.swift:23-40): DFT tables with the
+ * window folded in, cos_t/sin_t [257][400]: the 400-sample window sits centred in the 512-point
+ * frame (offset 56, torch.stft's zero-padded win_length), phase 2 pi k (n + 56) / 512 in double,
+ * entry = float(cos phase) * window[n] and float(-sin phase) * window[n] in float arithmetic. */
+ORC_API void orc_mel_tables(const float* window, float* cos_t, float* sin_t) {
+    const int off = (ORC_MEL_FFT - ORC_MEL_WIN) / 2;
+    for (int k = 0; k < ORC_MEL_BINS; k++)
+        for (int n = 0; n < ORC_MEL_WIN; n++) {
+            const double phase = 2.0 * 3.14159265358979323846 * (double)k * (double)(n + off) / (double)ORC_MEL_FFT;
+            cos_t[k * ORC_MEL_WIN + n] = (float)cos(phase) * window[n];
+            sin_t[k * ORC_MEL_WIN + n] = (float)(-sin(phase)) * window[n];
+        }
+}
+
+/* Mel frames [f0, f0 + nf) of one clip audio[0, n) (NemoMelFrontend.features and
+ * NemoMelStream.emit, NemoMel.swift:46-67, 85-107, 141-160): frame t takes the preemphasized
+ * samples [160 t - 200, 160 t + 200) -- x[0] = a[0], x[i] = a[i] - 0.97 a[i-1] in float, zero
+ * outside [0, n) (the centred STFT's constant padding) -- then re/im against the tables, power
+ * |X|^2, mel = fb . power, out = log(mel + 2^-24); frames >= valid_end are written as zeros.
+ * The DFT, power and mel sums accumulate in double (a tighter anchor than the reference's fp32
+ * sgemm); out [nf][n_mels] float.  fb [n_mels][257]. */
+ORC_API void orc_mel_frames(const float* audio, int64_t n, int64_t f0, int32_t nf, int64_t valid_end,
+                            const float* cos_t, const float* sin_t, const float* fb, int32_t n_mels, float* out) {
+    const double guard = ldexp(1.0, -24);
+#pragma omp parallel for schedule(static)
+    for (int32_t j = 0; j < nf; j++) {
+        const int64_t f = f0 + j;
+        float* o = out + (int64_t)j * n_mels;
+        if (f >= valid_end) {
+            memset(o, 0, (size_t)n_mels * sizeof(float));
+            continue;
+        }
+        float x[ORC_MEL_WIN];
+        const int64_t start = f * ORC_MEL_HOP - ORC_MEL_FFT / 2 + (ORC_MEL_FFT - ORC_MEL_WIN) / 2;
+        for (int i = 0; i < ORC_MEL_WIN; i++) {
+            const int64_t idx = start + i;
+            if (idx < 0 || idx >= n) x[i] = 0.0f;
+            else if (idx == 0) x[i] = audio[0];
+            else {
+                const float m = 0.97f * audio[idx - 1];
+                x[i] = audio[idx] - m;
+            }
+        }
+        double power[ORC_MEL_BINS];
+        for (int k = 0; k < ORC_MEL_BINS; k++) {
+            double re = 0.0, im = 0.0;
+            const float* c = cos_t + (int64_t)k * ORC_MEL_WIN;
+            const float* s = sin_t + (int64_t)k * ORC_MEL_WIN;
+            for (int i = 0; i < ORC_MEL_WIN; i++) {
+                re += (double)c[i] * (double)x[i];
+                im += (double)s[i] * (double)x[i];
+            }
+            power[k] = re * re + im * im;
+        }
+        for (int m = 0; m < n_mels; m++) {
+            double acc = 0.0;
+            const float* w = fb + (int64_t)m * ORC_MEL_BINS;
+            for (int k = 0; k < ORC_MEL_BINS; k++) acc += (double)w[k] * power[k];
+            o[m] = (float)log(acc + guard);
+        }
+    }
 }

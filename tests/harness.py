@@ -70,3 +70,14 @@ class OracleState:
         for s, st in enumerate(streams):
             for l in range(self.k.shape[1]):
                 st.import_cache(l, self.k[s, l], self.v[s, l], self.c[s, l], int(self.len[s]))
+
+
+def speechlike(n, seed, scale=0.3):
+    """Harmonics of a gliding 120 Hz pitch under a slow envelope, over low-level noise: a test
+    signal with ~60 dB of spectral dynamic range (16 kHz)."""
+    rng = np.random.default_rng(seed)
+    t = np.arange(n) / 16000.0
+    f0 = 120 + 40 * np.sin(2 * np.pi * 0.7 * t)
+    ph = 2 * np.pi * np.cumsum(f0) / 16000.0
+    x = sum(np.sin(h * ph) / h for h in range(1, 12)) * (0.2 + 0.15 * np.sin(2 * np.pi * 1.3 * t))
+    return (scale * x + 1e-3 * rng.standard_normal(n)).astype(np.float32)

@@ -174,3 +174,75 @@ def rnnt_greedy_nemo(f, w, state=None, max_symbols=10):
             state["h"], state["c"], state["token"] = nh, nc, k
             n += 1
     return toks, state
+
+
+def mel_nemo(audio, fb, window, dtype=None):
+    """NeMo FilterbankFeatures at inference (dither off, no normalization; docs/specs/nemotron.md
+    §9.1): x[0] = a[0], x[i] = a[i] - 0.97 a[i-1] (fp32, as NeMo runs it); torch.stft(n_fft=512,
+    hop 160, win_length 400, the symmetric window centred in 512, center=True, constant padding);
+    |X|^2; fb @ power; log(x + 2^-24); frames >= n // 160 zeroed.  The STFT onward in float64.
+    Returns [n // 160 + 1, n_mels]."""
+    import torch
+    a = torch.from_numpy(np.ascontiguousarray(audio, np.float32))
+    x = torch.cat([a[:1], a[1:] - 0.97 * a[:-1]]).double()
+    X = torch.stft(x, n_fft=512, hop_length=160, win_length=400, window=torch.from_numpy(window).double(),
+                   center=True, pad_mode="constant", return_complex=True)
+    power = X.abs().pow(2.0)                                   # [257, T]
+    mel = torch.from_numpy(np.asarray(fb, np.float64).reshape(-1, 257)) @ power
+    out = torch.log(mel + 2.0 ** -24).T.contiguous()
+    out[a.numel() // 160:] = 0
+    return out.numpy()
+
+
+def mel_rfft(audio, fb, window):
+    """The same features through numpy.fft.rfft of each zero-padded 512-sample frame (the window
+    zero-padded to 512, centred), float64 from the fp32 preemphasized signal."""
+    a = np.asarray(audio, np.float32)
+    x = np.concatenate([a[:1], a[1:] - np.float32(0.97) * a[:-1]]).astype(np.float64)
+    n = a.size
+    xp = np.concatenate([np.zeros(256), x, np.zeros(256)])
+    T = n // 160 + 1
+    w = np.zeros(512)
+    w[56:456] = np.asarray(window, np.float64)
+    frames = np.stack([xp[t * 160:t * 160 + 512] * w for t in range(T)])
+    power = np.abs(np.fft.rfft(frames, axis=1)) ** 2
+    out = np.log(power @ np.asarray(fb, np.float64).reshape(-1, 257).T + 2.0 ** -24)
+    out[n // 160:] = 0
+    return out
+
+
+def slaney_mel_fb(sr=16000, n_fft=512, n_mels=128):
+    """librosa.filters.mel(sr, n_fft, n_mels, htk=False, norm='slaney') restated (the checkpoint's
+    preprocessor.featurizer.fb is this matrix up to 1e-8, docs/specs/nemotron.md §9.1)."""
+    def hz_to_mel(f):
+        f = np.asarray(f, np.float64)
+        f_sp = 200.0 / 3
+        mels = f / f_sp
+        min_log_hz = 1000.0
+        min_log_mel = min_log_hz / f_sp
+        logstep = np.log(6.4) / 27.0
+        return np.where(f >= min_log_hz, min_log_mel + np.log(np.maximum(f, 1e-10) / min_log_hz) / logstep, mels)
+
+    def mel_to_hz(m):
+        m = np.asarray(m, np.float64)
+        f_sp = 200.0 / 3
+        freqs = f_sp * m
+        min_log_hz = 1000.0
+        min_log_mel = min_log_hz / f_sp
+        logstep = np.log(6.4) / 27.0
+        return np.where(m >= min_log_mel, min_log_hz * np.exp(logstep * (m - min_log_mel)), freqs)
+
+    fftfreqs = np.linspace(0, sr / 2, 1 + n_fft // 2)
+    mel_f = mel_to_hz(np.linspace(hz_to_mel(0.0), hz_to_mel(sr / 2.0), n_mels + 2))
+    fdiff = np.diff(mel_f)
+    ramps = mel_f[:, None] - fftfreqs[None, :]
+    lower = -ramps[:-2] / fdiff[:-1, None]
+    upper = ramps[2:] / fdiff[1:, None]
+    w = np.maximum(0, np.minimum(lower, upper))
+    w *= (2.0 / (mel_f[2:n_mels + 2] - mel_f[:n_mels]))[:, None]
+    return w.astype(np.float32)
+
+
+def hann_symmetric(n=400):
+    """torch.hann_window(400, periodic=False): 0.5 - 0.5 cos(2 pi i / 399)."""
+    return (0.5 - 0.5 * np.cos(2 * np.pi * np.arange(n) / (n - 1))).astype(np.float32)

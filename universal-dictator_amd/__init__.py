@@ -110,6 +110,23 @@ def _sig(lib):
         "ud_rnnt_reset": (i, [p, _i32]),
         "ud_rnnt_project": (i, [p, _i32, p, p, p]),
         "ud_rnnt_greedy": (i, [p, _i32, ip, p, _i32, ip, ip, _i32, ip, p]),
+        "ud_rnnt_get_info": (i, [p, ip, ip, ip, ip, ip, ip]),
+        "ud_mel_create": (i, [f, _i32, f, ctypes.POINTER(_vp)]),
+        "ud_mel_destroy": (v, [p]),
+        "ud_mel_bins": (_i32, [p]),
+        "ud_mel_features": (i, [p, _i32, p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64), p, _i32, ip, p]),
+        "ud_mel_load_safetensors": (i, [p, ctypes.POINTER(_vp)]),
+        "ud_streamer_create": (i, [p, p, p, _i32, _i32, ctypes.POINTER(_vp)]),
+        "ud_streamer_destroy": (v, [p]),
+        "ud_streamer_open": (i, [p, ip]),
+        "ud_streamer_close": (i, [p, _i32]),
+        "ud_streamer_set_options": (i, [p, _i32, _i32]),
+        "ud_streamer_push": (i, [p, _i32, ip, ctypes.POINTER(f), ctypes.POINTER(ctypes.c_int64)]),
+        "ud_streamer_flush": (i, [p, _i32, ip]),
+        "ud_streamer_run_buffered": (i, [p, _i32, ip, ctypes.POINTER(f), ip, ip]),
+        "ud_streamer_tokens": (i, [p, _i32, ip, _i32, ip]),
+        "ud_streamer_recorded": (i, [p, _i32, _i32, f, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
+        "ud_streamer_stats": (i, [p, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -704,3 +721,179 @@ def round_bf16(a):
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32) << 16
     r = np.where(np.isnan(a), np.uint32(0x7FC00000), r.astype(np.uint32))
     return r.astype(np.uint32).view(np.float32).reshape(a.shape)
+
+
+# ---------------------------------------------------------------- mel frontend and streaming
+
+
+class MelFrontend:
+    """NeMo log-mel frontend on the GPU (include/ud_mel.h), mirroring NemoMelFrontend
+    (Sources/DictatorCore/Audio/NemoMel.swift:11-108): fb [n_mels, 257] and window [400] are the
+    checkpoint's preprocessor.featurizer buffers."""
+
+    HOP = 160
+
+    def __init__(self, fb=None, window=None, handle=None):
+        if handle is None:
+            fb = np.ascontiguousarray(fb, np.float32).reshape(-1, 257)
+            window = np.ascontiguousarray(window, np.float32).reshape(400)
+            p = _vp()
+            F = ctypes.POINTER(ctypes.c_float)
+            _check(lib().ud_mel_create(fb.ctypes.data_as(F), fb.shape[0], window.ctypes.data_as(F), ctypes.byref(p)))
+            handle = p.value
+        self.handle = handle
+        self.n_mels = int(_lib.ud_mel_bins(self.handle))
+
+    @classmethod
+    def from_safetensors(cls, st):
+        p = _vp()
+        _check(lib().ud_mel_load_safetensors(st.handle, ctypes.byref(p)))
+        return cls(handle=p.value)
+
+    @staticmethod
+    def valid_frames(samples):
+        return samples // MelFrontend.HOP
+
+    def features_device(self, n, audio, stride, n_samples, out, out_rows, hip_stream=None):
+        """ud_mel_features on DeviceBuffers: audio fp32 [n, stride]; out fp32 [n, out_rows, n_mels].
+        Returns the frame counts."""
+        ns = np.ascontiguousarray(n_samples, np.int64)
+        fr = np.zeros(n, np.int32)
+        _check(_lib.ud_mel_features(self.handle, n, audio.ptr, int(stride), ns.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                    out.ptr, int(out_rows), fr.ctypes.data_as(ctypes.POINTER(_i32)),
+                                    hip_stream.ptr if hip_stream else None))
+        return fr
+
+    def features(self, clips):
+        """Full-utterance features of a list of 1-D fp32 clips: a list of [n // 160 + 1, n_mels]."""
+        clips = [np.ascontiguousarray(c, np.float32).ravel() for c in clips]
+        n = len(clips)
+        stride = max(1, max(c.size for c in clips))
+        a = np.zeros((n, stride), np.float32)
+        for b, c in enumerate(clips):
+            a[b, :c.size] = c
+        rows = stride // self.HOP + 1
+        ab = DeviceBuffer.from_numpy(a)
+        ob = DeviceBuffer(n * rows * self.n_mels * 4)
+        fr = self.features_device(n, ab, stride, [c.size for c in clips], ob, rows)
+        synchronize()
+        out = ob.download((n, rows, self.n_mels))
+        return [out[b, :fr[b]].copy() for b in range(n)]
+
+    def close(self):
+        if self.handle:
+            _lib.ud_mel_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Streamer:
+    """Cache-aware streaming transcription of many streams at once (include/ud_streamer.h), mirroring
+    NemotronStreamer (Sources/DictatorCore/Nemotron/NemotronStreamer.swift): open() gives a stream
+    id; push / flush / run_buffered / tokens act per stream id, and every stream with a complete
+    chunk joins one batched step."""
+
+    def __init__(self, encoder, rnnt, mel=None, lookahead=1, max_streams=None):
+        max_streams = max_streams or encoder.config.max_streams
+        p = _vp()
+        _check(lib().ud_streamer_create(encoder.handle, rnnt.handle, mel.handle if mel is not None else None,
+                                        int(lookahead), int(max_streams), ctypes.byref(p)))
+        self.handle = p.value
+        self.lookahead = lookahead
+        self._end_padding, self._record = True, False
+        self._keep = (encoder, rnnt, mel)
+
+    def _opts(self):
+        _check(_lib.ud_streamer_set_options(self.handle, int(self._end_padding), int(self._record)))
+
+    @property
+    def end_padding(self):
+        return self._end_padding
+
+    @end_padding.setter
+    def end_padding(self, on):
+        self._end_padding = bool(on)
+        self._opts()
+
+    @property
+    def record(self):
+        return self._record
+
+    @record.setter
+    def record(self, on):
+        self._record = bool(on)
+        self._opts()
+
+    def open(self):
+        i = _i32(0)
+        _check(_lib.ud_streamer_open(self.handle, ctypes.byref(i)))
+        return i.value
+
+    def close_stream(self, sid):
+        _check(_lib.ud_streamer_close(self.handle, int(sid)))
+
+    def push(self, chunks):
+        """chunks: {stream id: fp32 samples}.  Runs every chunk that became complete."""
+        ids = np.array(list(chunks.keys()), np.int32)
+        arrs = [np.ascontiguousarray(a, np.float32).ravel() for a in chunks.values()]
+        F = ctypes.POINTER(ctypes.c_float)
+        ptrs = (F * max(1, len(arrs)))(*[a.ctypes.data_as(F) for a in arrs])
+        cnt = np.array([a.size for a in arrs], np.int64)
+        _check(_lib.ud_streamer_push(self.handle, len(arrs), ids.ctypes.data_as(ctypes.POINTER(_i32)), ptrs,
+                                     cnt.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))))
+
+    def flush(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        _check(_lib.ud_streamer_flush(self.handle, ids.size, ids.ctypes.data_as(ctypes.POINTER(_i32))))
+
+    def run_buffered(self, runs):
+        """runs: {stream id: (mel [frames, n_mels], frames, valid_frames)} for fresh streams."""
+        ids = np.array(list(runs.keys()), np.int32)
+        mels = [np.ascontiguousarray(r[0], np.float32) for r in runs.values()]
+        F = ctypes.POINTER(ctypes.c_float)
+        ptrs = (F * max(1, len(mels)))(*[m.ctypes.data_as(F) for m in mels])
+        fr = np.array([r[1] for r in runs.values()], np.int32)
+        vf = np.array([r[2] for r in runs.values()], np.int32)
+        P = ctypes.POINTER(_i32)
+        _check(_lib.ud_streamer_run_buffered(self.handle, ids.size, ids.ctypes.data_as(P), ptrs, fr.ctypes.data_as(P),
+                                             vf.ctypes.data_as(P)))
+
+    def tokens(self, sid):
+        n = _i32(0)
+        _check(_lib.ud_streamer_tokens(self.handle, int(sid), None, 0, ctypes.byref(n)))
+        out = np.zeros(max(1, n.value), np.int32)
+        _check(_lib.ud_streamer_tokens(self.handle, int(sid), out.ctypes.data_as(ctypes.POINTER(_i32)), n.value,
+                                       ctypes.byref(n)))
+        return [int(t) for t in out[:n.value]]
+
+    def recorded(self, sid, which):
+        """Recorded kept rows (record = True): which 'enc' [rows, d_model] or 'proj' [rows, hidden]."""
+        w = 0 if which == "enc" else 1
+        r = ctypes.c_int64(0)
+        _check(_lib.ud_streamer_recorded(self.handle, int(sid), w, None, 0, ctypes.byref(r)))
+        width = self._keep[0].config.d_model if w == 0 else self._keep[1].H
+        out = np.zeros((r.value, width), np.float32)
+        _check(_lib.ud_streamer_recorded(self.handle, int(sid), w, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                         r.value, ctypes.byref(r)))
+        return out
+
+    def stats(self):
+        b, c = ctypes.c_int64(0), ctypes.c_int64(0)
+        _check(_lib.ud_streamer_stats(self.handle, ctypes.byref(b), ctypes.byref(c)))
+        return b.value, c.value
+
+    def close(self):
+        if self.handle:
+            _lib.ud_streamer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

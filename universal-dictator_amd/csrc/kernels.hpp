@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+struct ud_mel;
+
 namespace ud {
 
 // Activation codes (Sources/DictatorEngine/Core/Kernels.swift:4-6).
@@ -149,5 +151,25 @@ struct SubFlatArgs {
     int n, T3, F3, T, drop;
 };
 int launch_sub_flatten(const SubFlatArgs& a, bool half_out, hipStream_t st);
+
+// Mel frontend (mel.hip).  One job = frames [f0, f0 + nf) of one clip, written as rows
+// dst[(f - f0) * n_mels + m]; frame f takes the preemphasized samples [160 f - 200, 160 f + 200),
+// read from src[idx - first] (the caller stages every sample the frames need plus the one before);
+// indices >= n_audio are zero padding; frames >= zero_from are written as zeros.
+struct MelJob {
+    const float* src;
+    float* dst;
+    long long first, n_audio, f0, zero_from;
+    int nf, pad_;
+};
+struct MelTables {
+    const float* tab;    // [400][512]: cos (bins 0..255) | sin (bins 0..255), window folded in
+    const float* nyq;    // [2][400]: cos, sin of bin 256
+    const float* fbT;    // [257][n_mels]
+    int n_mels;
+};
+int launch_mel(const MelTables& t, const MelJob* jobs_dev, int n_jobs, int max_nf, hipStream_t st);
+// The device tables of a ud_mel (include/ud_mel.h).
+MelTables mel_tables_of(const struct ::ud_mel* m);
 
 }  // namespace ud

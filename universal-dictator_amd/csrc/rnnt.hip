@@ -247,6 +247,18 @@ static int rupload(float*& dst, const float* src, size_t n) {
     return UD_OK;
 }
 
+extern "C" UD_API int ud_rnnt_get_info(const ud_rnnt* r, int32_t* hidden, int32_t* vocab, int32_t* layers,
+                                       int32_t* enc_dim, int32_t* max_streams, int32_t* max_symbols_per_frame) {
+    if (!r) return rfail(UD_ERR_INVALID, "ud_rnnt_get_info: null decoder");
+    if (hidden) *hidden = r->H;
+    if (vocab) *vocab = r->V;
+    if (layers) *layers = r->L;
+    if (enc_dim) *enc_dim = r->E;
+    if (max_streams) *max_streams = r->S;
+    if (max_symbols_per_frame) *max_symbols_per_frame = r->max_sym;
+    return UD_OK;
+}
+
 extern "C" UD_API int ud_rnnt_set_weight(ud_rnnt* r, const char* name, const float* host, int64_t count) {
     if (!r || !name || !host) return rfail(UD_ERR_INVALID, "ud_rnnt_set_weight: null argument");
     const int64_t H = r->H, V = r->V, E = r->E;

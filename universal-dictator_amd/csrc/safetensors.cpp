@@ -441,3 +441,20 @@ extern "C" UD_API int ud_rnnt_load_safetensors(ud_rnnt* r, const ud_safetensors*
         st, [](const std::string& nn) { return nn.compare(0, 19, "decoder.prediction.") == 0 || nn.compare(0, 6, "joint.") == 0; },
         [r](const char* nn, const float* v, int64_t c) { return ud_rnnt_set_weight(r, nn, v, c); }, n_loaded);
 }
+
+extern "C" UD_API int ud_mel_load_safetensors(const ud_safetensors* st, ud_mel** out) {
+    if (!st || !out) return sfail(UD_ERR_INVALID, "ud_mel_load_safetensors: null argument");
+    *out = nullptr;
+    int32_t dt, nd;
+    int64_t shape[8];
+    int rc = ud_safetensors_info(st, "preprocessor.featurizer.fb", &dt, shape, &nd);
+    if (rc != UD_OK) return rc;
+    int64_t count = 1;
+    for (int i = 0; i < nd; i++) count *= shape[i];
+    if (nd < 1 || shape[nd - 1] != 257 || count % 257 != 0 || count / 257 < 1 || count / 257 > 256)
+        return sfail(UD_ERR_WEIGHT, "preprocessor.featurizer.fb: expected [.., n_mels, 257]");
+    std::vector<float> fb((size_t)count), win(400);
+    if ((rc = ud_safetensors_read_f32(st, "preprocessor.featurizer.fb", fb.data(), count)) != UD_OK) return rc;
+    if ((rc = ud_safetensors_read_f32(st, "preprocessor.featurizer.window", win.data(), 400)) != UD_OK) return rc;
+    return ud_mel_create(fb.data(), (int32_t)(count / 257), win.data(), out);
+}
