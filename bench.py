@@ -1,6 +1,6 @@
 """Benchmark of the cache-aware streaming FastConformer encoder step on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|offline|rnnt]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|offline|rnnt|stream]
                     [--no-cpu-baseline]
 
 A step is one cache-aware encoder chunk step for every stream of the batch: the mel chunk (new rows
@@ -18,7 +18,9 @@ x 128, contexts uniform in 512..4096 keys in bf16 pages of 16 (one line in the s
 tokens/s).  --workload offline measures the whole-utterance rel-pos attention: 8 utterances x 1500
 frames, 8 heads x 128, valid lengths uniform in 900..1500 as key padding (value in frames/s, roofline
 against the bf16 MFMA peak).  --workload rnnt measures the joint.enc projection and greedy RNN-T
-decoding of 64 streams x 2 frames per chunk.
+decoding of 64 streams x 2 frames per chunk.  --workload stream measures live transcription end to
+end through the batched streamer: 64 streams x 160 ms of audio pushed per step, mel frontend,
+subsampling, 24 layers, joint.enc and greedy RNN-T (value in audio-sec/sec, audio in to tokens out).
 """
 import argparse
 import importlib.util
@@ -39,6 +41,7 @@ WORKLOADS = {
     "decode": dict(seqs=64, q_heads=32, kv_heads=8, head_dim=128, page=16, ctx=(512, 4096)),
     "offline": dict(batch=8, frames=1500, heads=8, head_dim=128, valid=(900, 1500)),
     "rnnt": dict(streams=64, T=2, hidden=640, vocab=1025, layers=2),
+    "stream": dict(streams=64, lookahead=1),   # live audio -> tokens, 160 ms chunks
 }
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
 
@@ -328,6 +331,107 @@ def rnnt_bench(ud, args):
     print(json.dumps(result), flush=True)
 
 
+def stream_bench(ud, args):
+    """Live transcription end to end through the batched streamer (include/ud_streamer.h): every
+    timed step pushes 2560 new samples (160 ms) to each of 64 streams, which completes one chunk per
+    stream and runs one batched step: sample staging + H2D, the mel kernel (25 frames per stream,
+    the 9 pre-encode frames recomputed), subsampling, 24 bf16 layers, joint.enc and greedy RNN-T
+    with its host readbacks.  Caches are full before timing (40 warm-up chunks).  A random-init
+    joint emits on every frame or on none, so the decoder is timed at both ends, as in the rnnt
+    workload: every frame blank (value) and every frame at the 10-symbol cap.  value:
+    audio-sec/sec end to end."""
+    wl = WORKLOADS["stream"]
+    S, la = wl["streams"], wl["lookahead"]
+    T = la + 1
+    hop = 160 * 8 * T
+    cfg = ud.EncoderConfig(layers=24, max_chunk=T, max_streams=S, dtype="bf16")
+    log("device %s; workload stream: %d live streams, lookahead %d (%d ms chunks), 24 layers bf16"
+        % (ud.device_arch(), S, la, int(T * FRAME_SEC * 1000)))
+    enc = ud.Encoder(cfg)
+    for l in range(cfg.layers):
+        enc.set_layer_weights(l, ud.synthetic_layer_weights(cfg, 2024, l, ln_jitter=0.0))
+    enc.set_subsampling_weights(ud.synthetic_subsampling_weights(2025))
+    enc.finalize()
+    # a Slaney-like triangular filterbank and a symmetric Hann window (the checkpoint's buffers
+    # are of this form)
+    fb = np.zeros((128, 257), np.float32)
+    edges = np.linspace(1, 256, 130)
+    k = np.arange(257)
+    for m in range(128):
+        lo, mid, hi = edges[m], edges[m + 1], edges[m + 2]
+        fb[m] = np.clip(np.minimum((k - lo) / (mid - lo), (hi - k) / (hi - mid)), 0, None) * (2.0 / (hi - lo))
+    win = (0.5 - 0.5 * np.cos(2 * np.pi * np.arange(400) / 399)).astype(np.float32)
+    fe = ud.MelFrontend(fb, win)
+    rng = np.random.default_rng(5)
+    n_src = 16000 * 12
+    t = np.arange(n_src) / 16000.0
+    srcs = []
+    for b in range(S):
+        f0 = 100 + 60 * rng.random() + 30 * np.sin(2 * np.pi * 0.5 * t + b)
+        ph = 2 * np.pi * np.cumsum(f0) / 16000.0
+        x = sum(np.sin(h * ph) / h for h in range(1, 9)) * (0.2 + 0.15 * np.sin(2 * np.pi * 1.1 * t + b))
+        srcs.append((0.3 * x + 0.003 * rng.standard_normal(n_src)).astype(np.float32))
+    warm = max(args.warmup, 40)
+    res = {}
+    for regime, bias in (("blank", 50.0), ("cap", -50.0)):
+        dec = ud.Rnnt(max_streams=S)
+        dec.set_weights(ud.synthetic_rnnt_weights(2026, blank_bias=bias))
+        st = ud.Streamer(enc, dec, fe, lookahead=la, max_streams=S)
+        ids = [st.open() for _ in range(S)]
+        pos = [0]
+
+        def piece(first):
+            n = (8 * la + 1) * 160 + 40 if first else hop    # exactly completes the next chunk
+            out = {}
+            for b in range(S):
+                a = pos[0] % (n_src - n)
+                out[ids[b]] = srcs[b][a:a + n]
+            pos[0] += n
+            return out
+
+        st.push(piece(True))
+        for _ in range(warm):
+            st.push(piece(False))
+        steps = args.steps if regime == "blank" else max(5, args.steps // 5)
+        b0, c0 = st.stats()
+        tok0 = sum(len(st.tokens(i)) for i in ids)
+        pieces = [piece(False) for _ in range(steps)]
+        ud.synchronize()
+        t0 = time.perf_counter()
+        for p in pieces:
+            st.push(p)
+        wall = time.perf_counter() - t0
+        b1, c1 = st.stats()
+        toks = sum(len(st.tokens(i)) for i in ids) - tok0
+        if b1 - b0 != steps or c1 - c0 != steps * S:
+            raise RuntimeError("expected one batched step of %d streams per push, got %d steps / %d chunks"
+                               % (S, b1 - b0, c1 - c0))
+        res[regime] = (wall * 1000.0 / steps, toks / (steps * S), steps)
+        log("%s regime: %d steps, %.4f ms/step, %.2f tokens per stream-chunk" % (regime, steps, res[regime][0],
+                                                                                 res[regime][1]))
+        st.close()
+        dec.close()
+    ms = res["blank"][0]
+    value = S * T * FRAME_SEC / (ms / 1000.0)
+    result = {
+        "metric": "aggregate audio-sec/sec of live streaming transcription at 64 streams (audio in, tokens out)",
+        "value": round(value, 2),
+        "unit": "audio-sec/sec",
+        "n_gpus": 1, "steps": res["blank"][2], "warmup": warm, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded random-init weights, harmonic test audio, Slaney-like filterbank)",
+        "config": {"workload": "live streaming: 64 streams x 2560 samples pushed per step -> mel -> subsampling -> "
+                               "24 layers -> joint.enc -> greedy RNN-T, lookahead %d (%d ms chunks), every frame blank"
+                               % (la, int(T * FRAME_SEC * 1000)),
+                   "streams": S, "lookahead": la, "chunk_frames": T, "layers": cfg.layers},
+        "cap_regime_ms_per_step": round(res["cap"][0], 4),
+        "cap_regime_tokens_per_stream_chunk": round(res["cap"][1], 3),
+    }
+    fe.close()
+    enc.close()
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -363,6 +467,9 @@ def main():
         return
     if args.workload == "rnnt":
         rnnt_bench(ud, args)
+        return
+    if args.workload == "stream":
+        stream_bench(ud, args)
         return
     wl = WORKLOADS[args.workload]
     S, T = wl["streams"], wl["T"]

@@ -12,16 +12,19 @@
 //     per layer: GEMM xh . [W_ih | W_hh]^T -> slabs;  rnnt_cell_kernel: gates = b + sum(slabs),
 //                c' = f c + i g, h' = o tanh(c') -> cached state; xh = [h' ; h_{l+1}]
 //     GEMM h_top . W_pred^T -> slabs;  rnnt_sum_kernel -> cached projection g
-//   joint (all active streams):
+//   joint (every remaining frame of every active stream, under its current prediction):
 //     rnnt_joint_in_kernel     relu(f_t + g)
 //     GEMM . W_out^T -> slabs; rnnt_argmax_kernel: logits = b + sum(slabs), first index of the max
 //   commit (streams that emitted a token): rnnt_commit_kernel, h, c <- cached state
 //
 // The host keeps the greedy control (RNNT.swift:120-151): blank ends a frame, at most
 // max_symbols tokens per frame, and the prediction for the last token is cached until a token is
-// emitted (so frames that end in blank do not rerun the LSTM).
+// emitted (so frames that end in blank do not rerun the LSTM).  Because a blank leaves the
+// prediction unchanged, the joint results of the frames after a blank are known in advance: one
+// iteration evaluates them all and the host consumes them up to the first emission.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -182,12 +185,17 @@ struct ud_rnnt {
     // per-slot state: committed h, c [S][L][H]; cached prediction ph, pc [S][L][H], pg [S][H]
     float *h = nullptr, *c = nullptr, *ph = nullptr, *pc = nullptr, *pg = nullptr;
     std::vector<int> last, pending;
-    // workspace
-    float *xh = nullptr, *slabs = nullptr, *hsum = nullptr;
-    // slot lists of the three phases in separate buffers: no upload overwrites a list that an
-    // earlier kernel of the same iteration may still read
-    int32_t *dslot_p = nullptr, *dslot_j = nullptr, *dslot_c = nullptr, *dtok = nullptr, *drow = nullptr, *dbest = nullptr;
-    int32_t* hbest = nullptr;                   // pinned
+    // workspace of the prediction network (rows = slots, at most S)
+    float *xh = nullptr, *slabs = nullptr;
+    // workspace of the joint: one row per (stream, frame) pair, grown to the largest call
+    float *hsum = nullptr, *jslabs = nullptr;
+    int cap_pairs = 0;
+    // device lists of the three phases in separate buffers, each uploaded from its own pinned host
+    // buffer: no upload overwrites a list that an earlier kernel or copy may still read
+    int32_t *dslot_p = nullptr, *dtok = nullptr, *dslot_c = nullptr;          // [S]
+    int32_t *dslot_j = nullptr, *drow = nullptr, *dbest = nullptr;            // [cap_pairs]
+    int32_t *hslot_p = nullptr, *htok = nullptr, *hslot_c = nullptr;          // pinned [S]
+    int32_t *hslot_j = nullptr, *hrow = nullptr, *hbest = nullptr;            // pinned [cap_pairs]
 };
 
 static float* ralloc(size_t floats) {
@@ -202,10 +210,12 @@ static void free_rnnt(ud_rnnt* r) {
     for (float* p : r->w) if (p) (void)hipFree(p);
     for (float* p : r->wcat) if (p) (void)hipFree(p);
     for (float* p : r->bias) if (p) (void)hipFree(p);
-    void* ps[] = {r->h, r->c, r->ph, r->pc, r->pg, r->xh, r->slabs, r->hsum, r->dslot_p, r->dslot_j, r->dslot_c,
-                  r->dtok, r->drow, r->dbest};
+    void* ps[] = {r->h, r->c, r->ph, r->pc, r->pg, r->xh, r->slabs, r->hsum, r->jslabs, r->dslot_p, r->dslot_j,
+                  r->dslot_c, r->dtok, r->drow, r->dbest};
     for (void* p : ps) if (p) (void)hipFree(p);
-    if (r->hbest) (void)hipHostFree(r->hbest);
+    for (void* p : {(void*)r->hslot_p, (void*)r->htok, (void*)r->hslot_c, (void*)r->hslot_j, (void*)r->hrow,
+                    (void*)r->hbest})
+        if (p) (void)hipHostFree(p);
     delete r;
 }
 
@@ -225,10 +235,10 @@ extern "C" UD_API int ud_rnnt_create(int32_t hidden, int32_t vocab, int32_t laye
     const size_t gmax = 4 * H > V ? 4 * H : V;
     bool ok = (r->h = ralloc(S * L * H)) && (r->c = ralloc(S * L * H)) && (r->ph = ralloc(S * L * H)) &&
               (r->pc = ralloc(S * L * H)) && (r->pg = ralloc(S * H)) && (r->xh = ralloc(S * 2 * H)) &&
-              (r->slabs = ralloc((size_t)RNNT_KS * S * gmax)) && (r->hsum = ralloc(S * H)) &&
-              (r->dslot_p = (int32_t*)ralloc(S)) && (r->dslot_j = (int32_t*)ralloc(S)) &&
-              (r->dslot_c = (int32_t*)ralloc(S)) && (r->dtok = (int32_t*)ralloc(S)) && (r->drow = (int32_t*)ralloc(S)) &&
-              (r->dbest = (int32_t*)ralloc(S)) && hipHostMalloc((void**)&r->hbest, S * 4) == hipSuccess;
+              (r->slabs = ralloc((size_t)RNNT_KS * S * gmax)) && (r->dslot_p = (int32_t*)ralloc(S)) &&
+              (r->dslot_c = (int32_t*)ralloc(S)) && (r->dtok = (int32_t*)ralloc(S)) &&
+              hipHostMalloc((void**)&r->hslot_p, S * 4) == hipSuccess && hipHostMalloc((void**)&r->htok, S * 4) == hipSuccess &&
+              hipHostMalloc((void**)&r->hslot_c, S * 4) == hipSuccess;
     if (!ok || hipMemset(r->h, 0, S * L * H * 4) != hipSuccess || hipMemset(r->c, 0, S * L * H * 4) != hipSuccess) {
         free_rnnt(r);
         return rfail(UD_ERR_NOMEM, "ud_rnnt_create: device allocation failed");
@@ -330,9 +340,9 @@ extern "C" UD_API int ud_rnnt_reset(ud_rnnt* r, int32_t slot) {
 }
 
 // C[n, N] slabs = A[n, K] (row stride lda) . W[N, K]^T, RNNT_KS K splits, fp32.
-static int slab_gemm(ud_rnnt* r, const float* A, int lda, const float* W, int n, int N, int K, hipStream_t st) {
+static int slab_gemm(float* slabs, const float* A, int lda, const float* W, int n, int N, int K, hipStream_t st) {
     GemmArgs g{};
-    g.A = A; g.W = W; g.C = r->slabs; g.M = n; g.N = N; g.K = K; g.lda = lda; g.ldw = K; g.ldc = N;
+    g.A = A; g.W = W; g.C = slabs; g.M = n; g.N = N; g.K = K; g.lda = lda; g.ldw = K; g.ldc = N;
     g.epi = EPI_PARTIAL; g.act = ACT_NONE; g.out_scale = 1.0f; g.ksplit = RNNT_KS;
     if (launch_gemm(g, false, st) != 0) return rfail(UD_ERR_HIP, "rnnt GEMM launch failed");
     return UD_OK;
@@ -354,27 +364,59 @@ extern "C" UD_API int ud_rnnt_project(ud_rnnt* r, int32_t rows, const float* enc
 // The prediction network for rows (slots) without a cached prediction.
 static int predict(ud_rnnt* r, const std::vector<int>& slots, hipStream_t st) {
     const int n = (int)slots.size(), H = r->H, L = r->L;
-    std::vector<int32_t> tok(n);
-    for (int i = 0; i < n; i++) tok[i] = r->last[slots[i]];
-    RHIPC(hipMemcpyAsync(r->dslot_p, slots.data(), n * 4, hipMemcpyHostToDevice, st));
-    RHIPC(hipMemcpyAsync(r->dtok, tok.data(), n * 4, hipMemcpyHostToDevice, st));
+    for (int i = 0; i < n; i++) {
+        r->hslot_p[i] = slots[i];
+        r->htok[i] = r->last[slots[i]];
+    }
+    RHIPC(hipMemcpyAsync(r->dslot_p, r->hslot_p, n * 4, hipMemcpyHostToDevice, st));
+    RHIPC(hipMemcpyAsync(r->dtok, r->htok, n * 4, hipMemcpyHostToDevice, st));
     hipLaunchKernelGGL(rnnt_embed_kernel, dim3(n), dim3(256), 0, st, r->w[R_EMBED], r->dslot_p, r->dtok, r->h, r->xh, H, L,
                        r->V - 1);
     RLAUNCH("rnnt embed");
     for (int l = 0; l < L; l++) {
-        int rc = slab_gemm(r, r->xh, 2 * H, r->wcat[l], n, 4 * H, 2 * H, st);
+        int rc = slab_gemm(r->slabs, r->xh, 2 * H, r->wcat[l], n, 4 * H, 2 * H, st);
         if (rc != UD_OK) return rc;
         hipLaunchKernelGGL(rnnt_cell_kernel, dim3(n), dim3(256), 0, st, r->slabs, RNNT_KS, n, r->bias[l], r->h, r->c,
                            r->ph, r->pc, r->xh, r->dslot_p, H, L, l);
         RLAUNCH("rnnt cell");
     }
-    int rc = slab_gemm(r, r->xh, 2 * H, r->w[R_PRED_W], n, H, H, st);
+    int rc = slab_gemm(r->slabs, r->xh, 2 * H, r->w[R_PRED_W], n, H, H, st);
     if (rc != UD_OK) return rc;
     hipLaunchKernelGGL(rnnt_sum_kernel, dim3(n), dim3(256), 0, st, r->slabs, RNNT_KS, n, r->w[R_PRED_B], r->pg, r->dslot_p, H);
     RLAUNCH("rnnt pred");
     for (int s : slots) r->pending[s] = 1;
     return UD_OK;
 }
+
+// Grows the joint's pair workspace to P rows.  Called between greedy calls only (every call ends
+// with a stream synchronize), so nothing in flight uses the old buffers.
+static int ensure_pairs(ud_rnnt* r, int P) {
+    if (P <= r->cap_pairs) return UD_OK;
+    void* ds[] = {r->hsum, r->jslabs, r->dslot_j, r->drow, r->dbest};
+    for (void* p : ds) if (p) (void)hipFree(p);
+    for (void* p : {(void*)r->hslot_j, (void*)r->hrow, (void*)r->hbest}) if (p) (void)hipHostFree(p);
+    r->hsum = r->jslabs = nullptr;
+    r->dslot_j = r->drow = r->dbest = r->hslot_j = r->hrow = r->hbest = nullptr;
+    r->cap_pairs = 0;
+    const size_t n = (size_t)P;
+    bool ok = (r->hsum = ralloc(n * r->H)) && (r->jslabs = ralloc((size_t)RNNT_KS * n * r->V)) &&
+              (r->dslot_j = (int32_t*)ralloc(n)) && (r->drow = (int32_t*)ralloc(n)) && (r->dbest = (int32_t*)ralloc(n)) &&
+              hipHostMalloc((void**)&r->hslot_j, n * 4) == hipSuccess && hipHostMalloc((void**)&r->hrow, n * 4) == hipSuccess &&
+              hipHostMalloc((void**)&r->hbest, n * 4) == hipSuccess;
+    if (!ok) return rfail(UD_ERR_NOMEM, "ud_rnnt_greedy: joint workspace allocation failed (%d pairs)", P);
+    r->cap_pairs = P;
+    return UD_OK;
+}
+
+// Greedy decoding with speculative frames.  The sequential rule (RNNT.swift:120-151) evaluates the
+// joint at (frame t, current prediction); a blank moves to t + 1 with the prediction unchanged.  So
+// for each active stream one iteration evaluates the joint at EVERY remaining frame of the call
+// (up to RNNT_SPEC of them) under the current prediction, and the host walks the results: leading
+// blanks advance the frame, the first non-blank is emitted (its frame's symbol count continues
+// from the previous emissions there), and later results of that stream are discarded because the
+// prediction changes.  Every decision is the one the sequential loop makes; a chunk whose frames
+// are all blank costs one iteration instead of one per frame.
+constexpr int RNNT_SPEC = 16;
 
 extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots_host, const float* proj_dev,
                                      int32_t rows_per_stream, const int32_t* frames_host, int32_t* tokens_host,
@@ -395,53 +437,65 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
         if (frames_host[b] > max_frames) max_frames = frames_host[b];
         n_tokens_host[b] = 0;
     }
+    if ((rc = ensure_pairs(r, n * std::min(max_frames, RNNT_SPEC))) != UD_OK) return rc;
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     const int H = r->H, V = r->V, blank = V - 1;
-    std::vector<int> act, emitted(n), pred_slots, commit_slots, next;
-    std::vector<int32_t> aslot, arow;
-    for (int t = 0; t < max_frames; t++) {
+    std::vector<int> act, t(n, 0), em(n, 0), pred_slots, p0(n), p1(n);
+    for (;;) {
         act.clear();
         for (int b = 0; b < n; b++)
-            if (t < frames_host[b]) { act.push_back(b); emitted[b] = 0; }
-        while (!act.empty()) {
-            pred_slots.clear();
-            for (int b : act)
-                if (!r->pending[slots_host[b]]) pred_slots.push_back(slots_host[b]);
-            if (!pred_slots.empty() && (rc = predict(r, pred_slots, st)) != UD_OK) return rc;
-            const int m = (int)act.size();
-            aslot.resize(m);
-            arow.resize(m);
-            for (int i = 0; i < m; i++) { aslot[i] = slots_host[act[i]]; arow[i] = act[i] * rows_per_stream + t; }
-            RHIPC(hipMemcpyAsync(r->dslot_j, aslot.data(), m * 4, hipMemcpyHostToDevice, st));
-            RHIPC(hipMemcpyAsync(r->drow, arow.data(), m * 4, hipMemcpyHostToDevice, st));
-            hipLaunchKernelGGL(rnnt_joint_in_kernel, dim3(m), dim3(256), 0, st, proj_dev, r->drow, r->pg, r->dslot_j,
-                               r->hsum, H);
-            RLAUNCH("rnnt joint input");
-            if ((rc = slab_gemm(r, r->hsum, H, r->w[R_OUT_W], m, V, H, st)) != UD_OK) return rc;
-            hipLaunchKernelGGL(rnnt_argmax_kernel, dim3(m), dim3(256), 0, st, r->slabs, RNNT_KS, m, r->w[R_OUT_B],
-                               r->dbest, V);
-            RLAUNCH("rnnt argmax");
-            RHIPC(hipMemcpyAsync(r->hbest, r->dbest, m * 4, hipMemcpyDeviceToHost, st));
-            RHIPC(hipStreamSynchronize(st));
-            commit_slots.clear();
-            next.clear();
-            for (int i = 0; i < m; i++) {
-                const int b = act[i], s = slots_host[b], k = r->hbest[i];
-                if (k == blank || k < 0 || k >= V) continue;   // (out of range only for NaN logits)
+            if (t[b] < frames_host[b]) act.push_back(b);
+        if (act.empty()) break;
+        pred_slots.clear();
+        for (int b : act)
+            if (!r->pending[slots_host[b]]) pred_slots.push_back(slots_host[b]);
+        if (!pred_slots.empty() && (rc = predict(r, pred_slots, st)) != UD_OK) return rc;
+        int m = 0;
+        for (int b : act) {
+            p0[b] = m;
+            const int end = std::min(frames_host[b], t[b] + RNNT_SPEC);
+            for (int tt = t[b]; tt < end; tt++, m++) {
+                r->hslot_j[m] = slots_host[b];
+                r->hrow[m] = b * rows_per_stream + tt;
+            }
+            p1[b] = m;
+        }
+        RHIPC(hipMemcpyAsync(r->dslot_j, r->hslot_j, m * 4, hipMemcpyHostToDevice, st));
+        RHIPC(hipMemcpyAsync(r->drow, r->hrow, m * 4, hipMemcpyHostToDevice, st));
+        hipLaunchKernelGGL(rnnt_joint_in_kernel, dim3(m), dim3(256), 0, st, proj_dev, r->drow, r->pg, r->dslot_j, r->hsum, H);
+        RLAUNCH("rnnt joint input");
+        if ((rc = slab_gemm(r->jslabs, r->hsum, H, r->w[R_OUT_W], m, V, H, st)) != UD_OK) return rc;
+        hipLaunchKernelGGL(rnnt_argmax_kernel, dim3(m), dim3(256), 0, st, r->jslabs, RNNT_KS, m, r->w[R_OUT_B], r->dbest, V);
+        RLAUNCH("rnnt argmax");
+        RHIPC(hipMemcpyAsync(r->hbest, r->dbest, m * 4, hipMemcpyDeviceToHost, st));
+        RHIPC(hipStreamSynchronize(st));
+        int nc = 0;
+        for (int b : act) {
+            const int s = slots_host[b];
+            for (int p = p0[b]; p < p1[b]; p++) {
+                const int tt = t[b], k = r->hbest[p];
+                if (k == blank || k < 0 || k >= V) {   // (out of range only for NaN logits)
+                    t[b] = tt + 1;
+                    em[b] = 0;
+                    continue;
+                }
                 if (n_tokens_host[b] < cap) tokens_host[(int64_t)b * cap + n_tokens_host[b]] = k;
                 n_tokens_host[b]++;
                 r->last[s] = k;
                 r->pending[s] = 0;
-                commit_slots.push_back(s);
-                if (++emitted[b] < r->max_sym) next.push_back(b);
+                r->hslot_c[nc++] = s;
+                if (++em[b] >= r->max_sym) {
+                    t[b] = tt + 1;
+                    em[b] = 0;
+                }
+                break;
             }
-            if (!commit_slots.empty()) {
-                RHIPC(hipMemcpyAsync(r->dslot_c, commit_slots.data(), commit_slots.size() * 4, hipMemcpyHostToDevice, st));
-                hipLaunchKernelGGL(rnnt_commit_kernel, dim3((unsigned)commit_slots.size()), dim3(256), 0, st, r->ph,
-                                   r->pc, r->h, r->c, r->dslot_c, r->L * H);
-                RLAUNCH("rnnt commit");
-            }
-            act.swap(next);
+        }
+        if (nc) {
+            RHIPC(hipMemcpyAsync(r->dslot_c, r->hslot_c, nc * 4, hipMemcpyHostToDevice, st));
+            hipLaunchKernelGGL(rnnt_commit_kernel, dim3((unsigned)nc), dim3(256), 0, st, r->ph, r->pc, r->h, r->c,
+                               r->dslot_c, r->L * H);
+            RLAUNCH("rnnt commit");
         }
     }
     RHIPC(hipStreamSynchronize(st));
