@@ -405,6 +405,86 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- small-M fp32 (MFMA)
+
+// C = A[M, K] . W[N, K]^T in fp32 on the fp32 MFMA (v_mfma_f32_16x16x4_f32), for the decoder's
+// weight-streaming shapes (tens of rows against thousands of weight rows).
+//   workgroup = 4 waves; wave w owns the 16 output columns n0 = (4 blockIdx.x + w) * 16 ..
+//   blockIdx.y = K split kz (EPI_PARTIAL slabs); blockIdx.z = block of FS_MT * 16 rows of M
+//   per 16-wide k group, lane (c = lane % 16, q = lane / 16) loads W[n0 + c][k + 4q .. 4q + 3] and,
+//   for each of its row tiles t, A[m0 + 16 t + c][k + 4q .. 4q + 3] as float4; MFMA k-step s takes
+//   element s of both, so A and W see the same permutation of the group's 16 k values.
+// Every output sums its K range in the same order whatever M is, so a row's result does not
+// depend on the batch it is computed in.
+constexpr int FS_MT = 4;
+
+__global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmArgs a, int kper) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int c = lane & 15, q = lane >> 4;
+    const int n0 = (blockIdx.x * 4 + w) * 16;
+    if (n0 >= a.N) return;
+    const int kz = blockIdx.y;
+    const int kb = kz * kper, ke = min(a.K, kb + kper);
+    const int m0 = blockIdx.z * 16 * FS_MT;
+    const float* W = static_cast<const float*>(a.W) + (int64_t)min(n0 + c, a.N - 1) * a.ldw + 4 * q;
+    const float* A[FS_MT];
+    bool live[FS_MT];
+#pragma unroll
+    for (int t = 0; t < FS_MT; t++) {
+        const int m = m0 + 16 * t + c;
+        live[t] = m < a.M;
+        A[t] = static_cast<const float*>(a.A) + (int64_t)(live[t] ? m : 0) * a.lda + 4 * q;
+    }
+    f32x4_t acc[FS_MT];
+#pragma unroll
+    for (int t = 0; t < FS_MT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 2
+    for (int k = kb; k < ke; k += 16) {
+        const float4 wv = *reinterpret_cast<const float4*>(W + k);
+        float4 xv[FS_MT];
+#pragma unroll
+        for (int t = 0; t < FS_MT; t++)
+            xv[t] = live[t] ? *reinterpret_cast<const float4*>(A[t] + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int t = 0; t < FS_MT; t++) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t].x, wv.x, acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < FS_MT; t++) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t].y, wv.y, acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < FS_MT; t++) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t].z, wv.z, acc[t], 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < FS_MT; t++) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t].w, wv.w, acc[t], 0, 0, 0);
+    }
+    const int n = n0 + c;
+    if (n >= a.N) return;
+    float* C = static_cast<float*>(a.C);
+#pragma unroll
+    for (int t = 0; t < FS_MT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = m0 + 16 * t + 4 * q + r;
+            if (m >= a.M) continue;
+            float v = acc[t][r];
+            if (a.epi == EPI_PARTIAL) {
+                C[((int64_t)kz * a.M + m) * a.ldc + n] = a.out_scale * v;
+            } else {
+                if (a.bias != nullptr) v += a.bias[n];
+                C[(int64_t)m * a.ldc + n] = apply_act(v, a.act) * a.out_scale;
+            }
+        }
+}
+
+int launch_gemm_f32_small(const GemmArgs& a, int ks, hipStream_t st) {
+    if (a.epi != EPI_PARTIAL && a.epi != EPI_STORE) return -2;
+    if (ks < 1 || (a.epi != EPI_PARTIAL && ks != 1) || a.M < 1 || a.N < 1) return -2;
+    if (a.K % (16 * ks) != 0 || a.lda % 4 != 0 || a.ldw % 4 != 0) return -2;
+    if ((reinterpret_cast<uintptr_t>(a.A) | reinterpret_cast<uintptr_t>(a.W)) & 15) return -2;
+    const int kper = a.K / ks;
+    dim3 grid((a.N + 63) / 64, ks, (a.M + 16 * FS_MT - 1) / (16 * FS_MT));
+    if (grid.z > 65535) return -2;
+    hipLaunchKernelGGL(gemm_f32_small_kernel, grid, dim3(256), 0, st, a, kper);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // ---------------------------------------------------------------- launch
 
 template <int MT, int WK, int NT, int EPI, int ACT, bool H = false, bool BIAS = false>

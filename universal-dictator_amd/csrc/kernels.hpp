@@ -86,6 +86,10 @@ struct GemmArgs {
                                     // (EPI_STORE_F32 with a bias only)
 };
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st);
+// fp32 GEMM for few rows (tens) on the fp32 MFMA: EPI_PARTIAL with ks K splits (slabs
+// [ks][M][ldc]) or EPI_STORE (ks = 1, optional bias, act).  K % (16 ks) == 0, lda and ldw multiples
+// of 4, A and W 16-byte aligned; any M and N.
+int launch_gemm_f32_small(const GemmArgs& a, int ks, hipStream_t st);
 // Most K splits of a bf16 residual projection (partial slabs the workspace holds).
 constexpr int KSPLIT = 4;
 // Rows from which the bf16 projections use the LDS-staged 256-row-tile kernel.

@@ -74,7 +74,7 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
 #pragma unroll
         for (int t = 0; t < MEL_FR; t++) re[t] = im[t] = 0.0f;
         const float* tc = tb.tab + tid;
-#pragma unroll 4
+#pragma unroll 8
         for (int n = 0; n < MEL_WIN; n++) {
             const float c = tc[n * 512], s = tc[n * 512 + 256];
 #pragma unroll
@@ -114,6 +114,7 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
     for (int m = tid & 127; m < tb.n_mels; m += 128) {
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         const float* w = tb.fbT + m;
+#pragma unroll 8
         for (int k = 0; k < MEL_NB; k++) {
             const float fw = w[(long long)k * tb.n_mels];
             const float4 p = pw[k][quad];

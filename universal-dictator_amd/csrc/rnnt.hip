@@ -64,7 +64,9 @@ __global__ void rnnt_cell_kernel(const float* __restrict__ slabs, int ks, int n,
                                  int H, int L, int layer) {
     const int b = blockIdx.x, s = slot[b];
     const int64_t G = 4 * (int64_t)H;
-    for (int j = threadIdx.x; j < H; j += blockDim.x) {
+    {
+        const int j = blockIdx.y * blockDim.x + threadIdx.x;
+        if (j >= H) return;
         float g[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
@@ -88,7 +90,9 @@ __global__ void rnnt_sum_kernel(const float* __restrict__ slabs, int ks, int n, 
                                 float* __restrict__ out, const int32_t* __restrict__ slot, int N) {
     const int b = blockIdx.x;
     const int64_t o = (int64_t)(slot ? slot[b] : b) * N;
-    for (int j = threadIdx.x; j < N; j += blockDim.x) {
+    {
+        const int j = blockIdx.y * blockDim.x + threadIdx.x;
+        if (j >= N) return;
         float v = bias[j];
         for (int z = 0; z < ks; z++) v += slabs[((int64_t)z * n + b) * N + j];
         out[o + j] = v;
@@ -190,6 +194,9 @@ struct ud_rnnt {
     // workspace of the joint: one row per (stream, frame) pair, grown to the largest call
     float *hsum = nullptr, *jslabs = nullptr;
     int cap_pairs = 0;
+    // split-K slabs of ud_rnnt_project, grown to the largest call
+    float* pslabs = nullptr;
+    int cap_proj = 0;
     // device lists of the three phases in separate buffers, each uploaded from its own pinned host
     // buffer: no upload overwrites a list that an earlier kernel or copy may still read
     int32_t *dslot_p = nullptr, *dtok = nullptr, *dslot_c = nullptr;          // [S]
@@ -210,7 +217,7 @@ static void free_rnnt(ud_rnnt* r) {
     for (float* p : r->w) if (p) (void)hipFree(p);
     for (float* p : r->wcat) if (p) (void)hipFree(p);
     for (float* p : r->bias) if (p) (void)hipFree(p);
-    void* ps[] = {r->h, r->c, r->ph, r->pc, r->pg, r->xh, r->slabs, r->hsum, r->jslabs, r->dslot_p, r->dslot_j,
+    void* ps[] = {r->h, r->c, r->ph, r->pc, r->pg, r->xh, r->slabs, r->hsum, r->jslabs, r->pslabs, r->dslot_p, r->dslot_j,
                   r->dslot_c, r->dtok, r->drow, r->dbest};
     for (void* p : ps) if (p) (void)hipFree(p);
     for (void* p : {(void*)r->hslot_p, (void*)r->htok, (void*)r->hslot_c, (void*)r->hslot_j, (void*)r->hrow,
@@ -340,11 +347,13 @@ extern "C" UD_API int ud_rnnt_reset(ud_rnnt* r, int32_t slot) {
 }
 
 // C[n, N] slabs = A[n, K] (row stride lda) . W[N, K]^T, RNNT_KS K splits, fp32.
-static int slab_gemm(float* slabs, const float* A, int lda, const float* W, int n, int N, int K, hipStream_t st) {
+static int slab_gemm(float* slabs, const float* A, int lda, const float* W, int n, int N, int K, hipStream_t st,
+                     int ks = RNNT_KS) {
     GemmArgs g{};
     g.A = A; g.W = W; g.C = slabs; g.M = n; g.N = N; g.K = K; g.lda = lda; g.ldw = K; g.ldc = N;
-    g.epi = EPI_PARTIAL; g.act = ACT_NONE; g.out_scale = 1.0f; g.ksplit = RNNT_KS;
-    if (launch_gemm(g, false, st) != 0) return rfail(UD_ERR_HIP, "rnnt GEMM launch failed");
+    g.epi = EPI_PARTIAL; g.act = ACT_NONE; g.out_scale = 1.0f; g.ksplit = ks;
+    const int rc = launch_gemm_f32_small(g, ks, st);
+    if (rc != 0) return rfail(rc == -2 ? UD_ERR_SHAPE : UD_ERR_HIP, "rnnt GEMM launch failed (%d x %d x %d)", n, N, K);
     return UD_OK;
 }
 
@@ -354,10 +363,22 @@ extern "C" UD_API int ud_rnnt_project(ud_rnnt* r, int32_t rows, const float* enc
         return rfail(UD_ERR_STATE, "ud_rnnt_project: joint.enc weights not set");
     if (rows < 1) return rfail(UD_ERR_SHAPE, "ud_rnnt_project: rows must be >= 1");
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
-    GemmArgs g{};
-    g.A = enc_dev; g.W = r->w[R_ENC_W]; g.C = out_dev; g.M = rows; g.N = r->H; g.K = r->E; g.lda = r->E; g.ldw = r->E;
-    g.ldc = r->H; g.epi = EPI_STORE; g.act = ACT_NONE; g.out_scale = 1.0f; g.bias = r->w[R_ENC_B];
-    if (launch_gemm(g, false, st) != 0) return rfail(UD_ERR_HIP, "ud_rnnt_project: GEMM launch failed");
+    if (rows > r->cap_proj) {
+        // grown between calls only: the caller orders its project calls on one stream, so a
+        // synchronize covers the previous call's use of the old buffer
+        RHIPC(hipStreamSynchronize(st));
+        if (r->pslabs) (void)hipFree(r->pslabs);
+        r->cap_proj = 0;
+        if (!(r->pslabs = ralloc((size_t)RNNT_KS * rows * r->H)))
+            return rfail(UD_ERR_NOMEM, "ud_rnnt_project: workspace allocation failed (%d rows)", rows);
+        r->cap_proj = rows;
+    }
+    const int ks = r->E % (16 * RNNT_KS) == 0 ? RNNT_KS : 1;
+    int rc = slab_gemm(r->pslabs, enc_dev, r->E, r->w[R_ENC_W], rows, r->H, r->E, st, ks);
+    if (rc != UD_OK) return rc;
+    hipLaunchKernelGGL(rnnt_sum_kernel, dim3(rows, (r->H + 63) / 64), dim3(64), 0, st, r->pslabs, ks, rows,
+                       r->w[R_ENC_B], out_dev, (const int32_t*)nullptr, r->H);
+    RLAUNCH("ud_rnnt_project sum");
     return UD_OK;
 }
 
@@ -376,13 +397,14 @@ static int predict(ud_rnnt* r, const std::vector<int>& slots, hipStream_t st) {
     for (int l = 0; l < L; l++) {
         int rc = slab_gemm(r->slabs, r->xh, 2 * H, r->wcat[l], n, 4 * H, 2 * H, st);
         if (rc != UD_OK) return rc;
-        hipLaunchKernelGGL(rnnt_cell_kernel, dim3(n), dim3(256), 0, st, r->slabs, RNNT_KS, n, r->bias[l], r->h, r->c,
+        hipLaunchKernelGGL(rnnt_cell_kernel, dim3(n, (H + 63) / 64), dim3(64), 0, st, r->slabs, RNNT_KS, n, r->bias[l], r->h, r->c,
                            r->ph, r->pc, r->xh, r->dslot_p, H, L, l);
         RLAUNCH("rnnt cell");
     }
     int rc = slab_gemm(r->slabs, r->xh, 2 * H, r->w[R_PRED_W], n, H, H, st);
     if (rc != UD_OK) return rc;
-    hipLaunchKernelGGL(rnnt_sum_kernel, dim3(n), dim3(256), 0, st, r->slabs, RNNT_KS, n, r->w[R_PRED_B], r->pg, r->dslot_p, H);
+    hipLaunchKernelGGL(rnnt_sum_kernel, dim3(n, (H + 63) / 64), dim3(64), 0, st, r->slabs, RNNT_KS, n, r->w[R_PRED_B], r->pg,
+                       r->dslot_p, H);
     RLAUNCH("rnnt pred");
     for (int s : slots) r->pending[s] = 1;
     return UD_OK;
