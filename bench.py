@@ -371,6 +371,21 @@ def stream_bench(ud, args):
         ph = 2 * np.pi * np.cumsum(f0) / 16000.0
         x = sum(np.sin(h * ph) / h for h in range(1, 9)) * (0.2 + 0.15 * np.sin(2 * np.pi * 1.1 * t + b))
         srcs.append((0.3 * x + 0.003 * rng.standard_normal(n_src)).astype(np.float32))
+    # the mel kernel alone at the streamer's launch shape (64 jobs x 25 frames), HIP events on its stream
+    hs = ud.HipStream()
+    clip = 24 * 160                      # 25 frames
+    ab = ud.DeviceBuffer.from_numpy(np.stack([s[:clip] for s in srcs]))
+    mb = ud.DeviceBuffer(S * 25 * 128 * 4)
+    for _ in range(5):
+        fe.features_device(S, ab, clip, [clip] * S, mb, 25, hip_stream=hs)
+    e0, e1 = ud.Event(), ud.Event()
+    e0.record(hs)
+    for _ in range(50):
+        fe.features_device(S, ab, clip, [clip] * S, mb, 25, hip_stream=hs)
+    e1.record(hs)
+    e1.synchronize()
+    mel_us = e0.elapsed_ms(e1) * 1000.0 / 50
+    log("mel kernel: %.1f us per step (64 streams x 25 frames)" % mel_us)
     warm = max(args.warmup, 40)
     res = {}
     for regime, bias in (("blank", 50.0), ("cap", -50.0)):
@@ -424,6 +439,7 @@ def stream_bench(ud, args):
                                "24 layers -> joint.enc -> greedy RNN-T, lookahead %d (%d ms chunks), every frame blank"
                                % (la, int(T * FRAME_SEC * 1000)),
                    "streams": S, "lookahead": la, "chunk_frames": T, "layers": cfg.layers},
+        "mel_us_per_step": round(mel_us, 2),
         "cap_regime_ms_per_step": round(res["cap"][0], 4),
         "cap_regime_tokens_per_stream_chunk": round(res["cap"][1], 3),
     }

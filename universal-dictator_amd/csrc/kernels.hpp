@@ -167,8 +167,8 @@ struct MelJob {
     int nf, pad_;
 };
 struct MelTables {
-    const float* tab;    // [400][512]: cos (bins 0..255) | sin (bins 0..255), window folded in
-    const float* nyq;    // [2][400]: cos, sin of bin 256
+    const float* cos512; // cos(2 pi j / 512), j < 512
+    const float* win;    // [400] analysis window
     const float* fbT;    // [257][n_mels]
     int n_mels;
 };

@@ -3,20 +3,25 @@
 // The reference computes the features on the CPU (Sources/DictatorCore/Audio/NemoMel.swift:85-107):
 // two sgemms of the [T, 400] frame matrix against window-folded cos/sin tables [257, 400], the
 // power |X|^2 (as sqrt then square), a third sgemm against the filterbank and log(x + 2^-24).
-// Here one workgroup takes MEL_FR frames of one job and does all of it:
+// Here one workgroup takes MEL_FR frames of one job and does all of it in LDS:
 //
-//   stage    the frames' preemphasized samples into LDS, sample-major (xs[n][t]), so one
-//            16-byte LDS read broadcasts 4 frames' sample n to the whole wave
-//   DFT      thread k = bin k (0..255) runs over the 400 samples: 2 table loads (tab[n][k],
-//            coalesced over the wave, L2-resident: the tables are 820 KB), 2 LDS reads and
-//            2 * MEL_FR FMAs per sample; bin 256 (Nyquist) is a 32-lane split reduction per frame
+//   stage    the frames' preemphasized samples times the window, sample-major (xs[n][t]), so one
+//            16-byte LDS read broadcasts 4 frames' sample n to the whole wave; the 512-entry
+//            cos table; all global loads of a thread are issued before its first LDS store
+//   DFT      thread k = bin k (0..255) runs over the 400 samples.  The angle of (k, n) is
+//            2 pi j / 512 with j = k (n + 56) mod 512 (the window sits at offset 56 of the
+//            512-point frame), so cos and -sin are two reads of the LDS cos table, at j and at
+//            j + 128; j advances by k per sample.  No global load in the loop: 2 table reads,
+//            2 broadcast frame reads and 2 * MEL_FR FMAs per sample.  Bin 256 (Nyquist) is a
+//            32-lane split reduction per frame
 //   power    into LDS pw[k][t]
 //   mel      thread (m, frame quad) sums fbT[k][m] * pw[k][t] over the 257 bins, then log
 //
-// Every frame is computed the same way wherever it sits in the grid (fixed summation order), so a
-// frame recomputed by a later streaming chunk is bit-identical to its first computation.  The
-// preemphasis is evaluated as the reference writes it, a[i] - 0.97 * a[i-1] with both roundings
-// (no contraction), so the staged samples are exactly the reference's.
+// Rounding: the reference multiplies x by float(cos) * window (its table entries); here
+// (x * window) * float(cos): the same terms to within an ulp each.  Every frame is computed the
+// same way wherever it sits in the grid (fixed summation order), so a frame recomputed by a later
+// streaming chunk is bit-identical to its first computation.  The preemphasis is evaluated as the
+// reference writes it, a[i] - 0.97 * a[i-1] with both roundings (contraction off).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -36,16 +41,24 @@ constexpr int MEL_FR = 8;          // frames per workgroup
 constexpr int MEL_WIN = 400;
 constexpr int MEL_HOP = 160;
 constexpr int MEL_NB = 257;        // rfft bins of n_fft 512
+constexpr int MEL_OFF = 56;        // (512 - 400) / 2
 constexpr int MEL_THREADS = 256;
 
+__device__ __forceinline__ float preemph(float a, float prev) {
+#pragma clang fp contract(off)
+    return a - 0.97f * prev;
+}
+
 __device__ __forceinline__ float mel_power(float re, float im) {
-    const float mag = __fsqrt_rn(__fadd_rn(__fmul_rn(re, re), __fmul_rn(im, im)));
-    return __fmul_rn(mag, mag);
+#pragma clang fp contract(off)
+    const float mag = sqrtf(re * re + im * im);
+    return mag * mag;
 }
 
 __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restrict__ jobs, MelTables tb) {
     __shared__ float4 xs[MEL_WIN][MEL_FR / 4];
     __shared__ float4 pw[MEL_NB][MEL_FR / 4];
+    __shared__ float cs[512];
     const MelJob J = jobs[blockIdx.y];
     const int j0 = blockIdx.x * MEL_FR;
     if (j0 >= J.nf) return;
@@ -53,30 +66,70 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
     const int nfr = min(MEL_FR, J.nf - j0);
     const long long fbase = J.f0 + j0;
 
+    constexpr int SU = (MEL_FR * MEL_WIN + MEL_THREADS - 1) / MEL_THREADS;
     float* xsf = reinterpret_cast<float*>(xs);
-    for (int e = tid; e < MEL_FR * MEL_WIN; e += MEL_THREADS) {
+    float va[SU], vb[SU], wv[SU];
+    long long ix[SU];
+#pragma unroll
+    for (int u = 0; u < SU; u++) {
+        const int e = tid + MEL_THREADS * u;
         const int t = e / MEL_WIN, i = e - t * MEL_WIN;
         const long long f = fbase + t;
-        float v = 0.0f;
-        if (t < nfr && f < J.zero_from) {
+        ix[u] = -1;
+        va[u] = vb[u] = wv[u] = 0.0f;
+        if (e < MEL_FR * MEL_WIN && t < nfr && f < J.zero_from) {
             const long long idx = f * MEL_HOP - 200 + i;
             if (idx >= 0 && idx < J.n_audio) {
-                const float a = J.src[idx - J.first];
-                v = idx == 0 ? a : __fsub_rn(a, __fmul_rn(0.97f, J.src[idx - 1 - J.first]));
+                ix[u] = idx;
+                va[u] = J.src[idx - J.first];
+                if (idx > 0) vb[u] = J.src[idx - 1 - J.first];
+                wv[u] = tb.win[i];
             }
         }
-        xsf[i * MEL_FR + t] = v;
     }
+    const float c0 = tb.cos512[tid], c1 = tb.cos512[tid + MEL_THREADS];
+#pragma unroll
+    for (int u = 0; u < SU; u++) {
+        const int e = tid + MEL_THREADS * u;
+        if (e < MEL_FR * MEL_WIN) {
+            const int t = e / MEL_WIN, i = e - t * MEL_WIN;
+            const float x = ix[u] < 0 ? 0.0f : ix[u] == 0 ? va[u] : preemph(va[u], vb[u]);
+            xsf[i * MEL_FR + t] = x * wv[u];
+        }
+    }
+    cs[tid] = c0;
+    cs[tid + MEL_THREADS] = c1;
     __syncthreads();
 
+    {
+        // bin 256: j = 256 (n + 56) mod 512; frame t = tid / 32, lane l of 32 takes samples
+        // l, l + 32, ...; butterfly over the 32 lanes (xor offsets below 32 stay inside each half
+        // of the wave)
+        const int t = tid >> 5, l = tid & 31;
+        float r = 0.0f, q = 0.0f;
+        for (int n = l; n < MEL_WIN; n += 32) {
+            const int j = (256 * (n + MEL_OFF)) & 511;
+            const float x = xsf[n * MEL_FR + t];
+            r = fmaf(cs[j], x, r);
+            q = fmaf(cs[(j + 128) & 511], x, q);
+        }
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) {
+            r += __shfl_xor(r, o);
+            q += __shfl_xor(q, o);
+        }
+        if (l == 0) reinterpret_cast<float*>(pw[256])[t] = mel_power(r, q);
+    }
     {
         float re[MEL_FR], im[MEL_FR];
 #pragma unroll
         for (int t = 0; t < MEL_FR; t++) re[t] = im[t] = 0.0f;
-        const float* tc = tb.tab + tid;
-#pragma unroll 8
+        const int k = tid;
+        int j = (k * MEL_OFF) & 511;
+#pragma unroll 4
         for (int n = 0; n < MEL_WIN; n++) {
-            const float c = tc[n * 512], s = tc[n * 512 + 256];
+            const float c = cs[j], s = cs[(j + 128) & 511];
+            j = (j + k) & 511;
 #pragma unroll
             for (int q = 0; q < MEL_FR / 4; q++) {
                 const float4 x = xs[n][q];
@@ -91,30 +144,13 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
             pw[tid][q] = make_float4(mel_power(re[4 * q], im[4 * q]), mel_power(re[4 * q + 1], im[4 * q + 1]),
                                      mel_power(re[4 * q + 2], im[4 * q + 2]), mel_power(re[4 * q + 3], im[4 * q + 3]));
     }
-    {
-        // bin 256: frame t = tid / 32, lane l of 32 takes samples l, l + 32, ...; butterfly over
-        // the 32 lanes (xor offsets below 32 stay inside each half of the wave)
-        const int t = tid >> 5, l = tid & 31;
-        float r = 0.0f, q = 0.0f;
-        for (int n = l; n < MEL_WIN; n += 32) {
-            const float x = xsf[n * MEL_FR + t];
-            r = fmaf(tb.nyq[n], x, r);
-            q = fmaf(tb.nyq[MEL_WIN + n], x, q);
-        }
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) {
-            r += __shfl_xor(r, o);
-            q += __shfl_xor(q, o);
-        }
-        if (l == 0) reinterpret_cast<float*>(pw[256])[t] = mel_power(r, q);
-    }
     __syncthreads();
 
     const int quad = tid >> 7;   // frames 4 quad .. 4 quad + 3
     for (int m = tid & 127; m < tb.n_mels; m += 128) {
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         const float* w = tb.fbT + m;
-#pragma unroll 8
+#pragma unroll 32
         for (int k = 0; k < MEL_NB; k++) {
             const float fw = w[(long long)k * tb.n_mels];
             const float4 p = pw[k][quad];
@@ -155,25 +191,32 @@ static int mfail(int code, const char* fmt, ...) {
     return ud_set_error(code, buf);
 }
 
+constexpr int MEL_RING = 4;   // job lists of ud_mel_features in flight before a call waits
+
 struct ud_mel {
     int n_mels = 0;
-    float *tab = nullptr, *nyq = nullptr, *fbT = nullptr;
-    MelJob* djobs = nullptr;     // device job list of ud_mel_features
-    MelJob* hjobs = nullptr;     // pinned staging of it
-    int cap_jobs = 0;
-    hipEvent_t copied = nullptr;  // the last job upload; the staging is rewritten only after it
+    float *cos512 = nullptr, *win = nullptr, *fbT = nullptr;
+    // ring of job lists for ud_mel_features: slot i's pinned staging is rewritten only after the
+    // kernel that read slot i's device copy has finished (its event)
+    MelJob* djobs[MEL_RING] = {};
+    MelJob* hjobs[MEL_RING] = {};
+    hipEvent_t done[MEL_RING] = {};
+    int cap_jobs = 0, next = 0;
 };
 
 namespace ud {
-MelTables mel_tables_of(const ::ud_mel* m) { return MelTables{m->tab, m->nyq, m->fbT, m->n_mels}; }
+MelTables mel_tables_of(const ::ud_mel* m) { return MelTables{m->cos512, m->win, m->fbT, m->n_mels}; }
 }  // namespace ud
 
 static void free_mel(ud_mel* m) {
     if (!m) return;
     (void)hipDeviceSynchronize();
-    for (void* p : {(void*)m->tab, (void*)m->nyq, (void*)m->fbT, (void*)m->djobs}) if (p) (void)hipFree(p);
-    if (m->hjobs) (void)hipHostFree(m->hjobs);
-    if (m->copied) (void)hipEventDestroy(m->copied);
+    for (void* p : {(void*)m->cos512, (void*)m->win, (void*)m->fbT}) if (p) (void)hipFree(p);
+    for (int i = 0; i < MEL_RING; i++) {
+        if (m->djobs[i]) (void)hipFree(m->djobs[i]);
+        if (m->hjobs[i]) (void)hipHostFree(m->hjobs[i]);
+        if (m->done[i]) (void)hipEventDestroy(m->done[i]);
+    }
     delete m;
 }
 
@@ -181,30 +224,19 @@ extern "C" UD_API int ud_mel_create(const float* fb_host, int32_t n_mels, const 
     if (!out || !fb_host || !window_host) return mfail(UD_ERR_INVALID, "ud_mel_create: null argument");
     *out = nullptr;
     if (n_mels < 1 || n_mels > 256) return mfail(UD_ERR_SHAPE, "ud_mel_create: n_mels %d outside 1..256", n_mels);
-    // Tables as NemoMel.swift:28-39 builds them: phase in double, float(cos) * window in float.
-    const int off = (512 - MEL_WIN) / 2;
-    std::vector<float> tab((size_t)MEL_WIN * 512), nyq(2 * MEL_WIN), fbT((size_t)MEL_NB * n_mels);
-    for (int k = 0; k < MEL_NB; k++)
-        for (int n = 0; n < MEL_WIN; n++) {
-            const double phase = 2.0 * 3.14159265358979323846 * (double)k * (double)(n + off) / 512.0;
-            const float c = (float)cos(phase) * window_host[n];
-            const float s = (float)(-sin(phase)) * window_host[n];
-            if (k < 256) {
-                tab[(size_t)n * 512 + k] = c;
-                tab[(size_t)n * 512 + 256 + k] = s;
-            } else {
-                nyq[n] = c;
-                nyq[MEL_WIN + n] = s;
-            }
-        }
+    // cos(2 pi j / 512) in double, rounded to float (the reference's float(cos(phase)),
+    // NemoMel.swift:33-35), the window as given, the filterbank transposed to [257][n_mels]
+    std::vector<float> cs(512), fbT((size_t)MEL_NB * n_mels);
+    for (int j = 0; j < 512; j++) cs[j] = (float)cos(2.0 * 3.14159265358979323846 * (double)j / 512.0);
     for (int m = 0; m < n_mels; m++)
         for (int k = 0; k < MEL_NB; k++) fbT[(size_t)k * n_mels + m] = fb_host[(size_t)m * MEL_NB + k];
     ud_mel* m = new ud_mel();
     m->n_mels = n_mels;
-    bool ok = hipMalloc(&m->tab, tab.size() * 4) == hipSuccess && hipMalloc(&m->nyq, nyq.size() * 4) == hipSuccess &&
-              hipMalloc(&m->fbT, fbT.size() * 4) == hipSuccess && hipEventCreateWithFlags(&m->copied, hipEventDisableTiming) == hipSuccess;
-    ok = ok && hipMemcpy(m->tab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(m->nyq, nyq.data(), nyq.size() * 4, hipMemcpyHostToDevice) == hipSuccess &&
+    bool ok = hipMalloc(&m->cos512, 512 * 4) == hipSuccess && hipMalloc(&m->win, MEL_WIN * 4) == hipSuccess &&
+              hipMalloc(&m->fbT, fbT.size() * 4) == hipSuccess;
+    for (int i = 0; ok && i < MEL_RING; i++) ok = hipEventCreateWithFlags(&m->done[i], hipEventDisableTiming) == hipSuccess;
+    ok = ok && hipMemcpy(m->cos512, cs.data(), 512 * 4, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(m->win, window_host, MEL_WIN * 4, hipMemcpyHostToDevice) == hipSuccess &&
          hipMemcpy(m->fbT, fbT.data(), fbT.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
     if (!ok) {
         free_mel(m);
@@ -235,21 +267,27 @@ extern "C" UD_API int ud_mel_features(ud_mel* m, int32_t n, const float* audio_d
     }
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     if (n > m->cap_jobs) {
-        (void)hipEventSynchronize(m->copied);
-        if (m->djobs) (void)hipFree(m->djobs);
-        if (m->hjobs) (void)hipHostFree(m->hjobs);
-        m->djobs = nullptr;
-        m->hjobs = nullptr;
+        for (int i = 0; i < MEL_RING; i++) {
+            (void)hipEventSynchronize(m->done[i]);
+            if (m->djobs[i]) (void)hipFree(m->djobs[i]);
+            if (m->hjobs[i]) (void)hipHostFree(m->hjobs[i]);
+            m->djobs[i] = nullptr;
+            m->hjobs[i] = nullptr;
+        }
         m->cap_jobs = 0;
-        if (hipMalloc(&m->djobs, (size_t)n * sizeof(MelJob)) != hipSuccess ||
-            hipHostMalloc((void**)&m->hjobs, (size_t)n * sizeof(MelJob)) != hipSuccess)
-            return mfail(UD_ERR_NOMEM, "ud_mel_features: job list allocation failed");
+        for (int i = 0; i < MEL_RING; i++)
+            if (hipMalloc(&m->djobs[i], (size_t)n * sizeof(MelJob)) != hipSuccess ||
+                hipHostMalloc((void**)&m->hjobs[i], (size_t)n * sizeof(MelJob)) != hipSuccess)
+                return mfail(UD_ERR_NOMEM, "ud_mel_features: job list allocation failed");
         m->cap_jobs = n;
     }
-    if (hipEventSynchronize(m->copied) != hipSuccess) return mfail(UD_ERR_HIP, "ud_mel_features: event wait failed");
+    const int slot = m->next;
+    m->next = (m->next + 1) % MEL_RING;
+    if (hipEventSynchronize(m->done[slot]) != hipSuccess) return mfail(UD_ERR_HIP, "ud_mel_features: event wait failed");
+    MelJob* hj = m->hjobs[slot];
     for (int b = 0; b < n; b++) {
         const int64_t ns = n_samples_host[b];
-        MelJob& j = m->hjobs[b];
+        MelJob& j = hj[b];
         j.src = audio_dev + (int64_t)b * audio_stride;
         j.dst = out_dev + (int64_t)b * out_rows * m->n_mels;
         j.first = 0;
@@ -260,10 +298,10 @@ extern "C" UD_API int ud_mel_features(ud_mel* m, int32_t n, const float* audio_d
         j.pad_ = 0;
         if (frames_host) frames_host[b] = j.nf;
     }
-    if (hipMemcpyAsync(m->djobs, m->hjobs, (size_t)n * sizeof(MelJob), hipMemcpyHostToDevice, st) != hipSuccess ||
-        hipEventRecord(m->copied, st) != hipSuccess)
+    if (hipMemcpyAsync(m->djobs[slot], hj, (size_t)n * sizeof(MelJob), hipMemcpyHostToDevice, st) != hipSuccess)
         return mfail(UD_ERR_HIP, "ud_mel_features: job upload failed");
-    const int rc = launch_mel(mel_tables_of(m), m->djobs, n, max_nf, st);
+    const int rc = launch_mel(mel_tables_of(m), m->djobs[slot], n, max_nf, st);
     if (rc != 0) return mfail(rc == -2 ? UD_ERR_SHAPE : UD_ERR_HIP, "ud_mel_features: launch failed");
+    if (hipEventRecord(m->done[slot], st) != hipSuccess) return mfail(UD_ERR_HIP, "ud_mel_features: event record failed");
     return UD_OK;
 }
