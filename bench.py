@@ -282,7 +282,7 @@ def offline_bench(ud, args):
 
 def rnnt_bench(ud, args):
     """joint.enc projection + greedy RNN-T decode of 64 streams x 2 encoder frames per chunk (the
-    step after the encoder, Nemotron.swift:82-90 + RNNT.swift:120-151), timed at the two emission
+    step after the encoder, Nemotron.swift:82-90 + RNNT.swift:125-151), timed at the two emission
     extremes: every frame blank (one joint per frame, the cached prediction reused) and every frame
     at the 10-symbol cap (a prediction and a joint per symbol).  value: audio-sec/sec of the
     all-blank regime."""

@@ -52,7 +52,7 @@ UD_API int ud_rnnt_reset(ud_rnnt* r, int32_t slot);
  * enc [rows, enc_dim] . W_enc^T + b_enc, fp32.  Asynchronous on hip_stream. */
 UD_API int ud_rnnt_project(ud_rnnt* r, int32_t rows, const float* enc_dev, float* out_dev, void* hip_stream);
 
-/* RNNTDecoder.greedy (RNNT.swift:120-151) for n streams at once.
+/* RNNTDecoder.greedy (RNNT.swift:125-151) for n streams at once.
  *   slots_host[n]     distinct stream slots; their states advance
  *   proj_dev          fp32 projected frames: stream b's frame t is row b * rows_per_stream + t
  *   frames_host[n]    frames to decode per stream (<= rows_per_stream)

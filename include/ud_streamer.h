@@ -4,7 +4,7 @@
  * Replaces NemotronStreamer (Sources/DictatorCore/Nemotron/NemotronStreamer.swift:16-153) with
  * the schedule of NemotronSchedule (Sources/DictatorCore/Nemotron/NemotronSchedule.swift:7-17)
  * and the encoder step of MetalNemotronEncoder.step (Sources/DictatorEngine/Models/Nemotron.swift:
- * 75-100).  The reference runs one streamer per stream, one chunk at a time.  Here every open
+ * 74-92).  The reference runs one streamer per stream, one chunk at a time.  Here every open
  * stream of the streamer that has a chunk ready joins ONE batched step:
  *
  *   mel frames (live input: ud_mel from the stream's samples; buffered input: the caller's rows)

@@ -430,7 +430,7 @@ class Schedule:
 class Streamer:
     """NemotronStreamer (Sources/DictatorCore/Nemotron/NemotronStreamer.swift:16-153) driving the
     oracle encoder step of MetalNemotronEncoder.step (Sources/DictatorEngine/Models/Nemotron.swift:
-    75-100): subsampling + drop, the stream step, joint.enc on the kept frames, greedy RNN-T.
+    74-92): subsampling + drop, the stream step, joint.enc on the kept frames, greedy RNN-T.
     One stream; every chunk runs at its own (unpadded) size, as the reference does.
 
     model: an oracle Model prepared for the rel range of the schedule; sw: subsampling weights;

@@ -35,18 +35,31 @@ def _hf_rnnt(name):
     return name
 
 
-def _write(path, entries):
-    """entries: name -> (fp32 array, 'F32' | 'BF16' | 'F16').  Returns name -> the fp32 values a
-    reader widens the stored tensor to."""
-    import torch
-    from safetensors.torch import save_file
-    dt = {"F32": torch.float32, "BF16": torch.bfloat16, "F16": torch.float16}
-    ts, widened = {}, {}
+def _write(ud, path, entries):
+    """Writes a safetensors file (8-byte little-endian header length, JSON header, raw data) without
+    torch, which must not load into a GPU test process.  entries: name -> (fp32 array, 'F32' |
+    'BF16' | 'F16').  Returns name -> the fp32 values a reader widens the stored tensor to."""
+    import json
+    import struct
+    header, blobs, widened, off = {"__metadata__": {"format": "pt"}}, [], {}, 0
     for name, (a, d) in entries.items():
-        t = torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(dt[d]).contiguous()
-        ts[name] = t
-        widened[name] = t.to(torch.float32).numpy()
-    save_file(ts, path, metadata={"format": "pt"})
+        a = np.ascontiguousarray(a, np.float32)
+        if d == "F32":
+            raw, w = a.tobytes(), a
+        elif d == "F16":
+            h = a.astype(np.float16)
+            raw, w = h.tobytes(), h.astype(np.float32)
+        else:
+            w = ud.round_bf16(a)
+            raw = (w.view(np.uint32) >> 16).astype(np.uint16).tobytes()
+        header[name] = {"dtype": d, "shape": list(a.shape), "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        widened[name] = w.reshape(a.shape)
+        off += len(raw)
+    h = json.dumps(header).encode()
+    h += b" " * (-len(h) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)) + h + b"".join(blobs))
     return widened
 
 
@@ -76,7 +89,7 @@ def test_encoder_loader_matches_set_weight(gpu, tmp_path):
         entries[k] = (a, "F32")
     entries["preprocessor.featurizer.fb"] = (np.ones((1, 128, 257), np.float32), "F32")
     p = str(tmp_path / "enc.safetensors")
-    widened = _write(p, entries)
+    widened = _write(ud, p, entries)
 
     st = ud.SafeTensors(p)
     a = ud.Encoder(cfg)
@@ -121,7 +134,7 @@ def test_rnnt_loader_matches_set_weight(gpu, tmp_path):
         expect[name] = k
     entries["encoder.layers.0.norm_out.weight"] = (np.ones(1024, np.float32), "F32")
     p = str(tmp_path / "dec.safetensors")
-    widened = _write(p, entries)
+    widened = _write(ud, p, entries)
     assert sum(n != expect[n] for n in entries if n in expect) >= 7   # HF aliases in the file
 
     st = ud.SafeTensors(p)

@@ -17,7 +17,7 @@
 //     GEMM . W_out^T -> slabs; rnnt_argmax_kernel: logits = b + sum(slabs), first index of the max
 //   commit (streams that emitted a token): rnnt_commit_kernel, h, c <- cached state
 //
-// The host keeps the greedy control (RNNT.swift:120-151): blank ends a frame, at most
+// The host keeps the greedy control (RNNT.swift:125-151): blank ends a frame, at most
 // max_symbols tokens per frame, and the prediction for the last token is cached until a token is
 // emitted (so frames that end in blank do not rerun the LSTM).  Because a blank leaves the
 // prediction unchanged, the joint results of the frames after a blank are known in advance: one
@@ -430,7 +430,7 @@ static int ensure_pairs(ud_rnnt* r, int P) {
     return UD_OK;
 }
 
-// Greedy decoding with speculative frames.  The sequential rule (RNNT.swift:120-151) evaluates the
+// Greedy decoding with speculative frames.  The sequential rule (RNNT.swift:125-151) evaluates the
 // joint at (frame t, current prediction); a blank moves to t + 1 with the prediction unchanged.  So
 // for each active stream one iteration evaluates the joint at EVERY remaining frame of the call
 // (up to RNNT_SPEC of them) under the current prediction, and the host walks the results: leading
