@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <numeric>
 #include <string>
 #include <vector>
 
@@ -108,6 +109,8 @@ struct LayerDev {
     uint32_t set_mask = 0;
 };
 
+constexpr int MAX_GROUPS = 4;
+
 struct GraphEntry {
     int n, T;
     const void* x;
@@ -165,6 +168,11 @@ struct ud_encoder {
     bool finalized = false;
     bool use_graphs = true;
     hipStream_t capture_stream = nullptr;
+    // groups of streams stepped concurrently (fork/join inside the captured graph)
+    hipStream_t gstream[MAX_GROUPS] = {};
+    hipEvent_t fork_ev = nullptr;
+    hipEvent_t join_ev[MAX_GROUPS] = {};
+    int groups_override = 0;        // UD_GROUPS (1..MAX_GROUPS), 0 = the built-in rule
     std::vector<GraphEntry> graphs;
     SubDev sub;
 };
@@ -194,6 +202,11 @@ static void free_encoder(ud_encoder* e) {
         if (e->desc_ev[i]) (void)hipEventDestroy(e->desc_ev[i]);
     }
     if (e->capture_stream) (void)hipStreamDestroy(e->capture_stream);
+    for (int g = 0; g < MAX_GROUPS; g++) {
+        if (e->gstream[g]) (void)hipStreamDestroy(e->gstream[g]);
+        if (e->join_ev[g]) (void)hipEventDestroy(e->join_ev[g]);
+    }
+    if (e->fork_ev) (void)hipEventDestroy(e->fork_ev);
     for (ud_stream* s : e->live) delete s;
     delete e;
 }
@@ -279,9 +292,20 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
     if (hipMemset(e->kring, 0, e->ring_layer_elems * e->layers * esz) != hipSuccess ||
         hipMemset(e->vring, 0, e->ring_layer_elems * e->layers * esz) != hipSuccess ||
         hipMemset(e->cring, 0, e->cring_layer_elems * e->layers * 4) != hipSuccess ||
-        hipStreamCreateWithFlags(&e->capture_stream, hipStreamNonBlocking) != hipSuccess) {
+        hipStreamCreateWithFlags(&e->capture_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&e->fork_ev, hipEventDisableTiming) != hipSuccess) {
         free_encoder(e);
         return fail(UD_ERR_HIP, "ud_encoder_create: initialisation failed");
+    }
+    for (int g = 0; g < MAX_GROUPS; g++)
+        if (hipStreamCreateWithFlags(&e->gstream[g], hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&e->join_ev[g], hipEventDisableTiming) != hipSuccess) {
+            free_encoder(e);
+            return fail(UD_ERR_HIP, "ud_encoder_create: initialisation failed");
+        }
+    if (const char* gs = getenv("UD_GROUPS")) {
+        const int v = atoi(gs);
+        if (v >= 1 && v <= MAX_GROUPS) e->groups_override = v;
     }
     for (int s = (int)slots - 1; s >= 0; s--) e->free_slots.push_back(s);
     *out = e;
@@ -596,14 +620,36 @@ static int upload_desc(ud_encoder* e, ud_stream* const* streams, int n, int T, c
 
 // ---------------------------------------------------------------- the step
 
-// encodeLayer (FastConformer.swift:262-321) for every layer, over n streams x T rows, on `st`.
-// The fp32 residual stream `res` advances in place.  In bf16 mode the residual projections write
-// K-split partial slabs that the next LayerNorm folds into `res` (in slab order); in fp32 mode they
-// accumulate into `res` directly.
-static int enqueue_step(ud_encoder* e, int n, int T, const float* x, float* out, hipStream_t st) {
+// The workspace rows of streams s0 .. s0+n-1 of a step (rows r0 = s0 * T on, r0 a multiple of 16,
+// so the fragment-major operands start on a whole 16-row tile: their element offset is r0 * width
+// like the row-major buffers').  The split-K slabs of the group are [ks][n*T][D] at
+// KSPLIT * r0 * D, disjoint from every other group's.
+struct Ws {
+    float* res; void* z; void* h; void* qkv; void* att; float* pw; float* part; int32_t* desc;
+};
+static Ws ws_view(ud_encoder* e, int s0, int T) {
+    const size_t r0 = (size_t)s0 * T, D = e->D, esz = e->esz;
+    Ws w;
+    w.res = e->res + r0 * D;
+    w.z = static_cast<char*>(e->z) + r0 * D * esz;
+    w.h = static_cast<char*>(e->h) + r0 * e->ff * esz;
+    w.qkv = static_cast<char*>(e->qkv) + r0 * 3 * D * esz;
+    w.att = static_cast<char*>(e->att) + r0 * D * esz;
+    w.pw = e->pw + r0 * 2 * D;
+    w.part = e->part ? e->part + (size_t)KSPLIT * r0 * D : nullptr;
+    w.desc = e->desc_dev + (size_t)s0 * DESC_INTS;
+    return w;
+}
+
+// encodeLayer (FastConformer.swift:262-321) for every layer, over streams s0 .. s0+n-1 of the step
+// (x and out point at their first row), on `st`.  The fp32 residual stream advances in place.  In
+// bf16 mode the residual projections write K-split partial slabs that the next LayerNorm folds into
+// the residual (in slab order); in fp32 mode they accumulate into it directly.
+static int enqueue_rows(ud_encoder* e, int s0, int n, int T, const float* x, float* out, hipStream_t st) {
     const int D = e->D, ff = e->ff, M = n * T;
     const bool bf = e->bf;
-    Partials pend{e->part, 0};
+    const Ws w = ws_view(e, s0, T);
+    Partials pend{w.part, 0};
     auto gemm = [&](const void* A, const void* W, void* C, int N, int K, int ldc, int epi, int act, float scale,
                     const char* what) -> int {
         GemmArgs g{};
@@ -613,9 +659,9 @@ static int enqueue_step(ud_encoder* e, int n, int T, const float* x, float* out,
     };
     // res += scale * A . W^T (N = D)
     auto resid = [&](const void* A, const void* W, int K, float scale, const char* what) -> int {
-        if (!bf) return gemm(A, W, e->res, D, K, D, EPI_RESID, ACT_NONE, scale, what);
+        if (!bf) return gemm(A, W, w.res, D, K, D, EPI_RESID, ACT_NONE, scale, what);
         GemmArgs g{};
-        g.A = A; g.W = W; g.C = e->part; g.M = M; g.N = D; g.K = K; g.lda = K; g.ldw = K; g.ldc = D;
+        g.A = A; g.W = W; g.C = w.part; g.M = M; g.N = D; g.K = K; g.lda = K; g.ldw = K; g.ldc = D;
         g.epi = EPI_PARTIAL; g.act = ACT_NONE; g.out_scale = scale;
         g.ksplit = gemm_partial_splits(M, D, K, bf);
         pend.n = g.ksplit;
@@ -628,44 +674,79 @@ static int enqueue_step(ud_encoder* e, int n, int T, const float* x, float* out,
         const size_t roff = (size_t)li * e->ring_layer_elems * e->esz;
         // res <- x (layer 0) or norm_out of the previous layer; z <- norm_feed_forward1(res)
         if (li == 0)
-            LAUNCH(launch_layernorm2(x, take(), e->res, nullptr, nullptr, l.ln[0], l.ln[1], e->z, bf, M, D, st),
+            LAUNCH(launch_layernorm2(x, take(), w.res, nullptr, nullptr, l.ln[0], l.ln[1], w.z, bf, M, D, st),
                    "layernorm");
         else
-            LAUNCH(launch_layernorm2(e->res, take(), e->res, e->lw[li - 1].ln[10], e->lw[li - 1].ln[11], l.ln[0],
-                                     l.ln[1], e->z, bf, M, D, st), "layernorm");
+            LAUNCH(launch_layernorm2(w.res, take(), w.res, e->lw[li - 1].ln[10], e->lw[li - 1].ln[11], l.ln[0],
+                                     l.ln[1], w.z, bf, M, D, st), "layernorm");
         int rc;
         // FF1: res += 0.5 * linear2(silu(linear1(z)))
-        if ((rc = gemm(e->z, l.ff1_w1, e->h, ff, D, ff, EPI_H, ACT_SILU, 1.0f, "ff1.linear1"))) return rc;
-        if ((rc = resid(e->h, l.ff1_w2, ff, 0.5f, "ff1.linear2"))) return rc;
+        if ((rc = gemm(w.z, l.ff1_w1, w.h, ff, D, ff, EPI_H, ACT_SILU, 1.0f, "ff1.linear1"))) return rc;
+        if ((rc = resid(w.h, l.ff1_w2, ff, 0.5f, "ff1.linear2"))) return rc;
         // MHSA: res += linear_out(relpos_attention(q, [cache; k], [cache; v]))
-        LAUNCH(launch_layernorm(e->res, take(), l.ln[2], l.ln[3], e->z, bf, M, D, ACT_NONE, st), "layernorm");
-        if ((rc = gemm(e->z, l.wqkv, e->qkv, 3 * D, D, 3 * D, EPI_STORE, ACT_NONE, 1.0f, "qkv"))) return rc;
+        LAUNCH(launch_layernorm(w.res, take(), l.ln[2], l.ln[3], w.z, bf, M, D, ACT_NONE, st), "layernorm");
+        if ((rc = gemm(w.z, l.wqkv, w.qkv, 3 * D, D, 3 * D, EPI_STORE, ACT_NONE, 1.0f, "qkv"))) return rc;
         RingArgs ra{};
         ra.kring = static_cast<char*>(e->kring) + roff;
         ra.vring = static_cast<char*>(e->vring) + roff;
-        ra.qkv = e->qkv; ra.P = l.P; ra.u = l.bias_u; ra.vb = l.bias_v; ra.att = e->att; ra.desc = e->desc_dev;
+        ra.qkv = w.qkv; ra.P = l.P; ra.u = l.bias_u; ra.vb = l.bias_v; ra.att = w.att; ra.desc = w.desc;
         ra.n = n; ra.T = T; ra.L = e->L; ra.H = e->H; ra.rel_offset = e->rel_offset; ra.n_rel = e->n_rel;
         ra.scale = 1.0f / std::sqrt((float)e->dk);
         ra.att_frag = bf ? 1 : 0;
         LAUNCH(launch_relpos_ring(ra, bf, st), "relpos attention");
-        if ((rc = resid(e->att, l.wo, D, 1.0f, "linear_out"))) return rc;
+        if ((rc = resid(w.att, l.wo, D, 1.0f, "linear_out"))) return rc;
         // Conv module: res += pw2(silu(LN(dwconv([ring; mask(glu(pw1(z)))]))))
-        LAUNCH(launch_layernorm(e->res, take(), l.ln[4], l.ln[5], e->z, bf, M, D, ACT_NONE, st), "layernorm");
-        if ((rc = gemm(e->z, l.pw1, e->pw, 2 * D, D, 2 * D, EPI_STORE_F32, ACT_NONE, 1.0f, "pointwise_conv1")))
+        LAUNCH(launch_layernorm(w.res, take(), l.ln[4], l.ln[5], w.z, bf, M, D, ACT_NONE, st), "layernorm");
+        if ((rc = gemm(w.z, l.pw1, w.pw, 2 * D, D, 2 * D, EPI_STORE_F32, ACT_NONE, 1.0f, "pointwise_conv1")))
             return rc;
         ConvArgs ca{};
-        ca.pw = e->pw; ca.ring = e->cring + (size_t)li * e->cring_layer_elems; ca.w_t = l.dw_t;
-        ca.ln_g = l.ln[6]; ca.ln_b = l.ln[7]; ca.z = e->z; ca.desc = e->desc_dev;
+        ca.pw = w.pw; ca.ring = e->cring + (size_t)li * e->cring_layer_elems; ca.w_t = l.dw_t;
+        ca.ln_g = l.ln[6]; ca.ln_b = l.ln[7]; ca.z = w.z; ca.desc = w.desc;
         ca.n = n; ca.T = T; ca.D = D; ca.K = e->Kc; ca.z_bf16 = bf;
         LAUNCH(launch_dwconv_ln(ca, st), "depthwise conv");
-        if ((rc = resid(e->z, l.pw2, D, 1.0f, "pointwise_conv2"))) return rc;
+        if ((rc = resid(w.z, l.pw2, D, 1.0f, "pointwise_conv2"))) return rc;
         // FF2: res += 0.5 * linear2(silu(linear1(LN(res))))
-        LAUNCH(launch_layernorm(e->res, take(), l.ln[8], l.ln[9], e->z, bf, M, D, ACT_NONE, st), "layernorm");
-        if ((rc = gemm(e->z, l.ff2_w1, e->h, ff, D, ff, EPI_H, ACT_SILU, 1.0f, "ff2.linear1"))) return rc;
-        if ((rc = resid(e->h, l.ff2_w2, ff, 0.5f, "ff2.linear2"))) return rc;
+        LAUNCH(launch_layernorm(w.res, take(), l.ln[8], l.ln[9], w.z, bf, M, D, ACT_NONE, st), "layernorm");
+        if ((rc = gemm(w.z, l.ff2_w1, w.h, ff, D, ff, EPI_H, ACT_SILU, 1.0f, "ff2.linear1"))) return rc;
+        if ((rc = resid(w.h, l.ff2_w2, ff, 0.5f, "ff2.linear2"))) return rc;
     }
     LayerDev& last = e->lw[e->layers - 1];
-    LAUNCH(launch_layernorm(e->res, take(), last.ln[10], last.ln[11], out, false, M, D, ACT_NONE, st), "layernorm");
+    LAUNCH(launch_layernorm(w.res, take(), last.ln[10], last.ln[11], out, false, M, D, ACT_NONE, st), "layernorm");
+    return UD_OK;
+}
+
+// How many groups a step of n streams x T frames runs as: one chain by default.  Independent
+// chains of part of the streams on separate HIP streams (UD_GROUPS = 2..4) were measured on
+// MI355X to be slower, not faster: 64 x 2 frames 2.19 -> 2.30 ms with 2 groups (2.92 with 3),
+// 256 x 14 frames 9.8 -> 30 ms with 2; the latency-bound kernels of one chain do not overlap with
+// another chain's.  Group boundaries fall on whole 16-row tiles.
+static int step_groups(const ud_encoder* e, int n, int T) {
+    int G = e->groups_override;
+    if (G == 0) G = 1;
+    const int q = 16 / std::gcd(T, 16);          // streams per 16-row tile boundary
+    while (G > 1 && n / q < G) G--;
+    return G;
+}
+
+// The step over all n streams: one chain, or G chains of consecutive streams forked from `st`
+// and joined back into it (inside a graph capture this records a forked graph).
+static int enqueue_step(ud_encoder* e, int n, int T, const float* x, float* out, hipStream_t st) {
+    const int G = step_groups(e, n, T);
+    if (G == 1) return enqueue_rows(e, 0, n, T, x, out, st);
+    const int q = 16 / std::gcd(T, 16);
+    const int tiles = n / q;                      // whole boundary units; the last group takes the rest
+    HIPC(hipEventRecord(e->fork_ev, st));
+    int s0 = 0;
+    for (int g = 0; g < G; g++) {
+        const int s1 = g + 1 == G ? n : (tiles * (g + 1) / G) * q;
+        HIPC(hipStreamWaitEvent(e->gstream[g], e->fork_ev, 0));
+        const size_t r0 = (size_t)s0 * T * e->D;
+        int rc = enqueue_rows(e, s0, s1 - s0, T, x + r0, out + r0, e->gstream[g]);
+        if (rc != UD_OK) return rc;
+        HIPC(hipEventRecord(e->join_ev[g], e->gstream[g]));
+        HIPC(hipStreamWaitEvent(st, e->join_ev[g], 0));
+        s0 = s1;
+    }
     return UD_OK;
 }
 
