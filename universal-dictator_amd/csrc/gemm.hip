@@ -411,51 +411,75 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
 // weight-streaming shapes (tens of rows against thousands of weight rows).
 //   workgroup = 4 waves; wave w owns the 16 output columns n0 = (4 blockIdx.x + w) * 16 ..
 //   blockIdx.y = K split kz (EPI_PARTIAL slabs); blockIdx.z = block of FS_MT * 16 rows of M
-//   per 16-wide k group, lane (c = lane % 16, q = lane / 16) loads W[n0 + c][k + 4q .. 4q + 3] and,
-//   for each of its row tiles t, A[m0 + 16 t + c][k + 4q .. 4q + 3] as float4; MFMA k-step s takes
-//   element s of both, so A and W see the same permutation of the group's 16 k values.
+//   The workgroup's A rows are shared by its 4 waves: per 64-wide K chunk they are staged in LDS
+//   (each thread one float4 per 16 rows), so A crosses L2 once per workgroup, not once per wave.
+//   Per 16-wide k group, lane (c = lane % 16, q = lane / 16) takes W[n0 + c][k + 4q .. 4q + 3] as a
+//   float4 from global memory and, for each row tile t, A[m0 + 16 t + c][k + 4q .. 4q + 3] from
+//   LDS; MFMA k-step s takes element s of both, so A and W see the same permutation of the
+//   group's 16 k values.
 // Every output sums its K range in the same order whatever M is, so a row's result does not
 // depend on the batch it is computed in.
 constexpr int FS_MT = 4;
+constexpr int FS_KC = 64;                      // K chunk staged in LDS
 
 __global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmArgs a, int kper) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __shared__ float4 As[16 * FS_MT][FS_KC / 4 + 1];   // +1: conflict-free column reads
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int c = lane & 15, q = lane >> 4;
     const int n0 = (blockIdx.x * 4 + w) * 16;
-    if (n0 >= a.N) return;
+    const bool wave_live = n0 < a.N;            // waves past N still help stage A
     const int kz = blockIdx.y;
     const int kb = kz * kper, ke = min(a.K, kb + kper);
     const int m0 = blockIdx.z * 16 * FS_MT;
     const float* W = static_cast<const float*>(a.W) + (int64_t)min(n0 + c, a.N - 1) * a.ldw + 4 * q;
-    const float* A[FS_MT];
-    bool live[FS_MT];
-#pragma unroll
-    for (int t = 0; t < FS_MT; t++) {
-        const int m = m0 + 16 * t + c;
-        live[t] = m < a.M;
-        A[t] = static_cast<const float*>(a.A) + (int64_t)(live[t] ? m : 0) * a.lda + 4 * q;
-    }
+    const float* A = static_cast<const float*>(a.A);
+    // staging: thread tid loads row (tid / 16) + 16 i, float4 column tid % 16 of each chunk
+    const int sr = tid >> 4, sc4 = tid & 15;
     f32x4_t acc[FS_MT];
 #pragma unroll
     for (int t = 0; t < FS_MT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 2
-    for (int k = kb; k < ke; k += 16) {
-        const float4 wv = *reinterpret_cast<const float4*>(W + k);
-        float4 xv[FS_MT];
+    // registers of the next chunk: loaded one chunk ahead, while the current one is multiplied
+    float4 st[FS_MT], wv[FS_KC / 16], wn[FS_KC / 16];
+    auto load_chunk = [&](int k0, float4 (&wd)[FS_KC / 16]) {
+        const int kn = min(FS_KC, ke - k0);     // a multiple of 16
 #pragma unroll
-        for (int t = 0; t < FS_MT; t++)
-            xv[t] = live[t] ? *reinterpret_cast<const float4*>(A[t] + k) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int i = 0; i < FS_MT; i++) {
+            const int m = m0 + sr + 16 * i;
+            st[i] = (m < a.M && 4 * sc4 < kn) ? *reinterpret_cast<const float4*>(A + (int64_t)m * a.lda + k0 + 4 * sc4)
+                                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
 #pragma unroll
-        for (int t = 0; t < FS_MT; t++) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t].x, wv.x, acc[t], 0, 0, 0);
+        for (int g = 0; g < FS_KC / 16; g++)
+            wd[g] = (wave_live && 16 * g < kn) ? *reinterpret_cast<const float4*>(W + k0 + 16 * g)
+                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    };
+    load_chunk(kb, wv);
+    for (int k0 = kb; k0 < ke; k0 += FS_KC) {
+        const int kn = min(FS_KC, ke - k0);
+        if (k0 != kb) __syncthreads();          // every wave is done with the previous chunk
 #pragma unroll
-        for (int t = 0; t < FS_MT; t++) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t].y, wv.y, acc[t], 0, 0, 0);
+        for (int i = 0; i < FS_MT; i++) As[sr + 16 * i][sc4] = st[i];
+        __syncthreads();
+        if (k0 + FS_KC < ke) load_chunk(k0 + FS_KC, wn);
+        if (wave_live) {
 #pragma unroll
-        for (int t = 0; t < FS_MT; t++) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t].z, wv.z, acc[t], 0, 0, 0);
+            for (int g = 0; g < FS_KC / 16; g++) {
+                if (16 * g >= kn) break;
 #pragma unroll
-        for (int t = 0; t < FS_MT; t++) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[t].w, wv.w, acc[t], 0, 0, 0);
+                for (int t = 0; t < FS_MT; t++) {
+                    const float4 xv = As[16 * t + c][4 * g + q];
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, wv[g].x, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, wv[g].y, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.z, wv[g].z, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.w, wv[g].w, acc[t], 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < FS_KC / 16; g++) wv[g] = wn[g];
     }
     const int n = n0 + c;
-    if (n >= a.N) return;
+    if (!wave_live || n >= a.N) return;
     float* C = static_cast<float*>(a.C);
 #pragma unroll
     for (int t = 0; t < FS_MT; t++)

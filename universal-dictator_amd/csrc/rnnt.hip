@@ -41,7 +41,7 @@ int ud_set_error(int code, const char* msg);   // encoder.hip
 
 namespace ud {
 
-constexpr int RNNT_KS = 8;          // K splits of the decoder GEMMs
+constexpr int RNNT_KS = 4;          // K splits of the decoder GEMMs
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
