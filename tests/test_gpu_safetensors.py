@@ -156,3 +156,33 @@ def test_rnnt_loader_matches_set_weight(gpu, tmp_path):
     st.close()
     a.close()
     b.close()
+
+
+def test_mel_loader_matches_direct(gpu, tmp_path):
+    """ud_mel_load_safetensors reads preprocessor.featurizer.fb [1, 128, 257] and .window [400]
+    (NemotronModel.init, Sources/DictatorEngine/Models/Nemotron.swift:45-46): its features equal
+    those of a frontend built from the same arrays, bit for bit; a file without them is rejected."""
+    import refimpl
+    ud = gpu
+    fb, win = refimpl.slaney_mel_fb(), refimpl.hann_symmetric()
+    p = str(tmp_path / "mel.safetensors")
+    _write(ud, p, {"preprocessor.featurizer.fb": (fb.reshape(1, 128, 257), "F32"),
+                   "preprocessor.featurizer.window": (win, "F32"),
+                   "joint.enc.bias": (np.zeros(640, np.float32), "F32")})
+    st = ud.SafeTensors(p)
+    a = ud.MelFrontend.from_safetensors(st)
+    b = ud.MelFrontend(fb, win)
+    assert a.n_mels == 128
+    audio = np.sin(np.arange(7777, dtype=np.float32) * 0.05).astype(np.float32)
+    fa, fbb = a.features([audio])[0], b.features([audio])[0]
+    assert np.array_equal(fa.view(np.uint32), fbb.view(np.uint32))
+    st.close()
+    q = str(tmp_path / "nomel.safetensors")
+    _write(ud, q, {"joint.enc.bias": (np.zeros(640, np.float32), "F32")})
+    st = ud.SafeTensors(q)
+    with pytest.raises(ud.EngineError) as e:
+        ud.MelFrontend.from_safetensors(st)
+    assert e.value.status == -6
+    st.close()
+    a.close()
+    b.close()
