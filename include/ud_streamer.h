@@ -30,7 +30,8 @@
  * The streamer owns one encoder stream (ud_stream) and one RNN-T slot per open stream; stream ids
  * are the slot numbers 0 .. max_streams-1.  Calls are synchronous (each batched step ends with
  * the greedy decoder's readback) and not thread-safe; one streamer at a time may drive a given
- * encoder and decoder.
+ * encoder and decoder.  If a batched step fails, the call returns its error and the streams of
+ * that batch take no further chunks (their tokens so far stay readable); close and reopen them.
  *
  * Conventions as in ud_encoder.h (0 or a negative ud_status, ud_last_error()).
  */

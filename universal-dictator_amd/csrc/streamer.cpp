@@ -289,7 +289,12 @@ int drain(ud_streamer* s) {
         }
         if (plans.empty()) return UD_OK;
         const int rc = run_batch(s, plans);
-        if (rc != UD_OK) return rc;
+        if (rc != UD_OK) {
+            // the batch may have advanced some device state (encoder caches, decoder slots) and
+            // not the schedule: its streams end here rather than continue out of step
+            for (const Plan& p : plans) s->st[p.id].done = true;
+            return rc;
+        }
     }
 }
 
