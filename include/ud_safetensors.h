@@ -4,7 +4,7 @@
  * Replaces SafeTensorsHeader / SafeTensorsReader / widenToFloats
  * (Sources/DictatorCore/Weights/WeightSource.swift:13-90), the memory-mapped SafeTensorsFile
  * (Sources/DictatorEngine/Core/SafeTensors.swift:6-112) and the name handling of the model loaders
- * (docs/specs/nemotron.md §8: NeMo state_dict names, and the HF model.safetensors aliases).  The
+ * (docs/specs/nemotron.md:246-287: NeMo state_dict names, and the HF model.safetensors aliases).  The
  * file is memory-mapped read-only; tensors are widened to fp32 on request (F32, F16, BF16) and the
  * encoder / decoder convert them to their storage dtype on upload (the keep-fp32 policy of
  * Sources/DictatorEngine/Core/Convert.swift:74-83).  Host-only; no device work.
@@ -41,7 +41,7 @@ UD_API int ud_safetensors_info(const ud_safetensors* st, const char* name, int32
 /* The tensor widened to fp32 (WeightSource.floats); count must equal its element count. */
 UD_API int ud_safetensors_read_f32(const ud_safetensors* st, const char* name, float* out, int64_t count);
 /* The NeMo state_dict name of a tensor name: HF model.safetensors aliases are mapped
- * (docs/specs/nemotron.md §8), NeMo names are returned unchanged.  Writes at most cap bytes. */
+ * (docs/specs/nemotron.md:246-287), NeMo names are returned unchanged.  Writes at most cap bytes. */
 UD_API int ud_nemo_name(const char* name, char* out, int32_t cap);
 
 /* Sets every encoder tensor of the file (encoder.layers.{l}.* for l < the encoder's layer count,

@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (oracle/ud_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke entry point and by the benchmark's
-cpu_baseline leg, as the checker and the timed CPU baseline.  The product path never imports it.
+cpu_baseline leg, as the parity reference and the timed CPU baseline.  The product path never imports it.
 
 Each wrapper takes and returns float32/int32 numpy arrays (C-contiguous).  The reference file:line
 each function restates is in the C source.

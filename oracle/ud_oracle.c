@@ -2,7 +2,7 @@
  * ud_oracle.c -- CPU restatement of DictatorEngine's cache-aware streaming
  * FastConformer encoder step.
  *
- * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity reference for the HIP
  * library and the timed CPU baseline of the benchmark.  Only tests/, the
  * smoke entry point and the benchmark's cpu_baseline leg may load it; the
  * product path never calls it.

@@ -1,10 +1,10 @@
-"""Independent checkers used to pin the oracle (tests only).
+"""Independent restatements used to pin the oracle (tests only).
 
 These restate NeMo's modules with torch/numpy library routines in float64, in the structure NeMo
 uses rather than the oracle's: rel_shift is the literal pad/view trick
 (Tests/DictatorEngineTests/ConformerOpTests.swift:111-122; reference/nemo/check_spec.py:143-146),
 the depthwise conv is torch conv1d with causal left padding, masks are boolean matrices filled
-with -10000 before softmax and zeroed after (docs/specs/nemotron.md §3).
+with -10000 before softmax and zeroed after (docs/specs/nemotron.md:83-135).
 """
 import numpy as np
 
@@ -35,7 +35,7 @@ def nemo_pe(T, D):
 
 
 def layer_nemo(x, w, pe, mask, valid, H, Kc=9):
-    """One NeMo ConformerLayer (conformer_modules.py:160-233 per docs/specs/nemotron.md §3) on a
+    """One NeMo ConformerLayer (conformer_modules.py:160-233 per docs/specs/nemotron.md:83-135) on a
     full utterance x [T, D] (float64 torch).  pe: projected-input table rows for positions
     T-1..-(T-1) [2T-1, D]; mask [T, T] bool, True = hidden; rows >= valid are padding."""
     import torch
@@ -74,7 +74,7 @@ def layer_nemo(x, w, pe, mask, valid, H, Kc=9):
 
 
 def chunked_limited_mask(T, left, right, valid):
-    """NeMo chunked_limited visibility (conformer_encoder.py:803-822 per docs/specs/nemotron.md §4):
+    """NeMo chunked_limited visibility (conformer_encoder.py:803-822 per docs/specs/nemotron.md:137-149):
     visible(i,j) = 0 <= i//chunk - j//chunk <= left//chunk; keys >= valid hidden.  True = hidden."""
     cs = right + 1
     i = np.arange(T)[:, None] // cs
@@ -86,7 +86,7 @@ def chunked_limited_mask(T, left, right, valid):
 
 def subsampling_nemo(mel, valid, w):
     """NeMo ConvSubsampling, dw_striding causal 8x (subsampling.py:142-215, 425-431 per
-    docs/specs/nemotron.md §2) on one utterance, float64 torch: the image is [1, 1, T, F] (time =
+    docs/specs/nemotron.md:52-81) on one utterance, float64 torch: the image is [1, 1, T, F] (time =
     height), CausalConv2D pads (left 2, right 1, top 2, bottom 1) and convolves with stride 2,
     MaskedConvSequential zeroes time rows >= the running length before every layer and after the
     last, the length after a stride-2 conv is (L + 2 + 1 - 3) // 2 + 1, and the flatten is
@@ -123,7 +123,7 @@ def subsampling_nemo(mel, valid, w):
 
 
 def rnnt_greedy_nemo(f, w, state=None, max_symbols=10):
-    """NeMo greedy RNN-T (reference/nemo/check_spec.py:176-207 structure; docs/specs/nemotron.md §7)
+    """NeMo greedy RNN-T (reference/nemo/check_spec.py:176-207 structure; docs/specs/nemotron.md:210-244)
     on projected encoder frames f [T, H] (joint.enc applied), float64 torch with torch.nn.LSTMCell,
     with no prediction cache: the prediction is recomputed from the committed state whenever the
     loop needs it.  state (dict h, c: lists of [H], token) carries across calls; returns tokens."""
@@ -213,7 +213,7 @@ def mel_rfft(audio, fb, window):
 
 def slaney_mel_fb(sr=16000, n_fft=512, n_mels=128):
     """librosa.filters.mel(sr, n_fft, n_mels, htk=False, norm='slaney') restated (the checkpoint's
-    preprocessor.featurizer.fb is this matrix up to 1e-8, docs/specs/nemotron.md §9.1)."""
+    preprocessor.featurizer.fb is this matrix up to 1e-8, docs/specs/nemotron.md:291)."""
     def hz_to_mel(f):
         f = np.asarray(f, np.float64)
         f_sp = 200.0 / 3

@@ -1,5 +1,5 @@
 """GPU check of the safetensors loaders (ud_encoder_load_safetensors, ud_rnnt_load_safetensors):
-one file holding NeMo names and HF aliases (docs/specs/nemotron.md §8), F32 / BF16 / F16 tensors,
+one file holding NeMo names and HF aliases (docs/specs/nemotron.md:246-287), F32 / BF16 / F16 tensors,
 a layer beyond the encoder's depth and tensors of other modules must give an encoder and a decoder
 whose outputs are bit-identical to ones whose weights were set tensor by tensor (set_weight with the
 same widened values)."""

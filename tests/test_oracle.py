@@ -10,7 +10,7 @@ import refimpl
 
 
 def _torch():
-    # torch is a CPU-side checker here; it is imported lazily so that a GPU test process that only
+    # torch is a CPU-side reference here; it is imported lazily so that a GPU test process that only
     # collects this module never loads torch's bundled HIP runtime.
     import torch
     import torch.nn.functional as F
@@ -256,7 +256,7 @@ def test_encoder_offline_matches_torch_nemo_layer(ud, orc, valid):
 
 def test_streaming_equals_offline_chunked(ud, orc):
     """Cache-aware streaming (L cached frames, chunks of T) equals the offline chunked_limited
-    forward with [L, T-1] (docs/specs/nemotron.md §6.4), here exactly since there is no
+    forward with [L, T-1] (docs/specs/nemotron.md:197-208), here exactly since there is no
     subsampling edge: pins the cache rule, cache_len masking and the conv cache."""
     torch, F = _torch()
     L, T, steps, S = 6, 2, 6, 2

@@ -1,5 +1,5 @@
 """Pins the oracle's NemotronStreamer restatement (oracle.Streamer): the schedule constants
-(NemotronSchedule.swift:7-17; docs/specs/nemotron.md §9.2: 9 pre-encode frames, drop 2), the
+(NemotronSchedule.swift:7-17; docs/specs/nemotron.md:292: 9 pre-encode frames, drop 2), the
 reference property live == buffered (StreamingEquivalenceTests.swift:22-40), and chunk geometry
 (every full chunk yields lookahead + 1 kept frames)."""
 import numpy as np

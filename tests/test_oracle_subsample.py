@@ -52,7 +52,7 @@ def test_subsample_matches_nemo_restatement(orc, T0, valid):
 
 def test_subsample_length_rule_and_receptive_field(orc):
     """Output length L -> L//2+1 three times; frame k depends only on mel rows 8k-14 .. 8k
-    (docs/specs/nemotron.md §2): perturbing row r changes exactly frames ceil(r/8) .. (r+14)//8."""
+    (docs/specs/nemotron.md:52-81): perturbing row r changes exactly frames ceil(r/8) .. (r+14)//8."""
     ud = load_pkg()
     sw = ud.synthetic_subsampling_weights(seed=6)
     rng = np.random.default_rng(3)

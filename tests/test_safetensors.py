@@ -1,7 +1,7 @@
 """The safetensors reader and NeMo name map of the library (include/ud_safetensors.h), host-only,
 pinned against the safetensors package (files written by safetensors.torch / safetensors.numpy):
 dtypes F32/F16/BF16 widened bit-exactly, shapes, names, metadata, malformed files, and the HF ->
-NeMo name map of docs/specs/nemotron.md §8."""
+NeMo name map of docs/specs/nemotron.md:246-287."""
 import json
 import os
 import struct
@@ -111,7 +111,7 @@ def test_escaped_names_and_metadata(ud, tmp_path):
     st.close()
 
 
-# docs/specs/nemotron.md §8: HF model.safetensors name -> NeMo state_dict name
+# docs/specs/nemotron.md:246-287: HF model.safetensors name -> NeMo state_dict name
 HF_TO_NEMO = [
     ("encoder.subsampling.conv_in.weight", "encoder.pre_encode.conv.0.weight"),
     ("encoder.subsampling.conv_in.bias", "encoder.pre_encode.conv.0.bias"),

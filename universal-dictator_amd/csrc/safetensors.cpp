@@ -171,7 +171,7 @@ struct JParser {
 };
 
 // ------------------------------------------------------------------ name map
-// HF model.safetensors name -> NeMo state_dict name (docs/specs/nemotron.md §8).  Prefix rewrites
+// HF model.safetensors name -> NeMo state_dict name (docs/specs/nemotron.md:246-287).  Prefix rewrites
 // first (whole-name prefixes), then per-layer attention / conv-norm suffixes.
 struct Rewrite { const char* from; const char* to; };
 const Rewrite kPrefix[] = {

@@ -1,5 +1,5 @@
 // Causal dw_striding 8x subsampling of the streaming step (FastConformer.swift:219-243 encodeSubsampling;
-// Metal/20_conformer.metal:104-138 conv2d_cl; NeMo ConvSubsampling as in docs/specs/nemotron.md §2),
+// Metal/20_conformer.metal:104-138 conv2d_cl; NeMo ConvSubsampling as in docs/specs/nemotron.md:52-81),
 // batched over streams.  Activations are channel-last [stream, time, freq, C = 256]; every stride-2
 // stage is a 3 x 3 causal conv with 2 zero rows/columns of top/left padding, L -> L/2 + 1.
 //
