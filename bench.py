@@ -1,6 +1,6 @@
 """Benchmark of the cache-aware streaming FastConformer encoder step on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|offline|rnnt|stream]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|offline|rnnt|stream|stream14]
                     [--no-cpu-baseline]
 
 A step is one cache-aware encoder chunk step for every stream of the batch: the mel chunk (new rows
@@ -41,7 +41,8 @@ WORKLOADS = {
     "decode": dict(seqs=64, q_heads=32, kv_heads=8, head_dim=128, page=16, ctx=(512, 4096)),
     "offline": dict(batch=8, frames=1500, heads=8, head_dim=128, valid=(900, 1500)),
     "rnnt": dict(streams=64, T=2, hidden=640, vocab=1025, layers=2),
-    "stream": dict(streams=64, lookahead=1),   # live audio -> tokens, 160 ms chunks
+    "stream": dict(streams=64, lookahead=1),     # live audio -> tokens, 160 ms chunks
+    "stream14": dict(streams=256, lookahead=13), # live audio -> tokens, 1120 ms chunks
 }
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
 
@@ -333,20 +334,20 @@ def rnnt_bench(ud, args):
 
 def stream_bench(ud, args):
     """Live transcription end to end through the batched streamer (include/ud_streamer.h): every
-    timed step pushes 2560 new samples (160 ms) to each of 64 streams, which completes one chunk per
-    stream and runs one batched step: sample staging + H2D, the mel kernel (25 frames per stream,
-    the 9 pre-encode frames recomputed), subsampling, 24 bf16 layers, joint.enc and greedy RNN-T
-    with its host readbacks.  Caches are full before timing (40 warm-up chunks).  A random-init
-    joint emits on every frame or on none, so the decoder is timed at both ends, as in the rnnt
-    workload: every frame blank (value) and every frame at the 10-symbol cap.  value:
-    audio-sec/sec end to end."""
-    wl = WORKLOADS["stream"]
+    timed step pushes one chunk of new samples to each stream (stream: 64 streams x 2560 samples =
+    160 ms; stream14: 256 streams x 17920 samples = 1120 ms), which completes one chunk per stream
+    and runs one batched step: sample staging + H2D, the mel kernel (the chunk's frames plus the 9
+    pre-encode frames, recomputed), subsampling, 24 bf16 layers, joint.enc and greedy RNN-T with
+    its host readbacks.  Caches are full before timing.  A random-init joint emits on every frame
+    or on none, so the decoder is timed at both ends, as in the rnnt workload: every frame blank
+    (value) and every frame at the 10-symbol cap.  value: audio-sec/sec end to end."""
+    wl = WORKLOADS[args.workload]
     S, la = wl["streams"], wl["lookahead"]
     T = la + 1
     hop = 160 * 8 * T
     cfg = ud.EncoderConfig(layers=24, max_chunk=T, max_streams=S, dtype="bf16")
-    log("device %s; workload stream: %d live streams, lookahead %d (%d ms chunks), 24 layers bf16"
-        % (ud.device_arch(), S, la, int(T * FRAME_SEC * 1000)))
+    log("device %s; workload %s: %d live streams, lookahead %d (%d ms chunks), 24 layers bf16"
+        % (ud.device_arch(), args.workload, S, la, int(T * FRAME_SEC * 1000)))
     enc = ud.Encoder(cfg)
     for l in range(cfg.layers):
         enc.set_layer_weights(l, ud.synthetic_layer_weights(cfg, 2024, l, ln_jitter=0.0))
@@ -371,22 +372,24 @@ def stream_bench(ud, args):
         ph = 2 * np.pi * np.cumsum(f0) / 16000.0
         x = sum(np.sin(h * ph) / h for h in range(1, 9)) * (0.2 + 0.15 * np.sin(2 * np.pi * 1.1 * t + b))
         srcs.append((0.3 * x + 0.003 * rng.standard_normal(n_src)).astype(np.float32))
-    # the mel kernel alone at the streamer's launch shape (64 jobs x 25 frames), HIP events on its stream
+    # the mel kernel alone at the streamer's launch shape (S jobs x (9 + 8T) frames), HIP events on
+    # its stream
     hs = ud.HipStream()
-    clip = 24 * 160                      # 25 frames
+    rows = 9 + 8 * T
+    clip = (rows - 1) * 160
     ab = ud.DeviceBuffer.from_numpy(np.stack([s[:clip] for s in srcs]))
-    mb = ud.DeviceBuffer(S * 25 * 128 * 4)
+    mb = ud.DeviceBuffer(S * rows * 128 * 4)
     for _ in range(5):
-        fe.features_device(S, ab, clip, [clip] * S, mb, 25, hip_stream=hs)
+        fe.features_device(S, ab, clip, [clip] * S, mb, rows, hip_stream=hs)
     e0, e1 = ud.Event(), ud.Event()
     e0.record(hs)
     for _ in range(50):
-        fe.features_device(S, ab, clip, [clip] * S, mb, 25, hip_stream=hs)
+        fe.features_device(S, ab, clip, [clip] * S, mb, rows, hip_stream=hs)
     e1.record(hs)
     e1.synchronize()
     mel_us = e0.elapsed_ms(e1) * 1000.0 / 50
-    log("mel kernel: %.1f us per step (64 streams x 25 frames)" % mel_us)
-    warm = max(args.warmup, 40)
+    log("mel kernel: %.1f us per step (%d streams x %d frames)" % (mel_us, S, rows))
+    warm = max(args.warmup, 40) if T <= 2 else max(args.warmup // 4, 8)
     res = {}
     for regime, bias in (("blank", 50.0), ("cap", -50.0)):
         dec = ud.Rnnt(max_streams=S)
@@ -407,7 +410,8 @@ def stream_bench(ud, args):
         st.push(piece(True))
         for _ in range(warm):
             st.push(piece(False))
-        steps = args.steps if regime == "blank" else max(5, args.steps // 5)
+        steps = (args.steps if regime == "blank" else max(5, args.steps // 5)) if T <= 2 else \
+            (max(10, args.steps // 5) if regime == "blank" else 5)
         b0, c0 = st.stats()
         tok0 = sum(len(st.tokens(i)) for i in ids)
         pieces = [piece(False) for _ in range(steps)]
@@ -429,15 +433,15 @@ def stream_bench(ud, args):
     ms = res["blank"][0]
     value = S * T * FRAME_SEC / (ms / 1000.0)
     result = {
-        "metric": "aggregate audio-sec/sec of live streaming transcription at 64 streams (audio in, tokens out)",
+        "metric": "aggregate audio-sec/sec of live streaming transcription at %d streams (audio in, tokens out)" % S,
         "value": round(value, 2),
         "unit": "audio-sec/sec",
         "n_gpus": 1, "steps": res["blank"][2], "warmup": warm, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded random-init weights, harmonic test audio, Slaney-like filterbank)",
-        "config": {"workload": "live streaming: 64 streams x 2560 samples pushed per step -> mel -> subsampling -> "
+        "config": {"workload": "live streaming: %d streams x %d samples pushed per step -> mel -> subsampling -> "
                                "24 layers -> joint.enc -> greedy RNN-T, lookahead %d (%d ms chunks), every frame blank"
-                               % (la, int(T * FRAME_SEC * 1000)),
+                               % (S, hop, la, int(T * FRAME_SEC * 1000)),
                    "streams": S, "lookahead": la, "chunk_frames": T, "layers": cfg.layers},
         "mel_us_per_step": round(mel_us, 2),
         "cap_regime_ms_per_step": round(res["cap"][0], 4),
@@ -484,7 +488,7 @@ def main():
     if args.workload == "rnnt":
         rnnt_bench(ud, args)
         return
-    if args.workload == "stream":
+    if args.workload in ("stream", "stream14"):
         stream_bench(ud, args)
         return
     wl = WORKLOADS[args.workload]
