@@ -100,23 +100,27 @@ def test_relpos_multiblock_and_ragged_ranges(gpu, orc, dtype):
         harness.assert_bf16_close(got, ref, "multiblock bf16")
 
 
-@pytest.mark.parametrize("dtype,T", [("f32", 2), ("bf16", 2), ("bf16", 14), ("f32", 5)])
-def test_ring_attention_and_cache_update(gpu, orc, dtype, T):
+@pytest.mark.parametrize("dtype,T,L", [("f32", 2, 70), ("bf16", 2, 70), ("bf16", 14, 70), ("f32", 5, 70),
+                                       ("bf16", 1, 70), ("bf16", 3, 70), ("bf16", 4, 70), ("bf16", 2, 63),
+                                       ("bf16", 2, 17)])
+def test_ring_attention_and_cache_update(gpu, orc, dtype, T, L):
     """The step's fused attention over ring caches (ud_layer_attention): output against the oracle
     on [cache ; new] keys with range [L - cache_len, L + valid), and the ring update bit-exact:
-    afterwards the exported window is exactly the last L rows of [old window ; new rows]."""
+    afterwards the exported window is exactly the last L rows of [old window ; new rows].  The
+    fourth stream has an empty range (no cache, no valid frame): its output is 0.  L = 63 puts
+    ring rows and new rows in the same 16-key pass; L = 17 leaves most passes past the window."""
     ud = gpu
-    cfg = ud.EncoderConfig(layers=2, max_chunk=max(T, 2), max_streams=4, dtype=dtype)
+    cfg = ud.EncoderConfig(layers=2, left_context=L, max_chunk=max(T, 2), max_streams=4, dtype=dtype)
     enc, model, _ = harness.make_encoder(ud, orc, cfg, seed=5)
-    L, D, H = cfg.left_context, cfg.d_model, cfg.heads
+    D, H = cfg.d_model, cfg.heads
     rng = np.random.default_rng(3)
-    S = 3
+    S = 4
     streams = [enc.new_stream() for _ in range(S)]
     st = harness.OracleState(S, cfg)
     st.seed_random(rng, 0)
-    st.len[:] = [L, 33, 0]
+    st.len[:] = [L, min(33, L), 0, 0]
     st.import_into(streams, ud, dtype == "bf16")
-    valid = np.array([T, max(T - 1, 0), T], np.int32)
+    valid = np.array([T, max(T - 1, 0), T, 0], np.int32)
     layer = 1
     qkv = rng.standard_normal((S, T, 3 * D)).astype(np.float32)
     if dtype == "bf16":
@@ -142,6 +146,9 @@ def test_ring_attention_and_cache_update(gpu, orc, dtype, T):
         u = model.layers[layer][11]
         vb = model.layers[layer][12]
         ref = orc.relpos_attention(qkv[s, :, :D], keys, vals, P, u, vb, rr, model.rel_offset, H)
+        if valid[s] == 0 and st.len[s] == 0:
+            assert not np.any(ref) and not np.any(got[s]), s
+            continue
         if dtype == "f32":
             assert harness.rel_err(got[s], ref) <= 1e-4, s
         else:

@@ -120,6 +120,18 @@ __device__ __forceinline__ float xsum16(float a, float b) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+// Every lane receives op(v[l], v[l ^ 32]) (resp. v[l ^ 16]): the swap of v with itself hands each
+// lane both values of its pair.
+__device__ __forceinline__ float xmax32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xmax16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xadd32(float v) { return xsum32(v, v); }
+__device__ __forceinline__ float xadd16(float v) { return xsum16(v, v); }
 
 
 }  // namespace ud
