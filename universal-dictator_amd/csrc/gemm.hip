@@ -128,35 +128,15 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
         mma_frag<MT, NT, H>(f0, acc);
     }
 
-    if constexpr (WK > 1) {
-        __shared__ f32x4_t red[WK - 1][NT][MT][64];
-        if (wave > 0) {
-#pragma unroll
-            for (int j = 0; j < NT; j++)
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++) red[wave - 1][j][mt][lane] = acc[j][mt];
-        }
-        __syncthreads();
-        if (wave != 0) return;
-#pragma unroll
-        for (int w = 0; w < WK - 1; w++)
-#pragma unroll
-            for (int j = 0; j < NT; j++)
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++) acc[j][mt] += red[w][j][mt][lane];
-    }
-
-    // Lane holds rows 16*(mb*MT + mt) + 4*g + i (i < 4) of column 16*(nt*NT + j) + r16.
-#pragma unroll
-    for (int j = 0; j < NT; j++)
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
+    // Epilogue of one finished 16 x 16 accumulator (j, mt): the lane holds rows
+    // 16*(mb*MT + mt) + 4*g + i (i < 4) of column 16*(nt*NT + j) + r16.
+    auto finish = [&](int j, int mt, const f32x4_t& v4) {
         const int n = (nt * NT + j) * 16 + r16;
 #pragma unroll
         for (int i2 = 0; i2 < 4; i2++) {
             const int64_t m = (int64_t)(mb * MT + mt) * 16 + g * 4 + i2;
             if (m >= a.M) continue;
-            float v = acc[j][mt][i2];
+            float v = v4[i2];
             if constexpr (BIAS) v += kz == 0 ? a.bias[n] : 0.0f;
             if constexpr (EPI == EPI_PARTIAL) {
                 static_cast<float*>(a.C)[((int64_t)kz * a.M + m) * a.ldc + n] = a.out_scale * v;
@@ -168,6 +148,30 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
                 static_cast<bf16*>(a.C)[m * a.ldc + n] = f2bf(apply_act(v, ACT) * a.out_scale);
             }
         }
+    };
+    if constexpr (WK > 1) {
+        // Every wave parks its partial accumulators in LDS; wave w then finishes the accumulators
+        // idx = j*MT + mt with idx % WK == w: the sum of the WK partials in wave order, and the
+        // epilogue.  Spreading the sums and the stores over the waves keeps the workgroup's tail
+        // short (one wave finishing every accumulator measured ~3 us per launch at 128 rows).
+        __shared__ f32x4_t red[WK][NT][MT][64];
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) red[wave][j][mt][lane] = acc[j][mt];
+        __syncthreads();
+        for (int idx = wave; idx < NT * MT; idx += WK) {
+            const int j = idx / MT, mt = idx % MT;
+            f32x4_t v = red[0][j][mt][lane];
+#pragma unroll
+            for (int w = 1; w < WK; w++) v += red[w][j][mt][lane];
+            finish(j, mt, v);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) finish(j, mt, acc[j][mt]);
     }
 }
 
@@ -597,6 +601,7 @@ int gemm_partial_splits(int M, int N, int K, bool bf16_data) {
         const BigTile bt = big_tile(M, N, K, true);
         if (bt.nt != 0) return bt.ks;
     }
+    if (M <= 128 && K == 1024 && N % 32 == 0) return 2;   // linear_out, pointwise_conv2 (launch_bf16)
     return K % (128 * KSPLIT) == 0 ? KSPLIT : 1;
 }
 
@@ -608,13 +613,16 @@ static int launch_act(const GemmArgs& a, int ks, hipStream_t st) {
     return -2;
 }
 
-// Tile shapes measured on MI355X for the streaming step's M <= 128 projections (weights from HBM):
-// every column tile re-reads its rows of the activation panel, so the output tile of a wave trades
-// rows for columns (MT x NT tiles of 16 x 16) to cut that traffic.
-//   ff linear1 (N 4096, K 1024, fragment out):   MT 2 x NT 4, 2 waves    9.0 -> 7.7 us
-//   q/k/v (N 3072) and pointwise_conv1 (N 2048): MT 4 x NT 2, 4 waves    7.8 -> 6.8 us
-//   split-K 4, K >= 4096 (ff linear2):           MT 4 x NT 2, 4 waves    7.8 -> 6.5 us
-//   split-K 4, K 1024 (linear_out, pw2):         MT 4 x NT 1, 2 waves    5.0 -> 3.7 us
+// Tile shapes measured on MI355X for the streaming step's M <= 128 projections (weights from HBM,
+// 48 rotating copies; the waves of a workgroup split K and share the reduction and the epilogue):
+//   ff linear1 (N 4096, K 1024, fragment out):  MT 2 x NT 4, 8 waves            6.97 -> 5.94 us
+//   q/k/v (N 3072, K 1024, bf16 out):           MT 4 x NT 2, 8 waves            5.77 -> 5.53 us
+//   pointwise_conv1 (N 2048, K 1024, fp32 out): MT 2 x NT 2, 8 waves            4.31 -> 3.76 us
+//   ff linear2 (N 1024, K 4096, split-K 4):     MT 4 x NT 2, 8 waves            5.91 -> 5.76 us
+//   linear_out, pw2 (N 1024, K 1024):           MT 2 x NT 2, 8 waves, split-K 2 3.40 -> 3.12 us
+//                                               (half the slabs for the LayerNorm that adds them)
+// Wider tiles cut the re-reads of the activation panel; more waves per workgroup put more of a
+// tile's K range in flight at once.
 // Larger M keeps 128-row tiles (MT 8, 2 waves).
 // IEEE-half operands with a bias (the subsampling front-end's GEMMs): fp32 outputs, no activation
 // or ReLU.  The bias is a template parameter: a runtime-optional bias in the encoder's own GEMMs
@@ -644,18 +652,20 @@ static int launch_bf16(const GemmArgs& a, int ks, hipStream_t st) {
     if (a.M <= 128) {
         switch (a.epi) {
             case EPI_STORE_FRAG:
+                if (a.N % 64 == 0 && a.K % 512 == 0) return launch_act<2, 8, 4, EPI_STORE_FRAG>(a, ks, st);
                 if (a.N % 64 == 0) return launch_act<2, 2, 4, EPI_STORE_FRAG>(a, ks, st);
                 break;
             case EPI_STORE:
-                if (a.N % 32 == 0 && a.K % 256 == 0) return launch_act<4, 4, 2, EPI_STORE>(a, ks, st);
+                if (a.N % 32 == 0 && a.K % 512 == 0) return launch_act<4, 8, 2, EPI_STORE>(a, ks, st);
                 break;
             case EPI_STORE_F32:
-                if (a.N % 32 == 0 && a.K % 256 == 0) return launch_act<4, 4, 2, EPI_STORE_F32>(a, ks, st);
+                if (a.N % 32 == 0 && a.K % 512 == 0) return launch_act<2, 8, 2, EPI_STORE_F32>(a, ks, st);
                 break;
             case EPI_PARTIAL:
                 if (a.act != ACT_NONE) return -2;
-                if (a.K >= 4096 && a.N % 32 == 0 && a.K % (256 * ks) == 0)
-                    return launch_bf16_cfg<4, 4, 2, EPI_PARTIAL, ACT_NONE>(a, ks, st);
+                if (a.N % 32 == 0 && a.K % (512 * ks) == 0)
+                    return a.K >= 4096 ? launch_bf16_cfg<4, 8, 2, EPI_PARTIAL, ACT_NONE>(a, ks, st)
+                                       : launch_bf16_cfg<2, 8, 2, EPI_PARTIAL, ACT_NONE>(a, ks, st);
                 if (a.K % (128 * ks) == 0) return launch_bf16_cfg<4, 2, 1, EPI_PARTIAL, ACT_NONE>(a, ks, st);
                 break;
             default: return -2;   // the residual accumulate is an fp32-path epilogue
