@@ -85,31 +85,6 @@ constexpr int DPP_QUAD_2301 = 0x4E;   // quad_perm [2,3,0,1]
 constexpr int DPP_ROW_HALF_MIRROR = 0x141;
 constexpr int DPP_ROW_MIRROR = 0x140;
 
-// Sum over aligned groups of W lanes (W a power of two <= 64); every lane of a group receives the
-// group total.  DPP inside a 16-lane row, cross-row steps through ds_swizzle/bpermute shuffles.
-template <int W> __device__ __forceinline__ float group_sum(float v) {
-    if constexpr (W >= 2) v += dpp_mov<DPP_QUAD_1032>(v);
-    if constexpr (W >= 4) v += dpp_mov<DPP_QUAD_2301>(v);
-    if constexpr (W >= 8) v += dpp_mov<DPP_ROW_HALF_MIRROR>(v);
-    if constexpr (W >= 16) v += dpp_mov<DPP_ROW_MIRROR>(v);
-    if constexpr (W >= 32) v += __shfl_xor(v, 16, 64);
-    if constexpr (W >= 64) v += __shfl_xor(v, 32, 64);
-    return v;
-}
-
-template <int W> __device__ __forceinline__ float group_max(float v) {
-    if constexpr (W >= 2) v = fmaxf(v, dpp_mov<DPP_QUAD_1032>(v));
-    if constexpr (W >= 4) v = fmaxf(v, dpp_mov<DPP_QUAD_2301>(v));
-    if constexpr (W >= 8) v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
-    if constexpr (W >= 16) v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
-    if constexpr (W >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
-    if constexpr (W >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
-}
-
-__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
-__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
-
 // Cross-row sums with the gfx950 lane-swap instructions: a + (a from lane l^32) into lanes 0-31 and
 // b + (b from lane l^32) into lanes 32-63; likewise for l^16 (rows 0, 2 get a, rows 1, 3 get b).
 __device__ __forceinline__ float xsum32(float a, float b) {
@@ -132,6 +107,33 @@ __device__ __forceinline__ float xmax16(float v) {
 }
 __device__ __forceinline__ float xadd32(float v) { return xsum32(v, v); }
 __device__ __forceinline__ float xadd16(float v) { return xsum16(v, v); }
+
+// Sum over aligned groups of W lanes (W a power of two <= 64); every lane of a group receives the
+// group total.  DPP inside a 16-lane row; the cross-row steps pair lane l with l ^ 16 and l ^ 32
+// through the lane-swap instructions (VALU, no LDS round trip).
+template <int W> __device__ __forceinline__ float group_sum(float v) {
+    if constexpr (W >= 2) v += dpp_mov<DPP_QUAD_1032>(v);
+    if constexpr (W >= 4) v += dpp_mov<DPP_QUAD_2301>(v);
+    if constexpr (W >= 8) v += dpp_mov<DPP_ROW_HALF_MIRROR>(v);
+    if constexpr (W >= 16) v += dpp_mov<DPP_ROW_MIRROR>(v);
+    if constexpr (W >= 32) v = xadd16(v);
+    if constexpr (W >= 64) v = xadd32(v);
+    return v;
+}
+
+template <int W> __device__ __forceinline__ float group_max(float v) {
+    if constexpr (W >= 2) v = fmaxf(v, dpp_mov<DPP_QUAD_1032>(v));
+    if constexpr (W >= 4) v = fmaxf(v, dpp_mov<DPP_QUAD_2301>(v));
+    if constexpr (W >= 8) v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
+    if constexpr (W >= 16) v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
+    if constexpr (W >= 32) v = xmax16(v);
+    if constexpr (W >= 64) v = xmax32(v);
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
+
 
 
 }  // namespace ud
