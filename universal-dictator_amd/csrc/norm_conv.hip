@@ -154,17 +154,36 @@ __global__ __launch_bounds__(256) void layernorm2_kernel(const float* src, Parti
 // [KC + T] x 4 window in registers.  The cache is a ring of KC rows per stream: logical row r is
 // slot (frames + r) % KC; new row t (only the last KC matter) goes to slot (frames + t) % KC,
 // written by the thread that read the slot, so the update is in place with no hazard.
+// The stream's descriptor is the first load; the pointwise_conv1 rows, the weights and the LN
+// parameters (none of which depend on it) are in flight before the ring rows, and the frame mask
+// is applied to the loaded rows.
 template <int KC, int TMAX>
 __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
     const int s = blockIdx.x;
+    constexpr int NW = 4;                 // 256 threads, 4 channels each (launch_dwconv_ln)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nw = blockDim.x / 64;
     const int D = a.D, T = a.T;
     const int c0 = tid * 4;
-    const int32_t* d = a.desc + s * DESC_INTS;
-    const int slot = d[0], cpos = d[4], valid = d[2];
-    float* ring = a.ring + (int64_t)slot * KC * D;
+    const int4 dsc = *reinterpret_cast<const int4*>(a.desc + s * DESC_INTS);
+    const int cpos = a.desc[s * DESC_INTS + 4];
+    __builtin_amdgcn_sched_barrier(0);
 
+    float4 pv[TMAX], pg[TMAX];
+#pragma unroll
+    for (int t = 0; t < TMAX; t++) {
+        const float* row = a.pw + ((int64_t)s * T + min(t, T - 1)) * 2 * D;
+        pv[t] = *reinterpret_cast<const float4*>(row + c0);
+        pg[t] = *reinterpret_cast<const float4*>(row + D + c0);
+    }
+    float4 w[KC + 1];
+#pragma unroll
+    for (int k = 0; k <= KC; k++) w[k] = *reinterpret_cast<const float4*>(a.w_t + (int64_t)k * D + c0);
+    const float4 gg = *reinterpret_cast<const float4*>(a.ln_g + c0);
+    const float4 bb = *reinterpret_cast<const float4*>(a.ln_b + c0);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int slot = dsc.x, valid = dsc.z;
+    float* ring = a.ring + (int64_t)slot * KC * D;
     float4 in[KC + TMAX];
 #pragma unroll
     for (int r = 0; r < KC; r++) {
@@ -174,18 +193,10 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
     }
 #pragma unroll
     for (int t = 0; t < TMAX; t++) {
-        float4 y = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (t < T && t < valid) {
-            const float* row = a.pw + ((int64_t)s * T + t) * 2 * D;
-            const float4 v = *reinterpret_cast<const float4*>(row + c0);
-            const float4 gt = *reinterpret_cast<const float4*>(row + D + c0);
-            y = make_float4(v.x * sigmoidf(gt.x), v.y * sigmoidf(gt.y), v.z * sigmoidf(gt.z), v.w * sigmoidf(gt.w));
-        }
-        in[KC + t] = y;
+        const float4 v = pv[t], gt = pg[t];
+        const float4 y = make_float4(v.x * sigmoidf(gt.x), v.y * sigmoidf(gt.y), v.z * sigmoidf(gt.z), v.w * sigmoidf(gt.w));
+        in[KC + t] = (t < T && t < valid) ? y : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    float4 w[KC + 1];
-#pragma unroll
-    for (int k = 0; k <= KC; k++) w[k] = *reinterpret_cast<const float4*>(a.w_t + (int64_t)k * D + c0);
 
     float4 o[TMAX];
 #pragma unroll
@@ -207,56 +218,49 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
         }
     }
 
-    // LayerNorm over the D channels of each frame: block reductions through LDS.
-    __shared__ float red[4][TMAX];
-    __shared__ float stat[TMAX];
+    // LayerNorm over the D channels of each frame, two passes: per-wave partial sums through LDS,
+    // and every thread adds the waves' partials itself (one barrier per pass; the second pass
+    // writes a second buffer, so no barrier separates the passes' reads and writes).
+    __shared__ float red[2][NW][TMAX];
     float part[TMAX];
 #pragma unroll
     for (int t = 0; t < TMAX; t++) part[t] = wave_sum((o[t].x + o[t].y) + (o[t].z + o[t].w));
     if (lane == 0)
 #pragma unroll
-        for (int t = 0; t < TMAX; t++) red[wave][t] = part[t];
-    __syncthreads();
-    if (tid < TMAX) {
-        float sum = 0.f;
-        for (int w2 = 0; w2 < nw; w2++) sum += red[w2][tid];
-        stat[tid] = sum / (float)D;
-    }
+        for (int t = 0; t < TMAX; t++) red[0][wave][t] = part[t];
     __syncthreads();
     float mean[TMAX];
 #pragma unroll
     for (int t = 0; t < TMAX; t++) {
-        mean[t] = stat[t];
+        float sum = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < NW; w2++) sum += red[0][w2][t];
+        mean[t] = sum / (float)D;
         float a0 = o[t].x - mean[t], a1 = o[t].y - mean[t], a2 = o[t].z - mean[t], a3 = o[t].w - mean[t];
         part[t] = wave_sum((a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3));
     }
-    __syncthreads();
     if (lane == 0)
 #pragma unroll
-        for (int t = 0; t < TMAX; t++) red[wave][t] = part[t];
+        for (int t = 0; t < TMAX; t++) red[1][wave][t] = part[t];
     __syncthreads();
-    if (tid < TMAX) {
-        float sum = 0.f;
-        for (int w2 = 0; w2 < nw; w2++) sum += red[w2][tid];
-        stat[tid] = 1.0f / sqrtf(sum / (float)D + LN_EPS);
-    }
-    __syncthreads();
-    const float4 gg = *reinterpret_cast<const float4*>(a.ln_g + c0);
-    const float4 bb = *reinterpret_cast<const float4*>(a.ln_b + c0);
 #pragma unroll
     for (int t = 0; t < TMAX; t++) {
-        if (t >= T) break;
-        const float rstd = stat[t];
-        float4 y;
-        y.x = silu((o[t].x - mean[t]) * rstd * gg.x + bb.x);
-        y.y = silu((o[t].y - mean[t]) * rstd * gg.y + bb.y);
-        y.z = silu((o[t].z - mean[t]) * rstd * gg.z + bb.z);
-        y.w = silu((o[t].w - mean[t]) * rstd * gg.w + bb.w);
-        const int64_t row = (int64_t)s * T + t;
-        if (a.z_bf16) {
-            store4_frag(a.z, row, c0, D, y);
-        } else {
-            *reinterpret_cast<float4*>(static_cast<float*>(a.z) + row * D + c0) = y;
+        if (t < T) {
+            float sum = 0.f;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; w2++) sum += red[1][w2][t];
+            const float rstd = 1.0f / sqrtf(sum / (float)D + LN_EPS);
+            float4 y;
+            y.x = silu((o[t].x - mean[t]) * rstd * gg.x + bb.x);
+            y.y = silu((o[t].y - mean[t]) * rstd * gg.y + bb.y);
+            y.z = silu((o[t].z - mean[t]) * rstd * gg.z + bb.z);
+            y.w = silu((o[t].w - mean[t]) * rstd * gg.w + bb.w);
+            const int64_t row = (int64_t)s * T + t;
+            if (a.z_bf16) {
+                store4_frag(a.z, row, c0, D, y);
+            } else {
+                *reinterpret_cast<float4*>(static_cast<float*>(a.z) + row * D + c0) = y;
+            }
         }
     }
 }
