@@ -216,13 +216,10 @@ __device__ __forceinline__ void pin_acc(f32x4_t (&acc)[NT][MT]) {
         for (int i = 0; i < MT; i++) asm volatile("" : "+a"(acc[j][i]));
 }
 
-// SiLU for epilogues that round to bf16: v_exp_f32 and v_rcp_f32 (about 1 ulp of fp32 each) in
-// place of expf and an IEEE divide; exact 0 / x limits for large |x|.
-__device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
-
+// The activation as a compile-time choice (silu is v_exp_f32 + v_rcp_f32, about 1 ulp each).
 template <int ACT>
 __device__ __forceinline__ float act_fast(float x) {
-    if constexpr (ACT == ACT_SILU) return silu_fast(x);
+    if constexpr (ACT == ACT_SILU) return silu(x);
     else return apply_act(x, ACT);
 }
 
