@@ -47,8 +47,9 @@ template <> __device__ __forceinline__ bf16 from_f<bf16>(float v) { return f2bf(
 
 // SiLU x * sigmoid(x) (00_common.metal:25).
 // SiLU and the logistic function with v_exp_f32 and v_rcp_f32 (about 1 ulp each) instead of an
-// IEEE divide, whose correctly rounded sequence is ~10 instructions (Metal's fast-math division is
-// approximate too).  Limits: exp(-x) = inf gives 1 / inf = 0, so x -> -inf yields (-)0.
+// IEEE divide, whose correctly rounded sequence is ~10 instructions.  The reference's fp32
+// x / (1 + exp(-x)) (Metal/00_common.metal:7-29) differs by a few ulp at most.  Limits:
+// exp(-x) = inf gives 1 / inf = 0, so x -> -inf yields (-)0.
 __device__ __forceinline__ float sigmoidf(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x * sigmoidf(x); }
 
