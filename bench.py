@@ -599,8 +599,7 @@ def main():
         "attention_steps_per_sec": round(1000.0 / attn_ms, 1),
         "attention_us_per_launch": round(attn_ms * 1000.0, 3),
         "roofline": {
-            "kernel": ("relpos_ring_pair_kernel" if T <= 2 else "relpos_ring_small_kernel" if T <= 4
-                       else "relpos_ring_mfma_kernel")
+            "kernel": ("relpos_ring_small_kernel" if T <= 4 else "relpos_ring_mfma_kernel")
                       + " (fused rel-pos attention + K/V ring commit)",
             "bound": "hbm",
             "achieved": round(achieved, 1),

@@ -345,14 +345,15 @@ template <int Q> __device__ __forceinline__ int tsum16_index(int lane) {
     else return 0;
 }
 
-// Window rows of the streaming kernel for one 16-lane group: key j = grp + 16k (clamped to W - 1)
+// Window rows of the streaming kernel for one 16-lane group: key j = grp + G k (clamped to W - 1;
+// G = the workgroup's number of groups)
 // is ring row (wpos + j) mod L of the stream's slot while j < L, else new row j - L of the chunk.
 // prepare() needs only the launch and runs while the stream's descriptor is in flight; load() then
 // costs three VALU operations per pass.  Offsets are 32-bit byte offsets from bases that are the
 // same for the whole workgroup (ring: the (slot, head) block; new rows: this head's K/V columns of
 // the stream's chunk), so the loads take a scalar base plus a vector offset.  When L >= 16 (KR - 1)
 // the first KR - 1 passes hold ring rows only; the remaining passes select per lane.
-template <int KR>
+template <int KR, int G = 16>
 struct WindowRows {
     int j[KR];
     uint32_t noff[KR];    // bytes to new row j - L, lane's 8 columns (j >= L only)
@@ -361,7 +362,7 @@ struct WindowRows {
     __device__ __forceinline__ void prepare(int grp, int sub, int L, int W, int D) {
 #pragma unroll
         for (int k = 0; k < KR; k++) {
-            j[k] = min(grp + k * 16, W - 1);
+            j[k] = min(grp + k * G, W - 1);
             cached[k] = j[k] < L;
             noff[k] = ((uint32_t)(j[k] - L) * 3u * (uint32_t)D + (uint32_t)sub * 8u) * 2u;
         }
@@ -379,7 +380,7 @@ struct WindowRows {
             const uint32_t r = (uint32_t)(wpos + j[k]);
             roff[k] = (min(r, r - (uint32_t)L) << 8) | ((uint32_t)sub << 4);
         }
-        const bool ring_only = L >= 16 * (KR - 1);
+        const bool ring_only = L >= G * (KR - 1);
         if (ring_only) {
 #pragma unroll
             for (int k = 0; k < KR - 1; k++) kreg[k] = ld16(kb + roff[k]);
@@ -596,199 +597,8 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
     }
 }
 
-// Streaming chunks of T <= 2 frames.  Same grid, lane layout and window loads as
-// relpos_ring_small_kernel, but the scores never leave the lanes that hold V:
-//  - the band (the same rows for every stream of the launch, from L2) is staged once per workgroup
-//    in LDS, behind an early barrier that completes while K and V are still arriving from HBM;
-//  - score (i, j) reads band row W - 1 + i - j, so the group that holds key j reads rows W - 1 - j
-//    and W - j from LDS and reduces (q_i + u) . K_j + (q_i + v) . band row with ONE transposed
-//    butterfly: rel_shift is the LDS address, nothing is gathered across groups;
-//  - the softmax runs per wave (flash style): each wave takes the maximum and the sum over its own
-//    keys and accumulates exp(s - m_wave) V; the 4 waves are merged once at the end with the factors
-//    exp(m_wave - m) (the second and last barrier).
-template <int KR, int PR>
-__global__ __launch_bounds__(256) void relpos_ring_pair_kernel(RingArgs a) {
-    using T = bf16;
-    constexpr int TQ = 2, DK = 128, VEC = 8, LPR = 16, G = 16, NV = TQ * VEC, NQ = NV / 4;
-    // KR passes cover the window's W = L + T keys, PR passes the band's NB = W + T - 1 rows
-    __shared__ __align__(16) bf16 band[PR * G][DK];
-    __shared__ __align__(16) float red[4][TQ * DK];
-    __shared__ float2 wst[4][TQ];      // per wave and query: (max, sum of exp(s - max))
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int grp = tid / LPR, sub = tid % LPR, row4 = lane >> 4;
-    const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
-    const int L = a.L, Tq = a.T, D = a.H * DK, W = L + Tq, NB = L + 2 * Tq - 1;
-    // the stream's descriptor first: one scalar load, in flight while the launch-only loads issue
-    const int4 dsc = *reinterpret_cast<const int4*>(a.desc + s * DESC_INTS);
-    __builtin_amdgcn_sched_barrier(0);
-    const T* qkvh = static_cast<const T*>(a.qkv) + (int64_t)s * Tq * 3 * D + h * DK;
-    const T* qkv = qkvh + sub * VEC;
-    const T* P = static_cast<const T*>(a.P) + (int64_t)(a.rel_offset + 1 - Tq) * D + h * DK + sub * VEC;
-
-    // ---- launch-only addresses: q, u/v, the band (row grp + 16k of pass k)
-    uint4 qreg[TQ];
-#pragma unroll
-    for (int i = 0; i < TQ; i++) qreg[i] = ld16(qkv + (int64_t)min(i, Tq - 1) * 3 * D);
-    const float4 u0 = *reinterpret_cast<const float4*>(a.u + h * DK + sub * VEC);
-    const float4 u1 = *reinterpret_cast<const float4*>(a.u + h * DK + sub * VEC + 4);
-    const float4 v0 = *reinterpret_cast<const float4*>(a.vb + h * DK + sub * VEC);
-    const float4 v1 = *reinterpret_cast<const float4*>(a.vb + h * DK + sub * VEC + 4);
-    uint4 preg[PR];
-#pragma unroll
-    for (int k = 0; k < PR; k++) preg[k] = ld16(P + (int64_t)min(grp + k * G, NB - 1) * D);
-    WindowRows<KR> win;
-    win.prepare(grp, sub, L, W, D);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- K and V of the window
-    const int slot = dsc.x, wpos = dsc.y, valid = min(max(dsc.z, 0), Tq), cache_len = dsc.w;
-    const int ks = L - cache_len, ke = L + valid;
-    T* kbase = static_cast<T*>(a.kring) + ((int64_t)slot * a.H + h) * L * DK;
-    T* vbase = static_cast<T*>(a.vring) + ((int64_t)slot * a.H + h) * L * DK;
-    uint4 kreg[KR], vreg[KR];
-    win.load(kreg, vreg, kbase, vbase, qkvh + D, qkvh + 2 * D, wpos, L, sub);
-
-    // ---- q + u, q + v
-    const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    float qu[TQ][VEC], qv[TQ][VEC];
-#pragma unroll
-    for (int i = 0; i < TQ; i++) {
-        float f[VEC];
-        unpack16<T>(qreg[i], f);
-#pragma unroll
-        for (int e = 0; e < VEC; e++) { qu[i][e] = f[e] + uu[e]; qv[i][e] = f[e] + vv[e]; }
-    }
-    const int qi = tsum16_index<TQ>(sub);     // the query whose scores this lane ends up holding
-
-    // ---- the band into LDS (its loads were issued before K and V, so this waits for the band only)
-#pragma unroll
-    for (int k = 0; k < PR; k++) *reinterpret_cast<uint4*>(&band[grp + k * G][sub * VEC]) = preg[k];
-    __builtin_amdgcn_sched_barrier(0);     // no K arithmetic above the barrier (it would wait for K)
-    __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- scores: s(i, j) = ((q_i + u) . K_j + (q_i + v) . band[W - 1 + i - j]) * scale, masked to [ks, ke)
-    float x[KR];
-#pragma unroll
-    for (int k = 0; k < KR; k++) {
-        float fk[VEC];
-        unpack16<T>(kreg[k], fk);
-        const int jc = min(grp + k * G, W - 1);
-        float part[TQ];
-#pragma unroll
-        for (int i = 0; i < TQ; i++) {
-            float fb[VEC];
-            unpack16<T>(*reinterpret_cast<const uint4*>(&band[min(W - 1 + i - jc, NB - 1)][sub * VEC]), fb);
-            float acc = 0.0f;
-#pragma unroll
-            for (int e = 0; e < VEC; e++) acc += qu[i][e] * fk[e];
-#pragma unroll
-            for (int e = 0; e < VEC; e++) acc += qv[i][e] * fb[e];
-            part[i] = acc;
-        }
-        const float tot = tsum16<TQ>(part, sub);
-        const int j = grp + k * G;
-        x[k] = (j >= ks && j < ke) ? tot * a.scale : -INFINITY;
-    }
-
-    // ---- this wave's softmax statistics for query qi: over the lane's keys, then the wave's 4 groups
-    float m = x[0];
-#pragma unroll
-    for (int k = 1; k < KR; k++) m = fmaxf(m, x[k]);
-    m = xmax32(xmax16(m));
-    float pk[KR], l = 0.0f;
-#pragma unroll
-    for (int k = 0; k < KR; k++) {
-        pk[k] = x[k] == -INFINITY ? 0.0f : __expf(x[k] - m);
-        l += pk[k];
-    }
-    l = xadd32(xadd16(l));
-
-    // ---- exp(s - m_wave) . V from the V registers (rows outside the range zeroed); the other
-    //      query's probability of the same key is in lane ^ 1
-    float acc[NV];
-#pragma unroll
-    for (int f = 0; f < NV; f++) acc[f] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < KR; k++) {
-        const int j = grp + k * G;
-        const bool in = j >= ks && j < ke;
-        float f[VEC];
-        unpack16<T>(in ? vreg[k] : make_uint4(0, 0, 0, 0), f);
-        const float po = dpp_mov<DPP_QUAD_1032>(pk[k]);
-        const float p0 = qi == 0 ? pk[k] : po, p1 = qi == 0 ? po : pk[k];
-#pragma unroll
-        for (int e = 0; e < VEC; e++) {
-            acc[e] += p0 * f[e];
-            acc[VEC + e] += p1 * f[e];
-        }
-    }
-    // over the 4 row groups of the wave: lane (row4, sub) ends with flat sums row4*NQ .. +NQ-1
-    float h1[NV / 2], h2[NQ];
-#pragma unroll
-    for (int q = 0; q < NV / 2; q++) h1[q] = xsum32(acc[q], acc[q + NV / 2]);
-#pragma unroll
-    for (int q = 0; q < NQ; q++) h2[q] = xsum16(h1[q], h1[q + NQ]);
-#pragma unroll
-    for (int q = 0; q < NQ; q += 4) {
-        const int f = row4 * NQ + q, i = f >> 3, e = f & 7;
-        *reinterpret_cast<float4*>(&red[wave][i * DK + sub * VEC + e]) = make_float4(h2[q], h2[q + 1], h2[q + 2], h2[q + 3]);
-    }
-    if (lane < TQ) wst[wave][lane] = make_float2(m, l);      // lanes 0, 1 hold queries 0, 1
-    __syncthreads();
-
-    // ---- commit the T new K/V rows over the T oldest ring slots (every ring read is done)
-#pragma unroll
-    for (int k = 0; k < KR; k++) {
-        const int j = grp + k * G;
-        if (j >= L && j < W) {
-            int rr = wpos + (j - L);
-            rr -= (rr >= L) ? L : 0;
-            st16(kbase + (int64_t)rr * DK + sub * VEC, kreg[k]);
-            st16(vbase + (int64_t)rr * DK + sub * VEC, vreg[k]);
-        }
-    }
-    // ---- merge the waves: out = sum_w e^(m_w - m) acc_w / sum_w e^(m_w - m) l_w (0 for an empty range)
-    if (tid < Tq * LPR) {
-        const int i = tid / LPR;
-        float2 st[4];
-#pragma unroll
-        for (int w = 0; w < 4; w++) st[w] = wst[w][i];
-        const float mm = fmaxf(fmaxf(st[0].x, st[1].x), fmaxf(st[2].x, st[3].x));
-        float fw[4], den = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            fw[w] = st[w].x == -INFINITY ? 0.0f : __expf(st[w].x - mm);
-            den += fw[w] * st[w].y;
-        }
-        const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-        float o[VEC];
-#pragma unroll
-        for (int e = 0; e < VEC; e += 4) {
-            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                const float4 y = *reinterpret_cast<const float4*>(&red[w][i * DK + sub * VEC + e]);
-                t.x += fw[w] * y.x; t.y += fw[w] * y.y; t.z += fw[w] * y.z; t.w += fw[w] * y.w;
-            }
-            o[e] = t.x * inv; o[e + 1] = t.y * inv; o[e + 2] = t.z * inv; o[e + 3] = t.w * inv;
-        }
-        const bool empty = ke <= ks;
-        uint32_t pkd[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            pkd[e] = empty ? 0u : ((uint32_t)f2bf(o[2 * e]) | ((uint32_t)f2bf(o[2 * e + 1]) << 16));
-        const int64_t row = (int64_t)s * Tq + i;
-        T* att = static_cast<T*>(a.att);
-        T* dst = a.att_frag ? att + frag_index(row, h * DK + sub * VEC, D / 64) : att + row * D + h * DK + sub * VEC;
-        st16(dst, make_uint4(pkd[0], pkd[1], pkd[2], pkd[3]));
-    }
-}
-
-// Read floor of the streaming kernel's access pattern (relpos_ring_pair_kernel): the same grid, the
-// same loads (q, u/v, the band, K and V of the window, through the same addressing), no arithmetic
+// Read floor of the streaming kernel's access pattern (relpos_ring_small_kernel, T <= 2): the same
+// grid, the same loads (q, u/v, the band, K and V of the window, through the same addressing), no arithmetic
 // beyond folding the words together, no stores (one store to att[0] on a value that never occurs
 // keeps the loads live).  Its time per launch is what memory alone costs for this shape; the
 // attention kernel is measured against it.
@@ -1356,10 +1166,8 @@ static int launch_ring_t(const RingArgs& a, hipStream_t st) {
     const bool band_ok = a.rel_offset + 1 - a.T >= 0 && a.rel_offset + a.L + a.T - 1 < a.n_rel;
     if (sizeof(T) == 2 && a.T <= 4 && a.L >= 16 && a.L + a.T <= 96 && a.L + 2 * a.T - 1 <= 112 && band_ok) {
         const int kr = (a.L + a.T + 15) / 16, pr = (a.L + 2 * a.T - 1 + 15) / 16;
-        if (a.T <= 2 && kr <= 5 && pr <= 5) hipLaunchKernelGGL((relpos_ring_pair_kernel<5, 5>), grid, block, 0, st, a);
-        else if (a.T <= 2 && kr <= 5) hipLaunchKernelGGL((relpos_ring_pair_kernel<5, 6>), grid, block, 0, st, a);
-        else if (a.T <= 2 && pr <= 6) hipLaunchKernelGGL((relpos_ring_pair_kernel<6, 6>), grid, block, 0, st, a);
-        else if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_pair_kernel<6, 7>), grid, block, 0, st, a);
+        if (a.T <= 2 && kr <= 5 && pr <= 5) hipLaunchKernelGGL((relpos_ring_small_kernel<2, 5, 5>), grid, block, 0, st, a);
+        else if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_small_kernel<2, 6, 7>), grid, block, 0, st, a);
         else if (kr <= 5 && pr <= 5) hipLaunchKernelGGL((relpos_ring_small_kernel<4, 5, 5>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((relpos_ring_small_kernel<4, 6, 7>), grid, block, 0, st, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;
