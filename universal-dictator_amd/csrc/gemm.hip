@@ -627,8 +627,14 @@ static int launch_act(const GemmArgs& a, int ks, hipStream_t st) {
 template <int ACT>
 static int launch_f16(const GemmArgs& a, hipStream_t st) {
     if (a.M <= 128 && a.N % 32 == 0 && a.K % 256 == 0) return launch_bf16_cfg<4, 4, 2, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+    // The LDS kernel's 256-row tiles leave most CUs idle below ~64 tiles (the second pointwise conv
+    // of 64 streams x 160 ms: 4,352 x 256 x 256, 34 tiles, 10.5 us; the register kernel's 64 x 32
+    // tiles 6.6 us).
+    const int nt = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false).nt : 0;
+    if (nt != 0 && (int64_t)((a.M + 255) / 256) * (a.N / (64 * nt)) < 64 && a.N % 32 == 0 && a.K % 128 == 0)
+        return launch_bf16_cfg<4, 2, 2, EPI_STORE_F32, ACT, true, true>(a, 1, st);
     if (a.M >= LDS_MIN_ROWS) {
-        switch (big_tile(a.M, a.N, a.K, false).nt) {
+        switch (nt) {
             case 4: return launch_lds_cfg<4, EPI_STORE_F32, ACT, true, true>(a, 1, st);
             case 3: return launch_lds_cfg<3, EPI_STORE_F32, ACT, true, true>(a, 1, st);
             case 2: return launch_lds_cfg<2, EPI_STORE_F32, ACT, true, true>(a, 1, st);
