@@ -81,6 +81,28 @@ def test_step_bf16_24_layers(gpu, orc):
     enc.close()
 
 
+def test_step_bf16_config2_full(gpu, orc):
+    """Config 2 exactly: 64 streams x 2 frames, 24 layers, seeded full caches, two steps (the second
+    with a short final chunk on some streams), against the oracle's fp32 step."""
+    cfg = gpu.EncoderConfig(layers=24, max_chunk=2, max_streams=64, dtype="bf16")
+    plan = lambda step, S, T: [T - (s % 5 == 2 and step == 1) for s in range(S)]
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=64, T=2, n_steps=2, seed=43, seed_caches=True, valid_plan=plan)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
+def test_step_bf16_mid_rows(gpu, orc):
+    """48 streams x 6 frames = 288 rows: between the 128-row tiles of the streaming shapes and the
+    2,048 rows where the LDS-staged projection kernel starts (128-row register tiles, split-K 4)."""
+    cfg = gpu.EncoderConfig(layers=2, max_chunk=6, max_streams=48, dtype="bf16")
+    plan = lambda step, S, T: [(T, 4, 0, T)[s % 4] if step == 1 else T for s in range(S)]
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=48, T=6, n_steps=2, seed=47, seed_caches=True, valid_plan=plan)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
 def test_step_bf16_chunk14(gpu, orc):
     """Config 3's chunk shape (14 frames, 84 keys) on a few streams."""
     cfg = gpu.EncoderConfig(layers=2, max_chunk=14, max_streams=8, dtype="bf16")
