@@ -200,9 +200,9 @@ struct ud_rnnt {
     // device lists of the three phases in separate buffers, each uploaded from its own pinned host
     // buffer: no upload overwrites a list that an earlier kernel or copy may still read
     int32_t *dslot_p = nullptr, *dtok = nullptr, *dslot_c = nullptr;          // [S]
-    int32_t *dslot_j = nullptr, *drow = nullptr, *dbest = nullptr;            // [cap_pairs]
+    int32_t *dpair = nullptr, *dbest = nullptr;   // dpair [2 cap_pairs]: slots of the joint rows, then their rows
     int32_t *hslot_p = nullptr, *htok = nullptr, *hslot_c = nullptr;          // pinned [S]
-    int32_t *hslot_j = nullptr, *hrow = nullptr, *hbest = nullptr;            // pinned [cap_pairs]
+    int32_t *hpair = nullptr, *hbest = nullptr;   // pinned: hpair [2 cap_pairs] as dpair, hbest [cap_pairs]
 };
 
 static float* ralloc(size_t floats) {
@@ -217,10 +217,10 @@ static void free_rnnt(ud_rnnt* r) {
     for (float* p : r->w) if (p) (void)hipFree(p);
     for (float* p : r->wcat) if (p) (void)hipFree(p);
     for (float* p : r->bias) if (p) (void)hipFree(p);
-    void* ps[] = {r->h, r->c, r->ph, r->pc, r->pg, r->xh, r->slabs, r->hsum, r->jslabs, r->pslabs, r->dslot_p, r->dslot_j,
-                  r->dslot_c, r->dtok, r->drow, r->dbest};
+    void* ps[] = {r->h, r->c, r->ph, r->pc, r->pg, r->xh, r->slabs, r->hsum, r->jslabs, r->pslabs, r->dslot_p, r->dpair,
+                  r->dslot_c, r->dtok, r->dbest};
     for (void* p : ps) if (p) (void)hipFree(p);
-    for (void* p : {(void*)r->hslot_p, (void*)r->htok, (void*)r->hslot_c, (void*)r->hslot_j, (void*)r->hrow,
+    for (void* p : {(void*)r->hslot_p, (void*)r->htok, (void*)r->hslot_c, (void*)r->hpair,
                     (void*)r->hbest})
         if (p) (void)hipHostFree(p);
     delete r;
@@ -414,17 +414,16 @@ static int predict(ud_rnnt* r, const std::vector<int>& slots, hipStream_t st) {
 // with a stream synchronize), so nothing in flight uses the old buffers.
 static int ensure_pairs(ud_rnnt* r, int P) {
     if (P <= r->cap_pairs) return UD_OK;
-    void* ds[] = {r->hsum, r->jslabs, r->dslot_j, r->drow, r->dbest};
+    void* ds[] = {r->hsum, r->jslabs, r->dpair, r->dbest};
     for (void* p : ds) if (p) (void)hipFree(p);
-    for (void* p : {(void*)r->hslot_j, (void*)r->hrow, (void*)r->hbest}) if (p) (void)hipHostFree(p);
+    for (void* p : {(void*)r->hpair, (void*)r->hbest}) if (p) (void)hipHostFree(p);
     r->hsum = r->jslabs = nullptr;
-    r->dslot_j = r->drow = r->dbest = r->hslot_j = r->hrow = r->hbest = nullptr;
+    r->dpair = r->dbest = r->hpair = r->hbest = nullptr;
     r->cap_pairs = 0;
     const size_t n = (size_t)P;
     bool ok = (r->hsum = ralloc(n * r->H)) && (r->jslabs = ralloc((size_t)RNNT_KS * n * r->V)) &&
-              (r->dslot_j = (int32_t*)ralloc(n)) && (r->drow = (int32_t*)ralloc(n)) && (r->dbest = (int32_t*)ralloc(n)) &&
-              hipHostMalloc((void**)&r->hslot_j, n * 4) == hipSuccess && hipHostMalloc((void**)&r->hrow, n * 4) == hipSuccess &&
-              hipHostMalloc((void**)&r->hbest, n * 4) == hipSuccess;
+              (r->dpair = (int32_t*)ralloc(2 * n)) && (r->dbest = (int32_t*)ralloc(n)) &&
+              hipHostMalloc((void**)&r->hpair, 2 * n * 4) == hipSuccess && hipHostMalloc((void**)&r->hbest, n * 4) == hipSuccess;
     if (!ok) return rfail(UD_ERR_NOMEM, "ud_rnnt_greedy: joint workspace allocation failed (%d pairs)", P);
     r->cap_pairs = P;
     return UD_OK;
@@ -475,16 +474,17 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
         int m = 0;
         for (int b : act) {
             p0[b] = m;
-            const int end = std::min(frames_host[b], t[b] + RNNT_SPEC);
-            for (int tt = t[b]; tt < end; tt++, m++) {
-                r->hslot_j[m] = slots_host[b];
-                r->hrow[m] = b * rows_per_stream + tt;
-            }
+            m += std::min(frames_host[b], t[b] + RNNT_SPEC) - t[b];
             p1[b] = m;
         }
-        RHIPC(hipMemcpyAsync(r->dslot_j, r->hslot_j, m * 4, hipMemcpyHostToDevice, st));
-        RHIPC(hipMemcpyAsync(r->drow, r->hrow, m * 4, hipMemcpyHostToDevice, st));
-        hipLaunchKernelGGL(rnnt_joint_in_kernel, dim3(m), dim3(256), 0, st, proj_dev, r->drow, r->pg, r->dslot_j, r->hsum, H);
+        // the joint rows' slots, then their proj rows: one upload
+        for (int b : act)
+            for (int p = p0[b]; p < p1[b]; p++) {
+                r->hpair[p] = slots_host[b];
+                r->hpair[m + p] = b * rows_per_stream + t[b] + (p - p0[b]);
+            }
+        RHIPC(hipMemcpyAsync(r->dpair, r->hpair, (size_t)2 * m * 4, hipMemcpyHostToDevice, st));
+        hipLaunchKernelGGL(rnnt_joint_in_kernel, dim3(m), dim3(256), 0, st, proj_dev, r->dpair + m, r->pg, r->dpair, r->hsum, H);
         RLAUNCH("rnnt joint input");
         if ((rc = slab_gemm(r->jslabs, r->hsum, H, r->w[R_OUT_W], m, V, H, st)) != UD_OK) return rc;
         hipLaunchKernelGGL(rnnt_argmax_kernel, dim3(m), dim3(256), 0, st, r->jslabs, RNNT_KS, m, r->w[R_OUT_B], r->dbest, V);
