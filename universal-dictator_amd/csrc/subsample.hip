@@ -32,19 +32,21 @@ __device__ __forceinline__ void store_a(void* A, int64_t m, int col, int cols, f
 // One workgroup per conv.2 output row (stream s, time t2); thread c = channel.  conv.2 output
 // (t2, f2) reads conv.0's output at rows 2 t2 - 2 .. 2 t2 and columns 2 f2 - 2 .. 2 f2; conv.0 at
 // (h, w) reads mel rows 2 h - 2 .. 2 h and columns 2 w - 2 .. 2 w.  The 7 mel rows 4 t2 - 6 ..
-// 4 t2 sit in LDS with 2 zero columns of left padding (rows outside the chunk or >= v0 are zero);
-// along the row each thread keeps a 3 x 3 window of its channel's conv.0 outputs in registers
-// and computes the 2 new columns per output position.
-constexpr int SUB_PW = 132;       // 2 + 128 mel columns, rounded up
+// 4 t2 sit in LDS with 3 zero columns of left padding (rows outside the chunk or >= v0 are zero).
+// Along the row each thread keeps a 3 x 3 window of its channel's conv.0 outputs and the 7 x 5 mel
+// values they need in registers: output position f2 adds conv.0 columns 2 f2 - 1 and 2 f2, which
+// read mel columns 4 f2 - 4 .. 4 f2, of which 4 f2 - 3 .. 4 f2 are new -- one aligned 16-byte
+// LDS read per mel row (patch column = mel column + 3).
+constexpr int SUB_PW = 132;       // 3 + 128 mel columns + 1, a multiple of 4
 
 template <bool H>
 __global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
     const int c = threadIdx.x;
     const int t2 = blockIdx.x % a.T2, s = blockIdx.x / a.T2;
     const int v0 = a.vlen[s * 4 + 0], v1 = a.vlen[s * 4 + 1];
-    __shared__ float patch[7][SUB_PW];
+    __shared__ __align__(16) float patch[7][SUB_PW];
     for (int i = c; i < 7 * SUB_PW; i += SUB_C) {
-        const int pr = i / SUB_PW, q = i % SUB_PW - 2;
+        const int pr = i / SUB_PW, q = i % SUB_PW - 3;
         const int r = 4 * t2 - 6 + pr;
         float v = 0.0f;
         if (r >= 0 && r < a.T0 && r < v0 && q >= 0 && q < a.F0) v = a.mel[((int64_t)s * a.T0 + r) * a.F0 + q];
@@ -61,14 +63,18 @@ __global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
         hv[kh] = h >= 0 && h < a.T1 && h < v1;        // else padding or a masked row: zero
     }
     __syncthreads();
-    // conv.0 + ReLU at (row 2 t2 + kh - 2, column w); patch column 2 w + j holds mel column 2 w + j - 2.
-    auto conv0 = [&](int kh, int w) -> float {
+    // mel[r][j]: mel row 4 t2 - 6 + r, columns 4 f2 - 4 + j (j < 5) of the current position
+    float mel[7][5];
+#pragma unroll
+    for (int r = 0; r < 7; r++) mel[r][4] = 0.0f;      // column -4 (read only by conv.0 column -1)
+    // conv.0 + ReLU at (row 2 t2 + kh - 2, column w) from mel columns j0 .. j0 + 2 of the window
+    auto conv0 = [&](int kh, int w, int j0) -> float {
         if (!hv[kh] || w < 0 || w >= a.F1) return 0.0f;
         float y = b0;
 #pragma unroll
         for (int i = 0; i < 3; i++)
 #pragma unroll
-            for (int j = 0; j < 3; j++) y += w0[i * 3 + j] * patch[2 * kh + i][2 * w + j];
+            for (int j = 0; j < 3; j++) y += w0[i * 3 + j] * mel[2 * kh + i][j0 + j];
         return y > 0.0f ? y : 0.0f;
     };
     float win[3][3];
@@ -76,12 +82,18 @@ __global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
     for (int kh = 0; kh < 3; kh++) win[kh][2] = 0.0f;     // column -2
     const int64_t row0 = ((int64_t)s * a.T2 + t2) * a.F2;
     for (int f2 = 0; f2 < a.F2; f2++) {
+#pragma unroll
+        for (int r = 0; r < 7; r++) {
+            const float4 v = *reinterpret_cast<const float4*>(&patch[r][4 * f2]);
+            mel[r][0] = mel[r][4];
+            mel[r][1] = v.x; mel[r][2] = v.y; mel[r][3] = v.z; mel[r][4] = v.w;
+        }
         float acc = b2;
 #pragma unroll
         for (int kh = 0; kh < 3; kh++) {
             win[kh][0] = win[kh][2];
-            win[kh][1] = conv0(kh, 2 * f2 - 1);
-            win[kh][2] = conv0(kh, 2 * f2);
+            win[kh][1] = conv0(kh, 2 * f2 - 1, 0);
+            win[kh][2] = conv0(kh, 2 * f2, 2);
 #pragma unroll
             for (int kw = 0; kw < 3; kw++) acc += w2[kh * 3 + kw] * win[kh][kw];
         }
@@ -146,7 +158,8 @@ __global__ __launch_bounds__(SUB_C) void sub_flatten_kernel(SubFlatArgs a) {
 }
 
 int launch_sub_conv01(const SubArgs& a, bool half, hipStream_t st) {
-    if (a.F0 + 2 > SUB_PW || 2 * (a.F1 - 1) + 2 >= SUB_PW) return -2;
+    // patch columns: mel + 3 up to F0 + 2; reads up to 4 F2 - 1
+    if (a.F0 + 3 > SUB_PW || 4 * a.F2 > SUB_PW || a.F1 > 2 * a.F2) return -2;
     const int blocks = a.n * a.T2;
     if (blocks <= 0) return 0;
     if (half) hipLaunchKernelGGL(sub_conv01_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
