@@ -60,6 +60,22 @@ def test_frames_independent_of_batch(gpu, orc):
         assert np.array_equal(swapped[len(clips) - 1 - b], together[b])
 
 
+def test_frames_independent_of_workgroup_size(gpu, orc):
+    """A large call runs 8 frames per workgroup, a small one 4 (below 1024 workgroups of 8); a
+    clip's frames are bit-identical either way, and match the oracle in the large call."""
+    ud = gpu
+    fb, win = refimpl.slaney_mel_fb(), refimpl.hann_symmetric()
+    fe = ud.MelFrontend(fb, win)
+    ofe = orc.MelFrontend(fb, win)
+    clips = [harness.speechlike(16000 + 37 * b, 100 + b) for b in range(80)]   # 80 x 13 groups of 8
+    big = fe.features(clips)
+    for b in (0, 41, 79):
+        alone = fe.features([clips[b]])[0]
+        assert np.array_equal(alone.view(np.uint32), big[b].view(np.uint32)), b
+        _close(big[b], ofe.features(clips[b]), "clip %d of the large call" % b)
+    fe.close()
+
+
 def test_constant_filterbank_kat(gpu, orc):
     """The reference KAT's frontend (StreamingEquivalenceTests.swift:10-11): constant 0.01
     filterbank, symmetric Hann, 16123 LCG samples of seed 5."""
@@ -68,6 +84,25 @@ def test_constant_filterbank_kat(gpu, orc):
     audio = orc.lcg_floats(16123, 5)
     got = ud.MelFrontend(fb, win).features([audio])[0]
     _close(got, orc.MelFrontend(fb, win).features(audio), "kat")
+
+
+def test_sparse_filterbank_bands(gpu, orc):
+    """Each band sums only its first..last nonzero bins: one-bin bands at every bin position (0 and
+    256 included), a band with weights at the two end bins only, and an all-zero band."""
+    ud = gpu
+    fb = np.zeros((130, 257), np.float32)
+    for m in range(128):
+        fb[m, 2 * m + (m & 1)] = 0.5
+    fb[128, 0] = fb[128, 256] = 1.0
+    fb = np.concatenate([fb, np.zeros((1, 257), np.float32)])[:130]    # band 129: all zero
+    fb[127, 256] = 0.25
+    win = refimpl.hann_symmetric()
+    audio = harness.speechlike(8000 + 11, 7)
+    got = ud.MelFrontend(fb, win).features([audio])[0]
+    ref = orc.MelFrontend(fb, win).features(audio)
+    _close(got, ref, "sparse filterbank")
+    z = got[:-1, 129]
+    assert np.all(z == z[0]) and abs(float(z[0]) - np.log(2.0 ** -24)) < 1e-6
 
 
 def test_mel_error_paths(gpu):

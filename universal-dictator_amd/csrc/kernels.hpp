@@ -170,6 +170,7 @@ struct MelTables {
     const float* cos512; // cos(2 pi j / 512), j < 512
     const float* win;    // [400] analysis window
     const float* fbT;    // [257][n_mels]
+    const int2* krange;  // [n_mels] bins lo .. hi-1 hold band m's nonzero filterbank weights
     int n_mels;
 };
 int launch_mel(const MelTables& t, const MelJob* jobs_dev, int n_jobs, int max_nf, hipStream_t st);

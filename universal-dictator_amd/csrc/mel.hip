@@ -3,7 +3,8 @@
 // The reference computes the features on the CPU (Sources/DictatorCore/Audio/NemoMel.swift:85-107):
 // two sgemms of the [T, 400] frame matrix against window-folded cos/sin tables [257, 400], the
 // power |X|^2 (as sqrt then square), a third sgemm against the filterbank and log(x + 2^-24).
-// Here one workgroup takes MEL_FR frames of one job and does all of it in LDS:
+// Here one workgroup takes FR frames of one job (8, or 4 when the grid is small) and does all of
+// it in LDS:
 //
 //   stage    the frames' preemphasized samples times the window, sample-major (xs[n][t]), so one
 //            16-byte LDS read broadcasts 4 frames' sample n to the whole wave; the 512-entry
@@ -12,18 +13,21 @@
 //            2 pi j / 512 with j = k (n + 56) mod 512 (the window sits at offset 56 of the
 //            512-point frame), so cos and -sin are two reads of the LDS cos table, at j and at
 //            j + 128; j advances by k per sample.  No global load in the loop: 2 table reads,
-//            2 broadcast frame reads and 2 * MEL_FR FMAs per sample.  Bin 256 (Nyquist) is a
+//            FR / 4 broadcast frame reads and 2 * FR FMAs per sample.  Bin 256 (Nyquist) is a
 //            32-lane split reduction per frame
 //   power    into LDS pw[k][t]
-//   mel      thread (m, frame quad) sums fbT[k][m] * pw[k][t] over the 257 bins, then log
+//   mel      thread (m, frame quad) sums fbT[k][m] * pw[k][t] over the bins from band m's first
+//            to its last nonzero weight (the products outside are +0, so the sum is the same as
+//            over all 257 bins for any finite power), then log
 //
 // Rounding: the reference multiplies x by float(cos) * window (its table entries); here
 // (x * window) * float(cos): the same terms to within an ulp each.  Every frame is computed the
-// same way wherever it sits in the grid (fixed summation order), so a frame recomputed by a later
-// streaming chunk is bit-identical to its first computation.  The preemphasis is evaluated as the
+// same way wherever it sits in the grid and whatever FR (fixed summation order), so a frame
+// recomputed by a later streaming chunk is bit-identical to its first computation.  The preemphasis is evaluated as the
 // reference writes it, a[i] - 0.97 * a[i-1] with both roundings (contraction off).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -37,7 +41,6 @@ int ud_set_error(int code, const char* msg);   // encoder.hip
 
 namespace ud {
 
-constexpr int MEL_FR = 8;          // frames per workgroup
 constexpr int MEL_WIN = 400;
 constexpr int MEL_HOP = 160;
 constexpr int MEL_NB = 257;        // rfft bins of n_fft 512
@@ -55,18 +58,20 @@ __device__ __forceinline__ float mel_power(float re, float im) {
     return mag * mag;
 }
 
+template <int FR>
 __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restrict__ jobs, MelTables tb) {
-    __shared__ float4 xs[MEL_WIN][MEL_FR / 4];
-    __shared__ float4 pw[MEL_NB][MEL_FR / 4];
+    static_assert(FR == 4 || FR == 8, "frames per workgroup");
+    __shared__ float4 xs[MEL_WIN][FR / 4];
+    __shared__ float4 pw[MEL_NB][FR / 4];
     __shared__ float cs[512];
     const MelJob J = jobs[blockIdx.y];
-    const int j0 = blockIdx.x * MEL_FR;
+    const int j0 = blockIdx.x * FR;
     if (j0 >= J.nf) return;
     const int tid = threadIdx.x;
-    const int nfr = min(MEL_FR, J.nf - j0);
+    const int nfr = min(FR, J.nf - j0);
     const long long fbase = J.f0 + j0;
 
-    constexpr int SU = (MEL_FR * MEL_WIN + MEL_THREADS - 1) / MEL_THREADS;
+    constexpr int SU = (FR * MEL_WIN + MEL_THREADS - 1) / MEL_THREADS;
     float* xsf = reinterpret_cast<float*>(xs);
     float va[SU], vb[SU], wv[SU];
     long long ix[SU];
@@ -77,7 +82,7 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
         const long long f = fbase + t;
         ix[u] = -1;
         va[u] = vb[u] = wv[u] = 0.0f;
-        if (e < MEL_FR * MEL_WIN && t < nfr && f < J.zero_from) {
+        if (e < FR * MEL_WIN && t < nfr && f < J.zero_from) {
             const long long idx = f * MEL_HOP - 200 + i;
             if (idx >= 0 && idx < J.n_audio) {
                 ix[u] = idx;
@@ -91,10 +96,10 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
 #pragma unroll
     for (int u = 0; u < SU; u++) {
         const int e = tid + MEL_THREADS * u;
-        if (e < MEL_FR * MEL_WIN) {
+        if (e < FR * MEL_WIN) {
             const int t = e / MEL_WIN, i = e - t * MEL_WIN;
             const float x = ix[u] < 0 ? 0.0f : ix[u] == 0 ? va[u] : preemph(va[u], vb[u]);
-            xsf[i * MEL_FR + t] = x * wv[u];
+            xsf[i * FR + t] = x * wv[u];
         }
     }
     cs[tid] = c0;
@@ -102,14 +107,14 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
     __syncthreads();
 
     {
-        // bin 256: j = 256 (n + 56) mod 512; frame t = tid / 32, lane l of 32 takes samples
-        // l, l + 32, ...; butterfly over the 32 lanes (xor offsets below 32 stay inside each half
-        // of the wave)
+        // bin 256: j = 256 (n + 56) mod 512; frame t = tid / 32 (< FR), lane l of 32 takes
+        // samples l, l + 32, ...; butterfly over the 32 lanes (xor offsets below 32 stay inside
+        // each half of the wave)
         const int t = tid >> 5, l = tid & 31;
         float r = 0.0f, q = 0.0f;
-        for (int n = l; n < MEL_WIN; n += 32) {
+        for (int n = l; t < FR && n < MEL_WIN; n += 32) {
             const int j = (256 * (n + MEL_OFF)) & 511;
-            const float x = xsf[n * MEL_FR + t];
+            const float x = xsf[n * FR + t];
             r = fmaf(cs[j], x, r);
             q = fmaf(cs[(j + 128) & 511], x, q);
         }
@@ -118,12 +123,12 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
             r += __shfl_xor(r, o);
             q += __shfl_xor(q, o);
         }
-        if (l == 0) reinterpret_cast<float*>(pw[256])[t] = mel_power(r, q);
+        if (l == 0 && t < FR) reinterpret_cast<float*>(pw[256])[t] = mel_power(r, q);
     }
     {
-        float re[MEL_FR], im[MEL_FR];
+        float re[FR], im[FR];
 #pragma unroll
-        for (int t = 0; t < MEL_FR; t++) re[t] = im[t] = 0.0f;
+        for (int t = 0; t < FR; t++) re[t] = im[t] = 0.0f;
         const int k = tid;
         int j = (k * MEL_OFF) & 511;
 #pragma unroll 4
@@ -131,7 +136,7 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
             const float c = cs[j], s = cs[(j + 128) & 511];
             j = (j + k) & 511;
 #pragma unroll
-            for (int q = 0; q < MEL_FR / 4; q++) {
+            for (int q = 0; q < FR / 4; q++) {
                 const float4 x = xs[n][q];
                 re[4 * q + 0] = fmaf(c, x.x, re[4 * q + 0]); im[4 * q + 0] = fmaf(s, x.x, im[4 * q + 0]);
                 re[4 * q + 1] = fmaf(c, x.y, re[4 * q + 1]); im[4 * q + 1] = fmaf(s, x.y, im[4 * q + 1]);
@@ -140,18 +145,20 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
             }
         }
 #pragma unroll
-        for (int q = 0; q < MEL_FR / 4; q++)
+        for (int q = 0; q < FR / 4; q++)
             pw[tid][q] = make_float4(mel_power(re[4 * q], im[4 * q]), mel_power(re[4 * q + 1], im[4 * q + 1]),
                                      mel_power(re[4 * q + 2], im[4 * q + 2]), mel_power(re[4 * q + 3], im[4 * q + 3]));
     }
     __syncthreads();
 
-    const int quad = tid >> 7;   // frames 4 quad .. 4 quad + 3
-    for (int m = tid & 127; m < tb.n_mels; m += 128) {
+    constexpr int MT = MEL_THREADS / (FR / 4);   // threads per frame quad
+    const int quad = tid / MT;                    // frames 4 quad .. 4 quad + 3
+    for (int m = tid % MT; m < tb.n_mels; m += MT) {
         float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         const float* w = tb.fbT + m;
-#pragma unroll 32
-        for (int k = 0; k < MEL_NB; k++) {
+        const int2 kr = tb.krange[m];
+#pragma unroll 8
+        for (int k = kr.x; k < kr.y; k++) {
             const float fw = w[(long long)k * tb.n_mels];
             const float4 p = pw[k][quad];
             acc[0] = fmaf(fw, p.x, acc[0]);
@@ -173,8 +180,11 @@ __global__ __launch_bounds__(MEL_THREADS) void mel_kernel(const MelJob* __restri
 int launch_mel(const MelTables& t, const MelJob* jobs_dev, int n_jobs, int max_nf, hipStream_t st) {
     if (n_jobs < 1 || max_nf < 1) return 0;
     if (t.n_mels < 1 || t.n_mels > 256 || n_jobs > 65535) return -2;
-    dim3 grid((max_nf + MEL_FR - 1) / MEL_FR, n_jobs);
-    mel_kernel<<<grid, MEL_THREADS, 0, st>>>(jobs_dev, t);
+    // 8 frames per workgroup share each cos-table read; below 4 such workgroups per CU the
+    // grid is too small to hide the DFT loop's latency, and 4 frames per workgroup halve it
+    const int wg8 = (max_nf + 7) / 8 * n_jobs;
+    if (wg8 < 1024) mel_kernel<4><<<dim3((max_nf + 3) / 4, n_jobs), MEL_THREADS, 0, st>>>(jobs_dev, t);
+    else mel_kernel<8><<<dim3((max_nf + 7) / 8, n_jobs), MEL_THREADS, 0, st>>>(jobs_dev, t);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -196,6 +206,7 @@ constexpr int MEL_RING = 4;   // job lists of ud_mel_features in flight before a
 struct ud_mel {
     int n_mels = 0;
     float *cos512 = nullptr, *win = nullptr, *fbT = nullptr;
+    int2* krange = nullptr;
     // ring of job lists for ud_mel_features: slot i's pinned staging is rewritten only after the
     // kernel that read slot i's device copy has finished (its event)
     MelJob* djobs[MEL_RING] = {};
@@ -205,13 +216,13 @@ struct ud_mel {
 };
 
 namespace ud {
-MelTables mel_tables_of(const ::ud_mel* m) { return MelTables{m->cos512, m->win, m->fbT, m->n_mels}; }
+MelTables mel_tables_of(const ::ud_mel* m) { return MelTables{m->cos512, m->win, m->fbT, m->krange, m->n_mels}; }
 }  // namespace ud
 
 static void free_mel(ud_mel* m) {
     if (!m) return;
     (void)hipDeviceSynchronize();
-    for (void* p : {(void*)m->cos512, (void*)m->win, (void*)m->fbT}) if (p) (void)hipFree(p);
+    for (void* p : {(void*)m->cos512, (void*)m->win, (void*)m->fbT, (void*)m->krange}) if (p) (void)hipFree(p);
     for (int i = 0; i < MEL_RING; i++) {
         if (m->djobs[i]) (void)hipFree(m->djobs[i]);
         if (m->hjobs[i]) (void)hipHostFree(m->hjobs[i]);
@@ -228,16 +239,25 @@ extern "C" UD_API int ud_mel_create(const float* fb_host, int32_t n_mels, const 
     // NemoMel.swift:33-35), the window as given, the filterbank transposed to [257][n_mels]
     std::vector<float> cs(512), fbT((size_t)MEL_NB * n_mels);
     for (int j = 0; j < 512; j++) cs[j] = (float)cos(2.0 * 3.14159265358979323846 * (double)j / 512.0);
-    for (int m = 0; m < n_mels; m++)
-        for (int k = 0; k < MEL_NB; k++) fbT[(size_t)k * n_mels + m] = fb_host[(size_t)m * MEL_NB + k];
+    std::vector<int2> kr(n_mels);
+    for (int m = 0; m < n_mels; m++) {
+        int lo = MEL_NB, hi = 0;
+        for (int k = 0; k < MEL_NB; k++) {
+            const float w = fb_host[(size_t)m * MEL_NB + k];
+            fbT[(size_t)k * n_mels + m] = w;
+            if (w != 0.0f) { lo = std::min(lo, k); hi = k + 1; }
+        }
+        kr[m] = make_int2(lo < hi ? lo : 0, hi);
+    }
     ud_mel* m = new ud_mel();
     m->n_mels = n_mels;
     bool ok = hipMalloc(&m->cos512, 512 * 4) == hipSuccess && hipMalloc(&m->win, MEL_WIN * 4) == hipSuccess &&
-              hipMalloc(&m->fbT, fbT.size() * 4) == hipSuccess;
+              hipMalloc(&m->fbT, fbT.size() * 4) == hipSuccess && hipMalloc(&m->krange, n_mels * sizeof(int2)) == hipSuccess;
     for (int i = 0; ok && i < MEL_RING; i++) ok = hipEventCreateWithFlags(&m->done[i], hipEventDisableTiming) == hipSuccess;
     ok = ok && hipMemcpy(m->cos512, cs.data(), 512 * 4, hipMemcpyHostToDevice) == hipSuccess &&
          hipMemcpy(m->win, window_host, MEL_WIN * 4, hipMemcpyHostToDevice) == hipSuccess &&
-         hipMemcpy(m->fbT, fbT.data(), fbT.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
+         hipMemcpy(m->fbT, fbT.data(), fbT.size() * 4, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(m->krange, kr.data(), n_mels * sizeof(int2), hipMemcpyHostToDevice) == hipSuccess;
     if (!ok) {
         free_mel(m);
         return mfail(UD_ERR_NOMEM, "ud_mel_create: device allocation or upload failed");
