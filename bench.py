@@ -372,8 +372,8 @@ def stream_bench(ud, args):
         ph = 2 * np.pi * np.cumsum(f0) / 16000.0
         x = sum(np.sin(h * ph) / h for h in range(1, 9)) * (0.2 + 0.15 * np.sin(2 * np.pi * 1.1 * t + b))
         srcs.append((0.3 * x + 0.003 * rng.standard_normal(n_src)).astype(np.float32))
-    # the mel kernel alone at the streamer's launch shape (S jobs x (9 + 8T) frames), HIP events on
-    # its stream
+    # ud_mel_features alone at the streamer's launch shape (S jobs x (9 + 8T) frames), HIP events on
+    # its stream: the job-list copy and the kernel
     hs = ud.HipStream()
     rows = 9 + 8 * T
     clip = (rows - 1) * 160
@@ -388,7 +388,7 @@ def stream_bench(ud, args):
     e1.record(hs)
     e1.synchronize()
     mel_us = e0.elapsed_ms(e1) * 1000.0 / 50
-    log("mel kernel: %.1f us per step (%d streams x %d frames)" % (mel_us, S, rows))
+    log("mel call (job-list copy + kernel): %.1f us per step (%d streams x %d frames)" % (mel_us, S, rows))
     warm = max(args.warmup, 40) if T <= 2 else max(args.warmup // 4, 8)
     res = {}
     for regime, bias in (("blank", 50.0), ("cap", -50.0)):
