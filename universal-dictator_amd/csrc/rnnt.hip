@@ -199,9 +199,9 @@ struct ud_rnnt {
     int cap_proj = 0;
     // device lists of the three phases in separate buffers, each uploaded from its own pinned host
     // buffer: no upload overwrites a list that an earlier kernel or copy may still read
-    int32_t *dslot_p = nullptr, *dtok = nullptr, *dslot_c = nullptr;          // [S]
+    int32_t *dslot_p = nullptr, *dslot_c = nullptr;   // dslot_p [2 S]: n slots, then their n last tokens; dslot_c [S]
     int32_t *dpair = nullptr, *dbest = nullptr;   // dpair [2 cap_pairs]: slots of the joint rows, then their rows
-    int32_t *hslot_p = nullptr, *htok = nullptr, *hslot_c = nullptr;          // pinned [S]
+    int32_t *hslot_p = nullptr, *hslot_c = nullptr;   // pinned, as dslot_p / dslot_c
     int32_t *hpair = nullptr, *hbest = nullptr;   // pinned: hpair [2 cap_pairs] as dpair, hbest [cap_pairs]
 };
 
@@ -218,9 +218,9 @@ static void free_rnnt(ud_rnnt* r) {
     for (float* p : r->wcat) if (p) (void)hipFree(p);
     for (float* p : r->bias) if (p) (void)hipFree(p);
     void* ps[] = {r->h, r->c, r->ph, r->pc, r->pg, r->xh, r->slabs, r->hsum, r->jslabs, r->pslabs, r->dslot_p, r->dpair,
-                  r->dslot_c, r->dtok, r->dbest};
+                  r->dslot_c, r->dbest};
     for (void* p : ps) if (p) (void)hipFree(p);
-    for (void* p : {(void*)r->hslot_p, (void*)r->htok, (void*)r->hslot_c, (void*)r->hpair,
+    for (void* p : {(void*)r->hslot_p, (void*)r->hslot_c, (void*)r->hpair,
                     (void*)r->hbest})
         if (p) (void)hipHostFree(p);
     delete r;
@@ -242,9 +242,8 @@ extern "C" UD_API int ud_rnnt_create(int32_t hidden, int32_t vocab, int32_t laye
     const size_t gmax = 4 * H > V ? 4 * H : V;
     bool ok = (r->h = ralloc(S * L * H)) && (r->c = ralloc(S * L * H)) && (r->ph = ralloc(S * L * H)) &&
               (r->pc = ralloc(S * L * H)) && (r->pg = ralloc(S * H)) && (r->xh = ralloc(S * 2 * H)) &&
-              (r->slabs = ralloc((size_t)RNNT_KS * S * gmax)) && (r->dslot_p = (int32_t*)ralloc(S)) &&
-              (r->dslot_c = (int32_t*)ralloc(S)) && (r->dtok = (int32_t*)ralloc(S)) &&
-              hipHostMalloc((void**)&r->hslot_p, S * 4) == hipSuccess && hipHostMalloc((void**)&r->htok, S * 4) == hipSuccess &&
+              (r->slabs = ralloc((size_t)RNNT_KS * S * gmax)) && (r->dslot_p = (int32_t*)ralloc(2 * S)) &&
+              (r->dslot_c = (int32_t*)ralloc(S)) && hipHostMalloc((void**)&r->hslot_p, 2 * S * 4) == hipSuccess &&
               hipHostMalloc((void**)&r->hslot_c, S * 4) == hipSuccess;
     if (!ok || hipMemset(r->h, 0, S * L * H * 4) != hipSuccess || hipMemset(r->c, 0, S * L * H * 4) != hipSuccess) {
         free_rnnt(r);
@@ -387,11 +386,10 @@ static int predict(ud_rnnt* r, const std::vector<int>& slots, hipStream_t st) {
     const int n = (int)slots.size(), H = r->H, L = r->L;
     for (int i = 0; i < n; i++) {
         r->hslot_p[i] = slots[i];
-        r->htok[i] = r->last[slots[i]];
+        r->hslot_p[n + i] = r->last[slots[i]];
     }
-    RHIPC(hipMemcpyAsync(r->dslot_p, r->hslot_p, n * 4, hipMemcpyHostToDevice, st));
-    RHIPC(hipMemcpyAsync(r->dtok, r->htok, n * 4, hipMemcpyHostToDevice, st));
-    hipLaunchKernelGGL(rnnt_embed_kernel, dim3(n), dim3(256), 0, st, r->w[R_EMBED], r->dslot_p, r->dtok, r->h, r->xh, H, L,
+    RHIPC(hipMemcpyAsync(r->dslot_p, r->hslot_p, (size_t)2 * n * 4, hipMemcpyHostToDevice, st));   // slots + tokens
+    hipLaunchKernelGGL(rnnt_embed_kernel, dim3(n), dim3(256), 0, st, r->w[R_EMBED], r->dslot_p, r->dslot_p + n, r->h, r->xh, H, L,
                        r->V - 1);
     RLAUNCH("rnnt embed");
     for (int l = 0; l < L; l++) {
