@@ -121,13 +121,22 @@ __global__ __launch_bounds__(SUB_C) void sub_dw_kernel(SubDwArgs a) {
         hv[kh] = h >= 0 && h < a.Hin && h < vin;
         rows[kh] = a.x + (((int64_t)s * a.Hin + (hv[kh] ? h : 0)) * a.Win) * SUB_C + c;
     }
+    // The load is unconditional (row and column clamped into the input, Win >= 1) and padding /
+    // masked rows are zeroed by a 0 / 1 factor rather than a branch, so the unrolled loop's loads
+    // issue together.  For finite inputs (rows past the valid length hold conv outputs of
+    // zero-masked rows, so they are finite too) v * 0 is a zero and the sums equal a select's.
+    float hm[3];
+#pragma unroll
+    for (int kh = 0; kh < 3; kh++) hm[kh] = hv[kh] ? 1.0f : 0.0f;
     auto ld = [&](int kh, int col) -> float {
-        return (hv[kh] && col >= 0 && col < a.Win) ? rows[kh][(int64_t)col * SUB_C] : 0.0f;
+        const float v = rows[kh][(int64_t)min(max(col, 0), a.Win - 1) * SUB_C];
+        return v * ((col >= 0 && col < a.Win) ? hm[kh] : 0.0f);
     };
     float win[3][3];
 #pragma unroll
     for (int kh = 0; kh < 3; kh++) win[kh][2] = 0.0f;     // column -2
     const int64_t row0 = ((int64_t)s * a.Hout + ho) * a.Wout;
+#pragma unroll 4
     for (int wo = 0; wo < a.Wout; wo++) {
         float acc = b;
 #pragma unroll
@@ -168,6 +177,7 @@ int launch_sub_conv01(const SubArgs& a, bool half, hipStream_t st) {
 }
 
 int launch_sub_dw(const SubDwArgs& a, bool half, hipStream_t st) {
+    if (a.Win < 1 || a.Hin < 1) return -2;
     const int blocks = a.n * a.Hout;
     if (blocks <= 0) return 0;
     if (half) hipLaunchKernelGGL(sub_dw_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
