@@ -157,7 +157,40 @@ def test_subsample_error_paths(gpu):
     with pytest.raises(ud.EngineError) as e:
         enc.subsample(3, mbuf, obuf, drop=2, mel_rows=25)  # n > max_streams
     assert e.value.status == -2
+    with pytest.raises(ud.EngineError) as e:
+        # 33 rows with drop 3 leave 2 frames, but the stages would need 9 conv rows where the
+        # workspace holds 8 * max_chunk + 9 = 25 mel rows' worth: refused before any launch
+        enc.subsample(2, mbuf, obuf, drop=3, mel_rows=33)
+    assert e.value.status == -2 and "workspace" in str(e.value)
     T, vt = enc.subsample(2, mbuf, obuf, drop=2, mel_rows=25)
     assert T == 2 and list(vt) == [2, 2]
     ud.synchronize()
+    enc.close()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_subsample_nonfinite_masked_rows(gpu, dtype):
+    """NaN and Inf in mel rows past a chunk's valid length never reach the output: every frame
+    equals (bit for bit) the frame computed with those rows zeroed, and all frames are finite."""
+    ud = gpu
+    cfg = ud.EncoderConfig(layers=1, max_chunk=14, max_streams=3, dtype=dtype)
+    enc = ud.Encoder(cfg)
+    enc.set_subsampling_weights(ud.synthetic_subsampling_weights(14))
+    n, rows, drop = 3, 121, 2
+    valid = np.array([rows - 7, 60, 33], np.int32)
+    rng = np.random.default_rng(5)
+    clean = rng.standard_normal((n, rows, 128)).astype(np.float32)
+    for s in range(n):
+        clean[s, valid[s]:] = 0.0
+    dirty = clean.copy()
+    for s in range(n):
+        dirty[s, valid[s]:] = np.where(rng.random((rows - valid[s], 128)) < 0.5, np.nan, np.inf)
+    outs = []
+    for mel in (clean, dirty):
+        mbuf = ud.DeviceBuffer.from_numpy(mel)
+        obuf = ud.DeviceBuffer(n * 14 * 1024 * 4)
+        T, _ = enc.subsample(n, mbuf, obuf, valid_mel=valid, drop=drop)
+        outs.append(obuf.download((n, T, 1024)))
+    assert np.isfinite(outs[1]).all()
+    np.testing.assert_array_equal(outs[1], outs[0])
     enc.close()

@@ -121,16 +121,13 @@ __global__ __launch_bounds__(SUB_C) void sub_dw_kernel(SubDwArgs a) {
         hv[kh] = h >= 0 && h < a.Hin && h < vin;
         rows[kh] = a.x + (((int64_t)s * a.Hin + (hv[kh] ? h : 0)) * a.Win) * SUB_C + c;
     }
-    // The load is unconditional (row and column clamped into the input, Win >= 1) and padding /
-    // masked rows are zeroed by a 0 / 1 factor rather than a branch, so the unrolled loop's loads
-    // issue together.  For finite inputs (rows past the valid length hold conv outputs of
-    // zero-masked rows, so they are finite too) v * 0 is a zero and the sums equal a select's.
-    float hm[3];
-#pragma unroll
-    for (int kh = 0; kh < 3; kh++) hm[kh] = hv[kh] ? 1.0f : 0.0f;
+    // The load is unconditional (row and column clamped into the input, Win >= 1), so the unrolled
+    // loop's loads issue together; a padding tap or a masked row's tap is then replaced by zero
+    // with a select (v_cndmask), so whatever the clamped load read -- NaN or Inf included -- never
+    // reaches the sum.
     auto ld = [&](int kh, int col) -> float {
         const float v = rows[kh][(int64_t)min(max(col, 0), a.Win - 1) * SUB_C];
-        return v * ((col >= 0 && col < a.Win) ? hm[kh] : 0.0f);
+        return (hv[kh] && col >= 0 && col < a.Win) ? v : 0.0f;
     };
     float win[3][3];
 #pragma unroll
