@@ -559,8 +559,7 @@ def main():
     log("parts: subsampling %.4f ms, 24 layers %.4f ms" % (front_ms, layers_ms))
 
     # The fused attention kernel alone, on the stream it is launched on.
-    qkv = ud.DeviceBuffer.from_numpy((ud.round_bf16(rng.standard_normal((S * T, 3 * D), dtype=np.float32))
-                                      .view(np.uint32) >> 16).astype(np.uint16))
+    qkv = ud.DeviceBuffer.from_numpy(ud.f16_bits(rng.standard_normal((S * T, 3 * D), dtype=np.float32)))
     att = ud.DeviceBuffer(S * T * D * 2)
     attn_ms = enc.time_layer_attention(streams, T, 0, qkv, att, args.attn_iters, hip_stream=hs)
     Tk, n_rel = L + T, L + 2 * T - 1

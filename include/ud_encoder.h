@@ -40,10 +40,18 @@ typedef enum {
 
 typedef enum {
     UD_F32 = 0,               /* fp32 weights, activations, caches */
-    UD_BF16 = 1,              /* bf16 weights, GEMM inputs, K/V caches and position tables;
+    UD_BF16 = 1,              /* encoder: bf16 weights (each linear weight rounded to bf16, RNE,
+                                 Tensor.swift:116-122 -- the reference's bf16-weight setting),
+                                 held as IEEE half (exactly, for |w| >= 2^-17) and multiplied on
+                                 the f16 MFMA; 16-bit activations (GEMM inputs, q/k/v,
+                                 attention output), K/V caches and position tables are IEEE half;
                                  fp32 accumulation, residual stream, norms, pos_bias, depthwise
                                  conv and conv cache (the keep-fp32 policy of
-                                 Sources/DictatorEngine/Core/Convert.swift:76-83) */
+                                 Sources/DictatorEngine/Core/Convert.swift:76-83).  Half's 11-bit
+                                 significand (bf16: 8) keeps a 24-layer step within 2e-2 of
+                                 the fp32-activation reference at 14-frame chunks, where bf16
+                                 activations exceed it.
+                                 Single-op attention entries: bfloat16 operands. */
     UD_F16 = 2                /* IEEE half: the decoder K/V cache format of the reference
                                  (Sources/DictatorEngine/Core/Ops.swift:147); decode entry points only */
 } ud_dtype;
@@ -94,7 +102,10 @@ UD_API int ud_encoder_finalize(ud_encoder* enc);
 
 /* Replaces makeStreamState / StreamState (FastConformer.swift:406-435): takes one slot of the
  * encoder's stream pool (K/V ring caches [layers][heads][L][head_dim] and the conv ring
- * [layers][K-1][d_model]), zero-initialised, cache_len 0. */
+ * [layers][K-1][d_model]), zero-initialised, cache_len 0.  Create and reset wait for all work
+ * on the device (hipDeviceSynchronize) before clearing the slot, so a slot freed while a step
+ * that used it was still running starts clean.  Destroy only returns the slot to the pool; it
+ * does not wait. */
 UD_API int ud_stream_create(ud_encoder* enc, ud_stream** out);
 UD_API int ud_stream_reset(ud_stream* s);              /* zero caches, cache_len 0, steps 0 */
 UD_API void ud_stream_destroy(ud_stream* s);
@@ -121,10 +132,12 @@ UD_API int ud_encoder_step(ud_encoder* enc, ud_stream* const* streams, int32_t n
 /* Replaces encodeSubsampling (FastConformer.swift:219-243) and the drop/validT rule of
  * encodeStreamStep (:444-453): NeMo's causal dw_striding 8x subsampling of a batch of mel chunks.
  *   n              streams (1 <= n <= max_streams); all chunks have mel_rows rows
+ *   mel_rows       1 <= mel_rows <= 8 * max_chunk + 9 (the workspace's chunk length); longer
+ *                  chunks return UD_ERR_SHAPE before anything is launched
  *   mel_dev        fp32 [n, mel_rows, 128] mel rows, pre-encode cache rows included
  *   valid_mel_host [n] real rows per chunk (NULL = all); rows beyond are masked as NeMo's
  *                  MaskedConvSequential does, and the valid length follows L -> L/2 + 1 per stage
- *   drop           leading subsampled frames to discard (2 after a stream's first step,
+ *   drop           leading subsampled frames to discard, >= 0 (2 after a stream's first step,
  *                  NemotronSchedule.swift dropExtra; 0 on the first)
  *   out_dev        fp32 [n, T, d_model] encoder input rows, T = mel_rows -> 3 x (L/2 + 1) - drop,
  *                  1 <= T <= max_chunk; feed it to ud_encoder_step
@@ -156,7 +169,8 @@ UD_API int ud_stream_import_cache(ud_stream* s, int32_t layer, const float* k_ho
  * for j in [max(r_i.x,0), min(r_i.y,Tk)), softmax, . V; an empty range gives 0.
  *   q [Tq, H*dk], k/v [Tk, H*dk], P [n_rel, H*dk], u/v [H, dk] (fp32), ranges int32 [Tq, 2],
  *   out [Tq, H*dk]; all device pointers, dtype UD_F32 or UD_BF16 for q/k/v/P/out.
- * Supported: dk in {16, 32, 64, 128}, Tq <= 16; rows 16-byte aligned.
+ * Supported: dk in {16, 32, 64, 128}, Tq <= 16; rows 16-byte aligned.  UD_BF16 here means
+ * bfloat16 operands.
  * Rows referenced by a valid (i, j) pair must lie inside P (caller contract, as in the
  * reference).  Asynchronous on hip_stream. */
 UD_API int ud_relpos_attention(int32_t dtype, const void* q_dev, const void* k_dev, const void* v_dev,
@@ -178,11 +192,30 @@ UD_API int ud_relpos_attention_batched(int32_t dtype, const void* q, const void*
                                        int32_t B, int32_t T, int32_t H, int32_t dk, int32_t rel_offset,
                                        int32_t n_rel, void* hip_stream);
 
+/* Key ranges of the offline path's streaming masks: replaces MaskSpec.ranges(T:) and
+ * chunkedLimitedRanges (Sources/DictatorEngine/Models/FastConformer.swift:324-357) together with
+ * forwardOffline's clip of each range's end to the valid length (:380-381), for B utterances of T
+ * frames, giving the ranges argument of ud_relpos_attention_batched:
+ *   UD_MASK_CHUNKED_LIMITED     NeMo chunked_limited [left, right] (chunk ignored): chunks of
+ *                               right+1 frames aligned at frame 0, left/(right+1) chunks back;
+ *                               query i sees [(c - left/(right+1)) (right+1), (c+1)(right+1)) with
+ *                               c = i / (right+1), clipped to [0, T)
+ *   UD_MASK_CHUNKED_LIMITED_RC  NeMo chunked_limited_with_rc [left, chunk, right]: query i sees
+ *                               [c chunk - left, c chunk + chunk + right) with c = i / chunk
+ *   valid_host    [B] valid frames per utterance (NULL = T); every range's end is clipped to it
+ *                 (its start is not, so a chunk past the valid length is an empty range)
+ *   ranges_host   int32 [B, T, 2], written
+ * Host computation only (no device work). */
+typedef enum { UD_MASK_CHUNKED_LIMITED = 0, UD_MASK_CHUNKED_LIMITED_RC = 1 } ud_mask_kind;
+UD_API int ud_chunked_limited_ranges(int32_t kind, int32_t B, int32_t T, const int32_t* valid_host, int32_t left,
+                                     int32_t chunk, int32_t right, int32_t* ranges_host);
+
 /* The streaming attention of one layer on its own, over the stream's ring caches: the fused
  * kernel the step runs between the QKV projection and linear_out (FastConformer.swift:285-291 with
  * the cache rule of :458-472).
- *   qkv_dev  [n, T, 3*d_model] in the encoder dtype: q | k_new | v_new per row
- *   att_dev  [n, T, d_model] in the encoder dtype, row-major
+ *   qkv_dev  [n, T, 3*d_model]: q | k_new | v_new per row; fp32, or IEEE half for a 16-bit
+ *            (UD_BF16) encoder
+ *   att_dev  [n, T, d_model], row-major, in the same format as qkv_dev
  * Keys are [L cached ; T new], range [L - cache_len, L + valid); afterwards the T new K/V rows
  * are in the ring and the logical window is the last L rows.  Does not advance cache_len or the
  * ring position: call ud_stream_advance to commit the step (ud_encoder_step does both).
@@ -209,7 +242,7 @@ UD_API int ud_time_layer_attention(ud_encoder* enc, ud_stream* const* streams, i
 /* Profiling hook (no reference counterpart): like ud_time_layer_attention, but each launch is a
  * kernel that performs only the loads of the bf16 streaming attention kernel (same grid, same
  * addresses, no arithmetic and no stores to the rings) -- the memory floor that kernel is measured
- * against.  bf16 encoders, T <= 2, L + T <= 80.  att_dev may be written with garbage.  Synchronizes
+ * against.  16-bit encoders, T <= 2, L + T <= 80.  att_dev may be written with garbage.  Synchronizes
  * hip_stream. */
 UD_API int ud_time_ring_read_floor(ud_encoder* enc, ud_stream* const* streams, int32_t n, int32_t T,
                                    int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,

@@ -1,6 +1,9 @@
 """Shared set-up for GPU parity tests: the same seeded weights go to the HIP encoder and to the
-oracle (fp32 activations; in bf16 mode the oracle gets the bf16-rounded linear weights that the
-encoder stores, which is the reference's own bf16-weight setting, Core/Kernels.swift:79-112)."""
+oracle (fp32 activations; for a 16-bit encoder (dtype "bf16") the oracle gets the bf16-rounded
+linear weights that the encoder computes with, which is the reference's own bf16-weight setting,
+Core/Kernels.swift:79-112; the encoder holds them, its activations and its K/V caches as IEEE half)."""
+import os
+
 import numpy as np
 
 # Linear weights that a bf16 encoder stores in bf16 (the rest stay fp32: norms, pos_bias, depthwise
@@ -26,9 +29,21 @@ def make_encoder(ud, orc, cfg, seed=1234, ln_jitter=0.1):
     return enc, model, lw
 
 
+# Achieved errors of the parity checks of this session, printed by the terminal summary of
+# tests/conftest.py so that the margins against the bars are on record: (test, what, kind, values).
+MARGINS = []
+
+
+def _test_id():
+    cur = os.environ.get("PYTEST_CURRENT_TEST", "?")
+    return cur.split(" ")[0].split("::", 1)[-1]
+
+
 def rel_err(got, ref):
     """Max abs error relative to max |ref| (the fp32 path's <= 1e-4 bar)."""
-    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+    e = float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+    MARGINS.append((_test_id(), "", "fp32", e, None))
+    return e
 
 
 def cosine(a, b):
@@ -41,6 +56,7 @@ def assert_bf16_close(got, ref, what=""):
     """The bf16 bar: max abs error <= 2e-2 and cosine >= 0.9995."""
     err = float(np.abs(got - ref).max())
     cos = cosine(got, ref)
+    MARGINS.append((_test_id(), what, "bf16", err, cos))
     assert err <= 2e-2 and cos >= 0.9995, "%s: max abs err %.3g, cosine %.6f" % (what, err, cos)
     return err, cos
 
@@ -62,11 +78,11 @@ class OracleState:
         self.len[:] = cache_len
 
     def import_into(self, streams, ud, bf16):
-        """Loads these caches into the encoder's streams (bf16 caches are rounded on import, so the
-        oracle copy is rounded the same way)."""
+        """Loads these caches into the encoder's streams (a 16-bit encoder's K/V caches are IEEE
+        half, rounded on import, so the oracle copy is rounded the same way)."""
         if bf16:
-            self.k[:] = ud.round_bf16(self.k)
-            self.v[:] = ud.round_bf16(self.v)
+            self.k[:] = ud.round_f16(self.k)
+            self.v[:] = ud.round_f16(self.v)
         for s, st in enumerate(streams):
             for l in range(self.k.shape[1]):
                 st.import_cache(l, self.k[s, l], self.v[s, l], self.c[s, l], int(self.len[s]))

@@ -124,8 +124,9 @@ def test_ring_attention_and_cache_update(gpu, orc, dtype, T, L):
     layer = 1
     qkv = rng.standard_normal((S, T, 3 * D)).astype(np.float32)
     if dtype == "bf16":
-        qkv = ud.round_bf16(qkv)
-        qbuf = _bf16_dev(ud, qkv)
+        # a 16-bit encoder's activations (qkv in, att out) are IEEE half
+        qkv = ud.round_f16(qkv)
+        qbuf = _dev(ud, ud.f16_bits(qkv))
         att = ud.DeviceBuffer(S * T * D * 2)
     else:
         qbuf = _dev(ud, qkv)
@@ -133,12 +134,12 @@ def test_ring_attention_and_cache_update(gpu, orc, dtype, T, L):
     enc.layer_attention(streams, T, layer, qbuf, att, valid=valid)
     ud.synchronize()
     if dtype == "bf16":
-        got = (att.download((S, T, D), np.uint16).astype(np.uint32) << 16).view(np.float32)
+        got = ud.from_f16_bits(att.download((S, T, D), np.uint16))
     else:
         got = att.download((S, T, D))
     P = model.P[layer]
     if dtype == "bf16":
-        P = ud.round_bf16(P)
+        P = ud.round_f16(P)
     for s in range(S):
         keys = np.concatenate([st.k[s, layer], qkv[s, :, D:2 * D]])
         vals = np.concatenate([st.v[s, layer], qkv[s, :, 2 * D:]])

@@ -62,10 +62,9 @@ def test_offline_chunked_limited_mask(gpu, orc):
     rng = np.random.default_rng(32)
     B, T = 1, 300
     q, k, v, P, u, vb = _inputs(ud, rng, B, T)
-    r = orc.chunked_limited_ranges(T, 70, 1)
-    r[:, 1] = np.minimum(r[:, 1], 250)
-    r[17] = [40, 40]
-    ranges = r[None]
+    # the product's range builder: chunked_limited [70, 1] with the clip to 250 valid frames
+    ranges = ud.chunked_limited_ranges(T, 70, 1, valid=[250])
+    ranges[0, 17] = [40, 40]
     got = _run(ud, q, k, v, P, u, vb, ranges)
     assert not np.any(got[0, 17])
     harness.assert_bf16_close(got, _oracle(orc, q, k, v, P, u, vb, ranges), "offline chunked mask")

@@ -125,6 +125,28 @@ def test_step_bf16_chunk14_many_rows(gpu, orc):
     enc.close()
 
 
+def test_step_bf16_chunk14_24_layers(gpu, orc):
+    """Config 3's chunk at full depth: 32 streams x 14 frames x 24 layers from seeded full caches,
+    two steps (ragged valid counts on the second), against the oracle's fp32 step -- the bf16
+    error accumulated over 24 layers at 84 keys."""
+    cfg = gpu.EncoderConfig(layers=24, max_chunk=14, max_streams=32, dtype="bf16")
+    plan = lambda step, S, T: [(T, 11, T, 2)[s % 4] if step == 1 else T for s in range(S)]
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=32, T=14, n_steps=2, seed=65, seed_caches=True, valid_plan=plan)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
+def test_step_bf16_chunk14_24_layers_lds_tiles(gpu, orc):
+    """24 layers at 148 streams x 14 frames = 2,072 rows: the LDS-staged projection kernel (the
+    config-3 GEMM path) at full depth, two steps from fresh streams."""
+    cfg = gpu.EncoderConfig(layers=24, max_chunk=14, max_streams=148, dtype="bf16")
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=148, T=14, n_steps=2, seed=67, seed_caches=False)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
 def test_graph_replay_matches_eager(gpu, orc):
     """The captured hipGraph replay gives bit-identical results to eager launches (the step is
     deterministic: split-K partials are reduced in a fixed order)."""
@@ -203,3 +225,29 @@ def test_error_paths(gpu, orc):
     s0.reset()
     assert s0.cache_len == 0 and s0.step == 0
     enc.close()
+
+
+def test_recycled_slot_starts_clean_after_async_step(gpu, orc):
+    """A stream destroyed while its step still runs on a non-blocking HIP stream, and a new stream
+    created at once in the freed slot: the new stream's K/V and conv caches are all zero (creation
+    waits for the device before clearing the slot)."""
+    ud = gpu
+    cfg = ud.EncoderConfig(layers=4, max_chunk=14, max_streams=4, dtype="bf16")
+    enc, _, _ = harness.make_encoder(ud, orc, cfg, seed=91)
+    streams = [enc.new_stream() for _ in range(4)]
+    rng = np.random.default_rng(3)
+    x = ud.DeviceBuffer.from_numpy(rng.standard_normal((4, 14, 1024)).astype(np.float32))
+    o = ud.DeviceBuffer(4 * 14 * 1024 * 4)
+    hs = ud.HipStream()
+    for _ in range(3):
+        enc.encode_stream_step(streams, x, o, T=14, hip_stream=hs)
+    victim = streams[2]
+    victim.close()                   # the queued steps may still be writing its rings
+    fresh = enc.new_stream()
+    hs.synchronize()
+    assert fresh.cache_len == 0
+    for l in range(cfg.layers):
+        k, v, c, _ = fresh.export_cache(l)
+        assert not np.any(k) and not np.any(v) and not np.any(c), "layer %d" % l
+    enc.close()
+

@@ -69,6 +69,7 @@ def _sig(lib):
         "ud_relpos_attention": (i, [_i32, p, p, p, p, p, p, p, p, _i32, _i32, _i32, _i32, _i32, _i32, p]),
         "ud_relpos_attention_batched": (i, [_i32, p, p, p, p, p, p, p, p, _i32, _i32, _i32, _i32, _i32, _i32, p]),
         "ud_layer_attention": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, ip, p, p]),
+        "ud_chunked_limited_ranges": (i, [_i32, _i32, _i32, ip, _i32, _i32, _i32, ip]),
         "ud_stream_advance": (i, [ctypes.POINTER(_vp), _i32, _i32]),
         "ud_time_layer_attention": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, p, _i32, p, f]),
         "ud_time_ring_read_floor": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, p, _i32, p, f]),
@@ -461,6 +462,29 @@ def rel_pos_attention(q, k, v, pos_table, rel_offset, bias_u, bias_v, ranges, ou
                                      hip_stream.ptr if hip_stream else None))
 
 
+MASK_CHUNKED_LIMITED, MASK_CHUNKED_LIMITED_RC = 0, 1
+
+
+def chunked_limited_ranges(T, left, right, valid=None, chunk=None):
+    """Key ranges int32 [B, T, 2] of the offline streaming masks (MaskSpec.ranges +
+    forwardOffline's clip to the valid length, FastConformer.swift:324-357, 380-381).  chunk None:
+    chunked_limited [left, right]; else chunked_limited_with_rc [left, chunk, right].  valid: None
+    (one utterance, no clip), an int, or a sequence of B valid lengths.  Host computation only."""
+    if valid is None:
+        vals = None
+        B = 1
+    else:
+        vals = np.atleast_1d(np.asarray(valid, np.int32))
+        B = len(vals)
+    out = np.empty((B, T, 2), np.int32)
+    ip = ctypes.POINTER(_i32)
+    kind = MASK_CHUNKED_LIMITED if chunk is None else MASK_CHUNKED_LIMITED_RC
+    _check(load_library().ud_chunked_limited_ranges(
+        kind, B, T, vals.ctypes.data_as(ip) if vals is not None else None, left, 0 if chunk is None else chunk, right,
+        out.ctypes.data_as(ip)))
+    return out
+
+
 def rel_pos_attention_batched(q, k, v, pos_table, rel_offset, bias_u, bias_v, ranges, out, B, T, heads,
                               n_rel, head_dim=128, hip_stream=None):
     """Offline relPosAttention over B whole utterances (bf16): q/k/v/out [B, T, H*128], pos_table
@@ -711,6 +735,21 @@ def synthetic_rnnt_weights(seed, H=640, V=1025, L=2, enc_dim=1024, blank_bias=0.
     w["joint.joint_net.2.weight"], w["joint.joint_net.2.bias"] = u((V, H), k), u(V, k)
     w["joint.joint_net.2.bias"][V - 1] += np.float32(blank_bias)
     return w
+
+
+def round_f16(a):
+    """IEEE-half rounding (round to nearest even) of float32 values, returned as float32: the
+    storage format of a 16-bit (UD_BF16) encoder's activations, K/V caches and position tables."""
+    return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
+
+
+def f16_bits(a):
+    """uint16 bit patterns of IEEE half(a) (round to nearest even)."""
+    return np.ascontiguousarray(np.asarray(a, np.float32).astype(np.float16)).view(np.uint16)
+
+
+def from_f16_bits(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
 
 
 def round_bf16(a):

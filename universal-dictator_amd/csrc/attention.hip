@@ -61,11 +61,11 @@ template <typename T>
 struct RingSrc {
     const T* kr; const T* vr;      // this (stream, head) ring slice: [L][dk]
     const T* qkv;                  // first row of this stream in [n*T, 3*D]
-    const T* P; T* O;              // P [n_rel, D]; O = att [n*T, D] (bf16: fragment-major)
+    const T* P; T* O;              // P [n_rel, D]; O = att [n*T, D] (16-bit: fragment-major)
     const float* u; const float* vb;
     int Tq, Tk, L, D, hoff, wpos, rel_offset, n_rel, ks, ke;
     int64_t row0;                  // global row of this stream's first query
-    bool frag;                     // bf16 output in the fragment-major layout
+    bool frag;                     // 16-bit output in the fragment-major layout
     __device__ const T* qrow(int i) const { return qkv + (int64_t)i * 3 * D + hoff; }
     __device__ const T* krow(int j) const {
         if (j < L) { int s = wpos + j; s -= (s >= L) ? L : 0; return kr + (int64_t)s * 128; }
@@ -76,7 +76,7 @@ struct RingSrc {
         return qkv + (int64_t)(j - L) * 3 * D + 2 * D + hoff;
     }
     __device__ const T* prow(int r) const { return P + (int64_t)r * D + hoff; }
-    // The output feeds linear_out: bf16 goes fragment-major (the GEMM's operand order).
+    // The output feeds linear_out: 16-bit goes fragment-major (the GEMM's operand order).
     __device__ void store(int i, int d, float v) const {
         if (sizeof(T) == 2 && frag) O[frag_index(row0 + i, hoff + d, D / 64)] = from_f<T>(v);
         else O[(row0 + i) * D + hoff + d] = from_f<T>(v);
@@ -290,7 +290,7 @@ __global__ __launch_bounds__(256) void relpos_ring_kernel(RingArgs a) {
 }
 
 // ------------------------------------------------------------------ streaming ring kernel (T <= 4)
-// The chunk shapes of streaming (2..4 queries over L + T <= 96 keys, bf16, head_dim 128) get a
+// The chunk shapes of streaming (2..4 queries over L + T <= 96 keys, IEEE half, head_dim 128) get a
 // kernel built for one memory round trip.  It works on the whole window [L cached ; T new] and on
 // the whole positional band of the chunk (rel = 1-T .. L+T-1, the same rows for every stream), so
 // the addresses of q, u/v and the band depend only on the launch, and those of K/V only on the
@@ -367,8 +367,8 @@ struct WindowRows {
             noff[k] = ((uint32_t)(j[k] - L) * 3u * (uint32_t)D + (uint32_t)sub * 8u) * 2u;
         }
     }
-    __device__ __forceinline__ void load(uint4 (&kreg)[KR], uint4 (&vreg)[KR], const bf16* kbase, const bf16* vbase,
-                                         const bf16* knew, const bf16* vnew, int wpos, int L, int sub) const {
+    __device__ __forceinline__ void load(uint4 (&kreg)[KR], uint4 (&vreg)[KR], const f16* kbase, const f16* vbase,
+                                         const f16* knew, const f16* vnew, int wpos, int L, int sub) const {
         const char* kb = reinterpret_cast<const char*>(kbase);
         const char* vb = reinterpret_cast<const char*>(vbase);
         const char* kn = reinterpret_cast<const char*>(knew);
@@ -404,12 +404,12 @@ struct WindowRows {
 };
 
 
-// One workgroup (4 waves) per (stream, head).  16 lanes own one 128-wide bf16 row (8 values per
+// One workgroup (4 waves) per (stream, head).  16 lanes own one 128-wide half row (8 values per
 // lane), 16 row groups per pass: KR passes cover the window's L + T keys, PR passes the band's
 // L + 2T - 1 rows.  TQ in {2, 4} queries (T < TQ runs with clamped duplicate queries).
 template <int TQ, int KR, int PR>
 __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
-    using T = bf16;
+    using T = f16;
     constexpr int DK = 128, VEC = 8, LPR = 16, G = 16;
     constexpr int KMAX = KR * G, BMAX = PR * G, NV = TQ * VEC, NQ = NV / 4;
     static_assert(NQ % 4 == 0, "float4 partial sums");
@@ -589,7 +589,7 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
         uint32_t pk[4];
 #pragma unroll
         for (int e = 0; e < 4; e++)
-            pk[e] = empty ? 0u : ((uint32_t)f2bf(o[2 * e]) | ((uint32_t)f2bf(o[2 * e + 1]) << 16));
+            pk[e] = empty ? 0u : ((uint32_t)f2h(o[2 * e]) | ((uint32_t)f2h(o[2 * e + 1]) << 16));
         const int64_t row = (int64_t)s * Tq + i;
         T* att = static_cast<T*>(a.att);
         T* dst = a.att_frag ? att + frag_index(row, h * DK + sub * VEC, D / 64) : att + row * D + h * DK + sub * VEC;
@@ -604,7 +604,7 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
 // attention kernel is measured against it.
 template <int KR, int PR>
 __global__ __launch_bounds__(256) void ring_read_floor_kernel(RingArgs a) {
-    using T = bf16;
+    using T = f16;
     constexpr int TQ = 2, DK = 128, VEC = 8, LPR = 16, G = 16;
     const int tid = threadIdx.x, grp = tid / LPR, sub = tid % LPR;
     const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
@@ -654,27 +654,27 @@ int launch_ring_read_floor(const RingArgs& a, hipStream_t st) {
 // ------------------------------------------------------------------ streaming ring kernel on MFMA (T <= 16)
 // Longer chunks (config of 14 frames) make the per-(stream, head) work a real matrix product:
 // 16 query rows (T of them real) against L + T keys and L + 2T - 1 band rows.  One wave64 per
-// (stream, head), everything on v_mfma_f32_16x16x32_bf16:
+// (stream, head), everything on v_mfma_f32_16x16x32_f16:
 //   bd^T-free form: C[query][band row] = (q+v) . P_band^T   (A = q+v, B = P rows straight from HBM/L2)
 //   C[query][key] = (q+u) . K^T                              (B = K rows straight from the ring)
 //   out[query][chan] = softmax . V                           (A = probabilities, B = V^T)
 // A lane's B operand is 8 consecutive k values for one n: for the score products that is one
 // 16-byte chunk of a K / P row (n = row, k = channels), loaded directly; for P.V it is 8 keys of one
 // channel, which ds_read_b64_tr_b16 produces from V rows staged row-major in LDS.  q+u, q+v and the
-// probabilities are fp32 and enter as bf16 hi/lo pairs (two MFMAs), so products keep ~2^-17
+// probabilities are fp32 and enter as IEEE-half hi/lo pairs (two MFMAs), so products keep ~2^-21
 // relative accuracy.  Scores stay in registers (lane: queries 4g..4g+3 of key 16t + lane%16);
 // rel_shift is a gather of the band tile from LDS; softmax reduces within 16-lane DPP rows.
 
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
-// fp32 x 8 -> bf16 hi (round to nearest even) and lo = bf16(x - hi), packed for an MFMA operand.
-__device__ __forceinline__ void split_bf16x8(const float (&x)[8], uint4& hi, uint4& lo) {
+// fp32 x 8 -> half hi (round to nearest even) and lo = half(x - hi), packed for an MFMA operand.
+__device__ __forceinline__ void split_f16x8(const float (&x)[8], uint4& hi, uint4& lo) {
     uint32_t hw[4], lw[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
-        const bf16 h0 = f2bf(x[e]), h1 = f2bf(x[e + 1]);
+        const uint16_t h0 = f2h(x[e]), h1 = f2h(x[e + 1]);
         hw[e / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-        lw[e / 2] = (uint32_t)f2bf(x[e] - bf2f(h0)) | ((uint32_t)f2bf(x[e + 1] - bf2f(h1)) << 16);
+        lw[e / 2] = (uint32_t)f2h(x[e] - h2f(h0)) | ((uint32_t)f2h(x[e + 1] - h2f(h1)) << 16);
     }
     hi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     lo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
@@ -682,10 +682,10 @@ __device__ __forceinline__ void split_bf16x8(const float (&x)[8], uint4& hi, uin
 
 template <int KT, int BT>
 __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
-    using T = bf16;
+    using T = f16;
     constexpr int DK = 128, KMAX = KT * 16, BMAX = BT * 16, VST = DK + 8;
     static_assert(KMAX % 32 == 0, "P.V k-steps of 32 keys");
-    __shared__ __align__(16) bf16 vl[KMAX][VST];          // V rows of the window (masked rows 0)
+    __shared__ __align__(16) uint16_t vl[KMAX][VST];      // V rows of the window (masked rows 0)
     __shared__ __align__(16) float sl[16][BMAX + 4];       // band tile for the gather, then probabilities
 
     const int lane = threadIdx.x, col = lane & 15, g = lane >> 4;
@@ -731,7 +731,7 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
         for (int st = 0; st < 4; st++) kb[t][st] = ld16(row + (4 * st + g) * 8);
     }
 
-    // ---- A operands: q + u and q + v as bf16 hi/lo
+    // ---- A operands: q + u and q + v as half hi/lo
     uint4 auh[4], aul[4], avh[4], avl[4];
 #pragma unroll
     for (int st = 0; st < 4; st++) {
@@ -741,8 +741,8 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
         const float vv[8] = {va[st][0].x, va[st][0].y, va[st][0].z, va[st][0].w, va[st][1].x, va[st][1].y, va[st][1].z, va[st][1].w};
 #pragma unroll
         for (int e = 0; e < 8; e++) { x[e] = q[e] + uu[e]; y[e] = q[e] + vv[e]; }
-        split_bf16x8(x, auh[st], aul[st]);
-        split_bf16x8(y, avh[st], avl[st]);
+        split_f16x8(x, auh[st], aul[st]);
+        split_f16x8(y, avh[st], avl[st]);
     }
 
     // ---- bd tiles -> LDS: sl[query][band row]
@@ -751,8 +751,8 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
         f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int st = 0; st < 4; st++) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avh[st]), as_bf16x8(pb[t][st]), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(avl[st]), as_bf16x8(pb[t][st]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(avh[st]), as_f16x8(pb[t][st]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(avl[st]), as_f16x8(pb[t][st]), acc, 0, 0, 0);
         }
 #pragma unroll
         for (int r = 0; r < 4; r++) sl[4 * g + r][16 * t + col] = acc[r];
@@ -770,8 +770,8 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
         f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int st = 0; st < 4; st++) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(auh[st]), as_bf16x8(kb[t][st]), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aul[st]), as_bf16x8(kb[t][st]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(auh[st]), as_f16x8(kb[t][st]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(aul[st]), as_f16x8(kb[t][st]), acc, 0, 0, 0);
         }
         sacc[t] = acc;
     }
@@ -852,7 +852,7 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
         const float4 p1 = *reinterpret_cast<const float4*>(&sl[col][32 * kk + 8 * g + 4]);
         pf[0] = p0.x; pf[1] = p0.y; pf[2] = p0.z; pf[3] = p0.w; pf[4] = p1.x; pf[5] = p1.y; pf[6] = p1.z; pf[7] = p1.w;
         uint4 ph, pl;
-        split_bf16x8(pf, ph, pl);
+        split_f16x8(pf, ph, pl);
         const int k0 = 32 * kk + 8 * g + (col >> 2);
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
@@ -862,8 +862,8 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
             uint4 bv;
             __builtin_memcpy(&bv.x, &b0, 8);
             __builtin_memcpy(&bv.z, &b1, 8);
-            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ph), as_bf16x8(bv), oacc[dt], 0, 0, 0);
-            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pl), as_bf16x8(bv), oacc[dt], 0, 0, 0);
+            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(ph), as_f16x8(bv), oacc[dt], 0, 0, 0);
+            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(pl), as_f16x8(bv), oacc[dt], 0, 0, 0);
         }
     }
 
@@ -879,7 +879,7 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
             for (int dt = 0; dt < 8; dt++) {
                 const int c = h * DK + 16 * dt + col;
                 const int64_t idx = a.att_frag ? frag_index(orow, c, D / 64) : orow * D + c;
-                att[idx] = empty ? (T)0 : f2bf(oacc[dt][r]);
+                att[idx] = empty ? (T)0 : (T)oacc[dt][r];
             }
         }
     }
@@ -1161,7 +1161,7 @@ int launch_relpos_op(const OpArgs& a, bool bf16_data, hipStream_t st) {
 template <typename T>
 static int launch_ring_t(const RingArgs& a, hipStream_t st) {
     dim3 grid(a.n * a.H), block(256);
-    // bf16 streaming chunks (T <= 4, 16 <= L, L + T <= 96 keys, head_dim 128): the one-round-trip kernel.
+    // 16-bit streaming chunks (T <= 4, 16 <= L, L + T <= 96 keys, head_dim 128): the one-round-trip kernel.
     // It reads the band rel = 1-T .. L+T-1 (table rows rel_offset+1-T .. rel_offset+L+T-1).
     const bool band_ok = a.rel_offset + 1 - a.T >= 0 && a.rel_offset + a.L + a.T - 1 < a.n_rel;
     if (sizeof(T) == 2 && a.T <= 4 && a.L >= 16 && a.L + a.T <= 96 && a.L + 2 * a.T - 1 <= 112 && band_ok) {
@@ -1172,7 +1172,7 @@ static int launch_ring_t(const RingArgs& a, hipStream_t st) {
         else hipLaunchKernelGGL((relpos_ring_small_kernel<4, 6, 7>), grid, block, 0, st, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    // bf16 chunks of 5..16 frames (L + T <= 96 keys): the MFMA kernel, one wave per (stream, head).
+    // 16-bit chunks of 5..16 frames (L + T <= 96 keys): the MFMA kernel, one wave per (stream, head).
     if (sizeof(T) == 2 && a.T <= 16 && a.L + a.T <= 96 && a.L + 2 * a.T - 1 <= 112 && band_ok) {
         hipLaunchKernelGGL((relpos_ring_mfma_kernel<6, 7>), dim3(a.n * a.H), dim3(64), 0, st, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;
@@ -1184,9 +1184,9 @@ static int launch_ring_t(const RingArgs& a, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-int launch_relpos_ring(const RingArgs& a, bool bf16_data, hipStream_t st) {
+int launch_relpos_ring(const RingArgs& a, bool half_data, hipStream_t st) {
     if (a.T < 1 || a.T > 16 || a.T > a.L || a.n < 1) return -2;
-    return bf16_data ? launch_ring_t<bf16>(a, st) : launch_ring_t<float>(a, st);
+    return half_data ? launch_ring_t<f16>(a, st) : launch_ring_t<float>(a, st);
 }
 
 }  // namespace ud

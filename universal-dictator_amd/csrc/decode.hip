@@ -142,13 +142,14 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
     // ---- K and V rows: key s0 + grp + RG p; pages outside [klo, khi) are never looked up
     const int blo = klo / PAGE, bhi = (khi - 1) / PAGE;
     const int32_t* bt = a.bt + (int64_t)seq * a.max_blocks;
-    uint32_t off[NP];
+    // element offsets in 64 bits: a pool may hold 2^32 elements or more (8 GiB of 16-bit K or V)
+    int64_t off[NP];
 #pragma unroll
     for (int p = 0; p < NP; p++) {
         const int j = s0 + grp + RG * p;
         const int b = min(max(j / PAGE, blo), bhi);
-        const int phys = bt[b];
-        off[p] = ((uint32_t)(phys * a.Hkv + kvh) * PAGE + (uint32_t)(j % PAGE)) * D + sub * 8;
+        const int64_t phys = bt[b];
+        off[p] = ((phys * a.Hkv + kvh) * PAGE + (j % PAGE)) * D + sub * 8;
     }
     const uint16_t* kp = static_cast<const uint16_t*>(a.kp);
     const uint16_t* vp = static_cast<const uint16_t*>(a.vp);
@@ -376,42 +377,66 @@ static int launch_gqa(const GqaArgs& a, int n, int G, int nsplit, float* out, hi
     return UD_OK;
 }
 
-extern "C" UD_API int ud_gqa_attention_paged(int32_t kv_dtype, const float* q_dev, const void* k_pages,
-                                             const void* v_pages, const int32_t* block_table, int32_t max_blocks,
-                                             const int32_t* ranges_dev, float* out_dev, int32_t n, int32_t q_heads,
-                                             int32_t kv_heads, int32_t head_dim, int32_t block_size, int32_t max_keys,
-                                             void* workspace, size_t workspace_bytes, void* hip_stream) {
-    if (!q_dev || !k_pages || !v_pages || !block_table || !ranges_dev || !out_dev || !workspace)
-        return dfail(UD_ERR_INVALID, "ud_gqa_attention_paged: null pointer");
-    if (kv_dtype != UD_BF16 && kv_dtype != UD_F16) return dfail(UD_ERR_INVALID, "ud_gqa_attention_paged: kv dtype %d", kv_dtype);
-    if (n < 1 || q_heads < 1 || kv_heads < 1 || q_heads % kv_heads) return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: heads %d/%d, n %d", q_heads, kv_heads, n);
+// Argument checks shared by both decode entry points (everything but the workspace).
+static int gqa_check(const char* who, int32_t kv_dtype, const float* q_dev, const void* k_pages, const void* v_pages,
+                     const int32_t* block_table, int32_t max_blocks, const int32_t* ranges_dev, const float* out_dev,
+                     int32_t n, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t block_size,
+                     int32_t max_keys) {
+    if (!q_dev || !k_pages || !v_pages || !block_table || !ranges_dev || !out_dev)
+        return dfail(UD_ERR_INVALID, "%s: null pointer", who);
+    if (kv_dtype != UD_BF16 && kv_dtype != UD_F16) return dfail(UD_ERR_INVALID, "%s: kv dtype %d", who, kv_dtype);
+    if (n < 1 || q_heads < 1 || kv_heads < 1 || q_heads % kv_heads)
+        return dfail(UD_ERR_SHAPE, "%s: heads %d/%d, n %d", who, q_heads, kv_heads, n);
     const int G = q_heads / kv_heads;
-    if (G != 1 && G != 2 && G != 4 && G != 8) return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: group %d not in {1,2,4,8}", G);
-    if (head_dim != 64 && head_dim != 128) return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: head_dim %d", head_dim);
-    if (block_size != PAGE) return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: block_size %d (16 supported)", block_size);
+    if (G != 1 && G != 2 && G != 4 && G != 8) return dfail(UD_ERR_SHAPE, "%s: group %d not in {1,2,4,8}", who, G);
+    if (head_dim != 64 && head_dim != 128) return dfail(UD_ERR_SHAPE, "%s: head_dim %d", who, head_dim);
+    if (block_size != PAGE) return dfail(UD_ERR_SHAPE, "%s: block_size %d (16 supported)", who, block_size);
     if (max_blocks < 1 || max_keys < 0 || max_keys > max_blocks * PAGE)
-        return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: max_keys %d beyond %d blocks", max_keys, max_blocks);
-    if (workspace_bytes < ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys))
-        return dfail(UD_ERR_SHAPE, "ud_gqa_attention_paged: workspace %zu < %zu bytes", workspace_bytes,
-                     ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys));
-    if (((uintptr_t)q_dev | (uintptr_t)k_pages | (uintptr_t)v_pages | (uintptr_t)workspace) & 15)
-        return dfail(UD_ERR_INVALID, "ud_gqa_attention_paged: buffers must be 16-byte aligned");
+        return dfail(UD_ERR_SHAPE, "%s: max_keys %d beyond %d blocks", who, max_keys, max_blocks);
+    if (((uintptr_t)q_dev | (uintptr_t)k_pages | (uintptr_t)v_pages) & 15)
+        return dfail(UD_ERR_INVALID, "%s: buffers must be 16-byte aligned", who);
+    return UD_OK;
+}
+
+// Launches split + combine with `workspace` as the split partials (checked by the caller).
+static int gqa_launch(const char* who, int32_t kv_dtype, const float* q_dev, const void* k_pages, const void* v_pages,
+                      const int32_t* block_table, int32_t max_blocks, const int32_t* ranges_dev, float* out_dev,
+                      int32_t n, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t max_keys,
+                      float* workspace, hipStream_t st) {
+    const int G = q_heads / kv_heads;
     GqaArgs a{};
     a.q = q_dev; a.kp = k_pages; a.vp = v_pages; a.bt = block_table; a.ranges = ranges_dev;
-    a.part = static_cast<float*>(workspace);
+    a.part = workspace;
     a.max_blocks = max_blocks; a.Hq = q_heads; a.Hkv = kv_heads; a.NS = nsplits(max_keys);
     a.kmax = min(max_blocks * PAGE, a.NS * SPLIT);
     a.scale = 1.0f / sqrtf((float)head_dim);
-    hipStream_t st = static_cast<hipStream_t>(hip_stream);
     int rc;
     if (kv_dtype == UD_BF16)
         rc = head_dim == 128 ? launch_gqa<BF16, 128>(a, n, G, a.NS, out_dev, st) : launch_gqa<BF16, 64>(a, n, G, a.NS, out_dev, st);
     else
         rc = head_dim == 128 ? launch_gqa<F16, 128>(a, n, G, a.NS, out_dev, st) : launch_gqa<F16, 64>(a, n, G, a.NS, out_dev, st);
-    if (rc != UD_OK) return dfail(rc, "ud_gqa_attention_paged: unsupported shape");
+    if (rc != UD_OK) return dfail(rc, "%s: unsupported shape", who);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return dfail(UD_ERR_HIP, "ud_gqa_attention_paged: %s", hipGetErrorString(e));
+    if (e != hipSuccess) return dfail(UD_ERR_HIP, "%s: %s", who, hipGetErrorString(e));
     return UD_OK;
+}
+
+extern "C" UD_API int ud_gqa_attention_paged(int32_t kv_dtype, const float* q_dev, const void* k_pages,
+                                             const void* v_pages, const int32_t* block_table, int32_t max_blocks,
+                                             const int32_t* ranges_dev, float* out_dev, int32_t n, int32_t q_heads,
+                                             int32_t kv_heads, int32_t head_dim, int32_t block_size, int32_t max_keys,
+                                             void* workspace, size_t workspace_bytes, void* hip_stream) {
+    static const char* who = "ud_gqa_attention_paged";
+    int rc = gqa_check(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, q_heads,
+                       kv_heads, head_dim, block_size, max_keys);
+    if (rc != UD_OK) return rc;
+    if (!workspace) return dfail(UD_ERR_INVALID, "%s: null workspace", who);
+    if (workspace_bytes < ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys))
+        return dfail(UD_ERR_SHAPE, "%s: workspace %zu < %zu bytes", who, workspace_bytes,
+                     ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys));
+    if ((uintptr_t)workspace & 15) return dfail(UD_ERR_INVALID, "%s: workspace must be 16-byte aligned", who);
+    return gqa_launch(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, q_heads,
+                      kv_heads, head_dim, max_keys, static_cast<float*>(workspace), static_cast<hipStream_t>(hip_stream));
 }
 
 extern "C" UD_API int ud_rope_rotate_half(int32_t dtype, void* x_dev, int32_t rows, int32_t heads, int32_t head_dim,

@@ -2,8 +2,11 @@
 //
 // Mirrors FastConformerEncoder + StreamState + encodeStreamStep
 // (Sources/DictatorEngine/Models/FastConformer.swift:62-480) for a batch of streams:
-//  - one encoder owns device weights (bf16 or fp32), per-layer position tables, a step workspace
-//    sized for max_streams x max_chunk rows and a pool of per-stream caches;
+//  - one encoder owns device weights, per-layer position tables, a step workspace sized for
+//    max_streams x max_chunk rows and a pool of per-stream caches; a 16-bit (UD_BF16) encoder
+//    holds bf16-valued weights as IEEE half and computes on the f16 MFMA with half activations,
+//    K/V caches and tables (fp32 accumulation, fp32 residual stream, norms and conv cache), an
+//    fp32 encoder keeps everything in fp32;
 //  - caches are rings updated in place by the attention and conv kernels (no ping-pong copies);
 //    a stream's ring origin is derived from its frame counter, so the host carries one integer
 //    per stream and uploads a small descriptor {slot, ring origins, valid, cache_len} per step;
@@ -80,6 +83,25 @@ static inline float host_bf16_to_f(uint16_t b) {
     return f;
 }
 
+// IEEE half (round to nearest even): a 16-bit encoder's storage format for weights, activations,
+// K/V caches and position tables.
+static inline uint16_t host_f16(float f) {
+    const _Float16 h = (_Float16)f;
+    uint16_t b;
+    memcpy(&b, &h, 2);
+    return b;
+}
+static inline float host_f16_to_f(uint16_t b) {
+    _Float16 h;
+    memcpy(&h, &b, 2);
+    return (float)h;
+}
+// A weight of a 16-bit encoder: its bf16 value (the reference's bf16-weight setting), held as IEEE
+// half for the f16 MFMA.  Exact for every bf16 value of magnitude 2^-17 .. 65504 (half's 11-bit
+// significand holds bf16's 8 bits); smaller magnitudes keep half's subnormal resolution, 2^-24.
+static inline uint16_t host_weight16(float f) { return host_f16(host_bf16_to_f(host_bf16(f))); }
+static constexpr float kHalfMax = 65504.0f;
+
 // ---------------------------------------------------------------- weights
 
 // The 26 tensors of one layer (docs/specs/nemotron.md tensor-name map; loading at
@@ -146,7 +168,7 @@ struct SubDev {
 
 struct ud_encoder {
     ud_encoder_config cfg;
-    bool bf;
+    bool bf;                        // 16-bit encoder (UD_BF16): half storage, f16 MFMA
     size_t esz;
     int D, H, dk, ff, Kc, L, layers, n_rel, rel_offset, max_rows;
     std::vector<LayerDev> lw;
@@ -176,6 +198,20 @@ struct ud_encoder {
     std::vector<GraphEntry> graphs;
     SubDev sub;
 };
+
+// Whether a rocprofiler-sdk tool is configured for this process (rocprofv3 exports these before it
+// starts the program).  Under such a tool the step is launched eagerly, never by hipGraph replay:
+// with the kernel tracer active, replaying the captured step ended the host process with a
+// SIGSEGV inside the tool's library -- a host memcpy reading a device-mapped address, reached from
+// hipGraphLaunch -- while the same kernels launched one by one trace normally.
+static bool profiler_tool_loaded() {
+    const char* names[] = {"ROCP_TOOL_LIBRARIES", "ROCPROFILER_LIBRARY_CTOR"};
+    for (const char* n : names) {
+        const char* v = getenv(n);
+        if (v && v[0]) return true;
+    }
+    return false;
+}
 
 static void* dev_alloc(size_t bytes) {
     void* p = nullptr;
@@ -240,7 +276,7 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
     e->n_rel = c.left_context + 2 * c.max_chunk - 1;
     e->max_rows = c.max_streams * c.max_chunk;
     const char* ev = getenv("UD_GRAPHS");
-    e->use_graphs = !(ev && ev[0] == '0');
+    e->use_graphs = !(ev && ev[0] == '0') && !profiler_tool_loaded();
     e->lw.resize(c.layers);
 
     const size_t D = e->D, ff = e->ff, esz = e->esz;
@@ -333,8 +369,12 @@ static int upload_matrix(ud_encoder* e, void* dst, size_t dst_row0, const float*
     if (e->bf) {
         std::vector<uint16_t> tmp(n);
         const int nk = (int)(cols / 64);
+        for (size_t i = 0; i < n; i++)
+            if (!(std::fabs(host_bf16_to_f(host_bf16(src[i]))) <= kHalfMax))
+                return fail(UD_ERR_WEIGHT, "weight value %g at element %zu is outside the IEEE-half range of a 16-bit encoder",
+                            (double)src[i], i);
         for (size_t r = 0; r < rows; r++)
-            for (size_t c = 0; c < cols; c++) tmp[frag_index((int64_t)r, (int)c, nk)] = host_bf16(src[r * cols + c]);
+            for (size_t c = 0; c < cols; c++) tmp[frag_index((int64_t)r, (int)c, nk)] = host_weight16(src[r * cols + c]);
         return upload(static_cast<uint16_t*>(dst) + dst_row0 * cols, tmp.data(), n * 2);
     }
     return upload(static_cast<float*>(dst) + dst_row0 * cols, src, n * 4);
@@ -512,7 +552,7 @@ extern "C" UD_API int ud_encoder_finalize(ud_encoder* e) {
                 rc = fail(UD_ERR_HIP, "ud_encoder_finalize: copy back failed");
                 break;
             }
-            for (size_t i = 0; i < P.size(); i++) Pb[i] = host_bf16(P[i]);
+            for (size_t i = 0; i < P.size(); i++) Pb[i] = host_f16(P[i]);
             rc = upload(l.P, Pb.data(), Pb.size() * 2);
         } else if (hipMemcpy(l.P, p_d, P.size() * 4, hipMemcpyDeviceToDevice) != hipSuccess) {
             rc = fail(UD_ERR_HIP, "ud_encoder_finalize: copy failed");
@@ -547,6 +587,10 @@ extern "C" UD_API int ud_stream_create(ud_encoder* e, ud_stream** out) {
     *out = nullptr;
     if (e->free_slots.empty()) return fail(UD_ERR_CAPACITY, "ud_stream_create: all %d stream slots in use", e->cfg.max_streams);
     int slot = e->free_slots.back();
+    // The slot may belong to a stream destroyed while a step on another (non-blocking) HIP stream
+    // was still committing its ring rows; wait for all device work before clearing it, or the new
+    // stream could start with the old one's rows.
+    HIPC(hipDeviceSynchronize());
     int rc = zero_slot(e, slot);
     if (rc != UD_OK) return rc;
     e->free_slots.pop_back();
@@ -654,7 +698,7 @@ static int enqueue_rows(ud_encoder* e, int s0, int n, int T, const float* x, flo
                     const char* what) -> int {
         GemmArgs g{};
         g.A = A; g.W = W; g.C = C; g.M = M; g.N = N; g.K = K; g.lda = K; g.ldw = K; g.ldc = ldc;
-        g.epi = epi; g.act = act; g.out_scale = scale; g.ksplit = 1;
+        g.epi = epi; g.act = act; g.out_scale = scale; g.ksplit = 1; g.f16 = bf ? 1 : 0;
         return launch_status(launch_gemm(g, bf, st), what);
     };
     // res += scale * A . W^T (N = D)
@@ -662,7 +706,7 @@ static int enqueue_rows(ud_encoder* e, int s0, int n, int T, const float* x, flo
         if (!bf) return gemm(A, W, w.res, D, K, D, EPI_RESID, ACT_NONE, scale, what);
         GemmArgs g{};
         g.A = A; g.W = W; g.C = w.part; g.M = M; g.N = D; g.K = K; g.lda = K; g.ldw = K; g.ldc = D;
-        g.epi = EPI_PARTIAL; g.act = ACT_NONE; g.out_scale = scale;
+        g.epi = EPI_PARTIAL; g.act = ACT_NONE; g.out_scale = scale; g.f16 = 1;
         g.ksplit = gemm_partial_splits(M, D, K, bf);
         pend.n = g.ksplit;
         return launch_status(launch_gemm(g, bf, st), what);
@@ -702,7 +746,7 @@ static int enqueue_rows(ud_encoder* e, int s0, int n, int T, const float* x, flo
         ConvArgs ca{};
         ca.pw = w.pw; ca.ring = e->cring + (size_t)li * e->cring_layer_elems; ca.w_t = l.dw_t;
         ca.ln_g = l.ln[6]; ca.ln_b = l.ln[7]; ca.z = w.z; ca.desc = w.desc;
-        ca.n = n; ca.T = T; ca.D = D; ca.K = e->Kc; ca.z_bf16 = bf;
+        ca.n = n; ca.T = T; ca.D = D; ca.K = e->Kc; ca.z16 = bf;
         LAUNCH(launch_dwconv_ln(ca, st), "depthwise conv");
         if ((rc = resid(w.z, l.pw2, D, 1.0f, "pointwise_conv2"))) return rc;
         // FF2: res += 0.5 * linear2(silu(linear1(LN(res))))
@@ -825,6 +869,13 @@ extern "C" UD_API int ud_encoder_subsample(ud_encoder* e, int32_t n, int32_t mel
                 return fail(UD_ERR_STATE, "ud_encoder_subsample: weight encoder.%s not set", kSubName[s]);
     }
     if (n < 1 || n > e->cfg.max_streams) return fail(UD_ERR_SHAPE, "ud_encoder_subsample: n = %d outside 1..%d", n, e->cfg.max_streams);
+    // The front-end workspace holds max_streams chunks of at most 8 max_chunk + 9 mel rows (every
+    // stage's length grows with the mel rows, so this bounds all of them); longer chunks are
+    // refused before anything is launched, whatever drop would leave.
+    const int max_mel = 8 * e->cfg.max_chunk + 9;
+    if (mel_rows > max_mel)
+        return fail(UD_ERR_SHAPE, "ud_encoder_subsample: %d mel rows exceed the %d this encoder's workspace holds "
+                    "(8 * max_chunk + 9)", mel_rows, max_mel);
     const int T0 = mel_rows, T1 = sub_len(T0), T2 = sub_len(T1), T3 = sub_len(T2);
     const int T = T3 - drop;
     if (mel_rows < 1 || drop < 0 || T < 1 || T > e->cfg.max_chunk)
@@ -949,7 +1000,7 @@ extern "C" UD_API int ud_time_layer_attention(ud_encoder* e, ud_stream* const* s
 extern "C" UD_API int ud_time_ring_read_floor(ud_encoder* e, ud_stream* const* streams, int32_t n, int32_t T,
                                               int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
                                               void* hip_stream, float* avg_ms) {
-    if (e && !e->bf) return fail(UD_ERR_INVALID, "ud_time_ring_read_floor: bf16 encoders only");
+    if (e && !e->bf) return fail(UD_ERR_INVALID, "ud_time_ring_read_floor: 16-bit encoders only");
     return time_layers(e, streams, n, T, layer, qkv_dev, att_dev, iters, hip_stream, avg_ms, "ud_time_ring_read_floor",
                        [](const RingArgs& a, hipStream_t st) { return launch_ring_read_floor(a, st); });
 }
@@ -980,11 +1031,11 @@ static int cache_io(ud_stream* s, int layer, float* k, float* v, float* conv, co
     std::vector<uint8_t> kr(per * e->esz), vr(per * e->esz);
     std::vector<float> cr(cper);
     auto get = [&](const std::vector<uint8_t>& buf, size_t i) -> float {
-        return e->bf ? host_bf16_to_f(reinterpret_cast<const uint16_t*>(buf.data())[i])
+        return e->bf ? host_f16_to_f(reinterpret_cast<const uint16_t*>(buf.data())[i])
                      : reinterpret_cast<const float*>(buf.data())[i];
     };
     auto put = [&](std::vector<uint8_t>& buf, size_t i, float x) {
-        if (e->bf) reinterpret_cast<uint16_t*>(buf.data())[i] = host_bf16(x);
+        if (e->bf) reinterpret_cast<uint16_t*>(buf.data())[i] = host_f16(x);
         else reinterpret_cast<float*>(buf.data())[i] = x;
     };
     if (!do_import) {
@@ -1034,6 +1085,43 @@ extern "C" UD_API int ud_stream_import_cache(ud_stream* s, int32_t layer, const 
     const int64_t cur = s->frames < e->L ? s->frames : e->L;
     if (cur != cache_len) s->frames = cache_len;
     return cache_io(s, layer, nullptr, nullptr, nullptr, k_host, v_host, conv_host, true);
+}
+
+// ---------------------------------------------------------------- offline key ranges
+
+// MaskSpec.ranges(T:) (FastConformer.swift:324-343) and chunkedLimitedRanges (:346-357), then the
+// clip of every range's end to the utterance's valid length (forwardOffline, :380-381), for B
+// utterances of T frames.  Only the end is clipped, as in the reference: a query whose chunk starts
+// past the valid length gets lo > hi, an empty range (output 0).
+extern "C" UD_API int ud_chunked_limited_ranges(int32_t kind, int32_t B, int32_t T, const int32_t* valid_host,
+                                                int32_t left, int32_t chunk, int32_t right, int32_t* ranges_host) {
+    if (!ranges_host) return fail(UD_ERR_INVALID, "ud_chunked_limited_ranges: null output");
+    if (B < 1 || T < 1) return fail(UD_ERR_SHAPE, "ud_chunked_limited_ranges: B = %d, T = %d", B, T);
+    if (left < 0 || right < 0) return fail(UD_ERR_SHAPE, "ud_chunked_limited_ranges: left %d, right %d", left, right);
+    int cs = 0, back = 0;
+    if (kind == UD_MASK_CHUNKED_LIMITED) {
+        cs = right + 1;                    // chunks of right + 1 frames, left / (right + 1) chunks back
+        back = left / cs * cs;
+    } else if (kind == UD_MASK_CHUNKED_LIMITED_RC) {
+        if (chunk < 1) return fail(UD_ERR_SHAPE, "ud_chunked_limited_ranges: chunk %d", chunk);
+        cs = chunk;                        // [c chunk - left, c chunk + chunk - 1 + right], inclusive
+        back = left;
+    } else {
+        return fail(UD_ERR_INVALID, "ud_chunked_limited_ranges: mask kind %d", kind);
+    }
+    const int extra = kind == UD_MASK_CHUNKED_LIMITED ? 0 : right;
+    for (int b = 0; b < B; b++) {
+        const int v = valid_host ? valid_host[b] : T;
+        int32_t* r = ranges_host + (size_t)b * T * 2;
+        for (int i = 0; i < T; i++) {
+            const int64_t c0 = (int64_t)(i / cs) * cs;
+            const int64_t lo = c0 - back, hi = c0 + cs + extra;
+            const int64_t end = hi < T ? hi : T;
+            r[2 * i] = (int32_t)(lo > 0 ? lo : 0);
+            r[2 * i + 1] = (int32_t)(end < v ? end : v);
+        }
+    }
+    return UD_OK;
 }
 
 // ---------------------------------------------------------------- single-op entry

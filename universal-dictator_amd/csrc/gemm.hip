@@ -143,9 +143,9 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
             } else if constexpr (EPI == EPI_STORE_F32) {
                 static_cast<float*>(a.C)[m * a.ldc + n] = apply_act(v, ACT) * a.out_scale;
             } else if constexpr (EPI == EPI_STORE_FRAG) {
-                static_cast<bf16*>(a.C)[frag_index(m, n, a.N / 64)] = f2bf(apply_act(v, ACT) * a.out_scale);
+                static_cast<uint16_t*>(a.C)[frag_index(m, n, a.N / 64)] = to16<H>(apply_act(v, ACT) * a.out_scale);
             } else {
-                static_cast<bf16*>(a.C)[m * a.ldc + n] = f2bf(apply_act(v, ACT) * a.out_scale);
+                static_cast<uint16_t*>(a.C)[m * a.ldc + n] = to16<H>(apply_act(v, ACT) * a.out_scale);
             }
         }
     };
@@ -345,8 +345,8 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
                 *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.C) + m * a.ldc + n) = o;
             } else {
                 uint2 o;
-                o.x = (uint32_t)f2bf(act_fast<ACT>(v[0]) * a.out_scale) | ((uint32_t)f2bf(act_fast<ACT>(v[1]) * a.out_scale) << 16);
-                o.y = (uint32_t)f2bf(act_fast<ACT>(v[2]) * a.out_scale) | ((uint32_t)f2bf(act_fast<ACT>(v[3]) * a.out_scale) << 16);
+                o.x = (uint32_t)to16<H>(act_fast<ACT>(v[0]) * a.out_scale) | ((uint32_t)to16<H>(act_fast<ACT>(v[1]) * a.out_scale) << 16);
+                o.y = (uint32_t)to16<H>(act_fast<ACT>(v[2]) * a.out_scale) | ((uint32_t)to16<H>(act_fast<ACT>(v[3]) * a.out_scale) << 16);
                 bf16* dst = static_cast<bf16*>(a.C) + (EPI == EPI_STORE_FRAG ? frag_index(m, n, a.N / 64) : m * a.ldc + n);
                 *reinterpret_cast<uint2*>(dst) = o;
             }
@@ -534,23 +534,23 @@ static int launch_lds_cfg(GemmArgs a, int ksplit, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-template <int NT, int EPI>
+template <int NT, int EPI, bool H>
 static int launch_lds_epi(const GemmArgs& a, int ks, hipStream_t st) {
     switch (a.act) {
-        case ACT_NONE: return launch_lds_cfg<NT, EPI, ACT_NONE>(a, ks, st);
-        case ACT_SILU: return launch_lds_cfg<NT, EPI, ACT_SILU>(a, ks, st);
-        case ACT_RELU: return launch_lds_cfg<NT, EPI, ACT_RELU>(a, ks, st);
+        case ACT_NONE: return launch_lds_cfg<NT, EPI, ACT_NONE, H>(a, ks, st);
+        case ACT_SILU: return launch_lds_cfg<NT, EPI, ACT_SILU, H>(a, ks, st);
+        case ACT_RELU: return launch_lds_cfg<NT, EPI, ACT_RELU, H>(a, ks, st);
         default: return -2;
     }
 }
 
-template <int NT>
+template <int NT, bool H>
 static int launch_lds_act(const GemmArgs& a, int ks, hipStream_t st) {
     switch (a.epi) {
-        case EPI_PARTIAL: return a.act == ACT_NONE ? launch_lds_cfg<NT, EPI_PARTIAL, ACT_NONE>(a, ks, st) : -2;
-        case EPI_STORE_F32: return launch_lds_epi<NT, EPI_STORE_F32>(a, ks, st);
-        case EPI_STORE_FRAG: return launch_lds_epi<NT, EPI_STORE_FRAG>(a, ks, st);
-        case EPI_STORE: return launch_lds_epi<NT, EPI_STORE>(a, ks, st);
+        case EPI_PARTIAL: return a.act == ACT_NONE ? launch_lds_cfg<NT, EPI_PARTIAL, ACT_NONE, H>(a, ks, st) : -2;
+        case EPI_STORE_F32: return launch_lds_epi<NT, EPI_STORE_F32, H>(a, ks, st);
+        case EPI_STORE_FRAG: return launch_lds_epi<NT, EPI_STORE_FRAG, H>(a, ks, st);
+        case EPI_STORE: return launch_lds_epi<NT, EPI_STORE, H>(a, ks, st);
         default: return -2;
     }
 }
@@ -602,11 +602,11 @@ int gemm_partial_splits(int M, int N, int K, bool bf16_data) {
     return K % (128 * KSPLIT) == 0 ? KSPLIT : 1;
 }
 
-template <int MT, int WK, int NT, int EPI>
+template <int MT, int WK, int NT, int EPI, bool H>
 static int launch_act(const GemmArgs& a, int ks, hipStream_t st) {
-    if (a.act == ACT_SILU) return launch_bf16_cfg<MT, WK, NT, EPI, ACT_SILU>(a, ks, st);
-    if (a.act == ACT_NONE) return launch_bf16_cfg<MT, WK, NT, EPI, ACT_NONE>(a, ks, st);
-    if (a.act == ACT_RELU) return launch_bf16_cfg<MT, WK, NT, EPI, ACT_RELU>(a, ks, st);
+    if (a.act == ACT_SILU) return launch_bf16_cfg<MT, WK, NT, EPI, ACT_SILU, H>(a, ks, st);
+    if (a.act == ACT_NONE) return launch_bf16_cfg<MT, WK, NT, EPI, ACT_NONE, H>(a, ks, st);
+    if (a.act == ACT_RELU) return launch_bf16_cfg<MT, WK, NT, EPI, ACT_RELU, H>(a, ks, st);
     return -2;
 }
 
@@ -644,32 +644,29 @@ static int launch_f16(const GemmArgs& a, hipStream_t st) {
     return launch_bf16_cfg<8, 2, 1, EPI_STORE_F32, ACT, true, true>(a, 1, st);
 }
 
-static int launch_bf16(const GemmArgs& a, int ks, hipStream_t st) {
-    if (a.f16) {
-        if (a.epi != EPI_STORE_F32 || ks != 1 || a.bias == nullptr) return -2;
-        if (a.act == ACT_NONE) return launch_f16<ACT_NONE>(a, st);
-        if (a.act == ACT_RELU) return launch_f16<ACT_RELU>(a, st);
-        return -2;
-    }
-    if (a.bias != nullptr) return -2;   // bf16 operands: the encoder's projections have no bias
+// The encoder's 16-bit projections: operands (and 16-bit outputs) IEEE half when H, bf16 otherwise;
+// no bias.
+template <bool H>
+static int launch_16(const GemmArgs& a, int ks, hipStream_t st) {
+    if (a.bias != nullptr) return -2;   // the encoder's projections have no bias
     if (a.M <= 128) {
         switch (a.epi) {
             case EPI_STORE_FRAG:
-                if (a.N % 64 == 0 && a.K % 512 == 0) return launch_act<2, 8, 4, EPI_STORE_FRAG>(a, ks, st);
-                if (a.N % 64 == 0) return launch_act<2, 2, 4, EPI_STORE_FRAG>(a, ks, st);
+                if (a.N % 64 == 0 && a.K % 512 == 0) return launch_act<2, 8, 4, EPI_STORE_FRAG, H>(a, ks, st);
+                if (a.N % 64 == 0) return launch_act<2, 2, 4, EPI_STORE_FRAG, H>(a, ks, st);
                 break;
             case EPI_STORE:
-                if (a.N % 32 == 0 && a.K % 512 == 0) return launch_act<4, 8, 2, EPI_STORE>(a, ks, st);
+                if (a.N % 32 == 0 && a.K % 512 == 0) return launch_act<4, 8, 2, EPI_STORE, H>(a, ks, st);
                 break;
             case EPI_STORE_F32:
-                if (a.N % 32 == 0 && a.K % 512 == 0) return launch_act<2, 8, 2, EPI_STORE_F32>(a, ks, st);
+                if (a.N % 32 == 0 && a.K % 512 == 0) return launch_act<2, 8, 2, EPI_STORE_F32, H>(a, ks, st);
                 break;
             case EPI_PARTIAL:
                 if (a.act != ACT_NONE) return -2;
                 if (a.N % 32 == 0 && a.K % (512 * ks) == 0)
-                    return a.K >= 4096 ? launch_bf16_cfg<4, 8, 2, EPI_PARTIAL, ACT_NONE>(a, ks, st)
-                                       : launch_bf16_cfg<2, 8, 2, EPI_PARTIAL, ACT_NONE>(a, ks, st);
-                if (a.K % (128 * ks) == 0) return launch_bf16_cfg<4, 2, 1, EPI_PARTIAL, ACT_NONE>(a, ks, st);
+                    return a.K >= 4096 ? launch_bf16_cfg<4, 8, 2, EPI_PARTIAL, ACT_NONE, H>(a, ks, st)
+                                       : launch_bf16_cfg<2, 8, 2, EPI_PARTIAL, ACT_NONE, H>(a, ks, st);
+                if (a.K % (128 * ks) == 0) return launch_bf16_cfg<4, 2, 1, EPI_PARTIAL, ACT_NONE, H>(a, ks, st);
                 break;
             default: return -2;   // the residual accumulate is an fp32-path epilogue
         }
@@ -678,19 +675,30 @@ static int launch_bf16(const GemmArgs& a, int ks, hipStream_t st) {
         const BigTile bt = big_tile(a.M, a.N, a.K, a.epi == EPI_PARTIAL);
         if (bt.nt != 0 && (a.epi != EPI_PARTIAL || bt.ks == ks)) {
             switch (bt.nt) {
-                case 4: return launch_lds_act<4>(a, ks, st);
-                case 3: return launch_lds_act<3>(a, ks, st);
-                default: return launch_lds_act<2>(a, ks, st);
+                case 4: return launch_lds_act<4, H>(a, ks, st);
+                case 3: return launch_lds_act<3, H>(a, ks, st);
+                default: return launch_lds_act<2, H>(a, ks, st);
             }
         }
     }
     switch (a.epi) {
-        case EPI_PARTIAL: return a.act == ACT_NONE ? launch_bf16_cfg<8, 2, 1, EPI_PARTIAL, ACT_NONE>(a, ks, st) : -2;
-        case EPI_STORE_F32: return launch_act<8, 2, 1, EPI_STORE_F32>(a, ks, st);
-        case EPI_STORE_FRAG: return launch_act<8, 2, 1, EPI_STORE_FRAG>(a, ks, st);
-        case EPI_STORE: return launch_act<8, 2, 1, EPI_STORE>(a, ks, st);
+        case EPI_PARTIAL: return a.act == ACT_NONE ? launch_bf16_cfg<8, 2, 1, EPI_PARTIAL, ACT_NONE, H>(a, ks, st) : -2;
+        case EPI_STORE_F32: return launch_act<8, 2, 1, EPI_STORE_F32, H>(a, ks, st);
+        case EPI_STORE_FRAG: return launch_act<8, 2, 1, EPI_STORE_FRAG, H>(a, ks, st);
+        case EPI_STORE: return launch_act<8, 2, 1, EPI_STORE, H>(a, ks, st);
         default: return -2;
     }
+}
+
+static int launch_bf16(const GemmArgs& a, int ks, hipStream_t st) {
+    if (a.f16 && a.bias != nullptr) {
+        // the subsampling front-end's GEMMs: IEEE half with a bias, fp32 out
+        if (a.epi != EPI_STORE_F32 || ks != 1) return -2;
+        if (a.act == ACT_NONE) return launch_f16<ACT_NONE>(a, st);
+        if (a.act == ACT_RELU) return launch_f16<ACT_RELU>(a, st);
+        return -2;
+    }
+    return a.f16 ? launch_16<true>(a, ks, st) : launch_16<false>(a, ks, st);
 }
 
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st) {

@@ -82,8 +82,8 @@ struct GemmArgs {
     int ksplit;                     // EPI_PARTIAL: K splits chosen by the caller (gemm_partial_splits)
     const float* bias;              // [N] added before the activation: fp32 path (optional) and the
                                     // IEEE-half path (required); not the bf16 path
-    int f16;                        // 16-bit path: operands are IEEE half instead of bf16
-                                    // (EPI_STORE_F32 with a bias only)
+    int f16;                        // 16-bit path: operands (and 16-bit outputs) are IEEE half
+                                    // instead of bf16
 };
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st);
 // fp32 GEMM for few rows (tens) on the fp32 MFMA: EPI_PARTIAL with ks K splits (slabs
@@ -108,13 +108,13 @@ struct Partials {
     int n;
 };
 // x <- x + sum(parts) (written back when parts.n > 0); out = act(LN(x; g, b)), fp32 row-major
-// or bf16 fragment-major.
-int launch_layernorm(float* x, Partials parts, const float* g, const float* b, void* out, bool out_bf16, int rows,
+// or (out16) IEEE half fragment-major.
+int launch_layernorm(float* x, Partials parts, const float* g, const float* b, void* out, bool out16, int rows,
                      int D, int act, hipStream_t st);
 // v = src + sum(parts); res <- LN_a(v) (v itself when ga == nullptr); z <- LN_b(res) (fp32
-// row-major or bf16 fragment-major).
+// row-major or (z16) IEEE half fragment-major).
 int launch_layernorm2(const float* src, Partials parts, float* res, const float* ga, const float* ba, const float* gb,
-                      const float* bb, void* z, bool z_bf16, int rows, int D, hipStream_t st);
+                      const float* bb, void* z, bool z16, int rows, int D, hipStream_t st);
 // GLU of pointwise_conv1's fp32 [n*T, 2D] output (value | gate) with the frame mask, causal
 // depthwise conv over [conv ring (K-1 rows) ; T new GLU rows], conv LayerNorm + SiLU; writes z
 // and the updated conv ring (which holds GLU rows).
@@ -123,10 +123,10 @@ struct ConvArgs {
     float* ring;                    // layer base of the conv pool: [slots][K-1][D]
     const float* w_t;               // [K][D] depthwise weights, tap-major
     const float* ln_g; const float* ln_b;
-    void* z;                        // [n*T, D]
+    void* z;                        // [n*T, D]: fp32 row-major, or IEEE half fragment-major (z16)
     const int32_t* desc;
     int n, T, D, K;
-    bool z_bf16;
+    bool z16;
 };
 int launch_dwconv_ln(const ConvArgs& a, hipStream_t st);
 

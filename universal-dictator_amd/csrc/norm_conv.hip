@@ -1,6 +1,7 @@
 // Row-wise kernels of the encoder step: LayerNorm (single and fused pair) and the conv module's
 // GLU + frame mask + causal depthwise conv + LayerNorm + SiLU, fused with the conv-cache ring.
-// bf16 outputs feed a GEMM and are written fragment-major (frag_index), fp32 outputs row-major.
+// 16-bit outputs (IEEE half, a 16-bit encoder's activation format) feed a GEMM and are written
+// fragment-major (frag_index); fp32 outputs row-major.
 //
 // LayerNorm semantics: Sources/DictatorEngine/Metal/20_conformer.metal:25-49 (two passes,
 // population variance, y = act((x-mean)*rsqrt(var+eps)*g + b)), eps 1e-5 (Core/Ops.swift:27).
@@ -52,12 +53,12 @@ __device__ __forceinline__ void ln_apply(float4 (&x)[NPER], const float4 (&gg)[N
     }
 }
 
-// Four consecutive columns c..c+3 (c % 4 == 0) of row `row`: bf16 fragment-major, 8 bytes.
+// Four consecutive columns c..c+3 (c % 4 == 0) of row `row`: IEEE half fragment-major, 8 bytes.
 __device__ __forceinline__ void store4_frag(void* out, int64_t row, int c, int D, float4 v) {
     uint2 u;
-    u.x = (uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16);
-    u.y = (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16);
-    *reinterpret_cast<uint2*>(static_cast<bf16*>(out) + frag_index(row, c, D / 64)) = u;
+    u.x = (uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16);
+    u.y = (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + frag_index(row, c, D / 64)) = u;
 }
 
 template <int NPER>
@@ -106,7 +107,7 @@ __device__ __forceinline__ void load_row(float4 (&v)[NPER], const float* __restr
 
 template <int NPER, int NP>
 __global__ __launch_bounds__(256) void layernorm_kernel(float* x, Partials parts, const float* __restrict__ g,
-                                                        const float* __restrict__ b, void* out, int out_bf16, int rows,
+                                                        const float* __restrict__ b, void* out, int out16, int rows,
                                                         int D, int act) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -118,7 +119,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(float* x, Partials parts
     float mean, rstd;
     ln_row_stats(v, D, mean, rstd);
     ln_apply(v, gg, bb, mean, rstd, act);
-    store_row(out, out_bf16 != 0, row, D, v, lane);
+    store_row(out, out16 != 0, row, D, v, lane);
 }
 
 // res <- LN_a(src) (copy when ga is null), z <- LN_b(res).  Joins one layer's norm_out with the
@@ -127,7 +128,7 @@ template <int NPER, int NP>
 __global__ __launch_bounds__(256) void layernorm2_kernel(const float* src, Partials parts, float* res,
                                                          const float* __restrict__ ga, const float* __restrict__ ba,
                                                          const float* __restrict__ gb, const float* __restrict__ bb,
-                                                         void* z, int z_bf16, int rows, int D) {
+                                                         void* z, int z16, int rows, int D) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(256) void layernorm2_kernel(const float* src, Parti
     store_row(res, false, row, D, v, lane);
     ln_row_stats(v, D, mean, rstd);
     ln_apply(v, g2, b2, mean, rstd, ACT_NONE);
-    store_row(z, z_bf16 != 0, row, D, v, lane);
+    store_row(z, z16 != 0, row, D, v, lane);
 }
 
 // The conv module after pointwise_conv1 (FastConformer.swift:298-306): GLU over channels,
@@ -256,7 +257,7 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
             y.z = silu((o[t].z - mean[t]) * rstd * gg.z + bb.z);
             y.w = silu((o[t].w - mean[t]) * rstd * gg.w + bb.w);
             const int64_t row = (int64_t)s * T + t;
-            if (a.z_bf16) {
+            if (a.z16) {
                 store4_frag(a.z, row, c0, D, y);
             } else {
                 *reinterpret_cast<float4*>(static_cast<float*>(a.z) + row * D + c0) = y;
@@ -281,12 +282,12 @@ static void ln_dispatch(dim3 grid, dim3 block, hipStream_t st, float* x, Partial
     else hipLaunchKernelGGL((layernorm_kernel<NPER, -1>), grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act);
 }
 
-int launch_layernorm(float* x, Partials parts, const float* g, const float* b, void* out, bool out_bf16, int rows,
+int launch_layernorm(float* x, Partials parts, const float* g, const float* b, void* out, bool out16, int rows,
                      int D, int act, hipStream_t st) {
     if (rows <= 0) return 0;
     const int rpb = ln_rows_per_block(rows);
     dim3 grid((rows + rpb - 1) / rpb), block(64 * rpb);
-    const int ob = out_bf16 ? 1 : 0;
+    const int ob = out16 ? 1 : 0;
     switch (D) {
         case 256: ln_dispatch<1>(grid, block, st, x, parts, g, b, out, ob, rows, D, act); break;
         case 512: ln_dispatch<2>(grid, block, st, x, parts, g, b, out, ob, rows, D, act); break;
@@ -308,11 +309,11 @@ static void ln2_dispatch(dim3 grid, dim3 block, hipStream_t st, const float* src
 }
 
 int launch_layernorm2(const float* src, Partials parts, float* res, const float* ga, const float* ba, const float* gb,
-                      const float* bb, void* z, bool z_bf16, int rows, int D, hipStream_t st) {
+                      const float* bb, void* z, bool z16, int rows, int D, hipStream_t st) {
     if (rows <= 0) return 0;
     const int rpb = ln_rows_per_block(rows);
     dim3 grid((rows + rpb - 1) / rpb), block(64 * rpb);
-    const int zb = z_bf16 ? 1 : 0;
+    const int zb = z16 ? 1 : 0;
     switch (D) {
         case 256: ln2_dispatch<1>(grid, block, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;
         case 512: ln2_dispatch<2>(grid, block, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D); break;

@@ -1,5 +1,5 @@
-// Shared device helpers for the gfx950 encoder-step kernels: bf16 storage, wave64 reductions,
-// vector loads, activations.
+// Shared device helpers for the gfx950 encoder-step kernels: bf16 and IEEE-half storage, wave64
+// reductions, vector loads, activations.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -36,14 +36,26 @@ __device__ __forceinline__ f16x8_t as_f16x8(uint4 v) {
     return r;
 }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+// A 16-bit operand value: IEEE half when H, bf16 otherwise (round to nearest even either way).
+template <bool H> __device__ __forceinline__ uint16_t to16(float f) {
+    if constexpr (H) return f2h(f);
+    else return f2bf(f);
+}
+
+// Element types of the attention kernels: fp32, bf16 (uint16_t storage) and IEEE half (_Float16,
+// the 16-bit format of a 16-bit encoder's activations, caches and tables).
+typedef _Float16 f16;
 
 template <typename T> __device__ __forceinline__ float to_f(T v);
 template <> __device__ __forceinline__ float to_f<float>(float v) { return v; }
 template <> __device__ __forceinline__ float to_f<bf16>(bf16 v) { return bf2f(v); }
+template <> __device__ __forceinline__ float to_f<f16>(f16 v) { return (float)v; }
 
 template <typename T> __device__ __forceinline__ T from_f(float v);
 template <> __device__ __forceinline__ float from_f<float>(float v) { return v; }
 template <> __device__ __forceinline__ bf16 from_f<bf16>(float v) { return f2bf(v); }
+template <> __device__ __forceinline__ f16 from_f<f16>(float v) { return (f16)v; }
 
 // SiLU x * sigmoid(x) (00_common.metal:25).
 // SiLU and the logistic function with v_exp_f32 and v_rcp_f32 (about 1 ulp each) instead of an
@@ -63,6 +75,7 @@ __device__ __forceinline__ float apply_act(float x, int act) {
 template <typename T> struct Vec16;
 template <> struct Vec16<float> { static constexpr int N = 4; };
 template <> struct Vec16<bf16> { static constexpr int N = 8; };
+template <> struct Vec16<f16> { static constexpr int N = 8; };
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
@@ -78,6 +91,12 @@ template <> __device__ __forceinline__ void unpack16<bf16>(uint4 v, float* f) {
     f[2] = __uint_as_float(v.y << 16); f[3] = __uint_as_float(v.y & 0xffff0000u);
     f[4] = __uint_as_float(v.z << 16); f[5] = __uint_as_float(v.z & 0xffff0000u);
     f[6] = __uint_as_float(v.w << 16); f[7] = __uint_as_float(v.w & 0xffff0000u);
+}
+template <> __device__ __forceinline__ void unpack16<f16>(uint4 v, float* f) {
+    f[0] = h2f((uint16_t)v.x); f[1] = h2f((uint16_t)(v.x >> 16));
+    f[2] = h2f((uint16_t)v.y); f[3] = h2f((uint16_t)(v.y >> 16));
+    f[4] = h2f((uint16_t)v.z); f[5] = h2f((uint16_t)(v.z >> 16));
+    f[6] = h2f((uint16_t)v.w); f[7] = h2f((uint16_t)(v.w >> 16));
 }
 
 // DPP lane moves within 16-lane rows.
