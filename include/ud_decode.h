@@ -48,6 +48,24 @@ UD_API int ud_gqa_attention_paged(int32_t kv_dtype, const float* q_dev, const vo
                                   int32_t block_size, int32_t max_keys, void* workspace, size_t workspace_bytes,
                                   void* hip_stream);
 
+/* Allocation-free variant of ud_gqa_attention_paged.  It has no counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * ud_gqa_attention_paged, minus the workspace: the split partials go to a static device array of
+ * UD_GQA_NOALLOC_SCRATCH_BYTES per device, held until the process ends (its address is looked up
+ * on the first call on each device).  The call allocates and frees nothing.
+ * Limit: ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys) <= UD_GQA_NOALLOC_SCRATCH_BYTES
+ * (e.g. 64 sequences x 32 query heads x 4096 keys at head_dim 128 use 32.5 MiB); larger calls
+ * return UD_ERR_SHAPE before anything is launched.  Every call on one device shares that device's
+ * array: calls that overlap on one device (on different HIP streams, or from several threads)
+ * race and must be serialised by the caller.  Nothing in the array needs to start at zero. */
+#define UD_GQA_NOALLOC_SCRATCH_BYTES (40u << 20)
+UD_API int ud_gqa_attention_paged_noalloc(int32_t kv_dtype, const float* q_dev, const void* k_pages,
+                                          const void* v_pages, const int32_t* block_table, int32_t max_blocks,
+                                          const int32_t* ranges_dev, float* out_dev, int32_t n, int32_t q_heads,
+                                          int32_t kv_heads, int32_t head_dim, int32_t block_size, int32_t max_keys,
+                                          void* hip_stream);
+
 /* Replaces Step.rope (Ops.swift rope) / rope_rotate_half (30_voxtral.metal:20-36): in place on
  * x [rows, ld] (dtype UD_F32, UD_BF16 or UD_F16), heads H of head_dim d starting at column 0:
  *   angle = pos(t) * inv_freq[i];  x_i' = x_i cos - x_{i+d/2} sin;  x_{i+d/2}' = x_{i+d/2} cos + x_i sin

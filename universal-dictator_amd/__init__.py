@@ -93,6 +93,8 @@ def _sig(lib):
         "ud_gqa_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32]),
         "ud_gqa_attention_paged": (i, [_i32, p, p, p, p, _i32, p, p, _i32, _i32, _i32, _i32, _i32, _i32, p,
                                        ctypes.c_size_t, p]),
+        "ud_gqa_attention_paged_noalloc": (i, [_i32, p, p, p, p, _i32, p, p, _i32, _i32, _i32, _i32, _i32, _i32,
+                                               p]),
         "ud_rope_rotate_half": (i, [_i32, p, _i32, _i32, _i32, _i32, p, _i32, p, p]),
         "ud_paged_kv_append": (i, [_i32, p, p, p, p, p, _i32, p, _i32, _i32, _i32, _i32, p]),
         "ud_encoder_get_config": (i, [p, ctypes.POINTER(_Config)]),
@@ -516,6 +518,20 @@ def gqa_attention_paged(q, k_pages, v_pages, block_table, max_blocks, ranges, ou
                                         max_blocks, ranges.ptr, out.ptr, n, q_heads, kv_heads, head_dim, block_size,
                                         max_keys, workspace.ptr, workspace.nbytes,
                                         hip_stream.ptr if hip_stream else None))
+
+
+# Static scratch of ud_gqa_attention_paged_noalloc (UD_GQA_NOALLOC_SCRATCH_BYTES in ud_decode.h).
+GQA_NOALLOC_SCRATCH_BYTES = 40 << 20
+
+
+def gqa_attention_paged_noalloc(q, k_pages, v_pages, block_table, max_blocks, ranges, out, n, q_heads, kv_heads,
+                                head_dim, max_keys, kv_dtype="bf16", block_size=16, hip_stream=None):
+    """gqa_attention_paged without a workspace: the split partials live in the library's static
+    per-device scratch, so the call allocates nothing (calls overlapping on one device race)."""
+    _check(lib().ud_gqa_attention_paged_noalloc(_DTYPES[kv_dtype], q.ptr, k_pages.ptr, v_pages.ptr,
+                                                block_table.ptr, max_blocks, ranges.ptr, out.ptr, n, q_heads,
+                                                kv_heads, head_dim, block_size, max_keys,
+                                                hip_stream.ptr if hip_stream else None))
 
 
 def rope_rotate_half(x, rows, heads, head_dim, ld, inv_freq, positions=None, pos0=0, dtype="f32", hip_stream=None):

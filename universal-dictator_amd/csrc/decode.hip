@@ -21,6 +21,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "../../include/ud_decode.h"
 #include "ud_common.hpp"
@@ -437,6 +438,58 @@ extern "C" UD_API int ud_gqa_attention_paged(int32_t kv_dtype, const float* q_de
     if ((uintptr_t)workspace & 15) return dfail(UD_ERR_INVALID, "%s: workspace must be 16-byte aligned", who);
     return gqa_launch(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, q_heads,
                       kv_heads, head_dim, max_keys, static_cast<float*>(workspace), static_cast<hipStream_t>(hip_stream));
+}
+
+// ---------------------------------------------------------------- allocation-free variant
+// The split partials of ud_gqa_attention_paged_noalloc live in this file-scope device array, one
+// copy per device, held until the process ends.  In host code `scratch` names a host-side stand-in,
+// not device memory: kernels get the address that hipGetSymbolAddress returned for the current
+// device (kept per device below), never the array's name.  No clearing is needed: the combine
+// kernel reads only the splits holding a key of the sequence's range, and the split kernel of each
+// of them writes its whole partial first (same stream).  Calls that overlap on one device race on
+// these bytes.
+static __device__ __align__(256) float scratch[UD_GQA_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_dev[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (looked up once per device, with that device current).
+static int scratch_of_current_device(const char* who, float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return dfail(UD_ERR_HIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return dfail(UD_ERR_HIP, "%s: device %d beyond %d", who, dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return dfail(UD_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", who, hipGetErrorString(e));
+        g_scratch_dev[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_dev[dev];
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_gqa_attention_paged_noalloc(int32_t kv_dtype, const float* q_dev, const void* k_pages,
+                                                     const void* v_pages, const int32_t* block_table,
+                                                     int32_t max_blocks, const int32_t* ranges_dev, float* out_dev,
+                                                     int32_t n, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                                                     int32_t block_size, int32_t max_keys, void* hip_stream) {
+    static const char* who = "ud_gqa_attention_paged_noalloc";
+    int rc = gqa_check(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, q_heads,
+                       kv_heads, head_dim, block_size, max_keys);
+    if (rc != UD_OK) return rc;
+    const size_t need = ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys);
+    if (need > (size_t)UD_GQA_NOALLOC_SCRATCH_BYTES)
+        return dfail(UD_ERR_SHAPE, "%s: %d sequences x %d heads x %d keys need %zu bytes of split partials, beyond the "
+                     "%zu-byte static scratch (UD_GQA_NOALLOC_SCRATCH_BYTES); use ud_gqa_attention_paged with a "
+                     "workspace", who, n, q_heads, max_keys, need, (size_t)UD_GQA_NOALLOC_SCRATCH_BYTES);
+    float* ws = nullptr;
+    if ((rc = scratch_of_current_device(who, &ws)) != UD_OK) return rc;
+    return gqa_launch(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, q_heads,
+                      kv_heads, head_dim, max_keys, ws, static_cast<hipStream_t>(hip_stream));
 }
 
 extern "C" UD_API int ud_rope_rotate_half(int32_t dtype, void* x_dev, int32_t rows, int32_t heads, int32_t head_dim,
