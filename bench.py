@@ -8,9 +8,11 @@ plus the 9-row pre-encode cache) through the causal dw_striding 8x subsampling w
 then 24 conformer layers (bf16 weights/activations, fp32 accumulation), with inputs already in HBM
 and full 70-frame caches seeded from N(0,1).  Default workload: 64 streams x 2 frames (25 mel rows
 in, 160 ms of audio per stream per step).  Prints one JSON
-line: aggregate streamed audio-seconds per second, the fused attention kernel's achieved HBM
-bandwidth against 8 TB/s (HIP events on the kernel's own stream), and the CPU oracle's throughput
-on a bounded sample timed on this host.
+line: aggregate streamed audio-seconds per second, per-step latency percentiles, the fused
+attention kernel's achieved HBM bandwidth against 8 TB/s and against the HBM read peak measured in
+the same run (HIP events on the kernel's own stream), each projection GEMM's MFMA throughput
+against the nominal and the measured peak, and the CPU oracle's throughput on a bounded sample
+timed on this host's cores.
 
 --workload chunk14 runs the same step at 256 streams x 14 frames.  --workload decode measures the
 decoder's paged grouped-query attention instead: 64 sequences x 1 new token, 32 query / 8 kv heads
@@ -74,41 +76,106 @@ def read_traffic(kernel_tag):
     return None
 
 
-def cpu_baseline(lw, sw, cfg, S, T, budget_s, threads):
-    """The oracle's encodeStreamStep (fp32, OpenMP) on this host: whole steps of the same workload
-    (subsampling of every stream's mel chunk, then all layers for all S streams) until about
-    budget_s seconds have passed."""
+def host_cpu():
+    """The host's CPUs as this job sees them: model, nproc, the CPUs in this process's affinity
+    mask, the physical cores among them, the cgroup CPU quota, and the OpenMP thread count the
+    environment grants (OMP_NUM_THREADS).  The baseline uses every physical core the job may run
+    on: the smallest of the affine physical cores, the quota and the granted thread count."""
+    info = {"model": None, "nproc": os.cpu_count()}
+    cores = {}
+    try:
+        cur = {}
+        for line in open("/proc/cpuinfo"):
+            if ":" in line:
+                k, v = [x.strip() for x in line.split(":", 1)]
+                cur[k] = v
+                if k == "model name" and info["model"] is None:
+                    info["model"] = v
+            elif cur:
+                if "processor" in cur:
+                    cores[int(cur["processor"])] = (cur.get("physical id", "0"), cur.get("core id", cur["processor"]))
+                cur = {}
+        if cur and "processor" in cur:
+            cores[int(cur["processor"])] = (cur.get("physical id", "0"), cur.get("core id", cur["processor"]))
+    except OSError:
+        pass
+    aff = sorted(os.sched_getaffinity(0))
+    info["affinity_cpus"] = len(aff)
+    info["affinity_physical_cores"] = len({cores[c] for c in aff if c in cores}) or len(aff)
+    quota = None
+    try:
+        q, per = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) / int(per)))
+    except (OSError, ValueError):
+        pass
+    info["cgroup_cpu_quota"] = quota
+    granted = os.environ.get("OMP_NUM_THREADS")
+    info["omp_num_threads_env"] = int(granted) if granted and granted.isdigit() else None
+    threads = info["affinity_physical_cores"]
+    for lim in (quota, info["omp_num_threads_env"]):
+        if lim:
+            threads = min(threads, lim)
+    info["threads"] = max(1, threads)
+    return info
+
+
+def load_oracle(threads):
+    """The oracle (test infrastructure, the CPU baseline here), with OpenMP threads bound close to
+    one physical core each; the binding is read when the OpenMP runtime loads with the oracle."""
+    os.environ["OMP_PROC_BIND"] = "close"
+    os.environ["OMP_PLACES"] = "cores"
     sys.path.insert(0, ROOT)
     from oracle import oracle as orc
     orc.set_threads(threads)
+    return orc
+
+
+def timed_median(fn, budget_s, min_steps=5, max_steps=60, warm=1):
+    """Median seconds of fn over >= min_steps timed calls after `warm` untimed ones, until about
+    budget_s has passed; returns (median, n, total seconds)."""
+    for _ in range(warm):
+        fn()
+    ts = []
+    t_all = time.perf_counter()
+    while len(ts) < min_steps or (time.perf_counter() - t_all < budget_s and len(ts) < max_steps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), len(ts), time.perf_counter() - t_all
+
+
+def cpu_baseline(lw, sw, cfg, S, T, budget_s, cpu, S_sample=None):
+    """The oracle's encodeStreamStep (fp32, OpenMP) on this host: whole steps of the same workload
+    (subsampling of every stream's mel chunk, then all layers) over S_sample of the S streams (all
+    when None), the median of >= 5 timed steps after one warm-up step."""
+    threads = cpu["threads"]
+    orc = load_oracle(threads)
+    Sn = S_sample or S
     model = orc.Model(lw, cfg.d_model, cfg.heads, cfg.ff_dim, cfg.conv_kernel)
     model.prepare(-(T - 1), cfg.left_context + T - 1)
     rng = np.random.default_rng(5)
     L, D = cfg.left_context, cfg.d_model
-    kc = rng.standard_normal((S, cfg.layers, L, D), dtype=np.float32)
-    vc = rng.standard_normal((S, cfg.layers, L, D), dtype=np.float32)
-    cc = rng.standard_normal((S, cfg.layers, cfg.conv_kernel - 1, D), dtype=np.float32)
-    cl = np.full(S, L, np.int32)
+    kc = rng.standard_normal((Sn, cfg.layers, L, D), dtype=np.float32)
+    vc = rng.standard_normal((Sn, cfg.layers, L, D), dtype=np.float32)
+    cc = rng.standard_normal((Sn, cfg.layers, cfg.conv_kernel - 1, D), dtype=np.float32)
+    cl = np.full(Sn, L, np.int32)
     rows = mel_rows(T)
-    mel = rng.standard_normal((S, rows, 128), dtype=np.float32)
-    valid = np.full(S, T, np.int32)
+    mel = rng.standard_normal((Sn, rows, 128), dtype=np.float32)
+    valid = np.full(Sn, T, np.int32)
 
     def step():
-        x = np.stack([orc.subsample(mel[s], rows, sw)[2:] for s in range(S)])
+        x = np.stack([orc.subsample(mel[s], rows, sw)[2:] for s in range(Sn)])
         orc.stream_step(model, x, valid, kc, vc, cc, cl)
 
-    step()                                                    # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        step()
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or n >= 50:
-            break
-    step_s = el / n
-    return dict(value=round(S * T * FRAME_SEC / step_s, 3), unit="audio-sec/sec", cores=threads, kind="port",
-                sample="%d full steps (%d streams x %d mel rows -> %d frames, %d layers, fp32) in %.1f s; "
-                       "%.3f s/step" % (n, S, rows, T, cfg.layers, el, step_s))
+    med, n, el = timed_median(step, budget_s)
+    return dict(value=round(Sn * T * FRAME_SEC / med, 3), unit="audio-sec/sec", cores=threads, kind="port",
+                threads=threads, cpu_model=cpu["model"], nproc=cpu["nproc"], affinity_cpus=cpu["affinity_cpus"],
+                affinity_physical_cores=cpu["affinity_physical_cores"], cgroup_cpu_quota=cpu["cgroup_cpu_quota"],
+                omp_num_threads_env=cpu["omp_num_threads_env"], omp_proc_bind="close", statistic="median",
+                sample="%s%d streams x %d mel rows -> %d frames, %d layers, fp32: median of %d whole steps "
+                       "(after 1 warm-up), %.3f s/step, %.1f s in all"
+                       % ("%d of the " % Sn if Sn != S else "", S, rows, T, cfg.layers, n, med, el))
 
 
 def mel_rows(T):
@@ -184,10 +251,9 @@ def decode_bench(ud, args):
                      "algorithmic_bytes_per_launch": algo},
     }
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
-        sys.path.insert(0, ROOT)
-        from oracle import oracle as orc
-        orc.set_threads(threads)
+        cpu = host_cpu()
+        threads = cpu["threads"]
+        orc = load_oracle(threads)
         log("cpu baseline: oracle attention on %d threads, ~%.0f s" % (threads, args.cpu_seconds))
         done, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < args.cpu_seconds and done < n:
@@ -199,6 +265,7 @@ def decode_bench(ud, args):
             done += 1
         el = time.perf_counter() - t0
         result["cpu_baseline"] = {"value": round(done / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+                                  "cpu_model": cpu["model"], "nproc": cpu["nproc"], "omp_proc_bind": "close",
                                   "sample": "%d of the %d sequences (one token each, all heads) in %.1f s, "
                                             "including the page gather" % (done, n, el)}
     print(json.dumps(result), flush=True)
@@ -219,8 +286,8 @@ def offline_bench(ud, args):
     P = ud.DeviceBuffer.from_numpy(bits((rng.standard_normal((n_rel, D)) * 0.5).astype(np.float32)))
     u = ud.DeviceBuffer.from_numpy((rng.standard_normal((H, dk)) * 0.02).astype(np.float32))
     vb = ud.DeviceBuffer.from_numpy((rng.standard_normal((H, dk)) * 0.02).astype(np.float32))
-    ranges_h = np.zeros((B, T, 2), np.int32)
-    ranges_h[:, :, 1] = lens[:, None]
+    # key padding: full context is one chunk of T frames, clipped to each utterance's valid length
+    ranges_h = ud.chunked_limited_ranges(T, T, T - 1, valid=lens)
     ranges = ud.DeviceBuffer.from_numpy(ranges_h)
     out = ud.DeviceBuffer(B * T * D * 2)
     hs = ud.HipStream()
@@ -258,10 +325,9 @@ def offline_bench(ud, args):
                      "algorithmic_flops_per_launch": flops_dense, "valid_key_flops_per_launch": flops_valid},
     }
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
-        sys.path.insert(0, ROOT)
-        from oracle import oracle as orc
-        orc.set_threads(threads)
+        cpu = host_cpu()
+        threads = cpu["threads"]
+        orc = load_oracle(threads)
         log("cpu baseline: oracle attention on %d threads, ~%.0f s" % (threads, args.cpu_seconds))
         qh = ud.round_bf16(rng.standard_normal((T, D)).astype(np.float32))
         kh = ud.round_bf16(rng.standard_normal((T, D)).astype(np.float32))
@@ -275,7 +341,8 @@ def offline_bench(ud, args):
             rows += 64
         el = time.perf_counter() - t0
         result["cpu_baseline"] = {"value": round(rows / el, 2), "unit": "frames/s (one layer, all heads)",
-                                  "cores": threads, "kind": "port",
+                                  "cores": threads, "kind": "port", "cpu_model": cpu["model"], "nproc": cpu["nproc"],
+                                  "omp_proc_bind": "close",
                                   "sample": "%d query frames of one %d-frame utterance (%d valid keys) in %.1f s"
                                             % (rows, T, lens[0], el)}
     print(json.dumps(result), flush=True)
@@ -551,12 +618,55 @@ def main():
     audio_per_step = S * T * FRAME_SEC
     value = audio_per_step / (ms_per_step / 1000.0)
     log("timed %d steps: %.4f ms/step (wall %.1f ms, events %.1f ms)" % (args.steps, ms_per_step, wall_ms, gpu_ms))
+
+    # Per-step latency, as the reference reports it (p50 / p99 per step, NemotronStreamer.swift:54-64,
+    # docs/PERF_LOG.md:26-28): HIP events around every step of a back-to-back run, and the host wall
+    # clock of a step launched and waited for on its own.
+    nlat = max(100, args.steps // 2)
+    evs = [(ud.Event(), ud.Event()) for _ in range(nlat)]
+    ud.synchronize()
+    for a0, a1 in evs:
+        a0.record(hs)
+        step()
+        a1.record(hs)
+    hs.synchronize()
+    lat = np.array([a0.elapsed_ms(a1) for a0, a1 in evs])
+    sync_lat = []
+    for _ in range(nlat):
+        t0 = time.perf_counter()
+        step()
+        hs.synchronize()
+        sync_lat.append((time.perf_counter() - t0) * 1000.0)
+    sync_lat = np.array(sync_lat)
+    pct = lambda a: {"p50": round(float(np.percentile(a, 50)), 4), "p99": round(float(np.percentile(a, 99)), 4),
+                     "mean": round(float(a.mean()), 4), "max": round(float(a.max()), 4), "n": int(len(a))}
+    log("step latency: events p50 %.4f p99 %.4f ms; launch+wait p50 %.4f p99 %.4f ms"
+        % (np.percentile(lat, 50), np.percentile(lat, 99), np.percentile(sync_lat, 50), np.percentile(sync_lat, 99)))
     parts = max(20, args.steps // 4)
     fw, fg = timed(lambda: enc.subsample(S, mel, x, drop=2, mel_rows=rows, hip_stream=hs), parts)
     valid = np.full(S, T, np.int32)
     lw_, lg = timed(lambda: enc.encode_stream_step(streams, x, out, valid=valid, T=T, hip_stream=hs), parts)
     front_ms, layers_ms = max(fw, fg) / parts, max(lw_, lg) / parts
     log("parts: subsampling %.4f ms, 24 layers %.4f ms" % (front_ms, layers_ms))
+
+    # Measured peaks of this device (same run), then the projections' MFMA use at this step's rows.
+    hbm_read, hbm_copy = ud.measure_hbm(4 << 30, 10, hip_stream=hs)
+    mfma_f16, mfma_bf16 = ud.measure_mfma(20000, hip_stream=hs)
+    log("measured peaks: HBM read %.0f GB/s, copy %.0f GB/s; MFMA f16 %.0f, bf16 %.0f TFLOP/s"
+        % (hbm_read, hbm_copy, mfma_f16, mfma_bf16))
+    rows_step = S * T
+    per_layer = {"ff_linear1": 2, "ff_linear2": 2, "qkv": 1, "linear_out": 1, "pointwise_conv1": 1, "pointwise_conv2": 1}
+    proj = {}
+    tot_fl = tot_ms = 0.0
+    for idx, name in enumerate(ud.Encoder.PROJECTIONS):
+        pms, pfl = enc.time_projection(idx, rows_step, 96, hip_stream=hs)
+        tf = pfl / (pms / 1000.0) / 1e12
+        proj[name] = {"us": round(pms * 1000.0, 3), "tflops": round(tf, 1),
+                      "frac_nominal": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "frac_measured": round(tf / mfma_f16, 4)}
+        tot_fl += per_layer[name] * pfl
+        tot_ms += per_layer[name] * pms
+        log("projection %-16s %8.2f us  %7.1f TFLOP/s" % (name, pms * 1000.0, tf))
+    proj_tf = tot_fl / (tot_ms / 1000.0) / 1e12
 
     # The fused attention kernel alone, on the stream it is launched on.
     qkv = ud.DeviceBuffer.from_numpy(ud.f16_bits(rng.standard_normal((S * T, 3 * D), dtype=np.float32)))
@@ -595,6 +705,18 @@ def main():
         },
         "subsampling_ms_per_step": round(front_ms, 5),
         "layers_ms_per_step": round(layers_ms, 5),
+        "step_latency_ms": dict(pct(lat), method="HIP events around each step of a back-to-back run"),
+        "sync_step_latency_ms": dict(pct(sync_lat), method="host wall clock of one step launched and waited for"),
+        "measured_peaks": {"hbm_read_gbs": round(hbm_read, 1), "hbm_copy_gbs": round(hbm_copy, 1),
+                           "mfma_f16_tflops": round(mfma_f16, 1), "mfma_bf16_tflops": round(mfma_bf16, 1),
+                           "method": "ud_measure_hbm (4 GiB buffers x 10, non-temporal streaming) and ud_measure_mfma "
+                                     "(v_mfma_f32_32x32x16 register chains) in this run"},
+        "mfma_utilisation": {
+            "rows": rows_step, "projections": proj,
+            "layer_tflops": round(proj_tf, 1), "frac_nominal": round(proj_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "frac_measured": round(proj_tf / mfma_f16, 4),
+            "note": "the seven projections of a layer (ff linear1/linear2 twice), each timed as the step "
+                    "launches it (ud_time_projection, weights from HBM), f16 operands with bf16-valued weights"},
         "realtime_factor": round(value, 2),
         "attention_steps_per_sec": round(1000.0 / attn_ms, 1),
         "attention_us_per_launch": round(attn_ms * 1000.0, 3),
@@ -606,6 +728,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "measured_peak": round(hbm_read, 1),
+            "frac_measured": round(achieved / hbm_read, 4),
             "traffic": read_traffic("relpos_ring_%s" % args.workload),
             "algorithmic_bytes_per_launch": attn_bytes,
             "read_floor_us": round(floor_ms * 1000.0, 3) if floor_ms else None,
@@ -614,9 +738,12 @@ def main():
     }
     enc.close()
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
-        log("cpu baseline: oracle on %d threads, ~%.0f s" % (threads, args.cpu_seconds))
-        result["cpu_baseline"] = cpu_baseline(lw, sw, cfg, S, T, args.cpu_seconds, threads)
+        cpu = host_cpu()
+        # a bounded sample: all 64 streams at 2-frame chunks (about 0.7 s per step on 16 cores); at
+        # 14-frame chunks the streams of about 256 rows (18 of the 256)
+        S_sample = S if S * T <= 256 else max(1, 256 // T)
+        log("cpu baseline: oracle on %d threads (%s), ~%.0f s" % (cpu["threads"], cpu["model"], args.cpu_seconds))
+        result["cpu_baseline"] = cpu_baseline(lw, sw, cfg, S, T, args.cpu_seconds, cpu, S_sample=S_sample)
     print(json.dumps(result), flush=True)
 
 

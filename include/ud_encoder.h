@@ -248,6 +248,23 @@ UD_API int ud_time_ring_read_floor(ud_encoder* enc, ud_stream* const* streams, i
                                    int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
                                    void* hip_stream, float* avg_ms);
 
+/* Profiling hook (no reference counterpart): times one of the step's projection GEMMs exactly as
+ * the step launches it for `rows` rows (tile shape, epilogue, split-K, operand format), `iters`
+ * launches back to back between two HIP events on hip_stream, launch i on layer (i + 1) % layers
+ * so the weights stream from HBM.  Inputs are whatever the workspace holds; the workspace's
+ * outputs are overwritten.  avg_ms receives the average launch duration, flops (may be NULL) the
+ * 2 rows N K flops of one launch.  Synchronizes hip_stream. */
+typedef enum {
+    UD_PROJ_FF_LINEAR1 = 0,   /* feed_forward{1,2}.linear1: N ff_dim, K d_model, SiLU */
+    UD_PROJ_FF_LINEAR2 = 1,   /* feed_forward{1,2}.linear2: N d_model, K ff_dim, x0.5, residual */
+    UD_PROJ_QKV = 2,          /* linear_q | linear_k | linear_v: N 3 d_model, K d_model */
+    UD_PROJ_LINEAR_OUT = 3,   /* linear_out: N d_model, K d_model, residual */
+    UD_PROJ_PW1 = 4,          /* conv.pointwise_conv1: N 2 d_model, K d_model, fp32 out */
+    UD_PROJ_PW2 = 5           /* conv.pointwise_conv2: N d_model, K d_model, residual */
+} ud_projection;
+UD_API int ud_time_projection(ud_encoder* enc, int32_t which, int32_t rows, int32_t iters, void* hip_stream,
+                              float* avg_ms, double* flops);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,19 @@ UD_API int ud_event_record(void* event, void* stream);
 UD_API int ud_event_synchronize(void* event);
 UD_API int ud_event_elapsed_ms(float* ms, void* start, void* stop);
 
+/* Measured peaks of the current device, the denominators of measured roofline fractions.  No
+ * reference counterpart beyond the same idea: the reference quotes its M3 roofline from its own
+ * micro-benchmarks (docs/PERF_LOG.md:7-16: read GB/s, GEMM TFLOPS).
+ *   ud_measure_hbm   streams a `bytes` buffer (>= 64 MiB; use >> the 256 MB last-level cache)
+ *                    `iters` times: read_gbs = bytes read per second by a read-only kernel;
+ *                    copy_gbs = bytes read + written per second by a device-to-device copy kernel.
+ *                    Allocates (and frees) two buffers of `bytes`.
+ *   ud_measure_mfma  dense v_mfma_f32_32x32x16 throughput in TFLOP/s, f16 and bf16 operands,
+ *                    register-only chains on every SIMD, `iters` loop trips per wave.
+ * Both synchronize hip_stream. */
+UD_API int ud_measure_hbm(size_t bytes, int32_t iters, void* hip_stream, float* read_gbs, float* copy_gbs);
+UD_API int ud_measure_mfma(int32_t iters, void* hip_stream, float* f16_tflops, float* bf16_tflops);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,6 +71,9 @@ def _sig(lib):
         "ud_layer_attention": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, ip, p, p]),
         "ud_chunked_limited_ranges": (i, [_i32, _i32, _i32, ip, _i32, _i32, _i32, ip]),
         "ud_stream_advance": (i, [ctypes.POINTER(_vp), _i32, _i32]),
+        "ud_time_projection": (i, [p, _i32, _i32, _i32, p, f, ctypes.POINTER(ctypes.c_double)]),
+        "ud_measure_hbm": (i, [ctypes.c_size_t, _i32, p, f, f]),
+        "ud_measure_mfma": (i, [_i32, p, f, f]),
         "ud_time_layer_attention": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, p, _i32, p, f]),
         "ud_time_ring_read_floor": (i, [p, ctypes.POINTER(_vp), _i32, _i32, _i32, p, p, _i32, p, f]),
         "ud_device_count": (i, [ip]),
@@ -161,6 +164,20 @@ def lib():
     if rc != 0 or n.value < 1:
         raise EngineError(-4, "no HIP device visible: the encoder step runs only on the GPU")
     return l
+
+
+def measure_hbm(nbytes=1 << 30, iters=10, hip_stream=None):
+    """(read GB/s, copy GB/s) of this device: streaming kernels over nbytes buffers."""
+    r, c = ctypes.c_float(0), ctypes.c_float(0)
+    _check(lib().ud_measure_hbm(nbytes, iters, hip_stream.ptr if hip_stream else None, ctypes.byref(r), ctypes.byref(c)))
+    return r.value, c.value
+
+
+def measure_mfma(iters=20000, hip_stream=None):
+    """(f16 TFLOP/s, bf16 TFLOP/s) of dense register-only MFMA chains on this device."""
+    h, b = ctypes.c_float(0), ctypes.c_float(0)
+    _check(lib().ud_measure_mfma(iters, hip_stream.ptr if hip_stream else None, ctypes.byref(h), ctypes.byref(b)))
+    return h.value, b.value
 
 
 def device_arch():
@@ -438,6 +455,17 @@ class Encoder:
         _check(_lib.ud_time_ring_read_floor(self.handle, _handles(streams), len(streams), T, layer, qkv.ptr, att.ptr,
                                             iters, hip_stream.ptr if hip_stream else None, ctypes.byref(ms)))
         return ms.value
+
+    PROJECTIONS = ("ff_linear1", "ff_linear2", "qkv", "linear_out", "pointwise_conv1", "pointwise_conv2")
+
+    def time_projection(self, which, rows, iters, hip_stream=None):
+        """(average ms per launch, flops per launch) of one of the step's projection GEMMs
+        (PROJECTIONS index) launched as the step launches it for `rows` rows."""
+        ms = ctypes.c_float(0)
+        fl = ctypes.c_double(0)
+        _check(_lib.ud_time_projection(self.handle, which, rows, iters, hip_stream.ptr if hip_stream else None,
+                                       ctypes.byref(ms), ctypes.byref(fl)))
+        return ms.value, fl.value
 
     @staticmethod
     def advance(streams, T):

@@ -1005,6 +1005,69 @@ extern "C" UD_API int ud_time_ring_read_floor(ud_encoder* e, ud_stream* const* s
                        [](const RingArgs& a, hipStream_t st) { return launch_ring_read_floor(a, st); });
 }
 
+// One projection of the step as the step launches it (shape, epilogue, split-K, operand layout),
+// over the encoder's workspace buffers and layer `layer`'s weights.
+static int launch_projection(ud_encoder* e, int which, int layer, int M, hipStream_t st, double* flops) {
+    const int D = e->D, ff = e->ff;
+    const LayerDev& l = e->lw[layer];
+    GemmArgs g{};
+    g.M = M; g.ksplit = 1; g.out_scale = 1.0f; g.act = ACT_NONE; g.f16 = e->bf ? 1 : 0;
+    switch (which) {
+        case UD_PROJ_FF_LINEAR1:
+            g.A = e->z; g.W = l.ff1_w1; g.C = e->h; g.N = ff; g.K = D; g.ldc = ff; g.act = ACT_SILU;
+            g.epi = e->bf ? EPI_STORE_FRAG : EPI_STORE;
+            break;
+        case UD_PROJ_FF_LINEAR2:
+            g.A = e->h; g.W = l.ff1_w2; g.N = D; g.K = ff; g.out_scale = 0.5f;
+            break;
+        case UD_PROJ_QKV:
+            g.A = e->z; g.W = l.wqkv; g.C = e->qkv; g.N = 3 * D; g.K = D; g.ldc = 3 * D; g.epi = EPI_STORE;
+            break;
+        case UD_PROJ_LINEAR_OUT:
+            g.A = e->att; g.W = l.wo; g.N = D; g.K = D;
+            break;
+        case UD_PROJ_PW1:
+            g.A = e->z; g.W = l.pw1; g.C = e->pw; g.N = 2 * D; g.K = D; g.ldc = 2 * D; g.epi = EPI_STORE_F32;
+            break;
+        case UD_PROJ_PW2:
+            g.A = e->z; g.W = l.pw2; g.N = D; g.K = D;
+            break;
+        default:
+            return fail(UD_ERR_INVALID, "ud_time_projection: projection %d", which);
+    }
+    if (g.N == D) {                       // the residual projections: split-K slabs (16-bit) or +=
+        g.ldc = D;
+        if (e->bf) { g.C = e->part; g.epi = EPI_PARTIAL; g.ksplit = gemm_partial_splits(M, D, g.K, true); }
+        else { g.C = e->res; g.epi = EPI_RESID; }
+    }
+    g.lda = g.K; g.ldw = g.K;
+    if (flops) *flops = 2.0 * M * g.N * g.K;
+    return launch_status(launch_gemm(g, e->bf, st), "projection");
+}
+
+extern "C" UD_API int ud_time_projection(ud_encoder* e, int32_t which, int32_t rows, int32_t iters, void* hip_stream,
+                                         float* avg_ms, double* flops) {
+    if (!e || !avg_ms || iters < 1) return fail(UD_ERR_INVALID, "ud_time_projection: bad argument");
+    if (!e->finalized) return fail(UD_ERR_STATE, "ud_time_projection: encoder not finalized");
+    if (rows < 1 || rows > e->max_rows) return fail(UD_ERR_SHAPE, "ud_time_projection: rows %d outside 1..%d", rows, e->max_rows);
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    hipEvent_t ev[2];
+    HIPC(hipEventCreate(&ev[0]));
+    HIPC(hipEventCreate(&ev[1]));
+    // launch i uses layer (i + 1) % layers, so the weights stream from HBM as in a real step
+    int rc = launch_projection(e, which, 0, rows, st, flops);
+    if (rc == UD_OK && hipEventRecord(ev[0], st) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventRecord failed");
+    for (int i = 0; rc == UD_OK && i < iters; i++) rc = launch_projection(e, which, (i + 1) % e->layers, rows, st, nullptr);
+    if (rc == UD_OK && hipEventRecord(ev[1], st) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventRecord failed");
+    float ms = 0.0f;
+    if (rc == UD_OK && hipEventSynchronize(ev[1]) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventSynchronize failed");
+    if (rc == UD_OK && hipEventElapsedTime(&ms, ev[0], ev[1]) != hipSuccess) rc = fail(UD_ERR_HIP, "hipEventElapsedTime failed");
+    (void)hipEventDestroy(ev[0]);
+    (void)hipEventDestroy(ev[1]);
+    if (rc == UD_OK) *avg_ms = ms / (float)iters;
+    return rc;
+}
+
 extern "C" UD_API int ud_stream_advance(ud_stream* const* streams, int32_t n, int32_t T) {
     if (!streams || n < 0 || T < 0) return fail(UD_ERR_INVALID, "ud_stream_advance: bad argument");
     for (int i = 0; i < n; i++) {

@@ -1,0 +1,199 @@
+// Measured peaks of the device the library runs on (include/ud_runtime.h): streaming HBM read and
+// copy bandwidth, and dense MFMA throughput.  The roofline fractions of the encoder's kernels are
+// quoted against these as well as against the vendor's nominal figures.
+//
+//  - hbm_read_kernel: every thread streams 16-byte non-temporal loads over a buffer much larger
+//    than the 256 MB last-level cache, grid-strided, eight loads in flight per iteration; the words
+//    are folded into a value that is stored only if it equals a constant no input produces, which
+//    keeps the loads live without writing.  Measured on MI355X, non-temporal loads and 32
+//    workgroups per CU read fastest of the forms tried (plain loads, 1-32 workgroups per CU,
+//    blocked or strided walks: 5.4-6.3 TB/s; this form 6.2-6.8 TB/s over 4 GiB).
+//  - hbm_copy_kernel: the same walk with a 16-byte non-temporal store per load.
+//  - mfma_peak_kernel: register-only v_mfma_f32_32x32x16_{f16,bf16} chains, four independent
+//    accumulators per wave, four waves per SIMD; 32 x 32 x 16 x 2 flops per instruction.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+
+#include "../../include/ud_encoder.h"
+#include "../../include/ud_runtime.h"
+#include "ud_common.hpp"
+
+int ud_set_error(int code, const char* msg);
+
+namespace ud {
+
+constexpr int PK_THREADS = 256;
+constexpr int PK_UNROLL = 8;
+constexpr int PK_WG_PER_CU = 32;
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_nt(const uint4* p) {
+    const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ void st_nt(uint4* p, uint4 v) {
+    const u32x4_t t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<u32x4_t*>(p));
+}
+
+__global__ __launch_bounds__(PK_THREADS) void hbm_read_kernel(const uint4* __restrict__ src, size_t n16,
+                                                              uint4* __restrict__ sink) {
+    const size_t stride = (size_t)gridDim.x * PK_THREADS;
+    size_t i = (size_t)blockIdx.x * PK_THREADS + threadIdx.x;
+    uint4 acc = make_uint4(0, 0, 0, 0);
+    for (; i + (PK_UNROLL - 1) * stride < n16; i += PK_UNROLL * stride) {
+        uint4 v[PK_UNROLL];
+#pragma unroll
+        for (int u = 0; u < PK_UNROLL; u++) v[u] = ld_nt(src + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < PK_UNROLL; u++) { acc.x ^= v[u].x; acc.y ^= v[u].y; acc.z ^= v[u].z; acc.w ^= v[u].w; }
+    }
+    for (; i < n16; i += stride) {
+        const uint4 v = src[i];
+        acc.x ^= v.x; acc.y ^= v.y; acc.z ^= v.z; acc.w ^= v.w;
+    }
+    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9E3779B9u && acc.x == 0x7F4A7C15u) sink[threadIdx.x] = acc;
+}
+
+__global__ __launch_bounds__(PK_THREADS) void hbm_copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                              size_t n16) {
+    const size_t stride = (size_t)gridDim.x * PK_THREADS;
+    size_t i = (size_t)blockIdx.x * PK_THREADS + threadIdx.x;
+    for (; i + (PK_UNROLL - 1) * stride < n16; i += PK_UNROLL * stride) {
+        uint4 v[PK_UNROLL];
+#pragma unroll
+        for (int u = 0; u < PK_UNROLL; u++) v[u] = ld_nt(src + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < PK_UNROLL; u++) st_nt(dst + i + u * stride, v[u]);
+    }
+    for (; i < n16; i += stride) st_nt(dst + i, ld_nt(src + i));
+}
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <bool H>
+__global__ __launch_bounds__(PK_THREADS) void mfma_peak_kernel(int iters, float* __restrict__ sink) {
+    // operands: small finite values (0.0039 .. 0.0078 in either format), different per lane
+    const uint32_t lo = H ? 0x1C00u + (threadIdx.x & 63) : 0x3B80u + (threadIdx.x & 63);
+    const uint32_t w = lo | (lo << 16);
+    const uint4 a = make_uint4(w, w ^ 0x00010001u, w, w ^ 0x00020002u);
+    const uint4 b = make_uint4(w ^ 0x00030003u, w, w ^ 0x00010001u, w);
+    f32x16_t acc[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[k][e] = 0.0f;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if constexpr (H)
+                acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_f16x8(a), as_f16x8(b), acc[k], 0, 0, 0);
+            else
+                acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), acc[k], 0, 0, 0);
+        }
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) s += acc[k][e];
+    if (s == -1.0f) sink[threadIdx.x] = s;   // never: every product is positive
+}
+
+}  // namespace ud
+
+using namespace ud;
+
+static int pk_fail(hipError_t e, const char* what) {
+    char buf[256];
+    snprintf(buf, sizeof buf, "%s: %s", what, hipGetErrorString(e));
+    return ud_set_error(UD_ERR_HIP, buf);
+}
+
+#define PKC(call)                                          \
+    do {                                                   \
+        hipError_t e_ = (call);                            \
+        if (e_ != hipSuccess) { rc = pk_fail(e_, #call); goto done; } \
+    } while (0)
+
+extern "C" UD_API int ud_measure_hbm(size_t bytes, int32_t iters, void* hip_stream, float* read_gbs, float* copy_gbs) {
+    if (bytes < (64u << 20) || bytes % 16 || iters < 1 || !read_gbs || !copy_gbs)
+        return ud_set_error(UD_ERR_INVALID, "ud_measure_hbm: need bytes >= 64 MiB, a multiple of 16, iters >= 1");
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    void *src = nullptr, *dst = nullptr, *sink = nullptr;
+    hipEvent_t ev[3] = {};
+    int rc = UD_OK;
+    const size_t n16 = bytes / 16;
+    int dev = 0, cus = 256;
+    float ms_read = 0.0f, ms_copy = 0.0f;
+    PKC(hipGetDevice(&dev));
+    PKC(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    PKC(hipMalloc(&src, bytes));
+    PKC(hipMalloc(&dst, bytes));
+    PKC(hipMalloc(&sink, PK_THREADS * 16));
+    PKC(hipMemsetAsync(src, 0x5A, bytes, st));
+    for (int k = 0; k < 3; k++) PKC(hipEventCreate(&ev[k]));
+    {
+        const dim3 grid(cus * PK_WG_PER_CU), block(PK_THREADS);
+        // warm-up (clocks, TLB), then the timed launches
+        hipLaunchKernelGGL(hbm_read_kernel, grid, block, 0, st, (const uint4*)src, n16, (uint4*)sink);
+        hipLaunchKernelGGL(hbm_copy_kernel, grid, block, 0, st, (const uint4*)src, (uint4*)dst, n16);
+        PKC(hipEventRecord(ev[0], st));
+        for (int i = 0; i < iters; i++)
+            hipLaunchKernelGGL(hbm_read_kernel, grid, block, 0, st, (const uint4*)src, n16, (uint4*)sink);
+        PKC(hipEventRecord(ev[1], st));
+        for (int i = 0; i < iters; i++)
+            hipLaunchKernelGGL(hbm_copy_kernel, grid, block, 0, st, (const uint4*)src, (uint4*)dst, n16);
+        PKC(hipEventRecord(ev[2], st));
+        PKC(hipGetLastError());
+        PKC(hipEventSynchronize(ev[2]));
+        PKC(hipEventElapsedTime(&ms_read, ev[0], ev[1]));
+        PKC(hipEventElapsedTime(&ms_copy, ev[1], ev[2]));
+        *read_gbs = (float)((double)bytes * iters / (ms_read * 1e-3) / 1e9);
+        *copy_gbs = (float)(2.0 * (double)bytes * iters / (ms_copy * 1e-3) / 1e9);
+    }
+done:
+    (void)hipStreamSynchronize(st);
+    for (int k = 0; k < 3; k++) if (ev[k]) (void)hipEventDestroy(ev[k]);
+    if (src) (void)hipFree(src);
+    if (dst) (void)hipFree(dst);
+    if (sink) (void)hipFree(sink);
+    return rc;
+}
+
+extern "C" UD_API int ud_measure_mfma(int32_t iters, void* hip_stream, float* f16_tflops, float* bf16_tflops) {
+    if (iters < 1 || !f16_tflops || !bf16_tflops) return ud_set_error(UD_ERR_INVALID, "ud_measure_mfma: bad argument");
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    float* sink = nullptr;
+    hipEvent_t ev[3] = {};
+    int rc = UD_OK;
+    int dev = 0, cus = 256;
+    float ms_h = 0.0f, ms_b = 0.0f;
+    PKC(hipGetDevice(&dev));
+    PKC(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    PKC(hipMalloc((void**)&sink, PK_THREADS * 4));
+    for (int k = 0; k < 3; k++) PKC(hipEventCreate(&ev[k]));
+    {
+        // 4 workgroups of 4 waves per CU: 4 waves per SIMD, each with 4 independent accumulators
+        const dim3 grid(cus * 4), block(PK_THREADS);
+        hipLaunchKernelGGL(mfma_peak_kernel<true>, grid, block, 0, st, iters, sink);   // warm-up
+        PKC(hipEventRecord(ev[0], st));
+        hipLaunchKernelGGL(mfma_peak_kernel<true>, grid, block, 0, st, iters, sink);
+        PKC(hipEventRecord(ev[1], st));
+        hipLaunchKernelGGL(mfma_peak_kernel<false>, grid, block, 0, st, iters, sink);
+        PKC(hipEventRecord(ev[2], st));
+        PKC(hipGetLastError());
+        PKC(hipEventSynchronize(ev[2]));
+        PKC(hipEventElapsedTime(&ms_h, ev[0], ev[1]));
+        PKC(hipEventElapsedTime(&ms_b, ev[1], ev[2]));
+        const double flops = (double)grid.x * (PK_THREADS / 64) * iters * 4 * (32.0 * 32 * 16 * 2);
+        *f16_tflops = (float)(flops / (ms_h * 1e-3) / 1e12);
+        *bf16_tflops = (float)(flops / (ms_b * 1e-3) / 1e12);
+    }
+done:
+    (void)hipStreamSynchronize(st);
+    for (int k = 0; k < 3; k++) if (ev[k]) (void)hipEventDestroy(ev[k]);
+    if (sink) (void)hipFree(sink);
+    return rc;
+}
