@@ -380,26 +380,27 @@ struct WindowRows {
             const uint32_t r = (uint32_t)(wpos + j[k]);
             roff[k] = (min(r, r - (uint32_t)L) << 8) | ((uint32_t)sub << 4);
         }
+        // ring rows are read once per step: non-temporal loads
         const bool ring_only = L >= G * (KR - 1);
         if (ring_only) {
 #pragma unroll
-            for (int k = 0; k < KR - 1; k++) kreg[k] = ld16(kb + roff[k]);
+            for (int k = 0; k < KR - 1; k++) kreg[k] = ld16_nt(kb + roff[k]);
         } else {
 #pragma unroll
-            for (int k = 0; k < KR - 1; k++) kreg[k] = ld16(cached[k] ? kb + roff[k] : kn + noff[k]);
+            for (int k = 0; k < KR - 1; k++) kreg[k] = ld16_nt(cached[k] ? kb + roff[k] : kn + noff[k]);
         }
-        kreg[KR - 1] = ld16(cached[KR - 1] ? kb + roff[KR - 1] : kn + noff[KR - 1]);
+        kreg[KR - 1] = ld16_nt(cached[KR - 1] ? kb + roff[KR - 1] : kn + noff[KR - 1]);
         // every K load before the first V load: loads complete in issue order, so the scores can
         // start while V is still arriving
         __builtin_amdgcn_sched_barrier(0);
         if (ring_only) {
 #pragma unroll
-            for (int k = 0; k < KR - 1; k++) vreg[k] = ld16(vb + roff[k]);
+            for (int k = 0; k < KR - 1; k++) vreg[k] = ld16_nt(vb + roff[k]);
         } else {
 #pragma unroll
-            for (int k = 0; k < KR - 1; k++) vreg[k] = ld16(cached[k] ? vb + roff[k] : vn + noff[k]);
+            for (int k = 0; k < KR - 1; k++) vreg[k] = ld16_nt(cached[k] ? vb + roff[k] : vn + noff[k]);
         }
-        vreg[KR - 1] = ld16(cached[KR - 1] ? vb + roff[KR - 1] : vn + noff[KR - 1]);
+        vreg[KR - 1] = ld16_nt(cached[KR - 1] ? vb + roff[KR - 1] : vn + noff[KR - 1]);
     }
 };
 
@@ -452,30 +453,33 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
     uint4 kreg[KR], vreg[KR];
     win.load(kreg, vreg, kbase, vbase, qkvh + D, qkvh + 2 * D, wpos, L, sub);
 
-    // ---- q + u, q + v
+    // ---- q + u, q + v, rounded once to IEEE-half pairs: the score products are v_dot2_f32_f16
+    //      (two products per instruction, fp32 sum) on the half words of K and the band as loaded
     const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
     const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-    float qu[TQ][VEC], qv[TQ][VEC];
+    half2_t qu2[TQ][VEC / 2], qv2[TQ][VEC / 2];
 #pragma unroll
     for (int i = 0; i < TQ; i++) {
         float f[VEC];
         unpack16<T>(qreg[i], f);
 #pragma unroll
-        for (int e = 0; e < VEC; e++) { qu[i][e] = f[e] + uu[e]; qv[i][e] = f[e] + vv[e]; }
+        for (int e = 0; e < VEC / 2; e++) {
+            qu2[i][e] = half2_t{(f16)(f[2 * e] + uu[2 * e]), (f16)(f[2 * e + 1] + uu[2 * e + 1])};
+            qv2[i][e] = half2_t{(f16)(f[2 * e] + vv[2 * e]), (f16)(f[2 * e + 1] + vv[2 * e + 1])};
+        }
     }
     const int qi = tsum16_index<TQ>(sub);
 
     // ---- bd[i][b] = (q_i + v) . band row b
 #pragma unroll
     for (int k = 0; k < PR; k++) {
-        float f[VEC];
-        unpack16<T>(preg[k], f);
+        const uint32_t w[4] = {preg[k].x, preg[k].y, preg[k].z, preg[k].w};
         float part[TQ];
 #pragma unroll
         for (int i = 0; i < TQ; i++) {
             float acc = 0.0f;
 #pragma unroll
-            for (int e = 0; e < VEC; e++) acc += qv[i][e] * f[e];
+            for (int e = 0; e < VEC / 2; e++) acc = __builtin_amdgcn_fdot2(qv2[i][e], as_half2(w[e]), acc, false);
             part[i] = acc;
         }
         const float tot = tsum16<TQ>(part, sub);
@@ -484,14 +488,13 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
     // ---- ac[i][j] = (q_i + u) . K_j
 #pragma unroll
     for (int k = 0; k < KR; k++) {
-        float f[VEC];
-        unpack16<T>(kreg[k], f);
+        const uint32_t w[4] = {kreg[k].x, kreg[k].y, kreg[k].z, kreg[k].w};
         float part[TQ];
 #pragma unroll
         for (int i = 0; i < TQ; i++) {
             float acc = 0.0f;
 #pragma unroll
-            for (int e = 0; e < VEC; e++) acc += qu[i][e] * f[e];
+            for (int e = 0; e < VEC / 2; e++) acc = __builtin_amdgcn_fdot2(qu2[i][e], as_half2(w[e]), acc, false);
             part[i] = acc;
         }
         const float tot = tsum16<TQ>(part, sub);
@@ -529,7 +532,8 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
     }
     __syncthreads();
 
-    // ---- out = P . V from the V registers (rows outside the range zeroed)
+    // ---- out = P . V from the V registers (rows outside the range zeroed): v_fma_mix_f32 takes the
+    //      half V words as they are (fp32 probability, fp32 sum)
     float acc[NV];
 #pragma unroll
     for (int f = 0; f < NV; f++) acc[f] = 0.0f;
@@ -538,13 +542,16 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
         const int j = grp + k * G;
         const bool in = j >= ks && j < ke;
         const uint4 z = make_uint4(0, 0, 0, 0);
-        float f[VEC];
-        unpack16<T>(in ? vreg[k] : z, f);
+        const uint4 vk = in ? vreg[k] : z;
+        const uint32_t w[4] = {vk.x, vk.y, vk.z, vk.w};
 #pragma unroll
         for (int i = 0; i < TQ; i++) {
             const float p = sc[i][j];
 #pragma unroll
-            for (int e = 0; e < VEC; e++) acc[i * VEC + e] += p * f[e];
+            for (int e = 0; e < VEC / 2; e++) {
+                acc[i * VEC + 2 * e] = fmaf(p, half_lo(w[e]), acc[i * VEC + 2 * e]);
+                acc[i * VEC + 2 * e + 1] = fmaf(p, half_hi(w[e]), acc[i * VEC + 2 * e + 1]);
+            }
         }
     }
     // over the 4 row groups of the wave: lane (row4, sub) ends with flat sums row4*NQ .. +NQ-1
@@ -651,78 +658,102 @@ int launch_ring_read_floor(const RingArgs& a, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// ------------------------------------------------------------------ streaming ring kernel on MFMA (T <= 16)
-// Longer chunks (config of 14 frames) make the per-(stream, head) work a real matrix product:
-// 16 query rows (T of them real) against L + T keys and L + 2T - 1 band rows.  One wave64 per
-// (stream, head), everything on v_mfma_f32_16x16x32_f16:
-//   bd^T-free form: C[query][band row] = (q+v) . P_band^T   (A = q+v, B = P rows straight from HBM/L2)
-//   C[query][key] = (q+u) . K^T                              (B = K rows straight from the ring)
-//   out[query][chan] = softmax . V                           (A = probabilities, B = V^T)
-// A lane's B operand is 8 consecutive k values for one n: for the score products that is one
-// 16-byte chunk of a K / P row (n = row, k = channels), loaded directly; for P.V it is 8 keys of one
-// channel, which ds_read_b64_tr_b16 produces from V rows staged row-major in LDS.  q+u, q+v and the
-// probabilities are fp32 and enter as IEEE-half hi/lo pairs (two MFMAs), so products keep ~2^-21
-// relative accuracy.  Scores stay in registers (lane: queries 4g..4g+3 of key 16t + lane%16);
-// rel_shift is a gather of the band tile from LDS; softmax reduces within 16-lane DPP rows.
-
+// ------------------------------------------------------------------ streaming ring kernel on MFMA (T 5..16)
+// Longer chunks (config of 14 frames: 256 streams x 8 heads, 103 MB per launch) make the
+// per-(stream, head) work a real matrix product: 16 query rows (T of them real) against
+// L + T <= 96 keys and L + 2T - 1 <= 112 band rows, all on v_mfma_f32_16x16x32_f16:
+//   C[query][band row] = (q+v) . P_band^T    (B = band rows from LDS)
+//   C[query][key]      = (q+u) . K^T         (B = K rows loaded straight into registers)
+//   out[query][chan]   = softmax . V         (A = probabilities, B = V^T via transposed LDS reads)
+// One wave64 per (stream, head); a workgroup is 8 waves = 8 streams of one head, so the head's
+// band is loaded once per workgroup into LDS (it is the same for every stream), and every wave
+// is resident at once at two waves per SIMD (2,048 waves on 1,024 SIMDs): one wave's MFMAs and
+// softmax run while the other's loads are in flight.  To fit two waves per SIMD (<= 256 VGPRs,
+// <= 20 KB of LDS each): the K window (96 VGPRs) and the first half of the V window are loaded up
+// front; the second half of V goes into K's registers once the scores are done; V reaches the MFMA
+// through a 32-key LDS piece (ds_read_b64_tr_b16), three pieces per unit.
+// q+u, q+v and the probabilities enter the MFMA rounded once to IEEE half (relative 2^-12).
+// Scores stay in registers (lane: queries 4g..4g+3 of key 16t + lane%16); rel_shift is a gather of
+// the band tile from LDS; the softmax reduces within 16-lane DPP rows.
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
-// fp32 x 8 -> half hi (round to nearest even) and lo = half(x - hi), packed for an MFMA operand.
-__device__ __forceinline__ void split_f16x8(const float (&x)[8], uint4& hi, uint4& lo) {
-    uint32_t hw[4], lw[4];
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-        const uint16_t h0 = f2h(x[e]), h1 = f2h(x[e + 1]);
-        hw[e / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-        lw[e / 2] = (uint32_t)f2h(x[e] - h2f(h0)) | ((uint32_t)f2h(x[e + 1] - h2f(h1)) << 16);
-    }
-    hi = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    lo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+namespace rm {
+constexpr int KT = 6, BT = 7;                    // key / band tiles of 16 rows
+constexpr int KMAX = 16 * KT, BMAX = 16 * BT;
+constexpr int NW = 8;                            // waves (streams of one head) per workgroup
+constexpr int RS = 17;                           // 16-byte slots per band row in LDS (16 + 1 pad)
+constexpr int BSLOTS = BMAX * RS;                // 16-byte slots of the band rows
+constexpr int BINS = (BSLOTS + 64 + 63) / 64;     // direct-load instructions: band rows, u and v
+constexpr int VST = 136;                         // halves per staged V row (128 + 8 pad)
+}  // namespace rm
+
+// ds_write / ds_read of one wave that exchange data across its lanes: wait for the wave's own LDS
+// operations (no other wave touches the region).
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0)
+    __asm__ volatile("" ::: "memory");
 }
 
-template <int KT, int BT>
-__global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
-    using T = f16;
-    constexpr int DK = 128, KMAX = KT * 16, BMAX = BT * 16, VST = DK + 8;
-    static_assert(KMAX % 32 == 0, "P.V k-steps of 32 keys");
-    __shared__ __align__(16) uint16_t vl[KMAX][VST];      // V rows of the window (masked rows 0)
-    __shared__ __align__(16) float sl[16][BMAX + 4];       // band tile for the gather, then probabilities
+// fp32 x 8 -> 8 IEEE halves packed for an MFMA operand.
+__device__ __forceinline__ uint4 pack_f16x8(const float (&x)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) w[e] = (uint32_t)f2h(x[2 * e]) | ((uint32_t)f2h(x[2 * e + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
 
-    const int lane = threadIdx.x, col = lane & 15, g = lane >> 4;
-    const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
-    const int L = a.L, Tq = a.T, D = a.H * DK, W = L + Tq, NB = L + 2 * Tq - 1;
-    const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)s * Tq * 3 * D + h * DK;
-    const T* P = static_cast<const T*>(a.P) + (int64_t)(a.rel_offset + 1 - Tq) * D + h * DK;
-    const int32_t* d = a.desc + s * DESC_INTS;
+__global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingArgs a) {
+    using namespace rm;
+    using T = f16;
+    __shared__ __align__(16) uint4 band[BINS * 64];            // band rows (17 slots each), then u, v
+    __shared__ __align__(16) float slw[NW][16][BMAX + 4];      // per wave: bd tile, then probabilities
+    __shared__ __align__(16) uint16_t vpw[NW][32][VST];        // per wave: a 32-key piece of V
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, g = lane >> 4;
+    const int H = a.H, L = a.L, Tq = a.T, D = H * 128, W = L + Tq, NB = L + 2 * Tq - 1;
+    const int h = blockIdx.x % H;
+    const int s = (blockIdx.x / H) * NW + wave;
+    const bool live = s < a.n;                                  // wave-uniform
+    float (*sl)[BMAX + 4] = slw[wave];
+    uint16_t (*vp)[VST] = vpw[wave];
+    // the descriptor first: read before any store of the kernel, it stays a scalar load.  A wave
+    // past the last stream works on stream 0 and stores nothing (no branch around the body).
+    const int sx = live ? s : 0;
+    const int32_t* d = a.desc + sx * DESC_INTS;
     const int slot = d[0], wpos = d[1], valid = min(max(d[2], 0), Tq), cache_len = d[3];
+
+    // ---- the head's band -> LDS (rows rel_offset + 1 - T + b, b < NB, of P; rel = 1-T .. L+T-1),
+    //      then its u and v biases (32 slots each)
+    {
+        const char* P = static_cast<const char*>(a.P) + ((int64_t)(a.rel_offset + 1 - Tq) * D + h * 128) * 2;
+        const char* zero = static_cast<const char*>(a.zero_row);
+#pragma unroll
+        for (int m = 0; m < (BINS + NW - 1) / NW; m++) {
+            const int ins = wave + NW * m;
+            if (ins < BINS) {
+                const int slot = 64 * ins + lane, r = slot / RS, c = slot % RS, k = slot - BSLOTS;
+                const char* src = (c < 16 && r < NB) ? P + (int64_t)r * D * 2 + c * 16 : zero;
+                if (k >= 0) src = k < 64 ? reinterpret_cast<const char*>((k < 32 ? a.u : a.vb) + h * 128 + 4 * (k & 31)) : zero;
+                __builtin_amdgcn_global_load_lds(src, &band[64 * ins], 16, 0, 0);
+            }
+        }
+    }
+    __asm__ volatile("" ::: "memory");          // the band loads stay ahead of the unit's loads
+    // ---- this wave's unit: q, K (B layout) and the first half of V
     const int ks = L - cache_len, ke = L + valid;
-    T* kring = static_cast<T*>(a.kring) + ((int64_t)slot * a.H + h) * L * DK;
-    T* vring = static_cast<T*>(a.vring) + ((int64_t)slot * a.H + h) * L * DK;
+    const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)sx * Tq * 3 * D + h * 128;
+    T* kring = static_cast<T*>(a.kring) + ((int64_t)slot * H + h) * L * 128;
+    T* vring = static_cast<T*>(a.vring) + ((int64_t)slot * H + h) * L * 128;
     auto key_row = [&](T* ring, int j, int part) -> const T* {   // part 1: K, 2: V
         int r = wpos + j;
         r -= (r >= L) ? L : 0;
-        return j < L ? ring + (int64_t)r * DK : qkv + (int64_t)(j - L) * 3 * D + part * D;
+        return j < L ? ring + (int64_t)r * 128 : qkv + (int64_t)(j - L) * 3 * D + part * D;
     };
-
-    // ---- loads: q (A rows = queries), u/v, the band tiles, the K tiles (B rows), k-chunk 4st + g
     uint4 qraw[4];
-    float4 ua[4][2], va[4][2];
 #pragma unroll
-    for (int st = 0; st < 4; st++) {
-        const int c = (4 * st + g) * 8;
-        qraw[st] = ld16(qkv + (int64_t)min(col, Tq - 1) * 3 * D + c);
-        ua[st][0] = *reinterpret_cast<const float4*>(a.u + h * DK + c);
-        ua[st][1] = *reinterpret_cast<const float4*>(a.u + h * DK + c + 4);
-        va[st][0] = *reinterpret_cast<const float4*>(a.vb + h * DK + c);
-        va[st][1] = *reinterpret_cast<const float4*>(a.vb + h * DK + c + 4);
-    }
-    uint4 pb[BT][4];
-#pragma unroll
-    for (int t = 0; t < BT; t++) {
-        const T* row = P + (int64_t)min(16 * t + col, NB - 1) * D;
-#pragma unroll
-        for (int st = 0; st < 4; st++) pb[t][st] = ld16(row + (4 * st + g) * 8);
-    }
+    for (int st = 0; st < 4; st++) qraw[st] = ld16(qkv + (int64_t)min(col, Tq - 1) * 3 * D + (4 * st + g) * 8);
     uint4 kb[KT][4];
 #pragma unroll
     for (int t = 0; t < KT; t++) {
@@ -730,63 +761,73 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
 #pragma unroll
         for (int st = 0; st < 4; st++) kb[t][st] = ld16(row + (4 * st + g) * 8);
     }
+    uint4 vr[KMAX / 4];                          // row 4 it + g, 16-byte column col
+#pragma unroll
+    for (int it = 0; it < KMAX / 8; it++) vr[it] = ld16(key_row(vring, min(4 * it + g, W - 1), 2) + col * 8);
+    // vmcnt(32): the 40 loads of the unit (q 4, K 24, V 12) were issued after the band loads and
+    // complete in order, so at most 32 outstanding means the band loads are done; the unit's data
+    // keeps arriving under the band product.
+    // A bare s_barrier, not __syncthreads(): the latter's workgroup fence waits for every
+    // outstanding load (vmcnt(0)); the band's direct loads are covered by the wait above.
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x8F70);
+    __builtin_amdgcn_s_barrier();                // every wave's band loads
+    __asm__ volatile("" ::: "memory");
+    const float (*uvl)[128] = reinterpret_cast<const float (*)[128]>(&band[BSLOTS]);
 
-    // ---- A operands: q + u and q + v as half hi/lo
-    uint4 auh[4], aul[4], avh[4], avl[4];
+    // ---- A operands: q + u, q + v (query col, k-chunk 4 st + g), rounded once to half
+    uint4 aqu[4], aqv[4];
 #pragma unroll
     for (int st = 0; st < 4; st++) {
+        const int c = (4 * st + g) * 8;
+        const float4 u0 = *reinterpret_cast<const float4*>(&uvl[0][c]), u1 = *reinterpret_cast<const float4*>(&uvl[0][c + 4]);
+        const float4 v0 = *reinterpret_cast<const float4*>(&uvl[1][c]), v1 = *reinterpret_cast<const float4*>(&uvl[1][c + 4]);
+        const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+        const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         float q[8], x[8], y[8];
         unpack16<T>(qraw[st], q);
-        const float uu[8] = {ua[st][0].x, ua[st][0].y, ua[st][0].z, ua[st][0].w, ua[st][1].x, ua[st][1].y, ua[st][1].z, ua[st][1].w};
-        const float vv[8] = {va[st][0].x, va[st][0].y, va[st][0].z, va[st][0].w, va[st][1].x, va[st][1].y, va[st][1].z, va[st][1].w};
 #pragma unroll
         for (int e = 0; e < 8; e++) { x[e] = q[e] + uu[e]; y[e] = q[e] + vv[e]; }
-        split_f16x8(x, auh[st], aul[st]);
-        split_f16x8(y, avh[st], avl[st]);
+        aqu[st] = pack_f16x8(x);
+        aqv[st] = pack_f16x8(y);
     }
 
-    // ---- bd tiles -> LDS: sl[query][band row]
+    // ---- bd tiles -> sl[query][band row]
 #pragma unroll
     for (int t = 0; t < BT; t++) {
         f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int st = 0; st < 4; st++) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(avh[st]), as_f16x8(pb[t][st]), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(avl[st]), as_f16x8(pb[t][st]), acc, 0, 0, 0);
-        }
+        for (int st = 0; st < 4; st++)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(aqv[st]), as_f16x8(band[(16 * t + col) * RS + 4 * st + g]),
+                                                         acc, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < 4; r++) sl[4 * g + r][16 * t + col] = acc[r];
     }
-
-    // ---- V rows of the window -> LDS (4 rows per pass, 16 lanes x 16 bytes per row)
-    uint4 vr[KMAX / 4];
-#pragma unroll
-    for (int it = 0; it < KMAX / 4; it++) vr[it] = ld16(key_row(vring, min(4 * it + g, W - 1), 2) + col * 8);
-
     // ---- ac tiles in registers: lane holds queries 4g..4g+3 of key 16t + col
     f32x4_t sacc[KT];
 #pragma unroll
     for (int t = 0; t < KT; t++) {
         f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int st = 0; st < 4; st++) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(auh[st]), as_f16x8(kb[t][st]), acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(aul[st]), as_f16x8(kb[t][st]), acc, 0, 0, 0);
-        }
+        for (int st = 0; st < 4; st++)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(aqu[st]), as_f16x8(kb[t][st]), acc, 0, 0, 0);
         sacc[t] = acc;
     }
-    // commit the new K rows (this wave read every ring row it overwrites, above)
+    // commit the new K rows (this wave read every ring row it overwrites, above); K's registers
+    // then take the second half of the V window
 #pragma unroll
     for (int t = 0; t < KT; t++) {
         const int j = 16 * t + col;
-        if (j >= L && j < W) {
+        if (live && j >= L && j < W) {
             int r = wpos + (j - L);
             r -= (r >= L) ? L : 0;
 #pragma unroll
-            for (int st = 0; st < 4; st++) st16(kring + (int64_t)r * DK + (4 * st + g) * 8, kb[t][st]);
+            for (int st = 0; st < 4; st++) st16(kring + (int64_t)r * 128 + (4 * st + g) * 8, kb[t][st]);
         }
     }
-    __syncthreads();
+#pragma unroll
+    for (int it = KMAX / 8; it < KMAX / 4; it++) vr[it] = ld16(key_row(vring, min(4 * it + g, W - 1), 2) + col * 8);
+    wave_lds_fence();
 
     // ---- scores, rel_shift gather, softmax over keys [ks, ke) (16-lane rows hold one query set)
     float pr[KT][4];
@@ -799,8 +840,8 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int i = 4 * g + r;
-            const int b = min(max(W - 1 + i - j, 0), BMAX - 1);
-            const float x = (sacc[t][r] + sl[i][b]) * a.scale;
+            const int bi = min(max(W - 1 + i - j, 0), BMAX - 1);
+            const float x = (sacc[t][r] + sl[i][bi]) * a.scale;
             pr[t][r] = (i < Tq && j >= ks && j < ke) ? x : -INFINITY;
             mx[r] = fmaxf(mx[r], pr[t][r]);
         }
@@ -816,15 +857,8 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
         }
 #pragma unroll
     for (int r = 0; r < 4; r++) { sm[r] = group_sum<16>(sm[r]); sm[r] = sm[r] > 0.0f ? 1.0f / sm[r] : 0.0f; }
-    // V rows to LDS (zero outside [ks, ke)); the band tile is no longer needed: probabilities
-    // overwrite it as sl[query][key]
-#pragma unroll
-    for (int it = 0; it < KMAX / 4; it++) {
-        const int j = 4 * it + g;
-        const bool in = j >= ks && j < ke;
-        *reinterpret_cast<uint4*>(&vl[j][col * 8]) = in ? vr[it] : make_uint4(0, 0, 0, 0);
-    }
-    __syncthreads();
+    wave_lds_fence();                            // every lane's gather read is done
+    // probabilities overwrite the band tile as sl[query][key]
 #pragma unroll
     for (int t = 0; t < KT; t++)
 #pragma unroll
@@ -833,56 +867,73 @@ __global__ __launch_bounds__(64) void relpos_ring_mfma_kernel(RingArgs a) {
 #pragma unroll
     for (int it = 0; it < KMAX / 4; it++) {
         const int j = 4 * it + g;
-        if (j >= L && j < W) {
+        if (live && j >= L && j < W) {
             int r = wpos + (j - L);
             r -= (r >= L) ? L : 0;
-            st16(vring + (int64_t)r * DK + col * 8, vr[it]);
+            st16(vring + (int64_t)r * 128 + col * 8, vr[it]);
         }
     }
-    __syncthreads();
+    wave_lds_fence();
 
-    // ---- out = P . V: A = probabilities (query col, keys 32kk + 8g ..), B = V^T via transposed reads
+    // ---- out^T = V^T . P^T, one 32-key piece of V at a time through LDS (rows outside [ks, ke)
+    //      zero): A = V^T by ds_read_b64_tr_b16 (lane c of a 16-lane group gets column c & 3 of the
+    //      rows named by lanes c / 4 + 4 e), B = probabilities (query col, keys 32 kk + 8 g ..).
+    //      The transposed product leaves each lane 4 consecutive channels of one query row.
     f32x4_t oacc[8];
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) oacc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kk = 0; kk < KMAX / 32; kk++) {
-        float pf[8];
+#pragma unroll
+        for (int it = 8 * kk; it < 8 * kk + 8; it++) {
+            const int j = 4 * it + g;
+            const uint32_t keep = (j >= ks && j < ke) ? 0xFFFFFFFFu : 0u;   // no branch: a mask
+            *reinterpret_cast<uint4*>(&vp[j - 32 * kk][col * 8]) =
+                make_uint4(vr[it].x & keep, vr[it].y & keep, vr[it].z & keep, vr[it].w & keep);
+        }
         const float4 p0 = *reinterpret_cast<const float4*>(&sl[col][32 * kk + 8 * g]);
         const float4 p1 = *reinterpret_cast<const float4*>(&sl[col][32 * kk + 8 * g + 4]);
-        pf[0] = p0.x; pf[1] = p0.y; pf[2] = p0.z; pf[3] = p0.w; pf[4] = p1.x; pf[5] = p1.y; pf[6] = p1.z; pf[7] = p1.w;
-        uint4 ph, pl;
-        split_f16x8(pf, ph, pl);
-        const int k0 = 32 * kk + 8 * g + (col >> 2);
+        const float pf[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        const uint4 pa = pack_f16x8(pf);
+        wave_lds_fence();
+        const int k0 = 8 * g + (col >> 2);
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
             const int c0 = 16 * dt + 4 * (col & 3);
-            const v4i16_t b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vl[k0][c0]);
-            const v4i16_t b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vl[k0 + 4][c0]);
+            const v4i16_t b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vp[k0][c0]);
+            const v4i16_t b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vp[k0 + 4][c0]);
             uint4 bv;
             __builtin_memcpy(&bv.x, &b0, 8);
             __builtin_memcpy(&bv.z, &b1, 8);
-            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(ph), as_f16x8(bv), oacc[dt], 0, 0, 0);
-            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(pl), as_f16x8(bv), oacc[dt], 0, 0, 0);
+            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(bv), as_f16x8(pa), oacc[dt], 0, 0, 0);
         }
+        wave_lds_fence();                        // this piece's reads are done before the next writes
     }
 
-    // ---- output: lane holds out[4g + r][16dt + col]  (0 for an empty key range)
-    const bool empty = ke <= ks;
+    // ---- output: lane holds out[col][16 dt + 4 g + r], r < 4 (exactly 0 for an empty key range:
+    //      every probability and every staged V row is 0); 8-byte stores, contiguous in either layout
     T* att = static_cast<T*>(a.att);
+    if (live && col < Tq) {
+        const int64_t orow = (int64_t)s * Tq + col;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int i = 4 * g + r;
-        if (i < Tq) {
-            const int64_t orow = (int64_t)s * Tq + i;
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) {
-                const int c = h * DK + 16 * dt + col;
-                const int64_t idx = a.att_frag ? frag_index(orow, c, D / 64) : orow * D + c;
-                att[idx] = empty ? (T)0 : (T)oacc[dt][r];
-            }
+        for (int dt = 0; dt < 8; dt++) {
+            const int c = h * 128 + 16 * dt + 4 * g;
+            const int64_t idx = a.att_frag ? frag_index(orow, c, D / 64) : orow * D + c;
+            const uint2 w = make_uint2((uint32_t)f2h(oacc[dt][0]) | ((uint32_t)f2h(oacc[dt][1]) << 16),
+                                       (uint32_t)f2h(oacc[dt][2]) | ((uint32_t)f2h(oacc[dt][3]) << 16));
+            *reinterpret_cast<uint2*>(att + idx) = w;
         }
     }
+}
+
+int launch_relpos_ring_mfma(const RingArgs& a, hipStream_t st) {
+    using namespace rm;
+    if (a.T < 1 || a.T > 16 || a.L + a.T > KMAX || a.L + 2 * a.T - 1 > BMAX || a.n < 1 || a.H < 1 || !a.zero_row)
+        return -2;
+    if (a.rel_offset + 1 - a.T < 0 || a.rel_offset + a.L + a.T - 1 >= a.n_rel) return -2;
+    const int grid = a.H * ((a.n + NW - 1) / NW);
+    hipLaunchKernelGGL(relpos_ring_mfma_kernel, dim3(grid), dim3(64 * NW), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // ------------------------------------------------------------------ offline (dense) MFMA kernel
@@ -1173,10 +1224,8 @@ static int launch_ring_t(const RingArgs& a, hipStream_t st) {
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     // 16-bit chunks of 5..16 frames (L + T <= 96 keys): the MFMA kernel, one wave per (stream, head).
-    if (sizeof(T) == 2 && a.T <= 16 && a.L + a.T <= 96 && a.L + 2 * a.T - 1 <= 112 && band_ok) {
-        hipLaunchKernelGGL((relpos_ring_mfma_kernel<6, 7>), dim3(a.n * a.H), dim3(64), 0, st, a);
-        return hipGetLastError() == hipSuccess ? 0 : -1;
-    }
+    if (sizeof(T) == 2 && a.T <= 16 && a.L + a.T <= 96 && a.L + 2 * a.T - 1 <= 112 && band_ok && a.zero_row)
+        return launch_relpos_ring_mfma(a, st);
     if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_kernel<T, 2, KeyBlock<T, 2>::KB>), grid, block, 0, st, a);
     else if (a.T <= 4) hipLaunchKernelGGL((relpos_ring_kernel<T, 4, KeyBlock<T, 4>::KB>), grid, block, 0, st, a);
     else if (a.T <= 8) hipLaunchKernelGGL((relpos_ring_kernel<T, 8, KeyBlock<T, 8>::KB>), grid, block, 0, st, a);

@@ -182,6 +182,7 @@ struct ud_encoder {
     float* res = nullptr; void* z = nullptr; void* h = nullptr; void* qkv = nullptr; void* att = nullptr;
     float* pw = nullptr;
     float* part = nullptr;          // split-K residual partial slabs [KSPLIT][max_rows][D]
+    void* zero_row = nullptr;       // 256 zero bytes: the attention kernels' loads of masked rows
     int32_t* desc_dev = nullptr;
     int32_t* desc_host[4] = {};
     hipEvent_t desc_ev[4] = {};
@@ -228,7 +229,8 @@ static void free_encoder(ud_encoder* e) {
         for (void* p : ps) if (p) (void)hipFree(p);
         for (float* p : l.ln) if (p) (void)hipFree(p);
     }
-    void* ws[] = {e->kring, e->vring, e->cring, e->res, e->z, e->h, e->qkv, e->att, e->pw, e->part, e->desc_dev};
+    void* ws[] = {e->kring, e->vring, e->cring, e->res, e->z, e->h, e->qkv, e->att, e->pw, e->part, e->desc_dev,
+                  e->zero_row};
     for (void* p : ws) if (p) (void)hipFree(p);
     for (void* p : e->sub.w) if (p) (void)hipFree(p);
     void* sws[] = {e->sub.a2, e->sub.a3, e->sub.a4, e->sub.a5, e->sub.af, e->sub.vlen};
@@ -316,6 +318,7 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
         ok &= (e->pw = (float*)dev_alloc(R * 2 * D * 4)) != nullptr;
         if (e->bf) ok &= (e->part = (float*)dev_alloc(KSPLIT * R * D * 4)) != nullptr;
         ok &= (e->desc_dev = (int32_t*)dev_alloc(slots * DESC_INTS * 4)) != nullptr;
+        ok &= (e->zero_row = dev_alloc(256)) != nullptr;
     }
     for (int i = 0; ok && i < 4; i++) {
         ok &= hipHostMalloc((void**)&e->desc_host[i], slots * DESC_INTS * 4, hipHostMallocDefault) == hipSuccess;
@@ -325,7 +328,8 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
         free_encoder(e);
         return fail(UD_ERR_NOMEM, "ud_encoder_create: device allocation failed");
     }
-    if (hipMemset(e->kring, 0, e->ring_layer_elems * e->layers * esz) != hipSuccess ||
+    if (hipMemset(e->zero_row, 0, 256) != hipSuccess ||
+        hipMemset(e->kring, 0, e->ring_layer_elems * e->layers * esz) != hipSuccess ||
         hipMemset(e->vring, 0, e->ring_layer_elems * e->layers * esz) != hipSuccess ||
         hipMemset(e->cring, 0, e->cring_layer_elems * e->layers * 4) != hipSuccess ||
         hipStreamCreateWithFlags(&e->capture_stream, hipStreamNonBlocking) != hipSuccess ||
@@ -734,6 +738,7 @@ static int enqueue_rows(ud_encoder* e, int s0, int n, int T, const float* x, flo
         ra.kring = static_cast<char*>(e->kring) + roff;
         ra.vring = static_cast<char*>(e->vring) + roff;
         ra.qkv = w.qkv; ra.P = l.P; ra.u = l.bias_u; ra.vb = l.bias_v; ra.att = w.att; ra.desc = w.desc;
+        ra.zero_row = e->zero_row;
         ra.n = n; ra.T = T; ra.L = e->L; ra.H = e->H; ra.rel_offset = e->rel_offset; ra.n_rel = e->n_rel;
         ra.scale = 1.0f / std::sqrt((float)e->dk);
         ra.att_frag = bf ? 1 : 0;
@@ -934,6 +939,7 @@ static RingArgs ring_args(ud_encoder* e, int n, int T, int layer, const void* qk
     ra.kring = static_cast<char*>(e->kring) + roff;
     ra.vring = static_cast<char*>(e->vring) + roff;
     ra.qkv = qkv; ra.P = l.P; ra.u = l.bias_u; ra.vb = l.bias_v; ra.att = att; ra.desc = e->desc_dev;
+    ra.zero_row = e->zero_row;
     ra.n = n; ra.T = T; ra.L = e->L; ra.H = e->H; ra.rel_offset = e->rel_offset; ra.n_rel = e->n_rel;
     ra.scale = 1.0f / std::sqrt((float)e->dk);
     return ra;

@@ -44,6 +44,7 @@ struct RingArgs {
     const float* u; const float* vb;   // [H*128]
     void* att;                      // [n*T, D]: row-major, or fragment-major when att_frag (bf16)
     const int32_t* desc;            // [n][DESC_INTS]
+    const void* zero_row;           // >= 256 zero bytes, 16-byte aligned (masked rows' loads)
     int n, T, L, H, rel_offset, n_rel;
     float scale;
     int att_frag;

@@ -27,11 +27,7 @@ constexpr int PK_THREADS = 256;
 constexpr int PK_UNROLL = 8;
 constexpr int PK_WG_PER_CU = 32;
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 ld_nt(const uint4* p) {
-    const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-    return make_uint4(t.x, t.y, t.z, t.w);
-}
+__device__ __forceinline__ uint4 ld_nt(const uint4* p) { return ld16_nt(p); }
 __device__ __forceinline__ void st_nt(uint4* p, uint4 v) {
     const u32x4_t t = {v.x, v.y, v.z, v.w};
     __builtin_nontemporal_store(t, reinterpret_cast<u32x4_t*>(p));

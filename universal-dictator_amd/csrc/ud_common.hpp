@@ -46,6 +46,11 @@ template <bool H> __device__ __forceinline__ uint16_t to16(float f) {
 // Element types of the attention kernels: fp32, bf16 (uint16_t storage) and IEEE half (_Float16,
 // the 16-bit format of a 16-bit encoder's activations, caches and tables).
 typedef _Float16 f16;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ half2_t as_half2(uint32_t w) { return __builtin_bit_cast(half2_t, w); }
+// The low / high half of a packed pair as fp32 (in an FMA, the conversion folds into v_fma_mix_f32).
+__device__ __forceinline__ float half_lo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)w); }
+__device__ __forceinline__ float half_hi(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)); }
 
 template <typename T> __device__ __forceinline__ float to_f(T v);
 template <> __device__ __forceinline__ float to_f<float>(float v) { return v; }
@@ -79,6 +84,13 @@ template <> struct Vec16<f16> { static constexpr int N = 8; };
 
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+// Non-temporal 16-byte load: data read once per step (a stream's K/V window), streamed past the
+// caches' normal retention.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld16_nt(const void* p) {
+    const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
 
 // Unpack a 16-byte vector of T into floats (N = Vec16<T>::N values).
 template <typename T> __device__ __forceinline__ void unpack16(uint4 v, float* f);
