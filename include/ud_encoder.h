@@ -101,8 +101,8 @@ UD_API int ud_encoder_finalize(ud_encoder* enc);
 /* ---------------------------------------------------------------- streams */
 
 /* Replaces makeStreamState / StreamState (FastConformer.swift:406-435): takes one slot of the
- * encoder's stream pool (K/V ring caches [layers][heads][L][head_dim] and the conv ring
- * [layers][K-1][d_model]), zero-initialised, cache_len 0.  Create and reset wait for all work
+ * encoder's stream pool (K/V ring caches [layers][heads][L + max_chunk][head_dim], frame f in row
+ * f mod (L + max_chunk), and the conv ring [layers][K-1][d_model]), zero-initialised, cache_len 0.  Create and reset wait for all work
  * on the device (hipDeviceSynchronize) before clearing the slot, so a slot freed while a step
  * that used it was still running starts clean.  Destroy only returns the slot to the pool; it
  * does not wait. */
@@ -216,10 +216,11 @@ UD_API int ud_chunked_limited_ranges(int32_t kind, int32_t B, int32_t T, const i
  *   qkv_dev  [n, T, 3*d_model]: q | k_new | v_new per row; fp32, or IEEE half for a 16-bit
  *            (UD_BF16) encoder
  *   att_dev  [n, T, d_model], row-major, in the same format as qkv_dev
- * Keys are [L cached ; T new], range [L - cache_len, L + valid); afterwards the T new K/V rows
- * are in the ring and the logical window is the last L rows.  Does not advance cache_len or the
- * ring position: call ud_stream_advance to commit the step (ud_encoder_step does both).
- * Asynchronous on hip_stream. */
+ * Keys are [L cached ; T new], range [L - cache_len, L + valid).  The T new K/V rows are first
+ * copied from qkv_dev into the rings, next to the cached ones (the step's QKV projection writes
+ * them there directly), then the attention reads the window from the rings.  Does not advance
+ * cache_len or the ring position (a repeated call rewrites the same rows): call
+ * ud_stream_advance to commit the step (ud_encoder_step does both).  Asynchronous on hip_stream. */
 UD_API int ud_layer_attention(ud_encoder* enc, ud_stream* const* streams, int32_t n, int32_t T,
                               int32_t layer, const void* qkv_dev, const int32_t* valid_T_host,
                               void* att_dev, void* hip_stream);
@@ -232,9 +233,9 @@ UD_API int ud_stream_advance(ud_stream* const* streams, int32_t n, int32_t T);
  * Sources/DictatorEngine/Core/Kernels.swift:33-42): uploads the batch descriptor once, then
  * launches the fused attention kernel `iters` times back to back between two HIP events on
  * hip_stream -- launch i on layer (layer + 1 + i) % layers, so that, as in a real step, the ring
- * caches stream from HBM -- and returns the average kernel duration in milliseconds.  Each launch
- * writes the T new rows of qkv_dev into that layer's rings at the stream's current write position
- * (overwriting the T oldest cached rows).  Synchronizes hip_stream. */
+ * caches stream from HBM -- and returns the average kernel duration in milliseconds.  Only the
+ * attention kernel is timed: it reads q from qkv_dev and the window from the rings (whatever the
+ * new rows' ring rows hold) and writes att_dev, nothing else.  Synchronizes hip_stream. */
 UD_API int ud_time_layer_attention(ud_encoder* enc, ud_stream* const* streams, int32_t n, int32_t T,
                                    int32_t layer, const void* qkv_dev, void* att_dev, int32_t iters,
                                    void* hip_stream, float* avg_ms);

@@ -17,10 +17,9 @@
 //  - dot products are reduced inside the LPR-lane row group with DPP; softmax max/sum are wave64
 //    DPP/shuffle reductions; V is staged in LDS and the P.V product is done by threads that own
 //    (query, channel) outputs.
-//  - ring mode: keys are [L cached ; T new]; cached row j lives in ring slot (wpos + j) % L of
-//    the stream's [H][L][dk] cache; after the block loop (every read done) the workgroup writes
-//    its head's T new K/V rows over the T oldest slots.  Each (stream, head) owns its ring slice,
-//    so no other workgroup touches those bytes.
+//  - ring mode: keys are the window [L cached ; T new] of the stream's [H][R][dk] rings, key j in
+//    row (start + j) mod R; the QKV projection (or launch_ring_append) has written the T new rows
+//    before the launch, so the attention kernels only read the rings.
 #include "ud_common.hpp"
 #include "kernels.hpp"
 
@@ -59,22 +58,17 @@ struct OpSrc {
 // Source adaptor: streaming step over one stream's ring caches.
 template <typename T>
 struct RingSrc {
-    const T* kr; const T* vr;      // this (stream, head) ring slice: [L][dk]
-    const T* qkv;                  // first row of this stream in [n*T, 3*D]
+    const T* kr; const T* vr;      // this (stream, head) ring slice: [R][dk]
+    const T* qkv;                  // first row of this stream in [n*T, 3*D] (q columns)
     const T* P; T* O;              // P [n_rel, D]; O = att [n*T, D] (16-bit: fragment-major)
     const float* u; const float* vb;
-    int Tq, Tk, L, D, hoff, wpos, rel_offset, n_rel, ks, ke;
+    int Tq, Tk, R, D, hoff, start, rel_offset, n_rel, ks, ke;
     int64_t row0;                  // global row of this stream's first query
     bool frag;                     // 16-bit output in the fragment-major layout
     __device__ const T* qrow(int i) const { return qkv + (int64_t)i * 3 * D + hoff; }
-    __device__ const T* krow(int j) const {
-        if (j < L) { int s = wpos + j; s -= (s >= L) ? L : 0; return kr + (int64_t)s * 128; }
-        return qkv + (int64_t)(j - L) * 3 * D + D + hoff;
-    }
-    __device__ const T* vrow(int j) const {
-        if (j < L) { int s = wpos + j; s -= (s >= L) ? L : 0; return vr + (int64_t)s * 128; }
-        return qkv + (int64_t)(j - L) * 3 * D + 2 * D + hoff;
-    }
+    // key j < L + T <= R of the window: ring row start + j (< 2R) mod R
+    __device__ const T* krow(int j) const { int s = start + j; s -= (s >= R) ? R : 0; return kr + (int64_t)s * 128; }
+    __device__ const T* vrow(int j) const { int s = start + j; s -= (s >= R) ? R : 0; return vr + (int64_t)s * 128; }
     __device__ const T* prow(int r) const { return P + (int64_t)r * D + hoff; }
     // The output feeds linear_out: 16-bit goes fragment-major (the GEMM's operand order).
     __device__ void store(int i, int d, float v) const {
@@ -255,10 +249,10 @@ __global__ __launch_bounds__(256) void relpos_ring_kernel(RingArgs a) {
     constexpr int DK = 128;
     const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
     const int32_t* d = a.desc + s * DESC_INTS;
-    const int slot = d[0], wpos = d[1], valid = d[2], cache_len = d[3];
+    const int slot = d[0], start = d[1], valid = d[2], cache_len = d[3];
     const int D = a.H * DK;
-    const T* kr = static_cast<const T*>(a.kring) + ((int64_t)slot * a.H + h) * a.L * DK;
-    const T* vr = static_cast<const T*>(a.vring) + ((int64_t)slot * a.H + h) * a.L * DK;
+    const T* kr = static_cast<const T*>(a.kring) + ((int64_t)slot * a.H + h) * a.R * DK;
+    const T* vr = static_cast<const T*>(a.vring) + ((int64_t)slot * a.H + h) * a.R * DK;
     const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)s * a.T * 3 * D;
 
     RingSrc<T> src;
@@ -268,24 +262,32 @@ __global__ __launch_bounds__(256) void relpos_ring_kernel(RingArgs a) {
     src.row0 = (int64_t)s * a.T;
     src.frag = a.att_frag != 0;
     src.u = a.u + h * DK; src.vb = a.vb + h * DK;
-    src.Tq = a.T; src.Tk = a.L + a.T; src.L = a.L; src.D = D; src.hoff = h * DK;
-    src.wpos = wpos; src.rel_offset = a.rel_offset; src.n_rel = a.n_rel;
+    src.Tq = a.T; src.Tk = a.L + a.T; src.R = a.R; src.D = D; src.hoff = h * DK;
+    src.start = start; src.rel_offset = a.rel_offset; src.n_rel = a.n_rel;
     src.ks = a.L - cache_len;
     src.ke = a.L + min(max(valid, 0), a.T);
     relpos_core<T, DK, TQ, KB>(src, a.scale);
+}
 
-    // Commit: the T new rows replace the T oldest ring slots (logical keys 0..T-1, all read above).
-    __syncthreads();
-    constexpr int VEC = Vec16<T>::N, LPR = DK / VEC;
-    T* kw = static_cast<T*>(a.kring) + ((int64_t)slot * a.H + h) * a.L * DK;
-    T* vw = static_cast<T*>(a.vring) + ((int64_t)slot * a.H + h) * a.L * DK;
+// The T new K/V rows of every stream, qkv -> ring rows (start + L + i) mod R; one workgroup per
+// (stream, head), 16 bytes per lane.
+template <typename T>
+__global__ __launch_bounds__(256) void ring_append_kernel(RingArgs a) {
+    constexpr int DK = 128, VEC = Vec16<T>::N, LPR = DK / VEC;
+    const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
+    const int32_t* d = a.desc + s * DESC_INTS;
+    const int slot = d[0], start = d[1];
+    const int D = a.H * DK;
+    const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)s * a.T * 3 * D + h * DK;
+    T* kw = static_cast<T*>(a.kring) + ((int64_t)slot * a.H + h) * a.R * DK;
+    T* vw = static_cast<T*>(a.vring) + ((int64_t)slot * a.H + h) * a.R * DK;
     for (int idx = threadIdx.x; idx < a.T * LPR; idx += 256) {
-        int t = idx / LPR, c = (idx % LPR) * VEC;
-        int slot_row = wpos + t;
-        slot_row -= (slot_row >= a.L) ? a.L : 0;
-        const T* q = qkv + (int64_t)t * 3 * D + h * DK + c;
-        st16(kw + (int64_t)slot_row * DK + c, ld16(q + D));
-        st16(vw + (int64_t)slot_row * DK + c, ld16(q + 2 * D));
+        const int i = idx / LPR, c = (idx % LPR) * VEC;
+        int row = start + a.L + i;               // < 2R
+        row -= (row >= a.R) ? a.R : 0;
+        const T* q = qkv + (int64_t)i * 3 * D + c;
+        st16(kw + (int64_t)row * DK + c, ld16(q + D));
+        st16(vw + (int64_t)row * DK + c, ld16(q + 2 * D));
     }
 }
 
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(256) void relpos_ring_kernel(RingArgs a) {
 // kernel built for one memory round trip.  It works on the whole window [L cached ; T new] and on
 // the whole positional band of the chunk (rel = 1-T .. L+T-1, the same rows for every stream), so
 // the addresses of q, u/v and the band depend only on the launch, and those of K/V only on the
-// stream's ring slot and position (read first, from a 32-byte descriptor).  Every load is
+// stream's ring slot and window start (read first, from a 32-byte descriptor).  Every load is
 // unconditional -- lanes past the window read a clamped row and are masked later -- so all of a
 // workgroup's loads issue back to back with no wait in between, and bd is computed from the
 // L2-resident band while K and V still arrive.  The key range [L - cache_len, L + valid) is a mask
@@ -303,7 +305,7 @@ __global__ __launch_bounds__(256) void relpos_ring_kernel(RingArgs a) {
 // Reductions: the TQ partial dot products of a 16-lane row group are reduced together with a
 // transposed DPP butterfly; P.V is reduced over the 4 row groups of a wave with
 // v_permlane32_swap / v_permlane16_swap (each lane keeps a quarter of the sums) and over the 4
-// waves once through LDS.  The T new K/V rows are committed from the registers that loaded them.
+// waves once through LDS.
 
 // DPP row rotation (within 16 lanes) by R.
 template <int R> __device__ __forceinline__ float dpp_ror(float v) {
@@ -346,61 +348,37 @@ template <int Q> __device__ __forceinline__ int tsum16_index(int lane) {
 }
 
 // Window rows of the streaming kernel for one 16-lane group: key j = grp + G k (clamped to W - 1;
-// G = the workgroup's number of groups)
-// is ring row (wpos + j) mod L of the stream's slot while j < L, else new row j - L of the chunk.
+// G = the workgroup's number of groups) is ring row (start + j) mod R of the stream's slot.
 // prepare() needs only the launch and runs while the stream's descriptor is in flight; load() then
-// costs three VALU operations per pass.  Offsets are 32-bit byte offsets from bases that are the
-// same for the whole workgroup (ring: the (slot, head) block; new rows: this head's K/V columns of
-// the stream's chunk), so the loads take a scalar base plus a vector offset.  When L >= 16 (KR - 1)
-// the first KR - 1 passes hold ring rows only; the remaining passes select per lane.
+// costs two VALU operations per pass.  Offsets are 32-bit byte offsets from the (slot, head) block,
+// the same for the whole workgroup, so the loads take a scalar base plus a vector offset.
 template <int KR, int G = 16>
 struct WindowRows {
     int j[KR];
-    uint32_t noff[KR];    // bytes to new row j - L, lane's 8 columns (j >= L only)
-    bool cached[KR];
 
-    __device__ __forceinline__ void prepare(int grp, int sub, int L, int W, int D) {
+    __device__ __forceinline__ void prepare(int grp, int W) {
 #pragma unroll
-        for (int k = 0; k < KR; k++) {
-            j[k] = min(grp + k * G, W - 1);
-            cached[k] = j[k] < L;
-            noff[k] = ((uint32_t)(j[k] - L) * 3u * (uint32_t)D + (uint32_t)sub * 8u) * 2u;
-        }
+        for (int k = 0; k < KR; k++) j[k] = min(grp + k * G, W - 1);
     }
     __device__ __forceinline__ void load(uint4 (&kreg)[KR], uint4 (&vreg)[KR], const f16* kbase, const f16* vbase,
-                                         const f16* knew, const f16* vnew, int wpos, int L, int sub) const {
+                                         int start, int R, int sub) const {
         const char* kb = reinterpret_cast<const char*>(kbase);
         const char* vb = reinterpret_cast<const char*>(vbase);
-        const char* kn = reinterpret_cast<const char*>(knew);
-        const char* vn = reinterpret_cast<const char*>(vnew);
-        // ring byte offsets of the cached keys (rows wpos + j < 2L: one conditional subtraction)
+        // ring byte offsets (rows start + j < 2R: one conditional subtraction)
         uint32_t roff[KR];
 #pragma unroll
         for (int k = 0; k < KR; k++) {
-            const uint32_t r = (uint32_t)(wpos + j[k]);
-            roff[k] = (min(r, r - (uint32_t)L) << 8) | ((uint32_t)sub << 4);
+            const uint32_t r = (uint32_t)(start + j[k]);
+            roff[k] = (min(r, r - (uint32_t)R) << 8) | ((uint32_t)sub << 4);
         }
         // ring rows are read once per step: non-temporal loads
-        const bool ring_only = L >= G * (KR - 1);
-        if (ring_only) {
 #pragma unroll
-            for (int k = 0; k < KR - 1; k++) kreg[k] = ld16_nt(kb + roff[k]);
-        } else {
-#pragma unroll
-            for (int k = 0; k < KR - 1; k++) kreg[k] = ld16_nt(cached[k] ? kb + roff[k] : kn + noff[k]);
-        }
-        kreg[KR - 1] = ld16_nt(cached[KR - 1] ? kb + roff[KR - 1] : kn + noff[KR - 1]);
+        for (int k = 0; k < KR; k++) kreg[k] = ld16_nt(kb + roff[k]);
         // every K load before the first V load: loads complete in issue order, so the scores can
         // start while V is still arriving
         __builtin_amdgcn_sched_barrier(0);
-        if (ring_only) {
 #pragma unroll
-            for (int k = 0; k < KR - 1; k++) vreg[k] = ld16_nt(vb + roff[k]);
-        } else {
-#pragma unroll
-            for (int k = 0; k < KR - 1; k++) vreg[k] = ld16_nt(cached[k] ? vb + roff[k] : vn + noff[k]);
-        }
-        vreg[KR - 1] = ld16_nt(cached[KR - 1] ? vb + roff[KR - 1] : vn + noff[KR - 1]);
+        for (int k = 0; k < KR; k++) vreg[k] = ld16_nt(vb + roff[k]);
     }
 };
 
@@ -444,14 +422,14 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
     // ---- K and V of the window (WindowRows): the launch-only part now, the rest once the
     //      descriptor is here
     WindowRows<KR> win;
-    win.prepare(grp, sub, L, W, D);
+    win.prepare(grp, W);
     __builtin_amdgcn_sched_barrier(0);
-    const int slot = dsc.x, wpos = dsc.y, valid = min(max(dsc.z, 0), Tq), cache_len = dsc.w;
+    const int slot = dsc.x, start = dsc.y, valid = min(max(dsc.z, 0), Tq), cache_len = dsc.w;
     const int ks = L - cache_len, ke = L + valid;
-    T* kbase = static_cast<T*>(a.kring) + ((int64_t)slot * a.H + h) * L * DK;
-    T* vbase = static_cast<T*>(a.vring) + ((int64_t)slot * a.H + h) * L * DK;
+    const T* kbase = static_cast<const T*>(a.kring) + ((int64_t)slot * a.H + h) * a.R * DK;
+    const T* vbase = static_cast<const T*>(a.vring) + ((int64_t)slot * a.H + h) * a.R * DK;
     uint4 kreg[KR], vreg[KR];
-    win.load(kreg, vreg, kbase, vbase, qkvh + D, qkvh + 2 * D, wpos, L, sub);
+    win.load(kreg, vreg, kbase, vbase, start, a.R, sub);
 
     // ---- q + u, q + v, rounded once to IEEE-half pairs: the score products are v_dot2_f32_f16
     //      (two products per instruction, fp32 sum) on the half words of K and the band as loaded
@@ -567,17 +545,6 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
     }
     __syncthreads();
 
-    // ---- commit the T new K/V rows over the T oldest ring slots (every ring read is done)
-#pragma unroll
-    for (int k = 0; k < KR; k++) {
-        const int j = grp + k * G;
-        if (j >= L && j < W) {
-            int rr = wpos + (j - L);
-            rr -= (rr >= L) ? L : 0;
-            st16(kbase + (int64_t)rr * DK + sub * VEC, kreg[k]);
-            st16(vbase + (int64_t)rr * DK + sub * VEC, vreg[k]);
-        }
-    }
     // ---- output rows (0 for an empty key range), 8 channels per thread
     if (tid < Tq * LPR) {
         const int i = tid / LPR;
@@ -634,13 +601,13 @@ __global__ __launch_bounds__(256) void ring_read_floor_kernel(RingArgs a) {
 #pragma unroll
     for (int k = 0; k < PR; k++) r[n++] = ld16(P + (int64_t)min(grp + k * G, NB - 1) * D);
     WindowRows<KR> win;
-    win.prepare(grp, sub, L, W, D);
+    win.prepare(grp, W);
     __builtin_amdgcn_sched_barrier(0);
-    const int slot = dsc.x, wpos = dsc.y;
-    const T* kbase = static_cast<const T*>(a.kring) + ((int64_t)slot * a.H + h) * L * DK;
-    const T* vbase = static_cast<const T*>(a.vring) + ((int64_t)slot * a.H + h) * L * DK;
+    const int slot = dsc.x, start = dsc.y;
+    const T* kbase = static_cast<const T*>(a.kring) + ((int64_t)slot * a.H + h) * a.R * DK;
+    const T* vbase = static_cast<const T*>(a.vring) + ((int64_t)slot * a.H + h) * a.R * DK;
     uint4 kreg[KR], vreg[KR];
-    win.load(kreg, vreg, kbase, vbase, qkvh + D, qkvh + 2 * D, wpos, L, sub);
+    win.load(kreg, vreg, kbase, vbase, start, a.R, sub);
 #pragma unroll
     for (int k = 0; k < KR; k++) r[n++] = kreg[k];
 #pragma unroll
@@ -653,7 +620,7 @@ __global__ __launch_bounds__(256) void ring_read_floor_kernel(RingArgs a) {
 int launch_ring_read_floor(const RingArgs& a, hipStream_t st) {
     const bool band_ok = a.rel_offset + 1 - a.T >= 0 && a.rel_offset + a.L + a.T - 1 < a.n_rel;
     const int kr = (a.L + a.T + 15) / 16, pr = (a.L + 2 * a.T - 1 + 15) / 16;
-    if (a.T > 2 || a.L < 16 || kr > 5 || pr > 5 || !band_ok || a.n < 1) return -2;
+    if (a.T > 2 || a.L < 16 || kr > 5 || pr > 5 || !band_ok || a.n < 1 || a.L + a.T > a.R) return -2;
     hipLaunchKernelGGL((ring_read_floor_kernel<5, 5>), dim3(a.n * a.H), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
@@ -722,7 +689,7 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
     // past the last stream works on stream 0 and stores nothing (no branch around the body).
     const int sx = live ? s : 0;
     const int32_t* d = a.desc + sx * DESC_INTS;
-    const int slot = d[0], wpos = d[1], valid = min(max(d[2], 0), Tq), cache_len = d[3];
+    const int slot = d[0], start = d[1], valid = min(max(d[2], 0), Tq), cache_len = d[3];
 
     // ---- the head's band -> LDS (rows rel_offset + 1 - T + b, b < NB, of P; rel = 1-T .. L+T-1),
     //      then its u and v biases (32 slots each)
@@ -741,15 +708,17 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
         }
     }
     __asm__ volatile("" ::: "memory");          // the band loads stay ahead of the unit's loads
-    // ---- this wave's unit: q, K (B layout) and the first half of V
+    // ---- this wave's unit: q, K (B layout) and the first half of V (K/V rows: the window of the
+    //      ring, the new rows included)
     const int ks = L - cache_len, ke = L + valid;
     const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)sx * Tq * 3 * D + h * 128;
-    T* kring = static_cast<T*>(a.kring) + ((int64_t)slot * H + h) * L * 128;
-    T* vring = static_cast<T*>(a.vring) + ((int64_t)slot * H + h) * L * 128;
-    auto key_row = [&](T* ring, int j, int part) -> const T* {   // part 1: K, 2: V
-        int r = wpos + j;
-        r -= (r >= L) ? L : 0;
-        return j < L ? ring + (int64_t)r * 128 : qkv + (int64_t)(j - L) * 3 * D + part * D;
+    const T* kring = static_cast<const T*>(a.kring) + ((int64_t)slot * H + h) * a.R * 128;
+    const T* vring = static_cast<const T*>(a.vring) + ((int64_t)slot * H + h) * a.R * 128;
+    const int R = a.R;
+    auto key_row = [&](const T* ring, int j) -> const T* {      // window key j < 2R - start
+        int r = start + j;
+        r -= (r >= R) ? R : 0;
+        return ring + (int64_t)r * 128;
     };
     uint4 qraw[4];
 #pragma unroll
@@ -757,13 +726,13 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
     uint4 kb[KT][4];
 #pragma unroll
     for (int t = 0; t < KT; t++) {
-        const T* row = key_row(kring, min(16 * t + col, W - 1), 1);
+        const T* row = key_row(kring, min(16 * t + col, W - 1));
 #pragma unroll
         for (int st = 0; st < 4; st++) kb[t][st] = ld16(row + (4 * st + g) * 8);
     }
     uint4 vr[KMAX / 4];                          // row 4 it + g, 16-byte column col
 #pragma unroll
-    for (int it = 0; it < KMAX / 8; it++) vr[it] = ld16(key_row(vring, min(4 * it + g, W - 1), 2) + col * 8);
+    for (int it = 0; it < KMAX / 8; it++) vr[it] = ld16(key_row(vring, min(4 * it + g, W - 1)) + col * 8);
     // vmcnt(32): the 40 loads of the unit (q 4, K 24, V 12) were issued after the band loads and
     // complete in order, so at most 32 outstanding means the band loads are done; the unit's data
     // keeps arriving under the band product.
@@ -813,20 +782,9 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(aqu[st]), as_f16x8(kb[t][st]), acc, 0, 0, 0);
         sacc[t] = acc;
     }
-    // commit the new K rows (this wave read every ring row it overwrites, above); K's registers
-    // then take the second half of the V window
+    // K's registers take the second half of the V window
 #pragma unroll
-    for (int t = 0; t < KT; t++) {
-        const int j = 16 * t + col;
-        if (live && j >= L && j < W) {
-            int r = wpos + (j - L);
-            r -= (r >= L) ? L : 0;
-#pragma unroll
-            for (int st = 0; st < 4; st++) st16(kring + (int64_t)r * 128 + (4 * st + g) * 8, kb[t][st]);
-        }
-    }
-#pragma unroll
-    for (int it = KMAX / 8; it < KMAX / 4; it++) vr[it] = ld16(key_row(vring, min(4 * it + g, W - 1), 2) + col * 8);
+    for (int it = KMAX / 8; it < KMAX / 4; it++) vr[it] = ld16(key_row(vring, min(4 * it + g, W - 1)) + col * 8);
     wave_lds_fence();
 
     // ---- scores, rel_shift gather, softmax over keys [ks, ke) (16-lane rows hold one query set)
@@ -863,16 +821,6 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
     for (int t = 0; t < KT; t++)
 #pragma unroll
         for (int r = 0; r < 4; r++) sl[4 * g + r][16 * t + col] = pr[t][r] * sm[r];
-    // commit the new V rows
-#pragma unroll
-    for (int it = 0; it < KMAX / 4; it++) {
-        const int j = 4 * it + g;
-        if (live && j >= L && j < W) {
-            int r = wpos + (j - L);
-            r -= (r >= L) ? L : 0;
-            st16(vring + (int64_t)r * 128 + col * 8, vr[it]);
-        }
-    }
     wave_lds_fence();
 
     // ---- out^T = V^T . P^T, one 32-key piece of V at a time through LDS (rows outside [ks, ke)
@@ -928,7 +876,8 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
 
 int launch_relpos_ring_mfma(const RingArgs& a, hipStream_t st) {
     using namespace rm;
-    if (a.T < 1 || a.T > 16 || a.L + a.T > KMAX || a.L + 2 * a.T - 1 > BMAX || a.n < 1 || a.H < 1 || !a.zero_row)
+    if (a.T < 1 || a.T > 16 || a.L + a.T > KMAX || a.L + 2 * a.T - 1 > BMAX || a.n < 1 || a.H < 1 || !a.zero_row ||
+        a.L + a.T > a.R)
         return -2;
     if (a.rel_offset + 1 - a.T < 0 || a.rel_offset + a.L + a.T - 1 >= a.n_rel) return -2;
     const int grid = a.H * ((a.n + NW - 1) / NW);
@@ -1234,8 +1183,15 @@ static int launch_ring_t(const RingArgs& a, hipStream_t st) {
 }
 
 int launch_relpos_ring(const RingArgs& a, bool half_data, hipStream_t st) {
-    if (a.T < 1 || a.T > 16 || a.T > a.L || a.n < 1) return -2;
+    if (a.T < 1 || a.T > 16 || a.T > a.L || a.n < 1 || a.L + a.T > a.R) return -2;
     return half_data ? launch_ring_t<f16>(a, st) : launch_ring_t<float>(a, st);
+}
+
+int launch_ring_append(const RingArgs& a, bool half_data, hipStream_t st) {
+    if (a.T < 1 || a.n < 1 || a.H < 1 || a.L + a.T > a.R) return -2;
+    if (half_data) hipLaunchKernelGGL(ring_append_kernel<f16>, dim3(a.n * a.H), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(ring_append_kernel<float>, dim3(a.n * a.H), dim3(256), 0, st, a);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 }  // namespace ud

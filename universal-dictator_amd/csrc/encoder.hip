@@ -7,9 +7,11 @@
 //    holds bf16-valued weights as IEEE half and computes on the f16 MFMA with half activations,
 //    K/V caches and tables (fp32 accumulation, fp32 residual stream, norms and conv cache), an
 //    fp32 encoder keeps everything in fp32;
-//  - caches are rings updated in place by the attention and conv kernels (no ping-pong copies);
-//    a stream's ring origin is derived from its frame counter, so the host carries one integer
-//    per stream and uploads a small descriptor {slot, ring origins, valid, cache_len} per step;
+//  - caches are rings updated in place (no ping-pong copies): the K/V rings hold L + max_chunk
+//    rows, the QKV projection writes a step's new K/V rows into them and the attention reads its
+//    window from them; the conv ring is updated by the conv kernel.  A stream's ring positions
+//    derive from its frame counter, so the host carries one integer per stream and uploads a
+//    small descriptor {slot, window start, valid, cache_len, conv origin} per step;
 //  - the 24-layer kernel sequence of a step is captured once per (batch size, T, input, output)
 //    into a hipGraph and replayed.
 #include <hip/hip_runtime.h>
@@ -171,10 +173,11 @@ struct ud_encoder {
     bool bf;                        // 16-bit encoder (UD_BF16): half storage, f16 MFMA
     size_t esz;
     int D, H, dk, ff, Kc, L, layers, n_rel, rel_offset, max_rows;
+    int R;                         // K/V ring rows per (slot, head): L + max_chunk
     std::vector<LayerDev> lw;
     // stream pool
     void* kring = nullptr; void* vring = nullptr; float* cring = nullptr;
-    size_t ring_layer_elems = 0;   // slots * H * L * dk
+    size_t ring_layer_elems = 0;   // slots * H * R * dk
     size_t cring_layer_elems = 0;  // slots * (K-1) * D
     std::vector<int> free_slots;
     std::vector<ud_stream*> live;
@@ -273,6 +276,7 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
     e->esz = e->bf ? 2 : 4;
     e->D = c.d_model; e->H = c.heads; e->dk = c.d_model / c.heads; e->ff = c.ff_dim; e->Kc = c.conv_kernel;
     e->L = c.left_context; e->layers = c.layers;
+    e->R = c.left_context + c.max_chunk;
     // makeStreamState: tables over rel = -(maxChunk-1) ... L+maxChunk-1 (FastConformer.swift:433)
     e->rel_offset = c.max_chunk - 1;
     e->n_rel = c.left_context + 2 * c.max_chunk - 1;
@@ -300,7 +304,7 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
         if (!ok) break;
     }
     const size_t slots = c.max_streams;
-    e->ring_layer_elems = slots * e->H * e->L * e->dk;
+    e->ring_layer_elems = slots * e->H * e->R * e->dk;
     e->cring_layer_elems = slots * (e->Kc - 1) * D;
     if (ok) {
         ok &= (e->kring = dev_alloc(e->ring_layer_elems * e->layers * esz)) != nullptr;
@@ -574,7 +578,7 @@ extern "C" UD_API int ud_encoder_finalize(ud_encoder* e) {
 // ---------------------------------------------------------------- streams
 
 static int zero_slot(ud_encoder* e, int slot) {
-    const size_t per = (size_t)e->H * e->L * e->dk, cper = (size_t)(e->Kc - 1) * e->D;
+    const size_t per = (size_t)e->H * e->R * e->dk, cper = (size_t)(e->Kc - 1) * e->D;
     for (int li = 0; li < e->layers; li++) {
         char* kb = static_cast<char*>(e->kring) + ((size_t)li * e->ring_layer_elems + slot * per) * e->esz;
         char* vb = static_cast<char*>(e->vring) + ((size_t)li * e->ring_layer_elems + slot * per) * e->esz;
@@ -592,7 +596,7 @@ extern "C" UD_API int ud_stream_create(ud_encoder* e, ud_stream** out) {
     if (e->free_slots.empty()) return fail(UD_ERR_CAPACITY, "ud_stream_create: all %d stream slots in use", e->cfg.max_streams);
     int slot = e->free_slots.back();
     // The slot may belong to a stream destroyed while a step on another (non-blocking) HIP stream
-    // was still committing its ring rows; wait for all device work before clearing it, or the new
+    // was still writing its ring rows; wait for all device work before clearing it, or the new
     // stream could start with the old one's rows.
     HIPC(hipDeviceSynchronize());
     int rc = zero_slot(e, slot);
@@ -654,7 +658,8 @@ static int upload_desc(ud_encoder* e, ud_stream* const* streams, int n, int T, c
         int v = valid ? valid[i] : T;
         int32_t* di = d + i * DESC_INTS;
         di[0] = streams[i]->slot;
-        di[1] = (int32_t)(streams[i]->frames % e->L);
+        // window start (frames - L) mod R: the oldest cached frame's row (frame f lives in row f mod R)
+        di[1] = (int32_t)(((streams[i]->frames - e->L) % e->R + e->R) % e->R);
         di[2] = v < 0 ? 0 : (v > T ? T : v);
         di[3] = (int32_t)(streams[i]->frames < e->L ? streams[i]->frames : e->L);
         di[4] = (int32_t)(streams[i]->frames % (e->Kc - 1));
@@ -733,15 +738,26 @@ static int enqueue_rows(ud_encoder* e, int s0, int n, int T, const float* x, flo
         if ((rc = resid(w.h, l.ff1_w2, ff, 0.5f, "ff1.linear2"))) return rc;
         // MHSA: res += linear_out(relpos_attention(q, [cache; k], [cache; v]))
         LAUNCH(launch_layernorm(w.res, take(), l.ln[2], l.ln[3], w.z, bf, M, D, ACT_NONE, st), "layernorm");
-        if ((rc = gemm(w.z, l.wqkv, w.qkv, 3 * D, D, 3 * D, EPI_STORE, ACT_NONE, 1.0f, "qkv"))) return rc;
         RingArgs ra{};
         ra.kring = static_cast<char*>(e->kring) + roff;
         ra.vring = static_cast<char*>(e->vring) + roff;
         ra.qkv = w.qkv; ra.P = l.P; ra.u = l.bias_u; ra.vb = l.bias_v; ra.att = w.att; ra.desc = w.desc;
         ra.zero_row = e->zero_row;
-        ra.n = n; ra.T = T; ra.L = e->L; ra.H = e->H; ra.rel_offset = e->rel_offset; ra.n_rel = e->n_rel;
+        ra.n = n; ra.T = T; ra.L = e->L; ra.R = e->R; ra.H = e->H; ra.rel_offset = e->rel_offset;
+        ra.n_rel = e->n_rel;
         ra.scale = 1.0f / std::sqrt((float)e->dk);
         ra.att_frag = bf ? 1 : 0;
+        if (bf) {
+            // q into the qkv buffer, the new K/V rows straight into the rings
+            GemmArgs g{};
+            g.A = w.z; g.W = l.wqkv; g.C = w.qkv; g.M = M; g.N = 3 * D; g.K = D; g.lda = D; g.ldw = D; g.ldc = 3 * D;
+            g.epi = EPI_QKV_RING; g.act = ACT_NONE; g.out_scale = 1.0f; g.ksplit = 1; g.f16 = 1;
+            g.ring = QkvRing{ra.kring, ra.vring, w.desc, T, e->L, e->R, e->H};
+            if ((rc = launch_status(launch_gemm(g, true, st), "qkv"))) return rc;
+        } else {
+            if ((rc = gemm(w.z, l.wqkv, w.qkv, 3 * D, D, 3 * D, EPI_STORE, ACT_NONE, 1.0f, "qkv"))) return rc;
+            LAUNCH(launch_ring_append(ra, false, st), "ring append");
+        }
         LAUNCH(launch_relpos_ring(ra, bf, st), "relpos attention");
         if ((rc = resid(w.att, l.wo, D, 1.0f, "linear_out"))) return rc;
         // Conv module: res += pw2(silu(LN(dwconv([ring; mask(glu(pw1(z)))]))))
@@ -940,7 +956,7 @@ static RingArgs ring_args(ud_encoder* e, int n, int T, int layer, const void* qk
     ra.vring = static_cast<char*>(e->vring) + roff;
     ra.qkv = qkv; ra.P = l.P; ra.u = l.bias_u; ra.vb = l.bias_v; ra.att = att; ra.desc = e->desc_dev;
     ra.zero_row = e->zero_row;
-    ra.n = n; ra.T = T; ra.L = e->L; ra.H = e->H; ra.rel_offset = e->rel_offset; ra.n_rel = e->n_rel;
+    ra.n = n; ra.T = T; ra.L = e->L; ra.R = e->R; ra.H = e->H; ra.rel_offset = e->rel_offset; ra.n_rel = e->n_rel;
     ra.scale = 1.0f / std::sqrt((float)e->dk);
     return ra;
 }
@@ -962,8 +978,10 @@ extern "C" UD_API int ud_layer_attention(ud_encoder* e, ud_stream* const* stream
     if (rc != UD_OK) return rc;
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
     if ((rc = upload_desc(e, streams, n, T, valid_T_host, st)) != UD_OK) return rc;
-    return launch_status(launch_relpos_ring(ring_args(e, n, T, layer, qkv_dev, att_dev), e->bf, st),
-                         "relpos attention");
+    // the chunk's K/V rows from qkv into the rings, then the attention over the ring windows
+    const RingArgs ra = ring_args(e, n, T, layer, qkv_dev, att_dev);
+    if ((rc = launch_status(launch_ring_append(ra, e->bf, st), "ring append")) != UD_OK) return rc;
+    return launch_status(launch_relpos_ring(ra, e->bf, st), "relpos attention");
 }
 
 // Launches `iters` kernels back to back between two HIP events, launch i on layer
@@ -1027,6 +1045,8 @@ static int launch_projection(ud_encoder* e, int which, int layer, int M, hipStre
             g.A = e->h; g.W = l.ff1_w2; g.N = D; g.K = ff; g.out_scale = 0.5f;
             break;
         case UD_PROJ_QKV:
+            // timed with the row-major store of all three parts (the step's split store puts K and V
+            // into the rings instead: the same bytes, and no stream's cache is touched here)
             g.A = e->z; g.W = l.wqkv; g.C = e->qkv; g.N = 3 * D; g.K = D; g.ldc = 3 * D; g.epi = EPI_STORE;
             break;
         case UD_PROJ_LINEAR_OUT:
@@ -1091,12 +1111,13 @@ static int cache_io(ud_stream* s, int layer, float* k, float* v, float* conv, co
     ud_encoder* e = s->enc;
     if (layer < 0 || layer >= e->layers) return fail(UD_ERR_SHAPE, "cache: bad layer %d", layer);
     HIPC(hipDeviceSynchronize());
-    const int L = e->L, H = e->H, dk = e->dk, D = e->D, KC = e->Kc - 1;
-    const size_t per = (size_t)H * L * dk, cper = (size_t)KC * D;
+    const int L = e->L, R = e->R, H = e->H, dk = e->dk, D = e->D, KC = e->Kc - 1;
+    const size_t per = (size_t)H * R * dk, cper = (size_t)KC * D;
     char* kb = static_cast<char*>(e->kring) + ((size_t)layer * e->ring_layer_elems + s->slot * per) * e->esz;
     char* vb = static_cast<char*>(e->vring) + ((size_t)layer * e->ring_layer_elems + s->slot * per) * e->esz;
     float* cb = e->cring + (size_t)layer * e->cring_layer_elems + s->slot * cper;
-    const int wpos = (int)(s->frames % L), cpos = (int)(s->frames % KC);
+    // cache row r (oldest first) = frame frames - L + r = ring row (frames - L + r) mod R
+    const int start = (int)(((s->frames - L) % R + R) % R), cpos = (int)(s->frames % KC);
     std::vector<uint8_t> kr(per * e->esz), vr(per * e->esz);
     std::vector<float> cr(cper);
     auto get = [&](const std::vector<uint8_t>& buf, size_t i) -> float {
@@ -1113,10 +1134,10 @@ static int cache_io(ud_stream* s, int layer, float* k, float* v, float* conv, co
         HIPC(hipMemcpy(cr.data(), cb, cr.size() * 4, hipMemcpyDeviceToHost));
     }
     for (int r = 0; r < L; r++) {
-        const int sl = (wpos + r) % L;
+        const int sl = (start + r) % R;
         for (int h = 0; h < H; h++)
             for (int d = 0; d < dk; d++) {
-                const size_t ri = ((size_t)h * L + sl) * dk + d, li = (size_t)r * D + h * dk + d;
+                const size_t ri = ((size_t)h * R + sl) * dk + d, li = (size_t)r * D + h * dk + d;
                 if (do_import) { put(kr, ri, ik[li]); put(vr, ri, iv[li]); }
                 else { if (k) k[li] = get(kr, ri); if (v) v[li] = get(vr, ri); }
             }

@@ -14,8 +14,10 @@
 //  - ksplit > 1 splits K over workgroups (parallelism for the N = 1024 projections); each split
 //    writes its own fp32 partial slab and the following LayerNorm adds the slabs, in order, to the
 //    residual row it reads anyway -- deterministic, no atomics, no extra kernel.
-// Epilogues: act + bf16 store (row-major for the QKV buffer the attention reads, fragment-major for
-// a following GEMM), fp32 store, in-place fp32 residual accumulate, split-K partial slabs.
+// Epilogues: act + bf16 store (row-major, or fragment-major for a following GEMM), fp32 store,
+// in-place fp32 residual accumulate, split-K partial slabs, and the QKV projection's split store:
+// q row-major into the buffer the attention reads, K and V straight into their K/V ring rows (so
+// the new rows are written once, and the attention kernel only reads the rings).
 #include "ud_common.hpp"
 #include "kernels.hpp"
 
@@ -27,6 +29,19 @@ namespace ud {
 __device__ __forceinline__ int xcd_tile(int bid, int total) {
     if (total % 8 != 0) return bid;
     return (bid % 8) * (total / 8) + bid / 8;
+}
+
+// The 16-bit K/V ring element of the QKV projection's output row m, column n in [D, 3D): row
+// m = s T + i of stream s goes to ring row (start_s + L + i) mod R of its slot, head (n - D) mod D / 128.
+__device__ __forceinline__ uint16_t* qkv_ring_dst(const QkvRing& r, int64_t m, int n) {
+    const int D = r.H * 128;
+    const int s = (int)(m / r.T), i = (int)(m - (int64_t)s * r.T);
+    const int32_t* d = r.desc + s * DESC_INTS;
+    int row = d[1] + r.L + i;                 // start < R and L + i < R: < 2R
+    row -= (row >= r.R) ? r.R : 0;
+    const int c = n - D, part = c >= D ? 1 : 0, cc = c - part * D;
+    uint16_t* base = static_cast<uint16_t*>(part ? r.vring : r.kring);
+    return base + (((int64_t)d[0] * r.H + (cc >> 7)) * r.R + row) * 128 + (cc & 127);
 }
 
 template <int MT, int NT>
@@ -144,6 +159,10 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
                 static_cast<float*>(a.C)[m * a.ldc + n] = apply_act(v, ACT) * a.out_scale;
             } else if constexpr (EPI == EPI_STORE_FRAG) {
                 static_cast<uint16_t*>(a.C)[frag_index(m, n, a.N / 64)] = to16<H>(apply_act(v, ACT) * a.out_scale);
+            } else if constexpr (EPI == EPI_QKV_RING) {
+                const uint16_t x = to16<H>(apply_act(v, ACT) * a.out_scale);
+                if (n < a.ring.H * 128) static_cast<uint16_t*>(a.C)[m * a.ldc + n] = x;
+                else *qkv_ring_dst(a.ring, m, n) = x;
             } else {
                 static_cast<uint16_t*>(a.C)[m * a.ldc + n] = to16<H>(apply_act(v, ACT) * a.out_scale);
             }
@@ -347,7 +366,11 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
                 uint2 o;
                 o.x = (uint32_t)to16<H>(act_fast<ACT>(v[0]) * a.out_scale) | ((uint32_t)to16<H>(act_fast<ACT>(v[1]) * a.out_scale) << 16);
                 o.y = (uint32_t)to16<H>(act_fast<ACT>(v[2]) * a.out_scale) | ((uint32_t)to16<H>(act_fast<ACT>(v[3]) * a.out_scale) << 16);
-                bf16* dst = static_cast<bf16*>(a.C) + (EPI == EPI_STORE_FRAG ? frag_index(m, n, a.N / 64) : m * a.ldc + n);
+                bf16* dst;
+                if constexpr (EPI == EPI_QKV_RING)   // 4 columns of one head: contiguous in the ring row
+                    dst = n < a.ring.H * 128 ? static_cast<bf16*>(a.C) + m * a.ldc + n : qkv_ring_dst(a.ring, m, n);
+                else
+                    dst = static_cast<bf16*>(a.C) + (EPI == EPI_STORE_FRAG ? frag_index(m, n, a.N / 64) : m * a.ldc + n);
                 *reinterpret_cast<uint2*>(dst) = o;
             }
         }
@@ -551,6 +574,7 @@ static int launch_lds_act(const GemmArgs& a, int ks, hipStream_t st) {
         case EPI_STORE_F32: return launch_lds_epi<NT, EPI_STORE_F32, H>(a, ks, st);
         case EPI_STORE_FRAG: return launch_lds_epi<NT, EPI_STORE_FRAG, H>(a, ks, st);
         case EPI_STORE: return launch_lds_epi<NT, EPI_STORE, H>(a, ks, st);
+        case EPI_QKV_RING: return launch_lds_cfg<NT, EPI_QKV_RING, ACT_NONE, H>(a, ks, st);
         default: return -2;
     }
 }
@@ -658,6 +682,9 @@ static int launch_16(const GemmArgs& a, int ks, hipStream_t st) {
             case EPI_STORE:
                 if (a.N % 32 == 0 && a.K % 512 == 0) return launch_act<4, 8, 2, EPI_STORE, H>(a, ks, st);
                 break;
+            case EPI_QKV_RING:
+                if (a.N % 32 == 0 && a.K % 512 == 0) return launch_bf16_cfg<4, 8, 2, EPI_QKV_RING, ACT_NONE, H>(a, ks, st);
+                break;
             case EPI_STORE_F32:
                 if (a.N % 32 == 0 && a.K % 512 == 0) return launch_act<2, 8, 2, EPI_STORE_F32, H>(a, ks, st);
                 break;
@@ -686,6 +713,7 @@ static int launch_16(const GemmArgs& a, int ks, hipStream_t st) {
         case EPI_STORE_F32: return launch_act<8, 2, 1, EPI_STORE_F32, H>(a, ks, st);
         case EPI_STORE_FRAG: return launch_act<8, 2, 1, EPI_STORE_FRAG, H>(a, ks, st);
         case EPI_STORE: return launch_act<8, 2, 1, EPI_STORE, H>(a, ks, st);
+        case EPI_QKV_RING: return launch_bf16_cfg<8, 2, 1, EPI_QKV_RING, ACT_NONE, H>(a, ks, st);
         default: return -2;
     }
 }
@@ -703,6 +731,14 @@ static int launch_bf16(const GemmArgs& a, int ks, hipStream_t st) {
 
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st) {
     if (a.M <= 0 || a.N <= 0 || a.K <= 0) return -2;
+    if (a.epi == EPI_QKV_RING) {
+        // 16-bit only, no activation; the rows are whole streams of T frames; every ring row written
+        // is outside the step's window (L + T <= R)
+        const QkvRing& r = a.ring;
+        if (!bf16_data || a.act != ACT_NONE || a.bias || !r.kring || !r.vring || !r.desc || r.T < 1 || r.H < 1 ||
+            a.N != 3 * r.H * 128 || a.M % r.T != 0 || r.L + r.T > r.R || a.ldc < r.H * 128)
+            return -2;
+    }
     if (!bf16_data) {
         if (a.epi == EPI_STORE_FRAG) return -2;
         const int ks = a.epi == EPI_PARTIAL ? a.ksplit : 1;

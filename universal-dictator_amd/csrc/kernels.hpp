@@ -12,9 +12,16 @@ namespace ud {
 // Activation codes (Sources/DictatorEngine/Core/Kernels.swift:4-6).
 enum Act : int { ACT_NONE = 0, ACT_RELU = 1, ACT_SILU = 2 };
 
-// Per-stream step descriptor, int32 x8: {pool slot, K/V ring origin (frames appended so far mod L),
-// valid frames this step, cached frames (min(frames, L)), conv ring origin (frames mod (K-1)),
-// 0, 0, 0}.  32 bytes: one scalar load per workgroup.
+// Per-stream step descriptor, int32 x8: {pool slot, K/V window start ((frames - L) mod R), valid
+// frames this step, cached frames (min(frames, L)), conv ring origin (frames mod (K-1)), 0, 0, 0}.
+// 32 bytes: one scalar load per workgroup.
+//
+// K/V rings: each (slot, head) holds R = L + max_chunk rows of 128 values; frame f of the stream
+// lives in row f mod R.  A step over frames F .. F+T-1 (T <= max_chunk) attends to the window of
+// keys j = 0 .. L+T-1 = frames F-L+j, rows (start + j) mod R with start = (F - L) mod R: the L
+// cached frames and the T new ones, which the QKV projection has already written to rows
+// (F + i) mod R -- with R >= L + T they overwrite no row of the window.  The attention kernels only
+// read the rings.
 constexpr int DESC_INTS = 8;
 
 // ---------------------------------------------------------------- attention
@@ -38,18 +45,22 @@ struct DenseArgs {
 int launch_relpos_dense(const DenseArgs& a, hipStream_t st);
 
 struct RingArgs {
-    void* kring; void* vring;       // layer base of the pool: [slots][H][L][128]
-    const void* qkv;                // [n*T, 3*D]
+    void* kring; void* vring;       // layer base of the pool: [slots][H][R][128]
+    const void* qkv;                // [n*T, 3*D]: the attention kernels read q (columns 0..D-1);
+                                    // launch_ring_append reads K and V
     const void* P;                  // [n_rel, D]
     const float* u; const float* vb;   // [H*128]
     void* att;                      // [n*T, D]: row-major, or fragment-major when att_frag (bf16)
     const int32_t* desc;            // [n][DESC_INTS]
     const void* zero_row;           // >= 256 zero bytes, 16-byte aligned (masked rows' loads)
-    int n, T, L, H, rel_offset, n_rel;
+    int n, T, L, R, H, rel_offset, n_rel;
     float scale;
     int att_frag;
 };
 int launch_relpos_ring(const RingArgs& a, bool bf16_data, hipStream_t st);
+// Copies the T new K/V rows of every stream from qkv into rows (start + L + i) mod R of its rings
+// (for callers whose K/V come in a qkv buffer rather than from the fused QKV projection).
+int launch_ring_append(const RingArgs& a, bool half_data, hipStream_t st);
 // Read floor of the bf16 streaming kernel (chunks of <= 2 frames, L + T <= 80): its loads only.
 int launch_ring_read_floor(const RingArgs& a, hipStream_t st);
 
@@ -71,7 +82,16 @@ enum Epi : int {
     EPI_RESID = 1,      // C[m,n] += out_scale * acc   (C fp32 residual, in place)
     EPI_STORE_F32 = 3,  // C[m,n] = act(acc) * out_scale as fp32, row-major
     EPI_STORE_FRAG = 4, // as EPI_STORE but bf16 in fragment-major layout (the next GEMM's A)
-    EPI_PARTIAL = 5     // C[kz][m][n] = out_scale * (K-split kz partial), fp32; slabs M*ldc apart
+    EPI_PARTIAL = 5,    // C[kz][m][n] = out_scale * (K-split kz partial), fp32; slabs M*ldc apart
+    EPI_QKV_RING = 6    // 16-bit QKV projection (N = 3 D): columns < D (q) as EPI_STORE, K and V
+                        // into their K/V ring rows (GemmArgs::ring)
+};
+// Where EPI_QKV_RING puts K and V: row m = stream s * T + i goes to ring row (start_s + L + i) mod R
+// of the stream's slot (descriptor s), head (n - D) mod D / 128.
+struct QkvRing {
+    void* kring; void* vring;       // layer base of the pool: [slots][H][R][128]
+    const int32_t* desc;            // [streams][DESC_INTS]
+    int T, L, R, H;
 };
 // bf16: A [M, K] and W [N, K] in fragment-major layout (lda/ldw unused); M may be any size, the
 // A buffer holding ceil(M/16)*16 rows.  fp32: row-major with leading dimensions lda/ldw/ldc.
@@ -85,6 +105,7 @@ struct GemmArgs {
                                     // IEEE-half path (required); not the bf16 path
     int f16;                        // 16-bit path: operands (and 16-bit outputs) are IEEE half
                                     // instead of bf16
+    QkvRing ring;                   // EPI_QKV_RING only
 };
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st);
 // fp32 GEMM for few rows (tens) on the fp32 MFMA: EPI_PARTIAL with ks K splits (slabs
