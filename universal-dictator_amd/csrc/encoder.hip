@@ -186,7 +186,8 @@ struct ud_encoder {
     float* pw = nullptr;
     float* part = nullptr;          // split-K residual partial slabs [KSPLIT][max_rows][D]
     void* zero_row = nullptr;       // 256 zero bytes: the attention kernels' loads of masked rows
-    int32_t* desc_dev = nullptr;
+    int32_t* desc_dev = nullptr;   // [slots][DESC_INTS] descriptors, then the QKV ring-row table
+    int32_t* rows_dev = nullptr;   // [slots * max_chunk + 256]: ring element offset of each step row
     int32_t* desc_host[4] = {};
     hipEvent_t desc_ev[4] = {};
     bool desc_used[4] = {};
@@ -250,6 +251,12 @@ static void free_encoder(ud_encoder* e) {
     if (e->fork_ev) (void)hipEventDestroy(e->fork_ev);
     for (ud_stream* s : e->live) delete s;
     delete e;
+}
+
+// Descriptor region: [slots][DESC_INTS], then the ring-row table of up to slots * max_chunk step
+// rows, padded by 256 entries (a GEMM tile's row-table load may run past the last row).
+static size_t desc_ints(const ud_encoder* e) {
+    return (size_t)e->cfg.max_streams * DESC_INTS + (size_t)e->cfg.max_streams * e->cfg.max_chunk + 256;
 }
 
 extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder** out) {
@@ -321,11 +328,12 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
         ok &= (e->att = dev_alloc(Rp * D * esz)) != nullptr;
         ok &= (e->pw = (float*)dev_alloc(R * 2 * D * 4)) != nullptr;
         if (e->bf) ok &= (e->part = (float*)dev_alloc(KSPLIT * R * D * 4)) != nullptr;
-        ok &= (e->desc_dev = (int32_t*)dev_alloc(slots * DESC_INTS * 4)) != nullptr;
+        ok &= (e->desc_dev = (int32_t*)dev_alloc(desc_ints(e) * 4)) != nullptr;
+        if (ok) e->rows_dev = e->desc_dev + slots * DESC_INTS;
         ok &= (e->zero_row = dev_alloc(256)) != nullptr;
     }
     for (int i = 0; ok && i < 4; i++) {
-        ok &= hipHostMalloc((void**)&e->desc_host[i], slots * DESC_INTS * 4, hipHostMallocDefault) == hipSuccess;
+        ok &= hipHostMalloc((void**)&e->desc_host[i], desc_ints(e) * 4, hipHostMallocDefault) == hipSuccess;
         ok &= hipEventCreateWithFlags(&e->desc_ev[i], hipEventDisableTiming) == hipSuccess;
     }
     if (!ok) {
@@ -648,12 +656,14 @@ static int check_batch(ud_encoder* e, ud_stream* const* streams, int n, int T, c
     return UD_OK;
 }
 
-// Writes the batch descriptor into the next pinned staging buffer and copies it to the device.
+// Writes the batch descriptor and the QKV projection's ring-row table into the next pinned staging
+// buffer and copies both to the device.
 static int upload_desc(ud_encoder* e, ud_stream* const* streams, int n, int T, const int32_t* valid, hipStream_t st) {
     const int k = e->desc_next;
     e->desc_next = (k + 1) % 4;
     if (e->desc_used[k]) HIPC(hipEventSynchronize(e->desc_ev[k]));
     int32_t* d = e->desc_host[k];
+    int32_t* rows = d + (size_t)e->cfg.max_streams * DESC_INTS;
     for (int i = 0; i < n; i++) {
         int v = valid ? valid[i] : T;
         int32_t* di = d + i * DESC_INTS;
@@ -664,8 +674,13 @@ static int upload_desc(ud_encoder* e, ud_stream* const* streams, int n, int T, c
         di[3] = (int32_t)(streams[i]->frames < e->L ? streams[i]->frames : e->L);
         di[4] = (int32_t)(streams[i]->frames % (e->Kc - 1));
         di[5] = di[6] = di[7] = 0;
+        // step row i T + t (frame frames + t) -> element offset of its ring row in the slot's head-0
+        // block: (slot H R + (start + L + t) mod R) * 128
+        for (int t = 0; t < T; t++)
+            rows[(size_t)i * T + t] = (int32_t)(((int64_t)di[0] * e->H * e->R + (di[1] + e->L + t) % e->R) * e->dk);
     }
-    HIPC(hipMemcpyAsync(e->desc_dev, d, (size_t)n * DESC_INTS * 4, hipMemcpyHostToDevice, st));
+    HIPC(hipMemcpyAsync(e->desc_dev, d, ((size_t)e->cfg.max_streams * DESC_INTS + (size_t)n * T) * 4,
+                        hipMemcpyHostToDevice, st));
     HIPC(hipEventRecord(e->desc_ev[k], st));
     e->desc_used[k] = true;
     return UD_OK;
@@ -678,7 +693,7 @@ static int upload_desc(ud_encoder* e, ud_stream* const* streams, int n, int T, c
 // like the row-major buffers').  The split-K slabs of the group are [ks][n*T][D] at
 // KSPLIT * r0 * D, disjoint from every other group's.
 struct Ws {
-    float* res; void* z; void* h; void* qkv; void* att; float* pw; float* part; int32_t* desc;
+    float* res; void* z; void* h; void* qkv; void* att; float* pw; float* part; int32_t* desc; int32_t* rows;
 };
 static Ws ws_view(ud_encoder* e, int s0, int T) {
     const size_t r0 = (size_t)s0 * T, D = e->D, esz = e->esz;
@@ -691,6 +706,7 @@ static Ws ws_view(ud_encoder* e, int s0, int T) {
     w.pw = e->pw + r0 * 2 * D;
     w.part = e->part ? e->part + (size_t)KSPLIT * r0 * D : nullptr;
     w.desc = e->desc_dev + (size_t)s0 * DESC_INTS;
+    w.rows = e->rows_dev + r0;
     return w;
 }
 
@@ -752,7 +768,7 @@ static int enqueue_rows(ud_encoder* e, int s0, int n, int T, const float* x, flo
             GemmArgs g{};
             g.A = w.z; g.W = l.wqkv; g.C = w.qkv; g.M = M; g.N = 3 * D; g.K = D; g.lda = D; g.ldw = D; g.ldc = 3 * D;
             g.epi = EPI_QKV_RING; g.act = ACT_NONE; g.out_scale = 1.0f; g.ksplit = 1; g.f16 = 1;
-            g.ring = QkvRing{ra.kring, ra.vring, w.desc, T, e->L, e->R, e->H};
+            g.ring = QkvRing{ra.kring, ra.vring, w.rows, T, e->L, e->R, e->H};
             if ((rc = launch_status(launch_gemm(g, true, st), "qkv"))) return rc;
         } else {
             if ((rc = gemm(w.z, l.wqkv, w.qkv, 3 * D, D, 3 * D, EPI_STORE, ACT_NONE, 1.0f, "qkv"))) return rc;

@@ -31,17 +31,20 @@ __device__ __forceinline__ int xcd_tile(int bid, int total) {
     return (bid % 8) * (total / 8) + bid / 8;
 }
 
-// The 16-bit K/V ring element of the QKV projection's output row m, column n in [D, 3D): row
-// m = s T + i of stream s goes to ring row (start_s + L + i) mod R of its slot, head (n - D) mod D / 128.
-__device__ __forceinline__ uint16_t* qkv_ring_dst(const QkvRing& r, int64_t m, int n) {
+// The 16-bit K/V ring element of a QKV projection output in column n of [D, 3D), for an output row
+// whose ring row starts at element rowoff of the slot's head-0 block (QkvRing::rows): K for
+// n < 2D, V above, head (n - D) mod D / 128.
+__device__ __forceinline__ uint16_t* qkv_ring_dst(const QkvRing& r, int rowoff, int n) {
     const int D = r.H * 128;
-    const int s = (int)(m / r.T), i = (int)(m - (int64_t)s * r.T);
-    const int32_t* d = r.desc + s * DESC_INTS;
-    int row = d[1] + r.L + i;                 // start < R and L + i < R: < 2R
-    row -= (row >= r.R) ? r.R : 0;
     const int c = n - D, part = c >= D ? 1 : 0, cc = c - part * D;
     uint16_t* base = static_cast<uint16_t*>(part ? r.vring : r.kring);
-    return base + (((int64_t)d[0] * r.H + (cc >> 7)) * r.R + row) * 128 + (cc & 127);
+    return base + rowoff + (int64_t)(cc >> 7) * r.R * 128 + (cc & 127);
+}
+
+// 16 bytes of the QKV ring-row table per lane, global -> LDS at dst + 16 * lane (a plain function:
+// the builtin written in a kernel template's body drops the host stub of some instantiations).
+__device__ __forceinline__ void lds_direct16_rows(const int32_t* src, int32_t* dst) {
+    __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
 template <int MT, int NT>
@@ -101,6 +104,13 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
 
     const bf16* A = static_cast<const bf16*>(a.A);
     const bf16* W = static_cast<const bf16*>(a.W);
+    // QKV split store: the ring offsets of the workgroup's 16 MT rows, into LDS (read in the
+    // epilogue, after the workgroup barrier); the table is padded past the last row
+    __shared__ __attribute__((aligned(16))) int32_t rtab[EPI == EPI_QKV_RING ? 16 * MT : 4];
+    if constexpr (EPI == EPI_QKV_RING) {
+        if (wave == 0 && lane < 4 * MT)
+            lds_direct16_rows(a.ring.rows + mb * 16 * MT + 4 * lane, rtab);
+    }
     const bf16* ap[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
@@ -162,7 +172,7 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
             } else if constexpr (EPI == EPI_QKV_RING) {
                 const uint16_t x = to16<H>(apply_act(v, ACT) * a.out_scale);
                 if (n < a.ring.H * 128) static_cast<uint16_t*>(a.C)[m * a.ldc + n] = x;
-                else *qkv_ring_dst(a.ring, m, n) = x;
+                else *qkv_ring_dst(a.ring, rtab[mt * 16 + g * 4 + i2], n) = x;
             } else {
                 static_cast<uint16_t*>(a.C)[m * a.ldc + n] = to16<H>(apply_act(v, ACT) * a.out_scale);
             }
@@ -178,6 +188,7 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
         for (int j = 0; j < NT; j++)
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) red[wave][j][mt][lane] = acc[j][mt];
+        if constexpr (EPI == EPI_QKV_RING) __builtin_amdgcn_s_waitcnt(0x0F70);   // the row table landed
         __syncthreads();
         for (int idx = wave; idx < NT * MT; idx += WK) {
             const int j = idx / MT, mt = idx % MT;
@@ -187,6 +198,10 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
             finish(j, mt, v);
         }
     } else {
+        if constexpr (EPI == EPI_QKV_RING) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the row table's direct load landed
+            __syncthreads();
+        }
 #pragma unroll
         for (int j = 0; j < NT; j++)
 #pragma unroll
@@ -253,6 +268,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
     constexpr int MT = 8, BB = 4 * NT;                       // W blocks (16 columns each) per tile
     constexpr int STAGE = (16 + BB) * 1024, CPW = 4 + NT;    // CPW: 1 KB copies per wave per chunk
     __shared__ __attribute__((aligned(16))) bf16 lds[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) int32_t rtab[EPI == EPI_QKV_RING ? 256 : 4];   // QKV: ring row offsets
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3;
@@ -310,6 +326,10 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
                     asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
                                  : "+a"(acc[j][i]) : "v"(as_bf16x8(fb[j])), "v"(as_bf16x8(fa[i])));
     };
+    // QKV split store: the ring offsets of the tile's 256 rows (the table is padded past the last row)
+    if constexpr (EPI == EPI_QKV_RING) {
+        if (wave == 0) lds_direct16_rows(a.ring.rows + mb * 256 + 4 * lane, rtab);
+    }
     copy_chunk(0, lds);
     __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0): this wave's direct loads landed
     __syncthreads();
@@ -368,7 +388,8 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
                 o.y = (uint32_t)to16<H>(act_fast<ACT>(v[2]) * a.out_scale) | ((uint32_t)to16<H>(act_fast<ACT>(v[3]) * a.out_scale) << 16);
                 bf16* dst;
                 if constexpr (EPI == EPI_QKV_RING)   // 4 columns of one head: contiguous in the ring row
-                    dst = n < a.ring.H * 128 ? static_cast<bf16*>(a.C) + m * a.ldc + n : qkv_ring_dst(a.ring, m, n);
+                    dst = n < a.ring.H * 128 ? static_cast<bf16*>(a.C) + m * a.ldc + n
+                                             : qkv_ring_dst(a.ring, rtab[(wm * MT + i) * 16 + r16], n);
                 else
                     dst = static_cast<bf16*>(a.C) + (EPI == EPI_STORE_FRAG ? frag_index(m, n, a.N / 64) : m * a.ldc + n);
                 *reinterpret_cast<uint2*>(dst) = o;
@@ -735,7 +756,7 @@ int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st) {
         // 16-bit only, no activation; the rows are whole streams of T frames; every ring row written
         // is outside the step's window (L + T <= R)
         const QkvRing& r = a.ring;
-        if (!bf16_data || a.act != ACT_NONE || a.bias || !r.kring || !r.vring || !r.desc || r.T < 1 || r.H < 1 ||
+        if (!bf16_data || a.act != ACT_NONE || a.bias || !r.kring || !r.vring || !r.rows || r.T < 1 || r.H < 1 ||
             a.N != 3 * r.H * 128 || a.M % r.T != 0 || r.L + r.T > r.R || a.ldc < r.H * 128)
             return -2;
     }

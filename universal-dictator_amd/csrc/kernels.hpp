@@ -87,10 +87,11 @@ enum Epi : int {
                         // into their K/V ring rows (GemmArgs::ring)
 };
 // Where EPI_QKV_RING puts K and V: row m = stream s * T + i goes to ring row (start_s + L + i) mod R
-// of the stream's slot (descriptor s), head (n - D) mod D / 128.
+// of the stream's slot, head (n - D) mod D / 128; rows[m] holds that row's element offset in the
+// slot's head-0 block, (slot H R + ring row) * 128 (the host computes it with the descriptor).
 struct QkvRing {
     void* kring; void* vring;       // layer base of the pool: [slots][H][R][128]
-    const int32_t* desc;            // [streams][DESC_INTS]
+    const int32_t* rows;            // [M + 256]: ring element offset per output row (padded)
     int T, L, R, H;
 };
 // bf16: A [M, K] and W [N, K] in fragment-major layout (lda/ldw unused); M may be any size, the
