@@ -87,6 +87,28 @@ UD_API int ud_streamer_recorded(const ud_streamer* s, int32_t id, int32_t which,
 /* Batched steps run and stream chunks processed since creation. */
 UD_API int ud_streamer_stats(const ud_streamer* s, int64_t* batches, int64_t* chunks);
 
+/* Replaces NemotronEncoder.step(mel:nRows:validRows:keepAll:) -> (proj, frames)
+ * (Sources/DictatorCore/Nemotron/NemotronStreamer.swift:6-12; the GPU body
+ * MetalNemotronEncoder.step, Sources/DictatorEngine/Models/Nemotron.swift:74-91) for n streams in
+ * one call, without the streamer's scheduling:
+ *   mel_dev          fp32 [n, mel_rows, 128]: each stream's chunk rows, pre-encode cache rows included
+ *   valid_rows_host  [n] real rows of each chunk (validRows)
+ *   keep_all_host    [n] nonzero for a final chunk (keepAll); NULL = none
+ *   drop_extra       frames dropped after subsampling on every step but a stream's first
+ *                    (NemotronSchedule.dropExtra; a first step drops 0)
+ *   out_frames       kept frames per chunk unless keep_all (NemotronSchedule.outFramesPerChunk)
+ *   proj_dev         fp32 [n, proj_rows, hidden]: stream i's kept joint.enc rows at row 0 on
+ *   frames_host      [n] kept frames: keep_all ? valid_T : min(valid_T, out_frames)
+ * Streams at their first step and the others run as two groups (a subsample, an encoder step and
+ * a projection each), so the call may mix them.  The encoder and decoder are used as by
+ * ud_encoder_subsample / ud_encoder_step / ud_rnnt_project, with scratch owned by the encoder
+ * (calls on one encoder must not overlap).  Asynchronous on hip_stream (frames_host is written
+ * before the call returns). */
+UD_API int ud_nemotron_step(ud_encoder* enc, ud_rnnt* rnnt, ud_stream* const* streams, int32_t n, int32_t mel_rows,
+                            const float* mel_dev, const int32_t* valid_rows_host, const int32_t* keep_all_host,
+                            int32_t drop_extra, int32_t out_frames, float* proj_dev, int32_t proj_rows,
+                            int32_t* frames_host, void* hip_stream);
+
 #ifdef __cplusplus
 }
 #endif

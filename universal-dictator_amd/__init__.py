@@ -133,6 +133,7 @@ def _sig(lib):
         "ud_streamer_tokens": (i, [p, _i32, ip, _i32, ip]),
         "ud_streamer_recorded": (i, [p, _i32, _i32, f, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
         "ud_streamer_stats": (i, [p, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
+        "ud_nemotron_step": (i, [p, p, ctypes.POINTER(_vp), _i32, _i32, p, ip, ip, _i32, _i32, p, _i32, ip, p]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -695,6 +696,22 @@ class Rnnt:
     def project(self, rows, enc, out, hip_stream=None):
         """out [rows, hidden] = joint.enc(enc [rows, enc_dim]); DeviceBuffers of fp32."""
         _check(_lib.ud_rnnt_project(self.handle, int(rows), enc.ptr, out.ptr, hip_stream.ptr if hip_stream else None))
+
+    def nemotron_step(self, enc, streams, mel, mel_rows, valid_rows, keep_all, drop_extra, out_frames, proj,
+                      proj_rows, hip_stream=None):
+        """NemotronEncoder.step for len(streams) streams (include/ud_streamer.h ud_nemotron_step):
+        mel a DeviceBuffer of fp32 [n, mel_rows, 128], proj a DeviceBuffer of fp32
+        [n, proj_rows, hidden]; returns the kept frames per stream."""
+        n = len(streams)
+        vr = np.ascontiguousarray(valid_rows, np.int32)
+        ka = np.ascontiguousarray([1 if k else 0 for k in keep_all], np.int32)
+        fr = np.zeros(n, np.int32)
+        P = ctypes.POINTER(_i32)
+        _check(_lib.ud_nemotron_step(enc.handle, self.handle, _handles(streams), n, int(mel_rows), mel.ptr,
+                                     vr.ctypes.data_as(P), ka.ctypes.data_as(P), int(drop_extra), int(out_frames),
+                                     proj.ptr, int(proj_rows), fr.ctypes.data_as(P),
+                                     hip_stream.ptr if hip_stream else None))
+        return [int(x) for x in fr]
 
     def greedy(self, slots, proj, rows_per_stream, frames, cap=4096, hip_stream=None):
         """Greedy decode: proj a DeviceBuffer of fp32 [len(slots) * rows_per_stream, hidden];

@@ -186,6 +186,8 @@ struct ud_encoder {
     float* pw = nullptr;
     float* part = nullptr;          // split-K residual partial slabs [KSPLIT][max_rows][D]
     void* zero_row = nullptr;       // 256 zero bytes: the attention kernels' loads of masked rows
+    void* aux = nullptr;           // ud_encoder_aux_scratch (host-side callers' device scratch)
+    size_t aux_bytes = 0;
     int32_t* desc_dev = nullptr;   // [slots][DESC_INTS] descriptors, then the QKV ring-row table
     int32_t* rows_dev = nullptr;   // [slots * max_chunk + 256]: ring element offset of each step row
     int32_t* desc_host[4] = {};
@@ -234,7 +236,7 @@ static void free_encoder(ud_encoder* e) {
         for (float* p : l.ln) if (p) (void)hipFree(p);
     }
     void* ws[] = {e->kring, e->vring, e->cring, e->res, e->z, e->h, e->qkv, e->att, e->pw, e->part, e->desc_dev,
-                  e->zero_row};
+                  e->zero_row, e->aux};
     for (void* p : ws) if (p) (void)hipFree(p);
     for (void* p : e->sub.w) if (p) (void)hipFree(p);
     void* sws[] = {e->sub.a2, e->sub.a3, e->sub.a4, e->sub.a5, e->sub.af, e->sub.vlen};
@@ -581,6 +583,19 @@ extern "C" UD_API int ud_encoder_finalize(ud_encoder* e) {
     HIPC(hipDeviceSynchronize());
     e->finalized = true;
     return UD_OK;
+}
+
+// Device scratch of at least `bytes` owned by the encoder (grown on demand, freed with it), for
+// host-side entry points that chain the encoder's calls (ud_nemotron_step).  Growing waits for the
+// device, so no earlier call still uses the old buffer.
+void* ud_encoder_aux_scratch(ud_encoder* e, size_t bytes) {
+    if (e->aux_bytes >= bytes) return e->aux;
+    if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+    if (e->aux) (void)hipFree(e->aux);
+    e->aux_bytes = 0;
+    e->aux = dev_alloc(bytes);
+    if (e->aux) e->aux_bytes = bytes;
+    return e->aux;
 }
 
 // ---------------------------------------------------------------- streams

@@ -6,6 +6,10 @@
 #include <stdint.h>
 
 struct ud_mel;
+struct ud_encoder;
+// Device scratch of at least `bytes` owned by the encoder (grown on demand, freed with it; growing
+// synchronizes the device); nullptr when the allocation fails.
+void* ud_encoder_aux_scratch(ud_encoder* e, size_t bytes);
 
 namespace ud {
 

@@ -503,3 +503,88 @@ extern "C" UD_API int ud_streamer_stats(const ud_streamer* s, int64_t* batches, 
     if (chunks) *chunks = s->chunks;
     return UD_OK;
 }
+
+// ---------------------------------------------------------------- one chunk step, mel -> joint.enc
+
+static int sub3(int t) {
+    for (int k = 0; k < 3; k++) t = t / 2 + 1;   // FastConformer.swift:219, three stride-2 stages
+    return t;
+}
+
+// NemotronEncoder.step (NemotronStreamer.swift:6-12; MetalNemotronEncoder.step, Nemotron.swift:74-91)
+// for n streams at once: streams at their first step subsample with drop 0, the others with
+// drop_extra, each group as one ud_encoder_subsample + ud_encoder_step + ud_rnnt_project; the
+// kept frames (valid_T, capped at out_frames unless keep_all) are copied to the caller's rows.
+extern "C" UD_API int ud_nemotron_step(ud_encoder* enc, ud_rnnt* rnnt, ud_stream* const* streams, int32_t n,
+                                       int32_t mel_rows, const float* mel_dev, const int32_t* valid_rows_host,
+                                       const int32_t* keep_all_host, int32_t drop_extra, int32_t out_frames,
+                                       float* proj_dev, int32_t proj_rows, int32_t* frames_host, void* hip_stream) {
+    if (!enc || !rnnt || !streams || !mel_dev || !valid_rows_host || !proj_dev || !frames_host)
+        return tfail(UD_ERR_INVALID, "ud_nemotron_step: null argument");
+    ud_encoder_config cfg;
+    int rc = ud_encoder_get_config(enc, &cfg);
+    if (rc != UD_OK) return rc;
+    int32_t Hd = 0, V = 0, Lr = 0, E = 0, RS = 0, MS = 0;
+    if ((rc = ud_rnnt_get_info(rnnt, &Hd, &V, &Lr, &E, &RS, &MS)) != UD_OK) return rc;
+    if (n < 1 || n > cfg.max_streams) return tfail(UD_ERR_SHAPE, "ud_nemotron_step: n = %d outside 1..%d", n, cfg.max_streams);
+    if (E != cfg.d_model) return tfail(UD_ERR_SHAPE, "ud_nemotron_step: decoder enc_dim %d != d_model %d", E, cfg.d_model);
+    if (mel_rows < 1 || drop_extra < 0 || out_frames < 1 || proj_rows < 1)
+        return tfail(UD_ERR_SHAPE, "ud_nemotron_step: bad mel_rows / drop_extra / out_frames / proj_rows");
+    // groups: first steps (drop 0) and the rest (drop_extra); each group's frame count must fit
+    std::vector<int> grp[2];
+    for (int i = 0; i < n; i++) {
+        if (!streams[i]) return tfail(UD_ERR_INVALID, "ud_nemotron_step: null stream %d", i);
+        int32_t cl = 0, steps = 0;
+        if ((rc = ud_stream_info(streams[i], &cl, &steps)) != UD_OK) return rc;
+        grp[steps == 0 ? 0 : 1].push_back(i);
+    }
+    for (int g = 0; g < 2; g++) {
+        const int T = sub3(mel_rows) - (g == 0 ? 0 : drop_extra);
+        if (!grp[g].empty() && (T < 1 || T > proj_rows))
+            return tfail(UD_ERR_SHAPE, "ud_nemotron_step: %d mel rows give %d frames (%s steps); proj_rows is %d",
+                         mel_rows, T, g == 0 ? "first" : "later", proj_rows);
+    }
+    // scratch: the group's mel rows, subsampled frames, encoder output, projection
+    constexpr int NM = 128;
+    auto al = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t rows_max = (size_t)n * cfg.max_chunk;
+    const size_t o_x = al((size_t)n * mel_rows * NM * 4), o_y = o_x + al(rows_max * cfg.d_model * 4);
+    const size_t o_p = o_y + al(rows_max * cfg.d_model * 4), total = o_p + al(rows_max * Hd * 4);
+    char* base = static_cast<char*>(ud_encoder_aux_scratch(enc, total));
+    if (!base) return tfail(UD_ERR_NOMEM, "ud_nemotron_step: scratch allocation failed");
+    float* gmel = reinterpret_cast<float*>(base);
+    float* x = reinterpret_cast<float*>(base + o_x);
+    float* y = reinterpret_cast<float*>(base + o_y);
+    float* p = reinterpret_cast<float*>(base + o_p);
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    const size_t chunk = (size_t)mel_rows * NM;
+    for (int g = 0; g < 2; g++) {
+        const std::vector<int>& idx = grp[g];
+        const int ng = (int)idx.size();
+        if (ng == 0) continue;
+        std::vector<int32_t> vmel(ng), vt(ng);
+        std::vector<ud_stream*> hs(ng);
+        for (int j = 0; j < ng; j++) {
+            TCHECK(hipMemcpyAsync(gmel + j * chunk, mel_dev + idx[j] * chunk, chunk * 4, hipMemcpyDeviceToDevice, st),
+                   "ud_nemotron_step: mel gather");
+            vmel[j] = valid_rows_host[idx[j]];
+            hs[j] = streams[idx[j]];
+        }
+        int T = 0;
+        if ((rc = ud_encoder_subsample(enc, ng, mel_rows, gmel, vmel.data(), g == 0 ? 0 : drop_extra, x, &T, vt.data(),
+                                       hip_stream)) != UD_OK)
+            return rc;
+        if ((rc = ud_encoder_step(enc, hs.data(), ng, T, x, vt.data(), y, hip_stream)) != UD_OK) return rc;
+        if ((rc = ud_rnnt_project(rnnt, ng * T, y, p, hip_stream)) != UD_OK) return rc;
+        for (int j = 0; j < ng; j++) {
+            const bool keep_all = keep_all_host && keep_all_host[idx[j]];
+            const int keep = keep_all ? vt[j] : std::min(vt[j], out_frames);
+            frames_host[idx[j]] = keep;
+            if (keep > 0)
+                TCHECK(hipMemcpyAsync(proj_dev + (size_t)idx[j] * proj_rows * Hd, p + (size_t)j * T * Hd,
+                                      (size_t)keep * Hd * 4, hipMemcpyDeviceToDevice, st),
+                       "ud_nemotron_step: projection copy");
+        }
+    }
+    return UD_OK;
+}
