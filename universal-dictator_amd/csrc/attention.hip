@@ -291,9 +291,10 @@ __global__ __launch_bounds__(256) void ring_append_kernel(RingArgs a) {
     }
 }
 
-// ------------------------------------------------------------------ streaming ring kernel (T <= 4)
-// The chunk shapes of streaming (2..4 queries over L + T <= 96 keys, IEEE half, head_dim 128) get a
-// kernel built for one memory round trip.  It works on the whole window [L cached ; T new] and on
+// ------------------------------------------------------------------ streaming ring kernels (T <= 4)
+// The chunk shapes of streaming (2..4 queries over L + T <= 96 keys, IEEE half, head_dim 128) get
+// kernels built for one memory round trip: relpos_ring_small_kernel (T 3..4) below and
+// relpos_ring_wave_kernel (T <= 2) after it.  It works on the whole window [L cached ; T new] and on
 // the whole positional band of the chunk (rel = 1-T .. L+T-1, the same rows for every stream), so
 // the addresses of q, u/v and the band depend only on the launch, and those of K/V only on the
 // stream's ring slot and window start (read first, from a 32-byte descriptor).  Every load is
@@ -571,12 +572,199 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
     }
 }
 
-// Read floor of the streaming kernel's access pattern (relpos_ring_small_kernel, T <= 2): the same
-// grid, the same loads (q, u/v, the band, K and V of the window, through the same addressing), no arithmetic
-// beyond folding the words together, no stores (one store to att[0] on a value that never occurs
-// keeps the loads live).  Its time per launch is what memory alone costs for this shape; the
-// attention kernel is measured against it.
-template <int KR, int PR>
+// Streaming kernel, one-barrier form (T <= 4).  One workgroup (4 waves) per (stream, head); a
+// 16-lane row group owns key j = grp + 16 p (p < KR), 8 channels per lane.  Each group loads, for
+// its keys, the K and V rows and the TQ band rows the keys need (band row W - 1 + i - j for query
+// i: rel_shift as the row index), so each score s_ij = ((q_i + u) . k_j + (q_i + v) . P_row) *
+// scale is complete inside the group (v_dot2_f32_f16 partials, 16-lane DPP sums) with no table
+// shared across waves.  Softmax is online per wave: the wave's running max and sum over its 4
+// groups (lane-swap reductions), P.V on its own V rows (v_fma_mix_f32), and the 4 waves' partial
+// outputs merge once through LDS with the usual max/sum rescaling.  Keys outside [ks, ke) score
+// -inf and their V rows are zeroed by a mask, so they contribute exact zeros.
+template <int TQ, int KR>
+__global__ __launch_bounds__(256) void relpos_ring_wave_kernel(RingArgs a) {
+    using T = f16;
+    constexpr int DK = 128, VEC = 8, G = 16, NV = TQ * VEC, NQ = NV / 4;
+    static_assert(NQ % 4 == 0, "float4 partial sums");
+    __shared__ __align__(16) float red[4][TQ * DK];
+    __shared__ float stat[4][TQ][2];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = tid >> 4, sub = tid & 15, row4 = lane >> 4;
+    const int s = blockIdx.x / a.H, h = blockIdx.x % a.H;
+    const int L = a.L, Tq = a.T, D = a.H * DK, W = L + Tq, NB = L + 2 * Tq - 1;
+    const int4 dsc = *reinterpret_cast<const int4*>(a.desc + s * DESC_INTS);
+    __builtin_amdgcn_sched_barrier(0);
+    const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)s * Tq * 3 * D + h * DK + sub * VEC;
+    // band row b (0 .. NB-1) is table row rel_offset + 1 - T + b
+    const char* Pb = reinterpret_cast<const char*>(static_cast<const T*>(a.P) + (int64_t)(a.rel_offset + 1 - Tq) * D +
+                                                   h * DK + sub * VEC);
+
+    // ---- launch-only loads: q, u/v, the band rows of this group's keys
+    uint4 qreg[TQ];
+#pragma unroll
+    for (int i = 0; i < TQ; i++) qreg[i] = ld16(qkv + (int64_t)min(i, Tq - 1) * 3 * D);
+    const float4 u0 = *reinterpret_cast<const float4*>(a.u + h * DK + sub * VEC);
+    const float4 u1 = *reinterpret_cast<const float4*>(a.u + h * DK + sub * VEC + 4);
+    const float4 v0 = *reinterpret_cast<const float4*>(a.vb + h * DK + sub * VEC);
+    const float4 v1 = *reinterpret_cast<const float4*>(a.vb + h * DK + sub * VEC + 4);
+    uint4 preg[KR][TQ];
+#pragma unroll
+    for (int p = 0; p < KR; p++) {
+        const int j = min(grp + G * p, W - 1);
+#pragma unroll
+        for (int i = 0; i < TQ; i++) {
+            const int b = min(W - 1 + i - j, NB - 1);       // >= 0: j <= W - 1; clamped for i >= T
+            preg[p][i] = ld16(Pb + (int64_t)b * D * 2);
+        }
+    }
+    // ---- K and V rows of the window (ring rows start + j mod R), K first
+    WindowRows<KR> win;
+    win.prepare(grp, W);
+    __builtin_amdgcn_sched_barrier(0);
+    const int slot = dsc.x, start = dsc.y, valid = min(max(dsc.z, 0), Tq), cache_len = dsc.w;
+    const int ks = L - cache_len, ke = L + valid;
+    const T* kbase = static_cast<const T*>(a.kring) + ((int64_t)slot * a.H + h) * a.R * DK;
+    const T* vbase = static_cast<const T*>(a.vring) + ((int64_t)slot * a.H + h) * a.R * DK;
+    uint4 kreg[KR], vreg[KR];
+    win.load(kreg, vreg, kbase, vbase, start, a.R, sub);
+
+    // ---- q + u, q + v rounded once to IEEE-half pairs
+    const float uu[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    half2_t qu2[TQ][VEC / 2], qv2[TQ][VEC / 2];
+#pragma unroll
+    for (int i = 0; i < TQ; i++) {
+        float f[VEC];
+        unpack16<T>(qreg[i], f);
+#pragma unroll
+        for (int e = 0; e < VEC / 2; e++) {
+            qu2[i][e] = half2_t{(f16)(f[2 * e] + uu[2 * e]), (f16)(f[2 * e + 1] + uu[2 * e + 1])};
+            qv2[i][e] = half2_t{(f16)(f[2 * e] + vv[2 * e]), (f16)(f[2 * e + 1] + vv[2 * e + 1])};
+        }
+    }
+    // ---- bd parts (band rows: L2-resident, in before K), then scores; every lane of a group gets
+    //      the group's totals
+    float sc[KR][TQ];
+#pragma unroll
+    for (int p = 0; p < KR; p++)
+#pragma unroll
+        for (int i = 0; i < TQ; i++) {
+            const uint32_t w[4] = {preg[p][i].x, preg[p][i].y, preg[p][i].z, preg[p][i].w};
+            float acc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < VEC / 2; e++) acc = __builtin_amdgcn_fdot2(qv2[i][e], as_half2(w[e]), acc, false);
+            sc[p][i] = acc;
+        }
+    float m[TQ];
+#pragma unroll
+    for (int i = 0; i < TQ; i++) m[i] = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < KR; p++) {
+        const uint32_t w[4] = {kreg[p].x, kreg[p].y, kreg[p].z, kreg[p].w};
+        const int j = grp + G * p;
+        const bool in = j >= ks && j < ke;
+#pragma unroll
+        for (int i = 0; i < TQ; i++) {
+            float acc = sc[p][i];
+#pragma unroll
+            for (int e = 0; e < VEC / 2; e++) acc = __builtin_amdgcn_fdot2(qu2[i][e], as_half2(w[e]), acc, false);
+            const float x = group_sum<16>(acc) * a.scale;
+            sc[p][i] = (in && i < Tq) ? x : -INFINITY;
+            m[i] = fmaxf(m[i], sc[p][i]);
+        }
+    }
+    // ---- wave softmax statistics over the wave's 4 groups (lanes l ^ 16, l ^ 32)
+    float l[TQ];
+#pragma unroll
+    for (int i = 0; i < TQ; i++) {
+        m[i] = xmax32(xmax16(m[i]));
+        l[i] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < KR; p++) {
+            sc[p][i] = sc[p][i] == -INFINITY ? 0.0f : __expf(sc[p][i] - m[i]);
+            l[i] += sc[p][i];
+        }
+    }
+    // ---- P.V on this group's V rows (masked rows zeroed): v_fma_mix_f32 on the half words
+    float acc[NV];
+#pragma unroll
+    for (int f = 0; f < NV; f++) acc[f] = 0.0f;
+#pragma unroll
+    for (int p = 0; p < KR; p++) {
+        const int j = grp + G * p;
+        const uint32_t keep = (j >= ks && j < ke) ? 0xFFFFFFFFu : 0u;
+        const uint32_t w[4] = {vreg[p].x & keep, vreg[p].y & keep, vreg[p].z & keep, vreg[p].w & keep};
+#pragma unroll
+        for (int i = 0; i < TQ; i++) {
+            const float pr = sc[p][i];
+#pragma unroll
+            for (int e = 0; e < VEC / 2; e++) {
+                acc[i * VEC + 2 * e] = fmaf(pr, half_lo(w[e]), acc[i * VEC + 2 * e]);
+                acc[i * VEC + 2 * e + 1] = fmaf(pr, half_hi(w[e]), acc[i * VEC + 2 * e + 1]);
+            }
+        }
+    }
+    // over the 4 row groups of the wave: lane (row4, sub) ends with flat sums row4*NQ .. +NQ-1
+    float h1[NV / 2], h2[NQ];
+#pragma unroll
+    for (int k = 0; k < NV / 2; k++) h1[k] = xsum32(acc[k], acc[k + NV / 2]);
+#pragma unroll
+    for (int k = 0; k < NQ; k++) h2[k] = xsum16(h1[k], h1[k + NQ]);
+#pragma unroll
+    for (int k = 0; k < NQ; k += 4) {
+        const int f = row4 * NQ + k, i = f >> 3, e = f & 7;
+        *reinterpret_cast<float4*>(&red[wave][i * DK + sub * VEC + e]) = make_float4(h2[k], h2[k + 1], h2[k + 2], h2[k + 3]);
+    }
+#pragma unroll
+    for (int i = 0; i < TQ; i++) l[i] = xadd32(xadd16(l[i]));     // every lane: the wave's sums
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < TQ; i++) { stat[wave][i][0] = m[i]; stat[wave][i][1] = l[i]; }
+    }
+    __syncthreads();
+
+    // ---- merge the waves: out_i = sum_w e^(m_w - M) acc_w / sum_w e^(m_w - M) l_w (0 for an empty
+    //      range: every weight is 0); 8 channels per thread, 16-byte stores
+    if (tid < Tq * 16) {
+        const int i = tid >> 4;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; w++) M = fmaxf(M, stat[w][i][0]);
+        float wt[4], Ls = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            wt[w] = stat[w][i][0] == -INFINITY ? 0.0f : __expf(stat[w][i][0] - M);
+            Ls += wt[w] * stat[w][i][1];
+        }
+        const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+        float o[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; e += 4) {
+            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                const float4 x = *reinterpret_cast<const float4*>(&red[w][i * DK + sub * VEC + e]);
+                t.x += wt[w] * x.x; t.y += wt[w] * x.y; t.z += wt[w] * x.z; t.w += wt[w] * x.w;
+            }
+            o[e] = t.x * inv; o[e + 1] = t.y * inv; o[e + 2] = t.z * inv; o[e + 3] = t.w * inv;
+        }
+        uint32_t pk[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) pk[e] = (uint32_t)f2h(o[2 * e]) | ((uint32_t)f2h(o[2 * e + 1]) << 16);
+        const int64_t row = (int64_t)s * Tq + i;
+        T* att = static_cast<T*>(a.att);
+        T* dst = a.att_frag ? att + frag_index(row, h * DK + sub * VEC, D / 64) : att + row * D + h * DK + sub * VEC;
+        st16(dst, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+    }
+}
+
+// Read floor of the streaming kernel's access pattern (relpos_ring_wave_kernel, T <= 2): the same
+// grid, the same loads (q, u/v, each key's band rows, K and V of the window, through the same
+// addressing), no arithmetic beyond folding the words together, no stores (one store to att[0] on
+// a value that never occurs keeps the loads live).  Its time per launch is what memory alone costs
+// for this shape; the attention kernel is measured against it.
+template <int KR>
 __global__ __launch_bounds__(256) void ring_read_floor_kernel(RingArgs a) {
     using T = f16;
     constexpr int TQ = 2, DK = 128, VEC = 8, LPR = 16, G = 16;
@@ -590,7 +778,7 @@ __global__ __launch_bounds__(256) void ring_read_floor_kernel(RingArgs a) {
     const T* P = static_cast<const T*>(a.P) + (int64_t)(a.rel_offset + 1 - Tq) * D + h * DK + sub * VEC;
     uint4 acc = make_uint4(0, 0, 0, 0);
     auto fold = [&](uint4 x) { acc.x ^= x.x; acc.y ^= x.y; acc.z ^= x.z; acc.w ^= x.w; };
-    uint4 r[TQ + 4 + PR + 2 * KR];
+    uint4 r[TQ + 4 + KR * TQ + 2 * KR];
     int n = 0;
 #pragma unroll
     for (int i = 0; i < TQ; i++) r[n++] = ld16(qkv + (int64_t)min(i, Tq - 1) * 3 * D);
@@ -599,7 +787,11 @@ __global__ __launch_bounds__(256) void ring_read_floor_kernel(RingArgs a) {
     r[n++] = *reinterpret_cast<const uint4*>(a.vb + h * DK + sub * VEC);
     r[n++] = *reinterpret_cast<const uint4*>(a.vb + h * DK + sub * VEC + 4);
 #pragma unroll
-    for (int k = 0; k < PR; k++) r[n++] = ld16(P + (int64_t)min(grp + k * G, NB - 1) * D);
+    for (int k = 0; k < KR; k++) {
+        const int j = min(grp + k * G, W - 1);
+#pragma unroll
+        for (int i = 0; i < TQ; i++) r[n++] = ld16(P + (int64_t)min(W - 1 + i - j, NB - 1) * D);
+    }
     WindowRows<KR> win;
     win.prepare(grp, W);
     __builtin_amdgcn_sched_barrier(0);
@@ -613,15 +805,15 @@ __global__ __launch_bounds__(256) void ring_read_floor_kernel(RingArgs a) {
 #pragma unroll
     for (int k = 0; k < KR; k++) r[n++] = vreg[k];
 #pragma unroll
-    for (int i = 0; i < TQ + 4 + PR + 2 * KR; i++) fold(r[i]);
+    for (int i = 0; i < TQ + 4 + KR * TQ + 2 * KR; i++) fold(r[i]);
     if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9E3779B9u && tid == 0) static_cast<T*>(a.att)[0] = (T)1;
 }
 
 int launch_ring_read_floor(const RingArgs& a, hipStream_t st) {
     const bool band_ok = a.rel_offset + 1 - a.T >= 0 && a.rel_offset + a.L + a.T - 1 < a.n_rel;
-    const int kr = (a.L + a.T + 15) / 16, pr = (a.L + 2 * a.T - 1 + 15) / 16;
-    if (a.T > 2 || a.L < 16 || kr > 5 || pr > 5 || !band_ok || a.n < 1 || a.L + a.T > a.R) return -2;
-    hipLaunchKernelGGL((ring_read_floor_kernel<5, 5>), dim3(a.n * a.H), dim3(256), 0, st, a);
+    const int kr = (a.L + a.T + 15) / 16;
+    if (a.T > 2 || a.L < 16 || kr > 5 || !band_ok || a.n < 1 || a.L + a.T > a.R) return -2;
+    hipLaunchKernelGGL((ring_read_floor_kernel<5>), dim3(a.n * a.H), dim3(256), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -1166,8 +1358,8 @@ static int launch_ring_t(const RingArgs& a, hipStream_t st) {
     const bool band_ok = a.rel_offset + 1 - a.T >= 0 && a.rel_offset + a.L + a.T - 1 < a.n_rel;
     if (sizeof(T) == 2 && a.T <= 4 && a.L >= 16 && a.L + a.T <= 96 && a.L + 2 * a.T - 1 <= 112 && band_ok) {
         const int kr = (a.L + a.T + 15) / 16, pr = (a.L + 2 * a.T - 1 + 15) / 16;
-        if (a.T <= 2 && kr <= 5 && pr <= 5) hipLaunchKernelGGL((relpos_ring_small_kernel<2, 5, 5>), grid, block, 0, st, a);
-        else if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_small_kernel<2, 6, 7>), grid, block, 0, st, a);
+        if (a.T <= 2 && kr <= 5) hipLaunchKernelGGL((relpos_ring_wave_kernel<2, 5>), grid, block, 0, st, a);
+        else if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_wave_kernel<2, 6>), grid, block, 0, st, a);
         else if (kr <= 5 && pr <= 5) hipLaunchKernelGGL((relpos_ring_small_kernel<4, 5, 5>), grid, block, 0, st, a);
         else hipLaunchKernelGGL((relpos_ring_small_kernel<4, 6, 7>), grid, block, 0, st, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;
