@@ -671,6 +671,8 @@ def main():
     # The fused attention kernel alone, on the stream it is launched on.
     qkv = ud.DeviceBuffer.from_numpy(ud.f16_bits(rng.standard_normal((S * T, 3 * D), dtype=np.float32)))
     att = ud.DeviceBuffer(S * T * D * 2)
+    # one untimed pass of the same loop first: the timed one then runs at steady clocks
+    enc.time_layer_attention(streams, T, 0, qkv, att, args.attn_iters, hip_stream=hs)
     attn_ms = enc.time_layer_attention(streams, T, 0, qkv, att, args.attn_iters, hip_stream=hs)
     Tk, n_rel = L + T, L + 2 * T - 1
     attn_bytes = S * Tk * H * dk * 2 * 2 + S * 2 * T * H * dk * 2 + n_rel * H * dk * 2 + 2 * H * dk * 4
@@ -679,6 +681,7 @@ def main():
     floor_ms = None
     if T <= 2:
         # the same loads with no arithmetic: what memory alone costs for this launch shape
+        enc.time_ring_read_floor(streams, T, 0, qkv, att, args.attn_iters, hip_stream=hs)
         floor_ms = enc.time_ring_read_floor(streams, T, 0, qkv, att, args.attn_iters, hip_stream=hs)
         log("read floor of the same access pattern: %.2f us/launch, %.0f GB/s"
             % (floor_ms * 1000.0, attn_bytes / (floor_ms / 1000.0) / 1e9))
@@ -721,8 +724,8 @@ def main():
         "attention_steps_per_sec": round(1000.0 / attn_ms, 1),
         "attention_us_per_launch": round(attn_ms * 1000.0, 3),
         "roofline": {
-            "kernel": ("relpos_ring_small_kernel" if T <= 4 else "relpos_ring_mfma_kernel")
-                      + " (fused rel-pos attention + K/V ring commit)",
+            "kernel": ("relpos_ring_wave_kernel" if T <= 2 else "relpos_ring_small_kernel" if T <= 4
+                       else "relpos_ring_mfma_kernel") + " (fused rel-pos attention over the K/V ring window)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
