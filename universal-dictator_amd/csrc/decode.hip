@@ -140,25 +140,34 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
         q[g][0] = x0.x; q[g][1] = x0.y; q[g][2] = x0.z; q[g][3] = x0.w;
         q[g][4] = x1.x; q[g][5] = x1.y; q[g][6] = x1.z; q[g][7] = x1.w;
     }
-    // ---- K and V rows: key s0 + grp + RG p; pages outside [klo, khi) are never looked up
+    // ---- K and V rows: key s0 + grp + RG p; pages outside [klo, khi) are never looked up.  A pass
+    //      covers RG / PAGE whole pages (s0 is a multiple of 128), so a lane's page is
+    //      (s0 + RG p) / PAGE + grp / PAGE: the page table entries are scalar loads, and a row's
+    //      address is a scalar page base plus the lane's fixed offset (row grp % PAGE, 8 channels).
     const int blo = klo / PAGE, bhi = (khi - 1) / PAGE;
     const int32_t* bt = a.bt + (int64_t)seq * a.max_blocks;
-    // element offsets in 64 bits: a pool may hold 2^32 elements or more (8 GiB of 16-bit K or V)
-    int64_t off[NP];
+    constexpr int PPP = RG / PAGE;                // pages per pass (1 for D = 128, 2 for D = 64)
+    const uint32_t lane_off = (uint32_t)(((grp % PAGE) * D + sub * 8) * 2);   // bytes
+    const int gp = grp / PAGE;                    // the lane's page within the pass
+    const char* kp = static_cast<const char*>(a.kp);
+    const char* vp = static_cast<const char*>(a.vp);
+    // page bases in 64 bits: a pool may hold 2^32 elements or more (8 GiB of 16-bit K or V)
+    const char* kb[NP][PPP];
+    const char* vb[NP][PPP];
 #pragma unroll
-    for (int p = 0; p < NP; p++) {
-        const int j = s0 + grp + RG * p;
-        const int b = min(max(j / PAGE, blo), bhi);
-        const int64_t phys = bt[b];
-        off[p] = ((phys * a.Hkv + kvh) * PAGE + (j % PAGE)) * D + sub * 8;
-    }
-    const uint16_t* kp = static_cast<const uint16_t*>(a.kp);
-    const uint16_t* vp = static_cast<const uint16_t*>(a.vp);
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+        for (int e = 0; e < PPP; e++) {
+            const int b = min(max((s0 + RG * p) / PAGE + e, blo), bhi);
+            const int64_t base = ((int64_t)bt[b] * a.Hkv + kvh) * (PAGE * D * 2);
+            kb[p][e] = kp + base;
+            vb[p][e] = vp + base;
+        }
     uint4 kr[NP], vr[NP];
 #pragma unroll
-    for (int p = 0; p < NP; p++) kr[p] = ld16(kp + off[p]);
+    for (int p = 0; p < NP; p++) kr[p] = ld16((PPP == 1 || gp == 0 ? kb[p][0] : kb[p][PPP - 1]) + lane_off);
 #pragma unroll
-    for (int p = 0; p < NP; p++) vr[p] = ld16(vp + off[p]);
+    for (int p = 0; p < NP; p++) vr[p] = ld16((PPP == 1 || gp == 0 ? vb[p][0] : vb[p][PPP - 1]) + lane_off);
 
     // ---- scores of the G heads -> sc (masked keys -inf)
     bool writer;
