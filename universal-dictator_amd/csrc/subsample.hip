@@ -7,7 +7,8 @@
 //   conv.2 (depthwise)                          } register window per channel, so its
 //                                                 T1 x 65 x 256 activation never reaches HBM
 //   conv.3 (pointwise) + ReLU                   GEMM (bias epilogue), fp32 out
-//   rows >= v2 zero; conv.5 (depthwise)         sub_dw_kernel (mask applied on read)
+//   rows >= v2 zero; conv.5 (depthwise)         sub_dw_kernel (mask applied on read; 4 channels
+//                                               of one position per thread, one round trip)
 //   conv.6 (pointwise) + ReLU                   GEMM, fp32 out
 //   rows >= v3 zero; drop; flatten (f, c)       sub_flatten_kernel -> rows of the out Linear's A
 //   out Linear (C*F3 -> D) + bias               GEMM, fp32 out = the encoder's input rows
@@ -102,49 +103,72 @@ __global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
 }
 
 // Depthwise 3 x 3 stride-2 causal conv over x [n, Hin, Win, C] fp32 whose rows >= vlen[s][stage]
-// read as zero (the mask NeMo applies before this layer).  One workgroup per output row (s, ho);
-// each thread slides a 3 x 3 window of its channel along the row, so every input is loaded once.
+// read as zero (the mask NeMo applies before this layer).  A thread computes 4 channels of one
+// output position: its 9 taps are 16-byte loads issued together (one memory round trip per
+// thread), its 36 weights 9 more; a workgroup covers 4 consecutive output columns of one output row
+// (64 threads per column).  Each output column's 4 channels are one 16-byte (fp32) or 8-byte
+// (half, fragment-major: 4 consecutive channels are contiguous) store.
+constexpr int SUB_DW_COLS = 4;
+
 template <bool H>
 __global__ __launch_bounds__(SUB_C) void sub_dw_kernel(SubDwArgs a) {
-    const int c = threadIdx.x;
-    const int ho = blockIdx.x % a.Hout, s = blockIdx.x / a.Hout;
+    const int tid = threadIdx.x, c4 = (tid & 63) * 4, wsub = tid >> 6;
+    const int ncg = (a.Wout + SUB_DW_COLS - 1) / SUB_DW_COLS;
+    const int cg = blockIdx.x % ncg, ho = (blockIdx.x / ncg) % a.Hout, s = blockIdx.x / (ncg * a.Hout);
+    const int wo = cg * SUB_DW_COLS + wsub;
+    if (wo >= a.Wout) return;                     // no barrier below
     const int vin = a.vlen[s * 4 + a.stage];
-    float w[9];
+    // weights [C][9]: channels c4 .. c4+3 are 36 consecutive floats (16-byte aligned)
+    float w[4][9];
+    {
+        const float4* wp = reinterpret_cast<const float4*>(a.w + c4 * 9);
+        float f[36];
 #pragma unroll
-    for (int k = 0; k < 9; k++) w[k] = a.w[c * 9 + k];
-    const float b = a.b[c];
-    const float* rows[3];
-    bool hv[3];
+        for (int k = 0; k < 9; k++) {
+            const float4 x = wp[k];
+            f[4 * k] = x.x; f[4 * k + 1] = x.y; f[4 * k + 2] = x.z; f[4 * k + 3] = x.w;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int k = 0; k < 9; k++) w[e][k] = f[e * 9 + k];
+    }
+    const float4 bias = *reinterpret_cast<const float4*>(a.b + c4);
+    // The loads are unconditional (row and column clamped into the input, Win >= 1) so all 9 issue
+    // together; a padding tap or a masked row's tap is then replaced by zero with a select
+    // (v_cndmask), so whatever the clamped load read -- NaN or Inf included -- never reaches the sum.
+    float4 tap[3][3];
+    bool ok[3][3];
 #pragma unroll
     for (int kh = 0; kh < 3; kh++) {
         const int h = 2 * ho + kh - 2;
-        hv[kh] = h >= 0 && h < a.Hin && h < vin;
-        rows[kh] = a.x + (((int64_t)s * a.Hin + (hv[kh] ? h : 0)) * a.Win) * SUB_C + c;
-    }
-    // The load is unconditional (row and column clamped into the input, Win >= 1), so the unrolled
-    // loop's loads issue together; a padding tap or a masked row's tap is then replaced by zero
-    // with a select (v_cndmask), so whatever the clamped load read -- NaN or Inf included -- never
-    // reaches the sum.
-    auto ld = [&](int kh, int col) -> float {
-        const float v = rows[kh][(int64_t)min(max(col, 0), a.Win - 1) * SUB_C];
-        return (hv[kh] && col >= 0 && col < a.Win) ? v : 0.0f;
-    };
-    float win[3][3];
+        const bool hv = h >= 0 && h < a.Hin && h < vin;
+        const float* row = a.x + (((int64_t)s * a.Hin + min(max(h, 0), a.Hin - 1)) * a.Win) * SUB_C + c4;
 #pragma unroll
-    for (int kh = 0; kh < 3; kh++) win[kh][2] = 0.0f;     // column -2
-    const int64_t row0 = ((int64_t)s * a.Hout + ho) * a.Wout;
-#pragma unroll 4
-    for (int wo = 0; wo < a.Wout; wo++) {
-        float acc = b;
-#pragma unroll
-        for (int kh = 0; kh < 3; kh++) {
-            win[kh][0] = win[kh][2];
-            win[kh][1] = ld(kh, 2 * wo - 1);
-            win[kh][2] = ld(kh, 2 * wo);
-#pragma unroll
-            for (int kw = 0; kw < 3; kw++) acc += w[kh * 3 + kw] * win[kh][kw];
+        for (int kw = 0; kw < 3; kw++) {
+            const int col = 2 * wo + kw - 2;
+            ok[kh][kw] = hv && col >= 0 && col < a.Win;
+            tap[kh][kw] = *reinterpret_cast<const float4*>(row + (int64_t)min(max(col, 0), a.Win - 1) * SUB_C);
         }
-        store_a<H>(a.out, row0 + wo, c, SUB_C, acc);
+    }
+    float acc[4] = {bias.x, bias.y, bias.z, bias.w};
+#pragma unroll
+    for (int kh = 0; kh < 3; kh++)
+#pragma unroll
+        for (int kw = 0; kw < 3; kw++) {
+            const float4 t = tap[kh][kw];
+            const float v[4] = {ok[kh][kw] ? t.x : 0.0f, ok[kh][kw] ? t.y : 0.0f, ok[kh][kw] ? t.z : 0.0f,
+                                ok[kh][kw] ? t.w : 0.0f};
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] += w[e][kh * 3 + kw] * v[e];
+        }
+    const int64_t m = ((int64_t)s * a.Hout + ho) * a.Wout + wo;
+    if constexpr (H) {
+        const uint2 o = make_uint2((uint32_t)f2h(acc[0]) | ((uint32_t)f2h(acc[1]) << 16),
+                                   (uint32_t)f2h(acc[2]) | ((uint32_t)f2h(acc[3]) << 16));
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + frag_index(m, c4, SUB_C / 64)) = o;
+    } else {
+        *reinterpret_cast<float4*>(static_cast<float*>(a.out) + m * SUB_C + c4) = make_float4(acc[0], acc[1], acc[2], acc[3]);
     }
 }
 
@@ -174,8 +198,8 @@ int launch_sub_conv01(const SubArgs& a, bool half, hipStream_t st) {
 }
 
 int launch_sub_dw(const SubDwArgs& a, bool half, hipStream_t st) {
-    if (a.Win < 1 || a.Hin < 1) return -2;
-    const int blocks = a.n * a.Hout;
+    if (a.Win < 1 || a.Hin < 1 || a.Wout < 1) return -2;
+    const int blocks = a.n * a.Hout * ((a.Wout + SUB_DW_COLS - 1) / SUB_DW_COLS);
     if (blocks <= 0) return 0;
     if (half) hipLaunchKernelGGL(sub_dw_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
     else hipLaunchKernelGGL(sub_dw_kernel<false>, dim3(blocks), dim3(SUB_C), 0, st, a);
