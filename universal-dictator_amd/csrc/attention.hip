@@ -819,30 +819,43 @@ int launch_ring_read_floor(const RingArgs& a, hipStream_t st) {
 
 // ------------------------------------------------------------------ streaming ring kernel on MFMA (T 5..16)
 // Longer chunks (config of 14 frames: 256 streams x 8 heads, 103 MB per launch) make the
-// per-(stream, head) work a real matrix product: 16 query rows (T of them real) against
-// L + T <= 96 keys and L + 2T - 1 <= 112 band rows, all on v_mfma_f32_16x16x32_f16:
-//   C[query][band row] = (q+v) . P_band^T    (B = band rows from LDS)
-//   C[query][key]      = (q+u) . K^T         (B = K rows loaded straight into registers)
-//   out[query][chan]   = softmax . V         (A = probabilities, B = V^T via transposed LDS reads)
+// per-(stream, head) work a real matrix product: 16 query rows (T of them real) against the
+// stream's R <= 96 ring rows and L + 2T - 1 <= 112 band rows, all on v_mfma_f32_16x16x32_f16,
+// every product transposed so that a lane ends up holding one query's values:
+//   C[band row][query] = P_band . (q+v)^T    (A = band rows from LDS, B = q+v)
+//   C[ring row][query] = K . (q+u)^T         (A = K rows loaded straight into registers, B = q+u)
+//   C[chan][query]     = V^T . P^T           (A = V^T via transposed LDS reads, B = probabilities)
+// Keys are taken in ring order: K tile t holds ring rows 16t .. 16t+15 and V load it ring rows
+// 4it .. 4it+3 of the (slot, head) block, so every address is the block's (scalar) base plus a
+// lane constant plus an immediate -- no modulo, no wrap.  Ring row r holds window key
+// j = (r - start) mod R; the score of (i, r) uses band row W - 1 + i - j (rel_shift as an index,
+// gathered from the band tile in LDS), and keys outside [ks, ke) (rows outside the window
+// included) score -inf.  Softmax sums and P.V do not depend on the order of the keys.
+// Lane (c, g) (c = lane % 16, g = lane / 16) holds the scores of query c at ring rows
+// 16t + 4g + r: the softmax statistics reduce over the 4 lanes c, c+16, c+32, c+48 (lane swaps),
+// and the probabilities stay in registers as the B operand of P.V, whose k order is the same
+// permutation of the 32 rows of a piece: position 8g + e holds row 4g + e (e < 4), then
+// 16 + 4g + e - 4.  V is staged into LDS in that order.
 // One wave64 per (stream, head); a workgroup is 8 waves = 8 streams of one head, so the head's
 // band is loaded once per workgroup into LDS (it is the same for every stream), and every wave
-// is resident at once at two waves per SIMD (2,048 waves on 1,024 SIMDs): one wave's MFMAs and
-// softmax run while the other's loads are in flight.  To fit two waves per SIMD (<= 256 VGPRs,
-// <= 20 KB of LDS each): the K window (96 VGPRs) and the first half of the V window are loaded up
-// front; the second half of V goes into K's registers once the scores are done; V reaches the MFMA
-// through a 32-key LDS piece (ds_read_b64_tr_b16), three pieces per unit.
+// is resident at once at two waves per SIMD (2,048 waves on 1,024 SIMDs).  Loads are spread over
+// the unit so that the wave computes between them instead of stalling on issue: q and K first,
+// the first half of V after the band product, the second half after the key product.  When every
+// ring row is a valid key (ks = 0, ke = R: the steady state of full chunks) V needs no mask;
+// otherwise V rows outside the key range are zeroed before P.V, so probability-0 keys contribute
+// exact zeros whatever the ring holds there.
 // q+u, q+v and the probabilities enter the MFMA rounded once to IEEE half (relative 2^-12).
-// Scores stay in registers (lane: queries 4g..4g+3 of key 16t + lane%16); rel_shift is a gather of
-// the band tile from LDS; the softmax reduces within 16-lane DPP rows.
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
 namespace rm {
-constexpr int KT = 6, BT = 7;                    // key / band tiles of 16 rows
-constexpr int KMAX = 16 * KT, BMAX = 16 * BT;
+constexpr int BT = 7;                            // band tiles of 16 rows
+constexpr int BMAX = 16 * BT;
+constexpr int KMAX = 96;                         // ring rows (6 key tiles)
 constexpr int NW = 8;                            // waves (streams of one head) per workgroup
 constexpr int RS = 17;                           // 16-byte slots per band row in LDS (16 + 1 pad)
 constexpr int BSLOTS = BMAX * RS;                // 16-byte slots of the band rows
 constexpr int BINS = (BSLOTS + 64 + 63) / 64;     // direct-load instructions: band rows, u and v
+constexpr int SLD = BMAX + 4;                    // floats per row of a wave's bd tile
 constexpr int VST = 136;                         // halves per staged V row (128 + 8 pad)
 }  // namespace rm
 
@@ -861,21 +874,32 @@ __device__ __forceinline__ uint4 pack_f16x8(const float (&x)[8]) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// s_waitcnt immediate for "at most n vector-memory operations outstanding" (n < 64), every other
+// counter left alone.
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+// KT key tiles cover ring rows 0 .. 16 KT - 1 (R <= 16 KT); NVL V loads cover rows 0 .. 4 NVL - 1.
+// NVL < 4 KT only when NVL == ceil(R / 4) (the launcher checks it), so that only the last V load
+// can reach past row R - 1.
+template <int KT, int NVL>
 __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingArgs a) {
     using namespace rm;
     using T = f16;
+    constexpr int KP = (16 * KT + 31) / 32;       // 32-row V pieces
+    constexpr int NV1 = NVL / 2;                  // V loads issued after the band product
+    static_assert(KT >= 1 && KT <= 6 && NVL <= 4 * KT && 4 * NVL > 16 * (KT - 1), "ring rows");
     __shared__ __align__(16) uint4 band[BINS * 64];            // band rows (17 slots each), then u, v
-    __shared__ __align__(16) float slw[NW][16][BMAX + 4];      // per wave: bd tile, then probabilities
-    __shared__ __align__(16) uint16_t vpw[NW][32][VST];        // per wave: a 32-key piece of V
+    __shared__ __align__(16) float slw[NW][16][SLD];           // per wave: bd tile [query][band row]
+    __shared__ __align__(16) uint16_t vpw[NW][32][VST];        // per wave: a 32-row piece of V
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, g = lane >> 4;
-    const int H = a.H, L = a.L, Tq = a.T, D = H * 128, W = L + Tq, NB = L + 2 * Tq - 1;
+    const int H = a.H, L = a.L, Tq = a.T, D = H * 128, W = L + Tq, NB = L + 2 * Tq - 1, R = a.R;
     const int h = blockIdx.x % H;
     const int s = (blockIdx.x / H) * NW + wave;
     const bool live = s < a.n;                                  // wave-uniform
-    float (*sl)[BMAX + 4] = slw[wave];
+    float (*sl)[SLD] = slw[wave];
     uint16_t (*vp)[VST] = vpw[wave];
     // the descriptor first: read before any store of the kernel, it stays a scalar load.  A wave
     // past the last stream works on stream 0 and stores nothing (no branch around the body).
@@ -900,44 +924,42 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
         }
     }
     __asm__ volatile("" ::: "memory");          // the band loads stay ahead of the unit's loads
-    // ---- this wave's unit: q, K (B layout) and the first half of V (K/V rows: the window of the
-    //      ring, the new rows included)
+    // ---- this wave's unit: q and the K tiles (B layout)
     const int ks = L - cache_len, ke = L + valid;
     const T* qkv = static_cast<const T*>(a.qkv) + (int64_t)sx * Tq * 3 * D + h * 128;
-    const T* kring = static_cast<const T*>(a.kring) + ((int64_t)slot * H + h) * a.R * 128;
-    const T* vring = static_cast<const T*>(a.vring) + ((int64_t)slot * H + h) * a.R * 128;
-    const int R = a.R;
-    auto key_row = [&](const T* ring, int j) -> const T* {      // window key j < 2R - start
-        int r = start + j;
-        r -= (r >= R) ? R : 0;
-        return ring + (int64_t)r * 128;
-    };
+    const char* kblk = static_cast<const char*>(a.kring) + ((int64_t)slot * H + h) * R * 256;
+    const char* vblk = static_cast<const char*>(a.vring) + ((int64_t)slot * H + h) * R * 256;
     uint4 qraw[4];
 #pragma unroll
     for (int st = 0; st < 4; st++) qraw[st] = ld16(qkv + (int64_t)min(col, Tq - 1) * 3 * D + (4 * st + g) * 8);
     uint4 kb[KT][4];
 #pragma unroll
     for (int t = 0; t < KT; t++) {
-        const T* row = key_row(kring, min(16 * t + col, W - 1));
+        const uint32_t off = (uint32_t)min(16 * t + col, R - 1) * 256u + (uint32_t)g * 16u;
 #pragma unroll
-        for (int st = 0; st < 4; st++) kb[t][st] = ld16(row + (4 * st + g) * 8);
+        for (int st = 0; st < 4; st++) kb[t][st] = ld16(kblk + off + 64 * st);
     }
-    uint4 vr[KMAX / 4];                          // row 4 it + g, 16-byte column col
-#pragma unroll
-    for (int it = 0; it < KMAX / 8; it++) vr[it] = ld16(key_row(vring, min(4 * it + g, W - 1)) + col * 8);
-    // vmcnt(32): the 40 loads of the unit (q 4, K 24, V 12) were issued after the band loads and
-    // complete in order, so at most 32 outstanding means the band loads are done; the unit's data
-    // keeps arriving under the band product.
-    // A bare s_barrier, not __syncthreads(): the latter's workgroup fence waits for every
-    // outstanding load (vmcnt(0)); the band's direct loads are covered by the wait above.
+    // V row 4 it + g, 16-byte column col (only the last load can pass row R - 1 when NVL < 4 KT)
+    uint4 vr[NVL];
+    const uint32_t voff = (uint32_t)g * 256u + (uint32_t)col * 16u;
+    auto vload = [&](int it) {
+        const bool clamp = NVL == 4 * KT || it == NVL - 1;
+        const uint32_t off = clamp ? (uint32_t)min(4 * it + g, R - 1) * 256u + (uint32_t)col * 16u : voff + 1024u * it;
+        vr[it] = ld16(vblk + off);
+    };
+    // Wait for the band (and q): the 4 + 4 KT loads of the unit were issued after the band loads
+    // and complete in order, so at most 4 KT outstanding means the band and q are in.  A bare
+    // s_barrier, not __syncthreads(): the latter's workgroup fence waits for every outstanding load
+    // (vmcnt(0)); the band's direct loads are covered by the wait above.
+    static_assert(4 * KT < 64, "vmcnt range");
     __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0x8F70);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * KT));
     __builtin_amdgcn_s_barrier();                // every wave's band loads
     __asm__ volatile("" ::: "memory");
     const float (*uvl)[128] = reinterpret_cast<const float (*)[128]>(&band[BSLOTS]);
 
-    // ---- A operands: q + u, q + v (query col, k-chunk 4 st + g), rounded once to half
-    uint4 aqu[4], aqv[4];
+    // ---- B operands: q + u, q + v (query col, k-chunk 4 st + g), rounded once to half
+    uint4 bqu[4], bqv[4];
 #pragma unroll
     for (int st = 0; st < 4; st++) {
         const int c = (4 * st + g) * 8;
@@ -949,91 +971,120 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
         unpack16<T>(qraw[st], q);
 #pragma unroll
         for (int e = 0; e < 8; e++) { x[e] = q[e] + uu[e]; y[e] = q[e] + vv[e]; }
-        aqu[st] = pack_f16x8(x);
-        aqv[st] = pack_f16x8(y);
+        bqu[st] = pack_f16x8(x);
+        bqv[st] = pack_f16x8(y);
     }
 
-    // ---- bd tiles -> sl[query][band row]
+    // ---- bd tiles -> sl[query][band row] (16-byte writes: lane holds band rows 16t + 4g .. +3 of
+    //      query col); the next tile's band fragments are read ahead of the current tile's MFMAs
+    {
+        uint4 fa[4], fb[4];
 #pragma unroll
-    for (int t = 0; t < BT; t++) {
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int st = 0; st < 4; st++) fa[st] = band[col * RS + 4 * st + g];
 #pragma unroll
-        for (int st = 0; st < 4; st++)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(aqv[st]), as_f16x8(band[(16 * t + col) * RS + 4 * st + g]),
-                                                         acc, 0, 0, 0);
+        for (int t = 0; t < BT; t++) {
+            if (t + 1 < BT) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) sl[4 * g + r][16 * t + col] = acc[r];
+                for (int st = 0; st < 4; st++) fb[st] = band[(16 * (t + 1) + col) * RS + 4 * st + g];
+            }
+            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < 4; st++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(fa[st]), as_f16x8(bqv[st]), acc, 0, 0, 0);
+            *reinterpret_cast<float4*>(&sl[col][16 * t + 4 * g]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+#pragma unroll
+            for (int st = 0; st < 4; st++) fa[st] = fb[st];
+        }
     }
-    // ---- ac tiles in registers: lane holds queries 4g..4g+3 of key 16t + col
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int it = 0; it < NV1; it++) vload(it);
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- ac tiles: lane holds query col at ring rows 16t + 4g + r
     f32x4_t sacc[KT];
 #pragma unroll
     for (int t = 0; t < KT; t++) {
         f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int st = 0; st < 4; st++)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(aqu[st]), as_f16x8(kb[t][st]), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(kb[t][st]), as_f16x8(bqu[st]), acc, 0, 0, 0);
         sacc[t] = acc;
     }
-    // K's registers take the second half of the V window
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int it = KMAX / 8; it < KMAX / 4; it++) vr[it] = ld16(key_row(vring, min(4 * it + g, W - 1)) + col * 8);
-    wave_lds_fence();
+    for (int it = NV1; it < NVL; it++) vload(it);
+    __builtin_amdgcn_sched_barrier(0);
+    wave_lds_fence();                            // the bd tile is written
 
-    // ---- scores, rel_shift gather, softmax over keys [ks, ke) (16-lane rows hold one query set)
+    // ---- scores, rel_shift gather, softmax over keys [ks, ke) of query col
+    const int i = col;
     float pr[KT][4];
-    float mx[4], sm[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) mx[r] = -INFINITY;
+    float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < KT; t++) {
-        const int j = 16 * t + col;
+        int j0 = 16 * t + 4 * g - start;         // window key of ring row 16t + 4g, before the wrap
+        j0 += j0 < 0 ? R : 0;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const int i = 4 * g + r;
+            const int rr = 16 * t + 4 * g + r;   // ring row
+            int j = j0 + r;
+            j -= j >= R ? R : 0;
+            const bool kin = i < Tq && rr < R && j >= ks && j < ke;
             const int bi = min(max(W - 1 + i - j, 0), BMAX - 1);
             const float x = (sacc[t][r] + sl[i][bi]) * a.scale;
-            pr[t][r] = (i < Tq && j >= ks && j < ke) ? x : -INFINITY;
-            mx[r] = fmaxf(mx[r], pr[t][r]);
+            pr[t][r] = kin ? x : -INFINITY;
+            mx = fmaxf(mx, pr[t][r]);
         }
     }
-#pragma unroll
-    for (int r = 0; r < 4; r++) { mx[r] = group_max<16>(mx[r]); sm[r] = 0.0f; }
+    mx = xmax32(xmax16(mx));
+    float sm = 0.0f;
 #pragma unroll
     for (int t = 0; t < KT; t++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            pr[t][r] = pr[t][r] == -INFINITY ? 0.0f : __expf(pr[t][r] - mx[r]);
-            sm[r] += pr[t][r];
+            pr[t][r] = pr[t][r] == -INFINITY ? 0.0f : __expf(pr[t][r] - mx);
+            sm += pr[t][r];
         }
-#pragma unroll
-    for (int r = 0; r < 4; r++) { sm[r] = group_sum<16>(sm[r]); sm[r] = sm[r] > 0.0f ? 1.0f / sm[r] : 0.0f; }
-    wave_lds_fence();                            // every lane's gather read is done
-    // probabilities overwrite the band tile as sl[query][key]
-#pragma unroll
-    for (int t = 0; t < KT; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) sl[4 * g + r][16 * t + col] = pr[t][r] * sm[r];
-    wave_lds_fence();
+    sm = xadd32(xadd16(sm));
+    const float inv = sm > 0.0f ? 1.0f / sm : 0.0f;
 
-    // ---- out^T = V^T . P^T, one 32-key piece of V at a time through LDS (rows outside [ks, ke)
-    //      zero): A = V^T by ds_read_b64_tr_b16 (lane c of a 16-lane group gets column c & 3 of the
-    //      rows named by lanes c / 4 + 4 e), B = probabilities (query col, keys 32 kk + 8 g ..).
-    //      The transposed product leaves each lane 4 consecutive channels of one query row.
+    // ---- out^T = V^T . P^T, one 32-row piece of V at a time through LDS.  A = V^T by
+    //      ds_read_b64_tr_b16: lane c of a 16-lane group gets column c & 3 of the rows named by
+    //      lanes c / 4 + 4 e, so lane (c, g) holds positions 8g .. 8g+7 of channel 16 dt + c.
+    //      B = this lane's probabilities of the piece's two tiles, positions 8g + e.  Row 4a + g'
+    //      of the piece (V load 8 kk + a of lane group g') goes to position 8a + g' (a < 4) or
+    //      8(a - 4) + 4 + g'.  Rows outside the key range are zeroed unless every ring row is a
+    //      key (wave-uniform).  The transposed product leaves each lane 4 consecutive channels
+    //      of query col.
+    const bool full = ks == 0 && ke == R;
+    const int jb = g - start;                    // window key of ring row g, before the wrap
     f32x4_t oacc[8];
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) oacc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int kk = 0; kk < KMAX / 32; kk++) {
+    for (int kk = 0; kk < KP; kk++) {
 #pragma unroll
-        for (int it = 8 * kk; it < 8 * kk + 8; it++) {
-            const int j = 4 * it + g;
-            const uint32_t keep = (j >= ks && j < ke) ? 0xFFFFFFFFu : 0u;   // no branch: a mask
-            *reinterpret_cast<uint4*>(&vp[j - 32 * kk][col * 8]) =
-                make_uint4(vr[it].x & keep, vr[it].y & keep, vr[it].z & keep, vr[it].w & keep);
+        for (int a8 = 0; a8 < 8; a8++) {
+            const int it = 8 * kk + a8;
+            const int pos = a8 < 4 ? 8 * a8 + g : 8 * (a8 - 4) + 4 + g;
+            uint4 w = make_uint4(0, 0, 0, 0);
+            if (it < NVL) {
+                if (full) {
+                    w = vr[it];
+                } else {
+                    int j = jb + 4 * it;
+                    j += j < 0 ? R : 0;
+                    const uint32_t keep = (4 * it + g < R && j >= ks && j < ke) ? 0xFFFFFFFFu : 0u;   // a mask, no branch
+                    w = make_uint4(vr[it].x & keep, vr[it].y & keep, vr[it].z & keep, vr[it].w & keep);
+                }
+            }
+            *reinterpret_cast<uint4*>(&vp[pos][col * 8]) = w;
         }
-        const float4 p0 = *reinterpret_cast<const float4*>(&sl[col][32 * kk + 8 * g]);
-        const float4 p1 = *reinterpret_cast<const float4*>(&sl[col][32 * kk + 8 * g + 4]);
-        const float pf[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        float pf[8];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            pf[e] = 2 * kk < KT ? pr[2 * kk][e] * inv : 0.0f;
+            pf[4 + e] = 2 * kk + 1 < KT ? pr[2 * kk + 1][e] * inv : 0.0f;
+        }
         const uint4 pa = pack_f16x8(pf);
         wave_lds_fence();
         const int k0 = 8 * g + (col >> 2);
@@ -1051,7 +1102,8 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
     }
 
     // ---- output: lane holds out[col][16 dt + 4 g + r], r < 4 (exactly 0 for an empty key range:
-    //      every probability and every staged V row is 0); 8-byte stores, contiguous in either layout
+    //      every probability is 0 and so is every staged V row); 8-byte stores, contiguous in
+    //      either layout
     T* att = static_cast<T*>(a.att);
     if (live && col < Tq) {
         const int64_t orow = (int64_t)s * Tq + col;
@@ -1068,12 +1120,21 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
 
 int launch_relpos_ring_mfma(const RingArgs& a, hipStream_t st) {
     using namespace rm;
-    if (a.T < 1 || a.T > 16 || a.L + a.T > KMAX || a.L + 2 * a.T - 1 > BMAX || a.n < 1 || a.H < 1 || !a.zero_row ||
+    if (a.T < 1 || a.T > 16 || a.R > KMAX || a.L + 2 * a.T - 1 > BMAX || a.n < 1 || a.H < 1 || !a.zero_row ||
         a.L + a.T > a.R)
         return -2;
     if (a.rel_offset + 1 - a.T < 0 || a.rel_offset + a.L + a.T - 1 >= a.n_rel) return -2;
-    const int grid = a.H * ((a.n + NW - 1) / NW);
-    hipLaunchKernelGGL(relpos_ring_mfma_kernel, dim3(grid), dim3(64 * NW), 0, st, a);
+    const dim3 grid(a.H * ((a.n + NW - 1) / NW)), block(64 * NW);
+    const int kt = (a.R + 15) / 16, nvl = (a.R + 3) / 4;
+    if (kt == 6 && nvl == 21) hipLaunchKernelGGL((relpos_ring_mfma_kernel<6, 21>), grid, block, 0, st, a);
+    else switch (kt) {
+        case 1: hipLaunchKernelGGL((relpos_ring_mfma_kernel<1, 4>), grid, block, 0, st, a); break;
+        case 2: hipLaunchKernelGGL((relpos_ring_mfma_kernel<2, 8>), grid, block, 0, st, a); break;
+        case 3: hipLaunchKernelGGL((relpos_ring_mfma_kernel<3, 12>), grid, block, 0, st, a); break;
+        case 4: hipLaunchKernelGGL((relpos_ring_mfma_kernel<4, 16>), grid, block, 0, st, a); break;
+        case 5: hipLaunchKernelGGL((relpos_ring_mfma_kernel<5, 20>), grid, block, 0, st, a); break;
+        default: hipLaunchKernelGGL((relpos_ring_mfma_kernel<6, 24>), grid, block, 0, st, a); break;
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -1364,8 +1425,8 @@ static int launch_ring_t(const RingArgs& a, hipStream_t st) {
         else hipLaunchKernelGGL((relpos_ring_small_kernel<4, 6, 7>), grid, block, 0, st, a);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    // 16-bit chunks of 5..16 frames (L + T <= 96 keys): the MFMA kernel, one wave per (stream, head).
-    if (sizeof(T) == 2 && a.T <= 16 && a.L + a.T <= 96 && a.L + 2 * a.T - 1 <= 112 && band_ok && a.zero_row)
+    // 16-bit chunks of 5..16 frames (rings of R <= 96 rows): the MFMA kernel, one wave per (stream, head).
+    if (sizeof(T) == 2 && a.T <= 16 && a.R <= 96 && a.L + 2 * a.T - 1 <= 112 && band_ok && a.zero_row)
         return launch_relpos_ring_mfma(a, st);
     if (a.T <= 2) hipLaunchKernelGGL((relpos_ring_kernel<T, 2, KeyBlock<T, 2>::KB>), grid, block, 0, st, a);
     else if (a.T <= 4) hipLaunchKernelGGL((relpos_ring_kernel<T, 4, KeyBlock<T, 4>::KB>), grid, block, 0, st, a);
