@@ -22,6 +22,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
+#include <type_traits>
 
 #include "../../include/ud_decode.h"
 #include "ud_common.hpp"
@@ -102,6 +103,18 @@ __device__ __forceinline__ int tsum_row_index(int lane, bool& writer) {
     return m;
 }
 
+// Two floats rounded to nearest-even bf16, packed (x in the low half), and the packed bf16 dot
+// product a.lo * b.lo + a.hi * b.hi + c (v_dot2_f32_bf16: exact bf16 products, fp32 sum).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
+    const f32x2_t v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
 // a + (a from lane l^8) into lanes with bit 3 clear, b + ... into lanes with bit 3 set.
 __device__ __forceinline__ float xsum8(float a, float b, bool bit3) {
     const float keep = bit3 ? b : a, send = bit3 ? a : b;
@@ -131,14 +144,21 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
     __shared__ float stat[G][2];
     __shared__ __align__(16) float red[4][G][D];
 
-    // ---- the G query heads of this kv head (8 channels per lane)
+    // ---- the G query heads of this kv head (8 channels per lane); for bf16 pages also as bf16
+    //      pairs (channels 2e, 2e + 1) for the packed dot products
+    constexpr bool PK = std::is_same<KT, BF16>::value;
     float q[G][8];
+    uint32_t qb[G][4];
 #pragma unroll
     for (int g = 0; g < G; g++) {
         const float* qr = a.q + (int64_t)seq * a.Hq * D + (kvh * G + g) * D + sub * 8;
         const float4 x0 = *reinterpret_cast<const float4*>(qr), x1 = *reinterpret_cast<const float4*>(qr + 4);
         q[g][0] = x0.x; q[g][1] = x0.y; q[g][2] = x0.z; q[g][3] = x0.w;
         q[g][4] = x1.x; q[g][5] = x1.y; q[g][6] = x1.z; q[g][7] = x1.w;
+        if constexpr (PK) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) qb[g][e] = pack_bf16x2(q[g][2 * e], q[g][2 * e + 1]);
+        }
     }
     // ---- K and V rows: key s0 + grp + RG p; pages outside [klo, khi) are never looked up.  A pass
     //      covers RG / PAGE whole pages (s0 is a multiple of 128), so a lane's page is
@@ -174,15 +194,26 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
     const int qi = tsum_row_index<LPR, G>(sub, writer);
 #pragma unroll
     for (int p = 0; p < NP; p++) {
-        float f[8];
-        KvTraits<KT>::unpack(kr[p], f);
         float part[G];
+        if constexpr (PK) {
+            const uint32_t kw[4] = {kr[p].x, kr[p].y, kr[p].z, kr[p].w};
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            float acc = 0.0f;
+            for (int g = 0; g < G; g++) {
+                float acc = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc += q[g][e] * f[e];
-            part[g] = acc;
+                for (int e = 0; e < 4; e++) acc = dot2_bf16(qb[g][e], kw[e], acc);
+                part[g] = acc;
+            }
+        } else {
+            float f[8];
+            KvTraits<KT>::unpack(kr[p], f);
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc += q[g][e] * f[e];
+                part[g] = acc;
+            }
         }
         const float tot = tsum_row<LPR, G>(part, sub);
         const int jj = grp + RG * p, j = s0 + jj;
@@ -213,17 +244,44 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
     float acc[NV];
 #pragma unroll
     for (int f = 0; f < NV; f++) acc[f] = 0.0f;
+    if constexpr (PK) {
+        // bf16 pages: keys of passes p and p + 1 (rows jj and jj + RG of this lane) in pairs.
+        // Channel c of the two V rows packed into one word, the two probabilities of head g
+        // rounded to a bf16 pair, one v_dot2_f32_bf16 per (head, channel).
+        static_assert(NP % 2 == 0, "key pairs");
 #pragma unroll
-    for (int p = 0; p < NP; p++) {
-        const int jj = grp + RG * p, j = s0 + jj;
-        const bool in = j >= klo && j < khi;
-        float f[8];
-        KvTraits<KT>::unpack(in ? vr[p] : make_uint4(0, 0, 0, 0), f);
+        for (int p = 0; p < NP; p += 2) {
+            const int jj = grp + RG * p, j = s0 + jj;
+            const uint4 z = make_uint4(0, 0, 0, 0);
+            const uint4 va = (j >= klo && j < khi) ? vr[p] : z;
+            const uint4 vb2 = (j + RG >= klo && j + RG < khi) ? vr[p + 1] : z;
+            const uint32_t wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb2.x, vb2.y, vb2.z, vb2.w};
+            uint32_t x[8];
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float pg = sc[g][jj];
+            for (int e = 0; e < 4; e++) {
+                x[2 * e] = __builtin_amdgcn_perm(wb[e], wa[e], 0x05040100u);       // (a lo, b lo)
+                x[2 * e + 1] = __builtin_amdgcn_perm(wb[e], wa[e], 0x07060302u);   // (a hi, b hi)
+            }
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc[g * 8 + e] += pg * f[e];
+            for (int g = 0; g < G; g++) {
+                const uint32_t pp = pack_bf16x2(sc[g][jj], sc[g][jj + RG]);
+#pragma unroll
+                for (int c = 0; c < 8; c++) acc[g * 8 + c] = dot2_bf16(pp, x[c], acc[g * 8 + c]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            const int jj = grp + RG * p, j = s0 + jj;
+            const bool in = j >= klo && j < khi;
+            float f[8];
+            KvTraits<KT>::unpack(in ? vr[p] : make_uint4(0, 0, 0, 0), f);
+#pragma unroll
+            for (int g = 0; g < G; g++) {
+                const float pg = sc[g][jj];
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[g * 8 + e] += pg * f[e];
+            }
         }
     }
     // over the row groups of the wave (lanes with equal sub): xor 32, 16 (and 8 when LPR = 8)
