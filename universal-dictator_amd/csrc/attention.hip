@@ -874,10 +874,6 @@ __device__ __forceinline__ uint4 pack_f16x8(const float (&x)[8]) {
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// s_waitcnt immediate for "at most n vector-memory operations outstanding" (n < 64), every other
-// counter left alone.
-constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
-
 // KT key tiles cover ring rows 0 .. 16 KT - 1 (R <= 16 KT); NVL V loads cover rows 0 .. 4 NVL - 1.
 // NVL < 4 KT only when NVL == ceil(R / 4) (the launcher checks it), so that only the last V load
 // can reach past row R - 1.

@@ -213,20 +213,17 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
 // For M in the thousands (256 streams x 14 frames = 3584 rows) the projections are MFMA-bound, and
 // the register-direct kernel above would re-read each activation fragment once per 16-column tile.
 // Here a workgroup of 8 waves (2 per SIMD, so one wave's MFMAs run while the other waits on LDS)
-// owns a 256 x 64*NT output tile.  Per 64-wide K chunk it copies the 16 row fragments and 4*NT
-// column fragments (each a contiguous 2 KB block in the fragment-major layout, so the copy is
-// linear) into one of two LDS buffers with direct global -> LDS loads (global_load_lds_dwordx4,
-// no staging registers), while the waves multiply out of the other buffer.  Phases per chunk c:
-//   P1  8 MFMAs on half 0 of c (read in the previous iteration); LDS reads of half 1 of c; direct
-//       loads of chunk c+1 into the other buffer
-//   P2  the remaining MFMAs on half 0
-//   P3  MFMAs on half 1, first half of the columns
-//   P4  wait for this wave's direct loads; barrier: chunk c+1 is in LDS, all waves are done with c
-//   P5  LDS reads of half 0 of chunk c+1
-//   P6  MFMAs on half 1, second half of the columns (hides P5)
-// The buffer written in P1 was last read in the previous iteration, before its barrier.  The LDS
-// reads of half 1 are issued before the direct loads because the compiler cannot tell the two
-// buffers apart and would otherwise wait for the direct loads first.
+// owns a 256 x 64*NT output tile.  Per 32-deep K step it copies the 16 row fragments and 4*NT
+// column fragments (each a contiguous 1 KB half of a 2 KB fragment-major block, so the copy is
+// linear) into LDS with direct global -> LDS loads (global_load_lds_dwordx4, no staging
+// registers).  LDS holds a ring of four steps: at the start of step s the wave waits until its own
+// loads of step s have landed (the loads of s+1 and s+2 may still be in flight), a barrier makes
+// every wave's loads visible and guarantees that step s-1's buffer has been read, the wave reads
+// its fragments of step s, issues the loads of step s+3 into step s-1's buffer, and multiplies.
+// Three steps of loads stay in flight behind the MFMAs (with two 64-deep buffers, less than one
+// chunk did, and the kernel waited on its loads).  The four buffers are separate arrays and the
+// loop is unrolled by four, so the compiler can tell the buffers apart and does not wait for
+// outstanding direct loads before the LDS reads of another buffer.
 //
 // The MFMAs are inline asm with the accumulators pinned in place in the accumulator registers:
 // compiled from the builtin, the register allocator copied part of the accumulator between
@@ -266,8 +263,13 @@ __device__ __forceinline__ float act_fast(float x) {
 template <int NT, int EPI, int ACT, bool H = false, bool BIAS = false>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
     constexpr int MT = 8, BB = 4 * NT;                       // W blocks (16 columns each) per tile
-    constexpr int STAGE = (16 + BB) * 1024, CPW = 4 + NT;    // CPW: 1 KB copies per wave per chunk
-    __shared__ __attribute__((aligned(16))) bf16 lds[2 * STAGE];
+    constexpr int NBLK = 16 + BB;                            // 1 KB half-blocks per 32-deep K step
+    constexpr int STAGE = NBLK * 512;                        // halves per LDS stage
+    constexpr int CPS = (NBLK + 7) / 8, CMIN = NBLK / 8;     // direct loads per wave per step (max, min)
+    __shared__ __attribute__((aligned(16))) bf16 st0[STAGE];
+    __shared__ __attribute__((aligned(16))) bf16 st1[STAGE];
+    __shared__ __attribute__((aligned(16))) bf16 st2[STAGE];
+    __shared__ __attribute__((aligned(16))) bf16 st3[STAGE];
     __shared__ __attribute__((aligned(16))) int32_t rtab[EPI == EPI_QKV_RING ? 256 : 4];   // QKV: ring row offsets
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -279,25 +281,29 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
     const int kz = t % ks, tile = t / ks;
     const int mb = tile / nN, nb = tile % nN;
     const int nk = a.K / 64, kper = nk / ks, kc0 = kz * kper;
+    const int nsteps = 2 * kper;                             // 32-deep K steps of this split
     const int rtiles = (a.M + 15) / 16;
     const bf16* A = static_cast<const bf16*>(a.A);
     const bf16* W = static_cast<const bf16*>(a.W);
 
-    // Wave w copies the 1 KB half-blocks u = w + 8j (j < CPW): A's row tiles for u < 32 (j < 4).
-    int soff[CPW];
+    // Wave w copies the 1 KB half-blocks u = w + 8j of each step: A's row tiles for u < 16, then W's.
+    int soff[CPS];
 #pragma unroll
-    for (int j = 0; j < CPW; j++) {
-        const int u = wave + 8 * j, b = u >> 1, hb = u & 1;
-        int o;
-        if (b < 16) o = ((min(mb * 16 + b, rtiles - 1) * nk + kc0) << 10) + hb * 512;   // clamped rows: not stored
-        else o = (((nb * BB + b - 16) * nk + kc0) << 10) + hb * 512;
+    for (int j = 0; j < CPS; j++) {
+        const int u = wave + 8 * j;
+        int o = 0;
+        if (u < 16) o = (min(mb * 16 + u, rtiles - 1) * nk + kc0) << 10;     // clamped rows: not stored
+        else if (u < NBLK) o = ((nb * BB + u - 16) * nk + kc0) << 10;
         soff[j] = o;
     }
     const int lo = lane * 8;
-    auto copy_chunk = [&](int c, bf16* dst) __attribute__((always_inline)) {
+    auto copy_step = [&](int s, bf16* dst) __attribute__((always_inline)) {
+        const int kofs = ((s >> 1) << 10) + (s & 1) * 512;
 #pragma unroll
-        for (int j = 0; j < CPW; j++)
-            lds_direct16((j < 4 ? A : W) + soff[j] + (c << 10) + lo, dst + wave * 512 + j * 4096);
+        for (int j = 0; j < CPS; j++) {
+            const int u = wave + 8 * j;
+            if (j < CMIN || u < NBLK) lds_direct16((u < 16 ? A : W) + soff[j] + kofs + lo, dst + u * 512);
+        }
     };
 
     f32x4_t acc[NT][MT];
@@ -306,17 +312,17 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < MT; i++) acc[j][i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int aoff = (wm * MT) * 1024 + lo, boff = (16 + wn * NT) * 1024 + lo;
-    uint4 fa0[MT], fb0[NT], fa1[MT], fb1[NT];
-    auto read_half = [&](const bf16* buf, int h, uint4 (&fa)[MT], uint4 (&fb)[NT]) __attribute__((always_inline)) {
+    const int aoff = (wm * MT) * 512 + lo, boff = (16 + wn * NT) * 512 + lo;
+    uint4 fa[MT], fb[NT];
+    auto read_step = [&](const bf16* buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < MT; i++) fa[i] = *reinterpret_cast<const uint4*>(buf + aoff + i * 1024 + h * 512);
+        for (int i = 0; i < MT; i++) fa[i] = *reinterpret_cast<const uint4*>(buf + aoff + i * 512);
 #pragma unroll
-        for (int j = 0; j < NT; j++) fb[j] = *reinterpret_cast<const uint4*>(buf + boff + j * 1024 + h * 512);
+        for (int j = 0; j < NT; j++) fb[j] = *reinterpret_cast<const uint4*>(buf + boff + j * 512);
     };
-    auto mma = [&](const uint4 (&fa)[MT], const uint4 (&fb)[NT], int j0, int j1) __attribute__((always_inline)) {
+    auto mma = [&]() __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = j0; j < j1; j++)
+        for (int j = 0; j < NT; j++)
 #pragma unroll
             for (int i = 0; i < MT; i++)
                 if constexpr (H)
@@ -330,33 +336,32 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
     if constexpr (EPI == EPI_QKV_RING) {
         if (wave == 0) lds_direct16_rows(a.ring.rows + mb * 256 + 4 * lane, rtab);
     }
-    copy_chunk(0, lds);
-    __builtin_amdgcn_s_waitcnt(0x0F70);                      // vmcnt(0): this wave's direct loads landed
-    __syncthreads();
-    read_half(lds, 0, fa0, fb0);
+    // Four-stage ring of 32-deep K steps: steps s+1, s+2 (and the loads of s+3, issued at the start
+    // of step s into the stage step s-1 used) are in flight while step s is multiplied.
+    copy_step(0, st0);
+    if (1 < nsteps) copy_step(1, st1);
+    if (2 < nsteps) copy_step(2, st2);
     pin_acc(acc);
     asm volatile("s_nop 7");                                 // accumulator zeroing -> first MFMA
-    for (int c = 0; c < kper; c++) {
-        const bf16* buf = lds + (c & 1) * STAGE;
-        bf16* nbuf = lds + ((c + 1) & 1) * STAGE;
-        const bool more = c + 1 < kper;
-        mma(fa0, fb0, 0, 1);
+    auto step = [&](int s, const bf16* cur, bf16* nxt) __attribute__((always_inline)) {
+        // step s landed: every later in-flight step's loads may still be outstanding
+        if (s + 2 < nsteps) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CMIN));
+        else if (s + 1 < nsteps) __builtin_amdgcn_s_waitcnt(vmcnt_imm(CMIN));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        __builtin_amdgcn_s_barrier();                        // every wave's loads of step s; step s-1 read
+        __asm__ volatile("" ::: "memory");
+        read_step(cur);
         __builtin_amdgcn_sched_barrier(0);
-        read_half(buf, 1, fa1, fb1);
-        if (more) copy_chunk(c + 1, nbuf);
+        if (s + 3 < nsteps) copy_step(s + 3, nxt);
         __builtin_amdgcn_sched_barrier(0);
-        mma(fa0, fb0, 1, NT);
+        mma();
         __builtin_amdgcn_sched_barrier(0);
-        mma(fa1, fb1, 0, NT / 2);
-        __builtin_amdgcn_sched_barrier(0);
-        if (more) {
-            __builtin_amdgcn_s_waitcnt(0x0F70);
-            __syncthreads();
-            read_half(nbuf, 0, fa0, fb0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        mma(fa1, fb1, NT / 2, NT);
-        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int s = 0; s < nsteps; s += 4) {
+        step(s, st0, st3);
+        if (s + 1 < nsteps) step(s + 1, st1, st0);
+        if (s + 2 < nsteps) step(s + 2, st2, st1);
+        if (s + 3 < nsteps) step(s + 3, st3, st2);
     }
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7");   // last MFMA results -> epilogue reads
     pin_acc(acc);

@@ -82,6 +82,10 @@ template <> struct Vec16<float> { static constexpr int N = 4; };
 template <> struct Vec16<bf16> { static constexpr int N = 8; };
 template <> struct Vec16<f16> { static constexpr int N = 8; };
 
+// s_waitcnt immediate for "at most n vector-memory operations outstanding" (n < 64), every other
+// counter left alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14).
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
 // Non-temporal 16-byte load: data read once per step (a stream's K/V window), streamed past the
