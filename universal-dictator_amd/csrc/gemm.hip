@@ -620,9 +620,11 @@ static int device_cus() {
 // Tile width (NT: 64*NT columns) and K splits of the LDS-staged kernel for one projection.  Cost
 // model: rounds of workgroups over the CUs x the per-workgroup MFMA work, scaled by the per-flop cost
 // measured on MI355X for each width (NT 4: 1.00, 3: 1.28, 2: 1.36 at 3584 rows), plus for K splits
-// the fp32 partial slabs they write (400 units per slab per 3584 x 1024 outputs).  Measured choices
-// at 3584 rows: N 4096 -> NT 4; N 3072 -> NT 3; N 2048 -> NT 2; N 1024, K 4096 -> NT 4 with 4 splits;
-// N 1024, K 1024 -> NT 2 with 2 splits.
+// the fp32 partial slabs they write and the LayerNorm after them reads back (900 units per slab per
+// 3584 x 1024 outputs: a slab's stores come at the end of the one round of workgroups, where
+// nothing hides them, about 2-3 us, and its read in the LayerNorm about 2.5 us).  Choices at 3584
+// rows: N 4096 -> NT 4; N 3072 -> NT 3; N 2048 -> NT 2; N 1024, K 4096 -> NT 2 with 2 splits; N 1024,
+// K 1024 -> NT 2, no split (the step ran 8.38 ms with 4 and 2 splits there, 8.29 ms with these).
 BigTile big_tile(int M, int N, int K, bool partial) {
     static const double cost_nt[5] = {0.0, 0.0, 1.36, 1.28, 1.0};
     const int cus = device_cus();
@@ -635,7 +637,7 @@ BigTile big_tile(int M, int N, int K, bool partial) {
             const long tiles = (long)(N / (64 * nt)) * ((M + 255) / 256) * ks;
             const long rounds = (tiles + cus - 1) / cus;
             double cost = (double)rounds * nt * (K / ks) * cost_nt[nt];
-            if (ks > 1) cost += 400.0 * ks * ((double)M * N / (3584.0 * 1024.0));
+            if (ks > 1) cost += 900.0 * ks * ((double)M * N / (3584.0 * 1024.0));
             if (cost < best_cost) { best_cost = cost; best = BigTile{nt, ks}; }
         }
     }
