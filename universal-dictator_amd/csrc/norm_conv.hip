@@ -277,6 +277,7 @@ template <int NPER>
 static void ln_dispatch(dim3 grid, dim3 block, hipStream_t st, float* x, Partials parts, const float* g, const float* b,
                         void* out, int ob, int rows, int D, int act) {
     if (parts.n == 0) hipLaunchKernelGGL((layernorm_kernel<NPER, 0>), grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act);
+    else if (parts.n == 1) hipLaunchKernelGGL((layernorm_kernel<NPER, 1>), grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act);
     else if (parts.n == 2) hipLaunchKernelGGL((layernorm_kernel<NPER, 2>), grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act);
     else if (parts.n == 4) hipLaunchKernelGGL((layernorm_kernel<NPER, 4>), grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act);
     else hipLaunchKernelGGL((layernorm_kernel<NPER, -1>), grid, block, 0, st, x, parts, g, b, out, ob, rows, D, act);
@@ -303,6 +304,7 @@ static void ln2_dispatch(dim3 grid, dim3 block, hipStream_t st, const float* src
                          const float* ga, const float* ba, const float* gb, const float* bb, void* z, int zb, int rows,
                          int D) {
     if (parts.n == 0) hipLaunchKernelGGL((layernorm2_kernel<NPER, 0>), grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D);
+    else if (parts.n == 1) hipLaunchKernelGGL((layernorm2_kernel<NPER, 1>), grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D);
     else if (parts.n == 2) hipLaunchKernelGGL((layernorm2_kernel<NPER, 2>), grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D);
     else if (parts.n == 4) hipLaunchKernelGGL((layernorm2_kernel<NPER, 4>), grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D);
     else hipLaunchKernelGGL((layernorm2_kernel<NPER, -1>), grid, block, 0, st, src, parts, res, ga, ba, gb, bb, z, zb, rows, D);
