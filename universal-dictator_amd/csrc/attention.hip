@@ -1146,6 +1146,10 @@ int launch_relpos_ring_mfma(const RingArgs& a, hipStream_t st) {
 //   tile fetches one new chunk;
 //   bd tiles are computed per wave over its 80-row sub-band and gathered through LDS for the
 //   rel_shift (score (i, j) reads band row i - j + 63 of the wave's window);
+//   every product is transposed (C[key][query] = K.(q+u)^T, C[band row][query] = P.(q+v)^T,
+//   C[chan][query] = V^T.P^T), so a lane holds one query: its softmax reduces over 4 lanes with
+//   lane swaps, its probabilities stay in registers as the B operand of P.V (k order permuted the
+//   same way in the transposed V reads), and its output is 4 consecutive channels per store;
 //   the next tile's K, V and band chunk are prefetched into registers during the current tile.
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): this wave's LDS ops are done
@@ -1180,15 +1184,10 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
     __syncthreads();
     const int t_lo = kbound[0] / KT, t_hi = kbound[0] < kbound[1] ? (kbound[1] + KT - 1) / KT : t_lo;
 
-    // ---- the lane's 4 queries (rows 4g + r of the wave's 16) and their key ranges
-    int qks[4], qke[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int i = iw + 4 * g + r;
-        qks[r] = i < Tn ? max(R[2 * i], 0) : 0;
-        qke[r] = i < Tn ? min(R[2 * i + 1], Tn) : 0;
-    }
-    // ---- A operands: q + u, q + v in bf16 (query iw + col, k-chunk 4st + g)
+    // ---- the lane's query (row col of the wave's 16) and its key range
+    const int qi = iw + col;
+    const int qks = qi < Tn ? max(R[2 * qi], 0) : 0, qke = qi < Tn ? min(R[2 * qi + 1], Tn) : 0;
+    // ---- B operands: q + u, q + v in bf16 (query iw + col, k-chunk 4st + g)
     uint4 aqu[4], aqv[4];
     {
         const T* qr = Q + (int64_t)min(iw + col, Tn - 1) * D;
@@ -1239,10 +1238,8 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
     };
     auto ring = [](int k) { return ((k % 3) + 3) % 3; };
 
-    float m[4], l[4];
-    f32x4_t oacc[8];
-#pragma unroll
-    for (int r = 0; r < 4; r++) { m[r] = -INFINITY; l[r] = 0.0f; }
+    float m = -INFINITY, l = 0.0f;
+    f32x4_t oacc[8];                          // out^T: lane holds channels 16dt + 4g + r of query col
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) oacc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -1260,90 +1257,107 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
         if (more) { load_rows(K, j0 + KT, nk); load_rows(V, j0 + KT, nv); load_chunk(t + 1, np); }
         __syncthreads();
 
-        // ---- ac: 4 key subtiles (lane: queries 4g.., key 16ts + col)
+        // ---- ac = K . (q+u)^T: lane holds query col at keys 16ts + 4g + r.  The k chunk is the
+        //      outer loop, so the 4 accumulators are independent and a chunk's fragments are read
+        //      together.
         f32x4_t sacc[4];
 #pragma unroll
+        for (int ts = 0; ts < 4; ts++) sacc[ts] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            uint4 ak[4];
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++) ak[ts] = *reinterpret_cast<const uint4*>(&kl[16 * ts + col][(4 * st + g) * 8]);
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++)
+                sacc[ts] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ak[ts]), as_bf16x8(aqu[st]), sacc[ts], 0, 0, 0);
+        }
+        // ---- bd = P_band . (q+v)^T over the wave's 80 band rows rel = iw - j0 - 63 + n (n < 80);
+        //      lane holds band rows 16tb + 4g .. +3 of query col: one 16-byte write per tile.  Five
+        //      independent accumulators, k chunk outermost.
+        {
+            int prow[5];
+#pragma unroll
+            for (int tb = 0; tb < 5; tb++) {
+                const int rel = iw - j0 - 63 + 16 * tb + col;
+                const int x = i0 - rel;
+                const int k = x >= 0 ? x / 64 : -((-x + 63) / 64);
+                prow[tb] = ring(k) * KT + (rel - (i0 - 63 - 64 * k));
+            }
+            f32x4_t bacc[5];
+#pragma unroll
+            for (int tb = 0; tb < 5; tb++) bacc[tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+                uint4 ap[5];
+#pragma unroll
+                for (int tb = 0; tb < 5; tb++) ap[tb] = *reinterpret_cast<const uint4*>(&pl[prow[tb]][(4 * st + g) * 8]);
+#pragma unroll
+                for (int tb = 0; tb < 5; tb++)
+                    bacc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ap[tb]), as_bf16x8(aqv[st]), bacc[tb], 0, 0, 0);
+            }
+#pragma unroll
+            for (int tb = 0; tb < 5; tb++)
+                *reinterpret_cast<float4*>(&sw[wave][col][16 * tb + 4 * g]) = make_float4(bacc[tb][0], bacc[tb][1], bacc[tb][2], bacc[tb][3]);
+        }
+        wave_lds_sync();
+
+        // ---- scores and the online softmax of query col.  Key 16ts + 4g + r uses band row
+        //      col - 16ts - 4g - r + 63 of the wave's window (0..78): four consecutive floats.
+        float sc[4][4];
+        float mx = -INFINITY;
+#pragma unroll
         for (int ts = 0; ts < 4; ts++) {
-            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            const float* bp = &sw[wave][col][col - 16 * ts - 4 * g + 60];
 #pragma unroll
-            for (int st = 0; st < 4; st++) {
-                const uint4 bk = *reinterpret_cast<const uint4*>(&kl[16 * ts + col][(4 * st + g) * 8]);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aqu[st]), as_bf16x8(bk), acc, 0, 0, 0);
+            for (int r = 0; r < 4; r++) {
+                const int j = j0 + 16 * ts + 4 * g + r;
+                const float x = (sacc[ts][r] + bp[3 - r]) * a.scale;
+                sc[ts][r] = (j >= qks && j < qke) ? x : -INFINITY;
+                mx = fmaxf(mx, sc[ts][r]);
             }
-            sacc[ts] = acc;
         }
-        // ---- bd over the wave's 80 band rows rel = iw - j0 - 63 + n (n < 80), gathered through LDS
+        mx = xmax32(xmax16(mx));
+        const float nm = fmaxf(m, mx);
+        const float corr = nm == -INFINITY ? 1.0f : __expf(m - nm);
+        float ps = 0.0f;
 #pragma unroll
-        for (int tb = 0; tb < 5; tb++) {
-            const int rel = iw - j0 - 63 + 16 * tb + col;
-            const int x = i0 - rel;
-            const int k = x >= 0 ? x / 64 : -((-x + 63) / 64);
-            const int prow = ring(k) * KT + (rel - (i0 - 63 - 64 * k));
-            f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ts = 0; ts < 4; ts++)
 #pragma unroll
-            for (int st = 0; st < 4; st++) {
-                const uint4 bp = *reinterpret_cast<const uint4*>(&pl[prow][(4 * st + g) * 8]);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(aqv[st]), as_bf16x8(bp), acc, 0, 0, 0);
+            for (int r = 0; r < 4; r++) {
+                sc[ts][r] = sc[ts][r] == -INFINITY ? 0.0f : __expf(sc[ts][r] - nm);
+                ps += sc[ts][r];
             }
+        l = l * corr + xadd32(xadd16(ps));
+        m = nm;
 #pragma unroll
-            for (int r = 0; r < 4; r++) sw[wave][4 * g + r][16 * tb + col] = acc[r];
-        }
-        wave_lds_sync();
+        for (int dt = 0; dt < 8; dt++) oacc[dt] *= corr;
 
-        // ---- scores and the online softmax of the lane's 4 queries
-        float s[4][4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int ts = 0; ts < 4; ts++) {
-                const int j = j0 + 16 * ts + col;
-                const float x = (sacc[ts][r] + sw[wave][4 * g + r][4 * g + r - 16 * ts - col + 63]) * a.scale;
-                s[ts][r] = (j >= qks[r] && j < qke[r]) ? x : -INFINITY;
-                mx = fmaxf(mx, s[ts][r]);
-            }
-            mx = group_max<16>(mx);
-            const float nm = fmaxf(m[r], mx);
-            const float corr = nm == -INFINITY ? 1.0f : __expf(m[r] - nm);
-            float ps = 0.0f;
-#pragma unroll
-            for (int ts = 0; ts < 4; ts++) {
-                s[ts][r] = s[ts][r] == -INFINITY ? 0.0f : __expf(s[ts][r] - nm);
-                ps += s[ts][r];
-            }
-            l[r] = l[r] * corr + group_sum<16>(ps);
-            m[r] = nm;
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) oacc[dt][r] *= corr;
-        }
-        wave_lds_sync();
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int ts = 0; ts < 4; ts++) sw[wave][4 * g + r][16 * ts + col] = s[ts][r];
-        wave_lds_sync();
-
-        // ---- P.V: A = probabilities (query col, keys 32kk + 8g ..), B = V^T by transposed LDS reads
+        // ---- out^T += V^T . P^T per 32-key piece (tiles 2kk, 2kk + 1).  B = this lane's
+        //      probabilities: position 8g + e holds key 32kk + 4g + e (e < 4), then 32kk + 16 + 4g + e - 4;
+        //      A = V^T by ds_read_b64_tr_b16 over the same keys (lane c of a 16-lane group gets column
+        //      c & 3 of the rows named by lanes c / 4 + 4e: rows 32kk + 4g .. +3, then 32kk + 16 + 4g ..).
 #pragma unroll
         for (int kk = 0; kk < 2; kk++) {
-            const float4 p0 = *reinterpret_cast<const float4*>(&sw[wave][col][32 * kk + 8 * g]);
-            const float4 p1 = *reinterpret_cast<const float4*>(&sw[wave][col][32 * kk + 8 * g + 4]);
-            const uint4 pa = make_uint4((uint32_t)f2bf(p0.x) | ((uint32_t)f2bf(p0.y) << 16),
-                                        (uint32_t)f2bf(p0.z) | ((uint32_t)f2bf(p0.w) << 16),
-                                        (uint32_t)f2bf(p1.x) | ((uint32_t)f2bf(p1.y) << 16),
-                                        (uint32_t)f2bf(p1.z) | ((uint32_t)f2bf(p1.w) << 16));
-            const int k0 = 32 * kk + 8 * g + (col >> 2);
+            const float* p0 = sc[2 * kk];
+            const float* p1 = sc[2 * kk + 1];
+            const uint4 pb = make_uint4((uint32_t)f2bf(p0[0]) | ((uint32_t)f2bf(p0[1]) << 16),
+                                        (uint32_t)f2bf(p0[2]) | ((uint32_t)f2bf(p0[3]) << 16),
+                                        (uint32_t)f2bf(p1[0]) | ((uint32_t)f2bf(p1[1]) << 16),
+                                        (uint32_t)f2bf(p1[2]) | ((uint32_t)f2bf(p1[3]) << 16));
+            const int k0 = 32 * kk + 4 * g + (col >> 2);
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
                 const int c0 = 16 * dt + 4 * (col & 3);
                 const v4i16_t b0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vl[k0][c0]);
-                const v4i16_t b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vl[k0 + 4][c0]);
-                uint4 bv;
-                __builtin_memcpy(&bv.x, &b0, 8);
-                __builtin_memcpy(&bv.z, &b1, 8);
-                oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pa), as_bf16x8(bv), oacc[dt], 0, 0, 0);
+                const v4i16_t b1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)&vl[k0 + 16][c0]);
+                uint4 av;
+                __builtin_memcpy(&av.x, &b0, 8);
+                __builtin_memcpy(&av.z, &b1, 8);
+                oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(pb), oacc[dt], 0, 0, 0);
             }
         }
+        wave_lds_sync();                          // every lane's reads of sw are done before the next tile writes it
         __syncthreads();
         if (more) {
             store_rows(kl, nk);
@@ -1352,15 +1366,15 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
         }
     }
 
-    // ---- output: out[iw + 4g + r][16dt + col] (0 for an empty key range)
+    // ---- output: out[iw + col][16dt + 4g .. +3] (0 for an empty key range): 8-byte stores
     T* O = static_cast<T*>(a.out) + (int64_t)b * Tn * D + h * DK;
+    if (qi < Tn) {
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int i = iw + 4 * g + r;
-        if (i < Tn) {
-            const float inv = l[r] > 0.0f ? 1.0f / l[r] : 0.0f;
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) O[(int64_t)i * D + 16 * dt + col] = f2bf(oacc[dt][r] * inv);
+        for (int dt = 0; dt < 8; dt++) {
+            const uint2 w = make_uint2((uint32_t)f2bf(oacc[dt][0] * inv) | ((uint32_t)f2bf(oacc[dt][1] * inv) << 16),
+                                       (uint32_t)f2bf(oacc[dt][2] * inv) | ((uint32_t)f2bf(oacc[dt][3] * inv) << 16));
+            *reinterpret_cast<uint2*>(O + (int64_t)qi * D + 16 * dt + 4 * g) = w;
         }
     }
 }
