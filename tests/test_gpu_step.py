@@ -164,26 +164,6 @@ def test_graph_replay_matches_eager(gpu, orc):
         np.testing.assert_array_equal(a, b)
 
 
-@pytest.mark.parametrize("dtype,groups,S,T", [("bf16", 2, 24, 2), ("f32", 3, 48, 1), ("bf16", 4, 40, 5)])
-def test_step_in_stream_groups(gpu, orc, dtype, groups, S, T):
-    """UD_GROUPS runs the step as independent chains over consecutive streams (whole 16-row tiles
-    each, forked from and joined into the step stream, inside the captured graph): each chain's
-    rows match the oracle to the step's bar, over steps with ragged valid counts."""
-    os.environ["UD_GROUPS"] = str(groups)
-    try:
-        cfg = gpu.EncoderConfig(layers=2, max_chunk=T, max_streams=S, dtype=dtype)
-        plan = lambda step, S_, T_: [T_ if (i + step) % 5 else max(T_ - 1, 0) for i in range(S_)]
-        enc, _, _, res = _run_steps(gpu, orc, cfg, S=S, T=T, n_steps=3, seed=81, seed_caches=True, valid_plan=plan)
-    finally:
-        os.environ.pop("UD_GROUPS", None)
-    for i, (got, ref) in enumerate(res):
-        if dtype == "bf16":
-            harness.assert_bf16_close(got, ref, "step %d" % i)
-        else:
-            assert harness.rel_err(got, ref) <= 1e-4, i
-    enc.close()
-
-
 def test_error_paths(gpu, orc):
     ud = gpu
     cfg = ud.EncoderConfig(layers=1, max_chunk=2, max_streams=2, dtype="bf16")

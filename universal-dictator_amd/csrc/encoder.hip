@@ -133,7 +133,6 @@ struct LayerDev {
     uint32_t set_mask = 0;
 };
 
-constexpr int MAX_GROUPS = 4;
 
 struct GraphEntry {
     int n, T;
@@ -197,11 +196,6 @@ struct ud_encoder {
     bool finalized = false;
     bool use_graphs = true;
     hipStream_t capture_stream = nullptr;
-    // groups of streams stepped concurrently (fork/join inside the captured graph)
-    hipStream_t gstream[MAX_GROUPS] = {};
-    hipEvent_t fork_ev = nullptr;
-    hipEvent_t join_ev[MAX_GROUPS] = {};
-    int groups_override = 0;        // UD_GROUPS (1..MAX_GROUPS), 0 = the built-in rule
     std::vector<GraphEntry> graphs;
     SubDev sub;
 };
@@ -246,11 +240,6 @@ static void free_encoder(ud_encoder* e) {
         if (e->desc_ev[i]) (void)hipEventDestroy(e->desc_ev[i]);
     }
     if (e->capture_stream) (void)hipStreamDestroy(e->capture_stream);
-    for (int g = 0; g < MAX_GROUPS; g++) {
-        if (e->gstream[g]) (void)hipStreamDestroy(e->gstream[g]);
-        if (e->join_ev[g]) (void)hipEventDestroy(e->join_ev[g]);
-    }
-    if (e->fork_ev) (void)hipEventDestroy(e->fork_ev);
     for (ud_stream* s : e->live) delete s;
     delete e;
 }
@@ -346,20 +335,9 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
         hipMemset(e->kring, 0, e->ring_layer_elems * e->layers * esz) != hipSuccess ||
         hipMemset(e->vring, 0, e->ring_layer_elems * e->layers * esz) != hipSuccess ||
         hipMemset(e->cring, 0, e->cring_layer_elems * e->layers * 4) != hipSuccess ||
-        hipStreamCreateWithFlags(&e->capture_stream, hipStreamNonBlocking) != hipSuccess ||
-        hipEventCreateWithFlags(&e->fork_ev, hipEventDisableTiming) != hipSuccess) {
+        hipStreamCreateWithFlags(&e->capture_stream, hipStreamNonBlocking) != hipSuccess) {
         free_encoder(e);
         return fail(UD_ERR_HIP, "ud_encoder_create: initialisation failed");
-    }
-    for (int g = 0; g < MAX_GROUPS; g++)
-        if (hipStreamCreateWithFlags(&e->gstream[g], hipStreamNonBlocking) != hipSuccess ||
-            hipEventCreateWithFlags(&e->join_ev[g], hipEventDisableTiming) != hipSuccess) {
-            free_encoder(e);
-            return fail(UD_ERR_HIP, "ud_encoder_create: initialisation failed");
-        }
-    if (const char* gs = getenv("UD_GROUPS")) {
-        const int v = atoi(gs);
-        if (v >= 1 && v <= MAX_GROUPS) e->groups_override = v;
     }
     for (int s = (int)slots - 1; s >= 0; s--) e->free_slots.push_back(s);
     *out = e;
@@ -705,8 +683,7 @@ static int upload_desc(ud_encoder* e, ud_stream* const* streams, int n, int T, c
 
 // The workspace rows of streams s0 .. s0+n-1 of a step (rows r0 = s0 * T on, r0 a multiple of 16,
 // so the fragment-major operands start on a whole 16-row tile: their element offset is r0 * width
-// like the row-major buffers').  The split-K slabs of the group are [ks][n*T][D] at
-// KSPLIT * r0 * D, disjoint from every other group's.
+// like the row-major buffers').  The split-K slabs are [ks][n*T][D] at KSPLIT * r0 * D.
 struct Ws {
     float* res; void* z; void* h; void* qkv; void* att; float* pw; float* part; int32_t* desc; int32_t* rows;
 };
@@ -811,39 +788,12 @@ static int enqueue_rows(ud_encoder* e, int s0, int n, int T, const float* x, flo
     return UD_OK;
 }
 
-// How many groups a step of n streams x T frames runs as: one chain by default.  Independent
-// chains of part of the streams on separate HIP streams (UD_GROUPS = 2..4) were measured on
-// MI355X to be slower, not faster: 64 x 2 frames 2.19 -> 2.30 ms with 2 groups (2.92 with 3),
-// 256 x 14 frames 9.8 -> 30 ms with 2; the latency-bound kernels of one chain do not overlap with
-// another chain's.  Group boundaries fall on whole 16-row tiles.
-static int step_groups(const ud_encoder* e, int n, int T) {
-    int G = e->groups_override;
-    if (G == 0) G = 1;
-    const int q = 16 / std::gcd(T, 16);          // streams per 16-row tile boundary
-    while (G > 1 && n / q < G) G--;
-    return G;
-}
-
-// The step over all n streams: one chain, or G chains of consecutive streams forked from `st`
-// and joined back into it (inside a graph capture this records a forked graph).
+// The step over all n streams: one chain of dependent launches on `st`.  (Independent chains over
+// groups of streams on separate HIP streams, forked and joined inside the graph, were measured on
+// MI355X to be slower: 64 x 2 frames 2.19 -> 2.30 ms with 2 groups, 256 x 14 frames 9.8 -> 30 ms;
+// the latency-bound kernels of one chain did not overlap another chain's.)
 static int enqueue_step(ud_encoder* e, int n, int T, const float* x, float* out, hipStream_t st) {
-    const int G = step_groups(e, n, T);
-    if (G == 1) return enqueue_rows(e, 0, n, T, x, out, st);
-    const int q = 16 / std::gcd(T, 16);
-    const int tiles = n / q;                      // whole boundary units; the last group takes the rest
-    HIPC(hipEventRecord(e->fork_ev, st));
-    int s0 = 0;
-    for (int g = 0; g < G; g++) {
-        const int s1 = g + 1 == G ? n : (tiles * (g + 1) / G) * q;
-        HIPC(hipStreamWaitEvent(e->gstream[g], e->fork_ev, 0));
-        const size_t r0 = (size_t)s0 * T * e->D;
-        int rc = enqueue_rows(e, s0, s1 - s0, T, x + r0, out + r0, e->gstream[g]);
-        if (rc != UD_OK) return rc;
-        HIPC(hipEventRecord(e->join_ev[g], e->gstream[g]));
-        HIPC(hipStreamWaitEvent(st, e->join_ev[g], 0));
-        s0 = s1;
-    }
-    return UD_OK;
+    return enqueue_rows(e, 0, n, T, x, out, st);
 }
 
 static int run_step(ud_encoder* e, int n, int T, const float* x, float* out, hipStream_t st) {
