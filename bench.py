@@ -10,9 +10,9 @@ and full 70-frame caches seeded from N(0,1).  Default workload: 64 streams x 2 f
 in, 160 ms of audio per stream per step).  Prints one JSON
 line: aggregate streamed audio-seconds per second, per-step latency percentiles, the fused
 attention kernel's achieved HBM bandwidth against 8 TB/s and against the HBM read peak measured in
-the same run (HIP events on the kernel's own stream), each projection GEMM's MFMA throughput
-against the nominal and the measured peak, and the CPU oracle's throughput on a bounded sample
-timed on this host's cores.
+the same run (HIP events on the kernel's own stream), the same attention at 256 streams x 14
+frames (roofline_long_chunk), each projection GEMM's MFMA throughput against the nominal and the
+measured peak, and the CPU oracle's throughput on a bounded sample timed on this host's cores.
 
 --workload chunk14 runs the same step at 256 streams x 14 frames.  --workload decode measures the
 decoder's paged grouped-query attention instead: 64 sequences x 1 new token, 32 query / 8 kv heads
@@ -520,6 +520,45 @@ def stream_bench(ud, args):
     print(json.dumps(result), flush=True)
 
 
+def long_chunk_attention(ud, lw, args, hbm_read):
+    """The same fused attention at the long-chunk shape, 256 streams x 14 frames over L = 70 (the
+    batched MFMA kernel: 103 MB per launch, where the fixed per-launch cost is a small part),
+    timed the same way as the default workload's kernel (HIP events over launches cycling the 24
+    layers' rings after one untimed pass).  The weights are the default workload's."""
+    wl = WORKLOADS["chunk14"]
+    S, T = wl["streams"], wl["T"]
+    cfg = ud.EncoderConfig(layers=24, max_chunk=T, max_streams=S, dtype="bf16")
+    L, D, H, dk = cfg.left_context, cfg.d_model, cfg.heads, cfg.d_model // cfg.heads
+    enc = ud.Encoder(cfg)
+    for l, w in enumerate(lw):
+        enc.set_layer_weights(l, w)
+    enc.finalize()
+    streams = [enc.new_stream() for _ in range(S)]
+    rng = np.random.default_rng(12)
+    k = rng.standard_normal((L, D), dtype=np.float32)
+    v = rng.standard_normal((L, D), dtype=np.float32)
+    conv = np.zeros((cfg.conv_kernel - 1, D), np.float32)
+    for i, s in enumerate(streams):           # N(0,1) rows, a different rotation per stream and layer
+        for l in range(cfg.layers):
+            s.import_cache(l, np.roll(k, i + 7 * l, axis=0), np.roll(v, 3 * i + 5 * l, axis=0), conv, L)
+    hs = ud.HipStream()
+    qkv = ud.DeviceBuffer.from_numpy(ud.f16_bits(rng.standard_normal((S * T, 3 * D), dtype=np.float32)))
+    att = ud.DeviceBuffer(S * T * D * 2)
+    enc.time_layer_attention(streams, T, 0, qkv, att, args.attn_iters, hip_stream=hs)
+    ms = enc.time_layer_attention(streams, T, 0, qkv, att, args.attn_iters, hip_stream=hs)
+    Tk, n_rel = L + T, L + 2 * T - 1
+    nbytes = S * Tk * H * dk * 2 * 2 + S * 2 * T * H * dk * 2 + n_rel * H * dk * 2 + 2 * H * dk * 4
+    achieved = nbytes / (ms / 1000.0) / 1e9
+    enc.close()
+    log("long-chunk attention (256 streams x 14 frames): %.2f us/launch, %.0f GB/s" % (ms * 1000.0, achieved))
+    return {"kernel": "relpos_ring_mfma_kernel (fused rel-pos attention over the K/V ring window)",
+            "workload": "256 streams x 14 frames, left context 70, 8 heads x 128, bf16 (the long-chunk step's attention)",
+            "us_per_launch": round(ms * 1000.0, 3), "bound": "hbm", "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "measured_peak": round(hbm_read, 1), "frac_measured": round(achieved / hbm_read, 4),
+            "traffic": read_traffic("relpos_ring_chunk14"), "algorithmic_bytes_per_launch": nbytes}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -529,6 +568,8 @@ def main():
     ap.add_argument("--attn-iters", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-long-chunk-attention", action="store_true",
+                    help="skip the default workload's second attention measurement at 256 streams x 14 frames")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a known-size kernel for "
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -740,6 +781,8 @@ def main():
         },
     }
     enc.close()
+    if args.workload == "chunk2" and not args.no_long_chunk_attention:
+        result["roofline_long_chunk"] = long_chunk_attention(ud, lw, args, hbm_read)
     if not args.no_cpu_baseline:
         cpu = host_cpu()
         # a bounded sample: all 64 streams at 2-frame chunks (about 0.7 s per step on 16 cores); at
