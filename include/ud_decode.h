@@ -40,7 +40,11 @@ extern "C" {
  *   max_keys     an upper bound of ranges[i].y over the batch (sizes the grid)
  *   workspace    device scratch of ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys) bytes
  * Supported: head_dim in {64, 128}, q_heads % kv_heads == 0, q_heads / kv_heads in {1, 2, 4, 8},
- * block_size 16. */
+ * block_size 16.
+ * Precision: f16 pages are widened and used in fp32 arithmetic, as the reference kernel does.
+ * bf16 pages use packed bf16 dot products: q and the softmax probabilities are rounded once to
+ * bf16 (products exact, sums in fp32), within the bf16 activation bar (max abs 2e-2, cosine
+ * 0.9995). */
 UD_API size_t ud_gqa_workspace_bytes(int32_t n, int32_t q_heads, int32_t head_dim, int32_t max_keys);
 UD_API int ud_gqa_attention_paged(int32_t kv_dtype, const float* q_dev, const void* k_pages, const void* v_pages,
                                   const int32_t* block_table, int32_t max_blocks, const int32_t* ranges_dev,
