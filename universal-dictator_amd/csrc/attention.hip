@@ -1158,16 +1158,19 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
     using T = bf16;
-    constexpr int DK = 128, KT = 64, VST = DK + 8, NW = 8;
+    // SWS: the bd rows' stride in floats; 84 = 4 (mod 32) spreads the 16-byte writes of 8
+    // consecutive rows over all 32 banks
+    constexpr int DK = 128, KT = 64, VST = DK + 8, NW = 8, SWS = 84;
     __shared__ __align__(16) bf16 kl[KT][VST];
     __shared__ __align__(16) bf16 vl[KT][VST];
     __shared__ __align__(16) bf16 pl[3 * KT][VST];
-    __shared__ __align__(16) float sw[NW][16][80];
+    __shared__ __align__(16) float sw[NW][16][SWS];
     __shared__ int kbound[2];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 15, g = lane >> 4;
     const int Tn = a.T, D = a.H * DK, h = blockIdx.y, b = blockIdx.z;
     const int i0 = blockIdx.x * 128, iw = i0 + 16 * wave;
+    const float c2 = a.scale * 1.4426950408889634f;      // scores in log2 units: exp(s * scale) = 2^(s * c2)
     const T* Q = static_cast<const T*>(a.q) + (int64_t)b * Tn * D + h * DK;
     const T* K = static_cast<const T*>(a.k) + (int64_t)b * Tn * D + h * DK;
     const T* V = static_cast<const T*>(a.v) + (int64_t)b * Tn * D + h * DK;
@@ -1205,8 +1208,8 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
             uint32_t pu[4], pv[4];
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
-                pu[e / 2] = (uint32_t)f2bf(qf[e] + uu[e]) | ((uint32_t)f2bf(qf[e + 1] + uu[e + 1]) << 16);
-                pv[e / 2] = (uint32_t)f2bf(qf[e] + vv[e]) | ((uint32_t)f2bf(qf[e + 1] + vv[e + 1]) << 16);
+                pu[e / 2] = pack_bf16x2(qf[e] + uu[e], qf[e + 1] + uu[e + 1]);
+                pv[e / 2] = pack_bf16x2(qf[e] + vv[e], qf[e + 1] + vv[e + 1]);
             }
             aqu[st] = make_uint4(pu[0], pu[1], pu[2], pu[3]);
             aqv[st] = make_uint4(pv[0], pv[1], pv[2], pv[3]);
@@ -1238,6 +1241,8 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
     };
     auto ring = [](int k) { return ((k % 3) + 3) % 3; };
 
+    // m: the query's running maximum of the unscaled scores; l: this lane's share (its 4 keys of
+    // each 16) of the running sum, all 4 lanes of a query rescaled alike, summed at the end
     float m = -INFINITY, l = 0.0f;
     f32x4_t oacc[8];                          // out^T: lane holds channels 16dt + 4g + r of query col
 #pragma unroll
@@ -1304,6 +1309,9 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
 
         // ---- scores and the online softmax of query col.  Key 16ts + 4g + r uses band row
         //      col - 16ts - 4g - r + 63 of the wave's window (0..78): four consecutive floats.
+        //      A tile inside every key range of the wave's queries (the common case) skips the
+        //      masks; the accumulator is rescaled only when some query's maximum grew.
+        const bool inside = __all(j0 >= qks && j0 + KT <= qke);
         float sc[4][4];
         float mx = -INFINITY;
 #pragma unroll
@@ -1312,26 +1320,38 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int j = j0 + 16 * ts + 4 * g + r;
-                const float x = (sacc[ts][r] + bp[3 - r]) * a.scale;
-                sc[ts][r] = (j >= qks && j < qke) ? x : -INFINITY;
+                const float x = sacc[ts][r] + bp[3 - r];
+                sc[ts][r] = (inside || (j >= qks && j < qke)) ? x : -INFINITY;
                 mx = fmaxf(mx, sc[ts][r]);
             }
         }
         mx = xmax32(xmax16(mx));
         const float nm = fmaxf(m, mx);
-        const float corr = nm == -INFINITY ? 1.0f : __expf(m - nm);
-        float ps = 0.0f;
+        if (!__all(nm == m)) {
+            const float corr = nm == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f((m - nm) * c2);
+            l *= corr;
 #pragma unroll
-        for (int ts = 0; ts < 4; ts++)
+            for (int dt = 0; dt < 8; dt++) oacc[dt] *= corr;
+            m = nm;
+        }
+        const float mc = m * c2;
+        if (inside) {
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                sc[ts][r] = sc[ts][r] == -INFINITY ? 0.0f : __expf(sc[ts][r] - nm);
-                ps += sc[ts][r];
-            }
-        l = l * corr + xadd32(xadd16(ps));
-        m = nm;
+            for (int ts = 0; ts < 4; ts++)
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) oacc[dt] *= corr;
+                for (int r = 0; r < 4; r++) {
+                    sc[ts][r] = __builtin_amdgcn_exp2f(fmaf(sc[ts][r], c2, -mc));
+                    l += sc[ts][r];
+                }
+        } else {
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    sc[ts][r] = sc[ts][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(sc[ts][r], c2, -mc));
+                    l += sc[ts][r];
+                }
+        }
 
         // ---- out^T += V^T . P^T per 32-key piece (tiles 2kk, 2kk + 1).  B = this lane's
         //      probabilities: position 8g + e holds key 32kk + 4g + e (e < 4), then 32kk + 16 + 4g + e - 4;
@@ -1341,10 +1361,8 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
         for (int kk = 0; kk < 2; kk++) {
             const float* p0 = sc[2 * kk];
             const float* p1 = sc[2 * kk + 1];
-            const uint4 pb = make_uint4((uint32_t)f2bf(p0[0]) | ((uint32_t)f2bf(p0[1]) << 16),
-                                        (uint32_t)f2bf(p0[2]) | ((uint32_t)f2bf(p0[3]) << 16),
-                                        (uint32_t)f2bf(p1[0]) | ((uint32_t)f2bf(p1[1]) << 16),
-                                        (uint32_t)f2bf(p1[2]) | ((uint32_t)f2bf(p1[3]) << 16));
+            const uint4 pb = make_uint4(pack_bf16x2(p0[0], p0[1]), pack_bf16x2(p0[2], p0[3]),
+                                        pack_bf16x2(p1[0], p1[1]), pack_bf16x2(p1[2], p1[3]));
             const int k0 = 32 * kk + 4 * g + (col >> 2);
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
@@ -1368,12 +1386,13 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
 
     // ---- output: out[iw + col][16dt + 4g .. +3] (0 for an empty key range): 8-byte stores
     T* O = static_cast<T*>(a.out) + (int64_t)b * Tn * D + h * DK;
+    l = xadd32(xadd16(l));
     if (qi < Tn) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
-            const uint2 w = make_uint2((uint32_t)f2bf(oacc[dt][0] * inv) | ((uint32_t)f2bf(oacc[dt][1] * inv) << 16),
-                                       (uint32_t)f2bf(oacc[dt][2] * inv) | ((uint32_t)f2bf(oacc[dt][3] * inv) << 16));
+            const uint2 w = make_uint2(pack_bf16x2(oacc[dt][0] * inv, oacc[dt][1] * inv),
+                                       pack_bf16x2(oacc[dt][2] * inv, oacc[dt][3] * inv));
             *reinterpret_cast<uint2*>(O + (int64_t)qi * D + 16 * dt + 4 * g) = w;
         }
     }

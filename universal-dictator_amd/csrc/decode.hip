@@ -103,14 +103,8 @@ __device__ __forceinline__ int tsum_row_index(int lane, bool& writer) {
     return m;
 }
 
-// Two floats rounded to nearest-even bf16, packed (x in the low half), and the packed bf16 dot
-// product a.lo * b.lo + a.hi * b.hi + c (v_dot2_f32_bf16: exact bf16 products, fp32 sum).
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-typedef float f32x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
-    const f32x2_t v = {x, y};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
-}
+// The packed bf16 dot product a.lo * b.lo + a.hi * b.hi + c (v_dot2_f32_bf16: exact bf16
+// products, fp32 sum).
 __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }

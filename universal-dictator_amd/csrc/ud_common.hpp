@@ -23,6 +23,13 @@ __device__ __forceinline__ bf16 f2bf(float f) {
 // MFMA operand types (v_mfma_f32_16x16x32_bf16: 8 bf16 of A and of B per lane, 4 fp32 of C).
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+// Two floats rounded to nearest-even bf16 by v_cvt_pk_bf16_f32, packed (x in the low half).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
+    const f32x2_t v = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
     bf16x8_t r;
     __builtin_memcpy(&r, &v, 16);
