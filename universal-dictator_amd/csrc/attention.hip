@@ -1158,11 +1158,13 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
     using T = bf16;
-    // SWS: the bd rows' stride in floats; 84 = 4 (mod 32) spreads the 16-byte writes of 8
-    // consecutive rows over all 32 banks
-    constexpr int DK = 128, KT = 64, VST = DK + 8, NW = 8, SWS = 84;
+    // Row strides (LDS has 32 banks of 4 bytes): K and band rows, read 16 bytes a lane along
+    // consecutive rows, take 136 bf16 (68 words = 4 mod 32); V rows, read by ds_read_b64_tr_b16 with
+    // 4 consecutive rows per 16 lanes, take 144 bf16 (72 words = 8 mod 32); the bd rows take 84
+    // floats (4 mod 32), so 16-byte writes of 8 consecutive rows cover all banks.
+    constexpr int DK = 128, KT = 64, VST = DK + 8, VVST = DK + 16, NW = 8, SWS = 84;
     __shared__ __align__(16) bf16 kl[KT][VST];
-    __shared__ __align__(16) bf16 vl[KT][VST];
+    __shared__ __align__(16) bf16 vl[KT][VVST];
     __shared__ __align__(16) bf16 pl[3 * KT][VST];
     __shared__ __align__(16) float sw[NW][16][SWS];
     __shared__ int kbound[2];
@@ -1232,7 +1234,7 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
             x[e] = ld16(P + (int64_t)tr * D + cc * 8);
         }
     };
-    auto store_rows = [&](bf16 (*dst)[VST], const uint4 (&x)[2]) {
+    auto store_rows = [&](auto dst, const uint4 (&x)[2]) {
 #pragma unroll
         for (int e = 0; e < 2; e++) {
             const int idx = tid + 512 * e, row = idx >> 4, cc = idx & 15;
@@ -1240,6 +1242,16 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
         }
     };
     auto ring = [](int k) { return ((k % 3) + 3) % 3; };
+    // Band row rel = iw - j0 - 63 + 16tb + col of tile t lies in chunk k = t + dch[tb], row boff[tb]
+    // of it: k = floor((i0 - rel) / 64) and i0 - rel = 64t + 63 - 16 wave - 16tb - col, whose
+    // remainder part lies in [-128, 63].
+    int dch[5], boff[5];
+#pragma unroll
+    for (int tb = 0; tb < 5; tb++) {
+        const int x = 63 - 16 * wave - 16 * tb - col;
+        dch[tb] = x >= 0 ? 0 : (x >= -64 ? -1 : -2);
+        boff[tb] = 16 * wave + 16 * tb + col + 64 * dch[tb];
+    }
 
     // m: the query's running maximum of the unscaled scores; l: this lane's share (its 4 keys of
     // each 16) of the running sum, all 4 lanes of a query rescaled alike, summed at the end
@@ -1281,13 +1293,13 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
         //      lane holds band rows 16tb + 4g .. +3 of query col: one 16-byte write per tile.  Five
         //      independent accumulators, k chunk outermost.
         {
+            const int r0 = t % 3;
             int prow[5];
 #pragma unroll
             for (int tb = 0; tb < 5; tb++) {
-                const int rel = iw - j0 - 63 + 16 * tb + col;
-                const int x = i0 - rel;
-                const int k = x >= 0 ? x / 64 : -((-x + 63) / 64);
-                prow[tb] = ring(k) * KT + (rel - (i0 - 63 - 64 * k));
+                int c = r0 + dch[tb] + 3;                      // ring slot of chunk t + dch[tb]
+                c = c >= 3 ? c - 3 : c;
+                prow[tb] = c * KT + boff[tb];
             }
             f32x4_t bacc[5];
 #pragma unroll
@@ -1313,18 +1325,30 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
         //      masks; the accumulator is rescaled only when some query's maximum grew.
         const bool inside = __all(j0 >= qks && j0 + KT <= qke);
         float sc[4][4];
-        float mx = -INFINITY;
 #pragma unroll
-        for (int ts = 0; ts < 4; ts++) {
+        for (int ts = 0; ts < 4; ts++) {              // the 16 band reads are issued together
             const float* bp = &sw[wave][col][col - 16 * ts - 4 * g + 60];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int j = j0 + 16 * ts + 4 * g + r;
-                const float x = sacc[ts][r] + bp[3 - r];
-                sc[ts][r] = (inside || (j >= qks && j < qke)) ? x : -INFINITY;
-                mx = fmaxf(mx, sc[ts][r]);
-            }
+            for (int r = 0; r < 4; r++) sc[ts][r] = bp[3 - r];
         }
+#pragma unroll
+        for (int ts = 0; ts < 4; ts++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sc[ts][r] += sacc[ts][r];
+        if (!inside) {                                // keys outside a query's range: -inf
+#pragma unroll
+            for (int ts = 0; ts < 4; ts++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int j = j0 + 16 * ts + 4 * g + r;
+                    sc[ts][r] += (j >= qks && j < qke) ? 0.0f : -INFINITY;
+                }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int ts = 0; ts < 4; ts++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) mx = fmaxf(mx, sc[ts][r]);
         mx = xmax32(xmax16(mx));
         const float nm = fmaxf(m, mx);
         if (!__all(nm == m)) {
@@ -1334,24 +1358,16 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
             for (int dt = 0; dt < 8; dt++) oacc[dt] *= corr;
             m = nm;
         }
-        const float mc = m * c2;
-        if (inside) {
+        // a masked score is -inf and 2^-inf = 0; while a query has no key yet (m = -inf) every
+        // score of it is -inf and any finite offset serves
+        const float mc = m == -INFINITY ? 0.0f : m * c2;
 #pragma unroll
-            for (int ts = 0; ts < 4; ts++)
+        for (int ts = 0; ts < 4; ts++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    sc[ts][r] = __builtin_amdgcn_exp2f(fmaf(sc[ts][r], c2, -mc));
-                    l += sc[ts][r];
-                }
-        } else {
-#pragma unroll
-            for (int ts = 0; ts < 4; ts++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    sc[ts][r] = sc[ts][r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(sc[ts][r], c2, -mc));
-                    l += sc[ts][r];
-                }
-        }
+            for (int r = 0; r < 4; r++) {
+                sc[ts][r] = __builtin_amdgcn_exp2f(fmaf(sc[ts][r], c2, -mc));
+                l += sc[ts][r];
+            }
 
         // ---- out^T += V^T . P^T per 32-key piece (tiles 2kk, 2kk + 1).  B = this lane's
         //      probabilities: position 8g + e holds key 32kk + 4g + e (e < 4), then 32kk + 16 + 4g + e - 4;
