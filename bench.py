@@ -13,6 +13,7 @@ attention kernel's achieved HBM bandwidth against 8 TB/s and against the HBM rea
 the same run (HIP events on the kernel's own stream), the same attention at 256 streams x 14
 frames (roofline_long_chunk), each projection GEMM's MFMA throughput against the nominal and the
 measured peak, and the CPU oracle's throughput on a bounded sample timed on this host's cores.
+--library-gemm adds the vendor GEMM (torch.matmul, hipBLASLt) timed on each projection's shape.
 
 --workload chunk14 runs the same step at 256 streams x 14 frames.  --workload decode measures the
 decoder's paged grouped-query attention instead: 64 sequences x 1 new token, 32 query / 8 kv heads
@@ -520,6 +521,48 @@ def stream_bench(ud, args):
     print(json.dumps(result), flush=True)
 
 
+_LIBRARY_GEMM_SCRIPT = r"""
+import json, sys, torch
+M, shapes, iters = json.loads(sys.argv[1])
+gen = torch.Generator(device="cuda").manual_seed(5)
+out = {}
+for name, (N, K) in shapes.items():
+    a = torch.randn(M, K, device="cuda", dtype=torch.bfloat16, generator=gen)
+    w = torch.randn(N, K, device="cuda", dtype=torch.bfloat16, generator=gen).t().contiguous()
+    for _ in range(10):
+        c = torch.matmul(a, w)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        c = torch.matmul(a, w)
+    e1.record()
+    torch.cuda.synchronize()
+    out[name] = e0.elapsed_time(e1) * 1000.0 / iters
+print(json.dumps(out))
+"""
+
+
+def library_gemm_times(M, D, F, iters=100):
+    """The vendor GEMM (torch.matmul on bf16, which runs hipBLASLt) on each projection's shape
+    [M, K] x [K, N]: a reference point for the projection kernels, plain output, no fused epilogue.
+    torch carries its own HIP runtime, so it runs in a child process."""
+    import subprocess
+    shapes = {"ff_linear1": (F, D), "ff_linear2": (D, F), "qkv": (3 * D, D), "linear_out": (D, D),
+              "pointwise_conv1": (2 * D, D), "pointwise_conv2": (D, D)}
+    r = subprocess.run([sys.executable, "-c", _LIBRARY_GEMM_SCRIPT, json.dumps([M, shapes, iters])],
+                       stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=300)
+    if r.returncode != 0:
+        log("library GEMM timing failed (%d): %s" % (r.returncode, r.stderr.strip().splitlines()[-1:]))
+        return None
+    us = json.loads(r.stdout.strip().splitlines()[-1])
+    out = {}
+    for name, (N, K) in shapes.items():
+        out[name] = {"us": round(us[name], 3), "tflops": round(2.0 * M * N * K / us[name] / 1e6, 1)}
+        log("library GEMM %-16s %8.2f us  %7.1f TFLOP/s  (M %d, N %d, K %d)" % (name, us[name], out[name]["tflops"], M, N, K))
+    return out
+
+
 def long_chunk_attention(ud, lw, args, hbm_read):
     """The same fused attention at the long-chunk shape, 256 streams x 14 frames over L = 70 (the
     batched MFMA kernel: 103 MB per launch, where the fixed per-launch cost is a small part),
@@ -573,6 +616,8 @@ def main():
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a known-size kernel for "
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="chunk workloads: also time the vendor GEMM (torch.matmul, hipBLASLt) on each projection shape")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -708,6 +753,7 @@ def main():
         tot_ms += per_layer[name] * pms
         log("projection %-16s %8.2f us  %7.1f TFLOP/s" % (name, pms * 1000.0, tf))
     proj_tf = tot_fl / (tot_ms / 1000.0) / 1e12
+    lib_gemm = library_gemm_times(rows_step, D, cfg.ff_dim) if args.library_gemm else None
 
     # The fused attention kernel alone, on the stream it is launched on.
     qkv = ud.DeviceBuffer.from_numpy(ud.f16_bits(rng.standard_normal((S * T, 3 * D), dtype=np.float32)))
@@ -761,6 +807,9 @@ def main():
             "frac_measured": round(proj_tf / mfma_f16, 4),
             "note": "the seven projections of a layer (ff linear1/linear2 twice), each timed as the step "
                     "launches it (ud_time_projection, weights from HBM), f16 operands with bf16-valued weights"},
+        **({"library_gemm": dict(lib_gemm, method="torch.matmul bf16 (hipBLASLt) on the same [rows, K] x [K, N], "
+                                               "100 back-to-back calls, HIP events; plain output, no epilogue")}
+           if lib_gemm else {}),
         "realtime_factor": round(value, 2),
         "attention_steps_per_sec": round(1000.0 / attn_ms, 1),
         "attention_us_per_launch": round(attn_ms * 1000.0, 3),
