@@ -1011,33 +1011,58 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
     __builtin_amdgcn_sched_barrier(0);
     wave_lds_fence();                            // the bd tile is written
 
-    // ---- scores, rel_shift gather, softmax over keys [ks, ke) of query col
+    // ---- scores, rel_shift gather, softmax over keys [ks, ke) of query col.  Scores stay unscaled
+    //      until the exponential: p = 2^(s c2 - max c2) with c2 = scale log2 e.  When every ring row
+    //      is a key (wave-uniform; steady-state full chunks) only the padding rows past R are masked:
+    //      lanes of queries i >= T compute finite values that no output uses.
     const int i = col;
+    const bool full = ks == 0 && ke == R && W == R;
+    const float c2 = a.scale * 1.4426950408889634f;
     float pr[KT][4];
     float mx = -INFINITY;
+    if (full) {
 #pragma unroll
-    for (int t = 0; t < KT; t++) {
-        int j0 = 16 * t + 4 * g - start;         // window key of ring row 16t + 4g, before the wrap
-        j0 += j0 < 0 ? R : 0;
+        for (int t = 0; t < KT; t++) {
+            int j0 = 16 * t + 4 * g - start;     // window key of ring row 16t + 4g, before the wrap
+            j0 += j0 < 0 ? R : 0;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int rr = 16 * t + 4 * g + r;   // ring row
-            int j = j0 + r;
-            j -= j >= R ? R : 0;
-            const bool kin = i < Tq && rr < R && j >= ks && j < ke;
-            const int bi = min(max(W - 1 + i - j, 0), BMAX - 1);
-            const float x = (sacc[t][r] + sl[i][bi]) * a.scale;
-            pr[t][r] = kin ? x : -INFINITY;
-            mx = fmaxf(mx, pr[t][r]);
+            for (int r = 0; r < 4; r++) {
+                int j = j0 + r;
+                j -= j >= R ? R : 0;
+                const int bi = min(W - 1 + i - j, BMAX - 1);
+                const float x = sacc[t][r] + sl[i][bi];
+                pr[t][r] = 16 * t + 4 * g + r < R ? x : -INFINITY;     // padding rows past R
+                mx = fmaxf(mx, pr[t][r]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < KT; t++) {
+            int j0 = 16 * t + 4 * g - start;     // window key of ring row 16t + 4g, before the wrap
+            j0 += j0 < 0 ? R : 0;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int rr = 16 * t + 4 * g + r;   // ring row
+                int j = j0 + r;
+                j -= j >= R ? R : 0;
+                const bool kin = i < Tq && rr < R && j >= ks && j < ke;
+                const int bi = min(max(W - 1 + i - j, 0), BMAX - 1);
+                const float x = sacc[t][r] + sl[i][bi];
+                pr[t][r] = kin ? x : -INFINITY;
+                mx = fmaxf(mx, pr[t][r]);
+            }
         }
     }
     mx = xmax32(xmax16(mx));
+    // a masked score is -inf and 2^-inf = 0; a query with no key at all has mx = -inf and any
+    // finite offset serves
+    const float mc = mx == -INFINITY ? 0.0f : mx * c2;
     float sm = 0.0f;
 #pragma unroll
     for (int t = 0; t < KT; t++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            pr[t][r] = pr[t][r] == -INFINITY ? 0.0f : __expf(pr[t][r] - mx);
+            pr[t][r] = __builtin_amdgcn_exp2f(fmaf(pr[t][r], c2, -mc));
             sm += pr[t][r];
         }
     sm = xadd32(xadd16(sm));
@@ -1051,7 +1076,7 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
     //      8(a - 4) + 4 + g'.  Rows outside the key range are zeroed unless every ring row is a
     //      key (wave-uniform).  The transposed product leaves each lane 4 consecutive channels
     //      of query col.
-    const bool full = ks == 0 && ke == R;
+    const bool vfull = ks == 0 && ke == R;
     const int jb = g - start;                    // window key of ring row g, before the wrap
     f32x4_t oacc[8];
 #pragma unroll
@@ -1064,7 +1089,7 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
             const int pos = a8 < 4 ? 8 * a8 + g : 8 * (a8 - 4) + 4 + g;
             uint4 w = make_uint4(0, 0, 0, 0);
             if (it < NVL) {
-                if (full) {
+                if (vfull) {
                     w = vr[it];
                 } else {
                     int j = jb + 4 * it;
