@@ -90,6 +90,26 @@ def test_offline_batch_1500_sampled(gpu, orc):
         harness.assert_bf16_close(got[b, rows], ref[rows], "utterance %d" % b)
 
 
+@pytest.mark.parametrize("order", ["growing", "shrinking"])
+def test_offline_running_max(gpu, orc, order):
+    """Scores that grow (or shrink) along the keys: with q and k aligned and k scaled by its key index,
+    every 64-key tile raises (or never raises) each query's running maximum, so the accumulator is
+    rescaled on every tile (or only on the first); scores reach about +-25 before the scale."""
+    ud = gpu
+    rng = np.random.default_rng(34)
+    B, T = 1, 320
+    q, k, v, P, u, vb = _inputs(ud, rng, B, T)
+    ramp = np.linspace(0.0, 1.0, T, dtype=np.float32)
+    if order == "shrinking":
+        ramp = ramp[::-1].copy()
+    q = ud.round_bf16((np.abs(q) * 0.5 + 0.5).astype(np.float32))
+    k = ud.round_bf16((0.25 * rng.standard_normal((B, T, H * DK)) + 2.0 * ramp[None, :, None]).astype(np.float32))
+    ranges = np.zeros((B, T, 2), np.int32)
+    ranges[:, :, 1] = T
+    got = _run(ud, q, k, v, P, u, vb, ranges)
+    harness.assert_bf16_close(got, _oracle(orc, q, k, v, P, u, vb, ranges), "offline running max " + order)
+
+
 def test_offline_error_paths(gpu):
     ud = gpu
     b = ud.DeviceBuffer(1 << 12)
