@@ -109,6 +109,18 @@ def test_ring_attention_and_cache_update(gpu, orc, dtype, T, L):
     afterwards the exported window is exactly the last L rows of [old window ; new rows].  The
     fourth stream has an empty range (no cache, no valid frame): its output is 0.  L = 63 puts
     ring rows and new rows in the same 16-key pass; L = 17 leaves most passes past the window."""
+    _ring_case(gpu, orc, dtype, T, L, 1.0)
+
+
+@pytest.mark.parametrize("T", [2, 14])
+def test_ring_attention_large_scores(gpu, orc, T):
+    """q scaled by 8: scores with a spread of about +-25 before the softmax (a nearly one-hot
+    softmax), through the wave kernel (T = 2) and the MFMA kernel's full-window path (T = 14, the
+    first stream's cache full and every frame valid)."""
+    _ring_case(gpu, orc, "bf16", T, 70, 8.0)
+
+
+def _ring_case(gpu, orc, dtype, T, L, q_scale):
     ud = gpu
     cfg = ud.EncoderConfig(layers=2, left_context=L, max_chunk=max(T, 2), max_streams=4, dtype=dtype)
     enc, model, _ = harness.make_encoder(ud, orc, cfg, seed=5)
@@ -123,6 +135,7 @@ def test_ring_attention_and_cache_update(gpu, orc, dtype, T, L):
     valid = np.array([T, max(T - 1, 0), T, 0], np.int32)
     layer = 1
     qkv = rng.standard_normal((S, T, 3 * D)).astype(np.float32)
+    qkv[:, :, :D] *= q_scale
     if dtype == "bf16":
         # a 16-bit encoder's activations (qkv in, att out) are IEEE half
         qkv = ud.round_f16(qkv)
