@@ -11,7 +11,7 @@ import harness
 pytestmark = pytest.mark.gpu
 
 
-def _run_steps(ud, orc, cfg, S, T, n_steps, seed, seed_caches, valid_plan=None, enc_model=None):
+def _run_steps(ud, orc, cfg, S, T, n_steps, seed, seed_caches, valid_plan=None, enc_model=None, make_x=None):
     enc, model, _ = enc_model or harness.make_encoder(ud, orc, cfg, seed=seed)
     rng = np.random.default_rng(seed + 1)
     streams = [enc.new_stream() for _ in range(S)]
@@ -24,7 +24,7 @@ def _run_steps(ud, orc, cfg, S, T, n_steps, seed, seed_caches, valid_plan=None, 
     obuf = ud.DeviceBuffer(S * T * D * 4)
     results = []
     for step in range(n_steps):
-        x = rng.standard_normal((S, T, D)).astype(np.float32)
+        x = (make_x or (lambda r, shape: r.standard_normal(shape)))(rng, (S, T, D)).astype(np.float32)
         valid = np.full(S, T, np.int32) if valid_plan is None else np.asarray(valid_plan(step, S, T), np.int32)
         xbuf.upload(x)
         enc.encode_stream_step(streams, xbuf, obuf, valid=valid, T=T)
@@ -87,6 +87,23 @@ def test_step_bf16_config2_full(gpu, orc):
     cfg = gpu.EncoderConfig(layers=24, max_chunk=2, max_streams=64, dtype="bf16")
     plan = lambda step, S, T: [T - (s % 5 == 2 and step == 1) for s in range(S)]
     enc, _, _, res = _run_steps(gpu, orc, cfg, S=64, T=2, n_steps=2, seed=43, seed_caches=True, valid_plan=plan)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
+def test_step_bf16_offset_rows(gpu, orc):
+    """Rows far from zero mean (offsets 20-60, scales 0.5-4 per row): the residual stream keeps the
+    offsets, so every LayerNorm of the step normalises rows whose mean is large against their
+    spread (the two-pass variance).  5 streams x 2 frames = 10 rows: the 16-row tiles of the
+    projections have padding rows too."""
+    cfg = gpu.EncoderConfig(layers=2, max_chunk=2, max_streams=5, dtype="bf16")
+
+    def make_x(r, shape):
+        off = r.uniform(20.0, 60.0, shape[:2] + (1,))
+        scale = r.uniform(0.5, 4.0, shape[:2] + (1,))
+        return off + scale * r.standard_normal(shape)
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=5, T=2, n_steps=2, seed=53, seed_caches=True, make_x=make_x)
     for i, (got, ref) in enumerate(res):
         harness.assert_bf16_close(got, ref, "step %d" % i)
     enc.close()
