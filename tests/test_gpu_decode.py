@@ -192,3 +192,7 @@ def test_decode_error_paths(gpu):
         ud.gqa_attention_paged(b, b, b, b, 4, b, b, 1, 8, 2, 128, 64, small)
     with pytest.raises(ud.EngineError):        # max_keys beyond the page table
         ud.gqa_attention_paged(b, b, b, b, 4, b, b, 1, 8, 2, 128, 65, b)
+    with pytest.raises(ud.EngineError):        # more than 65535 splits of 128 keys (grid y)
+        ud.gqa_attention_paged(b, b, b, b, 1 << 20, b, b, 1, 8, 2, 128, 65535 * 128 + 1, b)
+    with pytest.raises(ud.EngineError):        # more than 65535 sequences (grid z)
+        ud.gqa_attention_paged(b, b, b, b, 4, b, b, 65536, 8, 2, 128, 64, b)

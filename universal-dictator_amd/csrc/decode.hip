@@ -9,8 +9,9 @@
 // one pool of fixed-size pages addressed through a block table.
 //
 // Design (HBM-bound: every K/V byte of every sequence is read once per step):
-//  - split-K ("flash decoding"): workgroup = (128-key split, kv head, sequence), 4 wave64s.  The
-//    Hq/Hkv query heads of a kv head share each K/V row read, so GQA costs no extra traffic;
+//  - split-K ("flash decoding"): workgroup = (kv head, 128-key split, sequence), 4 wave64s, kv head
+//    fastest in the grid so that the workgroups in flight read whole pages.  The Hq/Hkv query heads
+//    of a kv head share each K/V row read, so GQA costs no extra traffic;
 //  - 16 B per lane loads: a head_dim row is D/8 lanes wide; K and V of the split are all issued
 //    before the first score, V zeroed in registers outside the key range;
 //  - scores: per-row dot products of the G query heads reduced together with a transposed DPP
@@ -129,7 +130,7 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
     constexpr int LPR = D / 8, RG = 256 / LPR, NP = SPLIT / RG, NV = G * 8;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = tid / LPR, sub = tid % LPR;
-    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
     const int lo = max(a.ranges[2 * seq], 0), hi = min(a.ranges[2 * seq + 1], a.kmax);
     const int s0 = split * SPLIT;
     const int klo = max(lo, s0), khi = min(hi, s0 + SPLIT);
@@ -427,7 +428,11 @@ extern "C" UD_API size_t ud_gqa_workspace_bytes(int32_t n, int32_t q_heads, int3
 
 template <typename KT, int D>
 static int launch_gqa(const GqaArgs& a, int n, int G, int nsplit, float* out, hipStream_t st) {
-    dim3 grid(nsplit, a.Hkv, n), block(256);
+    // kv head fastest: the Hkv workgroups of one split run side by side and read each physical page's
+    // Hkv x 4 KB as one contiguous block ([page][kv head][row][dim]); with the split fastest, the
+    // workgroups in flight read scattered 4 KB pieces (measured on MI355X at 64 sequences, 8 kv
+    // heads: 123.7 us per call against 143.8, and 106.0 against 113.1 for loads alone)
+    dim3 grid(a.Hkv, nsplit, n), block(256);
     switch (G) {
         case 1: hipLaunchKernelGGL((gqa_split_kernel<KT, D, 1>), grid, block, 0, st, a); break;
         case 2: hipLaunchKernelGGL((gqa_split_kernel<KT, D, 2>), grid, block, 0, st, a); break;
@@ -455,6 +460,10 @@ static int gqa_check(const char* who, int32_t kv_dtype, const float* q_dev, cons
     if (block_size != PAGE) return dfail(UD_ERR_SHAPE, "%s: block_size %d (16 supported)", who, block_size);
     if (max_blocks < 1 || max_keys < 0 || max_keys > max_blocks * PAGE)
         return dfail(UD_ERR_SHAPE, "%s: max_keys %d beyond %d blocks", who, max_keys, max_blocks);
+    // grid y (splits) and z (sequences) hold at most 65535 workgroups
+    if (n > 65535 || nsplits(max_keys) > 65535)
+        return dfail(UD_ERR_SHAPE, "%s: n %d or max_keys %d beyond the grid (65535 sequences, 65535 x %d keys)", who,
+                     n, max_keys, SPLIT);
     if (((uintptr_t)q_dev | (uintptr_t)k_pages | (uintptr_t)v_pages) & 15)
         return dfail(UD_ERR_INVALID, "%s: buffers must be 16-byte aligned", who);
     return UD_OK;
