@@ -114,6 +114,29 @@ def test_paged_gqa_ragged(gpu, orc, Hq, Hkv, d, kv_dtype):
         harness.assert_bf16_close(got, ref, "paged gqa %s" % kv_dtype)
 
 
+@pytest.mark.parametrize("kv_dtype", ["bf16", "f16"])
+def test_paged_gqa_long_context(gpu, orc, kv_dtype):
+    """Contexts past 64 splits of 128 keys (the combine merges them 64 at a time): 17,000 and 9,000
+    keys, a window [5,000, 13,100) whose first and last splits are partial, and a 300-key sequence
+    in the same call."""
+    ud = gpu
+    rng = np.random.default_rng(61)
+    Hq, Hkv, d = 8, 2, 64
+    lens = [17000, 9000, 300, 13100]
+    n = len(lens)
+    kseqs = [rng.standard_normal((L, Hkv * d)).astype(np.float32) for L in lens]
+    vseqs = [rng.standard_normal((L, Hkv * d)).astype(np.float32) for L in lens]
+    ranges = np.array([[0, L] for L in lens], np.int32)
+    ranges[3] = [5000, 13100]
+    q = rng.standard_normal((n, Hq * d)).astype(np.float32)
+    got = run_paged(ud, q, kseqs, vseqs, ranges, Hq, Hkv, d, kv_dtype, rng)
+    ref = oracle_paged(orc, q, kseqs, vseqs, ranges, Hq, Hkv, kv_dtype)
+    if kv_dtype == "f16":
+        assert np.abs(got - ref).max() < 1e-4
+    else:
+        harness.assert_bf16_close(got, ref, "long context")
+
+
 def test_paged_gqa_decode_shape(gpu, orc):
     """The 64-sequence decode step: 32 query heads on 8 kv heads x 128, context lengths uniform in
     512..4096, bf16 pages of 16."""

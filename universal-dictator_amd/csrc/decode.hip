@@ -313,11 +313,14 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
 
 // Merge the splits of one (sequence, head), one wave: out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
 // Lane s holds split s's (max, sum) of a chunk of up to 64 splits; the weights reach every lane
-// with readlane, and the dims (D/64 per lane) accumulate with independent loads.
+// with readlane, and the dims (D/64 per lane) accumulate.  The partials of a chunk's first CB
+// splits are loaded together with its statistics, before the reductions that give the weights, so
+// a chunk of up to CB splits (4,096 keys) costs one round trip to memory instead of one per 8
+// splits after the statistics.
 template <int D>
 __global__ __launch_bounds__(64) void gqa_combine_kernel(const float* part, const int32_t* ranges, float* out,
                                                          int Hq, int NS, int kmax) {
-    constexpr int DL = D / 64;
+    constexpr int DL = D / 64, CB = 32;
     const int h = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
     const int lo = max(ranges[2 * seq], 0), hi = min(ranges[2 * seq + 1], kmax);
     float* o = out + ((int64_t)seq * Hq + h) * D;
@@ -335,26 +338,42 @@ __global__ __launch_bounds__(64) void gqa_combine_kernel(const float* part, cons
         const int cnt = min(64, sb - c0 + 1);
         const float m = lane < cnt ? pr[(c0 + lane) * (D + 2) + D] : -INFINITY;
         const float l = lane < cnt ? pr[(c0 + lane) * (D + 2) + D + 1] : 0.0f;
+        float x[CB][DL];
+#pragma unroll
+        for (int u = 0; u < CB; u++) {
+            if (u < cnt) {                            // wave-uniform
+#pragma unroll
+                for (int k = 0; k < DL; k++) x[u][k] = pr[(c0 + u) * (D + 2) + lane + 64 * k];
+            }
+        }
         const float nm = fmaxf(M, wave_max(m));
         const float keep = M == -INFINITY ? 0.0f : __expf(M - nm);
         const float w = lane < cnt ? __expf(m - nm) : 0.0f;
         L = L * keep + wave_sum(w * l);
 #pragma unroll
         for (int k = 0; k < DL; k++) acc[k] *= keep;
-        for (int s0 = 0; s0 < cnt; s0 += 8) {         // 8 splits' loads in flight at a time
-            float ws[8], x[8][DL];
+#pragma unroll
+        for (int u = 0; u < CB; u++) {
+            if (u < cnt) {
+                const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+#pragma unroll
+                for (int k = 0; k < DL; k++) acc[k] += wu * x[u][k];
+            }
+        }
+        for (int s0 = CB; s0 < cnt; s0 += 8) {        // the rest of the chunk, 8 splits' loads in flight at a time
+            float ws[8], y[8][DL];
 #pragma unroll
             for (int u = 0; u < 8; u++) {
                 const int si = min(s0 + u, cnt - 1);
                 ws[u] = s0 + u < cnt ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), si)) : 0.0f;
                 const float* ps = pr + (c0 + si) * (D + 2);
 #pragma unroll
-                for (int k = 0; k < DL; k++) x[u][k] = ps[lane + 64 * k];
+                for (int k = 0; k < DL; k++) y[u][k] = ps[lane + 64 * k];
             }
 #pragma unroll
             for (int u = 0; u < 8; u++)
 #pragma unroll
-                for (int k = 0; k < DL; k++) acc[k] += ws[u] * x[u][k];
+                for (int k = 0; k < DL; k++) acc[k] += ws[u] * y[u][k];
         }
         M = nm;
     }
