@@ -311,6 +311,196 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- bf16 pages, head_dim 128: MFMA
+// The same split as gqa_split_kernel, with the products on the matrix cores and no K/V in
+// registers:
+//  - one 32 KB LDS tile holds K, then V: K rows go global -> LDS with direct loads
+//    (global_load_lds_dwordx4) while V rows are loaded into registers; once every wave has read K,
+//    V (rows outside the range zeroed) is written over it.  Rows are 256 bytes, their 16-byte
+//    pieces permuted per row (kv_swz) by choosing each lane's source piece, so that the operand
+//    reads below fall on distinct banks.  About 34 KB of LDS: four workgroups per CU;
+//  - scores S^T = q . K^T on v_mfma_f32_16x16x32_bf16: A = q (rows = the G heads of the kv head,
+//    rounded once to bf16, zero rows above G), B = K^T (lane (c, g): key c, channels 8g .. 8g + 7),
+//    so lane (c, g) gets heads 4g .. 4g + 3 of key c;
+//  - the softmax of the split as in gqa_split_kernel (probabilities in LDS);
+//  - out^T = V^T . P^T: A = V^T by ds_read_b64_tr_b16, B = P^T (lane (c, g): head c's
+//    probabilities rounded to bf16), each wave owning two 16-channel tiles over all 128 keys, so no
+//    reduction across waves.
+// V rows outside the key range are zeroed (pages may hold NaN there, and 0 x NaN is NaN); K rows
+// outside it only feed scores that are replaced by -inf.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int kv_swz(int r, int p) {
+    return r * 256 + ((p ^ (((r & 3) << 1) | ((r >> 2) & 1) | (r & 8))) << 4);
+}
+
+// 16 bytes per lane, global -> LDS at dst + 16 * lane (dst wave-uniform)
+__device__ __forceinline__ void kv_direct16(const bf16* src, bf16* dst) {
+    __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+}
+
+__device__ __forceinline__ v4i16_t kv_tr16(const char* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)p);
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void gqa_split_mfma_kernel(GqaArgs a) {
+    constexpr int D = 128, ROWB = 2 * D;
+    // the wave index as a wave-uniform value, so that the page lookups are scalar loads (a vector
+    // load there would make the wait for it cover every load in flight)
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, g = lane >> 4;
+    const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
+    const int lo = max(a.ranges[2 * seq], 0), hi = min(a.ranges[2 * seq + 1], a.kmax);
+    const int s0 = split * SPLIT;
+    const int klo = max(lo, s0), khi = min(hi, s0 + SPLIT);
+    if (klo >= khi) return;                       // this split holds no key of the range
+    __shared__ __align__(16) char kv[SPLIT * ROWB];      // K, then V
+    __shared__ __align__(16) float sc[G][SPLIT];
+    __shared__ float stat[G][2];
+
+    // ---- K of the split into LDS, V into registers: wave w takes pages 2w, 2w + 1 of the split
+    //      (rows 32w .. 32w + 31); each instruction covers 4 rows, lane L holding piece L % 16 of
+    //      row L / 16 of them, which is source piece (L % 16) xor f(row).  Pages outside [klo, khi)
+    //      are clamped to pages inside it (their rows are masked below).
+    // q rows first (their loads issued before the K and V rows, so the wait below covers them)
+    float4 qx[4][2];
+    {
+        const float* qr = a.q + (int64_t)seq * a.Hq * D + (kvh * G + min(col, G - 1)) * D + 8 * g;
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+            qx[kc][0] = *reinterpret_cast<const float4*>(qr + 32 * kc);
+            qx[kc][1] = *reinterpret_cast<const float4*>(qr + 32 * kc + 4);
+        }
+    }
+    const int blo = klo / PAGE, bhi = (khi - 1) / PAGE;
+    const int32_t* bt = a.bt + (int64_t)seq * a.max_blocks;
+    const char* kp = static_cast<const char*>(a.kp);
+    const char* vp = static_cast<const char*>(a.vp);
+    // both page lookups before the first direct load (after it, the table is read by vector loads)
+    int64_t pbase[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const int b = min(max((s0 + 32 * wave + 16 * e) / PAGE, blo), bhi);
+        pbase[e] = ((int64_t)bt[b] * a.Hkv + kvh) * (PAGE * ROWB);
+    }
+    int64_t off[2][4];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const int r0 = 32 * wave + 16 * e;                           // first row of the page in the split
+        const int64_t base = pbase[e];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int pr = 4 * i + (lane >> 4);                      // row within the page
+            const int sp = (lane & 15) ^ (((pr & 3) << 1) | ((pr >> 2) & 1) | (pr & 8));
+            off[e][i] = base + pr * ROWB + sp * 16;
+            kv_direct16(reinterpret_cast<const bf16*>(kp + off[e][i]), reinterpret_cast<bf16*>(kv + (r0 + 4 * i) * ROWB));
+        }
+    }
+    uint4 vr[2][4];
+#pragma unroll
+    for (int e = 0; e < 2; e++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) vr[e][i] = ld16(vp + off[e][i]);
+    __builtin_amdgcn_s_waitcnt(0x0F78);           // vmcnt(8): q and the K rows landed (the V loads may not)
+    // q as the A operand: lane (r, g) holds q[head r][32kc + 8g .. + 7] in bf16 (zero for r >= G)
+    uint4 qa[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; kc++) {
+        const float4 x0 = qx[kc][0], x1 = qx[kc][1];
+        qa[kc] = col < G ? make_uint4(pack_bf16x2(x0.x, x0.y), pack_bf16x2(x0.z, x0.w), pack_bf16x2(x1.x, x1.y),
+                                      pack_bf16x2(x1.z, x1.w))
+                         : make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+
+    // ---- scores of the wave's keys 32w + 16t + c -> sc (masked keys -inf)
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int r = 32 * wave + 16 * t + col;
+        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+            const uint4 kb = *reinterpret_cast<const uint4*>(kv + kv_swz(r, 4 * kc + g));
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa[kc]), as_bf16x8(kb), acc, 0, 0, 0);
+        }
+        const int j = s0 + r;
+        const bool in = j >= klo && j < khi;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (4 * g + i < G) sc[4 * g + i][r] = in ? acc[i] * a.scale : -INFINITY;
+    }
+    __syncthreads();                              // every wave has read K
+
+    // ---- V over K in LDS, where the direct loads put K (rows outside the range zeroed)
+#pragma unroll
+    for (int e = 0; e < 2; e++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int r = 32 * wave + 16 * e + 4 * i + (lane >> 4), j = s0 + r;
+            const uint4 v = (j >= klo && j < khi) ? vr[e][i] : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4*>(kv + (32 * wave + 16 * e + 4 * i) * ROWB + 16 * lane) = v;
+        }
+
+    // ---- softmax of the split, one wave per head: probabilities in sc, (max, sum) in stat
+    for (int gh = wave; gh < G; gh += 4) {
+        float v[SPLIT / 64];
+        float m = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < SPLIT / 64; k++) { v[k] = sc[gh][lane + 64 * k]; m = fmaxf(m, v[k]); }
+        m = wave_max(m);
+        float l = 0.0f;
+#pragma unroll
+        for (int k = 0; k < SPLIT / 64; k++) {
+            v[k] = v[k] == -INFINITY ? 0.0f : __expf(v[k] - m);
+            l += v[k];
+            sc[gh][lane + 64 * k] = v[k];
+        }
+        l = wave_sum(l);
+        if (lane == 0) { stat[gh][0] = m; stat[gh][1] = l; }
+    }
+    __syncthreads();
+
+    // ---- out^T += V^T . P^T per 32-key piece kk.  B: lane (c, g) holds head c's probabilities of
+    //      keys 32kk + 4g + e (e < 4), then 32kk + 16 + 4g + e; A: V^T over the same keys (lane c
+    //      of a 16-lane group reads column c & 3 of rows 32kk + 4g + c / 4 and, 16 keys on, of
+    //      rows 32kk + 16 + 4g + c / 4: channels 16dt + 4(c & 3) .., half c & 1 of piece pc)
+    f32x4_t oacc[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+    const int hc = min(col, G - 1);
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+        const float4 p0 = *reinterpret_cast<const float4*>(&sc[hc][32 * kk + 4 * g]);
+        const float4 p1 = *reinterpret_cast<const float4*>(&sc[hc][32 * kk + 16 + 4 * g]);
+        const uint4 pb = col < G ? make_uint4(pack_bf16x2(p0.x, p0.y), pack_bf16x2(p0.z, p0.w), pack_bf16x2(p1.x, p1.y),
+                                              pack_bf16x2(p1.z, p1.w))
+                                 : make_uint4(0, 0, 0, 0);
+        const int k0 = 32 * kk + 4 * g + (col >> 2);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int dt = 2 * wave + u;
+            const int pc = 2 * dt + ((col & 3) >> 1), hb = (col & 1) * 8;
+            const v4i16_t b0 = kv_tr16(kv + kv_swz(k0, pc) + hb);
+            const v4i16_t b1 = kv_tr16(kv + kv_swz(k0 + 16, pc) + hb);
+            uint4 av;
+            __builtin_memcpy(&av.x, &b0, 8);
+            __builtin_memcpy(&av.z, &b1, 8);
+            oacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(pb), oacc[u], 0, 0, 0);
+        }
+    }
+
+    // ---- partial of head c: out^T lane (c, g) holds channels 16dt + 4g .. + 3; (max, sum) from stat
+    if (col < G) {
+        float* pr = a.part + (((int64_t)seq * a.Hq + kvh * G + col) * a.NS + split) * (D + 2);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            float* o = pr + 16 * (2 * wave + u) + 4 * g;
+            *reinterpret_cast<float2*>(o) = make_float2(oacc[u][0], oacc[u][1]);
+            *reinterpret_cast<float2*>(o + 2) = make_float2(oacc[u][2], oacc[u][3]);
+        }
+        if (wave == 0 && g == 0) { pr[D] = stat[col][0]; pr[D + 1] = stat[col][1]; }
+    }
+}
+
 // Merge the splits of one (sequence, head), one wave: out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
 // Lane s holds split s's (max, sum) of a chunk of up to 64 splits; the weights reach every lane
 // with readlane, and the dims (D/64 per lane) accumulate.  The partials of a chunk's first CB
@@ -447,6 +637,19 @@ extern "C" UD_API size_t ud_gqa_workspace_bytes(int32_t n, int32_t q_heads, int3
 
 template <typename KT, int D>
 static int launch_gqa(const GqaArgs& a, int n, int G, int nsplit, float* out, hipStream_t st) {
+    if constexpr (std::is_same<KT, BF16>::value && D == 128) {
+        // bf16 pages at head_dim 128: the MFMA split kernel (grid as below)
+        dim3 grid(a.Hkv, nsplit, n), block(256);
+        switch (G) {
+            case 1: hipLaunchKernelGGL((gqa_split_mfma_kernel<1>), grid, block, 0, st, a); break;
+            case 2: hipLaunchKernelGGL((gqa_split_mfma_kernel<2>), grid, block, 0, st, a); break;
+            case 4: hipLaunchKernelGGL((gqa_split_mfma_kernel<4>), grid, block, 0, st, a); break;
+            case 8: hipLaunchKernelGGL((gqa_split_mfma_kernel<8>), grid, block, 0, st, a); break;
+            default: return UD_ERR_SHAPE;
+        }
+        hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n), dim3(64), 0, st, a.part, a.ranges, out, a.Hq, a.NS, a.kmax);
+        return UD_OK;
+    }
     // kv head fastest: the Hkv workgroups of one split run side by side and read each physical page's
     // Hkv x 4 KB as one contiguous block ([page][kv head][row][dim]); with the split fastest, the
     // workgroups in flight read scattered 4 KB pieces (measured on MI355X at 64 sequences, 8 kv
