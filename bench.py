@@ -246,7 +246,7 @@ def decode_bench(ud, args):
                                "%d query / %d kv heads x %d, context %d..%d, pages of %d"
                                % (n, Hq, Hkv, d, wl["ctx"][0], wl["ctx"][1], page),
                    "sequences": n, "q_heads": Hq, "kv_heads": Hkv, "head_dim": d, "total_keys": int(lens.sum())},
-        "roofline": {"kernel": "gqa_split_kernel + gqa_combine_kernel (timed together)", "bound": "hbm",
+        "roofline": {"kernel": "gqa_split_mfma_kernel + gqa_combine_kernel (timed together)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("gqa_decode"),
                      "algorithmic_bytes_per_launch": algo},

@@ -17,6 +17,8 @@
 //  - scores: per-row dot products of the G query heads reduced together with a transposed DPP
 //    butterfly inside the row's lanes; softmax of a split in LDS; P.V reduced across row groups with
 //    v_permlane32_swap / v_permlane16_swap / DPP and across waves once through LDS;
+//  - bf16 pages at head_dim 128 take gqa_split_mfma_kernel instead: the same split with K staged
+//    in LDS by direct loads and both products on v_mfma_f32_16x16x32_bf16;
 //  - a second kernel merges the splits of each (sequence, head) with the usual max/sum rescaling.
 #include <hip/hip_runtime.h>
 
