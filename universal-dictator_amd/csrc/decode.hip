@@ -34,7 +34,8 @@ int ud_set_error(int code, const char* msg);   // encoder.hip
 
 namespace ud {
 
-constexpr int SPLIT = 128;      // keys per split workgroup
+constexpr int SPLIT = 128;      // keys per split workgroup (gqa_split_kernel)
+constexpr int MSPLIT = 256;     // keys per split workgroup of gqa_split_mfma_kernel (32 per wave)
 constexpr int PAGE = 16;        // block_size
 
 // Element formats of 16-bit K/V and RoPE rows (both stored as uint16_t).
@@ -316,18 +317,19 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
 // ---------------------------------------------------------------- bf16 pages, head_dim 128: MFMA
 // The same split as gqa_split_kernel, with the products on the matrix cores and no K/V in
 // registers:
-//  - one 32 KB LDS tile holds K, then V: K rows go global -> LDS with direct loads
+//  - 256-key splits, 8 waves of 32 keys (half the partials of 128-key splits);
+//  - one 64 KB LDS tile holds K, then V: K rows go global -> LDS with direct loads
 //    (global_load_lds_dwordx4) while V rows are loaded into registers; once every wave has read K,
 //    V (rows outside the range zeroed) is written over it.  Rows are 256 bytes, their 16-byte
 //    pieces permuted per row (kv_swz) by choosing each lane's source piece, so that the operand
-//    reads below fall on distinct banks.  About 34 KB of LDS: four workgroups per CU;
+//    reads below fall on distinct banks.  About 68 KB of LDS: two workgroups per CU;
 //  - scores S^T = q . K^T on v_mfma_f32_16x16x32_bf16: A = q (rows = the G heads of the kv head,
 //    rounded once to bf16, zero rows above G), B = K^T (lane (c, g): key c, channels 8g .. 8g + 7),
 //    so lane (c, g) gets heads 4g .. 4g + 3 of key c;
 //  - the softmax of the split as in gqa_split_kernel (probabilities in LDS);
 //  - out^T = V^T . P^T: A = V^T by ds_read_b64_tr_b16, B = P^T (lane (c, g): head c's
-//    probabilities rounded to bf16), each wave owning two 16-channel tiles over all 128 keys, so no
-//    reduction across waves.
+//    probabilities rounded to bf16), each wave owning 8 / (waves per workgroup) 16-channel tiles over the
+//    split's keys, so no reduction across waves.
 // V rows outside the key range are zeroed (pages may hold NaN there, and 0 x NaN is NaN); K rows
 // outside it only feed scores that are replaced by -inf.
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
@@ -346,19 +348,20 @@ __device__ __forceinline__ v4i16_t kv_tr16(const char* p) {
 }
 
 template <int G>
-__global__ __launch_bounds__(256) void gqa_split_mfma_kernel(GqaArgs a) {
-    constexpr int D = 128, ROWB = 2 * D;
+__global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
+    constexpr int D = 128, ROWB = 2 * D, KS = MSPLIT, NWV = KS / 32, DPW = 8 / NWV;   // DPW: channel tiles per wave
+    static_assert(KS % 64 == 0 && 8 % NWV == 0, "split of 64 .. 256 keys");
     // the wave index as a wave-uniform value, so that the page lookups are scalar loads (a vector
     // load there would make the wait for it cover every load in flight)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, g = lane >> 4;
     const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
     const int lo = max(a.ranges[2 * seq], 0), hi = min(a.ranges[2 * seq + 1], a.kmax);
-    const int s0 = split * SPLIT;
-    const int klo = max(lo, s0), khi = min(hi, s0 + SPLIT);
+    const int s0 = split * KS;
+    const int klo = max(lo, s0), khi = min(hi, s0 + KS);
     if (klo >= khi) return;                       // this split holds no key of the range
-    __shared__ __align__(16) char kv[SPLIT * ROWB];      // K, then V
-    __shared__ __align__(16) float sc[G][SPLIT];
+    __shared__ __align__(16) char kv[KS * ROWB];         // K, then V
+    __shared__ __align__(16) float sc[G][KS];
     __shared__ float stat[G][2];
 
     // ---- K of the split into LDS, V into registers: wave w takes pages 2w, 2w + 1 of the split
@@ -445,15 +448,15 @@ __global__ __launch_bounds__(256) void gqa_split_mfma_kernel(GqaArgs a) {
         }
 
     // ---- softmax of the split, one wave per head: probabilities in sc, (max, sum) in stat
-    for (int gh = wave; gh < G; gh += 4) {
-        float v[SPLIT / 64];
+    for (int gh = wave; gh < G; gh += NWV) {
+        float v[KS / 64];
         float m = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < SPLIT / 64; k++) { v[k] = sc[gh][lane + 64 * k]; m = fmaxf(m, v[k]); }
+        for (int k = 0; k < KS / 64; k++) { v[k] = sc[gh][lane + 64 * k]; m = fmaxf(m, v[k]); }
         m = wave_max(m);
         float l = 0.0f;
 #pragma unroll
-        for (int k = 0; k < SPLIT / 64; k++) {
+        for (int k = 0; k < KS / 64; k++) {
             v[k] = v[k] == -INFINITY ? 0.0f : __expf(v[k] - m);
             l += v[k];
             sc[gh][lane + 64 * k] = v[k];
@@ -467,10 +470,12 @@ __global__ __launch_bounds__(256) void gqa_split_mfma_kernel(GqaArgs a) {
     //      keys 32kk + 4g + e (e < 4), then 32kk + 16 + 4g + e; A: V^T over the same keys (lane c
     //      of a 16-lane group reads column c & 3 of rows 32kk + 4g + c / 4 and, 16 keys on, of
     //      rows 32kk + 16 + 4g + c / 4: channels 16dt + 4(c & 3) .., half c & 1 of piece pc)
-    f32x4_t oacc[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+    f32x4_t oacc[DPW];
+#pragma unroll
+    for (int u = 0; u < DPW; u++) oacc[u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     const int hc = min(col, G - 1);
 #pragma unroll
-    for (int kk = 0; kk < 4; kk++) {
+    for (int kk = 0; kk < KS / 32; kk++) {
         const float4 p0 = *reinterpret_cast<const float4*>(&sc[hc][32 * kk + 4 * g]);
         const float4 p1 = *reinterpret_cast<const float4*>(&sc[hc][32 * kk + 16 + 4 * g]);
         const uint4 pb = col < G ? make_uint4(pack_bf16x2(p0.x, p0.y), pack_bf16x2(p0.z, p0.w), pack_bf16x2(p1.x, p1.y),
@@ -478,8 +483,8 @@ __global__ __launch_bounds__(256) void gqa_split_mfma_kernel(GqaArgs a) {
                                  : make_uint4(0, 0, 0, 0);
         const int k0 = 32 * kk + 4 * g + (col >> 2);
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int dt = 2 * wave + u;
+        for (int u = 0; u < DPW; u++) {
+            const int dt = DPW * wave + u;
             const int pc = 2 * dt + ((col & 3) >> 1), hb = (col & 1) * 8;
             const v4i16_t b0 = kv_tr16(kv + kv_swz(k0, pc) + hb);
             const v4i16_t b1 = kv_tr16(kv + kv_swz(k0 + 16, pc) + hb);
@@ -494,8 +499,8 @@ __global__ __launch_bounds__(256) void gqa_split_mfma_kernel(GqaArgs a) {
     if (col < G) {
         float* pr = a.part + (((int64_t)seq * a.Hq + kvh * G + col) * a.NS + split) * (D + 2);
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-            float* o = pr + 16 * (2 * wave + u) + 4 * g;
+        for (int u = 0; u < DPW; u++) {
+            float* o = pr + 16 * (DPW * wave + u) + 4 * g;
             *reinterpret_cast<float2*>(o) = make_float2(oacc[u][0], oacc[u][1]);
             *reinterpret_cast<float2*>(o + 2) = make_float2(oacc[u][2], oacc[u][3]);
         }
@@ -511,7 +516,7 @@ __global__ __launch_bounds__(256) void gqa_split_mfma_kernel(GqaArgs a) {
 // splits after the statistics.
 template <int D>
 __global__ __launch_bounds__(64) void gqa_combine_kernel(const float* part, const int32_t* ranges, float* out,
-                                                         int Hq, int NS, int kmax) {
+                                                         int Hq, int NS, int kmax, int split) {
     constexpr int DL = D / 64, CB = 32;
     const int h = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
     const int lo = max(ranges[2 * seq], 0), hi = min(ranges[2 * seq + 1], kmax);
@@ -521,7 +526,7 @@ __global__ __launch_bounds__(64) void gqa_combine_kernel(const float* part, cons
         for (int k = 0; k < DL; k++) o[lane + 64 * k] = 0.0f;
         return;
     }
-    const int sa = lo / SPLIT, sb = (hi - 1) / SPLIT;
+    const int sa = lo / split, sb = (hi - 1) / split;
     const float* pr = part + ((int64_t)seq * Hq + h) * NS * (D + 2);
     float M = -INFINITY, L = 0.0f, acc[DL];
 #pragma unroll
@@ -630,7 +635,7 @@ static int dfail(int code, const char* fmt, ...) {
     return ud_set_error(code, buf);
 }
 
-static int nsplits(int32_t max_keys) { return max_keys <= 0 ? 1 : (max_keys + SPLIT - 1) / SPLIT; }
+static int nsplits(int32_t max_keys, int split = SPLIT) { return max_keys <= 0 ? 1 : (max_keys + split - 1) / split; }
 
 extern "C" UD_API size_t ud_gqa_workspace_bytes(int32_t n, int32_t q_heads, int32_t head_dim, int32_t max_keys) {
     if (n <= 0 || q_heads <= 0 || head_dim <= 0) return 0;
@@ -641,7 +646,7 @@ template <typename KT, int D>
 static int launch_gqa(const GqaArgs& a, int n, int G, int nsplit, float* out, hipStream_t st) {
     if constexpr (std::is_same<KT, BF16>::value && D == 128) {
         // bf16 pages at head_dim 128: the MFMA split kernel (grid as below)
-        dim3 grid(a.Hkv, nsplit, n), block(256);
+        dim3 grid(a.Hkv, nsplit, n), block(2 * MSPLIT);
         switch (G) {
             case 1: hipLaunchKernelGGL((gqa_split_mfma_kernel<1>), grid, block, 0, st, a); break;
             case 2: hipLaunchKernelGGL((gqa_split_mfma_kernel<2>), grid, block, 0, st, a); break;
@@ -649,7 +654,8 @@ static int launch_gqa(const GqaArgs& a, int n, int G, int nsplit, float* out, hi
             case 8: hipLaunchKernelGGL((gqa_split_mfma_kernel<8>), grid, block, 0, st, a); break;
             default: return UD_ERR_SHAPE;
         }
-        hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n), dim3(64), 0, st, a.part, a.ranges, out, a.Hq, a.NS, a.kmax);
+        hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n), dim3(64), 0, st, a.part, a.ranges, out, a.Hq, a.NS, a.kmax,
+                           MSPLIT);
         return UD_OK;
     }
     // kv head fastest: the Hkv workgroups of one split run side by side and read each physical page's
@@ -664,7 +670,8 @@ static int launch_gqa(const GqaArgs& a, int n, int G, int nsplit, float* out, hi
         case 8: hipLaunchKernelGGL((gqa_split_kernel<KT, D, 8>), grid, block, 0, st, a); break;
         default: return UD_ERR_SHAPE;
     }
-    hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n), dim3(64), 0, st, a.part, a.ranges, out, a.Hq, a.NS, a.kmax);
+    hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n), dim3(64), 0, st, a.part, a.ranges, out, a.Hq, a.NS, a.kmax,
+                       SPLIT);
     return UD_OK;
 }
 
@@ -702,8 +709,11 @@ static int gqa_launch(const char* who, int32_t kv_dtype, const float* q_dev, con
     GqaArgs a{};
     a.q = q_dev; a.kp = k_pages; a.vp = v_pages; a.bt = block_table; a.ranges = ranges_dev;
     a.part = workspace;
-    a.max_blocks = max_blocks; a.Hq = q_heads; a.Hkv = kv_heads; a.NS = nsplits(max_keys);
-    a.kmax = min(max_blocks * PAGE, a.NS * SPLIT);
+    // keys per split: MSPLIT on the MFMA path (bf16 pages, head_dim 128), SPLIT otherwise; the
+    // workspace is sized for SPLIT, the smaller, so it holds either
+    const int sp = kv_dtype == UD_BF16 && head_dim == 128 ? MSPLIT : SPLIT;
+    a.max_blocks = max_blocks; a.Hq = q_heads; a.Hkv = kv_heads; a.NS = nsplits(max_keys, sp);
+    a.kmax = min(max_blocks * PAGE, a.NS * sp);
     a.scale = 1.0f / sqrtf((float)head_dim);
     int rc;
     if (kv_dtype == UD_BF16)
