@@ -315,8 +315,7 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
 }
 
 // ---------------------------------------------------------------- bf16 pages, head_dim 128: MFMA
-// The same split as gqa_split_kernel, with the products on the matrix cores and no K/V in
-// registers:
+// gqa_split_kernel's design with the products on the matrix cores and no K in registers:
 //  - 256-key splits, 8 waves of 32 keys (half the partials of 128-key splits);
 //  - one 64 KB LDS tile holds K, then V: K rows go global -> LDS with direct loads
 //    (global_load_lds_dwordx4) while V rows are loaded into registers; once every wave has read K,
