@@ -89,7 +89,8 @@ def test_paged_gqa_reference_kat_f16(gpu, orc):
 
 
 @pytest.mark.parametrize("Hq,Hkv,d,kv_dtype", [(32, 8, 128, "bf16"), (8, 8, 64, "bf16"), (16, 8, 128, "f16"),
-                                               (16, 2, 64, "bf16"), (8, 4, 128, "bf16")])
+                                               (16, 2, 64, "bf16"), (8, 4, 128, "bf16"), (8, 8, 128, "bf16"),
+                                               (64, 8, 128, "bf16")])
 def test_paged_gqa_ragged(gpu, orc, Hq, Hkv, d, kv_dtype):
     """Ragged lengths across split and page boundaries (1, 15, 16, 17, 255, 256, 257, 700), a window
     start, an empty range; pages shuffled, unused pages full of NaN."""
@@ -114,14 +115,14 @@ def test_paged_gqa_ragged(gpu, orc, Hq, Hkv, d, kv_dtype):
         harness.assert_bf16_close(got, ref, "paged gqa %s" % kv_dtype)
 
 
-@pytest.mark.parametrize("kv_dtype", ["bf16", "f16"])
-def test_paged_gqa_long_context(gpu, orc, kv_dtype):
-    """Contexts past 64 splits of 128 keys (the combine merges them 64 at a time): 17,000 and 9,000
-    keys, a window [5,000, 13,100) whose first and last splits are partial, and a 300-key sequence
-    in the same call."""
+@pytest.mark.parametrize("d,kv_dtype", [(64, "bf16"), (64, "f16"), (128, "bf16")])
+def test_paged_gqa_long_context(gpu, orc, d, kv_dtype):
+    """Contexts past 64 splits (the combine merges them 64 at a time; 128-key splits, 256-key on the
+    MFMA path of bf16 pages at head_dim 128): 17,000 and 9,000 keys, a window [5,000, 13,100)
+    whose first and last splits are partial, and a 300-key sequence in the same call."""
     ud = gpu
-    rng = np.random.default_rng(61)
-    Hq, Hkv, d = 8, 2, 64
+    rng = np.random.default_rng(61 + d)
+    Hq, Hkv = 8, 2
     lens = [17000, 9000, 300, 13100]
     n = len(lens)
     kseqs = [rng.standard_normal((L, Hkv * d)).astype(np.float32) for L in lens]
