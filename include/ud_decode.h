@@ -40,7 +40,7 @@ extern "C" {
  *   max_keys     an upper bound of ranges[i].y over the batch (sizes the grid)
  *   workspace    device scratch of ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys) bytes
  * Supported: head_dim in {64, 128}, q_heads % kv_heads == 0, q_heads / kv_heads in {1, 2, 4, 8},
- * block_size 16.
+ * block_size 16, n <= 65535, max_keys <= 65535 * 128 (UD_ERR_SHAPE otherwise).
  * Precision: f16 pages are widened and used in fp32 arithmetic, as the reference kernel does.
  * bf16 pages use packed bf16 dot products: q and the softmax probabilities are rounded once to
  * bf16 (products exact, sums in fp32), within the bf16 activation bar (max abs 2e-2, cosine
