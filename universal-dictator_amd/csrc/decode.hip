@@ -327,8 +327,8 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
 //    so lane (c, g) gets heads 4g .. 4g + 3 of key c;
 //  - the softmax of the split as in gqa_split_kernel (probabilities in LDS);
 //  - out^T = V^T . P^T: A = V^T by ds_read_b64_tr_b16, B = P^T (lane (c, g): head c's
-//    probabilities rounded to bf16), each wave owning 8 / (waves per workgroup) 16-channel tiles over the
-//    split's keys, so no reduction across waves.
+//    probabilities rounded to bf16), wave w owning the 16-channel tiles w, w + (waves per
+//    workgroup), .. over the split's keys, so no reduction across waves.
 // V rows outside the key range are zeroed (pages may hold NaN there, and 0 x NaN is NaN); K rows
 // outside it only feed scores that are replaced by -inf.
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
@@ -348,8 +348,9 @@ __device__ __forceinline__ v4i16_t kv_tr16(const char* p) {
 
 template <int G>
 __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
-    constexpr int D = 128, ROWB = 2 * D, KS = MSPLIT, NWV = KS / 32, DPW = 8 / NWV;   // DPW: channel tiles per wave
-    static_assert(KS % 64 == 0 && 8 % NWV == 0, "split of 64 .. 256 keys");
+    constexpr int D = 128, ROWB = 2 * D, KS = MSPLIT, NWV = KS / 32;
+    constexpr int DPW = (8 + NWV - 1) / NWV;      // channel tiles per wave (the last ones may have fewer)
+    static_assert(KS % 64 == 0 && KS <= 256, "split of 64 .. 256 keys");
     // the wave index as a wave-uniform value, so that the page lookups are scalar loads (a vector
     // load there would make the wait for it cover every load in flight)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -483,7 +484,8 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
         const int k0 = 32 * kk + 4 * g + (col >> 2);
 #pragma unroll
         for (int u = 0; u < DPW; u++) {
-            const int dt = DPW * wave + u;
+            const int dt = wave + NWV * u;                // wave-uniform
+            if (dt >= 8) break;
             const int pc = 2 * dt + ((col & 3) >> 1), hb = (col & 1) * 8;
             const v4i16_t b0 = kv_tr16(kv + kv_swz(k0, pc) + hb);
             const v4i16_t b1 = kv_tr16(kv + kv_swz(k0 + 16, pc) + hb);
@@ -499,7 +501,8 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
         float* pr = a.part + (((int64_t)seq * a.Hq + kvh * G + col) * a.NS + split) * (D + 2);
 #pragma unroll
         for (int u = 0; u < DPW; u++) {
-            float* o = pr + 16 * (DPW * wave + u) + 4 * g;
+            if (wave + NWV * u >= 8) break;
+            float* o = pr + 16 * (wave + NWV * u) + 4 * g;
             *reinterpret_cast<float2*>(o) = make_float2(oacc[u][0], oacc[u][1]);
             *reinterpret_cast<float2*>(o + 2) = make_float2(oacc[u][2], oacc[u][3]);
         }
