@@ -103,7 +103,12 @@ UD_API int ud_streamer_stats(const ud_streamer* s, int64_t* batches, int64_t* ch
  * a projection each), so the call may mix them.  The encoder and decoder are used as by
  * ud_encoder_subsample / ud_encoder_step / ud_rnnt_project, with scratch owned by the encoder
  * (calls on one encoder must not overlap).  Asynchronous on hip_stream (frames_host is written
- * before the call returns). */
+ * before the call returns).
+ * Errors: every argument and shape check of both groups comes before anything is launched, so such
+ * an error leaves every stream unchanged.  A HIP or allocation failure inside the second group's
+ * calls (later steps) comes after the first group's streams (first steps) have advanced and their
+ * frames_host entries have been written; after any error other than a shape or argument error the
+ * caller should reset the call's streams. */
 UD_API int ud_nemotron_step(ud_encoder* enc, ud_rnnt* rnnt, ud_stream* const* streams, int32_t n, int32_t mel_rows,
                             const float* mel_dev, const int32_t* valid_rows_host, const int32_t* keep_all_host,
                             int32_t drop_extra, int32_t out_frames, float* proj_dev, int32_t proj_rows,

@@ -82,6 +82,22 @@ def set_threads(n):
         pass
 
 
+class store_limit:
+    """Context manager: the storage-range model of a 16-bit encoder (orc_set_store_limit) -- values
+    stored in 16 bits clamp to [-limit, limit] -- for the duration of the block; 0 = off."""
+
+    def __init__(self, limit):
+        self.limit = float(limit)
+
+    def __enter__(self):
+        lib().orc_set_store_limit(ctypes.c_float(self.limit))
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_store_limit(ctypes.c_float(0.0))
+        return False
+
+
 def lcg_floats(n, seed):
     out = np.empty(n, np.float32)
     lib().orc_lcg_floats(_p(out), ctypes.c_int64(n), ctypes.c_uint64(seed))

@@ -28,6 +28,9 @@
  *                         rel_shift, chunked_limited mask)
  *   orc_stream_step       streaming == offline equivalence through the
  *                         torch restatement, and the cache rule
+ *   orc_set_store_limit   the torch restatement with the same clamps at the
+ *                         same points (a limit small enough that every clamp
+ *                         point engages), and limit 0 == no limit
  *   orc_gqa_attention     reference KAT (VoxtralOpTests.swift:6-38) against a
  *                         numpy float64 softmax attention; GQA head map
  *   orc_rope_rotate_half  reference KAT (VoxtralOpTests.swift:60-75) against
@@ -331,6 +334,20 @@ enum {
 
 ORC_API int orc_weight_count(void) { return W_COUNT; }
 
+/* Storage-range model of a 16-bit encoder (not part of the reference, whose activations are fp32):
+ * with a limit > 0, every value the 16-bit encoder stores in 16 bits -- the LayerNorm outputs that
+ * feed a projection, the FF hidden, q/k/v (and so the cached K/V rows), the attention output and
+ * the conv module's LayerNorm + SiLU output -- is clamped to [-limit, limit] (NaN kept), as the
+ * HIP library's saturating half stores do at limit 65504.  0 (the default) = no limit. */
+static float g_store_limit = 0.0f;
+ORC_API void orc_set_store_limit(float limit) { g_store_limit = limit > 0.0f ? limit : 0.0f; }
+static void orc_store_clip(float* x, int64_t n) {
+    const float lim = g_store_limit;
+    if (lim <= 0.0f) return;
+    for (int64_t i = 0; i < n; i++)
+        if (!isnan(x[i])) x[i] = x[i] < -lim ? -lim : (x[i] > lim ? lim : x[i]);
+}
+
 /* FastConformer.swift:161-178: P_l = PE . W_pos,l^T over rel = lo..hi (one table per layer). */
 ORC_API void orc_pos_table(const float* wpos, int lo, int hi, int D, float* P) {
     int n = hi - lo + 1;
@@ -368,14 +385,20 @@ ORC_API void orc_encoder_layer(const float* const* w, const float* P, int rel_of
 
     /* FF1 (macaron, x0.5): FastConformer.swift:276-279 */
     orc_layer_norm(x, w[W_NORM_FF1_W], w[W_NORM_FF1_B], tmp, M, D, 1e-5f, ORC_ACT_NONE);
+    orc_store_clip(tmp, M * D);
     orc_gemm_nt(tmp, w[W_FF1_W1], NULL, NULL, ffh, (int)M, ff, D, 1.0f, ORC_ACT_SILU, 1.0f, 1.0f);
+    orc_store_clip(ffh, M * ff);
     orc_gemm_nt(ffh, w[W_FF1_W2], NULL, x, r1, (int)M, D, ff, 1.0f, ORC_ACT_NONE, 0.5f, 1.0f);
 
     /* Self-attention: FastConformer.swift:282-292 */
     orc_layer_norm(r1, w[W_NORM_ATT_W], w[W_NORM_ATT_B], tmp, M, D, 1e-5f, ORC_ACT_NONE);
+    orc_store_clip(tmp, M * D);
     orc_gemm_nt(tmp, w[W_Q], NULL, NULL, q, (int)M, D, D, 1.0f, ORC_ACT_NONE, 1.0f, 1.0f);
     orc_gemm_nt(tmp, w[W_K], NULL, NULL, kn, (int)M, D, D, 1.0f, ORC_ACT_NONE, 1.0f, 1.0f);
     orc_gemm_nt(tmp, w[W_V], NULL, NULL, vn, (int)M, D, D, 1.0f, ORC_ACT_NONE, 1.0f, 1.0f);
+    orc_store_clip(q, M * D);
+    orc_store_clip(kn, M * D);
+    orc_store_clip(vn, M * D);
     for (int s = 0; s < S; s++) {
         memcpy(keys + ((int64_t)s * Tk + Tk - T) * D, kn + (int64_t)s * T * D, sizeof(float) * T * D);
         memcpy(vals + ((int64_t)s * Tk + Tk - T) * D, vn + (int64_t)s * T * D, sizeof(float) * T * D);
@@ -383,10 +406,12 @@ ORC_API void orc_encoder_layer(const float* const* w, const float* P, int rel_of
                              w[W_BIAS_U], w[W_BIAS_V], ranges + (int64_t)s * T * 2, att + (int64_t)s * T * D,
                              T, Tk, H, dk, D, D, D, D, rel_offset, n_rel, 1.0f / sqrtf((float)dk));
     }
+    orc_store_clip(att, M * D);
     orc_gemm_nt(att, w[W_O], NULL, r1, r2, (int)M, D, D, 1.0f, ORC_ACT_NONE, 1.0f, 1.0f);
 
     /* Convolution module: FastConformer.swift:295-311 (causal conv, conv LayerNorm + SiLU) */
     orc_layer_norm(r2, w[W_NORM_CONV_W], w[W_NORM_CONV_B], tmp, M, D, 1e-5f, ORC_ACT_NONE);
+    orc_store_clip(tmp, M * D);
     orc_gemm_nt(tmp, w[W_PW1], NULL, NULL, pw, (int)M, 2 * D, D, 1.0f, ORC_ACT_NONE, 1.0f, 1.0f);
     for (int s = 0; s < S; s++) {
         float* ci = convIn + (int64_t)s * CIN * D;
@@ -398,11 +423,14 @@ ORC_API void orc_encoder_layer(const float* const* w, const float* P, int rel_of
         orc_dwconv1d(ci, w[W_DW], NULL, r4 + (int64_t)s * T * D, T, D, Kc, ORC_ACT_NONE);
     }
     orc_layer_norm(r4, w[W_CONV_LN_W], w[W_CONV_LN_B], tmp, M, D, 1e-5f, ORC_ACT_SILU);
+    orc_store_clip(tmp, M * D);
     orc_gemm_nt(tmp, w[W_PW2], NULL, r2, r3, (int)M, D, D, 1.0f, ORC_ACT_NONE, 1.0f, 1.0f);
 
     /* FF2 (x0.5) and the output LayerNorm: FastConformer.swift:314-320 */
     orc_layer_norm(r3, w[W_NORM_FF2_W], w[W_NORM_FF2_B], tmp, M, D, 1e-5f, ORC_ACT_NONE);
+    orc_store_clip(tmp, M * D);
     orc_gemm_nt(tmp, w[W_FF2_W1], NULL, NULL, ffh, (int)M, ff, D, 1.0f, ORC_ACT_SILU, 1.0f, 1.0f);
+    orc_store_clip(ffh, M * ff);
     orc_gemm_nt(ffh, w[W_FF2_W2], NULL, r3, r4, (int)M, D, ff, 1.0f, ORC_ACT_NONE, 0.5f, 1.0f);
     orc_layer_norm(r4, w[W_NORM_OUT_W], w[W_NORM_OUT_B], out, M, D, 1e-5f, ORC_ACT_NONE);
 

@@ -1,12 +1,14 @@
 """Shared set-up for GPU parity tests: the same seeded weights go to the HIP encoder and to the
-oracle (fp32 activations; for a 16-bit encoder (dtype "bf16") the oracle gets the bf16-rounded
-linear weights that the encoder computes with, which is the reference's own bf16-weight setting,
-Core/Kernels.swift:79-112; the encoder holds them, its activations and its K/V caches as IEEE half)."""
+oracle (fp32 activations).  For a 16-bit encoder the oracle gets the rounded linear weights that
+the encoder computes with: bf16-rounded for dtype "bf16" (the reference's bf16-weight setting,
+Core/Kernels.swift:79-112), f16-rounded for dtype "f16" (WeightConverter.convert(.f16),
+Core/Convert.swift:76-112).  Either way the encoder holds the weights, its activations and its K/V
+caches as IEEE half."""
 import os
 
 import numpy as np
 
-# Linear weights that a bf16 encoder stores in bf16 (the rest stay fp32: norms, pos_bias, depthwise
+# Linear weights that a 16-bit encoder stores rounded (the rest stay fp32: norms, pos_bias, depthwise
 # conv -- Sources/DictatorEngine/Core/Convert.swift:76-83).
 BF16_WEIGHTS = {
     "feed_forward1.linear1.weight", "feed_forward1.linear2.weight", "self_attn.linear_q.weight",
@@ -16,17 +18,47 @@ BF16_WEIGHTS = {
 }
 
 
-def make_encoder(ud, orc, cfg, seed=1234, ln_jitter=0.1):
+def is16(cfg):
+    """A 16-bit encoder (dtype bf16 or f16): half activations and caches."""
+    return cfg.dtype in ("bf16", "f16")
+
+
+def round_weights(ud, cfg, lw):
+    """The layer weights as the encoder of cfg computes with them (linear weights rounded)."""
+    if cfg.dtype == "bf16":
+        return [{k: (ud.round_bf16(v) if k in BF16_WEIGHTS else v) for k, v in w.items()} for w in lw]
+    if cfg.dtype == "f16":
+        return [{k: (ud.round_f16(v) if k in BF16_WEIGHTS else v) for k, v in w.items()} for w in lw]
+    return lw
+
+
+def make_encoder(ud, orc, cfg, seed=1234, ln_jitter=0.1, edit=None):
+    """(encoder, oracle model, oracle weights); edit(layer, weights) may change the synthetic
+    weights before both sides get them."""
     lw = [ud.synthetic_layer_weights(cfg, seed, l, ln_jitter=ln_jitter) for l in range(cfg.layers)]
+    if edit is not None:
+        for l, w in enumerate(lw):
+            edit(l, w)
     enc = ud.Encoder(cfg)
     for l, w in enumerate(lw):
         enc.set_layer_weights(l, w)
     enc.finalize()
-    if cfg.dtype == "bf16":
-        lw = [{k: (ud.round_bf16(v) if k in BF16_WEIGHTS else v) for k, v in w.items()} for w in lw]
+    lw = round_weights(ud, cfg, lw)
     model = orc.Model(lw, cfg.d_model, cfg.heads, cfg.ff_dim, cfg.conv_kernel)
     model.prepare(-(cfg.max_chunk - 1), cfg.left_context + cfg.max_chunk - 1)
     return enc, model, lw
+
+
+def oracle_sub_weights(sw, half):
+    """The subsampling weights the oracle gets for an encoder whose front-end GEMMs run on half
+    operands (half=True) -- the reference's f16 checkpoint policy, WeightConverter.keepF32 and
+    convert(.f16) (Sources/DictatorEngine/Core/Convert.swift:76-112): pre_encode.out.weight
+    rounded to f16, and every encoder.pre_encode.conv.* tensor kept fp32 (the library holds
+    conv.3 and conv.6 as half too; that rounding shows up in the measured error)."""
+    if not half:
+        return dict(sw)
+    return {k: (np.asarray(v, np.float32).astype(np.float16).astype(np.float32)
+                if k == "encoder.pre_encode.out.weight" else v) for k, v in sw.items()}
 
 
 # Achieved errors of the parity checks of this session, printed by the terminal summary of
@@ -71,9 +103,21 @@ class OracleState:
         self.c = np.zeros((S, cfg.layers, KC, D), np.float32)
         self.len = np.zeros(S, np.int32)
 
-    def seed_random(self, rng, cache_len):
-        self.k[:] = rng.standard_normal(self.k.shape, dtype=np.float32)
-        self.v[:] = rng.standard_normal(self.v.shape, dtype=np.float32)
+    def seed_random(self, rng, cache_len, blocks=None):
+        """N(0,1) caches.  blocks: draw only that many distinct [L, D] K and V windows and deal them
+        to the (stream, layer) pairs in a fixed scrambled order (cheap for hundreds of streams x 24
+        layers; neighbouring streams and layers still get different windows)."""
+        if blocks is None:
+            self.k[:] = rng.standard_normal(self.k.shape, dtype=np.float32)
+            self.v[:] = rng.standard_normal(self.v.shape, dtype=np.float32)
+        else:
+            S, layers = self.k.shape[:2]
+            kb = rng.standard_normal((blocks,) + self.k.shape[2:], dtype=np.float32)
+            vb = rng.standard_normal((blocks,) + self.v.shape[2:], dtype=np.float32)
+            for s in range(S):
+                for l in range(layers):
+                    self.k[s, l] = kb[(7 * s + 13 * l) % blocks]
+                    self.v[s, l] = vb[(11 * s + 5 * l + 3) % blocks]
         self.c[:] = rng.standard_normal(self.c.shape, dtype=np.float32)
         self.len[:] = cache_len
 

@@ -34,22 +34,26 @@ def nemo_pe(T, D):
     return pe
 
 
-def layer_nemo(x, w, pe, mask, valid, H, Kc=9):
+def layer_nemo(x, w, pe, mask, valid, H, Kc=9, clip=None):
     """One NeMo ConformerLayer (conformer_modules.py:160-233 per docs/specs/nemotron.md:83-135) on a
     full utterance x [T, D] (float64 torch).  pe: projected-input table rows for positions
-    T-1..-(T-1) [2T-1, D]; mask [T, T] bool, True = hidden; rows >= valid are padding."""
+    T-1..-(T-1) [2T-1, D]; mask [T, T] bool, True = hidden; rows >= valid are padding.
+    clip: if set, the activations a 16-bit encoder stores in 16 bits (the LayerNorm outputs feeding
+    a projection, the FF hidden, q/k/v, the attention output, the conv LayerNorm + SiLU output) are
+    clamped to [-clip, clip] (torch.clamp)."""
     import torch
     import torch.nn.functional as F
     T, D = x.shape
     dk = D // H
+    c16 = (lambda y: torch.clamp(y, -clip, clip)) if clip else (lambda y: y)
     t = lambda k: torch.as_tensor(w[k], dtype=torch.float64)
-    ln = lambda y, n: F.layer_norm(y, (D,), t(n + ".weight"), t(n + ".bias"), eps=1e-5)
-    r = x + 0.5 * F.linear(F.silu(F.linear(ln(x, "norm_feed_forward1"), t("feed_forward1.linear1.weight"))),
+    ln = lambda y, n: c16(F.layer_norm(y, (D,), t(n + ".weight"), t(n + ".bias"), eps=1e-5))
+    r = x + 0.5 * F.linear(c16(F.silu(F.linear(ln(x, "norm_feed_forward1"), t("feed_forward1.linear1.weight")))),
                            t("feed_forward1.linear2.weight"))
     z = ln(r, "norm_self_att")
-    q = F.linear(z, t("self_attn.linear_q.weight")).view(T, H, dk).transpose(0, 1)
-    k = F.linear(z, t("self_attn.linear_k.weight")).view(T, H, dk).transpose(0, 1)
-    v = F.linear(z, t("self_attn.linear_v.weight")).view(T, H, dk).transpose(0, 1)
+    q = c16(F.linear(z, t("self_attn.linear_q.weight"))).view(T, H, dk).transpose(0, 1)
+    k = c16(F.linear(z, t("self_attn.linear_k.weight"))).view(T, H, dk).transpose(0, 1)
+    v = c16(F.linear(z, t("self_attn.linear_v.weight"))).view(T, H, dk).transpose(0, 1)
     p = F.linear(torch.as_tensor(pe), t("self_attn.linear_pos.weight")).view(2 * T - 1, H, dk).transpose(0, 1)
     qu = q + t("self_attn.pos_bias_u").view(H, 1, dk)
     qv = q + t("self_attn.pos_bias_v").view(H, 1, dk)
@@ -59,18 +63,18 @@ def layer_nemo(x, w, pe, mask, valid, H, Kc=9):
     m = torch.as_tensor(mask)
     s = s.masked_fill(m, -10000.0)
     a = torch.softmax(s, dim=-1).masked_fill(m, 0.0)
-    o = (a @ v).transpose(0, 1).reshape(T, D)
+    o = c16((a @ v).transpose(0, 1).reshape(T, D))
     r = r + F.linear(o, t("self_attn.linear_out.weight"))
     z = ln(r, "norm_conv")
     g = F.glu(F.linear(z, t("conv.pointwise_conv1.weight")), dim=-1)
     g[valid:] = 0.0
     dw = t("conv.depthwise_conv.weight").view(D, 1, Kc)
     c = F.conv1d(F.pad(g.T.unsqueeze(0), (Kc - 1, 0)), dw, groups=D)[0].T
-    c = F.silu(F.layer_norm(c, (D,), t("conv.batch_norm.weight"), t("conv.batch_norm.bias"), eps=1e-5))
+    c = c16(F.silu(F.layer_norm(c, (D,), t("conv.batch_norm.weight"), t("conv.batch_norm.bias"), eps=1e-5)))
     r = r + F.linear(c, t("conv.pointwise_conv2.weight"))
-    r = r + 0.5 * F.linear(F.silu(F.linear(ln(r, "norm_feed_forward2"), t("feed_forward2.linear1.weight"))),
+    r = r + 0.5 * F.linear(c16(F.silu(F.linear(ln(r, "norm_feed_forward2"), t("feed_forward2.linear1.weight")))),
                            t("feed_forward2.linear2.weight"))
-    return ln(r, "norm_out")
+    return F.layer_norm(r, (D,), t("norm_out.weight"), t("norm_out.bias"), eps=1e-5)
 
 
 def chunked_limited_mask(T, left, right, valid):

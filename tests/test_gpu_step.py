@@ -11,25 +11,31 @@ import harness
 pytestmark = pytest.mark.gpu
 
 
-def _run_steps(ud, orc, cfg, S, T, n_steps, seed, seed_caches, valid_plan=None, enc_model=None, make_x=None):
+def _run_steps(ud, orc, cfg, S, T, n_steps, seed, seed_caches, valid_plan=None, enc_model=None, make_x=None,
+               T_plan=None, store_limit=0.0, cache_blocks=None):
+    """n_steps steps of S streams (T frames each, or T_plan(step) frames) through the encoder and
+    the oracle; returns (encoder, streams, oracle state, [(got, ref) per step])."""
     enc, model, _ = enc_model or harness.make_encoder(ud, orc, cfg, seed=seed)
     rng = np.random.default_rng(seed + 1)
     streams = [enc.new_stream() for _ in range(S)]
     st = harness.OracleState(S, cfg)
     if seed_caches:
-        st.seed_random(rng, cfg.left_context)
-        st.import_into(streams, ud, cfg.dtype == "bf16")
+        st.seed_random(rng, cfg.left_context, blocks=cache_blocks)
+        st.import_into(streams, ud, harness.is16(cfg))
     D = cfg.d_model
-    xbuf = ud.DeviceBuffer(S * T * D * 4)
-    obuf = ud.DeviceBuffer(S * T * D * 4)
+    T0 = T
+    xbuf = ud.DeviceBuffer(S * cfg.max_chunk * D * 4)
+    obuf = ud.DeviceBuffer(S * cfg.max_chunk * D * 4)
     results = []
     for step in range(n_steps):
+        T = T_plan(step) if T_plan else T0
         x = (make_x or (lambda r, shape: r.standard_normal(shape)))(rng, (S, T, D)).astype(np.float32)
         valid = np.full(S, T, np.int32) if valid_plan is None else np.asarray(valid_plan(step, S, T), np.int32)
         xbuf.upload(x)
         enc.encode_stream_step(streams, xbuf, obuf, valid=valid, T=T)
         got = obuf.download((S, T, D))
-        ref = orc.stream_step(model, x, valid, st.k, st.v, st.c, st.len)
+        with orc.store_limit(store_limit):
+            ref = orc.stream_step(model, x, valid, st.k, st.v, st.c, st.len)
         results.append((got, ref))
         for s, stream in enumerate(streams):
             assert stream.cache_len == st.len[s]
@@ -162,6 +168,139 @@ def test_step_bf16_chunk14_24_layers_lds_tiles(gpu, orc):
     for i, (got, ref) in enumerate(res):
         harness.assert_bf16_close(got, ref, "step %d" % i)
     enc.close()
+
+
+def test_step_bf16_config3_full(gpu, orc):
+    """Config 3 exactly: 256 streams x 14 frames (84 keys), 24 layers, seeded full caches, two steps
+    (ragged valid counts on the second), against the oracle's fp32 step -- the workload the
+    benchmark's chunk-14 line times.  (The 24 x 256 cached K/V windows are dealt from 96 distinct
+    N(0,1) draws to keep the host-side set-up short.)"""
+    cfg = gpu.EncoderConfig(layers=24, max_chunk=14, max_streams=256, dtype="bf16")
+    plan = lambda step, S, T: [(T, 11, T, 0, 6, T, 1)[s % 7] if step == 1 else T for s in range(S)]
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=256, T=14, n_steps=2, seed=69, seed_caches=True, valid_plan=plan,
+                                cache_blocks=96)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
+def test_step_bf16_ring_longer_than_window(gpu, orc):
+    """An encoder sized for 14-frame chunks stepping shorter chunks: the K/V rings hold
+    L + max_chunk = 84 rows while a 5- or 7-frame step's window is 75 or 77 keys, so the chunk
+    attention kernel reads ring rows outside the window and must mask them (and its key-band
+    index clamps).  Eight steps of 5 and 7 frames wrap the 84-row rings several times; some
+    streams have valid < T."""
+    cfg = gpu.EncoderConfig(layers=2, max_chunk=14, max_streams=6, dtype="bf16")
+    Ts = (5, 7, 7, 5, 7, 5, 5, 7)
+    plan = lambda step, S, T: [(T, T - 2, 0, T, 1, T)[s] if step % 3 == 1 else T for s in range(S)]
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=6, T=7, n_steps=len(Ts), seed=73, seed_caches=True,
+                                valid_plan=plan, T_plan=lambda step: Ts[step])
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d (T = %d)" % (i, Ts[i]))
+    enc.close()
+
+
+@pytest.mark.parametrize("S,T,layers", [(64, 2, 24), (32, 14, 24)])
+def test_step_f16_weights(gpu, orc, S, T, layers):
+    """The f16-weight encoder (UD_F16): linear weights rounded fp32 -> half directly, as
+    WeightConverter.convert(.f16) writes the reference's f16 checkpoint (Core/Convert.swift:76-112),
+    against the oracle given the same f16-rounded weights, at config 2's shape and config 3's chunk,
+    24 layers, seeded full caches, two steps."""
+    cfg = gpu.EncoderConfig(layers=layers, max_chunk=T, max_streams=S, dtype="f16")
+    plan = lambda step, S_, T_: [(T_, T_ - 1, T_, 0)[s % 4] if step == 1 else T_ for s in range(S_)]
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=S, T=T, n_steps=2, seed=75 + T, seed_caches=True, valid_plan=plan)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
+def test_step_f16_weights_differ_from_bf16(gpu, orc):
+    """The two 16-bit modes hold different weights: the same seeded model stepped by a UD_F16 and a
+    UD_BF16 encoder gives different outputs, each within the bar of the oracle given its own
+    rounding and, on average, closer to its own oracle than to the other's (f16 rounding keeps 3
+    more bits)."""
+    outs = {}
+    for dt in ("f16", "bf16"):
+        cfg = gpu.EncoderConfig(layers=2, max_chunk=2, max_streams=4, dtype=dt)
+        enc, _, _, res = _run_steps(gpu, orc, cfg, S=4, T=2, n_steps=1, seed=77, seed_caches=True)
+        got, ref = res[0]
+        outs[dt] = (got, ref)
+        harness.assert_bf16_close(got, ref, dt)
+        enc.close()
+    (g16, r16), (gbf, rbf) = outs["f16"], outs["bf16"]
+    assert np.abs(g16 - gbf).max() > 0                  # different weights
+    assert np.abs(g16 - r16).mean() < np.abs(g16 - rbf).mean()
+
+
+def test_step_half_range_saturates(gpu, orc):
+    """A 16-bit encoder's activations beyond half's range: feed_forward1.linear1 of layer 0 scaled by
+    2e5 puts about a third of the FF hidden past 65504.  The library's 16-bit stores saturate at
+    +-65504 (NaN kept), so the output stays finite and matches the oracle run with the same
+    storage-range model (oracle.store_limit(65504)); the unclamped fp32 oracle differs from it by
+    far more than the bar, so the clamp is what the comparison checks."""
+    ud = gpu
+    cfg = ud.EncoderConfig(layers=2, max_chunk=2, max_streams=4, dtype="bf16")
+    scale = np.float32(2e5)
+
+    def edit(l, w):
+        if l == 0:
+            w["feed_forward1.linear1.weight"] = w["feed_forward1.linear1.weight"] * scale
+    enc_model = harness.make_encoder(ud, orc, cfg, seed=79, edit=edit)
+    # the same state through the unclamped oracle, for the sensitivity check
+    _, model, _ = enc_model
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4, 2, 1024)).astype(np.float32)
+    st = harness.OracleState(4, cfg)
+    st.seed_random(np.random.default_rng(80), cfg.left_context)
+    h = orc.layer_norm(x.reshape(8, 1024), model.layers[0][0], model.layers[0][1])
+    pre = orc.gemm_nt(h, model.layers[0][2])
+    assert (np.abs(pre) > 65504).mean() > 0.2           # the hidden does leave half's range
+    enc, _, _, res = _run_steps(ud, orc, cfg, S=4, T=2, n_steps=2, seed=79, seed_caches=True, enc_model=enc_model,
+                                store_limit=65504.0)
+    for i, (got, ref) in enumerate(res):
+        assert np.isfinite(got).all(), "step %d: non-finite output" % i
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    free = orc.stream_step(model, x, np.full(4, 2, np.int32), st.k, st.v, st.c, st.len)
+    with orc.store_limit(65504.0):
+        st2 = harness.OracleState(4, cfg)
+        st2.seed_random(np.random.default_rng(80), cfg.left_context)
+        clamped = orc.stream_step(model, x, np.full(4, 2, np.int32), st2.k, st2.v, st2.c, st2.len)
+    assert np.abs(free - clamped).max() > 0.1
+    enc.close()
+
+
+def test_alternating_hip_streams_and_graph_eviction(gpu, orc):
+    """Nine distinct (n, T) steps issued back to back, without host waits, on two HIP streams in
+    turn: more step shapes than the encoder's graph cache holds (8), so the ninth evicts a graph
+    whose last launch was on the other stream and may still be running.  The encoder orders its
+    calls across streams and waits for its own work before destroying a graph; the outputs are
+    bit-identical to the same steps launched eagerly and synchronously."""
+    ud = gpu
+    shapes = [(12, 2), (8, 3), (4, 6), (12, 1), (6, 5), (10, 4), (3, 6), (12, 6), (5, 2)]
+    rng = np.random.default_rng(17)
+    xs = [rng.standard_normal((n, T, 1024)).astype(np.float32) for n, T in shapes]
+    outs = []
+    for graphs in ("1", "0"):
+        os.environ["UD_GRAPHS"] = graphs
+        try:
+            cfg = ud.EncoderConfig(layers=2, max_chunk=6, max_streams=12, dtype="bf16")
+            enc, _, _ = harness.make_encoder(ud, orc, cfg, seed=81)
+        finally:
+            os.environ.pop("UD_GRAPHS", None)
+        streams = [enc.new_stream() for _ in range(12)]
+        xb = [ud.DeviceBuffer.from_numpy(x) for x in xs]
+        ob = [ud.DeviceBuffer(x.nbytes) for x in xs]
+        hs = [ud.HipStream(), ud.HipStream()]
+        for i, (n, T) in enumerate(shapes):
+            enc.encode_stream_step(streams[:n], xb[i], ob[i], T=T, hip_stream=hs[i % 2] if graphs == "1" else None)
+            if graphs == "0":
+                ud.synchronize()
+        for h in hs:
+            h.synchronize()
+        outs.append([o.download(x.shape) for o, x in zip(ob, xs)])
+        enc.close()
+    for i, (a, b) in enumerate(zip(*outs)):
+        np.testing.assert_array_equal(a, b, err_msg="step %d %s" % (i, shapes[i]))
 
 
 def test_graph_replay_matches_eager(gpu, orc):

@@ -160,15 +160,14 @@ def test_buffered_valid_frames_and_batching(gpu, orc):
 
 def test_bf16_live_stream(gpu, orc):
     """A bf16 encoder behind the streamer (front-end GEMMs in f16): kept encoder rows to the bf16
-    bar against the oracle with the stored (rounded) weights."""
+    bar against the oracle with the reference's f16 front-end policy (conv.* fp32, out f16)."""
     ud = gpu
     la = 1
     cfg = ud.EncoderConfig(layers=2, max_chunk=la + 1, max_streams=2, dtype="bf16")
     enc, model, _ = harness.make_encoder(ud, orc, cfg, seed=330)
     sw = ud.synthetic_subsampling_weights(331)
     enc.set_subsampling_weights(sw)
-    half = {"encoder.pre_encode.conv.3.weight", "encoder.pre_encode.conv.6.weight", "encoder.pre_encode.out.weight"}
-    osw = {k: (v.astype(np.float16).astype(np.float32) if k in half else v) for k, v in sw.items()}
+    osw = harness.oracle_sub_weights(sw, True)
     rw = ud.synthetic_rnnt_weights(332, blank_bias=0.6)
     dec = ud.Rnnt(max_streams=2)
     dec.set_weights(rw)

@@ -254,6 +254,34 @@ def test_encoder_offline_matches_torch_nemo_layer(ud, orc, valid):
     assert err < 1e-5, err
 
 
+def test_store_limit_matches_clamped_torch_layer(ud, orc):
+    """The oracle's storage-range model (orc_set_store_limit) against the torch restatement of
+    NeMo's layer with torch.clamp at the same points.  The limit (1.5) is below the typical LayerNorm
+    output, FF hidden and q/k/v magnitudes here, so those clamp points engage: a missing or
+    misplaced clamp there moves the result far beyond the tolerance (checked by removing the clamp
+    on v).  The attention output is a convex combination of clamped V rows, so its clamp never
+    engages.  Limit 0 restores the fp32 path."""
+    torch, F = _torch()
+    T, L, R, valid = 16, 6, 1, 16
+    cfg, lw = _small_model(ud, orc, layers=1)
+    D, H = cfg.d_model, cfg.heads
+    lw[0]["feed_forward1.linear1.weight"] = lw[0]["feed_forward1.linear1.weight"] * 4
+    model = orc.Model(lw, D, H, cfg.ff_dim, 9).prepare(-(T - 1), T - 1)
+    x = np.random.default_rng(6).standard_normal((T, D)).astype(np.float32)
+    ranges = orc.chunked_limited_ranges(T, L, R)
+    pe_in = refimpl.nemo_pe(T, D)
+    mask = refimpl.chunked_limited_mask(T, L, R, valid)
+    xt = torch.from_numpy(x).double()
+    ref_clip = refimpl.layer_nemo(xt, lw[0], pe_in, mask, valid, H, clip=1.5).numpy()
+    ref_free = refimpl.layer_nemo(xt, lw[0], pe_in, mask, valid, H).numpy()
+    with orc.store_limit(1.5):
+        got = orc.encoder_offline(model, x, ranges, valid)
+    free = orc.encoder_offline(model, x, ranges, valid)
+    assert np.abs(ref_clip - ref_free).max() > 0.1           # the clamps change the result
+    assert np.abs(got - ref_clip).max() / np.abs(ref_clip).max() < 1e-5
+    assert np.abs(free - ref_free).max() / np.abs(ref_free).max() < 1e-5
+
+
 def test_streaming_equals_offline_chunked(ud, orc):
     """Cache-aware streaming (L cached frames, chunks of T) equals the offline chunked_limited
     forward with [L, T-1] (docs/specs/nemotron.md:197-208), here exactly since there is no

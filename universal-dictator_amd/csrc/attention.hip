@@ -443,8 +443,8 @@ __global__ __launch_bounds__(256) void relpos_ring_small_kernel(RingArgs a) {
         unpack16<T>(qreg[i], f);
 #pragma unroll
         for (int e = 0; e < VEC / 2; e++) {
-            qu2[i][e] = half2_t{(f16)(f[2 * e] + uu[2 * e]), (f16)(f[2 * e + 1] + uu[2 * e + 1])};
-            qv2[i][e] = half2_t{(f16)(f[2 * e] + vv[2 * e]), (f16)(f[2 * e + 1] + vv[2 * e + 1])};
+            qu2[i][e] = half2_t{f2h_sat(f[2 * e] + uu[2 * e]), f2h_sat(f[2 * e + 1] + uu[2 * e + 1])};
+            qv2[i][e] = half2_t{f2h_sat(f[2 * e] + vv[2 * e]), f2h_sat(f[2 * e + 1] + vv[2 * e + 1])};
         }
     }
     const int qi = tsum16_index<TQ>(sub);
@@ -639,8 +639,8 @@ __global__ __launch_bounds__(256) void relpos_ring_wave_kernel(RingArgs a) {
         unpack16<T>(qreg[i], f);
 #pragma unroll
         for (int e = 0; e < VEC / 2; e++) {
-            qu2[i][e] = half2_t{(f16)(f[2 * e] + uu[2 * e]), (f16)(f[2 * e + 1] + uu[2 * e + 1])};
-            qv2[i][e] = half2_t{(f16)(f[2 * e] + vv[2 * e]), (f16)(f[2 * e + 1] + vv[2 * e + 1])};
+            qu2[i][e] = half2_t{f2h_sat(f[2 * e] + uu[2 * e]), f2h_sat(f[2 * e + 1] + uu[2 * e + 1])};
+            qv2[i][e] = half2_t{f2h_sat(f[2 * e] + vv[2 * e]), f2h_sat(f[2 * e + 1] + vv[2 * e + 1])};
         }
     }
     // ---- bd parts (band rows: L2-resident, in before K), then scores; every lane of a group gets
@@ -871,6 +871,15 @@ __device__ __forceinline__ uint4 pack_f16x8(const float (&x)[8]) {
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) w[e] = (uint32_t)f2h(x[2 * e]) | ((uint32_t)f2h(x[2 * e + 1]) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+// The same for softmax probabilities (in [0, 1], so no saturation is needed).
+__device__ __forceinline__ uint4 pack_f16x8_unit(const float (&x)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        w[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2 * e]) |
+               ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x[2 * e + 1]) << 16);
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
@@ -1106,7 +1115,7 @@ __global__ __launch_bounds__(64 * rm::NW, 1) void relpos_ring_mfma_kernel(RingAr
             pf[e] = 2 * kk < KT ? pr[2 * kk][e] * inv : 0.0f;
             pf[4 + e] = 2 * kk + 1 < KT ? pr[2 * kk + 1][e] * inv : 0.0f;
         }
-        const uint4 pa = pack_f16x8(pf);
+        const uint4 pa = pack_f16x8_unit(pf);
         wave_lds_fence();
         const int k0 = 8 * g + (col >> 2);
 #pragma unroll

@@ -378,6 +378,9 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
             qx[kc][1] = *reinterpret_cast<const float4*>(qr + 32 * kc + 4);
         }
     }
+    // The wait below counts vector-memory operations: the 8 q loads, then the 8 direct K loads, then
+    // the 8 V loads must be issued in that order, which the scheduling barriers pin.
+    __builtin_amdgcn_sched_barrier(0);
     const int blo = klo / PAGE, bhi = (khi - 1) / PAGE;
     const int32_t* bt = a.bt + (int64_t)seq * a.max_blocks;
     const char* kp = static_cast<const char*>(a.kp);
@@ -402,12 +405,14 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
             kv_direct16(reinterpret_cast<const bf16*>(kp + off[e][i]), reinterpret_cast<bf16*>(kv + (r0 + 4 * i) * ROWB));
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
     uint4 vr[2][4];
 #pragma unroll
     for (int e = 0; e < 2; e++)
 #pragma unroll
         for (int i = 0; i < 4; i++) vr[e][i] = ld16(vp + off[e][i]);
-    __builtin_amdgcn_s_waitcnt(0x0F78);           // vmcnt(8): q and the K rows landed (the V loads may not)
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));     // q and the K rows landed (the 8 V loads may not)
     // q as the A operand: lane (r, g) holds q[head r][32kc + 8g .. + 7] in bf16 (zero for r >= G)
     uint4 qa[4];
 #pragma unroll

@@ -85,9 +85,11 @@ static inline float host_bf16_to_f(uint16_t b) {
     return f;
 }
 
-// IEEE half (round to nearest even): a 16-bit encoder's storage format for weights, activations,
-// K/V caches and position tables.
+static constexpr float kHalfMax = 65504.0f;
+// IEEE half (round to nearest even), saturating at +-65504 (NaN stays NaN), as the device stores
+// saturate: a 16-bit encoder's storage format for activations, K/V caches and position tables.
 static inline uint16_t host_f16(float f) {
+    if (!std::isnan(f)) f = f < -kHalfMax ? -kHalfMax : (f > kHalfMax ? kHalfMax : f);
     const _Float16 h = (_Float16)f;
     uint16_t b;
     memcpy(&b, &h, 2);
@@ -98,11 +100,19 @@ static inline float host_f16_to_f(uint16_t b) {
     memcpy(&h, &b, 2);
     return (float)h;
 }
-// A weight of a 16-bit encoder: its bf16 value (the reference's bf16-weight setting), held as IEEE
-// half for the f16 MFMA.  Exact for every bf16 value of magnitude 2^-17 .. 65504 (half's 11-bit
-// significand holds bf16's 8 bits); smaller magnitudes keep half's subnormal resolution, 2^-24.
-static inline uint16_t host_weight16(float f) { return host_f16(host_bf16_to_f(host_bf16(f))); }
-static constexpr float kHalfMax = 65504.0f;
+// A linear weight of a 16-bit encoder, held as IEEE half for the f16 MFMA:
+//  - UD_BF16: its bf16 value (round to nearest even, Tensor.swift:116-122), exact in half for every
+//    bf16 value of magnitude 2^-17 .. 65504 (half's 11-bit significand holds bf16's 8 bits);
+//    smaller magnitudes keep half's subnormal resolution, 2^-24;
+//  - UD_F16: fp32 rounded straight to half, as WeightConverter.convert(.f16) writes the reference's
+//    f16 checkpoint (Sources/DictatorEngine/Core/Convert.swift:99-104, Float16(x)).
+// Callers check the range first (a weight beyond 65504 is refused, not saturated).
+static inline uint16_t host_weight16(float f, bool f16_weights) {
+    return f16_weights ? host_f16(f) : host_f16(host_bf16_to_f(host_bf16(f)));
+}
+static inline float host_weight16_value(float f, bool f16_weights) {
+    return f16_weights ? host_f16_to_f(host_f16(f)) : host_bf16_to_f(host_bf16(f));
+}
 
 // ---------------------------------------------------------------- weights
 
@@ -164,12 +174,19 @@ struct SubDev {
     uint32_t set_mask = 0;
     void* a2 = nullptr; float* a3 = nullptr; void* a4 = nullptr; float* a5 = nullptr; void* af = nullptr;
     int32_t* vlen = nullptr;
+    // the per-stage valid lengths of a call, staged in one of four pinned buffers [max_streams][4]
+    // (an event per buffer: a buffer is rewritten only after the copy that read it has run)
+    int32_t* vlen_host[4] = {};
+    hipEvent_t vlen_ev[4] = {};
+    bool vlen_used[4] = {};
+    int vlen_next = 0;
     bool ws = false;
 };
 
 struct ud_encoder {
     ud_encoder_config cfg;
-    bool bf;                        // 16-bit encoder (UD_BF16): half storage, f16 MFMA
+    bool bf;                        // 16-bit encoder (UD_BF16 or UD_F16): half storage, f16 MFMA
+    bool wf16;                      // UD_F16: linear weights rounded fp32 -> half directly
     size_t esz;
     int D, H, dk, ff, Kc, L, layers, n_rel, rel_offset, max_rows;
     int R;                         // K/V ring rows per (slot, head): L + max_chunk
@@ -194,6 +211,16 @@ struct ud_encoder {
     bool desc_used[4] = {};
     int desc_next = 0;
     bool finalized = false;
+    // Work order across HIP streams: every call that enqueues device work records done_ev on its
+    // stream when it is done enqueueing; a call on a different stream first makes its stream wait
+    // for done_ev.  The calls on one encoder therefore run in call order whatever streams they are
+    // issued on (they share the workspace), and done_ev always marks the end of all device work
+    // enqueued so far.
+    hipEvent_t done_ev = nullptr;
+    hipStream_t last_st = nullptr;
+    bool has_last = false;
+    hipEvent_t aux_ev = nullptr;   // recorded by ud_encoder_aux_release after the aux scratch's last use
+    bool aux_used = false;
     bool use_graphs = true;
     hipStream_t capture_stream = nullptr;
     std::vector<GraphEntry> graphs;
@@ -238,7 +265,11 @@ static void free_encoder(ud_encoder* e) {
     for (int i = 0; i < 4; i++) {
         if (e->desc_host[i]) (void)hipHostFree(e->desc_host[i]);
         if (e->desc_ev[i]) (void)hipEventDestroy(e->desc_ev[i]);
+        if (e->sub.vlen_host[i]) (void)hipHostFree(e->sub.vlen_host[i]);
+        if (e->sub.vlen_ev[i]) (void)hipEventDestroy(e->sub.vlen_ev[i]);
     }
+    if (e->done_ev) (void)hipEventDestroy(e->done_ev);
+    if (e->aux_ev) (void)hipEventDestroy(e->aux_ev);
     if (e->capture_stream) (void)hipStreamDestroy(e->capture_stream);
     for (ud_stream* s : e->live) delete s;
     delete e;
@@ -263,14 +294,16 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
     if (c.left_context < 1 || c.max_chunk < 1 || c.max_chunk > 16 || c.max_chunk > c.left_context)
         return fail(UD_ERR_SHAPE, "ud_encoder_create: need 1 <= max_chunk <= min(16, left_context)");
     if (c.max_streams < 1) return fail(UD_ERR_SHAPE, "ud_encoder_create: max_streams must be >= 1");
-    if (c.dtype != UD_F32 && c.dtype != UD_BF16) return fail(UD_ERR_INVALID, "ud_encoder_create: bad dtype");
+    if (c.dtype != UD_F32 && c.dtype != UD_BF16 && c.dtype != UD_F16)
+        return fail(UD_ERR_INVALID, "ud_encoder_create: bad dtype %d", c.dtype);
     int ndev = 0;
     if (hipGetDeviceCount(&ndev) != hipSuccess || ndev < 1)
         return fail(UD_ERR_HIP, "ud_encoder_create: no HIP device");
 
     ud_encoder* e = new ud_encoder();
     e->cfg = c;
-    e->bf = c.dtype == UD_BF16;
+    e->bf = c.dtype == UD_BF16 || c.dtype == UD_F16;
+    e->wf16 = c.dtype == UD_F16;
     e->esz = e->bf ? 2 : 4;
     e->D = c.d_model; e->H = c.heads; e->dk = c.d_model / c.heads; e->ff = c.ff_dim; e->Kc = c.conv_kernel;
     e->L = c.left_context; e->layers = c.layers;
@@ -326,7 +359,11 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
     for (int i = 0; ok && i < 4; i++) {
         ok &= hipHostMalloc((void**)&e->desc_host[i], desc_ints(e) * 4, hipHostMallocDefault) == hipSuccess;
         ok &= hipEventCreateWithFlags(&e->desc_ev[i], hipEventDisableTiming) == hipSuccess;
+        ok &= hipHostMalloc((void**)&e->sub.vlen_host[i], slots * 4 * sizeof(int32_t), hipHostMallocDefault) == hipSuccess;
+        ok &= hipEventCreateWithFlags(&e->sub.vlen_ev[i], hipEventDisableTiming) == hipSuccess;
     }
+    ok = ok && hipEventCreateWithFlags(&e->done_ev, hipEventDisableTiming) == hipSuccess;
+    ok = ok && hipEventCreateWithFlags(&e->aux_ev, hipEventDisableTiming) == hipSuccess;
     if (!ok) {
         free_encoder(e);
         return fail(UD_ERR_NOMEM, "ud_encoder_create: device allocation failed");
@@ -366,11 +403,12 @@ static int upload_matrix(ud_encoder* e, void* dst, size_t dst_row0, const float*
         std::vector<uint16_t> tmp(n);
         const int nk = (int)(cols / 64);
         for (size_t i = 0; i < n; i++)
-            if (!(std::fabs(host_bf16_to_f(host_bf16(src[i]))) <= kHalfMax))
+            if (!(std::fabs(host_weight16_value(src[i], e->wf16)) <= kHalfMax))
                 return fail(UD_ERR_WEIGHT, "weight value %g at element %zu is outside the IEEE-half range of a 16-bit encoder",
                             (double)src[i], i);
         for (size_t r = 0; r < rows; r++)
-            for (size_t c = 0; c < cols; c++) tmp[frag_index((int64_t)r, (int)c, nk)] = host_weight16(src[r * cols + c]);
+            for (size_t c = 0; c < cols; c++)
+                tmp[frag_index((int64_t)r, (int)c, nk)] = host_weight16(src[r * cols + c], e->wf16);
         return upload(static_cast<uint16_t*>(dst) + dst_row0 * cols, tmp.data(), n * 2);
     }
     return upload(static_cast<float*>(dst) + dst_row0 * cols, src, n * 4);
@@ -390,18 +428,21 @@ static bool parse_name(const char* name, int layers, int* layer, int* slot) {
     return false;
 }
 
-// As upload_matrix, for the front-end GEMMs: a bf16 encoder stores these as IEEE half.
+// As upload_matrix, for the front-end GEMMs (conv.3, conv.6, out): a 16-bit encoder stores these
+// as IEEE half, fp32 rounded straight to half in both 16-bit modes.  (The reference's f16 checkpoint
+// keeps conv.3 and conv.6 in fp32 -- WeightConverter.keepF32, Convert.swift:80 -- and rounds out
+// to f16; here the front-end's 1x1 convs run on the f16 MFMA as well.)
 static int upload_matrix_sub(ud_encoder* e, void* dst, const float* src, size_t rows, size_t cols) {
     if (!e->bf) return upload(dst, src, rows * cols * 4);
-    std::vector<uint16_t> tmp(rows * cols);
+    const size_t n = rows * cols;
+    for (size_t i = 0; i < n; i++)
+        if (!(std::fabs(src[i]) <= kHalfMax))
+            return fail(UD_ERR_WEIGHT, "subsampling weight value %g at element %zu is outside the IEEE-half range of a "
+                        "16-bit encoder", (double)src[i], i);
+    std::vector<uint16_t> tmp(n);
     const int nk = (int)(cols / 64);
     for (size_t r = 0; r < rows; r++)
-        for (size_t c = 0; c < cols; c++) {
-            const _Float16 h = (_Float16)src[r * cols + c];
-            uint16_t b;
-            memcpy(&b, &h, 2);
-            tmp[frag_index((int64_t)r, (int)c, nk)] = b;
-        }
+        for (size_t c = 0; c < cols; c++) tmp[frag_index((int64_t)r, (int)c, nk)] = host_f16(src[r * cols + c]);
     return upload(dst, tmp.data(), tmp.size() * 2);
 }
 
@@ -476,7 +517,7 @@ extern "C" UD_API int ud_encoder_set_weight(ud_encoder* e, const char* name, con
         case PW1: rc = upload_matrix(e, l.pw1, 0, host, 2 * D, D); break;
         case LIN_POS: {
             l.wpos.assign(host, host + D * D);
-            if (e->bf) for (auto& v : l.wpos) v = host_bf16_to_f(host_bf16(v));
+            if (e->bf) for (auto& v : l.wpos) v = host_weight16_value(v, e->wf16);
             e->finalized = false;
             break;
         }
@@ -564,16 +605,24 @@ extern "C" UD_API int ud_encoder_finalize(ud_encoder* e) {
 }
 
 // Device scratch of at least `bytes` owned by the encoder (grown on demand, freed with it), for
-// host-side entry points that chain the encoder's calls (ud_nemotron_step).  Growing waits for the
-// device, so no earlier call still uses the old buffer.
+// host-side entry points that chain the encoder's calls (ud_nemotron_step).  Growing first waits
+// for the event the last user recorded with ud_encoder_aux_release, so no earlier call still uses
+// the old buffer (other HIP streams and the rest of the device are not waited for).
 void* ud_encoder_aux_scratch(ud_encoder* e, size_t bytes) {
     if (e->aux_bytes >= bytes) return e->aux;
-    if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+    if (e->aux_used && hipEventSynchronize(e->aux_ev) != hipSuccess) return nullptr;
     if (e->aux) (void)hipFree(e->aux);
     e->aux_bytes = 0;
     e->aux = dev_alloc(bytes);
     if (e->aux) e->aux_bytes = bytes;
     return e->aux;
+}
+
+// Marks the end of a use of the aux scratch on `st` (after the last work that reads or writes it).
+int ud_encoder_aux_release(ud_encoder* e, hipStream_t st) {
+    HIPC(hipEventRecord(e->aux_ev, st));
+    e->aux_used = true;
+    return UD_OK;
 }
 
 // ---------------------------------------------------------------- streams
@@ -646,6 +695,20 @@ static int check_batch(ud_encoder* e, ud_stream* const* streams, int n, int T, c
         if (seen[s->slot]) return fail(UD_ERR_INVALID, "%s: stream %d appears twice in the batch", who, i);
         seen[s->slot] = 1;
     }
+    return UD_OK;
+}
+
+// The start of a call that enqueues device work on `st`: after every earlier call's work (see
+// ud_encoder::done_ev).
+static int order_after_last(ud_encoder* e, hipStream_t st) {
+    if (e->has_last && st != e->last_st) HIPC(hipStreamWaitEvent(st, e->done_ev, 0));
+    return UD_OK;
+}
+// The end of such a call: done_ev marks the end of its work.
+static int mark_done(ud_encoder* e, hipStream_t st) {
+    HIPC(hipEventRecord(e->done_ev, st));
+    e->last_st = st;
+    e->has_last = true;
     return UD_OK;
 }
 
@@ -803,7 +866,9 @@ static int run_step(ud_encoder* e, int n, int T, const float* x, float* out, hip
         if (g.n == n && g.T == T && g.x == x && g.out == out) { ge = &g; break; }
     if (!ge) {
         if (e->graphs.size() >= 8) {
-            HIPC(hipStreamSynchronize(st));
+            // The oldest graph may have been launched last on another HIP stream: wait for all of
+            // this encoder's work (done_ev follows every earlier call's) before destroying it.
+            if (e->has_last) HIPC(hipEventSynchronize(e->done_ev));
             (void)hipGraphExecDestroy(e->graphs.front().exec);
             (void)hipGraphDestroy(e->graphs.front().graph);
             e->graphs.erase(e->graphs.begin());
@@ -833,8 +898,10 @@ extern "C" UD_API int ud_encoder_step(ud_encoder* e, ud_stream* const* streams, 
     if (!x_dev || !out_dev) return fail(UD_ERR_INVALID, "ud_encoder_step: null input/output");
     if (x_dev == out_dev) return fail(UD_ERR_INVALID, "ud_encoder_step: out_dev aliases x_dev");
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    if ((rc = order_after_last(e, st)) != UD_OK) return rc;
     if ((rc = upload_desc(e, streams, n, T, valid_T_host, st)) != UD_OK) return rc;
     if ((rc = run_step(e, n, T, x_dev, out_dev, st)) != UD_OK) return rc;
+    if ((rc = mark_done(e, st)) != UD_OK) return rc;
     for (int i = 0; i < n; i++) { streams[i]->frames += T; streams[i]->steps++; }
     return UD_OK;
 }
@@ -885,8 +952,15 @@ extern "C" UD_API int ud_encoder_subsample(ud_encoder* e, int32_t n, int32_t mel
                     drop, T, e->cfg.max_chunk);
     int rc = sub_workspace(e);
     if (rc != UD_OK) return rc;
-    // Valid rows per stage (FastConformer.swift:446-450): mel rows, then L -> L/2 + 1 per stage.
-    std::vector<int32_t> vl((size_t)n * 4);
+    hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    if ((rc = order_after_last(e, st)) != UD_OK) return rc;
+    SubDev& u = e->sub;
+    // Valid rows per stage (FastConformer.swift:446-450): mel rows, then L -> L/2 + 1 per stage,
+    // staged in the next pinned buffer once the copy that last read it has run.
+    const int vk = u.vlen_next;
+    u.vlen_next = (vk + 1) % 4;
+    if (u.vlen_used[vk]) HIPC(hipEventSynchronize(u.vlen_ev[vk]));
+    int32_t* vl = u.vlen_host[vk];
     for (int i = 0; i < n; i++) {
         int v = valid_mel_host ? valid_mel_host[i] : T0;
         v = v < 0 ? 0 : (v > T0 ? T0 : v);
@@ -898,9 +972,9 @@ extern "C" UD_API int ud_encoder_subsample(ud_encoder* e, int32_t n, int32_t mel
         }
     }
     if (T_out) *T_out = T;
-    hipStream_t st = static_cast<hipStream_t>(hip_stream);
-    SubDev& u = e->sub;
-    HIPC(hipMemcpyAsync(u.vlen, vl.data(), vl.size() * sizeof(int32_t), hipMemcpyHostToDevice, st));
+    HIPC(hipMemcpyAsync(u.vlen, vl, (size_t)n * 4 * sizeof(int32_t), hipMemcpyHostToDevice, st));
+    HIPC(hipEventRecord(u.vlen_ev[vk], st));
+    u.vlen_used[vk] = true;
     const bool bf = e->bf;
     SubArgs c01{};
     c01.mel = mel_dev; c01.vlen = u.vlen;
@@ -926,7 +1000,9 @@ extern "C" UD_API int ud_encoder_subsample(ud_encoder* e, int32_t n, int32_t mel
     SubFlatArgs fl{};
     fl.x = u.a5; fl.vlen = u.vlen; fl.out = u.af; fl.n = n; fl.T3 = T3; fl.F3 = SUB_F3; fl.T = T; fl.drop = drop;
     LAUNCH(launch_sub_flatten(fl, bf, st), "subsampling flatten");
-    return gemm(u.af, SUB_OUTW, SUB_OUTB, out_dev, n * T, e->D, SUB_CH * SUB_F3, ACT_NONE, "subsampling out");
+    if ((rc = gemm(u.af, SUB_OUTW, SUB_OUTB, out_dev, n * T, e->D, SUB_CH * SUB_F3, ACT_NONE, "subsampling out")))
+        return rc;
+    return mark_done(e, st);
 }
 
 static RingArgs ring_args(ud_encoder* e, int n, int T, int layer, const void* qkv, void* att) {
@@ -958,11 +1034,13 @@ extern "C" UD_API int ud_layer_attention(ud_encoder* e, ud_stream* const* stream
     int rc = check_layer_call(e, streams, n, T, layer, qkv_dev, att_dev, "ud_layer_attention");
     if (rc != UD_OK) return rc;
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    if ((rc = order_after_last(e, st)) != UD_OK) return rc;
     if ((rc = upload_desc(e, streams, n, T, valid_T_host, st)) != UD_OK) return rc;
     // the chunk's K/V rows from qkv into the rings, then the attention over the ring windows
     const RingArgs ra = ring_args(e, n, T, layer, qkv_dev, att_dev);
     if ((rc = launch_status(launch_ring_append(ra, e->bf, st), "ring append")) != UD_OK) return rc;
-    return launch_status(launch_relpos_ring(ra, e->bf, st), "relpos attention");
+    if ((rc = launch_status(launch_relpos_ring(ra, e->bf, st), "relpos attention")) != UD_OK) return rc;
+    return mark_done(e, st);
 }
 
 // Launches `iters` kernels back to back between two HIP events, launch i on layer
@@ -975,6 +1053,7 @@ static int time_layers(ud_encoder* e, ud_stream* const* streams, int32_t n, int3
     if (rc != UD_OK) return rc;
     if (iters < 1 || !avg_ms) return fail(UD_ERR_INVALID, "%s: bad iters / output", what);
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    if ((rc = order_after_last(e, st)) != UD_OK) return rc;
     if ((rc = upload_desc(e, streams, n, T, nullptr, st)) != UD_OK) return rc;
     hipEvent_t ev[2];
     HIPC(hipEventCreate(&ev[0]));
@@ -992,6 +1071,7 @@ static int time_layers(ud_encoder* e, ud_stream* const* streams, int32_t n, int3
     (void)hipEventDestroy(ev[0]);
     (void)hipEventDestroy(ev[1]);
     if (rc == UD_OK) *avg_ms = ms / (float)iters;
+    if (rc == UD_OK) rc = mark_done(e, st);
     return rc;
 }
 
@@ -1058,6 +1138,8 @@ extern "C" UD_API int ud_time_projection(ud_encoder* e, int32_t which, int32_t r
     if (!e->finalized) return fail(UD_ERR_STATE, "ud_time_projection: encoder not finalized");
     if (rows < 1 || rows > e->max_rows) return fail(UD_ERR_SHAPE, "ud_time_projection: rows %d outside 1..%d", rows, e->max_rows);
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    int rc0 = order_after_last(e, st);
+    if (rc0 != UD_OK) return rc0;
     hipEvent_t ev[2];
     HIPC(hipEventCreate(&ev[0]));
     HIPC(hipEventCreate(&ev[1]));
@@ -1072,6 +1154,7 @@ extern "C" UD_API int ud_time_projection(ud_encoder* e, int32_t which, int32_t r
     (void)hipEventDestroy(ev[0]);
     (void)hipEventDestroy(ev[1]);
     if (rc == UD_OK) *avg_ms = ms / (float)iters;
+    if (rc == UD_OK) rc = mark_done(e, st);
     return rc;
 }
 

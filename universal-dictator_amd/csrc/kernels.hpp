@@ -8,8 +8,10 @@
 struct ud_mel;
 struct ud_encoder;
 // Device scratch of at least `bytes` owned by the encoder (grown on demand, freed with it; growing
-// synchronizes the device); nullptr when the allocation fails.
+// waits for the event of the last ud_encoder_aux_release); nullptr when the allocation fails.
 void* ud_encoder_aux_scratch(ud_encoder* e, size_t bytes);
+// Records, on `st`, the end of a use of that scratch (after the last work that touches it).
+int ud_encoder_aux_release(ud_encoder* e, hipStream_t st);
 
 namespace ud {
 

@@ -538,11 +538,17 @@ extern "C" UD_API int ud_nemotron_step(ud_encoder* enc, ud_rnnt* rnnt, ud_stream
         if ((rc = ud_stream_info(streams[i], &cl, &steps)) != UD_OK) return rc;
         grp[steps == 0 ? 0 : 1].push_back(i);
     }
+    // Every shape check of both groups' calls comes before anything is launched, so a shape error
+    // leaves every stream where it was (see ud_streamer.h for the failures that can still come
+    // after the first group has advanced).
+    if (mel_rows > 8 * cfg.max_chunk + 9)
+        return tfail(UD_ERR_SHAPE, "ud_nemotron_step: %d mel rows exceed the encoder's %d", mel_rows,
+                     8 * cfg.max_chunk + 9);
     for (int g = 0; g < 2; g++) {
         const int T = sub3(mel_rows) - (g == 0 ? 0 : drop_extra);
-        if (!grp[g].empty() && (T < 1 || T > proj_rows))
-            return tfail(UD_ERR_SHAPE, "ud_nemotron_step: %d mel rows give %d frames (%s steps); proj_rows is %d",
-                         mel_rows, T, g == 0 ? "first" : "later", proj_rows);
+        if (!grp[g].empty() && (T < 1 || T > proj_rows || T > cfg.max_chunk))
+            return tfail(UD_ERR_SHAPE, "ud_nemotron_step: %d mel rows give %d frames (%s steps); proj_rows is %d, "
+                         "max_chunk %d", mel_rows, T, g == 0 ? "first" : "later", proj_rows, cfg.max_chunk);
     }
     // scratch: the group's mel rows, subsampled frames, encoder output, projection
     constexpr int NM = 128;
@@ -586,5 +592,5 @@ extern "C" UD_API int ud_nemotron_step(ud_encoder* enc, ud_rnnt* rnnt, ud_stream
                        "ud_nemotron_step: projection copy");
         }
     }
-    return UD_OK;
+    return ud_encoder_aux_release(enc, st);
 }

@@ -42,7 +42,17 @@ __device__ __forceinline__ f16x8_t as_f16x8(uint4 v) {
     __builtin_memcpy(&r, &v, 16);
     return r;
 }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// fp32 -> IEEE half, round to nearest even, saturating: values beyond half's largest finite
+// magnitude (65504, infinities included) are stored as +-65504, NaN stays NaN.  Every 16-bit
+// activation, K/V cache row and table entry a 16-bit encoder writes goes through this, so a value
+// that outgrows half's range is clipped instead of turning into inf (and NaN after the next
+// LayerNorm).
+constexpr float kHalfMaxF = 65504.0f;
+__device__ __forceinline__ float sat_half_range(float f) {
+    return __builtin_isnan(f) ? f : fminf(fmaxf(f, -kHalfMaxF), kHalfMaxF);
+}
+__device__ __forceinline__ _Float16 f2h_sat(float f) { return (_Float16)sat_half_range(f); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, f2h_sat(f)); }
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 // A 16-bit operand value: IEEE half when H, bf16 otherwise (round to nearest even either way).
 template <bool H> __device__ __forceinline__ uint16_t to16(float f) {
@@ -67,7 +77,7 @@ template <> __device__ __forceinline__ float to_f<f16>(f16 v) { return (float)v;
 template <typename T> __device__ __forceinline__ T from_f(float v);
 template <> __device__ __forceinline__ float from_f<float>(float v) { return v; }
 template <> __device__ __forceinline__ bf16 from_f<bf16>(float v) { return f2bf(v); }
-template <> __device__ __forceinline__ f16 from_f<f16>(float v) { return (f16)v; }
+template <> __device__ __forceinline__ f16 from_f<f16>(float v) { return f2h_sat(v); }
 
 // SiLU x * sigmoid(x) (00_common.metal:25).
 // SiLU and the logistic function with v_exp_f32 and v_rcp_f32 (about 1 ulp each) instead of an
