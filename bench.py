@@ -1,24 +1,27 @@
 """Benchmark of the cache-aware streaming FastConformer encoder step on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|offline|rnnt|stream|stream14]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|decode_mq|offline|rnnt|stream|stream14]
                     [--no-cpu-baseline]
 
 A step is one cache-aware encoder chunk step for every stream of the batch: the mel chunk (new rows
 plus the 9-row pre-encode cache) through the causal dw_striding 8x subsampling with 2 frames dropped,
-then 24 conformer layers (bf16 weights/activations, fp32 accumulation), with inputs already in HBM
-and full 70-frame caches seeded from N(0,1).  Default workload: 64 streams x 2 frames (25 mel rows
-in, 160 ms of audio per stream per step).  Prints one JSON
-line: aggregate streamed audio-seconds per second, per-step latency percentiles, the fused
-attention kernel's achieved HBM bandwidth against 8 TB/s and against the HBM read peak measured in
-the same run (HIP events on the kernel's own stream), the same attention at 256 streams x 14
-frames (roofline_long_chunk), each projection GEMM's MFMA throughput against the nominal and the
-measured peak, and the CPU oracle's throughput on a bounded sample timed on this host's cores.
+then 24 conformer layers (bf16-valued weights held as IEEE half; half activations, K/V caches and
+MFMA operands; fp32 accumulation), with inputs already in HBM and full 70-frame caches seeded from
+N(0,1).  Default workload: 64 streams x 2 frames (25 mel rows in, 160 ms of audio per stream per
+step).  Prints one JSON line: aggregate streamed audio-seconds per second, per-step latency
+percentiles, the fused attention kernel's achieved HBM bandwidth against 8 TB/s and against the HBM
+read peak measured in the same run (HIP events on the kernel's own stream), each projection GEMM's
+MFMA throughput against the nominal and the measured peak, and the CPU oracle's throughput on a
+bounded sample timed on this host's cores; then the other configurations' figures: the long-chunk
+workload (256 streams x 14 frames) -- its attention kernel (roofline_long_chunk), its whole step
+and its projections' MFMA use (chunk14_step) -- the offline attention kernel's MFMA fraction
+(offline_attention) and the paged decode attention's HBM fraction (decode_attention).
 --library-gemm adds the vendor GEMM (torch.matmul, hipBLASLt) timed on each projection's shape.
 
 --workload chunk14 runs the same step at 256 streams x 14 frames.  --workload decode measures the
 decoder's paged grouped-query attention instead: 64 sequences x 1 new token, 32 query / 8 kv heads
 x 128, contexts uniform in 512..4096 keys in bf16 pages of 16 (one line in the same format, value in
-tokens/s).  --workload offline measures the whole-utterance rel-pos attention: 8 utterances x 1500
+tokens/s); --workload decode_mq the same with 4 new positions per sequence in one multi-query call.  --workload offline measures the whole-utterance rel-pos attention: 8 utterances x 1500
 frames, 8 heads x 128, valid lengths uniform in 900..1500 as key padding (value in frames/s, roofline
 against the bf16 MFMA peak).  --workload rnnt measures the joint.enc projection and greedy RNN-T
 decoding of 64 streams x 2 frames per chunk.  --workload stream measures live transcription end to
@@ -42,6 +45,8 @@ WORKLOADS = {
     "chunk2": dict(streams=64, T=2),     # 64 concurrent streams, 160 ms chunks
     "chunk14": dict(streams=256, T=14),  # 256 concurrent streams, 1120 ms chunks
     "decode": dict(seqs=64, q_heads=32, kv_heads=8, head_dim=128, page=16, ctx=(512, 4096)),
+    # the same cache with 4 new positions per sequence (one multi-query call)
+    "decode_mq": dict(seqs=64, q_heads=32, kv_heads=8, head_dim=128, page=16, ctx=(512, 4096), queries=4),
     "offline": dict(batch=8, frames=1500, heads=8, head_dim=128, valid=(900, 1500)),
     "rnnt": dict(streams=64, T=2, hidden=640, vocab=1025, layers=2),
     "stream": dict(streams=64, lookahead=1),     # live audio -> tokens, 160 ms chunks
@@ -185,10 +190,15 @@ def mel_rows(T):
     return 8 * (T + 2) - 7
 
 
-def decode_bench(ud, args):
-    """Paged GQA decode attention: one new token for each of 64 sequences."""
-    wl = WORKLOADS["decode"]
+def decode_bench(ud, args, summary=False, steps=None, warmup=None, workload="decode"):
+    """Paged GQA decode attention: one new token for each of 64 sequences (workload decode), or 4
+    new positions per sequence in one multi-query call (decode_mq).  summary: return the kernel's
+    figures as a dict (no CPU baseline, nothing printed) for the default line."""
+    steps = steps or args.steps
+    warmup = args.warmup if warmup is None else warmup
+    wl = WORKLOADS[workload]
     n, Hq, Hkv, d, page = wl["seqs"], wl["q_heads"], wl["kv_heads"], wl["head_dim"], wl["page"]
+    M = wl.get("queries", 1)
     rng = np.random.default_rng(17)
     lens = rng.integers(wl["ctx"][0], wl["ctx"][1] + 1, n)
     nb = (lens + page - 1) // page
@@ -200,52 +210,69 @@ def decode_bench(ud, args):
     for i in range(n):
         table[i, :nb[i]] = perm[o:o + nb[i]]
         o += nb[i]
-    log("device %s; workload decode: %d sequences, %d/%d heads x %d, context %d..%d (total %d keys), bf16 pages of %d"
-        % (ud.device_arch(), n, Hq, Hkv, d, lens.min(), lens.max(), lens.sum(), page))
+    log("device %s; workload %s: %d sequences x %d queries, %d/%d heads x %d, context %d..%d (total %d keys), "
+        "bf16 pages of %d" % (ud.device_arch(), workload, n, M, Hq, Hkv, d, lens.min(), lens.max(), lens.sum(), page))
 
     def pages():
         x = rng.standard_normal((nblk, Hkv, page, d), dtype=np.float32)
         return (ud.round_bf16(x).view(np.uint32) >> 16).astype(np.uint16)
     kp_h, vp_h = pages(), pages()
     kp, vp = ud.DeviceBuffer.from_numpy(kp_h), ud.DeviceBuffer.from_numpy(vp_h)
-    q_h = rng.standard_normal((n, Hq * d), dtype=np.float32)
+    q_h = rng.standard_normal((n, M, Hq * d), dtype=np.float32)
     q = ud.DeviceBuffer.from_numpy(q_h)
-    ranges_h = np.stack([np.zeros(n, np.int32), lens.astype(np.int32)], 1)
+    # query m of a sequence of L keys: keys [0, L - (M - 1) + m) (causal over the M new positions)
+    ranges_h = np.zeros((n, M, 2), np.int32)
+    for m in range(M):
+        ranges_h[:, m, 1] = lens - (M - 1) + m
     ranges = ud.DeviceBuffer.from_numpy(ranges_h)
     tbl = ud.DeviceBuffer.from_numpy(table)
     max_keys = int(lens.max())
-    ws = ud.DeviceBuffer.zeros(ud.gqa_workspace_bytes(n, Hq, d, max_keys))
-    out = ud.DeviceBuffer(n * Hq * d * 4)
+    ws = ud.DeviceBuffer.zeros(ud.gqa_workspace_bytes(n * M, Hq, d, max_keys))
+    out = ud.DeviceBuffer(n * M * Hq * d * 4)
     hs = ud.HipStream()
-    call = lambda: ud.gqa_attention_paged(q, kp, vp, tbl, max_blocks, ranges, out, n, Hq, Hkv, d, max_keys, ws,
-                                          hip_stream=hs)
-    for _ in range(args.warmup):
+    if M == 1:
+        call = lambda: ud.gqa_attention_paged(q, kp, vp, tbl, max_blocks, ranges, out, n, Hq, Hkv, d, max_keys, ws,
+                                              hip_stream=hs)
+    else:
+        call = lambda: ud.gqa_attention_paged_mq(q, kp, vp, tbl, max_blocks, ranges, out, n, M, Hq, Hkv, d, max_keys,
+                                                 ws, hip_stream=hs)
+    for _ in range(warmup):
         call()
     hs.synchronize()
     e0, e1 = ud.Event(), ud.Event()
     e0.record(hs)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         call()
     e1.record(hs)
     e1.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1000.0
-    ms = max(wall_ms, e0.elapsed_ms(e1)) / args.steps
+    ms = max(wall_ms, e0.elapsed_ms(e1)) / steps
     kv_bytes = int(lens.sum()) * Hkv * d * 2 * 2
-    algo = kv_bytes + n * Hq * d * 4 * 2 + int(nb.sum()) * 4
+    algo = kv_bytes + n * M * Hq * d * 4 * 2 + int(nb.sum()) * 4 + n * M * 8
     achieved = algo / (ms / 1000.0) / 1e9
-    log("timed %d calls: %.2f us per decode attention step (split + combine), %.0f GB/s" % (args.steps, ms * 1000, achieved))
+    log("timed %d calls: %.2f us per decode attention step (split + combine), %.0f GB/s" % (steps, ms * 1000, achieved))
+    if summary:
+        return {"kernel": "gqa_split_mfma_kernel + gqa_combine_kernel (timed together)",
+                "workload": "%d sequences x %d token%s, %d query / %d kv heads x %d, context %d..%d, bf16 pages of %d"
+                            % (n, M, "s" if M > 1 else "", Hq, Hkv, d, wl["ctx"][0], wl["ctx"][1], page),
+                "us_per_call": round(ms * 1000.0, 3), "tokens_per_sec": round(n * M / (ms / 1000.0), 1),
+                "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_call": algo,
+                "calls_timed": steps}
     result = {
         "metric": "paged GQA decode attention: tokens/s and HBM roofline fraction",
-        "value": round(n / (ms / 1000.0), 1),
+        "value": round(n * M / (ms / 1000.0), 1),
         "unit": "tokens/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 K/V pages, fp32 queries, softmax and accumulation (bf16 MFMA operands)",
         "data": "synthetic (seeded N(0,1) queries and bf16 K/V pages, random page table)",
-        "config": {"workload": "decode-step grouped-query attention over a paged K/V cache, %d sequences x 1 token, "
-                               "%d query / %d kv heads x %d, context %d..%d, pages of %d"
-                               % (n, Hq, Hkv, d, wl["ctx"][0], wl["ctx"][1], page),
-                   "sequences": n, "q_heads": Hq, "kv_heads": Hkv, "head_dim": d, "total_keys": int(lens.sum())},
+        "config": {"workload": "decode-step grouped-query attention over a paged K/V cache, %d sequences x %d "
+                               "token%s, %d query / %d kv heads x %d, context %d..%d, pages of %d"
+                               % (n, M, "s" if M > 1 else "", Hq, Hkv, d, wl["ctx"][0], wl["ctx"][1], page),
+                   "sequences": n, "queries_per_sequence": M, "q_heads": Hq, "kv_heads": Hkv, "head_dim": d,
+                   "total_keys": int(lens.sum())},
         "roofline": {"kernel": "gqa_split_mfma_kernel + gqa_combine_kernel (timed together)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("gqa_decode"),
@@ -262,18 +289,22 @@ def decode_bench(ud, args):
             rows = lambda pg: pg[table[i, :nb[i]]].transpose(0, 2, 1, 3).reshape(-1, Hkv * d)[:lens[i]]
             k = (rows(kp_h).astype(np.uint32) << 16).view(np.float32)
             v = (rows(vp_h).astype(np.uint32) << 16).view(np.float32)
-            orc.gqa_attention(q_h[i:i + 1], k, v, ranges_h[i:i + 1], Hq, Hkv)
+            orc.gqa_attention(q_h[i], k, v, ranges_h[i], Hq, Hkv)
             done += 1
         el = time.perf_counter() - t0
-        result["cpu_baseline"] = {"value": round(done / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-                                  "cpu_model": cpu["model"], "nproc": cpu["nproc"], "omp_proc_bind": "close",
-                                  "sample": "%d of the %d sequences (one token each, all heads) in %.1f s, "
-                                            "including the page gather" % (done, n, el)}
+        result["cpu_baseline"] = {"value": round(done * M / el, 3), "unit": "tokens/s", "cores": threads,
+                                  "kind": "port", "cpu_model": cpu["model"], "nproc": cpu["nproc"],
+                                  "omp_proc_bind": "close",
+                                  "sample": "%d of the %d sequences (%d token%s each, all heads) in %.1f s, "
+                                            "including the page gather" % (done, n, M, "s" if M > 1 else "", el)}
     print(json.dumps(result), flush=True)
 
 
-def offline_bench(ud, args):
-    """Offline rel-pos attention over a padded batch of whole utterances (one launch = one layer)."""
+def offline_bench(ud, args, summary=False, steps=None, warmup=None):
+    """Offline rel-pos attention over a padded batch of whole utterances (one launch = one layer).
+    summary: return the kernel's figures as a dict (no CPU baseline, nothing printed)."""
+    steps = steps or args.steps
+    warmup = args.warmup if warmup is None else warmup
     wl = WORKLOADS["offline"]
     B, T, H, dk = wl["batch"], wl["frames"], wl["heads"], wl["head_dim"]
     D = H * dk
@@ -293,29 +324,38 @@ def offline_bench(ud, args):
     out = ud.DeviceBuffer(B * T * D * 2)
     hs = ud.HipStream()
     call = lambda: ud.rel_pos_attention_batched(q, k, v, P, T - 1, u, vb, ranges, out, B, T, H, n_rel, hip_stream=hs)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         call()
     hs.synchronize()
     e0, e1 = ud.Event(), ud.Event()
     e0.record(hs)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         call()
     e1.record(hs)
     e1.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1000.0
-    ms = max(wall_ms, e0.elapsed_ms(e1)) / args.steps
+    ms = max(wall_ms, e0.elapsed_ms(e1)) / steps
     flops_dense = 6.0 * B * H * T * T * dk               # ac + bd + P.V over the padded T x T
     flops_valid = 6.0 * H * T * float(lens.sum()) * dk   # keys limited to each utterance's valid frames
     tflops = flops_dense / (ms / 1000.0) / 1e12
     log("timed %d launches: %.2f us each, %.1f TFLOP/s dense-equivalent (%.1f on valid keys)"
-        % (args.steps, ms * 1000, tflops, flops_valid / (ms / 1000.0) / 1e12))
+        % (steps, ms * 1000, tflops, flops_valid / (ms / 1000.0) / 1e12))
+    if summary:
+        return {"kernel": "relpos_dense_kernel",
+                "workload": "%d utterances x %d frames, %d heads x %d, key padding %d..%d, bf16"
+                            % (B, T, H, dk, wl["valid"][0], wl["valid"][1]),
+                "us_per_launch": round(ms * 1000.0, 3), "frames_per_sec": round(B * T / (ms / 1000.0), 1),
+                "bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_launch": flops_dense,
+                "valid_key_tflops": round(flops_valid / (ms / 1000.0) / 1e12, 2), "launches_timed": steps}
     result = {
         "metric": "offline rel-pos attention: frames/s and bf16 MFMA roofline fraction",
         "value": round(B * T / (ms / 1000.0), 1),
         "unit": "frames/s (one layer, all heads)",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 q/k/v/P operands, fp32 softmax and accumulation",
         "data": "synthetic (seeded N(0,1) q/k/v, random position table, random valid lengths)",
         "config": {"workload": "offline full-context rel-pos MHSA, %d utterances x %d frames (%d s), %d heads x %d, "
                                "key padding %d..%d" % (B, T, int(T * FRAME_SEC), H, dk, wl["valid"][0], wl["valid"][1]),
@@ -506,7 +546,8 @@ def stream_bench(ud, args):
         "value": round(value, 2),
         "unit": "audio-sec/sec",
         "n_gpus": 1, "steps": res["blank"][2], "warmup": warm, "ms_per_step": round(ms, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": PRECISION + " (encoder); mel frontend, joint and RNN-T fp32",
         "data": "synthetic (seeded random-init weights, harmonic test audio, Slaney-like filterbank)",
         "config": {"workload": "live streaming: %d streams x %d samples pushed per step -> mel -> subsampling -> "
                                "24 layers -> joint.enc -> greedy RNN-T, lookahead %d (%d ms chunks), every frame blank"
@@ -563,11 +604,40 @@ def library_gemm_times(M, D, F, iters=100):
     return out
 
 
-def long_chunk_attention(ud, lw, args, hbm_read):
-    """The same fused attention at the long-chunk shape, 256 streams x 14 frames over L = 70 (the
-    batched MFMA kernel: 103 MB per launch, where the fixed per-launch cost is a small part),
-    timed the same way as the default workload's kernel (HIP events over launches cycling the 24
-    layers' rings after one untimed pass).  The weights are the default workload's."""
+PRECISION = "f16 activations/K/V, bf16-valued weights, fp32 accumulation"
+PRECISION_NOTE = ("16-bit encoder (UD_BF16): linear weights rounded to bf16 and held as IEEE half; activations, "
+                  "K/V caches, position tables and MFMA operands IEEE half (saturating at +-65504); fp32 "
+                  "accumulation, residual stream, norms and conv cache")
+
+
+def projection_mfma(ud, enc, rows, mfma_f16, hs, iters=96):
+    """Each projection of the step timed as the step launches it (ud_time_projection, weights from
+    HBM) and the seven projections of a layer together (ff linear1/linear2 twice)."""
+    per_layer = {"ff_linear1": 2, "ff_linear2": 2, "qkv": 1, "linear_out": 1, "pointwise_conv1": 1, "pointwise_conv2": 1}
+    proj = {}
+    tot_fl = tot_ms = 0.0
+    for idx, name in enumerate(ud.Encoder.PROJECTIONS):
+        pms, pfl = enc.time_projection(idx, rows, iters, hip_stream=hs)
+        tf = pfl / (pms / 1000.0) / 1e12
+        proj[name] = {"us": round(pms * 1000.0, 3), "tflops": round(tf, 1),
+                      "frac_nominal": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "frac_measured": round(tf / mfma_f16, 4)}
+        tot_fl += per_layer[name] * pfl
+        tot_ms += per_layer[name] * pms
+        log("projection %-16s %8.2f us  %7.1f TFLOP/s  (%d rows)" % (name, pms * 1000.0, tf, rows))
+    tf = tot_fl / (tot_ms / 1000.0) / 1e12
+    return {"rows": rows, "projections": proj, "layer_tflops": round(tf, 1),
+            "frac_nominal": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "frac_measured": round(tf / mfma_f16, 4),
+            "note": "the seven projections of a layer (ff linear1/linear2 twice), each timed as the step launches it "
+                    "(ud_time_projection, weights from HBM), f16 operands with bf16-valued weights"}
+
+
+def long_chunk(ud, lw, sw, args, hbm_read, mfma_f16):
+    """The long-chunk workload (256 streams x 14 frames over L = 70) on one encoder with the
+    default workload's weights: (1) the fused attention at that shape (the batched MFMA kernel: 103
+    MB per launch, where the fixed per-launch cost is a small part), timed as the default
+    workload's kernel is (HIP events over launches cycling the 24 layers' rings after one untimed
+    pass); (2) the whole mel-in step (subsampling + 24 layers), steps timed back to back as the
+    default workload's are; (3) its projections' MFMA use."""
     wl = WORKLOADS["chunk14"]
     S, T = wl["streams"], wl["T"]
     cfg = ud.EncoderConfig(layers=24, max_chunk=T, max_streams=S, dtype="bf16")
@@ -575,6 +645,7 @@ def long_chunk_attention(ud, lw, args, hbm_read):
     enc = ud.Encoder(cfg)
     for l, w in enumerate(lw):
         enc.set_layer_weights(l, w)
+    enc.set_subsampling_weights(sw)
     enc.finalize()
     streams = [enc.new_stream() for _ in range(S)]
     rng = np.random.default_rng(12)
@@ -592,14 +663,51 @@ def long_chunk_attention(ud, lw, args, hbm_read):
     Tk, n_rel = L + T, L + 2 * T - 1
     nbytes = S * Tk * H * dk * 2 * 2 + S * 2 * T * H * dk * 2 + n_rel * H * dk * 2 + 2 * H * dk * 4
     achieved = nbytes / (ms / 1000.0) / 1e9
-    enc.close()
     log("long-chunk attention (256 streams x 14 frames): %.2f us/launch, %.0f GB/s" % (ms * 1000.0, achieved))
-    return {"kernel": "relpos_ring_mfma_kernel (fused rel-pos attention over the K/V ring window)",
-            "workload": "256 streams x 14 frames, left context 70, 8 heads x 128, bf16 (the long-chunk step's attention)",
+    roof = {"kernel": "relpos_ring_mfma_kernel (fused rel-pos attention over the K/V ring window)",
+            "workload": "256 streams x 14 frames, left context 70, 8 heads x 128, %s (the long-chunk step's attention)"
+                        % PRECISION,
             "us_per_launch": round(ms * 1000.0, 3), "bound": "hbm", "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
             "measured_peak": round(hbm_read, 1), "frac_measured": round(achieved / hbm_read, 4),
             "traffic": read_traffic("relpos_ring_chunk14"), "algorithmic_bytes_per_launch": nbytes}
+    # the whole step at this shape
+    rows = mel_rows(T)
+    mel = ud.DeviceBuffer.from_numpy(rng.standard_normal((S, rows, 128), dtype=np.float32))
+    x = ud.DeviceBuffer(S * T * D * 4)
+    out = ud.DeviceBuffer(S * T * D * 4)
+
+    def step():
+        Tn, valid = enc.subsample(S, mel, x, drop=2, mel_rows=rows, hip_stream=hs)
+        enc.encode_stream_step(streams, x, out, valid=valid, T=Tn, hip_stream=hs)
+
+    for _ in range(3):
+        step()
+    hs.synchronize()
+    n14 = 12
+    e0, e1 = ud.Event(), ud.Event()
+    ud.synchronize()
+    e0.record(hs)
+    t0 = time.perf_counter()
+    for _ in range(n14):
+        step()
+    e1.record(hs)
+    e1.synchronize()
+    wall = (time.perf_counter() - t0) * 1000.0
+    ms14 = max(wall, e0.elapsed_ms(e1)) / n14
+    value14 = S * T * FRAME_SEC / (ms14 / 1000.0)
+    log("long-chunk step (256 streams x 14 frames, 24 layers): %.4f ms/step, %.0f audio-sec/sec" % (ms14, value14))
+    mf = projection_mfma(ud, enc, S * T, mfma_f16, hs, iters=24)
+    flops = 2.0 * S * T * 24 * (2 * 2 * cfg.ff_dim * D + 4 * D * D + 2 * D * D + D * D)
+    step_tf = flops / (ms14 / 1000.0) / 1e12
+    chunk14 = {"workload": "cache-aware encoder step (dw_striding 8x subsampling + 24 layers), %d streams x %d mel "
+                           "rows -> %d frames (1120 ms), left context %d, %s" % (S, rows, T, L, PRECISION),
+               "ms_per_step": round(ms14, 5), "value": round(value14, 2), "unit": "audio-sec/sec",
+               "steps_timed": n14, "projection_tflops_per_step": round(step_tf, 1),
+               "step_frac_of_mfma_peak": round(step_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+               "mfma_utilisation": mf}
+    enc.close()
+    return roof, chunk14
 
 
 def main():
@@ -612,7 +720,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-long-chunk-attention", action="store_true",
-                    help="skip the default workload's second attention measurement at 256 streams x 14 frames")
+                    help="skip the default workload's long-chunk measurements (256 streams x 14 frames: the "
+                         "attention kernel, the whole step and its projections)")
+    ap.add_argument("--no-other-kernels", action="store_true",
+                    help="skip the default workload's offline-attention and decode-attention kernel figures")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="also run one device-to-device copy of this many MiB (a known-size kernel for "
                          "calibrating rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -633,8 +744,8 @@ def main():
         ud.synchronize()
         log("calibration copy: %d MiB device-to-device" % args.calibrate_copy_mib)
         src.free(); dst.free()
-    if args.workload == "decode":
-        decode_bench(ud, args)
+    if args.workload in ("decode", "decode_mq"):
+        decode_bench(ud, args, workload=args.workload)
         return
     if args.workload == "offline":
         offline_bench(ud, args)
@@ -649,8 +760,8 @@ def main():
     S, T = wl["streams"], wl["T"]
     cfg = ud.EncoderConfig(layers=24, max_chunk=T, max_streams=S, dtype="bf16")
     L, D, H, dk = cfg.left_context, cfg.d_model, cfg.heads, cfg.d_model // cfg.heads
-    log("device %s; workload %s: %d streams x %d frames, L=%d, %d layers, bf16"
-        % (ud.device_arch(), args.workload, S, T, L, cfg.layers))
+    log("device %s; workload %s: %d streams x %d frames, L=%d, %d layers, %s"
+        % (ud.device_arch(), args.workload, S, T, L, cfg.layers, PRECISION))
 
     lw = [ud.synthetic_layer_weights(cfg, 2024, l, ln_jitter=0.0) for l in range(cfg.layers)]
     sw = ud.synthetic_subsampling_weights(2025)
@@ -741,18 +852,7 @@ def main():
     log("measured peaks: HBM read %.0f GB/s, copy %.0f GB/s; MFMA f16 %.0f, bf16 %.0f TFLOP/s"
         % (hbm_read, hbm_copy, mfma_f16, mfma_bf16))
     rows_step = S * T
-    per_layer = {"ff_linear1": 2, "ff_linear2": 2, "qkv": 1, "linear_out": 1, "pointwise_conv1": 1, "pointwise_conv2": 1}
-    proj = {}
-    tot_fl = tot_ms = 0.0
-    for idx, name in enumerate(ud.Encoder.PROJECTIONS):
-        pms, pfl = enc.time_projection(idx, rows_step, 96, hip_stream=hs)
-        tf = pfl / (pms / 1000.0) / 1e12
-        proj[name] = {"us": round(pms * 1000.0, 3), "tflops": round(tf, 1),
-                      "frac_nominal": round(tf / MFMA_BF16_PEAK_TFLOPS, 4), "frac_measured": round(tf / mfma_f16, 4)}
-        tot_fl += per_layer[name] * pfl
-        tot_ms += per_layer[name] * pms
-        log("projection %-16s %8.2f us  %7.1f TFLOP/s" % (name, pms * 1000.0, tf))
-    proj_tf = tot_fl / (tot_ms / 1000.0) / 1e12
+    mfma_util = projection_mfma(ud, enc, rows_step, mfma_f16, hs)
     lib_gemm = library_gemm_times(rows_step, D, cfg.ff_dim) if args.library_gemm else None
 
     # The fused attention kernel alone, on the stream it is launched on.
@@ -784,12 +884,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": PRECISION,
+        "precision": PRECISION_NOTE,
         "data": "synthetic (seeded random-init weights, N(0,1) inputs and caches)",
         "config": {
             "workload": "cache-aware FastConformer encoder step (dw_striding 8x subsampling + 24 layers), "
-                        "%d streams x %d mel rows -> %d frames (%d ms), left context %d, bf16"
-                        % (S, rows, T, int(T * FRAME_SEC * 1000), L),
+                        "%d streams x %d mel rows -> %d frames (%d ms), left context %d, %s"
+                        % (S, rows, T, int(T * FRAME_SEC * 1000), L, PRECISION),
             "streams": S, "mel_rows": rows, "chunk_frames": T, "left_context": L, "layers": cfg.layers,
             "d_model": D, "heads": H, "ff_dim": cfg.ff_dim, "conv_kernel": cfg.conv_kernel,
         },
@@ -801,12 +902,7 @@ def main():
                            "mfma_f16_tflops": round(mfma_f16, 1), "mfma_bf16_tflops": round(mfma_bf16, 1),
                            "method": "ud_measure_hbm (4 GiB buffers x 10, non-temporal streaming) and ud_measure_mfma "
                                      "(v_mfma_f32_32x32x16 register chains) in this run"},
-        "mfma_utilisation": {
-            "rows": rows_step, "projections": proj,
-            "layer_tflops": round(proj_tf, 1), "frac_nominal": round(proj_tf / MFMA_BF16_PEAK_TFLOPS, 4),
-            "frac_measured": round(proj_tf / mfma_f16, 4),
-            "note": "the seven projections of a layer (ff linear1/linear2 twice), each timed as the step "
-                    "launches it (ud_time_projection, weights from HBM), f16 operands with bf16-valued weights"},
+        "mfma_utilisation": mfma_util,
         **({"library_gemm": dict(lib_gemm, method="torch.matmul bf16 (hipBLASLt) on the same [rows, K] x [K, N], "
                                                "100 back-to-back calls, HIP events; plain output, no epilogue")}
            if lib_gemm else {}),
@@ -831,7 +927,12 @@ def main():
     }
     enc.close()
     if args.workload == "chunk2" and not args.no_long_chunk_attention:
-        result["roofline_long_chunk"] = long_chunk_attention(ud, lw, args, hbm_read)
+        result["roofline_long_chunk"], result["chunk14_step"] = long_chunk(ud, lw, sw, args, hbm_read, mfma_f16)
+    if args.workload == "chunk2" and not args.no_other_kernels:
+        result["offline_attention"] = offline_bench(ud, args, summary=True, steps=40, warmup=5)
+        result["decode_attention"] = decode_bench(ud, args, summary=True, steps=200, warmup=20)
+        result["decode_attention_4_queries"] = decode_bench(ud, args, summary=True, steps=200, warmup=20,
+                                                            workload="decode_mq")
     if not args.no_cpu_baseline:
         cpu = host_cpu()
         # a bounded sample: all 64 streams at 2-frame chunks (about 0.7 s per step on 16 cores); at

@@ -3,7 +3,8 @@
  * K/V cache for one new token per sequence, the rotate-half RoPE and the paged cache append.
  *
  * This is the decode-step attention of DictatorEngine's Voxtral decoder (one token per sequence,
- * Sources/DictatorEngine/Models/Voxtral.swift:347-397), batched over independent sequences whose
+ * or up to 8 positions per sequence, Sources/DictatorEngine/Models/Voxtral.swift:347-397), batched
+ * over independent sequences whose
  * K/V caches live in fixed-size pages instead of the reference's per-session sliding window
  * (SlidingKV, Voxtral.swift:206-250).  Conventions are those of ud_encoder.h: 0 or a negative
  * ud_status, message in ud_last_error(), device pointers *_dev, asynchronous on hip_stream.
@@ -51,6 +52,24 @@ UD_API int ud_gqa_attention_paged(int32_t kv_dtype, const float* q_dev, const vo
                                   float* out_dev, int32_t n, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
                                   int32_t block_size, int32_t max_keys, void* workspace, size_t workspace_bytes,
                                   void* hip_stream);
+
+/* Replaces Step.attention with 2 .. 8 queries (Ops.swift:141-162 -> attention_mq_split_f16 +
+ * attention_combine, 30_voxtral.metal:240-338; the M positions VoxtralSession.decode passes per
+ * call, Voxtral.swift:347-371): n_queries (1 .. 8) query rows per sequence, each with its own key
+ * range, over the sequence's pages; every K/V page is read once for all of them.
+ *   q_dev        fp32 [n, n_queries, q_heads * head_dim]
+ *   ranges_dev   int32 [n, n_queries, 2]: query m of sequence i attends to keys
+ *                [ranges[i][m].x, ranges[i][m].y) (0 if empty)
+ *   out_dev      fp32 [n, n_queries, q_heads * head_dim]
+ *   workspace    ud_gqa_workspace_bytes(n * n_queries, q_heads, head_dim, max_keys) bytes
+ * Block-table entries are read for the blocks between the lowest start and the highest end of a
+ * sequence's non-empty query ranges.  Otherwise as ud_gqa_attention_paged (formula, formats,
+ * precision, limits; n * n_queries <= 65535), which is this call with n_queries = 1. */
+UD_API int ud_gqa_attention_paged_mq(int32_t kv_dtype, const float* q_dev, const void* k_pages, const void* v_pages,
+                                     const int32_t* block_table, int32_t max_blocks, const int32_t* ranges_dev,
+                                     float* out_dev, int32_t n, int32_t n_queries, int32_t q_heads, int32_t kv_heads,
+                                     int32_t head_dim, int32_t block_size, int32_t max_keys, void* workspace,
+                                     size_t workspace_bytes, void* hip_stream);
 
 /* Allocation-free variant of ud_gqa_attention_paged.  It has no counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph capture, tight serving

@@ -15,6 +15,9 @@
  *  - `hip_stream` is a hipStream_t (NULL = the null stream).  Device work is enqueued on it and
  *    the call returns without waiting, except where a function says it synchronizes.
  *  - One encoder may be stepped by one thread at a time; distinct encoders are independent.
+ *  - The device work of one encoder's calls runs in call order whatever HIP streams the calls are
+ *    given: a call on a different stream than the encoder's previous call first makes its stream
+ *    wait for that call's work (the calls share the encoder's workspace).
  */
 #ifndef UD_ENCODER_H
 #define UD_ENCODER_H
@@ -40,20 +43,30 @@ typedef enum {
 
 typedef enum {
     UD_F32 = 0,               /* fp32 weights, activations, caches */
-    UD_BF16 = 1,              /* encoder: bf16 weights (each linear weight rounded to bf16, RNE,
-                                 Tensor.swift:116-122 -- the reference's bf16-weight setting),
-                                 held as IEEE half (exactly, for |w| >= 2^-17) and multiplied on
-                                 the f16 MFMA; 16-bit activations (GEMM inputs, q/k/v,
-                                 attention output), K/V caches and position tables are IEEE half;
-                                 fp32 accumulation, residual stream, norms, pos_bias, depthwise
-                                 conv and conv cache (the keep-fp32 policy of
-                                 Sources/DictatorEngine/Core/Convert.swift:76-83).  Half's 11-bit
-                                 significand (bf16: 8) keeps a 24-layer step within 2e-2 of
-                                 the fp32-activation reference at 14-frame chunks, where bf16
-                                 activations exceed it.
+    UD_BF16 = 1,              /* encoder, 16-bit: bf16-valued linear weights (each rounded to bf16,
+                                 RNE, Tensor.swift:116-122 -- the bf16-weight setting) held as IEEE
+                                 half (exactly, for |w| >= 2^-17) and multiplied on the f16 MFMA.
+                                 What runs in 16 bits is IEEE half, not bfloat16: activations
+                                 (GEMM inputs, FF hidden, q/k/v, attention output), K/V caches and
+                                 position tables; fp32 accumulation, residual stream, norms,
+                                 pos_bias, depthwise conv and conv cache.  Half's 11-bit significand
+                                 (bf16: 8) keeps a 24-layer step within 2e-2 of the fp32-activation
+                                 reference at 14-frame chunks, where bf16 activations exceed it.
+                                 Range: every 16-bit store saturates at +-65504 (NaN stays NaN), so
+                                 an activation past half's range is clipped, not turned into inf; a
+                                 weight past it is refused (UD_ERR_WEIGHT).
+                                 Front-end: conv.3 / conv.6 / out weights are rounded fp32 -> half
+                                 and run on the f16 MFMA with half activations; conv.0 / 2 / 5 stay
+                                 fp32.  (The reference's f16 checkpoint keeps every
+                                 encoder.pre_encode.conv.* fp32, Convert.swift:80; the half
+                                 conv.3 / conv.6 are a measured deviation.)
                                  Single-op attention entries: bfloat16 operands. */
-    UD_F16 = 2                /* IEEE half: the decoder K/V cache format of the reference
-                                 (Sources/DictatorEngine/Core/Ops.swift:147); decode entry points only */
+    UD_F16 = 2                /* encoder: as UD_BF16 but the linear weights are rounded fp32 -> half
+                                 directly, the reference's f16 checkpoint
+                                 (WeightConverter.convert(.f16), Convert.swift:76-112: the
+                                 precision of its published step times); the same kernels.
+                                 Decode entry points: IEEE half K/V pages, the decoder K/V cache
+                                 format of the reference (Sources/DictatorEngine/Core/Ops.swift:147). */
 } ud_dtype;
 
 /* FastConformerConfig (Sources/DictatorEngine/Models/FastConformer.swift:5-38) plus the streaming
@@ -90,7 +103,8 @@ UD_API int ud_encoder_get_config(const ud_encoder* enc, ud_encoder_config* out);
  * checkpoint's name map, and the 12 optional encoder.pre_encode.* subsampling tensors); `host`
  * holds `count` fp32 values in the checkpoint layout ([out, in] for linears, k=1 axes squeezed,
  * depthwise [D, 1, K], conv2d [256, 1, 3, 3]).  The values are converted to the
- * encoder's dtype on upload (bf16: round-to-nearest-even, Tensor.swift:116-122).  Synchronous. */
+ * encoder's dtype on upload (UD_BF16: linear weights rounded to bf16, round-to-nearest-even,
+ * Tensor.swift:116-122; UD_F16: rounded to half; both held as half, see ud_dtype).  Synchronous. */
 UD_API int ud_encoder_set_weight(ud_encoder* enc, const char* name, const float* host, int64_t count);
 
 /* Replaces preparePositionTables (FastConformer.swift:161-178) as called by makeStreamState

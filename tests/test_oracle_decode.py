@@ -42,6 +42,21 @@ def test_gqa_attention_kat(orc):
     assert np.abs(got - numpy_gqa(q, k, v, ranges, Hq, Hkv)).max() < 2e-5
 
 
+def test_gqa_multi_query_kat(orc):
+    """VoxtralOpTests.swift:42-59: 4 queries, 32 heads x 64, f16 caches of 700 keys, ranges
+    [m, 697 + m): the oracle's several-query call equals one call per query (each query is
+    computed on its own) and the float64 numpy attention."""
+    Tq, Tk, H, d = 4, 700, 32, 64
+    q = orc.lcg_floats(Tq * H * d, 55).reshape(Tq, H * d)
+    k = _f16(orc.lcg_floats(Tk * H * d, 56)).reshape(Tk, H * d)
+    v = _f16(orc.lcg_floats(Tk * H * d, 57)).reshape(Tk, H * d)
+    ranges = np.array([[0, 697], [1, 698], [2, 699], [3, 700]], np.int32)
+    got = orc.gqa_attention(q, k, v, ranges, H, H)
+    per = np.concatenate([orc.gqa_attention(q[i:i + 1], k, v, ranges[i:i + 1], H, H) for i in range(Tq)])
+    assert np.abs(got - per).max() <= 1e-5
+    assert np.abs(got - numpy_gqa(q, k, v, ranges, H, H)).max() < 2e-5
+
+
 def test_gqa_head_map_and_edges(orc):
     """Query head h reads kv head h // (Hq/Hkv): with V constant per kv head the output of head h
     is exactly that constant; a single key returns its V row; an empty range returns 0."""

@@ -98,6 +98,8 @@ def _sig(lib):
                                        ctypes.c_size_t, p]),
         "ud_gqa_attention_paged_noalloc": (i, [_i32, p, p, p, p, _i32, p, p, _i32, _i32, _i32, _i32, _i32, _i32,
                                                p]),
+        "ud_gqa_attention_paged_mq": (i, [_i32, p, p, p, p, _i32, p, p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, p,
+                                          ctypes.c_size_t, p]),
         "ud_rope_rotate_half": (i, [_i32, p, _i32, _i32, _i32, _i32, p, _i32, p, p]),
         "ud_paged_kv_append": (i, [_i32, p, p, p, p, p, _i32, p, _i32, _i32, _i32, _i32, p]),
         "ud_encoder_get_config": (i, [p, ctypes.POINTER(_Config)]),
@@ -286,7 +288,12 @@ class Event:
 
 @dataclasses.dataclass
 class EncoderConfig:
-    """FastConformerConfig.nemotron (FastConformer.swift:5-38) plus streaming geometry."""
+    """FastConformerConfig.nemotron (FastConformer.swift:5-38) plus streaming geometry.
+
+    dtype: "f32"; "bf16" (bf16-valued linear weights held as IEEE half; half activations, K/V
+    caches and tables; fp32 accumulation); or "f16" (the same, with the weights rounded straight
+    to half, the reference's f16 checkpoint, Core/Convert.swift:76-112).  16-bit stores saturate
+    at +-65504."""
     layers: int = 24
     d_model: int = 1024
     heads: int = 8
@@ -549,6 +556,18 @@ def gqa_attention_paged(q, k_pages, v_pages, block_table, max_blocks, ranges, ou
                                         hip_stream.ptr if hip_stream else None))
 
 
+def gqa_attention_paged_mq(q, k_pages, v_pages, block_table, max_blocks, ranges, out, n, n_queries, q_heads, kv_heads,
+                           head_dim, max_keys, workspace, kv_dtype="bf16", block_size=16, hip_stream=None):
+    """Step.attention with n_queries (1 .. 8) positions per sequence (Ops.swift:141-162,
+    attention_mq_split): q/out fp32 [n, n_queries, q_heads*head_dim], ranges int32 [n, n_queries, 2],
+    each K/V page read once for all of a sequence's queries; workspace of
+    gqa_workspace_bytes(n * n_queries, q_heads, head_dim, max_keys) bytes."""
+    _check(lib().ud_gqa_attention_paged_mq(_DTYPES[kv_dtype], q.ptr, k_pages.ptr, v_pages.ptr, block_table.ptr,
+                                           max_blocks, ranges.ptr, out.ptr, n, n_queries, q_heads, kv_heads, head_dim,
+                                           block_size, max_keys, workspace.ptr, workspace.nbytes,
+                                           hip_stream.ptr if hip_stream else None))
+
+
 # Static scratch of ud_gqa_attention_paged_noalloc (UD_GQA_NOALLOC_SCRATCH_BYTES in ud_decode.h).
 GQA_NOALLOC_SCRATCH_BYTES = 40 << 20
 
@@ -800,7 +819,8 @@ def synthetic_rnnt_weights(seed, H=640, V=1025, L=2, enc_dim=1024, blank_bias=0.
 
 def round_f16(a):
     """IEEE-half rounding (round to nearest even) of float32 values, returned as float32: the
-    storage format of a 16-bit (UD_BF16) encoder's activations, K/V caches and position tables."""
+    storage format of a 16-bit (bf16 or f16) encoder's activations, K/V caches and position tables,
+    and the weight rounding of an f16 encoder."""
     return np.asarray(a, np.float32).astype(np.float16).astype(np.float32)
 
 

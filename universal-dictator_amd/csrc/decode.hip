@@ -120,9 +120,12 @@ __device__ __forceinline__ float xsum8(float a, float b, bool bit3) {
 }
 
 struct GqaArgs {
-    const float* q; const void* kp; const void* vp;
-    const int32_t* bt; const int32_t* ranges;
-    float* part;                   // [n][Hq][NS][D + 2]: unnormalised sum, max, sum of exp
+    const float* q;                // [n][M][Hq][D]
+    const void* kp; const void* vp;
+    const int32_t* bt;
+    const int32_t* ranges;         // [n][M][2]
+    float* part;                   // [n][M][Hq][NS][D + 2]: unnormalised sum, max, sum of exp
+    int M;                         // queries per sequence (1 .. 8), all over the sequence's pages
     int max_blocks, Hq, Hkv, NS;
     int kmax;                      // keys the pages and the split grid can hold
     float scale;
@@ -134,35 +137,27 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = tid / LPR, sub = tid % LPR;
     const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
-    const int lo = max(a.ranges[2 * seq], 0), hi = min(a.ranges[2 * seq + 1], a.kmax);
+    const int M = a.M;
+    const int32_t* rg = a.ranges + (int64_t)2 * seq * M;
+    // the span of the queries' non-empty key ranges within this split
+    int lo = a.kmax, hi = 0;
+    for (int m = 0; m < M; m++) {
+        const int l = max(rg[2 * m], 0), h = min(rg[2 * m + 1], a.kmax);
+        if (l < h) { lo = min(lo, l); hi = max(hi, h); }
+    }
     const int s0 = split * SPLIT;
-    const int klo = max(lo, s0), khi = min(hi, s0 + SPLIT);
-    if (klo >= khi) return;                       // this split holds no key of the range
+    const int ulo = max(lo, s0), uhi = min(hi, s0 + SPLIT);
+    if (ulo >= uhi) return;                       // this split holds no key of any query's range
     __shared__ float sc[G][SPLIT];
     __shared__ float stat[G][2];
     __shared__ __align__(16) float red[4][G][D];
-
-    // ---- the G query heads of this kv head (8 channels per lane); for bf16 pages also as bf16
-    //      pairs (channels 2e, 2e + 1) for the packed dot products
     constexpr bool PK = std::is_same<KT, BF16>::value;
-    float q[G][8];
-    uint32_t qb[G][4];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        const float* qr = a.q + (int64_t)seq * a.Hq * D + (kvh * G + g) * D + sub * 8;
-        const float4 x0 = *reinterpret_cast<const float4*>(qr), x1 = *reinterpret_cast<const float4*>(qr + 4);
-        q[g][0] = x0.x; q[g][1] = x0.y; q[g][2] = x0.z; q[g][3] = x0.w;
-        q[g][4] = x1.x; q[g][5] = x1.y; q[g][6] = x1.z; q[g][7] = x1.w;
-        if constexpr (PK) {
-#pragma unroll
-            for (int e = 0; e < 4; e++) qb[g][e] = pack_bf16x2(q[g][2 * e], q[g][2 * e + 1]);
-        }
-    }
-    // ---- K and V rows: key s0 + grp + RG p; pages outside [klo, khi) are never looked up.  A pass
+
+    // ---- K and V rows: key s0 + grp + RG p; pages outside [ulo, uhi) are never looked up.  A pass
     //      covers RG / PAGE whole pages (s0 is a multiple of 128), so a lane's page is
     //      (s0 + RG p) / PAGE + grp / PAGE: the page table entries are scalar loads, and a row's
     //      address is a scalar page base plus the lane's fixed offset (row grp % PAGE, 8 channels).
-    const int blo = klo / PAGE, bhi = (khi - 1) / PAGE;
+    const int blo = ulo / PAGE, bhi = (uhi - 1) / PAGE;
     const int32_t* bt = a.bt + (int64_t)seq * a.max_blocks;
     constexpr int PPP = RG / PAGE;                // pages per pass (1 for D = 128, 2 for D = 64)
     const uint32_t lane_off = (uint32_t)(((grp % PAGE) * D + sub * 8) * 2);   // bytes
@@ -186,6 +181,27 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
     for (int p = 0; p < NP; p++) kr[p] = ld16((PPP == 1 || gp == 0 ? kb[p][0] : kb[p][PPP - 1]) + lane_off);
 #pragma unroll
     for (int p = 0; p < NP; p++) vr[p] = ld16((PPP == 1 || gp == 0 ? vb[p][0] : vb[p][PPP - 1]) + lane_off);
+
+    // The split's K and V rows stay in registers while each query of the sequence is processed in
+    // turn (one read of the pages for all M queries).
+    for (int qm = 0; qm < M; qm++) {
+    const int klo = max(max(rg[2 * qm], 0), s0), khi = min(min(rg[2 * qm + 1], a.kmax), s0 + SPLIT);
+    if (klo >= khi) continue;                     // no key of this query's range here (uniform)
+    // ---- the G query heads of this kv head (8 channels per lane); for bf16 pages also as bf16
+    //      pairs (channels 2e, 2e + 1) for the packed dot products
+    float q[G][8];
+    uint32_t qb[G][4];
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        const float* qr = a.q + ((int64_t)(seq * M + qm) * a.Hq + kvh * G + g) * D + sub * 8;
+        const float4 x0 = *reinterpret_cast<const float4*>(qr), x1 = *reinterpret_cast<const float4*>(qr + 4);
+        q[g][0] = x0.x; q[g][1] = x0.y; q[g][2] = x0.z; q[g][3] = x0.w;
+        q[g][4] = x1.x; q[g][5] = x1.y; q[g][6] = x1.z; q[g][7] = x1.w;
+        if constexpr (PK) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) qb[g][e] = pack_bf16x2(q[g][2 * e], q[g][2 * e + 1]);
+        }
+    }
 
     // ---- scores of the G heads -> sc (masked keys -inf)
     bool writer;
@@ -308,9 +324,11 @@ __global__ __launch_bounds__(256) void gqa_split_kernel(GqaArgs a) {
     for (int idx = tid; idx < G * D; idx += 256) {
         const int g = idx / D, dd = idx % D;
         const float s = red[0][g][dd] + red[1][g][dd] + red[2][g][dd] + red[3][g][dd];
-        float* pr = a.part + (((int64_t)seq * a.Hq + kvh * G + g) * a.NS + split) * (D + 2);
+        float* pr = a.part + ((((int64_t)seq * M + qm) * a.Hq + kvh * G + g) * a.NS + split) * (D + 2);
         pr[dd] = s;
         if (dd == 0) { pr[D] = stat[g][0]; pr[D + 1] = stat[g][1]; }
+    }
+    if (qm + 1 < M) __syncthreads();              // sc, stat and red are reused by the next query
     }
 }
 
@@ -346,40 +364,58 @@ __device__ __forceinline__ v4i16_t kv_tr16(const char* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t*)p);
 }
 
-template <int G>
+// Query rows: the M queries of a sequence times the G query heads of the kv head, row r = m G + gh
+// (QR = M G rows, at most QM; RT = ceil(QM / 16) MFMA tiles of 16 rows).  Every K/V row of the
+// split is loaded once and multiplied against all of them.  QM == G is the one-query form.
+template <int G, int QM>
 __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
     constexpr int D = 128, ROWB = 2 * D, KS = MSPLIT, NWV = KS / 32;
     constexpr int DPW = (8 + NWV - 1) / NWV;      // channel tiles per wave (the last ones may have fewer)
+    constexpr int RT = (QM + 15) / 16;
+    constexpr bool ONE = QM == G;                 // one query per sequence
     static_assert(KS % 64 == 0 && KS <= 256, "split of 64 .. 256 keys");
+    static_assert(QM <= 64 && (ONE || QM % 16 == 0), "query rows");
     // the wave index as a wave-uniform value, so that the page lookups are scalar loads (a vector
     // load there would make the wait for it cover every load in flight)
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, g = lane >> 4;
     const int kvh = blockIdx.x, split = blockIdx.y, seq = blockIdx.z;
-    const int lo = max(a.ranges[2 * seq], 0), hi = min(a.ranges[2 * seq + 1], a.kmax);
+    const int M = ONE ? 1 : a.M, QR = ONE ? G : M * G;
+    const int32_t* rg = a.ranges + (int64_t)2 * seq * M;
+    // the span of the queries' non-empty key ranges (scalar loads)
+    int lo = a.kmax, hi = 0;
+    for (int m = 0; m < M; m++) {
+        const int l = max(rg[2 * m], 0), h = min(rg[2 * m + 1], a.kmax);
+        if (l < h) { lo = min(lo, l); hi = max(hi, h); }
+    }
     const int s0 = split * KS;
     const int klo = max(lo, s0), khi = min(hi, s0 + KS);
-    if (klo >= khi) return;                       // this split holds no key of the range
+    if (klo >= khi) return;                       // this split holds no key of any query's range
     __shared__ __align__(16) char kv[KS * ROWB];         // K, then V
-    __shared__ __align__(16) float sc[G][KS];
-    __shared__ float stat[G][2];
+    __shared__ __align__(16) float sc[QM][KS];
+    __shared__ float stat[QM][2];
+    __shared__ int2 qrng[ONE ? 1 : 8];            // each query's range clipped to the split
+    if (!ONE && tid < M) qrng[tid] = make_int2(max(max(rg[2 * tid], 0), s0), min(min(rg[2 * tid + 1], a.kmax), s0 + KS));
 
     // ---- K of the split into LDS, V into registers: wave w takes pages 2w, 2w + 1 of the split
     //      (rows 32w .. 32w + 31); each instruction covers 4 rows, lane L holding piece L % 16 of
     //      row L / 16 of them, which is source piece (L % 16) xor f(row).  Pages outside [klo, khi)
     //      are clamped to pages inside it (their rows are masked below).
     // q rows first (their loads issued before the K and V rows, so the wait below covers them)
-    float4 qx[4][2];
-    {
-        const float* qr = a.q + (int64_t)seq * a.Hq * D + (kvh * G + min(col, G - 1)) * D + 8 * g;
+    float4 qx[RT][4][2];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+        const int r = min(16 * rt + col, QR - 1);
+        const int m = ONE ? 0 : r / G, gh = ONE ? r : r % G;
+        const float* qr = a.q + ((int64_t)(seq * M + m) * a.Hq + kvh * G + gh) * D + 8 * g;
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
-            qx[kc][0] = *reinterpret_cast<const float4*>(qr + 32 * kc);
-            qx[kc][1] = *reinterpret_cast<const float4*>(qr + 32 * kc + 4);
+            qx[rt][kc][0] = *reinterpret_cast<const float4*>(qr + 32 * kc);
+            qx[rt][kc][1] = *reinterpret_cast<const float4*>(qr + 32 * kc + 4);
         }
     }
-    // The wait below counts vector-memory operations: the 8 q loads, then the 8 direct K loads, then
-    // the 8 V loads must be issued in that order, which the scheduling barriers pin.
+    // The wait below counts vector-memory operations: the 8 RT q loads, then the 8 direct K loads,
+    // then the 8 V loads must be issued in that order, which the scheduling barriers pin.
     __builtin_amdgcn_sched_barrier(0);
     const int blo = klo / PAGE, bhi = (khi - 1) / PAGE;
     const int32_t* bt = a.bt + (int64_t)seq * a.max_blocks;
@@ -413,36 +449,55 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
         for (int i = 0; i < 4; i++) vr[e][i] = ld16(vp + off[e][i]);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));     // q and the K rows landed (the 8 V loads may not)
-    // q as the A operand: lane (r, g) holds q[head r][32kc + 8g .. + 7] in bf16 (zero for r >= G)
-    uint4 qa[4];
+    // q as the A operand: lane (r, g) of tile rt holds row 16 rt + r's q[32kc + 8g .. + 7] in bf16
+    // (zero for rows >= QR)
+    uint4 qa[RT][4];
 #pragma unroll
-    for (int kc = 0; kc < 4; kc++) {
-        const float4 x0 = qx[kc][0], x1 = qx[kc][1];
-        qa[kc] = col < G ? make_uint4(pack_bf16x2(x0.x, x0.y), pack_bf16x2(x0.z, x0.w), pack_bf16x2(x1.x, x1.y),
-                                      pack_bf16x2(x1.z, x1.w))
-                         : make_uint4(0, 0, 0, 0);
-    }
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+            const float4 x0 = qx[rt][kc][0], x1 = qx[rt][kc][1];
+            qa[rt][kc] = 16 * rt + col < QR ? make_uint4(pack_bf16x2(x0.x, x0.y), pack_bf16x2(x0.z, x0.w),
+                                                         pack_bf16x2(x1.x, x1.y), pack_bf16x2(x1.z, x1.w))
+                                            : make_uint4(0, 0, 0, 0);
+        }
     __syncthreads();
 
-    // ---- scores of the wave's keys 32w + 16t + c -> sc (masked keys -inf)
+    // ---- scores of the wave's keys 32w + 16t + c -> sc (keys outside a row's range -inf)
 #pragma unroll
     for (int t = 0; t < 2; t++) {
         const int r = 32 * wave + 16 * t + col;
-        f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        f32x4_t acc[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) acc[rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
             const uint4 kb = *reinterpret_cast<const uint4*>(kv + kv_swz(r, 4 * kc + g));
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa[kc]), as_bf16x8(kb), acc, 0, 0, 0);
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+                acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa[rt][kc]), as_bf16x8(kb), acc[rt], 0, 0, 0);
         }
         const int j = s0 + r;
-        const bool in = j >= klo && j < khi;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (4 * g + i < G) sc[4 * g + i][r] = in ? acc[i] * a.scale : -INFINITY;
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = 16 * rt + 4 * g + i;
+                if (row < QR) {
+                    bool in;
+                    if constexpr (ONE) {
+                        in = j >= klo && j < khi;
+                    } else {
+                        const int2 qq = qrng[row / G];
+                        in = j >= qq.x && j < qq.y;
+                    }
+                    sc[row][r] = in ? acc[rt][i] * a.scale : -INFINITY;
+                }
+            }
     }
     __syncthreads();                              // every wave has read K
 
-    // ---- V over K in LDS, where the direct loads put K (rows outside the range zeroed)
+    // ---- V over K in LDS, where the direct loads put K (rows outside the span zeroed)
 #pragma unroll
     for (int e = 0; e < 2; e++)
 #pragma unroll
@@ -452,8 +507,9 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
             *reinterpret_cast<uint4*>(kv + (32 * wave + 16 * e + 4 * i) * ROWB + 16 * lane) = v;
         }
 
-    // ---- softmax of the split, one wave per head: probabilities in sc, (max, sum) in stat
-    for (int gh = wave; gh < G; gh += NWV) {
+    // ---- softmax of the split, one wave per row: probabilities in sc, (max, sum) in stat; a row
+    //      with no key in the split gets max -inf and sum 0 (never read by the combine)
+    for (int gh = wave; gh < QR; gh += NWV) {
         float v[KS / 64];
         float m = -INFINITY;
 #pragma unroll
@@ -471,21 +527,28 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
     }
     __syncthreads();
 
-    // ---- out^T += V^T . P^T per 32-key piece kk.  B: lane (c, g) holds head c's probabilities of
-    //      keys 32kk + 4g + e (e < 4), then 32kk + 16 + 4g + e; A: V^T over the same keys (lane c
-    //      of a 16-lane group reads column c & 3 of rows 32kk + 4g + c / 4 and, 16 keys on, of
-    //      rows 32kk + 16 + 4g + c / 4: channels 16dt + 4(c & 3) .., half c & 1 of piece pc)
-    f32x4_t oacc[DPW];
+    // ---- out^T += V^T . P^T per 32-key piece kk.  B (tile rt): lane (c, g) holds row 16 rt + c's
+    //      probabilities of keys 32kk + 4g + e (e < 4), then 32kk + 16 + 4g + e; A: V^T over the
+    //      same keys (lane c of a 16-lane group reads column c & 3 of rows 32kk + 4g + c / 4 and,
+    //      16 keys on, of rows 32kk + 16 + 4g + c / 4: channels 16dt + 4(c & 3) .., half c & 1 of
+    //      piece pc), shared by the RT tiles
+    f32x4_t oacc[DPW][RT];
 #pragma unroll
-    for (int u = 0; u < DPW; u++) oacc[u] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const int hc = min(col, G - 1);
+    for (int u = 0; u < DPW; u++)
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) oacc[u][rt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int kk = 0; kk < KS / 32; kk++) {
-        const float4 p0 = *reinterpret_cast<const float4*>(&sc[hc][32 * kk + 4 * g]);
-        const float4 p1 = *reinterpret_cast<const float4*>(&sc[hc][32 * kk + 16 + 4 * g]);
-        const uint4 pb = col < G ? make_uint4(pack_bf16x2(p0.x, p0.y), pack_bf16x2(p0.z, p0.w), pack_bf16x2(p1.x, p1.y),
-                                              pack_bf16x2(p1.z, p1.w))
-                                 : make_uint4(0, 0, 0, 0);
+        uint4 pb[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const int hc = min(16 * rt + col, QR - 1);
+            const float4 p0 = *reinterpret_cast<const float4*>(&sc[hc][32 * kk + 4 * g]);
+            const float4 p1 = *reinterpret_cast<const float4*>(&sc[hc][32 * kk + 16 + 4 * g]);
+            pb[rt] = 16 * rt + col < QR ? make_uint4(pack_bf16x2(p0.x, p0.y), pack_bf16x2(p0.z, p0.w),
+                                                     pack_bf16x2(p1.x, p1.y), pack_bf16x2(p1.z, p1.w))
+                                        : make_uint4(0, 0, 0, 0);
+        }
         const int k0 = 32 * kk + 4 * g + (col >> 2);
 #pragma unroll
         for (int u = 0; u < DPW; u++) {
@@ -497,21 +560,29 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
             uint4 av;
             __builtin_memcpy(&av.x, &b0, 8);
             __builtin_memcpy(&av.z, &b1, 8);
-            oacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(pb), oacc[u], 0, 0, 0);
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+                oacc[u][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av), as_bf16x8(pb[rt]), oacc[u][rt], 0, 0, 0);
         }
     }
 
-    // ---- partial of head c: out^T lane (c, g) holds channels 16dt + 4g .. + 3; (max, sum) from stat
-    if (col < G) {
-        float* pr = a.part + (((int64_t)seq * a.Hq + kvh * G + col) * a.NS + split) * (D + 2);
+    // ---- partial of row 16 rt + c (query m, head gh): out^T lane (c, g) holds channels
+    //      16dt + 4g .. + 3; (max, sum) from stat
 #pragma unroll
-        for (int u = 0; u < DPW; u++) {
-            if (wave + NWV * u >= 8) break;
-            float* o = pr + 16 * (wave + NWV * u) + 4 * g;
-            *reinterpret_cast<float2*>(o) = make_float2(oacc[u][0], oacc[u][1]);
-            *reinterpret_cast<float2*>(o + 2) = make_float2(oacc[u][2], oacc[u][3]);
+    for (int rt = 0; rt < RT; rt++) {
+        const int row = 16 * rt + col;
+        if (row < QR) {
+            const int m = ONE ? 0 : row / G, gh = ONE ? row : row % G;
+            float* pr = a.part + ((((int64_t)seq * M + m) * a.Hq + kvh * G + gh) * a.NS + split) * (D + 2);
+#pragma unroll
+            for (int u = 0; u < DPW; u++) {
+                if (wave + NWV * u >= 8) break;
+                float* o = pr + 16 * (wave + NWV * u) + 4 * g;
+                *reinterpret_cast<float2*>(o) = make_float2(oacc[u][rt][0], oacc[u][rt][1]);
+                *reinterpret_cast<float2*>(o + 2) = make_float2(oacc[u][rt][2], oacc[u][rt][3]);
+            }
+            if (wave == 0 && g == 0) { pr[D] = stat[row][0]; pr[D + 1] = stat[row][1]; }
         }
-        if (wave == 0 && g == 0) { pr[D] = stat[col][0]; pr[D + 1] = stat[col][1]; }
     }
 }
 
@@ -649,20 +720,41 @@ extern "C" UD_API size_t ud_gqa_workspace_bytes(int32_t n, int32_t q_heads, int3
     return (size_t)n * q_heads * nsplits(max_keys) * (head_dim + 2) * sizeof(float);
 }
 
+// The MFMA split kernel for G query heads per kv head and M queries per sequence: QM query rows
+// (G for one query, else M G rounded up to whole 16-row tiles).
+template <int G>
+static int launch_mfma_g(const GqaArgs& a, dim3 grid, dim3 block, hipStream_t st) {
+    const int rows = a.M * G;
+    if (a.M == 1) { hipLaunchKernelGGL((gqa_split_mfma_kernel<G, G>), grid, block, 0, st, a); return UD_OK; }
+    if (rows <= 16) { hipLaunchKernelGGL((gqa_split_mfma_kernel<G, 16>), grid, block, 0, st, a); return UD_OK; }
+    if constexpr (G >= 4) {
+        if (rows <= 32) { hipLaunchKernelGGL((gqa_split_mfma_kernel<G, 32>), grid, block, 0, st, a); return UD_OK; }
+    }
+    if constexpr (G == 8) {
+        if (rows <= 48) { hipLaunchKernelGGL((gqa_split_mfma_kernel<G, 48>), grid, block, 0, st, a); return UD_OK; }
+        if (rows <= 64) { hipLaunchKernelGGL((gqa_split_mfma_kernel<G, 64>), grid, block, 0, st, a); return UD_OK; }
+    }
+    return UD_ERR_SHAPE;
+}
+
+// Grid of the split kernels: (kv head, split, sequence); the combine runs over the n M (sequence,
+// query) rows, whose ranges, partials and outputs are contiguous in that order.
 template <typename KT, int D>
 static int launch_gqa(const GqaArgs& a, int n, int G, int nsplit, float* out, hipStream_t st) {
     if constexpr (std::is_same<KT, BF16>::value && D == 128) {
         // bf16 pages at head_dim 128: the MFMA split kernel (grid as below)
         dim3 grid(a.Hkv, nsplit, n), block(2 * MSPLIT);
+        int rc;
         switch (G) {
-            case 1: hipLaunchKernelGGL((gqa_split_mfma_kernel<1>), grid, block, 0, st, a); break;
-            case 2: hipLaunchKernelGGL((gqa_split_mfma_kernel<2>), grid, block, 0, st, a); break;
-            case 4: hipLaunchKernelGGL((gqa_split_mfma_kernel<4>), grid, block, 0, st, a); break;
-            case 8: hipLaunchKernelGGL((gqa_split_mfma_kernel<8>), grid, block, 0, st, a); break;
+            case 1: rc = launch_mfma_g<1>(a, grid, block, st); break;
+            case 2: rc = launch_mfma_g<2>(a, grid, block, st); break;
+            case 4: rc = launch_mfma_g<4>(a, grid, block, st); break;
+            case 8: rc = launch_mfma_g<8>(a, grid, block, st); break;
             default: return UD_ERR_SHAPE;
         }
-        hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n), dim3(64), 0, st, a.part, a.ranges, out, a.Hq, a.NS, a.kmax,
-                           MSPLIT);
+        if (rc != UD_OK) return rc;
+        hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n * a.M), dim3(64), 0, st, a.part, a.ranges, out, a.Hq,
+                           a.NS, a.kmax, MSPLIT);
         return UD_OK;
     }
     // kv head fastest: the Hkv workgroups of one split run side by side and read each physical page's
@@ -677,18 +769,19 @@ static int launch_gqa(const GqaArgs& a, int n, int G, int nsplit, float* out, hi
         case 8: hipLaunchKernelGGL((gqa_split_kernel<KT, D, 8>), grid, block, 0, st, a); break;
         default: return UD_ERR_SHAPE;
     }
-    hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n), dim3(64), 0, st, a.part, a.ranges, out, a.Hq, a.NS, a.kmax,
-                       SPLIT);
+    hipLaunchKernelGGL((gqa_combine_kernel<D>), dim3(a.Hq, n * a.M), dim3(64), 0, st, a.part, a.ranges, out, a.Hq, a.NS,
+                       a.kmax, SPLIT);
     return UD_OK;
 }
 
 // Argument checks shared by both decode entry points (everything but the workspace).
 static int gqa_check(const char* who, int32_t kv_dtype, const float* q_dev, const void* k_pages, const void* v_pages,
                      const int32_t* block_table, int32_t max_blocks, const int32_t* ranges_dev, const float* out_dev,
-                     int32_t n, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t block_size,
-                     int32_t max_keys) {
+                     int32_t n, int32_t n_queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                     int32_t block_size, int32_t max_keys) {
     if (!q_dev || !k_pages || !v_pages || !block_table || !ranges_dev || !out_dev)
         return dfail(UD_ERR_INVALID, "%s: null pointer", who);
+    if (n_queries < 1 || n_queries > 8) return dfail(UD_ERR_SHAPE, "%s: %d queries per sequence (1 .. 8)", who, n_queries);
     if (kv_dtype != UD_BF16 && kv_dtype != UD_F16) return dfail(UD_ERR_INVALID, "%s: kv dtype %d", who, kv_dtype);
     if (n < 1 || q_heads < 1 || kv_heads < 1 || q_heads % kv_heads)
         return dfail(UD_ERR_SHAPE, "%s: heads %d/%d, n %d", who, q_heads, kv_heads, n);
@@ -698,10 +791,11 @@ static int gqa_check(const char* who, int32_t kv_dtype, const float* q_dev, cons
     if (block_size != PAGE) return dfail(UD_ERR_SHAPE, "%s: block_size %d (16 supported)", who, block_size);
     if (max_blocks < 1 || max_keys < 0 || max_keys > max_blocks * PAGE)
         return dfail(UD_ERR_SHAPE, "%s: max_keys %d beyond %d blocks", who, max_keys, max_blocks);
-    // grid y (splits) and z (sequences) hold at most 65535 workgroups
-    if (n > 65535 || nsplits(max_keys) > 65535)
-        return dfail(UD_ERR_SHAPE, "%s: n %d or max_keys %d beyond the grid (65535 sequences, 65535 x %d keys)", who,
-                     n, max_keys, SPLIT);
+    // grid y (splits) and z (sequences) of the split kernels, and y (sequence x query rows) of the
+    // combine, hold at most 65535 workgroups
+    if ((int64_t)n * n_queries > 65535 || nsplits(max_keys) > 65535)
+        return dfail(UD_ERR_SHAPE, "%s: n %d x %d queries or max_keys %d beyond the grid (65535 rows, 65535 x %d keys)",
+                     who, n, n_queries, max_keys, SPLIT);
     if (((uintptr_t)q_dev | (uintptr_t)k_pages | (uintptr_t)v_pages) & 15)
         return dfail(UD_ERR_INVALID, "%s: buffers must be 16-byte aligned", who);
     return UD_OK;
@@ -710,12 +804,13 @@ static int gqa_check(const char* who, int32_t kv_dtype, const float* q_dev, cons
 // Launches split + combine with `workspace` as the split partials (checked by the caller).
 static int gqa_launch(const char* who, int32_t kv_dtype, const float* q_dev, const void* k_pages, const void* v_pages,
                       const int32_t* block_table, int32_t max_blocks, const int32_t* ranges_dev, float* out_dev,
-                      int32_t n, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t max_keys,
-                      float* workspace, hipStream_t st) {
+                      int32_t n, int32_t n_queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                      int32_t max_keys, float* workspace, hipStream_t st) {
     const int G = q_heads / kv_heads;
     GqaArgs a{};
     a.q = q_dev; a.kp = k_pages; a.vp = v_pages; a.bt = block_table; a.ranges = ranges_dev;
     a.part = workspace;
+    a.M = n_queries;
     // keys per split: MSPLIT on the MFMA path (bf16 pages, head_dim 128), SPLIT otherwise; the
     // workspace is sized for SPLIT, the smaller, so it holds either
     const int sp = kv_dtype == UD_BF16 && head_dim == 128 ? MSPLIT : SPLIT;
@@ -738,17 +833,28 @@ extern "C" UD_API int ud_gqa_attention_paged(int32_t kv_dtype, const float* q_de
                                              const int32_t* ranges_dev, float* out_dev, int32_t n, int32_t q_heads,
                                              int32_t kv_heads, int32_t head_dim, int32_t block_size, int32_t max_keys,
                                              void* workspace, size_t workspace_bytes, void* hip_stream) {
-    static const char* who = "ud_gqa_attention_paged";
-    int rc = gqa_check(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, q_heads,
-                       kv_heads, head_dim, block_size, max_keys);
+    return ud_gqa_attention_paged_mq(kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n,
+                                     1, q_heads, kv_heads, head_dim, block_size, max_keys, workspace, workspace_bytes,
+                                     hip_stream);
+}
+
+extern "C" UD_API int ud_gqa_attention_paged_mq(int32_t kv_dtype, const float* q_dev, const void* k_pages,
+                                                const void* v_pages, const int32_t* block_table, int32_t max_blocks,
+                                                const int32_t* ranges_dev, float* out_dev, int32_t n, int32_t n_queries,
+                                                int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t block_size,
+                                                int32_t max_keys, void* workspace, size_t workspace_bytes,
+                                                void* hip_stream) {
+    const char* who = n_queries == 1 ? "ud_gqa_attention_paged" : "ud_gqa_attention_paged_mq";
+    int rc = gqa_check(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n,
+                       n_queries, q_heads, kv_heads, head_dim, block_size, max_keys);
     if (rc != UD_OK) return rc;
+    const size_t need = ud_gqa_workspace_bytes(n * n_queries, q_heads, head_dim, max_keys);
     if (!workspace) return dfail(UD_ERR_INVALID, "%s: null workspace", who);
-    if (workspace_bytes < ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys))
-        return dfail(UD_ERR_SHAPE, "%s: workspace %zu < %zu bytes", who, workspace_bytes,
-                     ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys));
+    if (workspace_bytes < need) return dfail(UD_ERR_SHAPE, "%s: workspace %zu < %zu bytes", who, workspace_bytes, need);
     if ((uintptr_t)workspace & 15) return dfail(UD_ERR_INVALID, "%s: workspace must be 16-byte aligned", who);
-    return gqa_launch(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, q_heads,
-                      kv_heads, head_dim, max_keys, static_cast<float*>(workspace), static_cast<hipStream_t>(hip_stream));
+    return gqa_launch(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, n_queries,
+                      q_heads, kv_heads, head_dim, max_keys, static_cast<float*>(workspace),
+                      static_cast<hipStream_t>(hip_stream));
 }
 
 // ---------------------------------------------------------------- allocation-free variant
@@ -789,8 +895,8 @@ extern "C" UD_API int ud_gqa_attention_paged_noalloc(int32_t kv_dtype, const flo
                                                      int32_t n, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
                                                      int32_t block_size, int32_t max_keys, void* hip_stream) {
     static const char* who = "ud_gqa_attention_paged_noalloc";
-    int rc = gqa_check(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, q_heads,
-                       kv_heads, head_dim, block_size, max_keys);
+    int rc = gqa_check(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, 1,
+                       q_heads, kv_heads, head_dim, block_size, max_keys);
     if (rc != UD_OK) return rc;
     const size_t need = ud_gqa_workspace_bytes(n, q_heads, head_dim, max_keys);
     if (need > (size_t)UD_GQA_NOALLOC_SCRATCH_BYTES)
@@ -799,7 +905,7 @@ extern "C" UD_API int ud_gqa_attention_paged_noalloc(int32_t kv_dtype, const flo
                      "workspace", who, n, q_heads, max_keys, need, (size_t)UD_GQA_NOALLOC_SCRATCH_BYTES);
     float* ws = nullptr;
     if ((rc = scratch_of_current_device(who, &ws)) != UD_OK) return rc;
-    return gqa_launch(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, q_heads,
+    return gqa_launch(who, kv_dtype, q_dev, k_pages, v_pages, block_table, max_blocks, ranges_dev, out_dev, n, 1, q_heads,
                       kv_heads, head_dim, max_keys, ws, static_cast<hipStream_t>(hip_stream));
 }
 
