@@ -275,7 +275,7 @@ def decode_bench(ud, args, summary=False, steps=None, warmup=None, workload="dec
                    "total_keys": int(lens.sum())},
         "roofline": {"kernel": "gqa_split_mfma_kernel + gqa_combine_kernel (timed together)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("gqa_decode"),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic("gqa_decode" if M == 1 else "gqa_decode_mq"),
                      "algorithmic_bytes_per_launch": algo},
     }
     if not args.no_cpu_baseline:

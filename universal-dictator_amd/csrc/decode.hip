@@ -391,9 +391,10 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
     const int s0 = split * KS;
     const int klo = max(lo, s0), khi = min(hi, s0 + KS);
     if (klo >= khi) return;                       // this split holds no key of any query's range
+    constexpr int PROW = KS * 2 + 16;             // bytes per probability row (bf16, padded by 16 bytes)
     __shared__ __align__(16) char kv[KS * ROWB];         // K, then V
-    __shared__ __align__(16) float sc[QM][KS];
-    __shared__ float stat[QM][2];
+    __shared__ __align__(16) char pl[QM * PROW];         // probabilities, bf16 [row][key]
+    __shared__ float pmax[NWV][QM], psum[NWV][QM];       // per wave: row maxima, row sums of its 32 keys
     __shared__ int2 qrng[ONE ? 1 : 8];            // each query's range clipped to the split
     if (!ONE && tid < M) qrng[tid] = make_int2(max(max(rg[2 * tid], 0), s0), min(min(rg[2 * tid + 1], a.kmax), s0 + KS));
 
@@ -463,7 +464,9 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
         }
     __syncthreads();
 
-    // ---- scores of the wave's keys 32w + 16t + c -> sc (keys outside a row's range -inf)
+    // ---- scores of the wave's keys 32w + 16t + c, in registers: sv[rt][t][i] is row 16 rt + 4g + i
+    //      (-inf outside the row's range, and for padding rows)
+    float sv[RT][2][4];
 #pragma unroll
     for (int t = 0; t < 2; t++) {
         const int r = 32 * wave + 16 * t + col;
@@ -483,19 +486,26 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int row = 16 * rt + 4 * g + i;
-                if (row < QR) {
-                    bool in;
-                    if constexpr (ONE) {
-                        in = j >= klo && j < khi;
-                    } else {
-                        const int2 qq = qrng[row / G];
-                        in = j >= qq.x && j < qq.y;
-                    }
-                    sc[row][r] = in ? acc[rt][i] * a.scale : -INFINITY;
+                bool in;
+                if constexpr (ONE) {
+                    in = row < QR && j >= klo && j < khi;
+                } else {
+                    const int2 qq = qrng[min(row, QR - 1) / G];
+                    in = row < QR && j >= qq.x && j < qq.y;
                 }
+                sv[rt][t][i] = in ? acc[rt][i] * a.scale : -INFINITY;
             }
     }
-    __syncthreads();                              // every wave has read K
+    // the wave's row maxima over its 32 keys (the 16 lanes of a row group hold one key each)
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = 16 * rt + 4 * g + i;
+            const float m = group_max<16>(fmaxf(sv[rt][0][i], sv[rt][1][i]));
+            if (col == 0 && row < QM) pmax[wave][row] = m;
+        }
+    __syncthreads();                              // every wave has read K and posted its maxima
 
     // ---- V over K in LDS, where the direct loads put K (rows outside the span zeroed)
 #pragma unroll
@@ -507,24 +517,26 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
             *reinterpret_cast<uint4*>(kv + (32 * wave + 16 * e + 4 * i) * ROWB + 16 * lane) = v;
         }
 
-    // ---- softmax of the split, one wave per row: probabilities in sc, (max, sum) in stat; a row
-    //      with no key in the split gets max -inf and sum 0 (never read by the combine)
-    for (int gh = wave; gh < QR; gh += NWV) {
-        float v[KS / 64];
-        float m = -INFINITY;
+    // ---- softmax of the split from registers: probabilities exp(s - row max) rounded to bf16 into
+    //      pl, the wave's row sums into psum (a row with no key in the split: max -inf, all 0)
 #pragma unroll
-        for (int k = 0; k < KS / 64; k++) { v[k] = sc[gh][lane + 64 * k]; m = fmaxf(m, v[k]); }
-        m = wave_max(m);
-        float l = 0.0f;
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-        for (int k = 0; k < KS / 64; k++) {
-            v[k] = v[k] == -INFINITY ? 0.0f : __expf(v[k] - m);
-            l += v[k];
-            sc[gh][lane + 64 * k] = v[k];
+        for (int i = 0; i < 4; i++) {
+            const int row = 16 * rt + 4 * g + i, rr = min(row, QM - 1);
+            float m = pmax[0][rr];
+#pragma unroll
+            for (int w = 1; w < NWV; w++) m = fmaxf(m, pmax[w][rr]);
+            float l = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const float pv = sv[rt][t][i] == -INFINITY ? 0.0f : __expf(sv[rt][t][i] - m);
+                l += pv;
+                if (row < QM) *reinterpret_cast<uint16_t*>(pl + row * PROW + (32 * wave + 16 * t + col) * 2) = f2bf(pv);
+            }
+            l = group_sum<16>(l);
+            if (col == 0 && row < QM) psum[wave][row] = l;
         }
-        l = wave_sum(l);
-        if (lane == 0) { stat[gh][0] = m; stat[gh][1] = l; }
-    }
     __syncthreads();
 
     // ---- out^T += V^T . P^T per 32-key piece kk.  B (tile rt): lane (c, g) holds row 16 rt + c's
@@ -542,12 +554,10 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
         uint4 pb[RT];
 #pragma unroll
         for (int rt = 0; rt < RT; rt++) {
-            const int hc = min(16 * rt + col, QR - 1);
-            const float4 p0 = *reinterpret_cast<const float4*>(&sc[hc][32 * kk + 4 * g]);
-            const float4 p1 = *reinterpret_cast<const float4*>(&sc[hc][32 * kk + 16 + 4 * g]);
-            pb[rt] = 16 * rt + col < QR ? make_uint4(pack_bf16x2(p0.x, p0.y), pack_bf16x2(p0.z, p0.w),
-                                                     pack_bf16x2(p1.x, p1.y), pack_bf16x2(p1.z, p1.w))
-                                        : make_uint4(0, 0, 0, 0);
+            const char* pr = pl + min(16 * rt + col, QM - 1) * PROW + (32 * kk + 4 * g) * 2;
+            const uint2 p0 = *reinterpret_cast<const uint2*>(pr);           // keys 32kk + 4g .. + 3
+            const uint2 p1 = *reinterpret_cast<const uint2*>(pr + 32);      // 16 keys on
+            pb[rt] = 16 * rt + col < QR ? make_uint4(p0.x, p0.y, p1.x, p1.y) : make_uint4(0, 0, 0, 0);
         }
         const int k0 = 32 * kk + 4 * g + (col >> 2);
 #pragma unroll
@@ -567,7 +577,7 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
     }
 
     // ---- partial of row 16 rt + c (query m, head gh): out^T lane (c, g) holds channels
-    //      16dt + 4g .. + 3; (max, sum) from stat
+    //      16dt + 4g .. + 3; (max, sum) from the waves' row maxima and sums
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
         const int row = 16 * rt + col;
@@ -581,7 +591,13 @@ __global__ __launch_bounds__(2 * MSPLIT) void gqa_split_mfma_kernel(GqaArgs a) {
                 *reinterpret_cast<float2*>(o) = make_float2(oacc[u][rt][0], oacc[u][rt][1]);
                 *reinterpret_cast<float2*>(o + 2) = make_float2(oacc[u][rt][2], oacc[u][rt][3]);
             }
-            if (wave == 0 && g == 0) { pr[D] = stat[row][0]; pr[D + 1] = stat[row][1]; }
+            if (wave == 0 && g == 0) {
+                float m = pmax[0][row], l = psum[0][row];
+#pragma unroll
+                for (int w = 1; w < NWV; w++) { m = fmaxf(m, pmax[w][row]); l += psum[w][row]; }
+                pr[D] = m;
+                pr[D + 1] = l;
+            }
         }
     }
 }
