@@ -254,28 +254,31 @@ __device__ __forceinline__ float act_fast(float x) {
     else return apply_act(x, ACT);
 }
 
-// Waves form a 2 x 4 grid; each owns 128 x 16*NT (NT = 4: 128 pinned accumulator registers;
-// with about 120 vector registers two waves fit per SIMD).  Narrower tiles (NT 3, 2) give more
+// Waves form a 2 x 4 grid; each owns 16*MT x 16*NT (AB = 16: 256-row tiles, 128 x 16*NT per wave,
+// NT = 4: 128 pinned accumulator registers; with about 120 vector registers two waves fit per
+// SIMD).  Narrower tiles (NT 3, 2) and 128-row tiles (AB = 8, 64 rows per wave) give more
 // workgroups where 256 x 256 tiles would leave CUs idle.  The MFMA operands are swapped (weights as
 // the row operand), so each 16 x 16 accumulator holds C^T: a lane has 4 consecutive output columns
 // of one row, and the epilogue writes 16 bytes (fp32) or 8 bytes (bf16, row-major or
 // fragment-major) per lane.
-template <int NT, int EPI, int ACT, bool H = false, bool BIAS = false>
+template <int NT, int EPI, int ACT, bool H = false, bool BIAS = false, int AB = 16>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
-    constexpr int MT = 8, BB = 4 * NT;                       // W blocks (16 columns each) per tile
-    constexpr int NBLK = 16 + BB;                            // 1 KB half-blocks per 32-deep K step
+    static_assert(AB == 16 || AB == 8, "256- or 128-row tiles");
+    constexpr int MT = AB / 2, BB = 4 * NT;                  // wave row tiles; W blocks (16 columns each) per tile
+    constexpr int TR = 16 * AB;                              // tile rows
+    constexpr int NBLK = AB + BB;                            // 1 KB half-blocks per 32-deep K step
     constexpr int STAGE = NBLK * 512;                        // halves per LDS stage
     constexpr int CPS = (NBLK + 7) / 8, CMIN = NBLK / 8;     // direct loads per wave per step (max, min)
     __shared__ __attribute__((aligned(16))) bf16 st0[STAGE];
     __shared__ __attribute__((aligned(16))) bf16 st1[STAGE];
     __shared__ __attribute__((aligned(16))) bf16 st2[STAGE];
     __shared__ __attribute__((aligned(16))) bf16 st3[STAGE];
-    __shared__ __attribute__((aligned(16))) int32_t rtab[EPI == EPI_QKV_RING ? 256 : 4];   // QKV: ring row offsets
+    __shared__ __attribute__((aligned(16))) int32_t rtab[EPI == EPI_QKV_RING ? TR : 4];    // QKV: ring row offsets
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3;
     const int r16 = lane & 15, g = lane >> 4;
-    const int nN = a.N / (64 * NT), nM = (a.M + 255) / 256;
+    const int nN = a.N / (64 * NT), nM = (a.M + TR - 1) / TR;
     const int ks = a.ksplit;
     const int t = xcd_tile(blockIdx.x, nN * nM * ks);
     const int kz = t % ks, tile = t / ks;
@@ -286,14 +289,14 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
     const bf16* A = static_cast<const bf16*>(a.A);
     const bf16* W = static_cast<const bf16*>(a.W);
 
-    // Wave w copies the 1 KB half-blocks u = w + 8j of each step: A's row tiles for u < 16, then W's.
+    // Wave w copies the 1 KB half-blocks u = w + 8j of each step: A's row tiles for u < AB, then W's.
     int soff[CPS];
 #pragma unroll
     for (int j = 0; j < CPS; j++) {
         const int u = wave + 8 * j;
         int o = 0;
-        if (u < 16) o = (min(mb * 16 + u, rtiles - 1) * nk + kc0) << 10;     // clamped rows: not stored
-        else if (u < NBLK) o = ((nb * BB + u - 16) * nk + kc0) << 10;
+        if (u < AB) o = (min(mb * AB + u, rtiles - 1) * nk + kc0) << 10;     // clamped rows: not stored
+        else if (u < NBLK) o = ((nb * BB + u - AB) * nk + kc0) << 10;
         soff[j] = o;
     }
     const int lo = lane * 8;
@@ -302,7 +305,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < CPS; j++) {
             const int u = wave + 8 * j;
-            if (j < CMIN || u < NBLK) lds_direct16((u < 16 ? A : W) + soff[j] + kofs + lo, dst + u * 512);
+            if (j < CMIN || u < NBLK) lds_direct16((u < AB ? A : W) + soff[j] + kofs + lo, dst + u * 512);
         }
     };
 
@@ -312,7 +315,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < MT; i++) acc[j][i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int aoff = (wm * MT) * 512 + lo, boff = (16 + wn * NT) * 512 + lo;
+    const int aoff = (wm * MT) * 512 + lo, boff = (AB + wn * NT) * 512 + lo;
     uint4 fa[MT], fb[NT];
     auto read_step = [&](const bf16* buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -332,9 +335,9 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
                     asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
                                  : "+a"(acc[j][i]) : "v"(as_bf16x8(fb[j])), "v"(as_bf16x8(fa[i])));
     };
-    // QKV split store: the ring offsets of the tile's 256 rows (the table is padded past the last row)
+    // QKV split store: the ring offsets of the tile's TR rows (the table is padded past the last row)
     if constexpr (EPI == EPI_QKV_RING) {
-        if (wave == 0) lds_direct16_rows(a.ring.rows + mb * 256 + 4 * lane, rtab);
+        if (wave == 0 && lane < TR / 4) lds_direct16_rows(a.ring.rows + mb * TR + 4 * lane, rtab);
     }
     // Four-stage ring of 32-deep K steps: steps s+1, s+2 (and the loads of s+3, issued at the start
     // of step s into the stage step s-1 used) are in flight while step s is multiplied.
@@ -370,7 +373,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
     // 4 columns 16*ct + 4*g + e (e < 4).
 #pragma unroll
     for (int i = 0; i < MT; i++) {
-        const int64_t m = (int64_t)(mb * 16 + wm * MT + i) * 16 + r16;
+        const int64_t m = (int64_t)(mb * AB + wm * MT + i) * 16 + r16;
         if (m >= a.M) continue;
 #pragma unroll
         for (int j = 0; j < NT; j++) {
@@ -572,35 +575,35 @@ static int launch_bf16_cfg(GemmArgs a, int ksplit, hipStream_t st) {
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-template <int NT, int EPI, int ACT, bool H = false, bool BIAS = false>
+template <int NT, int EPI, int ACT, bool H = false, bool BIAS = false, int AB = 16>
 static int launch_lds_cfg(GemmArgs a, int ksplit, hipStream_t st) {
     if (a.N % (64 * NT) != 0 || ksplit < 1 || a.K % (64 * ksplit) != 0 || a.ldc % 4 != 0) return -2;
     if (ksplit > 1 && EPI != EPI_PARTIAL) return -2;
     if ((int64_t)((a.M + 15) / 16) * a.K * 16 >= (1ll << 31) || (int64_t)a.N * a.K >= (1ll << 31)) return -2;
     a.ksplit = ksplit;
-    const int tiles = (a.N / (64 * NT)) * ((a.M + 255) / 256) * ksplit;
-    hipLaunchKernelGGL((gemm_bf16_lds_kernel<NT, EPI, ACT, H, BIAS>), dim3(tiles), dim3(512), 0, st, a);
+    const int tiles = (a.N / (64 * NT)) * ((a.M + 16 * AB - 1) / (16 * AB)) * ksplit;
+    hipLaunchKernelGGL((gemm_bf16_lds_kernel<NT, EPI, ACT, H, BIAS, AB>), dim3(tiles), dim3(512), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-template <int NT, int EPI, bool H>
+template <int NT, int EPI, bool H, int AB>
 static int launch_lds_epi(const GemmArgs& a, int ks, hipStream_t st) {
     switch (a.act) {
-        case ACT_NONE: return launch_lds_cfg<NT, EPI, ACT_NONE, H>(a, ks, st);
-        case ACT_SILU: return launch_lds_cfg<NT, EPI, ACT_SILU, H>(a, ks, st);
-        case ACT_RELU: return launch_lds_cfg<NT, EPI, ACT_RELU, H>(a, ks, st);
+        case ACT_NONE: return launch_lds_cfg<NT, EPI, ACT_NONE, H, false, AB>(a, ks, st);
+        case ACT_SILU: return launch_lds_cfg<NT, EPI, ACT_SILU, H, false, AB>(a, ks, st);
+        case ACT_RELU: return launch_lds_cfg<NT, EPI, ACT_RELU, H, false, AB>(a, ks, st);
         default: return -2;
     }
 }
 
-template <int NT, bool H>
+template <int NT, bool H, int AB>
 static int launch_lds_act(const GemmArgs& a, int ks, hipStream_t st) {
     switch (a.epi) {
-        case EPI_PARTIAL: return a.act == ACT_NONE ? launch_lds_cfg<NT, EPI_PARTIAL, ACT_NONE, H>(a, ks, st) : -2;
-        case EPI_STORE_F32: return launch_lds_epi<NT, EPI_STORE_F32, H>(a, ks, st);
-        case EPI_STORE_FRAG: return launch_lds_epi<NT, EPI_STORE_FRAG, H>(a, ks, st);
-        case EPI_STORE: return launch_lds_epi<NT, EPI_STORE, H>(a, ks, st);
-        case EPI_QKV_RING: return launch_lds_cfg<NT, EPI_QKV_RING, ACT_NONE, H>(a, ks, st);
+        case EPI_PARTIAL: return a.act == ACT_NONE ? launch_lds_cfg<NT, EPI_PARTIAL, ACT_NONE, H, false, AB>(a, ks, st) : -2;
+        case EPI_STORE_F32: return launch_lds_epi<NT, EPI_STORE_F32, H, AB>(a, ks, st);
+        case EPI_STORE_FRAG: return launch_lds_epi<NT, EPI_STORE_FRAG, H, AB>(a, ks, st);
+        case EPI_STORE: return launch_lds_epi<NT, EPI_STORE, H, AB>(a, ks, st);
+        case EPI_QKV_RING: return launch_lds_cfg<NT, EPI_QKV_RING, ACT_NONE, H, false, AB>(a, ks, st);
         default: return -2;
     }
 }
@@ -617,30 +620,40 @@ static int device_cus() {
     return cus;
 }
 
-// Tile width (NT: 64*NT columns) and K splits of the LDS-staged kernel for one projection.  Cost
-// model: rounds of workgroups over the CUs x the per-workgroup MFMA work, scaled by the per-flop cost
-// measured on MI355X for each width (NT 4: 1.00, 3: 1.28, 2: 1.36 at 3584 rows), plus for K splits
-// the fp32 partial slabs they write and the LayerNorm after them reads back (900 units per slab per
-// 3584 x 1024 outputs: a slab's stores come at the end of the one round of workgroups, where
-// nothing hides them, about 2-3 us, and its read in the LayerNorm about 2.5 us).  Choices at 3584
-// rows: N 4096 -> NT 4; N 3072 -> NT 3; N 2048 -> NT 2; N 1024, K 4096 -> NT 2 with 2 splits; N 1024,
-// K 1024 -> NT 2, no split (the step ran 8.38 ms with 4 and 2 splits there, 8.29 ms with these).
-BigTile big_tile(int M, int N, int K, bool partial) {
-    static const double cost_nt[5] = {0.0, 0.0, 1.36, 1.28, 1.0};
+// Tile shape (256 or 128 rows, NT: 64*NT columns) and K splits of the LDS-staged kernel for one
+// projection.  Cost model: rounds of workgroups over the CUs (the wave quantisation: a second,
+// partly filled round costs a whole round) x the per-workgroup MFMA work, scaled by the per-flop
+// cost of each tile shape (256 rows: NT 4 1.00, 3 1.28, 2 1.36, measured at 3584 rows; 128 rows:
+// 2.0), plus for K splits the fp32 partial slabs they write and the LayerNorm after them reads
+// back (900 units per slab per 3584 x 1024 outputs: a slab's stores come at the end of the one
+// round of workgroups, where nothing hides them, about 2-3 us, and its read in the LayerNorm
+// about 2.5 us).
+// A 128-row tile re-reads each weight panel twice as often as a 256-row one.  Measured on the
+// 24-layer config-3 step (256 streams x 14 frames, eager launches, all choices in one process):
+// 8.409 ms with 256-row tiles everywhere; 8.218 ms with linear_out and pointwise_conv2 on 128 x 128
+// tiles (224 workgroups instead of 112 on 256 CUs: 19.7 -> 14.5 us each); 8.209 ms with the
+// subsampling's out projection too; worse with 128-row tiles for q/k/v (+0.134 ms),
+// pointwise_conv1 (+0.126 ms) or ff linear2 (+0.05 ms with 2 splits, more without), which already
+// launch 224 256-row workgroups.  The 128-row cost of 2.0 makes 128-row tiles win only where
+// 256-row tiles leave about half the CUs idle, which is what those runs show.
+BigTile big_tile(int M, int N, int K, bool partial, bool rows128) {
+    static const double cost_256[5] = {0.0, 0.0, 1.36, 1.28, 1.0};
+    static const double cost_128[5] = {0.0, 0.0, 2.0, 2.0, 2.0};
     const int cus = device_cus();
-    BigTile best{0, 1};
+    BigTile best{0, 1, 16};
     double best_cost = 1e300;
-    for (int nt = 4; nt >= 2; nt--) {
-        if (N % (64 * nt) != 0) continue;
-        for (int ks = 1; ks <= (partial ? 4 : 1); ks *= 2) {
-            if (K % (64 * ks) != 0 || (ks > 1 && K / ks < 256)) continue;
-            const long tiles = (long)(N / (64 * nt)) * ((M + 255) / 256) * ks;
-            const long rounds = (tiles + cus - 1) / cus;
-            double cost = (double)rounds * nt * (K / ks) * cost_nt[nt];
-            if (ks > 1) cost += 900.0 * ks * ((double)M * N / (3584.0 * 1024.0));
-            if (cost < best_cost) { best_cost = cost; best = BigTile{nt, ks}; }
+    for (int ab = 16; ab >= (rows128 ? 8 : 16); ab /= 2)
+        for (int nt = 4; nt >= 2; nt--) {
+            if (N % (64 * nt) != 0) continue;
+            for (int ks = 1; ks <= (partial ? 4 : 1); ks *= 2) {
+                if (K % (64 * ks) != 0 || (ks > 1 && K / ks < 256)) continue;
+                const long tiles = (long)(N / (64 * nt)) * ((M + 16 * ab - 1) / (16 * ab)) * ks;
+                const long rounds = (tiles + cus - 1) / cus;
+                double cost = (double)rounds * (ab / 16.0) * nt * (K / ks) * (ab == 16 ? cost_256[nt] : cost_128[nt]);
+                if (ks > 1) cost += 900.0 * ks * ((double)M * N / (3584.0 * 1024.0));
+                if (cost < best_cost) { best_cost = cost; best = BigTile{nt, ks, ab}; }
+            }
         }
-    }
     return best;
 }
 
@@ -682,10 +695,21 @@ static int launch_f16(const GemmArgs& a, hipStream_t st) {
     // The LDS kernel's 256-row tiles leave most CUs idle below ~64 tiles (the second pointwise conv
     // of 64 streams x 160 ms: 4,352 x 256 x 256, 34 tiles, 10.5 us; the register kernel's 64 x 32
     // tiles 6.6 us).
-    const int nt = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false).nt : 0;
-    if (nt != 0 && (int64_t)((a.M + 255) / 256) * (a.N / (64 * nt)) < 64 && a.N % 32 == 0 && a.K % 128 == 0)
+    // the register kernel where 256-row tiles would give fewer than 64 workgroups
+    const BigTile b256 = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false, false) : BigTile{0, 1, 16};
+    if (b256.nt != 0 && (int64_t)((a.M + 255) / 256) * (a.N / (64 * b256.nt)) < 64 && a.N % 32 == 0 && a.K % 128 == 0)
         return launch_bf16_cfg<4, 2, 2, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+    const BigTile bt = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false) : BigTile{0, 1, 16};
+    const int nt = bt.nt;
     if (a.M >= LDS_MIN_ROWS) {
+        if (bt.ab == 8) {
+            switch (nt) {
+                case 4: return launch_lds_cfg<4, EPI_STORE_F32, ACT, true, true, 8>(a, 1, st);
+                case 3: return launch_lds_cfg<3, EPI_STORE_F32, ACT, true, true, 8>(a, 1, st);
+                case 2: return launch_lds_cfg<2, EPI_STORE_F32, ACT, true, true, 8>(a, 1, st);
+                default: break;
+            }
+        }
         switch (nt) {
             case 4: return launch_lds_cfg<4, EPI_STORE_F32, ACT, true, true>(a, 1, st);
             case 3: return launch_lds_cfg<3, EPI_STORE_F32, ACT, true, true>(a, 1, st);
@@ -729,10 +753,17 @@ static int launch_16(const GemmArgs& a, int ks, hipStream_t st) {
     if (a.M >= LDS_MIN_ROWS) {
         const BigTile bt = big_tile(a.M, a.N, a.K, a.epi == EPI_PARTIAL);
         if (bt.nt != 0 && (a.epi != EPI_PARTIAL || bt.ks == ks)) {
+            if (H && bt.ab == 8) {          // 128-row tiles: instantiated for the encoder's half operands
+                switch (bt.nt) {
+                    case 4: return launch_lds_act<4, true, 8>(a, ks, st);
+                    case 3: return launch_lds_act<3, true, 8>(a, ks, st);
+                    default: return launch_lds_act<2, true, 8>(a, ks, st);
+                }
+            }
             switch (bt.nt) {
-                case 4: return launch_lds_act<4, H>(a, ks, st);
-                case 3: return launch_lds_act<3, H>(a, ks, st);
-                default: return launch_lds_act<2, H>(a, ks, st);
+                case 4: return launch_lds_act<4, H, 16>(a, ks, st);
+                case 3: return launch_lds_act<3, H, 16>(a, ks, st);
+                default: return launch_lds_act<2, H, 16>(a, ks, st);
             }
         }
     }
