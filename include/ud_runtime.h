@@ -45,6 +45,18 @@ UD_API int ud_event_record(void* event, void* stream);
 UD_API int ud_event_synchronize(void* event);
 UD_API int ud_event_elapsed_ms(float* ms, void* start, void* stop);
 
+/* Free and total device memory of the current device (hipMemGetInfo). */
+UD_API int ud_mem_get_info(size_t* free_bytes, size_t* total_bytes);
+
+/* Stream capture into a HIP graph, for callers that replay library calls (e.g. the allocation-free
+ * decode entry point): begin capturing `stream` (not the null stream; thread-local capture mode),
+ * end it and instantiate the graph (*graph receives an owned handle), launch it on a stream,
+ * destroy it.  Work enqueued on the stream between begin and end is recorded, not run. */
+UD_API int ud_graph_capture_begin(void* stream);
+UD_API int ud_graph_capture_end(void* stream, void** graph);
+UD_API int ud_graph_launch(void* graph, void* stream);
+UD_API int ud_graph_destroy(void* graph);
+
 /* Measured peaks of the current device, the denominators of measured roofline fractions.  No
  * reference counterpart beyond the same idea: the reference quotes its M3 roofline from its own
  * micro-benchmarks (docs/PERF_LOG.md:7-16: read GB/s, GEMM TFLOPS).

@@ -69,6 +69,38 @@ def test_noalloc_matches_workspace_entry_twice(gpu):
     np.testing.assert_array_equal(_run(ud, big, True), ref1)
 
 
+def test_noalloc_allocates_nothing_and_replays_from_a_graph(gpu):
+    """What the entry point is for: after one warm-up call on a stream, a second call there leaves
+    the device's free memory unchanged (hipMemGetInfo before and after), and the call captured into
+    a HIP graph replays to the eager result -- three replays, each after the output is overwritten
+    and after a different eager call has reused the shared scratch."""
+    ud = gpu
+    rng = np.random.default_rng(20261203)
+    c = _case(ud, rng, 16, 32, 8, 128, 512, 4096, "bf16")
+    other = _case(ud, rng, 3, 8, 2, 64, 1, 500, "f16")
+    ref = _run(ud, c, False)
+    hs = ud.HipStream()
+    out = ud.DeviceBuffer(c["n"] * c["Hq"] * c["d"] * 4)
+    args = (c["q"], c["kp"], c["vp"], c["table"], c["max_blocks"], c["ranges"], out, c["n"], c["Hq"], c["Hkv"],
+            c["d"], c["max_keys"])
+    ud.gqa_attention_paged_noalloc(*args, kv_dtype="bf16", hip_stream=hs)       # warm-up on this stream
+    hs.synchronize()
+    free0, _ = ud.mem_get_info()
+    ud.gqa_attention_paged_noalloc(*args, kv_dtype="bf16", hip_stream=hs)
+    hs.synchronize()
+    free1, _ = ud.mem_get_info()
+    assert free1 == free0, "free device memory changed by %d bytes" % (free0 - free1)
+    np.testing.assert_array_equal(out.download(ref.shape), ref)
+    with ud.Graph.capture(hs) as g:
+        ud.gqa_attention_paged_noalloc(*args, kv_dtype="bf16", hip_stream=hs)
+    for r in range(3):
+        ud.lib().ud_memset(out.ptr, 0xFF, out.nbytes)                           # NaN bit patterns
+        _run(ud, other, True)                                                   # the scratch reused eagerly
+        g.launch(hs)
+        hs.synchronize()
+        np.testing.assert_array_equal(out.download(ref.shape), ref, err_msg="replay %d" % r)
+
+
 def test_noalloc_refuses_beyond_scratch(gpu):
     """A call whose partials would exceed the static scratch fails with UD_ERR_SHAPE before any
     launch (64 sequences x 32 heads x 8192 keys at head_dim 128 need 65 MiB)."""

@@ -85,6 +85,11 @@ def _sig(lib):
         "ud_memcpy_dtod": (i, [p, p, ctypes.c_size_t]),
         "ud_memset": (i, [p, _i32, ctypes.c_size_t]),
         "ud_device_synchronize": (i, []),
+        "ud_mem_get_info": (i, [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]),
+        "ud_graph_capture_begin": (i, [p]),
+        "ud_graph_capture_end": (i, [p, ctypes.POINTER(_vp)]),
+        "ud_graph_launch": (i, [p, p]),
+        "ud_graph_destroy": (i, [p]),
         "ud_hip_stream_create": (i, [ctypes.POINTER(_vp)]),
         "ud_hip_stream_destroy": (i, [p]),
         "ud_hip_stream_synchronize": (i, [p]),
@@ -191,6 +196,49 @@ def device_arch():
 
 def synchronize():
     _check(lib().ud_device_synchronize())
+
+
+def mem_get_info():
+    """(free, total) bytes of device memory (hipMemGetInfo)."""
+    f, t = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    _check(lib().ud_mem_get_info(ctypes.byref(f), ctypes.byref(t)))
+    return f.value, t.value
+
+
+class Graph:
+    """Work captured from a HipStream into a HIP graph: `with Graph.capture(stream) as g:` records
+    the calls made on that stream inside the block; g.launch(stream) replays them."""
+
+    def __init__(self):
+        self.ptr = None
+
+    @classmethod
+    def capture(cls, stream):
+        g = cls()
+        g._stream = stream
+        return g
+
+    def __enter__(self):
+        _check(lib().ud_graph_capture_begin(self._stream.ptr))
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        p = _vp()
+        rc = _lib.ud_graph_capture_end(self._stream.ptr, ctypes.byref(p))
+        self.ptr = p.value
+        if exc_type is None:
+            _check(rc)
+        return False
+
+    def launch(self, stream):
+        _check(_lib.ud_graph_launch(self.ptr, stream.ptr))
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                _lib.ud_graph_destroy(self.ptr)
+        except Exception:
+            pass
 
 
 # ---------------------------------------------------------------- device memory, streams, events

@@ -102,3 +102,54 @@ extern "C" UD_API int ud_event_elapsed_ms(float* ms, void* start, void* stop) {
     return hip_status(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
                       "hipEventElapsedTime");
 }
+
+extern "C" UD_API int ud_mem_get_info(size_t* free_bytes, size_t* total_bytes) {
+    size_t f = 0, t = 0;
+    hipError_t e = hipMemGetInfo(&f, &t);
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return hip_status(e, "hipMemGetInfo");
+}
+
+// A captured and instantiated graph (ud_graph_capture_end), owned by the caller.
+struct ud_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+extern "C" UD_API int ud_graph_capture_begin(void* stream) {
+    if (!stream) return ud_set_error(UD_ERR_INVALID, "ud_graph_capture_begin: the null stream cannot be captured");
+    return hip_status(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal),
+                      "hipStreamBeginCapture");
+}
+
+extern "C" UD_API int ud_graph_capture_end(void* stream, void** graph) {
+    if (!stream || !graph) return ud_set_error(UD_ERR_INVALID, "ud_graph_capture_end: null argument");
+    *graph = nullptr;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(static_cast<hipStream_t>(stream), &g);
+    if (e != hipSuccess) return hip_status(e, "hipStreamEndCapture");
+    hipGraphExec_t x = nullptr;
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return hip_status(e, "hipGraphInstantiate");
+    }
+    *graph = new ud_graph{g, x};
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_graph_launch(void* graph, void* stream) {
+    if (!graph) return ud_set_error(UD_ERR_INVALID, "ud_graph_launch: null graph");
+    return hip_status(hipGraphLaunch(static_cast<ud_graph*>(graph)->exec, static_cast<hipStream_t>(stream)),
+                      "hipGraphLaunch");
+}
+
+extern "C" UD_API int ud_graph_destroy(void* graph) {
+    if (!graph) return UD_OK;
+    ud_graph* g = static_cast<ud_graph*>(graph);
+    hipError_t e = hipGraphExecDestroy(g->exec);
+    if (e == hipSuccess) e = hipGraphDestroy(g->graph);
+    delete g;
+    return hip_status(e, "hipGraphDestroy");
+}
