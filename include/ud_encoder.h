@@ -274,7 +274,8 @@ typedef enum {
     UD_PROJ_FF_LINEAR2 = 1,   /* feed_forward{1,2}.linear2: N d_model, K ff_dim, x0.5, residual */
     UD_PROJ_QKV = 2,          /* linear_q | linear_k | linear_v: N 3 d_model, K d_model */
     UD_PROJ_LINEAR_OUT = 3,   /* linear_out: N d_model, K d_model, residual */
-    UD_PROJ_PW1 = 4,          /* conv.pointwise_conv1: N 2 d_model, K d_model, fp32 out */
+    UD_PROJ_PW1 = 4,          /* conv.pointwise_conv1: N 2 d_model, K d_model; fp32 value | gate out, or for
+                                 a 16-bit encoder the GLU applied in the epilogue, half out */
     UD_PROJ_PW2 = 5           /* conv.pointwise_conv2: N d_model, K d_model, residual */
 } ud_projection;
 UD_API int ud_time_projection(ud_encoder* enc, int32_t which, int32_t rows, int32_t iters, void* hip_stream,

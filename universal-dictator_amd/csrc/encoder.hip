@@ -514,7 +514,19 @@ extern "C" UD_API int ud_encoder_set_weight(ud_encoder* e, const char* name, con
         case LIN_V: rc = upload_matrix(e, l.wqkv, 2 * D, host, D, D); break;
         case LIN_OUT: rc = upload_matrix(e, l.wo, 0, host, D, D); break;
         case PW2: rc = upload_matrix(e, l.pw2, 0, host, D, D); break;
-        case PW1: rc = upload_matrix(e, l.pw1, 0, host, 2 * D, D); break;
+        case PW1: {
+            if (e->bf) {
+                // GLU-pair row order for the fused GLU epilogue: rows 32k .. 32k+15 the value rows of
+                // channels 16k .. 16k+15, rows 32k+16 .. 32k+31 their gate rows
+                std::vector<float> perm((size_t)2 * D * D);
+                for (int64_t r = 0; r < 2 * D; r++)
+                    memcpy(&perm[(size_t)glu_row((int)r, (int)D) * D], host + r * D, (size_t)D * 4);
+                rc = upload_matrix(e, l.pw1, 0, perm.data(), 2 * D, D);
+            } else {
+                rc = upload_matrix(e, l.pw1, 0, host, 2 * D, D);
+            }
+            break;
+        }
         case LIN_POS: {
             l.wpos.assign(host, host + D * D);
             if (e->bf) for (auto& v : l.wpos) v = host_weight16_value(v, e->wf16);
@@ -833,10 +845,17 @@ static int enqueue_rows(ud_encoder* e, int s0, int n, int T, const float* x, flo
         if ((rc = resid(w.att, l.wo, D, 1.0f, "linear_out"))) return rc;
         // Conv module: res += pw2(silu(LN(dwconv([ring; mask(glu(pw1(z)))]))))
         LAUNCH(launch_layernorm(w.res, take(), l.ln[4], l.ln[5], w.z, bf, M, D, ACT_NONE, st), "layernorm");
-        if ((rc = gemm(w.z, l.pw1, w.pw, 2 * D, D, 2 * D, EPI_STORE_F32, ACT_NONE, 1.0f, "pointwise_conv1")))
+        // 16-bit: the GLU in pointwise_conv1's epilogue (weight rows in GLU-pair order), half rows
+        // [M, D] in the pw buffer; fp32: value | gate rows [M, 2D]
+        if (bf) {
+            if ((rc = gemm(w.z, l.pw1, w.pw, 2 * D, D, D, EPI_GLU, ACT_NONE, 1.0f, "pointwise_conv1 + GLU"))) return rc;
+        } else if ((rc = gemm(w.z, l.pw1, w.pw, 2 * D, D, 2 * D, EPI_STORE_F32, ACT_NONE, 1.0f, "pointwise_conv1"))) {
             return rc;
+        }
         ConvArgs ca{};
-        ca.pw = w.pw; ca.ring = e->cring + (size_t)li * e->cring_layer_elems; ca.w_t = l.dw_t;
+        ca.pw = bf ? nullptr : w.pw;
+        ca.glu = bf ? reinterpret_cast<const uint16_t*>(w.pw) : nullptr;
+        ca.ring = e->cring + (size_t)li * e->cring_layer_elems; ca.w_t = l.dw_t;
         ca.ln_g = l.ln[6]; ca.ln_b = l.ln[7]; ca.z = w.z; ca.desc = w.desc;
         ca.n = n; ca.T = T; ca.D = D; ca.K = e->Kc; ca.z16 = bf;
         LAUNCH(launch_dwconv_ln(ca, st), "depthwise conv");
@@ -1114,7 +1133,9 @@ static int launch_projection(ud_encoder* e, int which, int layer, int M, hipStre
             g.A = e->att; g.W = l.wo; g.N = D; g.K = D;
             break;
         case UD_PROJ_PW1:
-            g.A = e->z; g.W = l.pw1; g.C = e->pw; g.N = 2 * D; g.K = D; g.ldc = 2 * D; g.epi = EPI_STORE_F32;
+            g.A = e->z; g.W = l.pw1; g.C = e->pw; g.N = 2 * D; g.K = D;
+            if (e->bf) { g.ldc = D; g.epi = EPI_GLU; }
+            else { g.ldc = 2 * D; g.epi = EPI_STORE_F32; }
             break;
         case UD_PROJ_PW2:
             g.A = e->z; g.W = l.pw2; g.N = D; g.K = D;

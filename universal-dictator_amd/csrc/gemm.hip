@@ -178,6 +178,41 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
             }
         }
     };
+    // EPI_GLU: accumulators j (values) and j + 1 (gates) of the same 16 channels; the lane's
+    // channel is (nt NT / 2 + j / 2) * 16 + r16
+    auto finish_glu = [&](int j, int mt, const f32x4_t& vv, const f32x4_t& vg) {
+        const int c = (nt * NT / 2 + j / 2) * 16 + r16;
+#pragma unroll
+        for (int i2 = 0; i2 < 4; i2++) {
+            const int64_t m = (int64_t)(mb * MT + mt) * 16 + g * 4 + i2;
+            if (m >= a.M) continue;
+            static_cast<uint16_t*>(a.C)[m * a.ldc + c] = to16<H>(vv[i2] * sigmoidf(vg[i2]));
+        }
+    };
+    if constexpr (EPI == EPI_GLU) {
+        static_assert(NT % 2 == 0, "value and gate tiles in pairs");
+        if constexpr (WK > 1) {
+            __shared__ f32x4_t red[WK][NT][MT][64];
+#pragma unroll
+            for (int j = 0; j < NT; j++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) red[wave][j][mt][lane] = acc[j][mt];
+            __syncthreads();
+            for (int idx = wave; idx < NT / 2 * MT; idx += WK) {
+                const int j = 2 * (idx / MT), mt = idx % MT;
+                f32x4_t vv = red[0][j][mt][lane], vg = red[0][j + 1][mt][lane];
+#pragma unroll
+                for (int w = 1; w < WK; w++) { vv += red[w][j][mt][lane]; vg += red[w][j + 1][mt][lane]; }
+                finish_glu(j, mt, vv, vg);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NT; j += 2)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) finish_glu(j, mt, acc[j][mt], acc[j + 1][mt]);
+        }
+        return;
+    }
     if constexpr (WK > 1) {
         // Every wave parks its partial accumulators in LDS; wave w then finishes the accumulators
         // idx = j*MT + mt with idx % WK == w: the sum of the WK partials in wave order, and the
@@ -371,6 +406,25 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
 
     // acc[j][i] is tile (column tile j, row tile i) transposed: lane holds row 16*rt + r16 and the
     // 4 columns 16*ct + 4*g + e (e < 4).
+    if constexpr (EPI == EPI_GLU) {
+        // column tiles j (values) and j + 1 (gates) of channels 16 ((nb BB + wn NT + j) / 2) ..
+        static_assert(NT % 2 == 0, "value and gate tiles in pairs");
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            const int64_t m = (int64_t)(mb * AB + wm * MT + i) * 16 + r16;
+            if (m >= a.M) continue;
+#pragma unroll
+            for (int j = 0; j < NT; j += 2) {
+                const int c = ((nb * BB + wn * NT + j) / 2) * 16 + g * 4;
+                const f32x4_t vv = acc[j][i], vg = acc[j + 1][i];
+                uint2 o;
+                o.x = (uint32_t)to16<H>(vv[0] * sigmoidf(vg[0])) | ((uint32_t)to16<H>(vv[1] * sigmoidf(vg[1])) << 16);
+                o.y = (uint32_t)to16<H>(vv[2] * sigmoidf(vg[2])) | ((uint32_t)to16<H>(vv[3] * sigmoidf(vg[3])) << 16);
+                *reinterpret_cast<uint2*>(static_cast<bf16*>(a.C) + m * a.ldc + c) = o;
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < MT; i++) {
         const int64_t m = (int64_t)(mb * AB + wm * MT + i) * 16 + r16;
@@ -604,6 +658,9 @@ static int launch_lds_act(const GemmArgs& a, int ks, hipStream_t st) {
         case EPI_STORE_FRAG: return launch_lds_epi<NT, EPI_STORE_FRAG, H, AB>(a, ks, st);
         case EPI_STORE: return launch_lds_epi<NT, EPI_STORE, H, AB>(a, ks, st);
         case EPI_QKV_RING: return launch_lds_cfg<NT, EPI_QKV_RING, ACT_NONE, H, false, AB>(a, ks, st);
+        case EPI_GLU:
+            if constexpr (NT % 2 == 0) return a.act == ACT_NONE ? launch_lds_cfg<NT, EPI_GLU, ACT_NONE, H, false, AB>(a, ks, st) : -2;
+            return -2;
         default: return -2;
     }
 }
@@ -740,6 +797,9 @@ static int launch_16(const GemmArgs& a, int ks, hipStream_t st) {
             case EPI_STORE_F32:
                 if (a.N % 32 == 0 && a.K % 512 == 0) return launch_act<2, 8, 2, EPI_STORE_F32, H>(a, ks, st);
                 break;
+            case EPI_GLU:
+                if (a.K % 512 == 0) return launch_bf16_cfg<2, 8, 2, EPI_GLU, ACT_NONE, H>(a, ks, st);
+                break;
             case EPI_PARTIAL:
                 if (a.act != ACT_NONE) return -2;
                 if (a.N % 32 == 0 && a.K % (512 * ks) == 0)
@@ -752,7 +812,7 @@ static int launch_16(const GemmArgs& a, int ks, hipStream_t st) {
     }
     if (a.M >= LDS_MIN_ROWS) {
         const BigTile bt = big_tile(a.M, a.N, a.K, a.epi == EPI_PARTIAL);
-        if (bt.nt != 0 && (a.epi != EPI_PARTIAL || bt.ks == ks)) {
+        if (bt.nt != 0 && (a.epi != EPI_PARTIAL || bt.ks == ks) && (a.epi != EPI_GLU || bt.nt % 2 == 0)) {
             if (H && bt.ab == 8) {          // 128-row tiles: instantiated for the encoder's half operands
                 switch (bt.nt) {
                     case 4: return launch_lds_act<4, true, 8>(a, ks, st);
@@ -773,6 +833,7 @@ static int launch_16(const GemmArgs& a, int ks, hipStream_t st) {
         case EPI_STORE_FRAG: return launch_act<8, 2, 1, EPI_STORE_FRAG, H>(a, ks, st);
         case EPI_STORE: return launch_act<8, 2, 1, EPI_STORE, H>(a, ks, st);
         case EPI_QKV_RING: return launch_bf16_cfg<8, 2, 1, EPI_QKV_RING, ACT_NONE, H>(a, ks, st);
+        case EPI_GLU: return a.act == ACT_NONE ? launch_bf16_cfg<8, 2, 2, EPI_GLU, ACT_NONE, H>(a, ks, st) : -2;
         default: return -2;
     }
 }
@@ -790,6 +851,9 @@ static int launch_bf16(const GemmArgs& a, int ks, hipStream_t st) {
 
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st) {
     if (a.M <= 0 || a.N <= 0 || a.K <= 0) return -2;
+    // GLU pairs: 16-bit only, no activation, whole 32-column value/gate blocks, half the columns out
+    if (a.epi == EPI_GLU && (!bf16_data || a.act != ACT_NONE || a.bias || a.N % 32 != 0 || a.ldc < a.N / 2 || a.ldc % 4))
+        return -2;
     if (a.epi == EPI_QKV_RING) {
         // 16-bit only, no activation; the rows are whole streams of T frames; every ring row written
         // is outside the step's window (L + T <= R)

@@ -89,9 +89,19 @@ enum Epi : int {
     EPI_STORE_F32 = 3,  // C[m,n] = act(acc) * out_scale as fp32, row-major
     EPI_STORE_FRAG = 4, // as EPI_STORE but bf16 in fragment-major layout (the next GEMM's A)
     EPI_PARTIAL = 5,    // C[kz][m][n] = out_scale * (K-split kz partial), fp32; slabs M*ldc apart
-    EPI_QKV_RING = 6    // 16-bit QKV projection (N = 3 D): columns < D (q) as EPI_STORE, K and V
+    EPI_QKV_RING = 6,   // 16-bit QKV projection (N = 3 D): columns < D (q) as EPI_STORE, K and V
                         // into their K/V ring rows (GemmArgs::ring)
+    EPI_GLU = 7         // 16-bit pointwise_conv1 with its weight rows in GLU-pair order (glu_row):
+                        // output columns 32k .. 32k+15 are the values and 32k+16 .. 32k+31 the
+                        // gates of channels 16k .. 16k+15; C[m][c] = value * sigmoid(gate), IEEE
+                        // half row-major [M, N/2] (ldc = N/2)
 };
+// Row of a GLU-pair-ordered pointwise_conv1 weight that holds checkpoint row r of [2 D, K]
+// (r < D: value channel r; r >= D: gate channel r - D).
+__host__ __device__ inline int glu_row(int r, int D) {
+    const int gate = r >= D ? 1 : 0, c = r - gate * D;
+    return (c >> 4) * 32 + gate * 16 + (c & 15);
+}
 // Where EPI_QKV_RING puts K and V: row m = stream s * T + i goes to ring row (start_s + L + i) mod R
 // of the stream's slot, head (n - D) mod D / 128; rows[m] holds that row's element offset in the
 // slot's head-0 block, (slot H R + ring row) * 128 (the host computes it with the descriptor).
@@ -146,11 +156,13 @@ int launch_layernorm(float* x, Partials parts, const float* g, const float* b, v
 // row-major or (z16) IEEE half fragment-major).
 int launch_layernorm2(const float* src, Partials parts, float* res, const float* ga, const float* ba, const float* gb,
                       const float* bb, void* z, bool z16, int rows, int D, hipStream_t st);
-// GLU of pointwise_conv1's fp32 [n*T, 2D] output (value | gate) with the frame mask, causal
-// depthwise conv over [conv ring (K-1 rows) ; T new GLU rows], conv LayerNorm + SiLU; writes z
-// and the updated conv ring (which holds GLU rows).
+// GLU of pointwise_conv1's fp32 [n*T, 2D] output (value | gate), or its half GLU rows, with the
+// frame mask, causal depthwise conv over [conv ring (K-1 rows) ; T new GLU rows], conv LayerNorm +
+// SiLU; writes z and the updated conv ring (which holds GLU rows).
 struct ConvArgs {
-    const float* pw;                // [n*T, 2D] pointwise_conv1 output
+    const float* pw;                // [n*T, 2D] pointwise_conv1 output (value | gate), fp32; or
+    const uint16_t* glu;            // [n*T, D] the GLU already applied (EPI_GLU), IEEE half
+                                    // (exactly one of pw / glu is set)
     float* ring;                    // layer base of the conv pool: [slots][K-1][D]
     const float* w_t;               // [K][D] depthwise weights, tap-major
     const float* ln_g; const float* ln_b;

@@ -151,14 +151,16 @@ __global__ __launch_bounds__(256) void layernorm2_kernel(const float* src, Parti
 // out[t,d] = pw[t,d] * sigmoid(pw[t,D+d]) (Metal/20_conformer.metal:76-85), rows t >= valid zeroed
 // (maskRows, FastConformer.swift:302); causal depthwise conv k=KC+1 over [conv cache (KC rows,
 // oldest first) ; T GLU rows] (Metal/20_conformer.metal:87-102, tap KC = the current frame); then
-// the conv LayerNorm + SiLU.  One workgroup per stream, 4 channels per thread, the whole
+// the conv LayerNorm + SiLU.  With G16 the GLU was applied by pointwise_conv1's epilogue and the
+// rows come as IEEE half [n*T, D] (a quarter of the fp32 value | gate bytes).  One workgroup per
+// stream, 4 channels per thread, the whole
 // [KC + T] x 4 window in registers.  The cache is a ring of KC rows per stream: logical row r is
 // slot (frames + r) % KC; new row t (only the last KC matter) goes to slot (frames + t) % KC,
 // written by the thread that read the slot, so the update is in place with no hazard.
 // The stream's descriptor is the first load; the pointwise_conv1 rows, the weights and the LN
 // parameters (none of which depend on it) are in flight before the ring rows, and the frame mask
 // is applied to the loaded rows.
-template <int KC, int TMAX>
+template <int KC, int TMAX, bool G16>
 __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
     const int s = blockIdx.x;
     constexpr int NW = 4;                 // 256 threads, 4 channels each (launch_dwconv_ln)
@@ -170,11 +172,16 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     float4 pv[TMAX], pg[TMAX];
+    uint2 gh[TMAX];
 #pragma unroll
     for (int t = 0; t < TMAX; t++) {
-        const float* row = a.pw + ((int64_t)s * T + min(t, T - 1)) * 2 * D;
-        pv[t] = *reinterpret_cast<const float4*>(row + c0);
-        pg[t] = *reinterpret_cast<const float4*>(row + D + c0);
+        if constexpr (G16) {
+            gh[t] = *reinterpret_cast<const uint2*>(a.glu + ((int64_t)s * T + min(t, T - 1)) * D + c0);
+        } else {
+            const float* row = a.pw + ((int64_t)s * T + min(t, T - 1)) * 2 * D;
+            pv[t] = *reinterpret_cast<const float4*>(row + c0);
+            pg[t] = *reinterpret_cast<const float4*>(row + D + c0);
+        }
     }
     float4 w[KC + 1];
 #pragma unroll
@@ -194,8 +201,13 @@ __global__ __launch_bounds__(256) void dwconv_ln_kernel(ConvArgs a) {
     }
 #pragma unroll
     for (int t = 0; t < TMAX; t++) {
-        const float4 v = pv[t], gt = pg[t];
-        const float4 y = make_float4(v.x * sigmoidf(gt.x), v.y * sigmoidf(gt.y), v.z * sigmoidf(gt.z), v.w * sigmoidf(gt.w));
+        float4 y;
+        if constexpr (G16) {
+            y = make_float4(half_lo(gh[t].x), half_hi(gh[t].x), half_lo(gh[t].y), half_hi(gh[t].y));
+        } else {
+            const float4 v = pv[t], gt = pg[t];
+            y = make_float4(v.x * sigmoidf(gt.x), v.y * sigmoidf(gt.y), v.z * sigmoidf(gt.z), v.w * sigmoidf(gt.w));
+        }
         in[KC + t] = (t < T && t < valid) ? y : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
@@ -326,14 +338,21 @@ int launch_layernorm2(const float* src, Partials parts, float* res, const float*
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+template <bool G16>
+static void dwconv_dispatch(const ConvArgs& a, dim3 grid, dim3 block, hipStream_t st) {
+    if (a.T <= 2) hipLaunchKernelGGL((dwconv_ln_kernel<8, 2, G16>), grid, block, 0, st, a);
+    else if (a.T <= 4) hipLaunchKernelGGL((dwconv_ln_kernel<8, 4, G16>), grid, block, 0, st, a);
+    else if (a.T <= 8) hipLaunchKernelGGL((dwconv_ln_kernel<8, 8, G16>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((dwconv_ln_kernel<8, 16, G16>), grid, block, 0, st, a);
+}
+
 int launch_dwconv_ln(const ConvArgs& a, hipStream_t st) {
     if (a.K != 9 || a.D % 256 != 0 || a.D / 4 > 1024 || a.T < 1 || a.T > 16 || a.n < 1) return -2;
+    if ((a.pw == nullptr) == (a.glu == nullptr)) return -2;
     dim3 grid(a.n), block(a.D / 4);
     if (a.D / 4 != 256) return -2;   // the block reduction is sized for 4 waves
-    if (a.T <= 2) hipLaunchKernelGGL((dwconv_ln_kernel<8, 2>), grid, block, 0, st, a);
-    else if (a.T <= 4) hipLaunchKernelGGL((dwconv_ln_kernel<8, 4>), grid, block, 0, st, a);
-    else if (a.T <= 8) hipLaunchKernelGGL((dwconv_ln_kernel<8, 8>), grid, block, 0, st, a);
-    else hipLaunchKernelGGL((dwconv_ln_kernel<8, 16>), grid, block, 0, st, a);
+    if (a.glu) dwconv_dispatch<true>(a, grid, block, st);
+    else dwconv_dispatch<false>(a, grid, block, st);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
