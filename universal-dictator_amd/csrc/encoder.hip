@@ -172,7 +172,9 @@ constexpr int SUB_CH = 256, SUB_MEL = 128, SUB_F1 = SUB_MEL / 2 + 1, SUB_F2 = SU
 struct SubDev {
     void* w[SUB_NSLOTS] = {};      // conv.3 / conv.6 / out weights in the GEMM layout, the rest fp32
     uint32_t set_mask = 0;
-    void* a2 = nullptr; float* a3 = nullptr; void* a4 = nullptr; float* a5 = nullptr; void* af = nullptr;
+    // stage buffers: a2 conv.3's A operand; a3 conv.3's output (fp32, or half for a 16-bit encoder);
+    // a4 conv.6's A operand; a5 conv.6's output (fp32 encoders only); af the out Linear's A operand
+    void* a2 = nullptr; void* a3 = nullptr; void* a4 = nullptr; float* a5 = nullptr; void* af = nullptr;
     int32_t* vlen = nullptr;
     // the per-stage valid lengths of a call, staged in one of four pinned buffers [max_streams][4]
     // (an event per buffer: a buffer is rewritten only after the copy that read it has run)
@@ -937,9 +939,9 @@ static int sub_workspace(ud_encoder* e) {
     auto pad = [](size_t r) { return (r + 15) / 16 * 16; };
     SubDev& u = e->sub;
     bool ok = (u.a2 = dev_alloc(pad(r2) * SUB_CH * e->esz)) != nullptr;
-    ok = ok && (u.a3 = (float*)dev_alloc(r2 * SUB_CH * 4)) != nullptr;
+    ok = ok && (u.a3 = dev_alloc(r2 * SUB_CH * (e->bf ? 2 : 4))) != nullptr;
     ok = ok && (u.a4 = dev_alloc(pad(r3) * SUB_CH * e->esz)) != nullptr;
-    ok = ok && (u.a5 = (float*)dev_alloc(r3 * SUB_CH * 4)) != nullptr;
+    if (!e->bf) ok = ok && (u.a5 = (float*)dev_alloc(r3 * SUB_CH * 4)) != nullptr;   // 16-bit: conv.6 writes af
     ok = ok && (u.af = dev_alloc(pad(rf) * SUB_CH * SUB_F3 * e->esz)) != nullptr;
     ok = ok && (u.vlen = (int32_t*)dev_alloc(n * 4 * sizeof(int32_t))) != nullptr;
     if (!ok) return fail(UD_ERR_NOMEM, "ud_encoder_subsample: workspace allocation failed");
@@ -1008,17 +1010,33 @@ extern "C" UD_API int ud_encoder_subsample(ud_encoder* e, int32_t n, int32_t mel
         g.f16 = bf ? 1 : 0;
         return launch_status(launch_gemm(g, bf, st), what);
     };
-    if ((rc = gemm(u.a2, SUB_C3W, SUB_C3B, u.a3, n * T2 * SUB_F2, SUB_CH, SUB_CH, ACT_RELU, "subsampling conv.3")))
-        return rc;
+    // conv.3: half channel-last rows for a 16-bit encoder (the depthwise conv.5 reads them), fp32 otherwise
+    {
+        GemmArgs g{};
+        g.A = u.a2; g.W = u.w[SUB_C3W]; g.C = u.a3; g.M = n * T2 * SUB_F2; g.N = SUB_CH; g.K = SUB_CH;
+        g.lda = SUB_CH; g.ldw = SUB_CH; g.ldc = SUB_CH; g.epi = bf ? EPI_STORE : EPI_STORE_F32; g.act = ACT_RELU;
+        g.out_scale = 1.0f; g.ksplit = 1; g.bias = (const float*)u.w[SUB_C3B]; g.f16 = bf ? 1 : 0;
+        if ((rc = launch_status(launch_gemm(g, bf, st), "subsampling conv.3"))) return rc;
+    }
     SubDwArgs dw{};
     dw.x = u.a3; dw.vlen = u.vlen; dw.w = (const float*)u.w[SUB_C5W]; dw.b = (const float*)u.w[SUB_C5B]; dw.out = u.a4;
     dw.n = n; dw.Hin = T2; dw.Win = SUB_F2; dw.Hout = T3; dw.Wout = SUB_F3; dw.stage = 2;
     LAUNCH(launch_sub_dw(dw, bf, st), "subsampling conv.5");
-    if ((rc = gemm(u.a4, SUB_C6W, SUB_C6B, u.a5, n * T3 * SUB_F3, SUB_CH, SUB_CH, ACT_RELU, "subsampling conv.6")))
-        return rc;
-    SubFlatArgs fl{};
-    fl.x = u.a5; fl.vlen = u.vlen; fl.out = u.af; fl.n = n; fl.T3 = T3; fl.F3 = SUB_F3; fl.T = T; fl.drop = drop;
-    LAUNCH(launch_sub_flatten(fl, bf, st), "subsampling flatten");
+    if (bf) {
+        // conv.6 + ReLU writes the out Linear's rows itself: flatten (freq, channel), mask, drop
+        GemmArgs g{};
+        g.A = u.a4; g.W = u.w[SUB_C6W]; g.C = u.af; g.M = n * T3 * SUB_F3; g.N = SUB_CH; g.K = SUB_CH;
+        g.lda = SUB_CH; g.ldw = SUB_CH; g.ldc = SUB_CH; g.epi = EPI_SUBFLAT; g.act = ACT_RELU; g.out_scale = 1.0f;
+        g.ksplit = 1; g.bias = (const float*)u.w[SUB_C6B]; g.f16 = 1;
+        g.flat = SubFlat{u.vlen, T3, SUB_F3, T, drop};
+        if ((rc = launch_status(launch_gemm(g, true, st), "subsampling conv.6 + flatten"))) return rc;
+    } else {
+        if ((rc = gemm(u.a4, SUB_C6W, SUB_C6B, u.a5, n * T3 * SUB_F3, SUB_CH, SUB_CH, ACT_RELU, "subsampling conv.6")))
+            return rc;
+        SubFlatArgs fl{};
+        fl.x = u.a5; fl.vlen = u.vlen; fl.out = u.af; fl.n = n; fl.T3 = T3; fl.F3 = SUB_F3; fl.T = T; fl.drop = drop;
+        LAUNCH(launch_sub_flatten(fl, bf, st), "subsampling flatten");
+    }
     if ((rc = gemm(u.af, SUB_OUTW, SUB_OUTB, out_dev, n * T, e->D, SUB_CH * SUB_F3, ACT_NONE, "subsampling out")))
         return rc;
     return mark_done(e, st);

@@ -47,6 +47,17 @@ __device__ __forceinline__ void lds_direct16_rows(const int32_t* src, int32_t* d
     __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
 }
 
+// EPI_SUBFLAT: the out Linear's A-operand element of GEMM row m, column n (-1: row not stored), and
+// whether the row is masked (written as zero).
+__device__ __forceinline__ int64_t subflat_dst(const GemmArgs& a, int64_t m, int n, bool& masked) {
+    const SubFlat& f = a.flat;
+    const int per = f.T3 * f.F3;
+    const int s = (int)(m / per), rem = (int)(m - (int64_t)s * per), t3 = rem / f.F3, f3 = rem - t3 * f.F3;
+    masked = t3 >= f.vlen[4 * s + 3];
+    if (t3 < f.drop) return -1;
+    return frag_index((int64_t)s * f.T + t3 - f.drop, f3 * a.N + n, f.F3 * a.N / 64);
+}
+
 template <int MT, int NT>
 struct Frag {
     uint4 a[MT][2];
@@ -173,6 +184,10 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
                 const uint16_t x = to16<H>(apply_act(v, ACT) * a.out_scale);
                 if (n < a.ring.H * 128) static_cast<uint16_t*>(a.C)[m * a.ldc + n] = x;
                 else *qkv_ring_dst(a.ring, rtab[mt * 16 + g * 4 + i2], n) = x;
+            } else if constexpr (EPI == EPI_SUBFLAT) {
+                bool masked;
+                const int64_t d = subflat_dst(a, m, n, masked);
+                if (d >= 0) static_cast<uint16_t*>(a.C)[d] = masked ? (uint16_t)0 : to16<H>(apply_act(v, ACT) * a.out_scale);
             } else {
                 static_cast<uint16_t*>(a.C)[m * a.ldc + n] = to16<H>(apply_act(v, ACT) * a.out_scale);
             }
@@ -449,11 +464,18 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
                 o.x = (uint32_t)to16<H>(act_fast<ACT>(v[0]) * a.out_scale) | ((uint32_t)to16<H>(act_fast<ACT>(v[1]) * a.out_scale) << 16);
                 o.y = (uint32_t)to16<H>(act_fast<ACT>(v[2]) * a.out_scale) | ((uint32_t)to16<H>(act_fast<ACT>(v[3]) * a.out_scale) << 16);
                 bf16* dst;
-                if constexpr (EPI == EPI_QKV_RING)   // 4 columns of one head: contiguous in the ring row
+                if constexpr (EPI == EPI_QKV_RING) {   // 4 columns of one head: contiguous in the ring row
                     dst = n < a.ring.H * 128 ? static_cast<bf16*>(a.C) + m * a.ldc + n
                                              : qkv_ring_dst(a.ring, rtab[(wm * MT + i) * 16 + r16], n);
-                else
+                } else if constexpr (EPI == EPI_SUBFLAT) {   // 4 columns: contiguous in the fragment block
+                    bool masked;
+                    const int64_t d = subflat_dst(a, m, n, masked);
+                    if (d < 0) continue;
+                    if (masked) o = make_uint2(0, 0);
+                    dst = static_cast<bf16*>(a.C) + d;
+                } else {
                     dst = static_cast<bf16*>(a.C) + (EPI == EPI_STORE_FRAG ? frag_index(m, n, a.N / 64) : m * a.ldc + n);
+                }
                 *reinterpret_cast<uint2*>(dst) = o;
             }
         }
@@ -743,38 +765,45 @@ static int launch_act(const GemmArgs& a, int ks, hipStream_t st) {
 // Wider tiles cut the re-reads of the activation panel; more waves per workgroup put more of a
 // tile's K range in flight at once.
 // Larger M keeps 128-row tiles (MT 8, 2 waves).
-// IEEE-half operands with a bias (the subsampling front-end's GEMMs): fp32 outputs, no activation
-// or ReLU.  The bias is a template parameter: a runtime-optional bias in the encoder's own GEMMs
-// made their epilogues larger and cost ~2 us per launch at 128 rows.
-template <int ACT>
+// IEEE-half operands with a bias (the subsampling front-end's GEMMs): fp32 outputs (EPI_STORE_F32),
+// half outputs (EPI_STORE, row-major) or conv.6's flattened rows (EPI_SUBFLAT); no activation or
+// ReLU.  The bias is a template parameter: a runtime-optional bias in the encoder's own GEMMs made
+// their epilogues larger and cost ~2 us per launch at 128 rows.
+template <int EPI, int ACT>
 static int launch_f16(const GemmArgs& a, hipStream_t st) {
-    if (a.M <= 128 && a.N % 32 == 0 && a.K % 256 == 0) return launch_bf16_cfg<4, 4, 2, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+    if (a.M <= 128 && a.N % 32 == 0 && a.K % 256 == 0) return launch_bf16_cfg<4, 4, 2, EPI, ACT, true, true>(a, 1, st);
     // The LDS kernel's 256-row tiles leave most CUs idle below ~64 tiles (the second pointwise conv
     // of 64 streams x 160 ms: 4,352 x 256 x 256, 34 tiles, 10.5 us; the register kernel's 64 x 32
     // tiles 6.6 us).
-    // the register kernel where 256-row tiles would give fewer than 64 workgroups
     const BigTile b256 = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false, false) : BigTile{0, 1, 16};
     if (b256.nt != 0 && (int64_t)((a.M + 255) / 256) * (a.N / (64 * b256.nt)) < 64 && a.N % 32 == 0 && a.K % 128 == 0)
-        return launch_bf16_cfg<4, 2, 2, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+        return launch_bf16_cfg<4, 2, 2, EPI, ACT, true, true>(a, 1, st);
     const BigTile bt = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false) : BigTile{0, 1, 16};
     const int nt = bt.nt;
     if (a.M >= LDS_MIN_ROWS) {
         if (bt.ab == 8) {
             switch (nt) {
-                case 4: return launch_lds_cfg<4, EPI_STORE_F32, ACT, true, true, 8>(a, 1, st);
-                case 3: return launch_lds_cfg<3, EPI_STORE_F32, ACT, true, true, 8>(a, 1, st);
-                case 2: return launch_lds_cfg<2, EPI_STORE_F32, ACT, true, true, 8>(a, 1, st);
+                case 4: return launch_lds_cfg<4, EPI, ACT, true, true, 8>(a, 1, st);
+                case 3: return launch_lds_cfg<3, EPI, ACT, true, true, 8>(a, 1, st);
+                case 2: return launch_lds_cfg<2, EPI, ACT, true, true, 8>(a, 1, st);
                 default: break;
             }
         }
         switch (nt) {
-            case 4: return launch_lds_cfg<4, EPI_STORE_F32, ACT, true, true>(a, 1, st);
-            case 3: return launch_lds_cfg<3, EPI_STORE_F32, ACT, true, true>(a, 1, st);
-            case 2: return launch_lds_cfg<2, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+            case 4: return launch_lds_cfg<4, EPI, ACT, true, true>(a, 1, st);
+            case 3: return launch_lds_cfg<3, EPI, ACT, true, true>(a, 1, st);
+            case 2: return launch_lds_cfg<2, EPI, ACT, true, true>(a, 1, st);
             default: break;
         }
     }
-    return launch_bf16_cfg<8, 2, 1, EPI_STORE_F32, ACT, true, true>(a, 1, st);
+    return launch_bf16_cfg<8, 2, 1, EPI, ACT, true, true>(a, 1, st);
+}
+
+template <int EPI>
+static int launch_f16_act(const GemmArgs& a, hipStream_t st) {
+    if (a.act == ACT_NONE) return launch_f16<EPI, ACT_NONE>(a, st);
+    if (a.act == ACT_RELU) return launch_f16<EPI, ACT_RELU>(a, st);
+    return -2;
 }
 
 // The encoder's 16-bit projections: operands (and 16-bit outputs) IEEE half when H, bf16 otherwise;
@@ -840,11 +869,18 @@ static int launch_16(const GemmArgs& a, int ks, hipStream_t st) {
 
 static int launch_bf16(const GemmArgs& a, int ks, hipStream_t st) {
     if (a.f16 && a.bias != nullptr) {
-        // the subsampling front-end's GEMMs: IEEE half with a bias, fp32 out
-        if (a.epi != EPI_STORE_F32 || ks != 1) return -2;
-        if (a.act == ACT_NONE) return launch_f16<ACT_NONE>(a, st);
-        if (a.act == ACT_RELU) return launch_f16<ACT_RELU>(a, st);
-        return -2;
+        // the subsampling front-end's GEMMs: IEEE half with a bias
+        if (ks != 1) return -2;
+        switch (a.epi) {
+            case EPI_STORE_F32: return launch_f16_act<EPI_STORE_F32>(a, st);
+            case EPI_STORE: return launch_f16_act<EPI_STORE>(a, st);
+            case EPI_SUBFLAT:
+                if (!a.flat.vlen || a.flat.T3 < 1 || a.flat.F3 < 1 || a.flat.drop < 0 || a.flat.T != a.flat.T3 - a.flat.drop ||
+                    (int64_t)a.M != (int64_t)a.M / (a.flat.T3 * a.flat.F3) * a.flat.T3 * a.flat.F3 || (a.flat.F3 * a.N) % 64)
+                    return -2;
+                return launch_f16_act<EPI_SUBFLAT>(a, st);
+            default: return -2;
+        }
     }
     return a.f16 ? launch_16<true>(a, ks, st) : launch_16<false>(a, ks, st);
 }

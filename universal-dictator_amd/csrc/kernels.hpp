@@ -91,10 +91,19 @@ enum Epi : int {
     EPI_PARTIAL = 5,    // C[kz][m][n] = out_scale * (K-split kz partial), fp32; slabs M*ldc apart
     EPI_QKV_RING = 6,   // 16-bit QKV projection (N = 3 D): columns < D (q) as EPI_STORE, K and V
                         // into their K/V ring rows (GemmArgs::ring)
-    EPI_GLU = 7         // 16-bit pointwise_conv1 with its weight rows in GLU-pair order (glu_row):
+    EPI_GLU = 7,        // 16-bit pointwise_conv1 with its weight rows in GLU-pair order (glu_row):
                         // output columns 32k .. 32k+15 are the values and 32k+16 .. 32k+31 the
                         // gates of channels 16k .. 16k+15; C[m][c] = value * sigmoid(gate), IEEE
                         // half row-major [M, N/2] (ldc = N/2)
+    EPI_SUBFLAT = 8     // IEEE-half subsampling conv.6 (GemmArgs::flat): row m = (s T3 + t3) F3 + f3
+                        // of act(acc + bias) goes to row s T + t3 - drop, column f3 N + n of the out
+                        // Linear's fragment-major A operand [n T, F3 N] (rows t3 < drop skipped,
+                        // rows t3 >= vlen[4 s + 3] written as 0) -- the flatten, mask and drop
+};
+// EPI_SUBFLAT geometry.
+struct SubFlat {
+    const int32_t* vlen;            // [n][4]: valid rows per stage (index 3: after conv.5)
+    int T3, F3, T, drop;
 };
 // Row of a GLU-pair-ordered pointwise_conv1 weight that holds checkpoint row r of [2 D, K]
 // (r < D: value channel r; r >= D: gate channel r - D).
@@ -123,6 +132,7 @@ struct GemmArgs {
     int f16;                        // 16-bit path: operands (and 16-bit outputs) are IEEE half
                                     // instead of bf16
     QkvRing ring;                   // EPI_QKV_RING only
+    SubFlat flat;                   // EPI_SUBFLAT only
 };
 int launch_gemm(const GemmArgs& a, bool bf16_data, hipStream_t st);
 // fp32 GEMM for few rows (tens) on the fp32 MFMA: EPI_PARTIAL with ks K splits (slabs
@@ -184,7 +194,7 @@ struct SubArgs {
 };
 int launch_sub_conv01(const SubArgs& a, bool half_out, hipStream_t st);
 struct SubDwArgs {
-    const float* x;                 // [n, Hin, Win, C] fp32
+    const void* x;                  // [n, Hin, Win, C] fp32, or IEEE half for a half launch
     const int32_t* vlen;
     const float* w; const float* b; // [C][9], [C]
     void* out;                      // [n*Hout*Wout, C] GEMM A operand

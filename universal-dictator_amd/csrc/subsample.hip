@@ -6,11 +6,14 @@
 //   conv.0 (1 -> C) + ReLU, rows >= v1 zero     } sub_conv01_kernel: conv.0's outputs live in a
 //   conv.2 (depthwise)                          } register window per channel, so its
 //                                                 T1 x 65 x 256 activation never reaches HBM
-//   conv.3 (pointwise) + ReLU                   GEMM (bias epilogue), fp32 out
+//   conv.3 (pointwise) + ReLU                   GEMM (bias epilogue); fp32 out, or half for a
+//                                               16-bit encoder
 //   rows >= v2 zero; conv.5 (depthwise)         sub_dw_kernel (mask applied on read; 4 channels
 //                                               of one position per thread, one round trip)
-//   conv.6 (pointwise) + ReLU                   GEMM, fp32 out
-//   rows >= v3 zero; drop; flatten (f, c)       sub_flatten_kernel -> rows of the out Linear's A
+//   conv.6 (pointwise) + ReLU                   GEMM; fp32 out, then
+//   rows >= v3 zero; drop; flatten (f, c)       sub_flatten_kernel -> rows of the out Linear's A;
+//                                               a 16-bit encoder's conv.6 GEMM writes those rows
+//                                               itself (EPI_SUBFLAT epilogue: flatten, mask, drop)
 //   out Linear (C*F3 -> D) + bias               GEMM, fp32 out = the encoder's input rows
 //
 // The GEMM operands (conv.3 / conv.6 inputs, the flattened rows) are written in the GEMM's A
@@ -102,8 +105,8 @@ __global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
     }
 }
 
-// Depthwise 3 x 3 stride-2 causal conv over x [n, Hin, Win, C] fp32 whose rows >= vlen[s][stage]
-// read as zero (the mask NeMo applies before this layer).  A thread computes 4 channels of one
+// Depthwise 3 x 3 stride-2 causal conv over x [n, Hin, Win, C] (fp32, or IEEE half when H) whose
+// rows >= vlen[s][stage] read as zero (the mask NeMo applies before this layer).  A thread computes 4 channels of one
 // output position: its 9 taps are 16-byte loads issued together (one memory round trip per
 // thread), its 36 weights 9 more; a workgroup covers 4 consecutive output columns of one output row
 // (64 threads per column).  Each output column's 4 channels are one 16-byte (fp32) or 8-byte
@@ -138,18 +141,30 @@ __global__ __launch_bounds__(SUB_C) void sub_dw_kernel(SubDwArgs a) {
     // together; a padding tap or a masked row's tap is then replaced by zero with a select
     // (v_cndmask), so whatever the clamped load read -- NaN or Inf included -- never reaches the sum.
     float4 tap[3][3];
+    uint2 tap16[3][3];
     bool ok[3][3];
 #pragma unroll
     for (int kh = 0; kh < 3; kh++) {
         const int h = 2 * ho + kh - 2;
         const bool hv = h >= 0 && h < a.Hin && h < vin;
-        const float* row = a.x + (((int64_t)s * a.Hin + min(max(h, 0), a.Hin - 1)) * a.Win) * SUB_C + c4;
+        const int64_t row = (((int64_t)s * a.Hin + min(max(h, 0), a.Hin - 1)) * a.Win) * SUB_C + c4;
 #pragma unroll
         for (int kw = 0; kw < 3; kw++) {
             const int col = 2 * wo + kw - 2;
             ok[kh][kw] = hv && col >= 0 && col < a.Win;
-            tap[kh][kw] = *reinterpret_cast<const float4*>(row + (int64_t)min(max(col, 0), a.Win - 1) * SUB_C);
+            const int64_t at = row + (int64_t)min(max(col, 0), a.Win - 1) * SUB_C;
+            if constexpr (H) tap16[kh][kw] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(a.x) + at);
+            else tap[kh][kw] = *reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + at);
         }
+    }
+    if constexpr (H) {
+#pragma unroll
+        for (int kh = 0; kh < 3; kh++)
+#pragma unroll
+            for (int kw = 0; kw < 3; kw++) {
+                const uint2 u = tap16[kh][kw];
+                tap[kh][kw] = make_float4(half_lo(u.x), half_hi(u.x), half_lo(u.y), half_hi(u.y));
+            }
     }
     float acc[4] = {bias.x, bias.y, bias.z, bias.w};
 #pragma unroll
