@@ -1192,11 +1192,14 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
     using T = bf16;
-    // Row strides (LDS has 32 banks of 4 bytes): K and band rows, read 16 bytes a lane along
-    // consecutive rows, take 136 bf16 (68 words = 4 mod 32); V rows, read by ds_read_b64_tr_b16 with
-    // 4 consecutive rows per 16 lanes, take 144 bf16 (72 words = 8 mod 32); the bd rows take 84
-    // floats (4 mod 32), so 16-byte writes of 8 consecutive rows cover all banks.
-    constexpr int DK = 128, KT = 64, VST = DK + 8, VVST = DK + 16, NW = 8, SWS = 84;
+    // Row strides.  gfx950's LDS serves a ds_read_b128 16 lanes (256 bytes, 64 banks) at a time,
+    // but not as lanes 0-15: lanes 0-7 share a cycle with lanes 24-31 (and so on), so 16-byte
+    // reads of one piece along 16 consecutive rows (lane c: row c, piece p + lane / 16) are
+    // conflict-free only for a row stride of 2 mod 4 16-byte units (measured: 18 and 22 units run
+    // at full rate, 17 -- the obvious padding -- at half).  K and band rows therefore take 144 bf16
+    // (288 bytes, 18 units), like the V rows, which ds_read_b64_tr_b16 reads 4 consecutive rows per
+    // 16 lanes; the bd rows take 84 floats (measured faster than 88).
+    constexpr int DK = 128, KT = 64, VST = DK + 16, VVST = DK + 16, NW = 8, SWS = 84;
     __shared__ __align__(16) bf16 kl[KT][VST];
     __shared__ __align__(16) bf16 vl[KT][VVST];
     __shared__ __align__(16) bf16 pl[3 * KT][VST];
