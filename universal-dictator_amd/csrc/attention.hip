@@ -1297,6 +1297,7 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) oacc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+    f32x4_t bkeep = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};   // band rows 0..15 of the previous tile
     if (t_lo < t_hi) {                        // prologue: tile t_lo and its three band chunks
         uint4 x[2];
         load_rows(K, t_lo * KT, x); store_rows(kl, x);
@@ -1327,8 +1328,10 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
                 sacc[ts] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ak[ts]), as_bf16x8(aqu[st]), sacc[ts], 0, 0, 0);
         }
         // ---- bd = P_band . (q+v)^T over the wave's 80 band rows rel = iw - j0 - 63 + n (n < 80);
-        //      lane holds band rows 16tb + 4g .. +3 of query col: one 16-byte write per tile.  Five
-        //      independent accumulators, k chunk outermost.
+        //      lane holds band rows 16tb + 4g .. +3 of query col: one 16-byte write per tile.
+        //      Rows 64..79 of tile t are rows 0..15 of tile t - 1 (rel depends on j0 - n only), so
+        //      after the first tile the wave keeps that accumulator instead of recomputing it: four
+        //      independent accumulators (five in the first tile), k chunk outermost.
         {
             const int r0 = t % 3;
             int prow[5];
@@ -1343,13 +1346,23 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
             for (int tb = 0; tb < 5; tb++) bacc[tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int st = 0; st < 4; st++) {
-                uint4 ap[5];
+                uint4 ap[4];
 #pragma unroll
-                for (int tb = 0; tb < 5; tb++) ap[tb] = *reinterpret_cast<const uint4*>(&pl[prow[tb]][(4 * st + g) * 8]);
+                for (int tb = 0; tb < 4; tb++) ap[tb] = *reinterpret_cast<const uint4*>(&pl[prow[tb]][(4 * st + g) * 8]);
 #pragma unroll
-                for (int tb = 0; tb < 5; tb++)
+                for (int tb = 0; tb < 4; tb++)
                     bacc[tb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ap[tb]), as_bf16x8(aqv[st]), bacc[tb], 0, 0, 0);
             }
+            if (t == t_lo) {
+#pragma unroll
+                for (int st = 0; st < 4; st++) {
+                    const uint4 ap = *reinterpret_cast<const uint4*>(&pl[prow[4]][(4 * st + g) * 8]);
+                    bacc[4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ap), as_bf16x8(aqv[st]), bacc[4], 0, 0, 0);
+                }
+            } else {
+                bacc[4] = bkeep;
+            }
+            bkeep = bacc[0];
 #pragma unroll
             for (int tb = 0; tb < 5; tb++)
                 *reinterpret_cast<float4*>(&sw[wave][col][16 * tb + 4 * g]) = make_float4(bacc[tb][0], bacc[tb][1], bacc[tb][2], bacc[tb][3]);
