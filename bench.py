@@ -184,6 +184,21 @@ def cpu_baseline(lw, sw, cfg, S, T, budget_s, cpu, S_sample=None):
                        % ("%d of the " % Sn if Sn != S else "", S, rows, T, cfg.layers, n, med, el))
 
 
+def warm_up(fn, hs, min_calls, min_ms=150.0):
+    """Untimed calls until at least min_calls have run and min_ms of wall time has passed, waiting
+    for the stream every 10 calls.  Under sustained load the GPU's clock rises over the first
+    ~30-40 ms (the offline attention launch takes 214 us at first and 157 us from ~35 ms on; a
+    256-stream x 14-frame step 8.4 ms at first and 7.9 ms after 60 ms), so the figures that follow
+    are of the steady state.  Returns the number of calls run."""
+    n, t0 = 0, time.perf_counter()
+    while n < min_calls or (time.perf_counter() - t0) * 1000.0 < min_ms:
+        for _ in range(10):
+            fn()
+        n += 10
+        hs.synchronize()
+    return n
+
+
 def mel_rows(T):
     """Mel rows of a chunk that yields T encoder frames after the 2 dropped ones: 8 (T + 2) - 7
     (16 new rows + 9 pre-encode cache rows for T = 2, NemotronSchedule.swift)."""
@@ -236,9 +251,7 @@ def decode_bench(ud, args, summary=False, steps=None, warmup=None, workload="dec
     else:
         call = lambda: ud.gqa_attention_paged_mq(q, kp, vp, tbl, max_blocks, ranges, out, n, M, Hq, Hkv, d, max_keys,
                                                  ws, hip_stream=hs)
-    for _ in range(warmup):
-        call()
-    hs.synchronize()
+    warmed = warm_up(call, hs, warmup)
     e0, e1 = ud.Event(), ud.Event()
     e0.record(hs)
     t0 = time.perf_counter()
@@ -259,12 +272,12 @@ def decode_bench(ud, args, summary=False, steps=None, warmup=None, workload="dec
                 "us_per_call": round(ms * 1000.0, 3), "tokens_per_sec": round(n * M / (ms / 1000.0), 1),
                 "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_call": algo,
-                "calls_timed": steps}
+                "calls_timed": steps, "warmup_calls": warmed}
     result = {
         "metric": "paged GQA decode attention: tokens/s and HBM roofline fraction",
         "value": round(n * M / (ms / 1000.0), 1),
         "unit": "tokens/s",
-        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
+        "n_gpus": 1, "steps": steps, "warmup": warmed, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16 K/V pages, fp32 queries, softmax and accumulation (bf16 MFMA operands)",
         "data": "synthetic (seeded N(0,1) queries and bf16 K/V pages, random page table)",
@@ -324,9 +337,7 @@ def offline_bench(ud, args, summary=False, steps=None, warmup=None):
     out = ud.DeviceBuffer(B * T * D * 2)
     hs = ud.HipStream()
     call = lambda: ud.rel_pos_attention_batched(q, k, v, P, T - 1, u, vb, ranges, out, B, T, H, n_rel, hip_stream=hs)
-    for _ in range(warmup):
-        call()
-    hs.synchronize()
+    warmed = warm_up(call, hs, warmup)
     e0, e1 = ud.Event(), ud.Event()
     e0.record(hs)
     t0 = time.perf_counter()
@@ -348,12 +359,13 @@ def offline_bench(ud, args, summary=False, steps=None, warmup=None):
                 "us_per_launch": round(ms * 1000.0, 3), "frames_per_sec": round(B * T / (ms / 1000.0), 1),
                 "bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "algorithmic_flops_per_launch": flops_dense,
-                "valid_key_tflops": round(flops_valid / (ms / 1000.0) / 1e12, 2), "launches_timed": steps}
+                "valid_key_tflops": round(flops_valid / (ms / 1000.0) / 1e12, 2), "launches_timed": steps,
+                "warmup_launches": warmed}
     result = {
         "metric": "offline rel-pos attention: frames/s and bf16 MFMA roofline fraction",
         "value": round(B * T / (ms / 1000.0), 1),
         "unit": "frames/s (one layer, all heads)",
-        "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
+        "n_gpus": 1, "steps": steps, "warmup": warmed, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16 q/k/v/P operands, fp32 softmax and accumulation",
         "data": "synthetic (seeded N(0,1) q/k/v, random position table, random valid lengths)",
@@ -681,10 +693,8 @@ def long_chunk(ud, lw, sw, args, hbm_read, mfma_f16):
         Tn, valid = enc.subsample(S, mel, x, drop=2, mel_rows=rows, hip_stream=hs)
         enc.encode_stream_step(streams, x, out, valid=valid, T=Tn, hip_stream=hs)
 
-    for _ in range(3):
-        step()
-    hs.synchronize()
-    n14 = 12
+    warm14 = warm_up(step, hs, 10)
+    n14 = 25
     e0, e1 = ud.Event(), ud.Event()
     ud.synchronize()
     e0.record(hs)
@@ -703,7 +713,7 @@ def long_chunk(ud, lw, sw, args, hbm_read, mfma_f16):
     chunk14 = {"workload": "cache-aware encoder step (dw_striding 8x subsampling + 24 layers), %d streams x %d mel "
                            "rows -> %d frames (1120 ms), left context %d, %s" % (S, rows, T, L, PRECISION),
                "ms_per_step": round(ms14, 5), "value": round(value14, 2), "unit": "audio-sec/sec",
-               "steps_timed": n14, "projection_tflops_per_step": round(step_tf, 1),
+               "steps_timed": n14, "warmup_steps": warm14, "projection_tflops_per_step": round(step_tf, 1),
                "step_frac_of_mfma_peak": round(step_tf / MFMA_BF16_PEAK_TFLOPS, 4),
                "mfma_utilisation": mf}
     enc.close()
@@ -929,7 +939,7 @@ def main():
     if args.workload == "chunk2" and not args.no_long_chunk_attention:
         result["roofline_long_chunk"], result["chunk14_step"] = long_chunk(ud, lw, sw, args, hbm_read, mfma_f16)
     if args.workload == "chunk2" and not args.no_other_kernels:
-        result["offline_attention"] = offline_bench(ud, args, summary=True, steps=40, warmup=5)
+        result["offline_attention"] = offline_bench(ud, args, summary=True, steps=200, warmup=20)
         result["decode_attention"] = decode_bench(ud, args, summary=True, steps=200, warmup=20)
         result["decode_attention_4_queries"] = decode_bench(ud, args, summary=True, steps=200, warmup=20,
                                                             workload="decode_mq")

@@ -263,17 +263,18 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
 // For M in the thousands (256 streams x 14 frames = 3584 rows) the projections are MFMA-bound, and
 // the register-direct kernel above would re-read each activation fragment once per 16-column tile.
 // Here a workgroup of 8 waves (2 per SIMD, so one wave's MFMAs run while the other waits on LDS)
-// owns a 256 x 64*NT output tile.  Per 32-deep K step it copies the 16 row fragments and 4*NT
-// column fragments (each a contiguous 1 KB half of a 2 KB fragment-major block, so the copy is
-// linear) into LDS with direct global -> LDS loads (global_load_lds_dwordx4, no staging
-// registers).  LDS holds a ring of four steps: at the start of step s the wave waits until its own
-// loads of step s have landed (the loads of s+1 and s+2 may still be in flight), a barrier makes
-// every wave's loads visible and guarantees that step s-1's buffer has been read, the wave reads
-// its fragments of step s, issues the loads of step s+3 into step s-1's buffer, and multiplies.
-// Three steps of loads stay in flight behind the MFMAs (with two 64-deep buffers, less than one
-// chunk did, and the kernel waited on its loads).  The four buffers are separate arrays and the
-// loop is unrolled by four, so the compiler can tell the buffers apart and does not wait for
-// outstanding direct loads before the LDS reads of another buffer.
+// owns a 256 x 64*NT output tile (or 224 or 128 rows).  Per 32-deep K step it copies the row
+// fragments and 4*NT column fragments (each a contiguous 1 KB half of a 2 KB fragment-major block,
+// so the copy is linear) into LDS with direct global -> LDS loads (global_load_lds_dwordx4, no
+// staging registers).  LDS holds a ring of four steps and the fragments are read one step ahead:
+// at step s the wave waits until its own loads of step s+1 have landed (those of s+2 and s+3 may
+// still be in flight) and its LDS reads of step s are done, a barrier makes every wave's loads
+// visible and frees step s's buffer, the wave reads its step-(s+1) fragments into its second
+// register set, issues the loads of step s+4 into step s's buffer, and multiplies step s.  Three
+// steps of loads stay in flight behind the MFMAs (with two 64-deep buffers, less than one chunk
+// did, and the kernel waited on its loads).  The four buffers are separate arrays and the loop is
+// unrolled by four, so the compiler can tell the buffers apart and does not wait for outstanding
+// direct loads before the LDS reads of another buffer.
 //
 // The MFMAs are inline asm with the accumulators pinned in place in the accumulator registers:
 // compiled from the builtin, the register allocator copied part of the accumulator between
@@ -306,14 +307,15 @@ __device__ __forceinline__ float act_fast(float x) {
 
 // Waves form a 2 x 4 grid; each owns 16*MT x 16*NT (AB = 16: 256-row tiles, 128 x 16*NT per wave,
 // NT = 4: 128 pinned accumulator registers; with about 120 vector registers two waves fit per
-// SIMD).  Narrower tiles (NT 3, 2) and 128-row tiles (AB = 8, 64 rows per wave) give more
-// workgroups where 256 x 256 tiles would leave CUs idle.  The MFMA operands are swapped (weights as
+// SIMD).  Narrower tiles (NT 3, 2), 224-row tiles (AB = 14, 112 rows per wave) and 128-row tiles
+// (AB = 8, 64 rows per wave) give more workgroups where 256 x 256 tiles would leave CUs idle
+// (3,584 rows = 14 x 256 = 16 x 224: 224-row tiles turn 224 workgroups into 256).  The MFMA operands are swapped (weights as
 // the row operand), so each 16 x 16 accumulator holds C^T: a lane has 4 consecutive output columns
 // of one row, and the epilogue writes 16 bytes (fp32) or 8 bytes (bf16, row-major or
 // fragment-major) per lane.
 template <int NT, int EPI, int ACT, bool H = false, bool BIAS = false, int AB = 16>
 __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
-    static_assert(AB == 16 || AB == 8, "256- or 128-row tiles");
+    static_assert(AB == 16 || AB == 14 || AB == 8, "256-, 224- or 128-row tiles");
     constexpr int MT = AB / 2, BB = 4 * NT;                  // wave row tiles; W blocks (16 columns each) per tile
     constexpr int TR = 16 * AB;                              // tile rows
     constexpr int NBLK = AB + BB;                            // 1 KB half-blocks per 32-deep K step
@@ -326,6 +328,7 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) int32_t rtab[EPI == EPI_QKV_RING ? TR : 4];    // QKV: ring row offsets
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool extra = CPS > CMIN && wave + 8 * CMIN < NBLK;   // this wave copies CPS blocks per step, else CMIN
     const int wm = wave >> 2, wn = wave & 3;
     const int r16 = lane & 15, g = lane >> 4;
     const int nN = a.N / (64 * NT), nM = (a.M + TR - 1) / TR;
@@ -366,55 +369,82 @@ __global__ __launch_bounds__(512, 1) void gemm_bf16_lds_kernel(GemmArgs a) {
         for (int i = 0; i < MT; i++) acc[j][i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int aoff = (wm * MT) * 512 + lo, boff = (AB + wn * NT) * 512 + lo;
-    uint4 fa[MT], fb[NT];
-    auto read_step = [&](const bf16* buf) __attribute__((always_inline)) {
+    // Two fragment register sets: the MFMAs of step s run on one while the LDS reads of step s + 1
+    // fill the other.
+    uint4 fa0[MT], fb0[NT], fa1[MT], fb1[NT];
+    auto read_to = [&](const bf16* buf, uint4 (&xa)[MT], uint4 (&xb)[NT]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < MT; i++) fa[i] = *reinterpret_cast<const uint4*>(buf + aoff + i * 512);
+        for (int i = 0; i < MT; i++) xa[i] = *reinterpret_cast<const uint4*>(buf + aoff + i * 512);
 #pragma unroll
-        for (int j = 0; j < NT; j++) fb[j] = *reinterpret_cast<const uint4*>(buf + boff + j * 512);
+        for (int j = 0; j < NT; j++) xb[j] = *reinterpret_cast<const uint4*>(buf + boff + j * 512);
     };
-    auto mma = [&]() __attribute__((always_inline)) {
+    auto mma = [&](const uint4 (&xa)[MT], const uint4 (&xb)[NT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < NT; j++)
 #pragma unroll
             for (int i = 0; i < MT; i++)
                 if constexpr (H)
                     asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0"
-                                 : "+a"(acc[j][i]) : "v"(as_f16x8(fb[j])), "v"(as_f16x8(fa[i])));
+                                 : "+a"(acc[j][i]) : "v"(as_f16x8(xb[j])), "v"(as_f16x8(xa[i])));
                 else
                     asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
-                                 : "+a"(acc[j][i]) : "v"(as_bf16x8(fb[j])), "v"(as_bf16x8(fa[i])));
+                                 : "+a"(acc[j][i]) : "v"(as_bf16x8(xb[j])), "v"(as_bf16x8(xa[i])));
+    };
+    // This wave's loads of a step have landed once at most `later` steps' loads (issued after it)
+    // are outstanding: CPS or CMIN direct loads per step for this wave.
+    auto wait_landed = [&](int later) __attribute__((always_inline)) {
+        if (extra) {
+            if (later >= 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * CPS));
+            else if (later == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CPS));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(CPS));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        } else {
+            if (later >= 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * CMIN));
+            else if (later == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CMIN));
+            else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(CMIN));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+        }
     };
     // QKV split store: the ring offsets of the tile's TR rows (the table is padded past the last row)
     if constexpr (EPI == EPI_QKV_RING) {
         if (wave == 0 && lane < TR / 4) lds_direct16_rows(a.ring.rows + mb * TR + 4 * lane, rtab);
     }
-    // Four-stage ring of 32-deep K steps: steps s+1, s+2 (and the loads of s+3, issued at the start
-    // of step s into the stage step s-1 used) are in flight while step s is multiplied.
+    // Four-stage ring of 32-deep K steps, fragments one step ahead.  At step s: wait until this
+    // wave's loads of step s + 1 have landed and its LDS reads of step s are done; a barrier makes
+    // every wave's loads of s + 1 visible and frees step s's buffer (every wave holds its step-s
+    // fragments in registers); read the step s + 1 fragments, issue the loads of step s + 4 into
+    // step s's buffer, and multiply step s.  So the LDS reads of one step overlap the MFMAs of the
+    // previous one, and three steps of loads stay in flight behind them.
     copy_step(0, st0);
     if (1 < nsteps) copy_step(1, st1);
     if (2 < nsteps) copy_step(2, st2);
+    if (3 < nsteps) copy_step(3, st3);
+    wait_landed(min(3, nsteps - 1));
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    read_to(st0, fa0, fb0);
     pin_acc(acc);
     asm volatile("s_nop 7");                                 // accumulator zeroing -> first MFMA
-    auto step = [&](int s, const bf16* cur, bf16* nxt) __attribute__((always_inline)) {
-        // step s landed: every later in-flight step's loads may still be outstanding
-        if (s + 2 < nsteps) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CMIN));
-        else if (s + 1 < nsteps) __builtin_amdgcn_s_waitcnt(vmcnt_imm(CMIN));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-        __builtin_amdgcn_s_barrier();                        // every wave's loads of step s; step s-1 read
-        __asm__ volatile("" ::: "memory");
-        read_step(cur);
-        __builtin_amdgcn_sched_barrier(0);
-        if (s + 3 < nsteps) copy_step(s + 3, nxt);
-        __builtin_amdgcn_sched_barrier(0);
-        mma();
+    auto step = [&](int s, const uint4 (&ca)[MT], const uint4 (&cb)[NT], uint4 (&na)[MT], uint4 (&nb)[NT],
+                    const bf16* nbuf, bf16* cbuf) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(0xC07F);                  // lgkmcnt(0): this wave's step-s reads are done
+        if (s + 1 < nsteps) {
+            wait_landed(min(s + 3, nsteps - 1) - (s + 1));
+            __builtin_amdgcn_s_barrier();                    // every wave's loads of step s + 1; step s's buffer free
+            __asm__ volatile("" ::: "memory");
+            read_to(nbuf, na, nb);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 4 < nsteps) copy_step(s + 4, cbuf);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        mma(ca, cb);
         __builtin_amdgcn_sched_barrier(0);
     };
     for (int s = 0; s < nsteps; s += 4) {
-        step(s, st0, st3);
-        if (s + 1 < nsteps) step(s + 1, st1, st0);
-        if (s + 2 < nsteps) step(s + 2, st2, st1);
-        if (s + 3 < nsteps) step(s + 3, st3, st2);
+        step(s, fa0, fb0, fa1, fb1, st1, st0);
+        if (s + 1 < nsteps) step(s + 1, fa1, fb1, fa0, fb0, st2, st1);
+        if (s + 2 < nsteps) step(s + 2, fa0, fb0, fa1, fb1, st3, st2);
+        if (s + 3 < nsteps) step(s + 3, fa1, fb1, fa0, fb0, st0, st3);
     }
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7");   // last MFMA results -> epilogue reads
     pin_acc(acc);
@@ -715,20 +745,30 @@ static int device_cus() {
 // pointwise_conv1 (+0.126 ms) or ff linear2 (+0.05 ms with 2 splits, more without), which already
 // launch 224 256-row workgroups.  The 128-row cost of 2.0 makes 128-row tiles win only where
 // 256-row tiles leave about half the CUs idle, which is what those runs show.
-BigTile big_tile(int M, int N, int K, bool partial, bool rows128) {
+// 224-row tiles: each weight panel is re-read 8/7 as often per flop as with 256-row tiles.  At
+// 3,584 rows they give 256 workgroups instead of 224 (ff linear1, q/k/v, pointwise_conv1, ff
+// linear2 with 2 splits); with the fragments read one step ahead the config-3 step went 8.02 ->
+// 7.95 ms (the same fragment schedule with 256-row tiles only: 8.05 ms).
+constexpr double C224 = 1.05;
+BigTile big_tile(int M, int N, int K, bool partial, int heights_mask) {
     static const double cost_256[5] = {0.0, 0.0, 1.36, 1.28, 1.0};
     static const double cost_128[5] = {0.0, 0.0, 2.0, 2.0, 2.0};
     const int cus = device_cus();
     BigTile best{0, 1, 16};
     double best_cost = 1e300;
-    for (int ab = 16; ab >= (rows128 ? 8 : 16); ab /= 2)
+    static const int heights[3] = {16, 14, 8};
+    for (int hi = 0; hi < 3; hi++)
         for (int nt = 4; nt >= 2; nt--) {
+            if (!(heights_mask & (1 << hi))) continue;
+            const int ab = heights[hi];
+            // per-flop cost: 256-row measured; 224 rows re-read each weight panel 8/7 as often
+            const double pc = ab == 16 ? cost_256[nt] : ab == 14 ? cost_256[nt] * C224 : cost_128[nt];
             if (N % (64 * nt) != 0) continue;
             for (int ks = 1; ks <= (partial ? 4 : 1); ks *= 2) {
                 if (K % (64 * ks) != 0 || (ks > 1 && K / ks < 256)) continue;
                 const long tiles = (long)(N / (64 * nt)) * ((M + 16 * ab - 1) / (16 * ab)) * ks;
                 const long rounds = (tiles + cus - 1) / cus;
-                double cost = (double)rounds * (ab / 16.0) * nt * (K / ks) * (ab == 16 ? cost_256[nt] : cost_128[nt]);
+                double cost = (double)rounds * (ab / 16.0) * nt * (K / ks) * pc;
                 if (ks > 1) cost += 900.0 * ks * ((double)M * N / (3584.0 * 1024.0));
                 if (cost < best_cost) { best_cost = cost; best = BigTile{nt, ks, ab}; }
             }
@@ -739,7 +779,7 @@ BigTile big_tile(int M, int N, int K, bool partial, bool rows128) {
 int gemm_partial_splits(int M, int N, int K, bool bf16_data) {
     if (!bf16_data) return 1;
     if (M >= LDS_MIN_ROWS) {
-        const BigTile bt = big_tile(M, N, K, true);
+        const BigTile bt = big_tile(M, N, K, true, TILE_ALL);
         if (bt.nt != 0) return bt.ks;
     }
     if (M <= 128 && K == 1024 && N % 32 == 0) return 2;   // linear_out, pointwise_conv2 (launch_bf16)
@@ -775,10 +815,10 @@ static int launch_f16(const GemmArgs& a, hipStream_t st) {
     // The LDS kernel's 256-row tiles leave most CUs idle below ~64 tiles (the second pointwise conv
     // of 64 streams x 160 ms: 4,352 x 256 x 256, 34 tiles, 10.5 us; the register kernel's 64 x 32
     // tiles 6.6 us).
-    const BigTile b256 = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false, false) : BigTile{0, 1, 16};
+    const BigTile b256 = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false, TILE_256) : BigTile{0, 1, 16};
     if (b256.nt != 0 && (int64_t)((a.M + 255) / 256) * (a.N / (64 * b256.nt)) < 64 && a.N % 32 == 0 && a.K % 128 == 0)
         return launch_bf16_cfg<4, 2, 2, EPI, ACT, true, true>(a, 1, st);
-    const BigTile bt = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false) : BigTile{0, 1, 16};
+    const BigTile bt = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false, TILE_256 | TILE_128) : BigTile{0, 1, 16};
     const int nt = bt.nt;
     if (a.M >= LDS_MIN_ROWS) {
         if (bt.ab == 8) {
@@ -840,13 +880,20 @@ static int launch_16(const GemmArgs& a, int ks, hipStream_t st) {
         }
     }
     if (a.M >= LDS_MIN_ROWS) {
-        const BigTile bt = big_tile(a.M, a.N, a.K, a.epi == EPI_PARTIAL);
+        const BigTile bt = big_tile(a.M, a.N, a.K, a.epi == EPI_PARTIAL, TILE_ALL);
         if (bt.nt != 0 && (a.epi != EPI_PARTIAL || bt.ks == ks) && (a.epi != EPI_GLU || bt.nt % 2 == 0)) {
-            if (H && bt.ab == 8) {          // 128-row tiles: instantiated for the encoder's half operands
+            if (H && bt.ab == 8) {          // 128- and 224-row tiles: instantiated for the encoder's half operands
                 switch (bt.nt) {
                     case 4: return launch_lds_act<4, true, 8>(a, ks, st);
                     case 3: return launch_lds_act<3, true, 8>(a, ks, st);
                     default: return launch_lds_act<2, true, 8>(a, ks, st);
+                }
+            }
+            if (H && bt.ab == 14) {
+                switch (bt.nt) {
+                    case 4: return launch_lds_act<4, true, 14>(a, ks, st);
+                    case 3: return launch_lds_act<3, true, 14>(a, ks, st);
+                    default: return launch_lds_act<2, true, 14>(a, ks, st);
                 }
             }
             switch (bt.nt) {

@@ -143,10 +143,11 @@ int launch_gemm_f32_small(const GemmArgs& a, int ks, hipStream_t st);
 constexpr int KSPLIT = 4;
 // Rows from which the bf16 projections use the LDS-staged kernel (256- or 128-row tiles).
 constexpr int LDS_MIN_ROWS = 2048;
-struct BigTile { int nt, ks, ab; };   // 16*ab-row x 64*nt-column tiles (ab 16 or 8), ks K splits
+struct BigTile { int nt, ks, ab; };   // 16*ab-row x 64*nt-column tiles (ab 16, 14 or 8), ks K splits
                                       // (nt 0: shape not supported)
-// rows128: 128-row tiles are candidates too (else 256-row tiles only)
-BigTile big_tile(int M, int N, int K, bool partial, bool rows128 = true);
+// heights_mask: the tile heights that are candidates (TILE_256 | TILE_224 | TILE_128)
+constexpr int TILE_256 = 1, TILE_224 = 2, TILE_128 = 4, TILE_ALL = 7;
+BigTile big_tile(int M, int N, int K, bool partial, int heights_mask);
 // K splits (partial slabs) a residual projection of this shape writes; launch_gemm expects it in
 // GemmArgs::ksplit for EPI_PARTIAL.
 int gemm_partial_splits(int M, int N, int K, bool bf16_data);
