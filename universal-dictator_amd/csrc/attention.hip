@@ -1207,8 +1207,41 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
     __shared__ int kbound[2];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 15, g = lane >> 4;
-    const int Tn = a.T, D = a.H * DK, h = blockIdx.y, b = blockIdx.z;
-    const int i0 = blockIdx.x * 128, iw = i0 + 16 * wave;
+    const int Tn = a.T, D = a.H * DK;
+    // ---- which (utterance, head, 128-query block) this workgroup owns.  1-D grid; the pairs
+    //      (utterance, head) are taken longest utterance first (key span of its first and last
+    //      query; up to 64 utterances, else in order), and when they divide among the 8 XCDs
+    //      (workgroups are dealt round-robin) all query blocks of a pair run on one XCD, whose L2
+    //      then serves their shared K, V and band tiles.  Longest-first dispatch ends the sweep
+    //      with the short utterances' workgroups instead of leaving long ones to run alone.
+    __shared__ int bord[64];
+    const int nq = (Tn + 127) / 128, id = blockIdx.x;
+    if (a.B <= 64) {
+        __shared__ int bwork[64];
+        if (tid < a.B) {
+            const int32_t* Rb = a.ranges + (int64_t)tid * Tn * 2;
+            bwork[tid] = max(min(Rb[2 * (Tn - 1) + 1], Tn) - max(Rb[0], 0), 0);
+        }
+        __syncthreads();
+        if (tid < a.B) {
+            const int w = bwork[tid];
+            int rank = 0;
+            for (int o = 0; o < a.B; o++) rank += (bwork[o] > w || (bwork[o] == w && o < tid)) ? 1 : 0;
+            bord[rank] = tid;
+        }
+    } else if (tid == 0) {
+        bord[0] = -1;
+    }
+    __syncthreads();
+    int pr, qb;
+    if ((a.B * a.H) % 8 == 0) {
+        const int j = id >> 3;
+        pr = (id & 7) + 8 * (j / nq); qb = j % nq;
+    } else {
+        pr = id / nq; qb = id % nq;
+    }
+    const int h = pr % a.H, b = a.B <= 64 ? bord[pr / a.H] : pr / a.H;
+    const int i0 = qb * 128, iw = i0 + 16 * wave;
     const float c2 = a.scale * 1.4426950408889634f;      // scores in log2 units: exp(s * scale) = 2^(s * c2)
     const T* Q = static_cast<const T*>(a.q) + (int64_t)b * Tn * D + h * DK;
     const T* K = static_cast<const T*>(a.k) + (int64_t)b * Tn * D + h * DK;
@@ -1466,7 +1499,9 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
 
 int launch_relpos_dense(const DenseArgs& a, hipStream_t st) {
     if (a.B < 1 || a.T < 1 || a.H < 1) return -2;
-    hipLaunchKernelGGL(relpos_dense_kernel, dim3((a.T + 127) / 128, a.H, a.B), dim3(512), 0, st, a);
+    const int64_t blocks = (int64_t)((a.T + 127) / 128) * a.H * a.B;
+    if (blocks >= (1ll << 31)) return -2;
+    hipLaunchKernelGGL(relpos_dense_kernel, dim3((unsigned)blocks), dim3(512), 0, st, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
