@@ -1206,7 +1206,8 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
     __shared__ __align__(16) float sw[NW][16][SWS];
     __shared__ int kbound[2];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 15, g = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, col = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: its index math is scalar
     const int Tn = a.T, D = a.H * DK;
     // ---- which (utterance, head, 128-query block) this workgroup owns.  1-D grid; the pairs
     //      (utterance, head) are taken longest utterance first (key span of its first and last
