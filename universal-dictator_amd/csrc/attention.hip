@@ -1324,8 +1324,9 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
         boff[tb] = 16 * wave + 16 * tb + col + 64 * dch[tb];
     }
 
-    // m: the query's running maximum of the unscaled scores; l: this lane's share (its 4 keys of
-    // each 16) of the running sum, all 4 lanes of a query rescaled alike, summed at the end
+    // m: the query's exponent offset (a running maximum of its unscaled scores, raised lazily); l:
+    // this lane's share (its 4 keys of each 16) of the running sum, all 4 lanes of a query rescaled
+    // alike, summed at the end
     float m = -INFINITY, l = 0.0f;
     f32x4_t oacc[8];                          // out^T: lane holds channels 16dt + 4g + r of query col
 #pragma unroll
@@ -1406,7 +1407,7 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
         // ---- scores and the online softmax of query col.  Key 16ts + 4g + r uses band row
         //      col - 16ts - 4g - r + 63 of the wave's window (0..78): four consecutive floats.
         //      A tile inside every key range of the wave's queries (the common case) skips the
-        //      masks; the accumulator is rescaled only when some query's maximum grew.
+        //      masks; the accumulator is rescaled only when some query's maximum grew by more than 2^8.
         const bool inside = __all(j0 >= qks && j0 + KT <= qke);
         float sc[4][4];
 #pragma unroll
@@ -1434,9 +1435,15 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; r++) mx = fmaxf(mx, sc[ts][r]);
         mx = xmax32(xmax16(mx));
-        const float nm = fmaxf(m, mx);
-        if (!__all(nm == m)) {
-            const float corr = nm == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f((m - nm) * c2);
+        // The offset m is raised only when a score exceeds it by more than 8 in log2 units (a
+        // probability above 2^8): softmax does not depend on the offset, and between raises the
+        // probabilities stay in (0, 256], exact enough in fp32 and as bf16 P.V operands, so most
+        // tiles skip the accumulator's rescale.  (mx - m) is NaN, not > 8, while a query has no
+        // key yet, and +inf on its first key.
+        const bool grow = (mx - m) * c2 > 8.0f;
+        if (__any(grow)) {
+            const float nm = grow ? mx : m;
+            const float corr = (m == -INFINITY || !grow) ? 1.0f : __builtin_amdgcn_exp2f((m - nm) * c2);
             l *= corr;
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) oacc[dt] *= corr;
