@@ -110,6 +110,31 @@ def test_offline_running_max(gpu, orc, order):
     harness.assert_bf16_close(got, _oracle(orc, q, k, v, P, u, vb, ranges), "offline running max " + order)
 
 
+@pytest.mark.parametrize("B,Hh,T", [(3, 3, 150), (2, 8, 130), (66, 4, 24), (65, 1, 20)])
+def test_offline_grid_orders(gpu, orc, B, Hh, T):
+    """Every grid order of the kernel: (utterance, head) pairs that do not divide among the 8 XCDs
+    (3 x 3), that do (2 x 8), and more than 64 utterances (taken in order, with and without the
+    XCD grouping), each with ragged valid lengths so the longest-first order is not the identity."""
+    ud = gpu
+    rng = np.random.default_rng(35 + B + Hh)
+    D = Hh * DK
+    q, k, v = (ud.round_bf16(rng.standard_normal((B, T, D)).astype(np.float32)) for _ in range(3))
+    P = ud.round_bf16((rng.standard_normal((2 * T - 1, D)) * 0.5).astype(np.float32))
+    u = (rng.standard_normal((Hh, DK)) * 0.02).astype(np.float32)
+    vb = (rng.standard_normal((Hh, DK)) * 0.02).astype(np.float32)
+    lens = rng.integers(1, T + 1, B)
+    ranges = np.zeros((B, T, 2), np.int32)
+    ranges[:, :, 1] = lens[:, None]
+    dev = ud.DeviceBuffer.from_numpy
+    out = ud.DeviceBuffer(B * T * D * 2)
+    ud.rel_pos_attention_batched(dev(_bits(ud, q)), dev(_bits(ud, k)), dev(_bits(ud, v)), dev(_bits(ud, P)), T - 1,
+                                 dev(u), dev(vb), dev(ranges), out, B, T, Hh, P.shape[0])
+    ud.synchronize()
+    got = (out.download((B, T, D), np.uint16).astype(np.uint32) << 16).view(np.float32)
+    ref = np.stack([orc.relpos_attention(q[b], k[b], v[b], P, u, vb, ranges[b], T - 1, Hh) for b in range(B)])
+    harness.assert_bf16_close(got, ref, "offline grid order B=%d H=%d" % (B, Hh))
+
+
 def test_offline_error_paths(gpu):
     ud = gpu
     b = ud.DeviceBuffer(1 << 12)
