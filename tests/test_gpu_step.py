@@ -137,9 +137,9 @@ def test_step_bf16_chunk14(gpu, orc):
 
 
 def test_step_bf16_chunk14_many_rows(gpu, orc):
-    """250 streams x 14 frames = 3500 rows: the LDS-staged projection kernel at every tile width it
-    picks for config 3's shapes (256 x 256, 256 x 192, 256 x 128 tiles; 2 and 4 K splits), with a
-    partial last 256-row tile (3500 = 13 x 256 + 172)."""
+    """250 streams x 14 frames = 3500 rows: the LDS-staged projection kernel at every tile it picks
+    for the 14-frame chunk's shapes (224 x 256, 224 x 192, 224 x 128 with 2 K splits, 128 x 128),
+    with a partial last 224-row tile (3500 = 15 x 224 + 140)."""
     cfg = gpu.EncoderConfig(layers=2, max_chunk=14, max_streams=250, dtype="bf16")
     plan = lambda step, S, T: [(T, 9, 0, 3, T)[s % 5] if step == 1 else T for s in range(S)]
     enc, _, _, res = _run_steps(gpu, orc, cfg, S=250, T=14, n_steps=2, seed=63, seed_caches=True, valid_plan=plan)

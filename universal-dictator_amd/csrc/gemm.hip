@@ -738,7 +738,7 @@ static int device_cus() {
 // round of workgroups, where nothing hides them, about 2-3 us, and its read in the LayerNorm
 // about 2.5 us).
 // A 128-row tile re-reads each weight panel twice as often as a 256-row one.  Measured on the
-// 24-layer config-3 step (256 streams x 14 frames, eager launches, all choices in one process):
+// 24-layer 256-stream x 14-frame step (eager launches, all choices in one process):
 // 8.409 ms with 256-row tiles everywhere; 8.218 ms with linear_out and pointwise_conv2 on 128 x 128
 // tiles (224 workgroups instead of 112 on 256 CUs: 19.7 -> 14.5 us each); 8.209 ms with the
 // subsampling's out projection too; worse with 128-row tiles for q/k/v (+0.134 ms),
@@ -747,8 +747,8 @@ static int device_cus() {
 // 256-row tiles leave about half the CUs idle, which is what those runs show.
 // 224-row tiles: each weight panel is re-read 8/7 as often per flop as with 256-row tiles.  At
 // 3,584 rows they give 256 workgroups instead of 224 (ff linear1, q/k/v, pointwise_conv1, ff
-// linear2 with 2 splits); with the fragments read one step ahead the config-3 step went 8.02 ->
-// 7.95 ms (the same fragment schedule with 256-row tiles only: 8.05 ms).
+// linear2 with 2 splits); with the fragments read one step ahead that step went 8.02 -> 7.95 ms
+// (the same fragment schedule with 256-row tiles only: 8.05 ms).
 constexpr double C224 = 1.05;
 BigTile big_tile(int M, int N, int K, bool partial, int heights_mask) {
     static const double cost_256[5] = {0.0, 0.0, 1.36, 1.28, 1.0};
