@@ -1324,10 +1324,11 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
         boff[tb] = 16 * wave + 16 * tb + col + 64 * dch[tb];
     }
 
-    // m: the query's exponent offset (a running maximum of its unscaled scores, raised lazily); l:
-    // this lane's share (its 4 keys of each 16) of the running sum, all 4 lanes of a query rescaled
-    // alike, summed at the end
-    float m = -INFINITY, l = 0.0f;
+    // m: the query's exponent offset (a running maximum of its unscaled scores, raised lazily)
+    float m = -INFINITY;
+    // the query's running sum of its bf16 probabilities, on the matrix cores: every element of
+    // ones(16 x 32) . P^T is the sum over the piece's 32 keys, so each lane holds its query's total
+    f32x4_t lacc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     f32x4_t oacc[8];                          // out^T: lane holds channels 16dt + 4g + r of query col
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) oacc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1444,7 +1445,7 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
         if (__any(grow)) {
             const float nm = grow ? mx : m;
             const float corr = (m == -INFINITY || !grow) ? 1.0f : __builtin_amdgcn_exp2f((m - nm) * c2);
-            l *= corr;
+            lacc *= corr;
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) oacc[dt] *= corr;
             m = nm;
@@ -1457,7 +1458,6 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 sc[ts][r] = __builtin_amdgcn_exp2f(fmaf(sc[ts][r], c2, -mc));
-                l += sc[ts][r];
             }
 
         // ---- out^T += V^T . P^T per 32-key piece (tiles 2kk, 2kk + 1).  B = this lane's
@@ -1471,6 +1471,8 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
             const uint4 pb = make_uint4(pack_bf16x2(p0[0], p0[1]), pack_bf16x2(p0[2], p0[3]),
                                         pack_bf16x2(p1[0], p1[1]), pack_bf16x2(p1[2], p1[3]));
             const int k0 = 32 * kk + 4 * g + (col >> 2);
+            lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u)),
+                                                          as_bf16x8(pb), lacc, 0, 0, 0);
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
                 const int c0 = 16 * dt + 4 * (col & 3);
@@ -1493,7 +1495,7 @@ __global__ __launch_bounds__(512) void relpos_dense_kernel(DenseArgs a) {
 
     // ---- output: out[iw + col][16dt + 4g .. +3] (0 for an empty key range): 8-byte stores
     T* O = static_cast<T*>(a.out) + (int64_t)b * Tn * D + h * DK;
-    l = xadd32(xadd16(l));
+    const float l = lacc[0];
     if (qi < Tn) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
