@@ -51,8 +51,8 @@ __device__ __forceinline__ void lds_direct16_rows(const int32_t* src, int32_t* d
 // whether the row is masked (written as zero).
 __device__ __forceinline__ int64_t subflat_dst(const GemmArgs& a, int64_t m, int n, bool& masked) {
     const SubFlat& f = a.flat;
-    const int per = f.T3 * f.F3;
-    const int s = (int)(m / per), rem = (int)(m - (int64_t)s * per), t3 = rem / f.F3, f3 = rem - t3 * f.F3;
+    const int per = f.T3 * f.F3, mi = (int)m;                 // M < 2^31 (launch_gemm)
+    const int s = mi / per, rem = mi - s * per, t3 = rem / f.F3, f3 = rem - t3 * f.F3;
     masked = t3 >= f.vlen[4 * s + 3];
     if (t3 < f.drop) return -1;
     return frag_index((int64_t)s * f.T + t3 - f.drop, f3 * a.N + n, f.F3 * a.N / 64);
@@ -96,12 +96,13 @@ __device__ __forceinline__ void mma_frag(const Frag<MT, NT>& f, f32x4_t (&acc)[N
 }
 
 // Grid: (N/16) x ceil(M/(16*MT)) x ksplit workgroups of WK waves.  The host guarantees
-// K % (64 * WK * ksplit) == 0.  The epilogue kind and activation are template parameters: a
+// K % (64 * ksplit) == 0 and at least WK 64-deep chunks per split: wave w takes chunks w, w + WK,
+// .. of its split, so when WK does not divide the chunk count the first waves take one more.  The epilogue kind and activation are template parameters: a
 // runtime-switched, fully unrolled epilogue measured ~3.5 us slower per launch on MI355X (its
 // code does not stay in the instruction cache).
 template <int MT, int WK, int EPI, int ACT, int NT, bool H = false, bool BIAS = false>
 __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, g = lane >> 4;
     const int nN = a.N / (16 * NT), nM = (a.M + 16 * MT - 1) / (16 * MT);
     const int ks = a.ksplit;
@@ -138,7 +139,7 @@ __global__ __launch_bounds__(64 * WK, 1) void gemm_bf16_kernel(GemmArgs a) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) acc[j][mt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int cnt = kper / WK;            // chunks per wave (>= 1)
+    const int cnt = (kper - wave + WK - 1) / WK;   // chunks of this wave (>= 1)
     constexpr int STEP = WK * 1024;       // element stride between a wave's consecutive chunks
     auto off = [&](int i) { return (int64_t)i * STEP; };
     Frag<MT, NT> f0, f1;
@@ -672,7 +673,7 @@ int launch_gemm_f32_small(const GemmArgs& a, int ks, hipStream_t st) {
 
 template <int MT, int WK, int NT, int EPI, int ACT, bool H = false, bool BIAS = false>
 static int launch_bf16_cfg(GemmArgs a, int ksplit, hipStream_t st) {
-    if (a.N % (16 * NT) != 0 || ksplit < 1 || a.K % (64 * WK * ksplit) != 0) return -2;
+    if (a.N % (16 * NT) != 0 || ksplit < 1 || a.K % (64 * ksplit) != 0 || a.K / (64 * ksplit) < WK) return -2;
     if (ksplit > 1 && EPI != EPI_PARTIAL) return -2;
     if (EPI == EPI_STORE_FRAG && a.N % 64 != 0) return -2;
     a.ksplit = ksplit;
@@ -811,13 +812,19 @@ static int launch_act(const GemmArgs& a, int ks, hipStream_t st) {
 // their epilogues larger and cost ~2 us per launch at 128 rows.
 template <int EPI, int ACT>
 static int launch_f16(const GemmArgs& a, hipStream_t st) {
+    // (the subsampling's out Linear at 128 rows: K = 4,352 is 68 chunks, 8 or 9 per wave over 256
+    // workgroups of 8 waves; with 4 waves of 17 chunks over 64 workgroups it took ~4 us longer)
+    if (a.M <= 128 && a.N % 16 == 0 && a.K % 64 == 0 && a.K >= 512)
+        return launch_bf16_cfg<2, 8, 1, EPI, ACT, true, true>(a, 1, st);
     if (a.M <= 128 && a.N % 32 == 0 && a.K % 256 == 0) return launch_bf16_cfg<4, 4, 2, EPI, ACT, true, true>(a, 1, st);
     // The LDS kernel's 256-row tiles leave most CUs idle below ~64 tiles (the second pointwise conv
     // of 64 streams x 160 ms: 4,352 x 256 x 256, 34 tiles, 10.5 us; the register kernel's 64 x 32
-    // tiles 6.6 us).
+    // tiles 6.6 us, 11.7 us once its epilogue wrote the out Linear's flattened rows, 8.2 us with 4
+    // waves of one 64-deep chunk each instead of 2 of two).
     const BigTile b256 = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false, TILE_256) : BigTile{0, 1, 16};
     if (b256.nt != 0 && (int64_t)((a.M + 255) / 256) * (a.N / (64 * b256.nt)) < 64 && a.N % 32 == 0 && a.K % 128 == 0)
-        return launch_bf16_cfg<4, 2, 2, EPI, ACT, true, true>(a, 1, st);
+        return a.K >= 256 ? launch_bf16_cfg<4, 4, 2, EPI, ACT, true, true>(a, 1, st)
+                          : launch_bf16_cfg<4, 2, 2, EPI, ACT, true, true>(a, 1, st);
     const BigTile bt = a.M >= LDS_MIN_ROWS ? big_tile(a.M, a.N, a.K, false, TILE_256 | TILE_128) : BigTile{0, 1, 16};
     const int nt = bt.nt;
     if (a.M >= LDS_MIN_ROWS) {
@@ -923,6 +930,7 @@ static int launch_bf16(const GemmArgs& a, int ks, hipStream_t st) {
             case EPI_STORE: return launch_f16_act<EPI_STORE>(a, st);
             case EPI_SUBFLAT:
                 if (!a.flat.vlen || a.flat.T3 < 1 || a.flat.F3 < 1 || a.flat.drop < 0 || a.flat.T != a.flat.T3 - a.flat.drop ||
+                    (int64_t)a.M >= (1ll << 31) ||
                     (int64_t)a.M != (int64_t)a.M / (a.flat.T3 * a.flat.F3) * a.flat.T3 * a.flat.F3 || (a.flat.F3 * a.N) % 64)
                     return -2;
                 return launch_f16_act<EPI_SUBFLAT>(a, st);

@@ -41,15 +41,19 @@ __device__ __forceinline__ void store_a(void* A, int64_t m, int col, int cols, f
 // values they need in registers: output position f2 adds conv.0 columns 2 f2 - 1 and 2 f2, which
 // read mel columns 4 f2 - 4 .. 4 f2, of which 4 f2 - 3 .. 4 f2 are new -- one aligned 16-byte
 // LDS read per mel row (patch column = mel column + 3).
+// With NS > 1 the row's F2 positions are split into NS runs, one per group of SUB_C threads (for
+// launches too small to fill the chip: the chain of positions is each thread's latency).  A run
+// starting at p0 > 0 first computes position p0 - 1 without storing it: that iteration leaves the
+// window's last conv.0 column (2 p0 - 2) and mel column 4 p0 - 4 where the next one expects them.
 constexpr int SUB_PW = 132;       // 3 + 128 mel columns + 1, a multiple of 4
 
-template <bool H>
-__global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
-    const int c = threadIdx.x;
+template <bool H, int NS>
+__global__ __launch_bounds__(SUB_C * NS) void sub_conv01_kernel(SubArgs a) {
+    const int c = threadIdx.x % SUB_C, run = threadIdx.x / SUB_C;
     const int t2 = blockIdx.x % a.T2, s = blockIdx.x / a.T2;
     const int v0 = a.vlen[s * 4 + 0], v1 = a.vlen[s * 4 + 1];
     __shared__ __align__(16) float patch[7][SUB_PW];
-    for (int i = c; i < 7 * SUB_PW; i += SUB_C) {
+    for (int i = threadIdx.x; i < 7 * SUB_PW; i += SUB_C * NS) {
         const int pr = i / SUB_PW, q = i % SUB_PW - 3;
         const int r = 4 * t2 - 6 + pr;
         float v = 0.0f;
@@ -85,7 +89,8 @@ __global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
 #pragma unroll
     for (int kh = 0; kh < 3; kh++) win[kh][2] = 0.0f;     // column -2
     const int64_t row0 = ((int64_t)s * a.T2 + t2) * a.F2;
-    for (int f2 = 0; f2 < a.F2; f2++) {
+    const int per = (a.F2 + NS - 1) / NS, p0 = run * per, p1 = min(a.F2, p0 + per);
+    for (int f2 = p0 > 0 ? p0 - 1 : 0; f2 < p1; f2++) {
 #pragma unroll
         for (int r = 0; r < 7; r++) {
             const float4 v = *reinterpret_cast<const float4*>(&patch[r][4 * f2]);
@@ -101,7 +106,7 @@ __global__ __launch_bounds__(SUB_C) void sub_conv01_kernel(SubArgs a) {
 #pragma unroll
             for (int kw = 0; kw < 3; kw++) acc += w2[kh * 3 + kw] * win[kh][kw];
         }
-        store_a<H>(a.out, row0 + f2, c, SUB_C, acc);
+        if (f2 >= p0) store_a<H>(a.out, row0 + f2, c, SUB_C, acc);
     }
 }
 
@@ -207,8 +212,15 @@ int launch_sub_conv01(const SubArgs& a, bool half, hipStream_t st) {
     if (a.F0 + 3 > SUB_PW || 4 * a.F2 > SUB_PW || a.F1 > 2 * a.F2) return -2;
     const int blocks = a.n * a.T2;
     if (blocks <= 0) return 0;
-    if (half) hipLaunchKernelGGL(sub_conv01_kernel<true>, dim3(blocks), dim3(SUB_C), 0, st, a);
-    else hipLaunchKernelGGL(sub_conv01_kernel<false>, dim3(blocks), dim3(SUB_C), 0, st, a);
+    // below ~4 workgroups per CU, two runs per row (the first position of the second run computed
+    // twice)
+    if (blocks < 1024) {
+        if (half) hipLaunchKernelGGL((sub_conv01_kernel<true, 2>), dim3(blocks), dim3(2 * SUB_C), 0, st, a);
+        else hipLaunchKernelGGL((sub_conv01_kernel<false, 2>), dim3(blocks), dim3(2 * SUB_C), 0, st, a);
+    } else {
+        if (half) hipLaunchKernelGGL((sub_conv01_kernel<true, 1>), dim3(blocks), dim3(SUB_C), 0, st, a);
+        else hipLaunchKernelGGL((sub_conv01_kernel<false, 1>), dim3(blocks), dim3(SUB_C), 0, st, a);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
