@@ -49,7 +49,7 @@ constexpr int SUB_PW = 132;       // 3 + 128 mel columns + 1, a multiple of 4
 
 template <bool H, int NS>
 __global__ __launch_bounds__(SUB_C * NS) void sub_conv01_kernel(SubArgs a) {
-    const int c = threadIdx.x % SUB_C, run = threadIdx.x / SUB_C;
+    const int c = NS == 1 ? threadIdx.x : threadIdx.x % SUB_C, run = NS == 1 ? 0 : threadIdx.x / SUB_C;
     const int t2 = blockIdx.x % a.T2, s = blockIdx.x / a.T2;
     const int v0 = a.vlen[s * 4 + 0], v1 = a.vlen[s * 4 + 1];
     __shared__ __align__(16) float patch[7][SUB_PW];
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(SUB_C * NS) void sub_conv01_kernel(SubArgs a) {
 #pragma unroll
     for (int kh = 0; kh < 3; kh++) win[kh][2] = 0.0f;     // column -2
     const int64_t row0 = ((int64_t)s * a.T2 + t2) * a.F2;
-    const int per = (a.F2 + NS - 1) / NS, p0 = run * per, p1 = min(a.F2, p0 + per);
+    const int per = (a.F2 + NS - 1) / NS, p0 = NS == 1 ? 0 : run * per, p1 = NS == 1 ? a.F2 : min(a.F2, p0 + per);
     for (int f2 = p0 > 0 ? p0 - 1 : 0; f2 < p1; f2++) {
 #pragma unroll
         for (int r = 0; r < 7; r++) {
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(SUB_C * NS) void sub_conv01_kernel(SubArgs a) {
 #pragma unroll
             for (int kw = 0; kw < 3; kw++) acc += w2[kh * 3 + kw] * win[kh][kw];
         }
-        if (f2 >= p0) store_a<H>(a.out, row0 + f2, c, SUB_C, acc);
+        if (NS == 1 || f2 >= p0) store_a<H>(a.out, row0 + f2, c, SUB_C, acc);
     }
 }
 
