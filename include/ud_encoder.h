@@ -175,7 +175,7 @@ UD_API int ud_stream_export_cache(const ud_stream* s, int32_t layer, float* k_ho
 UD_API int ud_stream_import_cache(ud_stream* s, int32_t layer, const float* k_host, const float* v_host,
                                   const float* conv_host, int32_t cache_len);
 
-/* ---------------------------------------------------------------- single ops (KATs, config 1) */
+/* ---------------------------------------------------------------- single ops (KATs, one 72-key window) */
 
 /* Replaces Step.relPosAttention (Sources/DictatorEngine/Core/Ops.swift:80-90) and its kernel
  * (Sources/DictatorEngine/Metal/20_conformer.metal:140-220):

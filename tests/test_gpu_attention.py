@@ -1,5 +1,5 @@
-"""GPU parity of the fused rel-pos attention kernel through the C ABI: the reference KAT, config 1
-(fp32, 2 queries over 72 keys, 8 x 128) and bf16, multi-block keys, the ring-cache form with its
+"""GPU parity of the fused rel-pos attention kernel through the C ABI: the reference KAT, one
+72-key window (fp32, 2 queries over 72 keys, 8 x 128) and bf16, multi-block keys, the ring-cache form with its
 bit-exact cache update."""
 import numpy as np
 import pytest
@@ -40,7 +40,7 @@ def test_relpos_kat_fp32(gpu, orc):
     assert np.abs(got - kat_attention_reference(d)).max() < 1e-5
 
 
-def _config1_inputs(orc, seed=7, Tk=72, Tq=2, H=8, dk=128):
+def _window_inputs(orc, seed=7, Tk=72, Tq=2, H=8, dk=128):
     rng = np.random.default_rng(seed)
     D = H * dk
     L = Tk - Tq
@@ -58,19 +58,19 @@ def _config1_inputs(orc, seed=7, Tk=72, Tq=2, H=8, dk=128):
     return dict(Tq=Tq, Tk=Tk, H=H, dk=dk, q=q, k=k, v=v, u=u, vb=vb, table=table, offset=Tk - 1, ranges=ranges)
 
 
-def test_relpos_config1_fp32(gpu, orc):
-    d = _config1_inputs(orc)
+def test_relpos_window_fp32(gpu, orc):
+    d = _window_inputs(orc)
     ref = orc.relpos_attention(d["q"], d["k"], d["v"], d["table"], d["u"], d["vb"], d["ranges"], d["offset"], d["H"])
     got = _run_op(gpu, d)
     assert harness.rel_err(got, ref) <= 1e-4
 
 
-def test_relpos_config1_bf16(gpu, orc):
-    d = _config1_inputs(orc)
+def test_relpos_window_bf16(gpu, orc):
+    d = _window_inputs(orc)
     r = {n: gpu.round_bf16(d[n]) for n in ("q", "k", "v", "table")}
     ref = orc.relpos_attention(r["q"], r["k"], r["v"], r["table"], d["u"], d["vb"], d["ranges"], d["offset"], d["H"])
     got = _run_op(gpu, d, "bf16")
-    harness.assert_bf16_close(got, ref, "config 1 bf16")
+    harness.assert_bf16_close(got, ref, "72-key window bf16")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])

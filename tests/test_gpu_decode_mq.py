@@ -3,8 +3,8 @@ per sequence, each with its own key range, every K/V page read once for all of t
 reference's attention_mq_split, Sources/DictatorEngine/Metal/30_voxtral.metal:240-338, dispatched
 for 1 < Tq <= 8 by Core/Ops.swift:141-162).  Checked against the oracle (orc_gqa_attention takes
 several queries with their own ranges) and against one call per query: the reference's own KAT
-(Tests/DictatorEngineTests/VoxtralOpTests.swift:42-59, multi-query equals per-query), config 5's
-heads and contexts at 4 queries per sequence, and every tile shape of the MFMA kernel (4 .. 64
+(Tests/DictatorEngineTests/VoxtralOpTests.swift:42-59, multi-query equals per-query), the paged
+decode benchmark's heads and contexts at 4 queries per sequence, and every tile shape of the MFMA kernel (4 .. 64
 query rows per kv head) and of the VALU kernel."""
 import numpy as np
 import pytest
@@ -80,7 +80,7 @@ def test_mq_reference_kat(gpu, orc):
 
 
 def test_mq_decode_shape_four_queries(gpu, orc):
-    """Config 5's heads and contexts (64 sequences, 32 query / 8 kv heads x 128, contexts uniform
+    """The paged decode benchmark's heads and contexts (64 sequences, 32 query / 8 kv heads x 128, contexts uniform
     in 512..4096, bf16 pages of 16) at 4 new positions per sequence: query m sees keys
     [0, ctx - 3 + m) (causal over the new tokens), a sliding-window start on every fifth sequence."""
     ud = gpu

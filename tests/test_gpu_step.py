@@ -69,7 +69,7 @@ def test_step_fp32_full_cache_chunk5(gpu, orc):
 
 
 def test_step_bf16_64_streams_chunk2(gpu, orc):
-    """Config 2's shape (64 streams x 2 frames, L=70, seeded full caches) over 4 layers."""
+    """64 streams x 2 frames (L=70, seeded full caches) over 4 layers."""
     cfg = gpu.EncoderConfig(layers=4, max_chunk=2, max_streams=64, dtype="bf16")
     plan = lambda step, S, T: [T - (s % 3 == 1 and step == 1) for s in range(S)]
     enc, _, _, res = _run_steps(gpu, orc, cfg, S=64, T=2, n_steps=3, seed=41, seed_caches=True, valid_plan=plan)
@@ -87,8 +87,8 @@ def test_step_bf16_24_layers(gpu, orc):
     enc.close()
 
 
-def test_step_bf16_config2_full(gpu, orc):
-    """Config 2 exactly: 64 streams x 2 frames, 24 layers, seeded full caches, two steps (the second
+def test_step_bf16_64_streams_2_frames_full(gpu, orc):
+    """64 streams x 2 frames exactly, 24 layers, seeded full caches, two steps (the second
     with a short final chunk on some streams), against the oracle's fp32 step."""
     cfg = gpu.EncoderConfig(layers=24, max_chunk=2, max_streams=64, dtype="bf16")
     plan = lambda step, S, T: [T - (s % 5 == 2 and step == 1) for s in range(S)]
@@ -127,7 +127,7 @@ def test_step_bf16_mid_rows(gpu, orc):
 
 
 def test_step_bf16_chunk14(gpu, orc):
-    """Config 3's chunk shape (14 frames, 84 keys) on a few streams."""
+    """The 14-frame chunk (84 keys) on a few streams."""
     cfg = gpu.EncoderConfig(layers=2, max_chunk=14, max_streams=8, dtype="bf16")
     plan = lambda step, S, T: [T, 9, T, 0, T, T, 3, T][:S]
     enc, _, _, res = _run_steps(gpu, orc, cfg, S=8, T=14, n_steps=3, seed=61, seed_caches=True, valid_plan=plan)
@@ -149,7 +149,7 @@ def test_step_bf16_chunk14_many_rows(gpu, orc):
 
 
 def test_step_bf16_chunk14_24_layers(gpu, orc):
-    """Config 3's chunk at full depth: 32 streams x 14 frames x 24 layers from seeded full caches,
+    """The 14-frame chunk at full depth: 32 streams x 14 frames x 24 layers from seeded full caches,
     two steps (ragged valid counts on the second), against the oracle's fp32 step -- the bf16
     error accumulated over 24 layers at 84 keys."""
     cfg = gpu.EncoderConfig(layers=24, max_chunk=14, max_streams=32, dtype="bf16")
@@ -162,7 +162,7 @@ def test_step_bf16_chunk14_24_layers(gpu, orc):
 
 def test_step_bf16_chunk14_24_layers_lds_tiles(gpu, orc):
     """24 layers at 148 streams x 14 frames = 2,072 rows: the LDS-staged projection kernel (the
-    config-3 GEMM path) at full depth, two steps from fresh streams."""
+    256-stream x 14-frame GEMM path) at full depth, two steps from fresh streams."""
     cfg = gpu.EncoderConfig(layers=24, max_chunk=14, max_streams=148, dtype="bf16")
     enc, _, _, res = _run_steps(gpu, orc, cfg, S=148, T=14, n_steps=2, seed=67, seed_caches=False)
     for i, (got, ref) in enumerate(res):
@@ -170,8 +170,8 @@ def test_step_bf16_chunk14_24_layers_lds_tiles(gpu, orc):
     enc.close()
 
 
-def test_step_bf16_config3_full(gpu, orc):
-    """Config 3 exactly: 256 streams x 14 frames (84 keys), 24 layers, seeded full caches, two steps
+def test_step_bf16_256_streams_14_frames_full(gpu, orc):
+    """256 streams x 14 frames (84 keys) exactly, 24 layers, seeded full caches, two steps
     (ragged valid counts on the second), against the oracle's fp32 step -- the workload the
     benchmark's chunk-14 line times.  (The 24 x 256 cached K/V windows are dealt from 96 distinct
     N(0,1) draws to keep the host-side set-up short.)"""
@@ -204,7 +204,7 @@ def test_step_bf16_ring_longer_than_window(gpu, orc):
 def test_step_f16_weights(gpu, orc, S, T, layers):
     """The f16-weight encoder (UD_F16): linear weights rounded fp32 -> half directly, as
     WeightConverter.convert(.f16) writes the reference's f16 checkpoint (Core/Convert.swift:76-112),
-    against the oracle given the same f16-rounded weights, at config 2's shape and config 3's chunk,
+    against the oracle given the same f16-rounded weights, at 64 streams x 2 frames and at the 14-frame chunk,
     24 layers, seeded full caches, two steps."""
     cfg = gpu.EncoderConfig(layers=layers, max_chunk=T, max_streams=S, dtype="f16")
     plan = lambda step, S_, T_: [(T_, T_ - 1, T_, 0)[s % 4] if step == 1 else T_ for s in range(S_)]

@@ -65,7 +65,7 @@ def test_subsample_matches_oracle(gpu, orc, dtype, rows, drop):
 
 
 def test_subsample_64_streams_chunk2_shape(gpu, orc):
-    """Config 2's front-end: 64 streams x 25 mel rows (16 new + 9 pre-encode cache) -> 2 frames; the
+    """The 64-stream front-end: 64 streams x 25 mel rows (16 new + 9 pre-encode cache) -> 2 frames; the
     conv.3 GEMM has 64 x 7 x 33 = 14,784 rows (LDS-staged kernel)."""
     ud = gpu
     cfg = ud.EncoderConfig(layers=1, max_chunk=2, max_streams=64, dtype="bf16")
