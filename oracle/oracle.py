@@ -561,3 +561,56 @@ class Streamer:
             if is_last:
                 break
         return out
+
+
+# ---------------------------------------------------------------- SentencePiece detokenizer
+# Pure Python restatement of SentencePieceDecoder (Sources/DictatorCore/Decoding/SentencePiece.swift:
+# 5-31).  Pinned by the sentencepiece package's own decoder on a trained model (byte fallback
+# included), by the Unicode Standard's maximal-subpart example for ill-formed UTF-8, and by
+# hand-built cases of the Swift rules (tests/test_tokenizer.py).
+
+def sp_parse_vocab(data):
+    """SentencePiece.swift:8-13: the vocabulary file's bytes -> pieces (str), id = index.  The text
+    must be UTF-8 (String(contentsOf:encoding: .utf8) throws otherwise: UnicodeDecodeError here).
+    Lines end at a '\n' not preceded by '\r' ("\r\n" is one Swift Character, which '\n' does not
+    match); empty lines are dropped; a line's piece is its first non-empty tab-separated field
+    (Swift's split omits empty subsequences), '' when there is none."""
+    text = bytes(data).decode("utf-8")
+    lines, start = [], 0
+    for i, ch in enumerate(text):
+        if ch == "\n" and not (i > 0 and text[i - 1] == "\r"):
+            lines.append(text[start:i])
+            start = i + 1
+    lines.append(text[start:])
+    pieces = []
+    for line in lines:
+        if not line:
+            continue
+        fields = [f for f in line.split("\t") if f]
+        pieces.append(fields[0] if fields else "")
+    return pieces
+
+
+def sp_decode(pieces, ids):
+    """SentencePiece.swift:17-30: ids -> UTF-8 bytes of the text.  Out-of-range ids are skipped;
+    "<0xHH>" (two hex digits) is a raw byte; <unk>, <s>, </s>, <pad> add nothing; other pieces add
+    their UTF-8 with U+2581 replaced by a space.  The bytes are read as UTF-8 with each maximal
+    ill-formed subpart replaced by U+FFFD (CPython's errors="replace" follows the same Unicode
+    practice as Swift's String(decoding:as:)), and one leading space is dropped."""
+    out = bytearray()
+    hexd = "0123456789abcdefABCDEF"
+    for i in ids:
+        i = int(i)
+        if i < 0 or i >= len(pieces):
+            continue
+        p = pieces[i]
+        if len(p) == 6 and p.startswith("<0x") and p.endswith(">") and p[3] in hexd and p[4] in hexd:
+            out.append(int(p[3:5], 16))
+        elif p in ("<unk>", "<s>", "</s>", "<pad>"):
+            continue
+        else:
+            out += p.replace("\u2581", " ").encode("utf-8")
+    s = bytes(out).decode("utf-8", errors="replace")
+    if s.startswith(" "):
+        s = s[1:]
+    return s.encode("utf-8")

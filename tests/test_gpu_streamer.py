@@ -124,10 +124,24 @@ def test_live_equals_buffered(gpu, orc, la):
     o.run_buffered(mel, frames, frames)
     assert a.tokens(sa) == o.tokens
     assert harness.rel_err(ea, np.concatenate(o.enc_rows)) <= 1e-4
+    # NemotronStreamer.text: the transcript through a SentencePiece vocabulary (a synthetic one for
+    # the 1,025-id decoder: ordinary, byte-fallback and special pieces) equals the oracle's decode
+    pieces = _synthetic_vocab(1025)
+    tok = ud.Tokenizer.from_bytes("".join("%s\t%d\n" % (pc, -k) for k, pc in enumerate(pieces)).encode("utf-8"))
+    assert a.text(sa, tok) == orc.sp_decode(pieces, a.tokens(sa)) == b.text(sb, tok)
+    tok.close()
     a.close()
     b.close()
     dec.close()
     enc.close()
+
+
+def _synthetic_vocab(n):
+    """n SentencePiece-style pieces: specials, the 256 byte-fallback pieces, then word pieces."""
+    rng = np.random.default_rng(5)
+    words = ["".join(rng.choice(list("abcdefghé日▁"), size=int(rng.integers(1, 6)))) for _ in range(n)]
+    pieces = ["<unk>", "<s>", "</s>"] + ["<0x%02X>" % b for b in range(256)] + words
+    return pieces[:n]
 
 
 def test_buffered_valid_frames_and_batching(gpu, orc):

@@ -141,6 +141,13 @@ def _sig(lib):
         "ud_streamer_recorded": (i, [p, _i32, _i32, f, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
         "ud_streamer_stats": (i, [p, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
         "ud_nemotron_step": (i, [p, p, ctypes.POINTER(_vp), _i32, _i32, p, ip, ip, _i32, _i32, p, _i32, ip, p]),
+        "ud_tokenizer_load": (i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+        "ud_tokenizer_parse": (i, [ctypes.c_char_p, ctypes.c_int64, ctypes.POINTER(_vp)]),
+        "ud_tokenizer_destroy": (v, [p]),
+        "ud_tokenizer_size": (i, [p, ip]),
+        "ud_tokenizer_piece": (i, [p, _i32, ctypes.c_char_p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
+        "ud_tokenizer_decode": (i, [p, ip, _i32, ctypes.c_char_p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
+        "ud_streamer_text": (i, [p, _i32, p, ctypes.c_char_p, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -960,6 +967,63 @@ class MelFrontend:
             pass
 
 
+def _sized_bytes(call):
+    """Runs call(buf, cap, len_ptr) once to size the output and once to fill it."""
+    n = ctypes.c_int64(0)
+    _check(call(None, 0, ctypes.byref(n)))
+    buf = ctypes.create_string_buffer(max(1, n.value))
+    _check(call(buf, n.value, ctypes.byref(n)))
+    return buf.raw[:n.value]
+
+
+class Tokenizer:
+    """SentencePieceDecoder (Sources/DictatorCore/Decoding/SentencePiece.swift:5-31) through the C ABI
+    (include/ud_tokenizer.h): host code, no device needed.  Build from a tokenizer.vocab path, or
+    from the file's bytes with Tokenizer.from_bytes.  decode() returns UTF-8 bytes."""
+
+    def __init__(self, vocab_path=None, _handle=None):
+        load_library()
+        if _handle is not None:
+            self.handle = _handle
+            return
+        h = _vp()
+        _check(_lib.ud_tokenizer_load(os.fsencode(vocab_path), ctypes.byref(h)))
+        self.handle = h
+
+    @classmethod
+    def from_bytes(cls, data):
+        load_library()
+        data = bytes(data)
+        h = _vp()
+        _check(_lib.ud_tokenizer_parse(data, len(data), ctypes.byref(h)))
+        return cls(_handle=h)
+
+    def __len__(self):
+        n = _i32(0)
+        _check(_lib.ud_tokenizer_size(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def piece(self, i):
+        return _sized_bytes(lambda buf, cap, n: _lib.ud_tokenizer_piece(self.handle, int(i), buf, cap, n))
+
+    def decode(self, ids):
+        a = np.ascontiguousarray(np.asarray(ids, np.int32).reshape(-1))
+        P = ctypes.POINTER(_i32)
+        ptr = a.ctypes.data_as(P) if a.size else None
+        return _sized_bytes(lambda buf, cap, n: _lib.ud_tokenizer_decode(self.handle, ptr, a.size, buf, cap, n))
+
+    def close(self):
+        if getattr(self, "handle", None):
+            _lib.ud_tokenizer_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Streamer:
     """Cache-aware streaming transcription of many streams at once (include/ud_streamer.h), mirroring
     NemotronStreamer (Sources/DictatorCore/Nemotron/NemotronStreamer.swift): open() gives a stream
@@ -1051,6 +1115,11 @@ class Streamer:
         _check(_lib.ud_streamer_tokens(self.handle, int(sid), out.ctypes.data_as(ctypes.POINTER(_i32)), n.value,
                                        ctypes.byref(n)))
         return [int(t) for t in out[:n.value]]
+
+    def text(self, sid, tokenizer):
+        """NemotronStreamer.text: the stream's tokens so far decoded by `tokenizer` (a Tokenizer), as
+        UTF-8 bytes."""
+        return _sized_bytes(lambda buf, cap, n: _lib.ud_streamer_text(self.handle, int(sid), tokenizer.handle, buf, cap, n))
 
     def recorded(self, sid, which):
         """Recorded kept rows (record = True): which 'enc' [rows, d_model] or 'proj' [rows, hidden]."""

@@ -15,7 +15,7 @@ SRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libud_encoder.so")
-SOURCES = ["attention.hip", "gemm.hip", "norm_conv.hip", "encoder.hip", "runtime.hip", "decode.hip", "subsample.hip", "rnnt.hip", "mel.hip", "peaks.hip", "safetensors.cpp", "streamer.cpp"]
+SOURCES = ["attention.hip", "gemm.hip", "norm_conv.hip", "encoder.hip", "runtime.hip", "decode.hip", "subsample.hip", "rnnt.hip", "mel.hip", "peaks.hip", "safetensors.cpp", "streamer.cpp", "tokenizer.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
