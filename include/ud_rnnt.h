@@ -11,7 +11,9 @@
  * per frame, the cached prediction of RNNT.swift:18-26) runs on the host.
  *
  * Conventions as in ud_encoder.h: 0 or a negative ud_status, ud_last_error() for the message,
- * *_dev device pointers, *_host host pointers.
+ * *_dev device pointers, *_host host pointers.  The calls on one decoder share its workspaces and
+ * run in call order whatever HIP streams they are issued on: a call on a stream other than the
+ * previous call's first makes its stream wait for the previous call's work.
  */
 #ifndef UD_RNNT_H
 #define UD_RNNT_H

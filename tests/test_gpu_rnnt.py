@@ -61,6 +61,33 @@ def test_greedy_matches_oracle_across_calls(gpu, orc, blank_bias):
     r.close()
 
 
+def test_calls_on_alternating_hip_streams(gpu, orc):
+    """joint.enc projections and greedy calls issued on two HIP streams in turn, with no
+    synchronisation by the caller: each call waits for the previous one's work (the shared split-K
+    workspace), so the projections and tokens equal those of the same calls on one stream."""
+    ud = gpu
+    S, rows = 4, 6
+    r, ro, w = _dec(ud, orc, 11, 2.1, S)
+    rng = np.random.default_rng(9)
+    hs = [ud.HipStream(), ud.HipStream()]
+    slots = [2, 0, 3, 1]
+    ost = [ro.state() for _ in range(S)]
+    for call in range(6):
+        enc = rng.standard_normal((S * rows, 1024)).astype(np.float32)
+        eb = ud.DeviceBuffer.from_numpy(enc)
+        pb = ud.DeviceBuffer(S * rows * 640 * 4)
+        r.project(S * rows, eb, pb, hip_stream=hs[call % 2])
+        frames = [rows, rows - 1, 3, rows] if call % 3 else [rows] * S
+        got, cnt = r.greedy(slots, pb, rows, frames, cap=64, hip_stream=hs[(call + 1) % 2])
+        proj = pb.download((S * rows, 640))
+        ref = enc.astype(np.float64) @ w["joint.enc.weight"].astype(np.float64).T + w["joint.enc.bias"]
+        assert harness.rel_err(proj, ref) <= 1e-5, call
+        proj = proj.reshape(S, rows, 640)
+        for b in range(S):
+            assert got[b] == ro.greedy(proj[b, :frames[b]], ost[b])[:64], (call, b)
+    r.close()
+
+
 def test_mel_to_tokens_chain(gpu, orc):
     """Subsampling + 2-layer fp32 encoder step + joint.enc + greedy for 3 streams over 3 chunks
     (first chunk 9 mel rows, then 16 + 9 pre-encode rows with 2 frames dropped), against the

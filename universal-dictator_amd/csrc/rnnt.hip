@@ -203,6 +203,12 @@ struct ud_rnnt {
     int32_t *dpair = nullptr, *dbest = nullptr;   // dpair [2 cap_pairs]: slots of the joint rows, then their rows
     int32_t *hslot_p = nullptr, *hslot_c = nullptr;   // pinned, as dslot_p / dslot_c
     int32_t *hpair = nullptr, *hbest = nullptr;   // pinned: hpair [2 cap_pairs] as dpair, hbest [cap_pairs]
+    // Work order across HIP streams (the calls share the workspaces above): every call that
+    // enqueues device work records done_ev on its stream at its end, and a call on a different
+    // stream first makes its stream wait for done_ev, so calls run in call order.
+    hipEvent_t done_ev = nullptr;
+    hipStream_t last_st = nullptr;
+    bool has_last = false;
 };
 
 static float* ralloc(size_t floats) {
@@ -223,6 +229,7 @@ static void free_rnnt(ud_rnnt* r) {
     for (void* p : {(void*)r->hslot_p, (void*)r->hslot_c, (void*)r->hpair,
                     (void*)r->hbest})
         if (p) (void)hipHostFree(p);
+    if (r->done_ev) (void)hipEventDestroy(r->done_ev);
     delete r;
 }
 
@@ -244,7 +251,8 @@ extern "C" UD_API int ud_rnnt_create(int32_t hidden, int32_t vocab, int32_t laye
               (r->pc = ralloc(S * L * H)) && (r->pg = ralloc(S * H)) && (r->xh = ralloc(S * 2 * H)) &&
               (r->slabs = ralloc((size_t)RNNT_KS * S * gmax)) && (r->dslot_p = (int32_t*)ralloc(2 * S)) &&
               (r->dslot_c = (int32_t*)ralloc(S)) && hipHostMalloc((void**)&r->hslot_p, 2 * S * 4) == hipSuccess &&
-              hipHostMalloc((void**)&r->hslot_c, S * 4) == hipSuccess;
+              hipHostMalloc((void**)&r->hslot_c, S * 4) == hipSuccess &&
+              hipEventCreateWithFlags(&r->done_ev, hipEventDisableTiming) == hipSuccess;
     if (!ok || hipMemset(r->h, 0, S * L * H * 4) != hipSuccess || hipMemset(r->c, 0, S * L * H * 4) != hipSuccess) {
         free_rnnt(r);
         return rfail(UD_ERR_NOMEM, "ud_rnnt_create: device allocation failed");
@@ -345,6 +353,19 @@ extern "C" UD_API int ud_rnnt_reset(ud_rnnt* r, int32_t slot) {
     return UD_OK;
 }
 
+// The start of a call that enqueues device work on `st`: after every earlier call's work.
+static int order_after_last(ud_rnnt* r, hipStream_t st) {
+    if (r->has_last && st != r->last_st) RHIPC(hipStreamWaitEvent(st, r->done_ev, 0));
+    return UD_OK;
+}
+// The end of such a call: done_ev marks the end of its work.
+static int mark_done(ud_rnnt* r, hipStream_t st) {
+    RHIPC(hipEventRecord(r->done_ev, st));
+    r->last_st = st;
+    r->has_last = true;
+    return UD_OK;
+}
+
 // C[n, N] slabs = A[n, K] (row stride lda) . W[N, K]^T, RNNT_KS K splits, fp32.
 static int slab_gemm(float* slabs, const float* A, int lda, const float* W, int n, int N, int K, hipStream_t st,
                      int ks = RNNT_KS) {
@@ -362,9 +383,11 @@ extern "C" UD_API int ud_rnnt_project(ud_rnnt* r, int32_t rows, const float* enc
         return rfail(UD_ERR_STATE, "ud_rnnt_project: joint.enc weights not set");
     if (rows < 1) return rfail(UD_ERR_SHAPE, "ud_rnnt_project: rows must be >= 1");
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    int rc0 = order_after_last(r, st);
+    if (rc0 != UD_OK) return rc0;
     if (rows > r->cap_proj) {
-        // grown between calls only: the caller orders its project calls on one stream, so a
-        // synchronize covers the previous call's use of the old buffer
+        // grown between calls only: st now follows every earlier call's work, so a synchronize
+        // covers the previous call's use of the old buffer
         RHIPC(hipStreamSynchronize(st));
         if (r->pslabs) (void)hipFree(r->pslabs);
         r->cap_proj = 0;
@@ -378,7 +401,7 @@ extern "C" UD_API int ud_rnnt_project(ud_rnnt* r, int32_t rows, const float* enc
     hipLaunchKernelGGL(rnnt_sum_kernel, dim3(rows, (r->H + 63) / 64), dim3(64), 0, st, r->pslabs, ks, rows,
                        r->w[R_ENC_B], out_dev, (const int32_t*)nullptr, r->H);
     RLAUNCH("ud_rnnt_project sum");
-    return UD_OK;
+    return mark_done(r, st);
 }
 
 // The prediction network for rows (slots) without a cached prediction.
@@ -456,8 +479,9 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
         if (frames_host[b] > max_frames) max_frames = frames_host[b];
         n_tokens_host[b] = 0;
     }
-    if ((rc = ensure_pairs(r, n * std::min(max_frames, RNNT_SPEC))) != UD_OK) return rc;
     hipStream_t st = static_cast<hipStream_t>(hip_stream);
+    if ((rc = order_after_last(r, st)) != UD_OK) return rc;
+    if ((rc = ensure_pairs(r, n * std::min(max_frames, RNNT_SPEC))) != UD_OK) return rc;
     const int H = r->H, V = r->V, blank = V - 1;
     std::vector<int> act, t(n, 0), em(n, 0), pred_slots, p0(n), p1(n);
     for (;;) {
@@ -519,5 +543,5 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
         }
     }
     RHIPC(hipStreamSynchronize(st));
-    return UD_OK;
+    return mark_done(r, st);
 }
