@@ -79,7 +79,8 @@ typedef struct {
     int32_t conv_kernel;      /* 9 (causal depthwise conv) */
     int32_t left_context;     /* L = 70 cached frames */
     int32_t max_chunk;        /* largest T per step (position tables cover -(T-1)..L+T-1) */
-    int32_t max_streams;      /* stream pool capacity of this encoder */
+    int32_t max_streams;      /* stream pool capacity of this encoder; max_streams * max_chunk
+                                 <= 1,048,576 step rows */
     int32_t dtype;            /* ud_dtype */
 } ud_encoder_config;
 

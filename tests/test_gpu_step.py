@@ -322,6 +322,9 @@ def test_graph_replay_matches_eager(gpu, orc):
 
 def test_error_paths(gpu, orc):
     ud = gpu
+    with pytest.raises(ud.EngineError) as e:         # step rows past the 32-bit indexing bound
+        ud.Encoder(ud.EncoderConfig(layers=1, max_chunk=16, max_streams=65537, dtype="bf16"))
+    assert e.value.status == -2
     cfg = ud.EncoderConfig(layers=1, max_chunk=2, max_streams=2, dtype="bf16")
     enc = ud.Encoder(cfg)
     s0 = enc.new_stream()

@@ -296,6 +296,9 @@ extern "C" UD_API int ud_encoder_create(const ud_encoder_config* cfg, ud_encoder
     if (c.left_context < 1 || c.max_chunk < 1 || c.max_chunk > 16 || c.max_chunk > c.left_context)
         return fail(UD_ERR_SHAPE, "ud_encoder_create: need 1 <= max_chunk <= min(16, left_context)");
     if (c.max_streams < 1) return fail(UD_ERR_SHAPE, "ud_encoder_create: max_streams must be >= 1");
+    // step rows index the workspaces and kernel grids as 32-bit values
+    if ((int64_t)c.max_streams * c.max_chunk > (1 << 20))
+        return fail(UD_ERR_SHAPE, "ud_encoder_create: max_streams * max_chunk above 1,048,576 rows");
     if (c.dtype != UD_F32 && c.dtype != UD_BF16 && c.dtype != UD_F16)
         return fail(UD_ERR_INVALID, "ud_encoder_create: bad dtype %d", c.dtype);
     int ndev = 0;
