@@ -570,7 +570,9 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
 // C = A[M, K] . W[N, K]^T in fp32 on the fp32 MFMA (v_mfma_f32_16x16x4_f32), for the decoder's
 // weight-streaming shapes (tens of rows against thousands of weight rows).
 //   workgroup = 4 waves; wave w owns the 16 output columns n0 = (4 blockIdx.x + w) * 16 ..
-//   blockIdx.y = K split kz (EPI_PARTIAL slabs); blockIdx.z = block of FS_MT * 16 rows of M
+//   blockIdx.y = K split kz (EPI_PARTIAL slabs); blockIdx.z = block of MT * 16 rows of M (MT = 4,
+//   or the tiles M needs when it is below 64: a greedy iteration after the first often has a few
+//   active streams)
 //   The workgroup's A rows are shared by its 4 waves: per 64-wide K chunk they are staged in LDS
 //   (each thread one float4 per 16 rows), so A crosses L2 once per workgroup, not once per wave.
 //   Per 16-wide k group, lane (c = lane % 16, q = lane / 16) takes W[n0 + c][k + 4q .. 4q + 3] as a
@@ -582,28 +584,29 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs a) {
 constexpr int FS_MT = 4;
 constexpr int FS_KC = 64;                      // K chunk staged in LDS
 
+template <int MT>
 __global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmArgs a, int kper) {
-    __shared__ float4 As[16 * FS_MT][FS_KC / 4 + 1];   // +1: conflict-free column reads
+    __shared__ float4 As[16 * MT][FS_KC / 4 + 1];      // +1: conflict-free column reads
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int c = lane & 15, q = lane >> 4;
     const int n0 = (blockIdx.x * 4 + w) * 16;
     const bool wave_live = n0 < a.N;            // waves past N still help stage A
     const int kz = blockIdx.y;
     const int kb = kz * kper, ke = min(a.K, kb + kper);
-    const int m0 = blockIdx.z * 16 * FS_MT;
+    const int m0 = blockIdx.z * 16 * MT;
     const float* W = static_cast<const float*>(a.W) + (int64_t)min(n0 + c, a.N - 1) * a.ldw + 4 * q;
     const float* A = static_cast<const float*>(a.A);
     // staging: thread tid loads row (tid / 16) + 16 i, float4 column tid % 16 of each chunk
     const int sr = tid >> 4, sc4 = tid & 15;
-    f32x4_t acc[FS_MT];
+    f32x4_t acc[MT];
 #pragma unroll
-    for (int t = 0; t < FS_MT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < MT; t++) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     // registers of the next chunk: loaded one chunk ahead, while the current one is multiplied
-    float4 st[FS_MT], wv[FS_KC / 16], wn[FS_KC / 16];
+    float4 st[MT], wv[FS_KC / 16], wn[FS_KC / 16];
     auto load_chunk = [&](int k0, float4 (&wd)[FS_KC / 16]) {
         const int kn = min(FS_KC, ke - k0);     // a multiple of 16
 #pragma unroll
-        for (int i = 0; i < FS_MT; i++) {
+        for (int i = 0; i < MT; i++) {
             const int m = m0 + sr + 16 * i;
             st[i] = (m < a.M && 4 * sc4 < kn) ? *reinterpret_cast<const float4*>(A + (int64_t)m * a.lda + k0 + 4 * sc4)
                                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -618,7 +621,7 @@ __global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmArgs a, int kpe
         const int kn = min(FS_KC, ke - k0);
         if (k0 != kb) __syncthreads();          // every wave is done with the previous chunk
 #pragma unroll
-        for (int i = 0; i < FS_MT; i++) As[sr + 16 * i][sc4] = st[i];
+        for (int i = 0; i < MT; i++) As[sr + 16 * i][sc4] = st[i];
         __syncthreads();
         if (k0 + FS_KC < ke) load_chunk(k0 + FS_KC, wn);
         if (wave_live) {
@@ -626,7 +629,7 @@ __global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmArgs a, int kpe
             for (int g = 0; g < FS_KC / 16; g++) {
                 if (16 * g >= kn) break;
 #pragma unroll
-                for (int t = 0; t < FS_MT; t++) {
+                for (int t = 0; t < MT; t++) {
                     const float4 xv = As[16 * t + c][4 * g + q];
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.x, wv[g].x, acc[t], 0, 0, 0);
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv.y, wv[g].y, acc[t], 0, 0, 0);
@@ -642,7 +645,7 @@ __global__ __launch_bounds__(256) void gemm_f32_small_kernel(GemmArgs a, int kpe
     if (!wave_live || n >= a.N) return;
     float* C = static_cast<float*>(a.C);
 #pragma unroll
-    for (int t = 0; t < FS_MT; t++)
+    for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int m = m0 + 16 * t + 4 * q + r;
@@ -663,9 +666,15 @@ int launch_gemm_f32_small(const GemmArgs& a, int ks, hipStream_t st) {
     if (a.K % (16 * ks) != 0 || a.lda % 4 != 0 || a.ldw % 4 != 0) return -2;
     if ((reinterpret_cast<uintptr_t>(a.A) | reinterpret_cast<uintptr_t>(a.W)) & 15) return -2;
     const int kper = a.K / ks;
-    dim3 grid((a.N + 63) / 64, ks, (a.M + 16 * FS_MT - 1) / (16 * FS_MT));
+    const int mt = a.M >= 16 * FS_MT ? FS_MT : (a.M + 15) / 16;
+    dim3 grid((a.N + 63) / 64, ks, (a.M + 16 * mt - 1) / (16 * mt));
     if (grid.z > 65535) return -2;
-    hipLaunchKernelGGL(gemm_f32_small_kernel, grid, dim3(256), 0, st, a, kper);
+    switch (mt) {
+        case 1: hipLaunchKernelGGL(gemm_f32_small_kernel<1>, grid, dim3(256), 0, st, a, kper); break;
+        case 2: hipLaunchKernelGGL(gemm_f32_small_kernel<2>, grid, dim3(256), 0, st, a, kper); break;
+        case 3: hipLaunchKernelGGL(gemm_f32_small_kernel<3>, grid, dim3(256), 0, st, a, kper); break;
+        default: hipLaunchKernelGGL(gemm_f32_small_kernel<FS_MT>, grid, dim3(256), 0, st, a, kper); break;
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
