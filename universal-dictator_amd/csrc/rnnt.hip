@@ -197,12 +197,14 @@ struct ud_rnnt {
     // split-K slabs of ud_rnnt_project, grown to the largest call
     float* pslabs = nullptr;
     int cap_proj = 0;
-    // device lists of the three phases in separate buffers, each uploaded from its own pinned host
-    // buffer: no upload overwrites a list that an earlier kernel or copy may still read
-    int32_t *dslot_p = nullptr, *dslot_c = nullptr;   // dslot_p [2 S]: n slots, then their n last tokens; dslot_c [S]
-    int32_t *dpair = nullptr, *dbest = nullptr;   // dpair [2 cap_pairs]: slots of the joint rows, then their rows
-    int32_t *hslot_p = nullptr, *hslot_c = nullptr;   // pinned, as dslot_p / dslot_c
-    int32_t *hpair = nullptr, *hbest = nullptr;   // pinned: hpair [2 cap_pairs] as dpair, hbest [cap_pairs]
+    // A greedy iteration's lists, packed and uploaded in one copy from a pinned mirror:
+    // [slots to commit][slots to predict][their last tokens][joint rows' slots][joint rows' proj
+    // rows], 3 S + 2 cap_pairs entries.  The host rewrites the mirror only after the iteration's
+    // synchronize, when the previous copy from it is done.
+    int32_t *dlist = nullptr, *hlist = nullptr;
+    // the joint's argmax per row: pinned, mapped host memory the argmax kernel writes (dbest is its
+    // device address), read after the iteration's synchronize
+    int32_t *hbest = nullptr, *dbest = nullptr;
     // Work order across HIP streams (the calls share the workspaces above): every call that
     // enqueues device work records done_ev on its stream at its end, and a call on a different
     // stream first makes its stream wait for done_ev, so calls run in call order.
@@ -223,11 +225,9 @@ static void free_rnnt(ud_rnnt* r) {
     for (float* p : r->w) if (p) (void)hipFree(p);
     for (float* p : r->wcat) if (p) (void)hipFree(p);
     for (float* p : r->bias) if (p) (void)hipFree(p);
-    void* ps[] = {r->h, r->c, r->ph, r->pc, r->pg, r->xh, r->slabs, r->hsum, r->jslabs, r->pslabs, r->dslot_p, r->dpair,
-                  r->dslot_c, r->dbest};
+    void* ps[] = {r->h, r->c, r->ph, r->pc, r->pg, r->xh, r->slabs, r->hsum, r->jslabs, r->pslabs, r->dlist};
     for (void* p : ps) if (p) (void)hipFree(p);
-    for (void* p : {(void*)r->hslot_p, (void*)r->hslot_c, (void*)r->hpair,
-                    (void*)r->hbest})
+    for (void* p : {(void*)r->hlist, (void*)r->hbest})
         if (p) (void)hipHostFree(p);
     if (r->done_ev) (void)hipEventDestroy(r->done_ev);
     delete r;
@@ -249,9 +249,7 @@ extern "C" UD_API int ud_rnnt_create(int32_t hidden, int32_t vocab, int32_t laye
     const size_t gmax = 4 * H > V ? 4 * H : V;
     bool ok = (r->h = ralloc(S * L * H)) && (r->c = ralloc(S * L * H)) && (r->ph = ralloc(S * L * H)) &&
               (r->pc = ralloc(S * L * H)) && (r->pg = ralloc(S * H)) && (r->xh = ralloc(S * 2 * H)) &&
-              (r->slabs = ralloc((size_t)RNNT_KS * S * gmax)) && (r->dslot_p = (int32_t*)ralloc(2 * S)) &&
-              (r->dslot_c = (int32_t*)ralloc(S)) && hipHostMalloc((void**)&r->hslot_p, 2 * S * 4) == hipSuccess &&
-              hipHostMalloc((void**)&r->hslot_c, S * 4) == hipSuccess &&
+              (r->slabs = ralloc((size_t)RNNT_KS * S * gmax)) &&
               hipEventCreateWithFlags(&r->done_ev, hipEventDisableTiming) == hipSuccess;
     if (!ok || hipMemset(r->h, 0, S * L * H * 4) != hipSuccess || hipMemset(r->c, 0, S * L * H * 4) != hipSuccess) {
         free_rnnt(r);
@@ -405,27 +403,23 @@ extern "C" UD_API int ud_rnnt_project(ud_rnnt* r, int32_t rows, const float* enc
 }
 
 // The prediction network for rows (slots) without a cached prediction.
-static int predict(ud_rnnt* r, const std::vector<int>& slots, hipStream_t st) {
+// dslots: the slots on the device, then their last tokens (uploaded with the iteration's lists).
+static int predict(ud_rnnt* r, const std::vector<int>& slots, const int32_t* dslots, hipStream_t st) {
     const int n = (int)slots.size(), H = r->H, L = r->L;
-    for (int i = 0; i < n; i++) {
-        r->hslot_p[i] = slots[i];
-        r->hslot_p[n + i] = r->last[slots[i]];
-    }
-    RHIPC(hipMemcpyAsync(r->dslot_p, r->hslot_p, (size_t)2 * n * 4, hipMemcpyHostToDevice, st));   // slots + tokens
-    hipLaunchKernelGGL(rnnt_embed_kernel, dim3(n), dim3(256), 0, st, r->w[R_EMBED], r->dslot_p, r->dslot_p + n, r->h, r->xh, H, L,
+    hipLaunchKernelGGL(rnnt_embed_kernel, dim3(n), dim3(256), 0, st, r->w[R_EMBED], dslots, dslots + n, r->h, r->xh, H, L,
                        r->V - 1);
     RLAUNCH("rnnt embed");
     for (int l = 0; l < L; l++) {
         int rc = slab_gemm(r->slabs, r->xh, 2 * H, r->wcat[l], n, 4 * H, 2 * H, st);
         if (rc != UD_OK) return rc;
         hipLaunchKernelGGL(rnnt_cell_kernel, dim3(n, (H + 63) / 64), dim3(64), 0, st, r->slabs, RNNT_KS, n, r->bias[l], r->h, r->c,
-                           r->ph, r->pc, r->xh, r->dslot_p, H, L, l);
+                           r->ph, r->pc, r->xh, dslots, H, L, l);
         RLAUNCH("rnnt cell");
     }
     int rc = slab_gemm(r->slabs, r->xh, 2 * H, r->w[R_PRED_W], n, H, H, st);
     if (rc != UD_OK) return rc;
     hipLaunchKernelGGL(rnnt_sum_kernel, dim3(n, (H + 63) / 64), dim3(64), 0, st, r->slabs, RNNT_KS, n, r->w[R_PRED_B], r->pg,
-                       r->dslot_p, H);
+                       dslots, H);
     RLAUNCH("rnnt pred");
     for (int s : slots) r->pending[s] = 1;
     return UD_OK;
@@ -435,16 +429,17 @@ static int predict(ud_rnnt* r, const std::vector<int>& slots, hipStream_t st) {
 // with a stream synchronize), so nothing in flight uses the old buffers.
 static int ensure_pairs(ud_rnnt* r, int P) {
     if (P <= r->cap_pairs) return UD_OK;
-    void* ds[] = {r->hsum, r->jslabs, r->dpair, r->dbest};
+    void* ds[] = {r->hsum, r->jslabs, r->dlist};
     for (void* p : ds) if (p) (void)hipFree(p);
-    for (void* p : {(void*)r->hpair, (void*)r->hbest}) if (p) (void)hipHostFree(p);
+    for (void* p : {(void*)r->hlist, (void*)r->hbest}) if (p) (void)hipHostFree(p);
     r->hsum = r->jslabs = nullptr;
-    r->dpair = r->dbest = r->hpair = r->hbest = nullptr;
+    r->dlist = r->hlist = r->hbest = r->dbest = nullptr;
     r->cap_pairs = 0;
-    const size_t n = (size_t)P;
+    const size_t n = (size_t)P, nl = 3 * (size_t)r->S + 2 * n;
     bool ok = (r->hsum = ralloc(n * r->H)) && (r->jslabs = ralloc((size_t)RNNT_KS * n * r->V)) &&
-              (r->dpair = (int32_t*)ralloc(2 * n)) && (r->dbest = (int32_t*)ralloc(n)) &&
-              hipHostMalloc((void**)&r->hpair, 2 * n * 4) == hipSuccess && hipHostMalloc((void**)&r->hbest, n * 4) == hipSuccess;
+              (r->dlist = (int32_t*)ralloc(nl)) && hipHostMalloc((void**)&r->hlist, nl * 4) == hipSuccess &&
+              hipHostMalloc((void**)&r->hbest, n * 4, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess &&
+              hipHostGetDevicePointer((void**)&r->dbest, r->hbest, 0) == hipSuccess;
     if (!ok) return rfail(UD_ERR_NOMEM, "ud_rnnt_greedy: joint workspace allocation failed (%d pairs)", P);
     r->cap_pairs = P;
     return UD_OK;
@@ -483,7 +478,18 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
     if ((rc = order_after_last(r, st)) != UD_OK) return rc;
     if ((rc = ensure_pairs(r, n * std::min(max_frames, RNNT_SPEC))) != UD_OK) return rc;
     const int H = r->H, V = r->V, blank = V - 1;
-    std::vector<int> act, t(n, 0), em(n, 0), pred_slots, p0(n), p1(n);
+    std::vector<int> act, t(n, 0), em(n, 0), pred_slots, commit, p0(n), p1(n);
+    int32_t* hl = r->hlist;
+    // the commits of the previous iteration's emissions, uploaded with the next lists (or alone at
+    // the end) and applied before its predictions, which read the committed states
+    auto launch_commit = [&](int oc) -> int {
+        if (commit.empty()) return UD_OK;
+        hipLaunchKernelGGL(rnnt_commit_kernel, dim3((unsigned)commit.size()), dim3(256), 0, st, r->ph, r->pc, r->h, r->c,
+                           r->dlist + oc, r->L * H);
+        RLAUNCH("rnnt commit");
+        commit.clear();
+        return UD_OK;
+    };
     for (;;) {
         act.clear();
         for (int b = 0; b < n; b++)
@@ -492,28 +498,35 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
         pred_slots.clear();
         for (int b : act)
             if (!r->pending[slots_host[b]]) pred_slots.push_back(slots_host[b]);
-        if (!pred_slots.empty() && (rc = predict(r, pred_slots, st)) != UD_OK) return rc;
         int m = 0;
         for (int b : act) {
             p0[b] = m;
             m += std::min(frames_host[b], t[b] + RNNT_SPEC) - t[b];
             p1[b] = m;
         }
-        // the joint rows' slots, then their proj rows: one upload
+        // one upload: commits, predictions (slots, last tokens), joint rows (slots, proj rows)
+        int off = 0;
+        const int oc = off;
+        for (int s : commit) hl[off++] = s;
+        const int op = off;
+        for (int s : pred_slots) hl[off++] = s;
+        for (int s : pred_slots) hl[off++] = r->last[s];
+        const int oq = off;
         for (int b : act)
-            for (int p = p0[b]; p < p1[b]; p++) {
-                r->hpair[p] = slots_host[b];
-                r->hpair[m + p] = b * rows_per_stream + t[b] + (p - p0[b]);
-            }
-        RHIPC(hipMemcpyAsync(r->dpair, r->hpair, (size_t)2 * m * 4, hipMemcpyHostToDevice, st));
-        hipLaunchKernelGGL(rnnt_joint_in_kernel, dim3(m), dim3(256), 0, st, proj_dev, r->dpair + m, r->pg, r->dpair, r->hsum, H);
+            for (int p = p0[b]; p < p1[b]; p++) hl[oq + p] = slots_host[b];
+        for (int b : act)
+            for (int p = p0[b]; p < p1[b]; p++) hl[oq + m + p] = b * rows_per_stream + t[b] + (p - p0[b]);
+        off = oq + 2 * m;
+        RHIPC(hipMemcpyAsync(r->dlist, hl, (size_t)off * 4, hipMemcpyHostToDevice, st));
+        if ((rc = launch_commit(oc)) != UD_OK) return rc;
+        if (!pred_slots.empty() && (rc = predict(r, pred_slots, r->dlist + op, st)) != UD_OK) return rc;
+        const int32_t* dq = r->dlist + oq;
+        hipLaunchKernelGGL(rnnt_joint_in_kernel, dim3(m), dim3(256), 0, st, proj_dev, dq + m, r->pg, dq, r->hsum, H);
         RLAUNCH("rnnt joint input");
         if ((rc = slab_gemm(r->jslabs, r->hsum, H, r->w[R_OUT_W], m, V, H, st)) != UD_OK) return rc;
         hipLaunchKernelGGL(rnnt_argmax_kernel, dim3(m), dim3(256), 0, st, r->jslabs, RNNT_KS, m, r->w[R_OUT_B], r->dbest, V);
         RLAUNCH("rnnt argmax");
-        RHIPC(hipMemcpyAsync(r->hbest, r->dbest, m * 4, hipMemcpyDeviceToHost, st));
         RHIPC(hipStreamSynchronize(st));
-        int nc = 0;
         for (int b : act) {
             const int s = slots_host[b];
             for (int p = p0[b]; p < p1[b]; p++) {
@@ -527,7 +540,7 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
                 n_tokens_host[b]++;
                 r->last[s] = k;
                 r->pending[s] = 0;
-                r->hslot_c[nc++] = s;
+                commit.push_back(s);
                 if (++em[b] >= r->max_sym) {
                     t[b] = tt + 1;
                     em[b] = 0;
@@ -535,12 +548,11 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
                 break;
             }
         }
-        if (nc) {
-            RHIPC(hipMemcpyAsync(r->dslot_c, r->hslot_c, nc * 4, hipMemcpyHostToDevice, st));
-            hipLaunchKernelGGL(rnnt_commit_kernel, dim3((unsigned)nc), dim3(256), 0, st, r->ph, r->pc, r->h, r->c,
-                               r->dslot_c, r->L * H);
-            RLAUNCH("rnnt commit");
-        }
+    }
+    if (!commit.empty()) {
+        for (size_t i = 0; i < commit.size(); i++) hl[i] = commit[i];
+        RHIPC(hipMemcpyAsync(r->dlist, hl, commit.size() * 4, hipMemcpyHostToDevice, st));
+        if ((rc = launch_commit(0)) != UD_OK) return rc;
     }
     RHIPC(hipStreamSynchronize(st));
     return mark_done(r, st);
