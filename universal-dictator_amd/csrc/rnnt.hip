@@ -8,14 +8,17 @@
 // the following pointwise kernel sums in a fixed order (deterministic, no atomics):
 //
 //   predict (streams without a cached prediction):
-//     rnnt_embed_kernel        xh = [embed(last token) ; h_0]
+//     rnnt_embed_kernel        h, c <- cached state for a stream that just emitted (the commit of
+//                              RNNT.swift:144-147); xh = [embed(last token) ; h_0]
 //     per layer: GEMM xh . [W_ih | W_hh]^T -> slabs;  rnnt_cell_kernel: gates = b + sum(slabs),
 //                c' = f c + i g, h' = o tanh(c') -> cached state; xh = [h' ; h_{l+1}]
-//     GEMM h_top . W_pred^T -> slabs;  rnnt_sum_kernel -> cached projection g
+//     GEMM h_top . W_pred^T -> slabs
 //   joint (every remaining frame of every active stream, under its current prediction):
-//     rnnt_joint_in_kernel     relu(f_t + g)
-//     GEMM . W_out^T -> slabs; rnnt_argmax_kernel: logits = b + sum(slabs), first index of the max
-//   commit (streams that emitted a token): rnnt_commit_kernel, h, c <- cached state
+//     rnnt_joint_in_kernel     g = b + sum(slabs) for a stream predicted now (cached), else the
+//                              cached g; relu(f_t + g)
+//     GEMM . W_out^T -> slabs; rnnt_argmax_kernel: logits = b + sum(slabs), first index of the max,
+//                              into mapped host memory
+//   commit of a stream that emitted and is not predicted next: rnnt_commit_kernel
 //
 // The host keeps the greedy control (RNNT.swift:125-151): blank ends a frame, at most
 // max_symbols tokens per frame, and the prediction for the last token is cached until a token is
@@ -45,14 +48,25 @@ constexpr int RNNT_KS = 4;          // K splits of the decoder GEMMs
 
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// xh[b] = [x ; h[slot][0]] with x = embed[tok] (zeros for blank, NeMo's padding row).
+// xh[b] = [x ; h[slot][0]] with x = embed[tok] (zeros for blank, NeMo's padding row).  A slot
+// whose token was just emitted (commit[b]) first takes its cached state: h, c <- ph, pc over all
+// layers (RNNT.swift:144-147), and its row reads h from ph (the same values).
 __global__ void rnnt_embed_kernel(const float* __restrict__ embed, const int32_t* __restrict__ slot,
-                                  const int32_t* __restrict__ tok, const float* __restrict__ h, float* __restrict__ xh,
-                                  int H, int L, int blank) {
+                                  const int32_t* __restrict__ tok, const int32_t* __restrict__ commit,
+                                  const float* __restrict__ ph, const float* __restrict__ pc, float* __restrict__ h,
+                                  float* __restrict__ c, float* __restrict__ xh, int H, int L, int blank) {
     const int b = blockIdx.x, s = slot[b], t = tok[b];
+    const bool cm = commit[b] != 0;
+    const int64_t o = (int64_t)s * L * H;
+    if (cm)
+        for (int j = threadIdx.x; j < L * H; j += blockDim.x) {
+            h[o + j] = ph[o + j];
+            c[o + j] = pc[o + j];
+        }
+    const float* hr = (cm ? ph : h) + o;
     for (int j = threadIdx.x; j < H; j += blockDim.x) {
         xh[(int64_t)b * 2 * H + j] = t == blank ? 0.0f : embed[(int64_t)t * H + j];
-        xh[(int64_t)b * 2 * H + H + j] = h[((int64_t)s * L + 0) * H + j];
+        xh[(int64_t)b * 2 * H + H + j] = hr[j];
     }
 }
 
@@ -99,15 +113,29 @@ __global__ void rnnt_sum_kernel(const float* __restrict__ slabs, int ks, int n, 
     }
 }
 
-// hsum[b] = relu(f[erow(b)] + g[slot(b)]).
+// hsum[b] = relu(f[erow(b)] + g) with g the slot's prediction: for a slot predicted in this
+// iteration (prow[b] >= 0, its row in the prediction slabs [ks][npred][H]) bias + the sum of its
+// slabs, which the slot's first row (first[b]) also caches in gc[slot]; otherwise the cached
+// gc[slot(b)].
 __global__ void rnnt_joint_in_kernel(const float* __restrict__ f, const int32_t* __restrict__ erow,
-                                     const float* __restrict__ g, const int32_t* __restrict__ slot,
-                                     float* __restrict__ hsum, int H) {
-    const int b = blockIdx.x;
+                                     float* __restrict__ gc, const int32_t* __restrict__ slot,
+                                     const int32_t* __restrict__ prow, const int32_t* __restrict__ first,
+                                     const float* __restrict__ slabs, int ks, int npred,
+                                     const float* __restrict__ bias, float* __restrict__ hsum, int H) {
+    const int b = blockIdx.x, r = prow[b];
+    const bool st = r >= 0 && first[b] != 0;
     const float* fr = f + (int64_t)erow[b] * H;
-    const float* gr = g + (int64_t)slot[b] * H;
+    float* gr = gc + (int64_t)slot[b] * H;
     for (int j = threadIdx.x; j < H; j += blockDim.x) {
-        const float v = fr[j] + gr[j];
+        float g;
+        if (r >= 0) {
+            g = bias[j];
+            for (int z = 0; z < ks; z++) g += slabs[((int64_t)z * npred + r) * H + j];
+            if (st) gr[j] = g;
+        } else {
+            g = gr[j];
+        }
+        const float v = fr[j] + g;
         hsum[(int64_t)b * H + j] = v > 0.0f ? v : 0.0f;
     }
 }
@@ -197,9 +225,10 @@ struct ud_rnnt {
     // split-K slabs of ud_rnnt_project, grown to the largest call
     float* pslabs = nullptr;
     int cap_proj = 0;
-    // A greedy iteration's lists, packed and uploaded in one copy from a pinned mirror:
-    // [slots to commit][slots to predict][their last tokens][joint rows' slots][joint rows' proj
-    // rows], 3 S + 2 cap_pairs entries.  The host rewrites the mirror only after the iteration's
+    // A greedy iteration's lists, packed and uploaded in one copy from a pinned mirror: [slots to
+    // commit alone][slots to predict][their last tokens][their commit flags][joint rows' slots]
+    // [joint rows' proj rows][joint rows' prediction rows][joint rows' first-of-slot flags],
+    // 4 S + 4 cap_pairs entries.  The host rewrites the mirror only after the iteration's
     // synchronize, when the previous copy from it is done.
     int32_t *dlist = nullptr, *hlist = nullptr;
     // the joint's argmax per row: pinned, mapped host memory the argmax kernel writes (dbest is its
@@ -403,11 +432,13 @@ extern "C" UD_API int ud_rnnt_project(ud_rnnt* r, int32_t rows, const float* enc
 }
 
 // The prediction network for rows (slots) without a cached prediction.
-// dslots: the slots on the device, then their last tokens (uploaded with the iteration's lists).
+// dslots: the slots on the device, then their last tokens, then their commit flags (uploaded with
+// the iteration's lists).  Leaves the joint.pred projection as split-K slabs in r->slabs; the
+// joint input kernel adds them (and caches the sum).
 static int predict(ud_rnnt* r, const std::vector<int>& slots, const int32_t* dslots, hipStream_t st) {
     const int n = (int)slots.size(), H = r->H, L = r->L;
-    hipLaunchKernelGGL(rnnt_embed_kernel, dim3(n), dim3(256), 0, st, r->w[R_EMBED], dslots, dslots + n, r->h, r->xh, H, L,
-                       r->V - 1);
+    hipLaunchKernelGGL(rnnt_embed_kernel, dim3(n), dim3(256), 0, st, r->w[R_EMBED], dslots, dslots + n, dslots + 2 * n,
+                       r->ph, r->pc, r->h, r->c, r->xh, H, L, r->V - 1);
     RLAUNCH("rnnt embed");
     for (int l = 0; l < L; l++) {
         int rc = slab_gemm(r->slabs, r->xh, 2 * H, r->wcat[l], n, 4 * H, 2 * H, st);
@@ -418,9 +449,6 @@ static int predict(ud_rnnt* r, const std::vector<int>& slots, const int32_t* dsl
     }
     int rc = slab_gemm(r->slabs, r->xh, 2 * H, r->w[R_PRED_W], n, H, H, st);
     if (rc != UD_OK) return rc;
-    hipLaunchKernelGGL(rnnt_sum_kernel, dim3(n, (H + 63) / 64), dim3(64), 0, st, r->slabs, RNNT_KS, n, r->w[R_PRED_B], r->pg,
-                       dslots, H);
-    RLAUNCH("rnnt pred");
     for (int s : slots) r->pending[s] = 1;
     return UD_OK;
 }
@@ -435,7 +463,7 @@ static int ensure_pairs(ud_rnnt* r, int P) {
     r->hsum = r->jslabs = nullptr;
     r->dlist = r->hlist = r->hbest = r->dbest = nullptr;
     r->cap_pairs = 0;
-    const size_t n = (size_t)P, nl = 3 * (size_t)r->S + 2 * n;
+    const size_t n = (size_t)P, nl = 4 * (size_t)r->S + 4 * n;
     bool ok = (r->hsum = ralloc(n * r->H)) && (r->jslabs = ralloc((size_t)RNNT_KS * n * r->V)) &&
               (r->dlist = (int32_t*)ralloc(nl)) && hipHostMalloc((void**)&r->hlist, nl * 4) == hipSuccess &&
               hipHostMalloc((void**)&r->hbest, n * 4, hipHostMallocMapped | hipHostMallocCoherent) == hipSuccess &&
@@ -478,16 +506,17 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
     if ((rc = order_after_last(r, st)) != UD_OK) return rc;
     if ((rc = ensure_pairs(r, n * std::min(max_frames, RNNT_SPEC))) != UD_OK) return rc;
     const int H = r->H, V = r->V, blank = V - 1;
-    std::vector<int> act, t(n, 0), em(n, 0), pred_slots, commit, p0(n), p1(n);
+    std::vector<int> act, t(n, 0), em(n, 0), pred_slots, commit, rest, p0(n), p1(n), prow_of(r->S, -1);
+    std::vector<char> to_commit(r->S, 0);
     int32_t* hl = r->hlist;
-    // the commits of the previous iteration's emissions, uploaded with the next lists (or alone at
-    // the end) and applied before its predictions, which read the committed states
-    auto launch_commit = [&](int oc) -> int {
-        if (commit.empty()) return UD_OK;
-        hipLaunchKernelGGL(rnnt_commit_kernel, dim3((unsigned)commit.size()), dim3(256), 0, st, r->ph, r->pc, r->h, r->c,
+    // the commits of the previous iteration's emissions go up with the next lists: a slot predicted
+    // in that iteration takes its state in the embedding kernel, the others in the commit kernel
+    // (alone at the end)
+    auto launch_commit = [&](const std::vector<int>& slots, int oc) -> int {
+        if (slots.empty()) return UD_OK;
+        hipLaunchKernelGGL(rnnt_commit_kernel, dim3((unsigned)slots.size()), dim3(256), 0, st, r->ph, r->pc, r->h, r->c,
                            r->dlist + oc, r->L * H);
         RLAUNCH("rnnt commit");
-        commit.clear();
         return UD_OK;
     };
     for (;;) {
@@ -498,30 +527,49 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
         pred_slots.clear();
         for (int b : act)
             if (!r->pending[slots_host[b]]) pred_slots.push_back(slots_host[b]);
+        for (int s : commit) to_commit[s] = 1;
         int m = 0;
         for (int b : act) {
             p0[b] = m;
             m += std::min(frames_host[b], t[b] + RNNT_SPEC) - t[b];
             p1[b] = m;
         }
-        // one upload: commits, predictions (slots, last tokens), joint rows (slots, proj rows)
+        // one upload: commits, predictions (slots, last tokens, commit flags), joint rows (slots,
+        // proj rows, prediction rows, first-of-slot flags)
         int off = 0;
-        const int oc = off;
-        for (int s : commit) hl[off++] = s;
+        const int np = (int)pred_slots.size();
         const int op = off;
         for (int s : pred_slots) hl[off++] = s;
         for (int s : pred_slots) hl[off++] = r->last[s];
+        for (int i = 0; i < np; i++) {
+            const int s = pred_slots[i];
+            hl[off++] = to_commit[s];
+            to_commit[s] = 0;
+            prow_of[s] = i;
+        }
+        rest.clear();
+        for (int s : commit)
+            if (to_commit[s]) { rest.push_back(s); to_commit[s] = 0; }
+        commit.clear();
+        const int oc = off;
+        for (int s : rest) hl[off++] = s;
         const int oq = off;
         for (int b : act)
-            for (int p = p0[b]; p < p1[b]; p++) hl[oq + p] = slots_host[b];
-        for (int b : act)
-            for (int p = p0[b]; p < p1[b]; p++) hl[oq + m + p] = b * rows_per_stream + t[b] + (p - p0[b]);
-        off = oq + 2 * m;
+            for (int p = p0[b]; p < p1[b]; p++) {
+                const int s = slots_host[b];
+                hl[oq + p] = s;
+                hl[oq + m + p] = b * rows_per_stream + t[b] + (p - p0[b]);
+                hl[oq + 2 * m + p] = prow_of[s];
+                hl[oq + 3 * m + p] = p == p0[b] ? 1 : 0;
+            }
+        off = oq + 4 * m;
+        for (int s : pred_slots) prow_of[s] = -1;
         RHIPC(hipMemcpyAsync(r->dlist, hl, (size_t)off * 4, hipMemcpyHostToDevice, st));
-        if ((rc = launch_commit(oc)) != UD_OK) return rc;
-        if (!pred_slots.empty() && (rc = predict(r, pred_slots, r->dlist + op, st)) != UD_OK) return rc;
+        if ((rc = launch_commit(rest, oc)) != UD_OK) return rc;
+        if (np && (rc = predict(r, pred_slots, r->dlist + op, st)) != UD_OK) return rc;
         const int32_t* dq = r->dlist + oq;
-        hipLaunchKernelGGL(rnnt_joint_in_kernel, dim3(m), dim3(256), 0, st, proj_dev, dq + m, r->pg, dq, r->hsum, H);
+        hipLaunchKernelGGL(rnnt_joint_in_kernel, dim3(m), dim3(256), 0, st, proj_dev, dq + m, r->pg, dq, dq + 2 * m,
+                           dq + 3 * m, r->slabs, RNNT_KS, np, r->w[R_PRED_B], r->hsum, H);
         RLAUNCH("rnnt joint input");
         if ((rc = slab_gemm(r->jslabs, r->hsum, H, r->w[R_OUT_W], m, V, H, st)) != UD_OK) return rc;
         hipLaunchKernelGGL(rnnt_argmax_kernel, dim3(m), dim3(256), 0, st, r->jslabs, RNNT_KS, m, r->w[R_OUT_B], r->dbest, V);
@@ -552,7 +600,7 @@ extern "C" UD_API int ud_rnnt_greedy(ud_rnnt* r, int32_t n, const int32_t* slots
     if (!commit.empty()) {
         for (size_t i = 0; i < commit.size(); i++) hl[i] = commit[i];
         RHIPC(hipMemcpyAsync(r->dlist, hl, commit.size() * 4, hipMemcpyHostToDevice, st));
-        if ((rc = launch_commit(0)) != UD_OK) return rc;
+        if ((rc = launch_commit(commit, 0)) != UD_OK) return rc;
     }
     RHIPC(hipStreamSynchronize(st));
     return mark_done(r, st);
