@@ -455,6 +455,13 @@ def rnnt_bench(ud, args):
     print(json.dumps(result), flush=True)
 
 
+# (regime, blank logit bias of the synthetic joint): every frame blank, every frame at the
+# 10-symbol cap, and a mixed rate of about 0.7 tokens per 160 ms stream-chunk (~4.5 tokens/s, a
+# speech-like rate; the synthetic joint's blank margin is nearly the same on every frame, so the
+# rate moves from 20 to 0 tokens per stream-chunk between biases 1.0 and 1.3)
+STREAM_REGIMES = (("blank", 50.0), ("cap", -50.0), ("mixed", 1.24))
+
+
 def stream_bench(ud, args):
     """Live transcription end to end through the batched streamer (include/ud_streamer.h): every
     timed step pushes one chunk of new samples to each stream (stream: 64 streams x 2560 samples =
@@ -514,7 +521,7 @@ def stream_bench(ud, args):
     log("mel call (job-list copy + kernel): %.1f us per step (%d streams x %d frames)" % (mel_us, S, rows))
     warm = max(args.warmup, 40) if T <= 2 else max(args.warmup // 4, 8)
     res = {}
-    for regime, bias in (("blank", 50.0), ("cap", -50.0)):
+    for regime, bias in STREAM_REGIMES:
         dec = ud.Rnnt(max_streams=S)
         dec.set_weights(ud.synthetic_rnnt_weights(2026, blank_bias=bias))
         st = ud.Streamer(enc, dec, fe, lookahead=la, max_streams=S)
@@ -533,8 +540,8 @@ def stream_bench(ud, args):
         st.push(piece(True))
         for _ in range(warm):
             st.push(piece(False))
-        steps = (args.steps if regime == "blank" else max(5, args.steps // 5)) if T <= 2 else \
-            (max(10, args.steps // 5) if regime == "blank" else 5)
+        steps = (args.steps if regime != "cap" else max(5, args.steps // 5)) if T <= 2 else \
+            (max(10, args.steps // 5) if regime != "cap" else 5)
         b0, c0 = st.stats()
         tok0 = sum(len(st.tokens(i)) for i in ids)
         # each step's push arguments packed ahead (a C or Swift caller passes its pointers as they are)
@@ -571,6 +578,8 @@ def stream_bench(ud, args):
         "mel_us_per_step": round(mel_us, 2),
         "cap_regime_ms_per_step": round(res["cap"][0], 4),
         "cap_regime_tokens_per_stream_chunk": round(res["cap"][1], 3),
+        "mixed_regime_ms_per_step": round(res["mixed"][0], 4),
+        "mixed_regime_tokens_per_stream_chunk": round(res["mixed"][1], 3),
     }
     fe.close()
     enc.close()
