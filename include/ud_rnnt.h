@@ -30,7 +30,8 @@ typedef struct ud_rnnt ud_rnnt;
 
 /* RNNTDecoder.init (RNNT.swift:27-63): hidden 640, vocab 1025 (blank = vocab - 1), 2 LSTM layers,
  * enc_dim 1024 (joint.enc input), max_symbols_per_frame 10; decoder states for `max_streams`
- * stream slots, all in RNNTDecoder.initialState() (RNNT.swift:66-70). */
+ * stream slots, all in RNNTDecoder.initialState() (RNNT.swift:66-70).  hidden must be a multiple of
+ * 64 and enc_dim of 16 (the GEMM tiles), else UD_ERR_SHAPE. */
 UD_API int ud_rnnt_create(int32_t hidden, int32_t vocab, int32_t layers, int32_t enc_dim, int32_t max_streams,
                           int32_t max_symbols_per_frame, ud_rnnt** out);
 UD_API void ud_rnnt_destroy(ud_rnnt* r);

@@ -61,6 +61,39 @@ def test_greedy_matches_oracle_across_calls(gpu, orc, blank_bias):
     r.close()
 
 
+@pytest.mark.parametrize("blank_bias", [1.2, -50.0])
+def test_greedy_many_streams(gpu, orc, blank_bias):
+    """72 streams x 5 frames: the decoder GEMMs take several 64-row blocks (the joint's 360 rows,
+    the prediction's 72) and the iterations after the first a few rows (the 16- to 48-row tiles).
+    Tokens equal the oracle's over two calls, the joint.enc projection of 360 rows is within 1e-5.  (Blank bias 1.2 on these rows: about 950 tokens in the first call, 0 to 40 per
+    stream, so the iterations shrink from 72 streams to a few.)"""
+    ud = gpu
+    S, rows = 72, 5
+    r, ro, w = _dec(ud, orc, 13, blank_bias, S)
+    rng = np.random.default_rng(21)
+    ost = [ro.state() for _ in range(S)]
+    slots = list(range(S))[::-1]
+    for call in range(2):
+        enc = rng.standard_normal((S * rows, 1024)).astype(np.float32)
+        eb = ud.DeviceBuffer.from_numpy(enc)
+        pb = ud.DeviceBuffer(S * rows * 640 * 4)
+        r.project(S * rows, eb, pb)
+        proj = pb.download((S * rows, 640))
+        ref = enc.astype(np.float64) @ w["joint.enc.weight"].astype(np.float64).T + w["joint.enc.bias"]
+        assert harness.rel_err(proj, ref) <= 1e-5, call
+        frames = [rows - (b % 3 == 1) for b in range(S)] if call else [rows] * S
+        got, cnt = r.greedy(slots, pb, rows, frames, cap=64)
+        proj = proj.reshape(S, rows, 640)
+        n_tok = 0
+        for b in range(S):
+            want = ro.greedy(proj[b, :frames[b]], ost[b])
+            assert cnt[b] == len(want) and got[b] == want[:64], (call, b)
+            n_tok += len(want)
+        if blank_bias > 0:
+            assert 0 < n_tok < 10 * sum(frames), n_tok      # a mix of blank and emitting frames
+    r.close()
+
+
 def test_calls_on_alternating_hip_streams(gpu, orc):
     """joint.enc projections and greedy calls issued on two HIP streams in turn, with no
     synchronisation by the caller: each call waits for the previous one's work (the shared split-K
@@ -156,3 +189,6 @@ def test_rnnt_error_paths(gpu):
         r.reset(5)
     assert e.value.status == -2
     r.close()
+    with pytest.raises(ud.EngineError) as e:
+        ud.Rnnt(max_streams=2, hidden=96)            # hidden not a multiple of 64 (the GEMM tiles)
+    assert e.value.status == -2

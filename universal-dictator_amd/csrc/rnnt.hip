@@ -268,6 +268,8 @@ extern "C" UD_API int ud_rnnt_create(int32_t hidden, int32_t vocab, int32_t laye
     *out = nullptr;
     if (hidden < 1 || vocab < 2 || layers < 1 || layers > 8 || enc_dim < 1 || max_streams < 1 || max_symbols_per_frame < 1)
         return rfail(UD_ERR_SHAPE, "ud_rnnt_create: bad dimensions");
+    if (hidden % 64 != 0 || enc_dim % 16 != 0)
+        return rfail(UD_ERR_SHAPE, "ud_rnnt_create: hidden %d must be a multiple of 64 and enc_dim %d of 16", hidden, enc_dim);
     ud_rnnt* r = new ud_rnnt();
     r->H = hidden; r->V = vocab; r->L = layers; r->E = enc_dim; r->S = max_streams; r->max_sym = max_symbols_per_frame;
     const size_t H = hidden, V = vocab, L = layers, S = max_streams;
