@@ -456,9 +456,10 @@ def rnnt_bench(ud, args):
 
 
 # (regime, blank logit bias of the synthetic joint): every frame blank, every frame at the
-# 10-symbol cap, and a mixed rate of about 0.7 tokens per 160 ms stream-chunk (~4.5 tokens/s, a
-# speech-like rate; the synthetic joint's blank margin is nearly the same on every frame, so the
-# rate moves from 20 to 0 tokens per stream-chunk between biases 1.0 and 1.3)
+# 10-symbol cap, and a mixed rate of 0.2-0.7 tokens per 160 ms stream-chunk (1.4-4.5 tokens/s,
+# speech-like rates, depending on the audio the timed steps push; the synthetic joint's blank
+# margin is nearly the same on every frame, so the rate moves from 20 to 0 tokens per
+# stream-chunk between biases 1.0 and 1.3)
 STREAM_REGIMES = (("blank", 50.0), ("cap", -50.0), ("mixed", 1.24))
 
 
