@@ -84,6 +84,19 @@ UD_API int ud_streamer_tokens(const ud_streamer* s, int32_t id, int32_t* out, in
  * the first cap_rows rows are written; *rows receives the total. */
 UD_API int ud_streamer_recorded(const ud_streamer* s, int32_t id, int32_t which, float* out, int64_t cap_rows,
                                 int64_t* rows);
+/* Emission records of a live stream (NemotronStreamer's emissions, NemotronStreamer.swift:145,
+ * 158; Emission, Sources/DictatorCore/Nemotron/Streaming.swift:6-13): for each token emitted by
+ * ud_streamer_push or ud_streamer_flush, in order, the token, the samples pushed to the stream when
+ * its chunk ran (samplesSeen: / 16000 is the token's algorithmic emission time) and the wall
+ * seconds of the batched step that ran the chunk (computeSeconds).  Buffered input records none,
+ * as the reference's runBuffered.  Any of tokens / samples_seen / compute_seconds may be NULL; the
+ * first cap records are written; *count receives the total. */
+UD_API int ud_streamer_emissions(const ud_streamer* s, int32_t id, int32_t* tokens, int64_t* samples_seen,
+                                 double* compute_seconds, int32_t cap, int32_t* count);
+/* Wall seconds of each chunk of the stream (NemotronStreamer.wallTimes / stepWallTimes,
+ * NemotronStreamer.swift:24, 63, 159): the batched step that ran it, from its mel frames to its
+ * tokens (shared by the streams of that step).  The first cap go to out; *count receives the total. */
+UD_API int ud_streamer_step_times(const ud_streamer* s, int32_t id, double* out, int32_t cap, int32_t* count);
 /* Batched steps run and stream chunks processed since creation. */
 UD_API int ud_streamer_stats(const ud_streamer* s, int64_t* batches, int64_t* chunks);
 

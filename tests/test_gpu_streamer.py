@@ -110,13 +110,28 @@ def test_live_equals_buffered(gpu, orc, la):
     b.end_padding = False
     sb = b.open()
     i = 0
+    after_push = []                  # (tokens so far, samples pushed so far) after each push
     while i < audio.size:
         n = min(1600, audio.size - i)
         b.push({sb: audio[i:i + n]})
         i += n
+        after_push.append((len(b.tokens(sb)), i))
     b.flush([sb])
     assert a.tokens(sa) == b.tokens(sb)
     assert len(a.tokens(sa)) > 0
+    # NemotronStreamer's emissions: one per token of the live stream, in order, with the samples
+    # pushed when its chunk ran (flush pushes none) and that step's wall seconds; wallTimes: one
+    # per chunk, for live and buffered input; buffered input records no emissions
+    em = b.emissions(sb)
+    assert [e[0] for e in em] == b.tokens(sb)
+    k = 0
+    for cnt, pushed in after_push:
+        while k < cnt:
+            assert em[k][1] == pushed, k
+            k += 1
+    assert all(e[1] == audio.size for e in em[k:]) and all(e[2] > 0 for e in em)
+    assert len(b.step_times(sb)) == b.stats()[1] and min(b.step_times(sb)) > 0
+    assert a.emissions(sa) == [] and len(a.step_times(sa)) == a.stats()[1] > 1
     ea, eb = a.recorded(sa, "enc"), b.recorded(sb, "enc")
     assert ea.shape == eb.shape and np.array_equal(ea.view(np.uint32), eb.view(np.uint32))
     # and the buffered run equals the oracle's runBuffered over the same features

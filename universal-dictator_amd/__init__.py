@@ -140,6 +140,8 @@ def _sig(lib):
         "ud_streamer_tokens": (i, [p, _i32, ip, _i32, ip]),
         "ud_streamer_recorded": (i, [p, _i32, _i32, f, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
         "ud_streamer_stats": (i, [p, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
+        "ud_streamer_emissions": (i, [p, _i32, ip, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_double), _i32, ip]),
+        "ud_streamer_step_times": (i, [p, _i32, ctypes.POINTER(ctypes.c_double), _i32, ip]),
         "ud_nemotron_step": (i, [p, p, ctypes.POINTER(_vp), _i32, _i32, p, ip, ip, _i32, _i32, p, _i32, ip, p]),
         "ud_tokenizer_load": (i, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
         "ud_tokenizer_parse": (i, [ctypes.c_char_p, ctypes.c_int64, ctypes.POINTER(_vp)]),
@@ -1131,6 +1133,27 @@ class Streamer:
         _check(_lib.ud_streamer_recorded(self.handle, int(sid), w, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
                                          r.value, ctypes.byref(r)))
         return out
+
+    def emissions(self, sid):
+        """NemotronStreamer's emissions of a live stream: (token, samples_seen, compute_seconds) per
+        emitted token, in order."""
+        n = _i32(0)
+        _check(_lib.ud_streamer_emissions(self.handle, int(sid), None, None, None, 0, ctypes.byref(n)))
+        k = max(1, n.value)
+        tok, seen, secs = np.zeros(k, np.int32), np.zeros(k, np.int64), np.zeros(k, np.float64)
+        _check(_lib.ud_streamer_emissions(self.handle, int(sid), tok.ctypes.data_as(ctypes.POINTER(_i32)),
+                                          seen.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+                                          secs.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), n.value, ctypes.byref(n)))
+        return [(int(tok[e]), int(seen[e]), float(secs[e])) for e in range(n.value)]
+
+    def step_times(self, sid):
+        """NemotronStreamer.wallTimes of a stream: wall seconds of each of its chunks' batched steps."""
+        n = _i32(0)
+        _check(_lib.ud_streamer_step_times(self.handle, int(sid), None, 0, ctypes.byref(n)))
+        out = np.zeros(max(1, n.value), np.float64)
+        _check(_lib.ud_streamer_step_times(self.handle, int(sid), out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)),
+                                           n.value, ctypes.byref(n)))
+        return [float(x) for x in out[:n.value]]
 
     def stats(self):
         b, c = ctypes.c_int64(0), ctypes.c_int64(0)

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <climits>
 #include <cstdarg>
 #include <cstdio>
@@ -52,6 +53,11 @@ struct SStream {
     int64_t frames = 0, valid_frames = 0;
     std::vector<int32_t> tokens;
     std::vector<float> rec_enc, rec_proj;
+    // emissions of live input (token i of tokens is emission i while the stream is live): samples
+    // pushed when the token's chunk ran, and that batched step's wall seconds
+    std::vector<int64_t> emit_samples;
+    std::vector<double> emit_secs;
+    std::vector<double> step_secs;   // wall seconds of each chunk's batched step
 };
 
 struct Plan {
@@ -164,6 +170,7 @@ bool plan_buffered(const ud_streamer* s, SStream& x, int id, Plan& p) {
 
 // One batched step over plans (first chunks ordered first).
 int run_batch(ud_streamer* s, std::vector<Plan>& plans) {
+    const auto t_start = std::chrono::steady_clock::now();
     std::stable_partition(plans.begin(), plans.end(), [](const Plan& p) { return p.first; });
     const int n = (int)plans.size();
     int nF = 0;
@@ -249,11 +256,17 @@ int run_batch(ud_streamer* s, std::vector<Plan>& plans) {
         TCHECK(hipMemcpy(s->rec_y.data(), s->dy, (size_t)n * xrow * 4, hipMemcpyDeviceToHost), "streamer record");
         TCHECK(hipMemcpy(s->rec_p.data(), s->dproj, (size_t)n * s->T * s->Hd * 4, hipMemcpyDeviceToHost), "streamer record");
     }
+    const double secs = std::chrono::duration<double>(std::chrono::steady_clock::now() - t_start).count();
     for (int b = 0; b < n; b++) {
         const Plan& p = plans[b];
         SStream& x = s->st[p.id];
         const int c = std::min(s->counts[b], cap);
         x.tokens.insert(x.tokens.end(), s->toks.begin() + (size_t)b * cap, s->toks.begin() + (size_t)b * cap + c);
+        x.step_secs.push_back(secs);
+        if (x.mode == LIVE) {
+            x.emit_samples.insert(x.emit_samples.end(), (size_t)c, x.n_audio);
+            x.emit_secs.insert(x.emit_secs.end(), (size_t)c, secs);
+        }
         if (s->record) {
             const int keep = s->vt[b];
             x.rec_enc.insert(x.rec_enc.end(), s->rec_y.begin() + b * xrow, s->rec_y.begin() + b * xrow + (size_t)keep * s->D);
@@ -494,6 +507,30 @@ extern "C" UD_API int ud_streamer_recorded(const ud_streamer* s, int32_t id, int
     const int64_t r = (int64_t)v.size() / w;
     if (out && cap_rows > 0) memcpy(out, v.data(), (size_t)std::min(r, cap_rows) * w * 4);
     if (rows) *rows = r;
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_streamer_emissions(const ud_streamer* s, int32_t id, int32_t* tokens, int64_t* samples_seen,
+                                            double* compute_seconds, int32_t cap, int32_t* count) {
+    if (!s) return tfail(UD_ERR_INVALID, "ud_streamer_emissions: null streamer");
+    int rc = check_id(s, id, "ud_streamer_emissions");
+    if (rc != UD_OK) return rc;
+    const SStream& x = s->st[id];
+    const size_t n = x.emit_samples.size(), m = std::min<size_t>(n, cap > 0 ? (size_t)cap : 0);
+    if (tokens && m) memcpy(tokens, x.tokens.data(), m * 4);
+    if (samples_seen && m) memcpy(samples_seen, x.emit_samples.data(), m * 8);
+    if (compute_seconds && m) memcpy(compute_seconds, x.emit_secs.data(), m * 8);
+    if (count) *count = (int32_t)n;
+    return UD_OK;
+}
+
+extern "C" UD_API int ud_streamer_step_times(const ud_streamer* s, int32_t id, double* out, int32_t cap, int32_t* count) {
+    if (!s) return tfail(UD_ERR_INVALID, "ud_streamer_step_times: null streamer");
+    int rc = check_id(s, id, "ud_streamer_step_times");
+    if (rc != UD_OK) return rc;
+    const std::vector<double>& v = s->st[id].step_secs;
+    if (out && cap > 0) memcpy(out, v.data(), std::min<size_t>(v.size(), (size_t)cap) * 8);
+    if (count) *count = (int32_t)v.size();
     return UD_OK;
 }
 
