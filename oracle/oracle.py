@@ -12,7 +12,8 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "_build", "libud_oracle.so")
+# UD_ORACLE_LIB: another build of ud_oracle.c (the mutation tests load planted-mistake builds)
+LIB_PATH = os.environ.get("UD_ORACLE_LIB") or os.path.join(_HERE, "_build", "libud_oracle.so")
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i32p = ctypes.POINTER(ctypes.c_int32)

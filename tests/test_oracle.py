@@ -314,7 +314,9 @@ def test_streaming_equals_offline_chunked(ud, orc):
 
 def test_stream_cache_rule(ud, orc):
     """After a step the K cache equals the last L rows of [previous cache ; this chunk's K
-    projection]: checked by re-deriving layer 0's new K rows from its input."""
+    projection]: checked by re-deriving layer 0's new K rows from its input.  The conv cache is the
+    last K-1 rows of [previous conv cache ; this chunk's GLU rows] with the rows at and past the
+    valid count zeroed (maskRows, FastConformer.swift:302, 470-472): here the chunk's last row."""
     L, T, S = 6, 4, 1
     cfg, lw = _small_model(ud, orc, layers=1)
     D, H = cfg.d_model, cfg.heads
@@ -323,9 +325,9 @@ def test_stream_cache_rule(ud, orc):
     kc = rng.standard_normal((S, 1, L, D)).astype(np.float32)
     vc = rng.standard_normal((S, 1, L, D)).astype(np.float32)
     cc = rng.standard_normal((S, 1, 8, D)).astype(np.float32)
-    cl = np.array([3], np.int32)
+    cl = np.array([1], np.int32)
     x = rng.standard_normal((S, T, D)).astype(np.float32)
-    k0 = kc.copy()
+    k0, c0 = kc.copy(), cc.copy()
     orc.stream_step(smodel, x, np.array([T - 1], np.int32), kc, vc, cc, cl)
     w = lw[0]
     r1 = x[0] + 0.5 * orc.gemm_nt(orc.gemm_nt(orc.layer_norm(x[0], w["norm_feed_forward1.weight"],
@@ -336,4 +338,7 @@ def test_stream_cache_rule(ud, orc):
                        w["self_attn.linear_k.weight"])
     np.testing.assert_array_equal(kc[0, 0, :L - T], k0[0, 0, T:])
     np.testing.assert_allclose(kc[0, 0, L - T:], knew, rtol=1e-5, atol=1e-5)
-    assert cl[0] == min(3 + T, L)
+    assert cl[0] == 1 + T                   # advances by T, not by the valid count (FastConformer.swift:477)
+    np.testing.assert_array_equal(cc[0, 0, :8 - T], c0[0, 0, T:])
+    np.testing.assert_array_equal(cc[0, 0, 7], 0.0)                 # the masked GLU row
+    assert np.all(np.abs(cc[0, 0, 8 - T:7]).max(axis=1) > 0)          # the valid GLU rows
