@@ -184,6 +184,20 @@ def test_step_bf16_256_streams_14_frames_full(gpu, orc):
     enc.close()
 
 
+def test_step_bf16_1024_streams_chunk2(gpu, orc):
+    """The streaming chunk (2 frames, 72 keys) at 1,024 streams = 2,048 rows: the projections move
+    to the LDS-staged kernel, whose q/k/v epilogue then writes the K/V ring rows of 2-frame chunks
+    (the 14-frame tests cover its other ring shape), and the wave attention kernel runs 8,192
+    workgroups.  Two layers, seeded full caches, two steps with ragged valid counts on the second."""
+    cfg = gpu.EncoderConfig(layers=2, max_chunk=2, max_streams=1024, dtype="bf16")
+    plan = lambda step, S, T: [(T, 1, 0, T, T)[s % 5] if step == 1 else T for s in range(S)]
+    enc, _, _, res = _run_steps(gpu, orc, cfg, S=1024, T=2, n_steps=2, seed=71, seed_caches=True, valid_plan=plan,
+                                cache_blocks=64)
+    for i, (got, ref) in enumerate(res):
+        harness.assert_bf16_close(got, ref, "step %d" % i)
+    enc.close()
+
+
 def test_step_bf16_ring_longer_than_window(gpu, orc):
     """An encoder sized for 14-frame chunks stepping shorter chunks: the K/V rings hold
     L + max_chunk = 84 rows while a 5- or 7-frame step's window is 75 or 77 keys, so the chunk
