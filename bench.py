@@ -1,6 +1,6 @@
 """Benchmark of the cache-aware streaming FastConformer encoder step on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|decode|decode_mq|offline|rnnt|stream|stream14]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload chunk2|chunk14|chunk2x1024|decode|decode_mq|offline|rnnt|stream|stream14]
                     [--no-cpu-baseline]
 
 A step is one cache-aware encoder chunk step for every stream of the batch: the mel chunk (new rows
@@ -44,6 +44,7 @@ HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, vendor nominal
 WORKLOADS = {
     "chunk2": dict(streams=64, T=2),     # 64 concurrent streams, 160 ms chunks
     "chunk14": dict(streams=256, T=14),  # 256 concurrent streams, 1120 ms chunks
+    "chunk2x1024": dict(streams=1024, T=2),  # the 160 ms chunk at 1024 concurrent streams
     "decode": dict(seqs=64, q_heads=32, kv_heads=8, head_dim=128, page=16, ctx=(512, 4096)),
     # the same cache with 4 new positions per sequence (one multi-query call)
     "decode_mq": dict(seqs=64, q_heads=32, kv_heads=8, head_dim=128, page=16, ctx=(512, 4096), queries=4),
@@ -903,7 +904,7 @@ def main():
             % (floor_ms * 1000.0, attn_bytes / (floor_ms / 1000.0) / 1e9))
 
     result = {
-        "metric": "aggregate audio-sec/sec at 64 streams; attention-kernel % of HBM roofline",
+        "metric": "aggregate audio-sec/sec at %d streams; attention-kernel %% of HBM roofline" % S,
         "value": round(value, 2),
         "unit": "audio-sec/sec",
         "n_gpus": 1,
