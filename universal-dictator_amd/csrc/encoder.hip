@@ -16,6 +16,7 @@
 //    into a hipGraph and replayed.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -644,16 +645,32 @@ int ud_encoder_aux_release(ud_encoder* e, hipStream_t st) {
 
 // ---------------------------------------------------------------- streams
 
+// Zeroes one slot's rows in every layer: blockIdx.y = layer, blockIdx.z = K ring, V ring, conv
+// ring.  16-byte stores where the range is 16-byte aligned, else bytes.
+__global__ void slot_zero_kernel(char* kring, char* vring, char* cring, size_t ring_layer_bytes, size_t slot_bytes,
+                                 size_t cring_layer_bytes, size_t cslot_bytes, size_t slot_off, size_t cslot_off) {
+    const size_t li = blockIdx.y;
+    const int which = blockIdx.z;
+    char* base = which == 0 ? kring + li * ring_layer_bytes + slot_off
+               : which == 1 ? vring + li * ring_layer_bytes + slot_off : cring + li * cring_layer_bytes + cslot_off;
+    const size_t n = which < 2 ? slot_bytes : cslot_bytes;
+    const size_t stride = (size_t)gridDim.x * blockDim.x, first = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t n16 = (reinterpret_cast<uintptr_t>(base) & 15) == 0 ? n / 16 : 0;
+    for (size_t i = first; i < n16; i += stride) reinterpret_cast<uint4*>(base)[i] = make_uint4(0u, 0u, 0u, 0u);
+    for (size_t i = n16 * 16 + first; i < n; i += stride) base[i] = 0;
+}
+
+// One launch on the null stream, waited for (the caller has synchronized the device first).
 static int zero_slot(ud_encoder* e, int slot) {
     const size_t per = (size_t)e->H * e->R * e->dk, cper = (size_t)(e->Kc - 1) * e->D;
-    for (int li = 0; li < e->layers; li++) {
-        char* kb = static_cast<char*>(e->kring) + ((size_t)li * e->ring_layer_elems + slot * per) * e->esz;
-        char* vb = static_cast<char*>(e->vring) + ((size_t)li * e->ring_layer_elems + slot * per) * e->esz;
-        float* cb = e->cring + (size_t)li * e->cring_layer_elems + slot * cper;
-        HIPC(hipMemset(kb, 0, per * e->esz));
-        HIPC(hipMemset(vb, 0, per * e->esz));
-        HIPC(hipMemset(cb, 0, cper * 4));
-    }
+    const size_t slot_bytes = per * e->esz, cslot_bytes = cper * 4;
+    const size_t blocks = std::min<size_t>(64, (std::max(slot_bytes, cslot_bytes) / 16 + 255) / 256);
+    hipLaunchKernelGGL(slot_zero_kernel, dim3((unsigned)std::max<size_t>(blocks, 1), e->layers, 3), dim3(256), 0, 0,
+                       static_cast<char*>(e->kring), static_cast<char*>(e->vring), reinterpret_cast<char*>(e->cring),
+                       e->ring_layer_elems * e->esz, slot_bytes, e->cring_layer_elems * 4, cslot_bytes,
+                       (size_t)slot * slot_bytes, (size_t)slot * cslot_bytes);
+    HIPC(hipGetLastError());
+    HIPC(hipStreamSynchronize(0));
     return UD_OK;
 }
 
